@@ -1,0 +1,141 @@
+/*
+ * spq4k.h — C ABI of the MI355X (gfx950) Q4_K dequant-matvec library.
+ *
+ * The library computes what the reference's ggml CPU backend computes for
+ * GGML_TYPE_Q4_K weights (vendored ggml in nihilistau/shannon-prime-burnhard,
+ * paths below relative to vendor/ggml/): activations are quantised to Q8_K
+ * exactly as quantize_row_q8_K does, integer sub-block sums are exact, and
+ * outputs agree with ggml_vec_dot_q4_K_q8_K to fp32 summation order.
+ *
+ * Conventions
+ *   - Every function returns 0 on success or a negative errno value:
+ *     -EINVAL (bad argument: K not a multiple of 256, null or misaligned
+ *     pointer, T out of range), -ENOMEM (device allocation failed),
+ *     -ENODEV (no such HIP device), -EIO (a HIP runtime call failed;
+ *     spq4k_last_error() has the message). This follows the reference's
+ *     burnhard_residue_matmul.h:39-56 (0 / -EINVAL / -ENOMEM).
+ *   - Plain pointers are DEVICE pointers and the call only enqueues work on
+ *     the context's stream (like a ggml backend's compute); *_host variants
+ *     take host pointers, copy in and out, and return when the result is in
+ *     host memory.
+ *   - A context is single-writer: calls on one context must not overlap from
+ *     several threads (the reference's sp_crt_dispatch.h:30-33 contract).
+ *     Work on one context is ordered by its stream.
+ *   - Layouts are ggml's: a Q4_K weight matrix with ne[0] = K (inputs) and
+ *     ne[1] = M (outputs) is M rows of K/256 blocks of 144 bytes
+ *     (ggml-common.h:317-328); an expert bank adds ne[2] = E. Activations
+ *     X[T][K] fp32 (src1 with ne[0] = K, ne[1] = T); outputs Y[T][M].
+ *     Device pointers to weights must be 16-byte aligned, activation rows
+ *     16-byte aligned, Q8_K buffers 4-byte aligned.
+ */
+#ifndef SPQ4K_H
+#define SPQ4K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPQ4K_QK_K 256
+#define SPQ4K_Q4K_BLOCK_BYTES 144
+#define SPQ4K_Q8K_BLOCK_BYTES 292
+#define SPQ4K_GEMV_MAX_T 8
+
+typedef struct spq4k_ctx spq4k_ctx;
+typedef struct spq4k_weights spq4k_weights;
+
+/* ---- context ----------------------------------------------------------
+ * Replaces the backend bring-up of the CUDA path (ggml_backend_init_by_type,
+ * desktop/engine/src/cli/main.cpp:95-110; ForwardContext::create,
+ * desktop/engine/src/forward.cpp:694-705). Owns a HIP stream and the
+ * scratch used by split-K GEMV, prefill GEMM and MoE routing. */
+int         spq4k_init(int device, spq4k_ctx **out);
+void        spq4k_free(spq4k_ctx *ctx);
+/* Use the caller's hipStream_t (NULL restores the context's own stream). */
+int         spq4k_set_stream(spq4k_ctx *ctx, void *hip_stream);
+void       *spq4k_get_stream(spq4k_ctx *ctx);
+int         spq4k_synchronize(spq4k_ctx *ctx);
+const char *spq4k_last_error(const spq4k_ctx *ctx);
+int         spq4k_device_count(void);
+
+/* ---- weights -----------------------------------------------------------
+ * Replaces the backend weight upload (ggml_backend_tensor_set of a Q4_K
+ * tensor, desktop/engine/src/llama_weights.cpp:483-560). The device copy is
+ * byte-identical to the host bytes. E = 1 for a dense matrix. */
+int    spq4k_weights_upload(spq4k_ctx *ctx, const void *q4k_host, int64_t M, int64_t K, int64_t E,
+                            spq4k_weights **out);
+/* Wrap Q4_K bytes already in device memory (not copied, not freed). */
+int    spq4k_weights_wrap(spq4k_ctx *ctx, const void *q4k_dev, int64_t M, int64_t K, int64_t E,
+                          spq4k_weights **out);
+/* Allocate an uninitialised device weight buffer (filled by
+ * spq4k_quantize_q4K or a device copy). */
+int    spq4k_weights_alloc(spq4k_ctx *ctx, int64_t M, int64_t K, int64_t E, spq4k_weights **out);
+void   spq4k_weights_free(spq4k_weights *w);
+void  *spq4k_weights_data(const spq4k_weights *w);
+size_t spq4k_weights_nbytes(const spq4k_weights *w);
+
+/* ---- type traits (ggml.h:2791-2804, ggml-cpu.h:113-123) -----------------
+ * spq4k_dequant      : ggml_to_float_t for Q4_K   = dequantize_row_q4_K
+ *                      (ggml-quants.c:1467-1489); bit-exact fp32.
+ * spq4k_quantize_q8K : ggml_from_float_t for Q8_K = quantize_row_q8_K
+ *                      (ggml-cpu/arch/x86/quants.c:505 -> ggml-quants.c:2692);
+ *                      bit-exact blocks (an all-zero block gets zero bsums).
+ * spq4k_quantize_q4K : ggml_quantize_chunk(GGML_TYPE_Q4_K, ..., imatrix=NULL)
+ *                      = quantize_q4_K -> quantize_row_q4_K_ref
+ *                      (ggml-quants.c:1564-1568, :1395-1465); bit-exact bytes.
+ * spq4k_vec_dot      : ggml_vec_dot_t for Q4_K x Q8_K with nrc = 1
+ *                      (ggml_vec_dot_q4_K_q8_K, ggml-cpu/arch/x86/quants.c:1900);
+ *                      *s is a device float. */
+int spq4k_dequant(spq4k_ctx *ctx, const void *vx, float *y, int64_t k);
+int spq4k_quantize_q8K(spq4k_ctx *ctx, const float *x, void *vy, int64_t k);
+int spq4k_quantize_q4K(spq4k_ctx *ctx, const float *src, void *dst, int64_t nrow, int64_t n_per_row);
+int spq4k_vec_dot(spq4k_ctx *ctx, int n, float *s, const void *vx, const void *vy);
+
+int spq4k_dequant_host(spq4k_ctx *ctx, const void *vx, float *y, int64_t k);
+int spq4k_quantize_q8K_host(spq4k_ctx *ctx, const float *x, void *vy, int64_t k);
+int spq4k_quantize_q4K_host(spq4k_ctx *ctx, const float *src, void *dst, int64_t nrow, int64_t n_per_row);
+int spq4k_vec_dot_host(spq4k_ctx *ctx, int n, float *s, const void *vx, const void *vy);
+
+/* ---- matmul ------------------------------------------------------------
+ * spq4k_gemv     : GGML_OP_MUL_MAT for 1 <= T <= 8 (ggml_mul_mat(W[K,M],
+ *                  x[K,T]), ggml.h:1414-1420; CPU ggml-cpu.c:1241-1439; CUDA
+ *                  mmvq.cu:1029). Fused on-chip Q8_K quantisation.
+ * spq4k_gemv_multi: n <= 4 matrices with the same K and the same input x in
+ *                  one launch (q/k/v, gate/up: forward.cpp:1100-1104,
+ *                  1596-1600); y[i] is [T][M_i].
+ * spq4k_gemm     : GGML_OP_MUL_MAT for any T (prefill; CUDA mmq.cuh:3478):
+ *                  Q8_K activations and int8 MFMA on gfx950.
+ * spq4k_mul_mat  : dispatch by T, as ggml-cuda.cu:2366-2449 does
+ *                  (T <= 8 -> gemv, otherwise gemm).
+ * spq4k_moe      : GGML_OP_MUL_MAT_ID (ggml_mul_mat_id(as[K,M,E], b[K,ne11,T],
+ *                  ids[n_used,T]), ggml.h:1434-1438; CPU ggml-cpu.c:1521-1690):
+ *                  Y[t][s][r] = row r of expert ids[t][s] . Q8_K(X[t][s % ne11]),
+ *                  ne11 in {1, n_used}; ids are device int32 [T][n_used].
+ *                  Tokens are grouped per expert so each selected expert's
+ *                  weights stream once per call. */
+int spq4k_gemv(spq4k_ctx *ctx, const spq4k_weights *W, const float *x, float *y, int64_t T);
+int spq4k_gemv_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *W, const float *x,
+                     float *const *y, int64_t T);
+int spq4k_gemm(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
+int spq4k_mul_mat(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
+int spq4k_moe(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int64_t n_used,
+              int64_t ne11, int64_t T, const float *X, float *Y);
+
+int spq4k_mul_mat_host(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
+int spq4k_moe_host(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int64_t n_used,
+                   int64_t ne11, int64_t T, const float *X, float *Y);
+
+/* ---- diagnostics -------------------------------------------------------
+ * Exact integer sub-block sums S[r][b][j] = sum_{l<32} q4 * q8 over
+ * sub-block j of block b of row r, against Q8_K(x), formed by the same lane
+ * code as the GEMV. No reference function returns them; they are the integer
+ * core of ggml_vec_dot_q4_K_q8_K (ggml-cpu/quants.c:645-718). */
+int spq4k_subblock_sums(spq4k_ctx *ctx, const void *W, int64_t M, int64_t K, const float *x, int32_t *S);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPQ4K_H */

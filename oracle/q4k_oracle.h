@@ -1,0 +1,87 @@
+/*
+ * q4k_oracle.h — CPU restatement of the reference's Q4_K x Q8_K arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP kernels
+ * in shannon-prime-burnhard_amd/csrc. Only tests/, __graft_entry__.smoke()
+ * and the cpu_baseline leg of bench.py may load it. No product code path may
+ * call it, link it, or fall back to it.
+ *
+ * Every function restates a function of the vendored ggml in the reference
+ * (vendor/ggml/src/...), cited at its definition in q4k_oracle.c. It is
+ * compiled with -ffp-contract=off so that each floating-point operation is
+ * rounded exactly once, as in ggml-base (which is built without FMA flags).
+ *
+ * Parity pins (see tests/): golden fixtures written by tests/golden/gen_golden.py
+ * from the reference compiled in oracle/_ref, exhaustive and closed-form checks
+ * of the scale unpacker, dequantiser and Q8_K quantiser, and brute-force
+ * integer sub-block sums.
+ */
+#ifndef Q4K_ORACLE_H
+#define Q4K_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OR_QK_K 256
+#define OR_Q4K_BLOCK_BYTES 144   /* d, dmin (fp16), scales[12], qs[128] */
+#define OR_Q8K_BLOCK_BYTES 292   /* d (f32), qs[256] (i8), bsums[16] (i16) */
+
+typedef struct {
+    uint16_t d;
+    uint16_t dmin;
+    uint8_t  scales[12];
+    uint8_t  qs[128];
+} or_block_q4K;
+
+typedef struct {
+    float   d;
+    int8_t  qs[256];
+    int16_t bsums[16];
+} or_block_q8K;
+
+/* scalar helpers */
+float    or_fp16_to_fp32(uint16_t h);
+uint16_t or_fp32_to_fp16(float f);
+int      or_nearest_int(float v);
+void     or_scale_min_k4(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);
+
+/* type traits (ggml_to_float_t / ggml_from_float_t shapes) */
+void or_quantize_row_q4K(const float *x, void *y, int64_t k);
+size_t or_quantize_q4K(const float *src, void *dst, int64_t nrow, int64_t n_per_row);
+void or_dequantize_row_q4K(const void *x, float *y, int64_t k);
+void or_quantize_row_q8K(const float *x, void *y, int64_t k);
+
+/* dot products (ggml_vec_dot_t semantics, nrc == 1) */
+float  or_vec_dot_generic(int n, const void *vx, const void *vy);
+float  or_vec_dot_avx2order(int n, const void *vx, const void *vy);
+double or_vec_dot_exact(int n, const void *vx, const void *vy);
+/* S[b*8 + j] = sum over the 32 weights of sub-block j of block b of q4*q8 */
+void   or_subblock_sums(int n, const void *vx, const void *vy, int32_t *S);
+
+/* drivers: ggml_compute_forward_mul_mat / _mul_mat_id numerics.
+ * W: M rows of K/256 Q4_K blocks; X: T rows of K fp32; Y: T rows of M fp32.
+ * order: 0 = generic float order, 1 = x86 AVX2 float order. */
+void or_mul_mat(const void *W, int64_t M, int64_t K, const float *X, int64_t T,
+                float *Y, int order);
+/* as: E experts of [M x K]; X: [T][ne11][K] with ne11 in {1, k};
+ * ids: [T][k] int32; Y: [T][k][M]. Returns 0, or -22 on a bad expert id. */
+int  or_mul_mat_id(const void *as, int64_t M, int64_t K, int64_t E,
+                   const float *X, int64_t ne11, const int32_t *ids, int64_t k,
+                   int64_t T, float *Y, int order);
+/* dequant-then-dot in double: the "dequant-then-dot" branch of the parity bar */
+void or_mul_mat_dequant_f64(const void *W, int64_t M, int64_t K, const float *X,
+                            int64_t T, double *Y);
+
+/* synthetic data, bit-identical with the device generator */
+void or_synth_fill(float *out, int64_t n, uint64_t seed, int dist, int64_t cols,
+                   float mean, float std, float outlier_mult, int64_t offset);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q4K_ORACLE_H */

@@ -1,0 +1,534 @@
+// api.hip — the C ABI of libspq4k (include/spq4k.h, include/spq4k_synth.h).
+//
+// Host-side planning for the gfx950 kernels: argument checks, tile and
+// K-split choice, scratch management, host<->device staging for the *_host
+// entry points. There is no CPU compute path: every result comes from a HIP
+// kernel, and a missing or failing device is an error.
+#include <errno.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <hip/hip_runtime.h>
+
+#include "launch.h"
+#include "spq4k.h"
+#include "spq4k_synth.h"
+
+using namespace spq4k;
+
+struct spq4k_ctx {
+    int device = 0;
+    int num_cus = 256;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    // split-K GEMV
+    float* partial = nullptr;
+    size_t partial_cap = 0;      // floats
+    uint32_t* counters = nullptr;
+    size_t counters_cap = 0;     // entries
+    // generic device scratch (Q8_K activations, routing tables)
+    uint8_t* scratch = nullptr;
+    size_t scratch_cap = 0;
+    char err[256] = {0};
+};
+
+struct spq4k_weights {
+    spq4k_ctx* ctx = nullptr;
+    uint8_t* data = nullptr;
+    bool owned = false;
+    int64_t M = 0, K = 0, E = 0;
+    size_t nbytes = 0;
+};
+
+namespace {
+
+int set_err(spq4k_ctx* c, int code, const char* fmt, ...) {
+    if (c) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(c->err, sizeof c->err, fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+int hip_fail(spq4k_ctx* c, hipError_t e, const char* what) {
+    return set_err(c, -EIO, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define SPQ_HIP(ctx, call)                                            \
+    do {                                                              \
+        hipError_t _e = (call);                                       \
+        if (_e != hipSuccess) return hip_fail((ctx), _e, #call);      \
+    } while (0)
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int use_device(spq4k_ctx* c) {
+    if (!c) return -EINVAL;
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return hip_fail(c, e, "hipSetDevice");
+    return 0;
+}
+
+int ensure_partial(spq4k_ctx* c, size_t floats, size_t tiles) {
+    if (floats > c->partial_cap) {
+        if (c->partial) hipFree(c->partial);
+        c->partial = nullptr;
+        c->partial_cap = 0;
+        size_t cap = floats < (size_t)(1 << 20) ? (size_t)(1 << 20) : floats;
+        if (hipMalloc(&c->partial, cap * sizeof(float)) != hipSuccess) {
+            c->partial = nullptr;
+            return set_err(c, -ENOMEM, "partial buffer of %zu floats", cap);
+        }
+        c->partial_cap = cap;
+    }
+    if (tiles > c->counters_cap) {
+        // counters must be zero outside a launch; grow only between launches
+        SPQ_HIP(c, hipStreamSynchronize(c->stream));
+        if (c->counters) hipFree(c->counters);
+        c->counters = nullptr;
+        c->counters_cap = 0;
+        size_t cap = tiles < 65536 ? 65536 : tiles;
+        if (hipMalloc(&c->counters, cap * sizeof(uint32_t)) != hipSuccess) {
+            c->counters = nullptr;
+            return set_err(c, -ENOMEM, "counter buffer of %zu", cap);
+        }
+        SPQ_HIP(c, hipMemset(c->counters, 0, cap * sizeof(uint32_t)));
+        c->counters_cap = cap;
+    }
+    return 0;
+}
+
+int ensure_scratch(spq4k_ctx* c, size_t bytes) {
+    if (bytes <= c->scratch_cap) return 0;
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    if (c->scratch) hipFree(c->scratch);
+    c->scratch = nullptr;
+    c->scratch_cap = 0;
+    size_t cap = bytes < (size_t)(4 << 20) ? (size_t)(4 << 20) : bytes;
+    if (hipMalloc(&c->scratch, cap) != hipSuccess) {
+        c->scratch = nullptr;
+        return set_err(c, -ENOMEM, "scratch of %zu bytes", cap);
+    }
+    c->scratch_cap = cap;
+    return 0;
+}
+
+int check_shape(spq4k_ctx* c, int64_t M, int64_t K, int64_t E) {
+    if (M <= 0 || K <= 0 || E <= 0) return set_err(c, -EINVAL, "non-positive shape M=%lld K=%lld E=%lld",
+                                                   (long long)M, (long long)K, (long long)E);
+    if (K % SPQ4K_QK_K) return set_err(c, -EINVAL, "K=%lld is not a multiple of 256", (long long)K);
+    if (M > (1ll << 30) || K > (1ll << 30)) return set_err(c, -EINVAL, "shape too large");
+    return 0;
+}
+
+// ---- GEMV planning ---------------------------------------------------------
+struct GemvPlan {
+    int waves, ntiles, ksplit, kbps, cb;
+};
+
+constexpr int LDS_BUDGET = 48 * 1024;
+
+GemvPlan plan_gemv(const spq4k_ctx* c, int64_t total_tiles_64, int nb, int T) {
+    GemvPlan p;
+    p.waves = 4;  // 64 rows per workgroup
+    p.ntiles = (int)total_tiles_64;
+    // enough workgroups for every CU twice over; K splits of >= 2 blocks
+    const int target = 2 * c->num_cus;
+    int ks = 1;
+    if (p.ntiles < target) ks = (target + p.ntiles - 1) / p.ntiles;
+    int max_ks = nb / 2 > 0 ? nb / 2 : 1;
+    if (ks > max_ks) ks = max_ks;
+    if (ks < 1) ks = 1;
+    p.kbps = (nb + ks - 1) / ks;
+    p.ksplit = (nb + p.kbps - 1) / p.kbps;
+    const int cb_max = LDS_BUDGET / (T * 292);
+    p.cb = p.kbps < cb_max ? p.kbps : cb_max;
+    if (p.cb < 1) p.cb = 1;
+    return p;
+}
+
+int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* x, float* const* y, int64_t T) {
+    if (n < 1 || n > GEMV_MAX_SEG) return set_err(c, -EINVAL, "gemv: n=%d matrices (1..4)", n);
+    if (T < 1 || T > SPQ4K_GEMV_MAX_T) return set_err(c, -EINVAL, "gemv: T=%lld (1..8)", (long long)T);
+    if (!x || !aligned(x, 16)) return set_err(c, -EINVAL, "gemv: x null or not 16-byte aligned");
+    const int64_t K = W[0] ? W[0]->K : 0;
+    GemvParams p;
+    memset(&p, 0, sizeof p);
+    int64_t tiles = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!W[i] || !W[i]->data || !y || !y[i]) return set_err(c, -EINVAL, "gemv: null weight or output");
+        if (W[i]->K != K || W[i]->E != 1) return set_err(c, -EINVAL, "gemv: matrices must share K and have E=1");
+        if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemv: weights not 16-byte aligned");
+        p.seg[i].W = W[i]->data;
+        p.seg[i].Y = y[i];
+        p.seg[i].M = (int32_t)W[i]->M;
+        p.seg[i].y_tstride = W[i]->M;
+        p.seg[i].tile_begin = (int32_t)tiles;
+        tiles += (W[i]->M + 63) / 64;
+    }
+    if (tiles > (1 << 24)) return set_err(c, -EINVAL, "gemv: too many rows");
+    p.nseg = n;
+    p.nb = (int32_t)(K / SPQ4K_QK_K);
+    p.X = x;
+    p.x_tstride = K;
+    const GemvPlan pl = plan_gemv(c, tiles, p.nb, (int)T);
+    p.ksplit = pl.ksplit;
+    p.kb_per_split = pl.kbps;
+    p.chunk_blocks = pl.cb;
+    if (p.ksplit > 1) {
+        int rc = ensure_partial(c, (size_t)tiles * p.ksplit * T * 64, (size_t)tiles);
+        if (rc) return rc;
+        p.partial = c->partial;
+        p.counters = c->counters;
+    }
+    hipError_t e = launch_gemv(p, (int)T, pl.waves, (int)tiles, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "gemv launch");
+    return 0;
+}
+
+}  // namespace
+
+// ============================================================================
+extern "C" {
+
+int spq4k_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int spq4k_init(int device, spq4k_ctx** out) {
+    if (!out) return -EINVAL;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return -ENODEV;
+    spq4k_ctx* c = new (std::nothrow) spq4k_ctx();
+    if (!c) return -ENOMEM;
+    c->device = device;
+    if (hipSetDevice(device) != hipSuccess) { delete c; return -ENODEV; }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+        c->num_cus = prop.multiProcessorCount;
+    if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) { delete c; return -EIO; }
+    c->stream = c->own_stream;
+    *out = c;
+    return 0;
+}
+
+void spq4k_free(spq4k_ctx* c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    if (c->stream) hipStreamSynchronize(c->stream);
+    if (c->partial) hipFree(c->partial);
+    if (c->counters) hipFree(c->counters);
+    if (c->scratch) hipFree(c->scratch);
+    if (c->own_stream) hipStreamDestroy(c->own_stream);
+    delete c;
+}
+
+int spq4k_set_stream(spq4k_ctx* c, void* s) {
+    if (!c) return -EINVAL;
+    c->stream = s ? (hipStream_t)s : c->own_stream;
+    return 0;
+}
+
+void* spq4k_get_stream(spq4k_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+int spq4k_synchronize(spq4k_ctx* c) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+const char* spq4k_last_error(const spq4k_ctx* c) { return c ? c->err : "null context"; }
+
+// ---- weights -----------------------------------------------------------------
+static int weights_new(spq4k_ctx* c, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
+    if (!out) return set_err(c, -EINVAL, "weights: null out");
+    *out = nullptr;
+    int rc = check_shape(c, M, K, E);
+    if (rc) return rc;
+    spq4k_weights* w = new (std::nothrow) spq4k_weights();
+    if (!w) return -ENOMEM;
+    w->ctx = c;
+    w->M = M;
+    w->K = K;
+    w->E = E;
+    w->nbytes = (size_t)E * (size_t)M * (size_t)(K / SPQ4K_QK_K) * SPQ4K_Q4K_BLOCK_BYTES;
+    *out = w;
+    return 0;
+}
+
+int spq4k_weights_alloc(spq4k_ctx* c, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    spq4k_weights* w;
+    rc = weights_new(c, M, K, E, &w);
+    if (rc) return rc;
+    if (hipMalloc(&w->data, w->nbytes) != hipSuccess) {
+        delete w;
+        return set_err(c, -ENOMEM, "weights: %zu bytes", (size_t)0);
+    }
+    w->owned = true;
+    *out = w;
+    return 0;
+}
+
+int spq4k_weights_upload(spq4k_ctx* c, const void* host, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
+    if (!host) return set_err(c, -EINVAL, "weights_upload: null host pointer");
+    int rc = spq4k_weights_alloc(c, M, K, E, out);
+    if (rc) return rc;
+    hipError_t e = hipMemcpyAsync((*out)->data, host, (*out)->nbytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        spq4k_weights_free(*out);
+        *out = nullptr;
+        return hip_fail(c, e, "weights_upload copy");
+    }
+    return 0;
+}
+
+int spq4k_weights_wrap(spq4k_ctx* c, const void* dev, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
+    if (!dev || !aligned(dev, 16)) return set_err(c, -EINVAL, "weights_wrap: null or not 16-byte aligned");
+    int rc = weights_new(c, M, K, E, out);
+    if (rc) return rc;
+    (*out)->data = (uint8_t*)dev;
+    (*out)->owned = false;
+    return 0;
+}
+
+void spq4k_weights_free(spq4k_weights* w) {
+    if (!w) return;
+    if (w->owned && w->data) {
+        hipSetDevice(w->ctx->device);
+        hipStreamSynchronize(w->ctx->stream);
+        hipFree(w->data);
+    }
+    delete w;
+}
+
+void* spq4k_weights_data(const spq4k_weights* w) { return w ? (void*)w->data : nullptr; }
+size_t spq4k_weights_nbytes(const spq4k_weights* w) { return w ? w->nbytes : 0; }
+
+// ---- type traits ---------------------------------------------------------------
+int spq4k_dequant(spq4k_ctx* c, const void* vx, float* y, int64_t k) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!vx || !y || k < 0 || k % SPQ4K_QK_K || !aligned(vx, 16) || !aligned(y, 16))
+        return set_err(c, -EINVAL, "dequant: bad arguments");
+    hipError_t e = launch_dequant_q4k((const uint8_t*)vx, y, k / SPQ4K_QK_K, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "dequant launch");
+    return 0;
+}
+
+int spq4k_quantize_q8K(spq4k_ctx* c, const float* x, void* vy, int64_t k) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!x || !vy || k < 0 || k % SPQ4K_QK_K || !aligned(x, 16) || !aligned(vy, 4))
+        return set_err(c, -EINVAL, "quantize_q8K: bad arguments");
+    hipError_t e = launch_quantize_q8k(x, (uint8_t*)vy, k / SPQ4K_QK_K, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "quantize_q8K launch");
+    return 0;
+}
+
+int spq4k_quantize_q4K(spq4k_ctx* c, const float* src, void* dst, int64_t nrow, int64_t n_per_row) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!src || !dst || nrow < 0 || n_per_row <= 0 || n_per_row % SPQ4K_QK_K || !aligned(src, 16) ||
+        !aligned(dst, 16))
+        return set_err(c, -EINVAL, "quantize_q4K: bad arguments");
+    hipError_t e = launch_quantize_q4k(src, (uint8_t*)dst, nrow * (n_per_row / SPQ4K_QK_K), c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "quantize_q4K launch");
+    return 0;
+}
+
+int spq4k_vec_dot(spq4k_ctx* c, int n, float* s, const void* vx, const void* vy) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!s || !vx || !vy || n <= 0 || n % SPQ4K_QK_K || !aligned(vx, 16) || !aligned(vy, 4))
+        return set_err(c, -EINVAL, "vec_dot: bad arguments");
+    hipError_t e = launch_vec_dot_q8((const uint8_t*)vx, (const uint8_t*)vy, n / SPQ4K_QK_K, s, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "vec_dot launch");
+    return 0;
+}
+
+// host variants: stage through device scratch
+namespace {
+struct DevBuf {
+    void* p = nullptr;
+    ~DevBuf() { if (p) hipFree(p); }
+};
+}  // namespace
+
+int spq4k_dequant_host(spq4k_ctx* c, const void* vx, float* y, int64_t k) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!vx || !y || k < 0 || k % SPQ4K_QK_K) return set_err(c, -EINVAL, "dequant_host: bad arguments");
+    const size_t nin = (size_t)(k / SPQ4K_QK_K) * SPQ4K_Q4K_BLOCK_BYTES, nout = (size_t)k * sizeof(float);
+    DevBuf a, b;
+    if (hipMalloc(&a.p, nin + 16) != hipSuccess || hipMalloc(&b.p, nout + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "dequant_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, vx, nin, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_dequant(c, a.p, (float*)b.p, k);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(y, b.p, nout, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int spq4k_quantize_q8K_host(spq4k_ctx* c, const float* x, void* vy, int64_t k) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!x || !vy || k < 0 || k % SPQ4K_QK_K) return set_err(c, -EINVAL, "quantize_q8K_host: bad arguments");
+    const size_t nin = (size_t)k * sizeof(float), nout = (size_t)(k / SPQ4K_QK_K) * SPQ4K_Q8K_BLOCK_BYTES;
+    DevBuf a, b;
+    if (hipMalloc(&a.p, nin + 16) != hipSuccess || hipMalloc(&b.p, nout + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "quantize_q8K_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, x, nin, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_quantize_q8K(c, (const float*)a.p, b.p, k);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(vy, b.p, nout, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int spq4k_quantize_q4K_host(spq4k_ctx* c, const float* src, void* dst, int64_t nrow, int64_t n_per_row) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!src || !dst || nrow < 0 || n_per_row <= 0 || n_per_row % SPQ4K_QK_K)
+        return set_err(c, -EINVAL, "quantize_q4K_host: bad arguments");
+    const int64_t k = nrow * n_per_row;
+    const size_t nin = (size_t)k * sizeof(float), nout = (size_t)(k / SPQ4K_QK_K) * SPQ4K_Q4K_BLOCK_BYTES;
+    DevBuf a, b;
+    if (hipMalloc(&a.p, nin + 16) != hipSuccess || hipMalloc(&b.p, nout + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "quantize_q4K_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, src, nin, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_quantize_q4K(c, (const float*)a.p, b.p, nrow, n_per_row);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(dst, b.p, nout, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int spq4k_vec_dot_host(spq4k_ctx* c, int n, float* s, const void* vx, const void* vy) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!s || !vx || !vy || n <= 0 || n % SPQ4K_QK_K) return set_err(c, -EINVAL, "vec_dot_host: bad arguments");
+    const size_t nx = (size_t)(n / SPQ4K_QK_K) * SPQ4K_Q4K_BLOCK_BYTES;
+    const size_t ny = (size_t)(n / SPQ4K_QK_K) * SPQ4K_Q8K_BLOCK_BYTES;
+    DevBuf a, b, o;
+    if (hipMalloc(&a.p, nx + 16) != hipSuccess || hipMalloc(&b.p, ny + 16) != hipSuccess ||
+        hipMalloc(&o.p, 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "vec_dot_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, vx, nx, hipMemcpyHostToDevice, c->stream));
+    SPQ_HIP(c, hipMemcpyAsync(b.p, vy, ny, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_vec_dot(c, n, (float*)o.p, a.p, b.p);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(s, o.p, sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+// ---- matmul ----------------------------------------------------------------------
+int spq4k_gemv(spq4k_ctx* c, const spq4k_weights* W, const float* x, float* y, int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    const spq4k_weights* ws[1] = {W};
+    float* ys[1] = {y};
+    return gemv_launch(c, 1, ws, x, ys, T);
+}
+
+int spq4k_gemv_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* x, float* const* y,
+                     int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!W || !y) return set_err(c, -EINVAL, "gemv_multi: null arrays");
+    return gemv_launch(c, n, W, x, y, T);
+}
+
+int spq4k_gemm(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    (void)W; (void)X; (void)Y; (void)T;
+    return set_err(c, -ENOSYS, "gemm: not built yet");
+}
+
+int spq4k_mul_mat(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
+    if (T >= 1 && T <= SPQ4K_GEMV_MAX_T) return spq4k_gemv(c, W, X, Y, T);
+    return spq4k_gemm(c, W, X, Y, T);
+}
+
+int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t n_used, int64_t ne11,
+              int64_t T, const float* X, float* Y) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    (void)bank; (void)ids; (void)n_used; (void)ne11; (void)T; (void)X; (void)Y;
+    return set_err(c, -ENOSYS, "moe: not built yet");
+}
+
+int spq4k_mul_mat_host(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!W || !X || !Y || T < 1) return set_err(c, -EINVAL, "mul_mat_host: bad arguments");
+    const size_t nx = (size_t)T * W->K * sizeof(float), ny = (size_t)T * W->M * sizeof(float);
+    DevBuf a, b;
+    if (hipMalloc(&a.p, nx + 16) != hipSuccess || hipMalloc(&b.p, ny + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "mul_mat_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, X, nx, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_mul_mat(c, W, (const float*)a.p, (float*)b.p, T);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(Y, b.p, ny, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int spq4k_moe_host(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t n_used, int64_t ne11,
+                   int64_t T, const float* X, float* Y) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!bank || !ids || !X || !Y || T < 1 || n_used < 1 || (ne11 != 1 && ne11 != n_used))
+        return set_err(c, -EINVAL, "moe_host: bad arguments");
+    const size_t ni = (size_t)T * n_used * sizeof(int32_t);
+    const size_t nx = (size_t)T * ne11 * bank->K * sizeof(float);
+    const size_t ny = (size_t)T * n_used * bank->M * sizeof(float);
+    DevBuf a, b, d;
+    if (hipMalloc(&a.p, ni + 16) != hipSuccess || hipMalloc(&b.p, nx + 16) != hipSuccess ||
+        hipMalloc(&d.p, ny + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "moe_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, ids, ni, hipMemcpyHostToDevice, c->stream));
+    SPQ_HIP(c, hipMemcpyAsync(b.p, X, nx, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_moe(c, bank, (const int32_t*)a.p, n_used, ne11, T, (const float*)b.p, (float*)d.p);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(Y, d.p, ny, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+// ---- diagnostics / synth -------------------------------------------------------------
+int spq4k_subblock_sums(spq4k_ctx* c, const void* W, int64_t M, int64_t K, const float* x, int32_t* S) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    rc = check_shape(c, M, K, 1);
+    if (rc) return rc;
+    if (!W || !x || !S || !aligned(W, 16) || !aligned(x, 16)) return set_err(c, -EINVAL, "subblock_sums: bad pointers");
+    hipError_t e = launch_subblock_sums((const uint8_t*)W, (int)M, (int)(K / SPQ4K_QK_K), x, S, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "subblock_sums launch");
+    return 0;
+}
+
+int spq4k_synth_fill(spq4k_ctx* c, float* out, int64_t n, uint64_t seed, int dist, int64_t cols, float mean,
+                     float std, float outlier_mult, int64_t offset) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!out || n < 0 || (dist != SPQ4K_DIST_NORMAL && dist != SPQ4K_DIST_STUDENT_T4) || cols < 0)
+        return set_err(c, -EINVAL, "synth_fill: bad arguments");
+    hipError_t e = launch_synth(out, n, seed, dist, cols, mean, std, outlier_mult, offset, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "synth launch");
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,171 @@
+// gemv_core.h — the Q4_K x Q8_K matvec building blocks shared by the dense,
+// grouped and expert-gathered GEMV kernels.
+//
+// Lane mapping (wave64): four lanes per weight row. Lane l4 = lane & 3 of a
+// row's group reads, per 144 B super-block, the 16 B header (d, dmin, scales)
+// and the 32 contiguous bytes qs[32*l4 .. 32*l4+31]. Those bytes carry the
+// whole of sub-blocks j0 = 2*l4 (low nibbles, elements 64*l4 + 0..31) and
+// j1 = 2*l4 + 1 (high nibbles, elements 64*l4 + 32..63), so each lane forms the
+// two exact integer sub-block sums S_{b,j0}, S_{b,j1} with eight v_dot4_i32_i8
+// each, applies its two 6-bit scales and mins, and folds the block into an
+// fp32 accumulator:
+//     acc += (fp16(d) * d8) * (sc0*S0 + sc1*S1) - (fp16(dmin) * d8) * (m0*bs01 + m1*bs23)
+// This is the arithmetic of ggml_vec_dot_q4_K_q8_K
+// (vendor/ggml/src/ggml-cpu/quants.c:645-718, arch/x86/quants.c:1919-1982)
+// with the integer parts exact and only the fp32 summation order changed.
+//
+// Activations are quantised to Q8_K on chip and staged in LDS as
+//   q8[slot][256] int8 | bsum[slot][16] int16 | d8[slot] f32,  slot = t*CB + block
+#pragma once
+
+#include "q4k_device.h"
+
+namespace spq4k {
+
+// Registers of one lane for one super-block of one row.
+struct W4 {
+    uint4 hdr;   // d | dmin << 16, scale bytes 0-3, 4-7, 8-11
+    uint4 qa;    // qs[32*l4 + 0 .. 15]
+    uint4 qb;    // qs[32*l4 + 16 .. 31]
+};
+
+__device__ __forceinline__ W4 load_w4(const uint8_t* __restrict__ blk, int l4) {
+    W4 w;
+    w.hdr = *reinterpret_cast<const uint4*>(blk);
+    const uint4* q = reinterpret_cast<const uint4*>(blk + 16 + 32 * l4);
+    w.qa = q[0];
+    w.qb = q[1];
+    return w;
+}
+
+__device__ __forceinline__ W4 zero_w4() {
+    W4 w;
+    w.hdr = make_uint4(0, 0, 0, 0);
+    w.qa = w.hdr;
+    w.qb = w.hdr;
+    return w;
+}
+
+// Per-lane, per-block constants derived from the header.
+struct BlkC {
+    float d, dmin;
+    int sc0, sc1, m0, m1;
+};
+
+__device__ __forceinline__ BlkC block_consts(const uint4& h, int l4) {
+    BlkC c;
+    c.d = half_bits_to_float(h.x & 0xFFFFu);
+    c.dmin = half_bits_to_float(h.x >> 16);
+    const ScaleMin sm = unpack_scale_min(h.y, h.z, h.w);
+    const bool hi = l4 >= 2;
+    const uint32_t scw = hi ? sm.sc_hi : sm.sc_lo;
+    const uint32_t mw = hi ? sm.m_hi : sm.m_lo;
+    const int sh = 16 * (l4 & 1);
+    c.sc0 = (int)((scw >> sh) & 0xFFu);
+    c.sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
+    c.m0 = (int)((mw >> sh) & 0xFFu);
+    c.m1 = (int)((mw >> (sh + 8)) & 0xFFu);
+    return c;
+}
+
+// Nibble planes of the lane's 32 qs bytes: lo[i] holds elements 64*l4 + 4i..4i+3,
+// hi[i] elements 64*l4 + 32 + 4i..4i+3, as unsigned bytes 0..15.
+struct Nib {
+    int lo[8], hi[8];
+};
+
+__device__ __forceinline__ Nib split_nibbles(const W4& w) {
+    Nib n;
+    const uint32_t q[8] = {w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        n.lo[i] = (int)(q[i] & 0x0F0F0F0Fu);
+        n.hi[i] = (int)((q[i] >> 4) & 0x0F0F0F0Fu);
+    }
+    return n;
+}
+
+// LDS view of the staged Q8_K activations for one chunk.
+struct Q8Lds {
+    int8_t* q8;     // [slots][256]
+    int16_t* bs;    // [slots][16]
+    float* d8;      // [slots]
+};
+
+__host__ __device__ constexpr int q8lds_bytes(int slots) { return slots * (256 + 32 + 4); }
+
+__device__ __forceinline__ Q8Lds q8lds_carve(char* base, int slots) {
+    Q8Lds v;
+    v.q8 = reinterpret_cast<int8_t*>(base);
+    v.bs = reinterpret_cast<int16_t*>(base + slots * 256);
+    v.d8 = reinterpret_cast<float*>(base + slots * (256 + 32));
+    return v;
+}
+
+// Two integer sub-block sums of one lane against one staged activation block.
+__device__ __forceinline__ void subblock_pair(const Nib& n, const int8_t* q8blk, int l4, int& S0, int& S1) {
+    const int4* p = reinterpret_cast<const int4*>(q8blk + 64 * l4);
+    const int4 a0 = p[0], a1 = p[1], b0 = p[2], b1 = p[3];
+    int s = 0;
+    s = dot4(n.lo[0], a0.x, s); s = dot4(n.lo[1], a0.y, s);
+    s = dot4(n.lo[2], a0.z, s); s = dot4(n.lo[3], a0.w, s);
+    s = dot4(n.lo[4], a1.x, s); s = dot4(n.lo[5], a1.y, s);
+    s = dot4(n.lo[6], a1.z, s); s = dot4(n.lo[7], a1.w, s);
+    int u = 0;
+    u = dot4(n.hi[0], b0.x, u); u = dot4(n.hi[1], b0.y, u);
+    u = dot4(n.hi[2], b0.z, u); u = dot4(n.hi[3], b0.w, u);
+    u = dot4(n.hi[4], b1.x, u); u = dot4(n.hi[5], b1.y, u);
+    u = dot4(n.hi[6], b1.z, u); u = dot4(n.hi[7], b1.w, u);
+    S0 = s;
+    S1 = u;
+}
+
+// Min-term integer: m0 * (bsums[4 l4] + bsums[4 l4 + 1]) + m1 * (bsums[4 l4 + 2] + bsums[4 l4 + 3]).
+__device__ __forceinline__ int min_term(const int16_t* bsblk, int l4, int m0, int m1) {
+    const uint2 v = *reinterpret_cast<const uint2*>(bsblk + 4 * l4);
+    const int b0 = (int)(int16_t)(v.x & 0xFFFFu), b1 = (int)(int16_t)(v.x >> 16);
+    const int b2 = (int)(int16_t)(v.y & 0xFFFFu), b3 = (int)(int16_t)(v.y >> 16);
+    return m0 * (b0 + b1) + m1 * (b2 + b3);
+}
+
+// Quantise activation blocks into LDS. Work items are (t, block) pairs,
+// item i -> t = i / nblk, block kb0 + i % nblk. Each 16-lane slice of a wave
+// quantises one item per pass. X rows are 16-byte aligned (checked on host).
+template <int WAVES>
+__device__ __forceinline__ void stage_q8(const float* __restrict__ X, int64_t x_tstride, int T,
+                                         int kb0, int nblk, const Q8Lds& L, int slot_stride) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int e = lane & 15;
+    const int sub = lane >> 4;  // 0..3
+    const int nitems = T * nblk;
+    for (int base = 0; base < nitems; base += 4 * WAVES) {
+        const int item = base + wave * 4 + sub;
+        const bool valid = item < nitems;
+        const int t = valid ? item / nblk : 0;
+        const int bb = valid ? item - t * nblk : 0;
+        float x[16];
+        if (valid) {
+            const float4* src = reinterpret_cast<const float4*>(X + (int64_t)t * x_tstride +
+                                                                (int64_t)(kb0 + bb) * QK + 16 * e);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 v = src[i];
+                x[4 * i + 0] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[i] = 0.0f;
+        }
+        // all 16 lanes of a slice share `valid`, so the shuffles stay within live lanes
+        const Q8Lane q = quantize_q8k_16(x, e);
+        if (valid) {
+            const int slot = t * slot_stride + bb;
+            *reinterpret_cast<uint4*>(L.q8 + slot * 256 + 16 * e) = make_uint4(q.q[0], q.q[1], q.q[2], q.q[3]);
+            L.bs[slot * 16 + e] = (int16_t)q.bsum;
+            if (e == 0) L.d8[slot] = q.d;
+        }
+    }
+}
+
+}  // namespace spq4k

@@ -1,0 +1,355 @@
+// k_convert.hip — format conversions of the Q4_K path on gfx950:
+//   fp32 -> Q8_K     (quantize_row_q8_K_ref, ggml-quants.c:2692-2729)
+//   Q4_K -> fp32     (dequantize_row_q4_K, ggml-quants.c:1467-1489)
+//   fp32 -> Q4_K     (quantize_row_q4_K_ref + make_qkx2_quants,
+//                     ggml-quants.c:1395-1465, :737-816)
+//   Q4_K . Q8_K      (ggml_vec_dot_q4_K_q8_K shape, one row)
+//   synthetic data   (synth_math.h)
+// Every kernel reproduces the reference's rounding step for step (compiled
+// with -ffp-contract=off, IEEE division and square root), so the outputs are
+// bit-identical to the CPU path.
+#include "q4k_device.h"
+#include "gemv_core.h"
+#include "launch.h"
+#include "synth_math.h"
+
+namespace spq4k {
+
+// ---------------------------------------------------------------------------
+// fp32 -> Q8_K blocks in global memory (292 B each, 4-byte aligned).
+// 16 lanes per block, 16 blocks per 256-thread workgroup.
+__global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x, uint8_t* __restrict__ y,
+                                                           int64_t nblocks) {
+    const int lane = threadIdx.x & 63;
+    const int e = lane & 15;
+    const int64_t blk = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool valid = blk < nblocks;
+    float v[16];
+    if (valid) {
+        const float4* src = reinterpret_cast<const float4*>(x + blk * QK + 16 * e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 a = src[i];
+            v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+    }
+    const Q8Lane q = quantize_q8k_16(v, e);
+    if (!valid) return;
+    uint8_t* o = y + blk * Q8K_BYTES;
+    uint32_t* qs = reinterpret_cast<uint32_t*>(o + 4 + 16 * e);
+    qs[0] = q.q[0]; qs[1] = q.q[1]; qs[2] = q.q[2]; qs[3] = q.q[3];
+    reinterpret_cast<int16_t*>(o + 260)[e] = (int16_t)q.bsum;
+    if (e == 0) *reinterpret_cast<float*>(o) = q.d;
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K -> fp32. Thread i of a block's 32 handles qs bytes 4i..4i+3 of its
+// 32-byte group g = i/8: four low-nibble outputs (sub-block 2g) and four
+// high-nibble outputs (sub-block 2g+1). y = (d*sc)*q - (dmin*m), each step
+// rounded once, as in the reference.
+__global__ __launch_bounds__(256) void dequant_q4k_kernel(const uint8_t* __restrict__ x, float* __restrict__ y,
+                                                          int64_t nblocks) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t blk = gid >> 5;
+    if (blk >= nblocks) return;
+    const int i = (int)(gid & 31);
+    const int g = i >> 3;
+    const int l = 4 * (i & 7);
+    const uint8_t* b = x + blk * Q4K_BYTES;
+    const uint4 h = *reinterpret_cast<const uint4*>(b);
+    const float d = half_bits_to_float(h.x & 0xFFFFu);
+    const float dmin = half_bits_to_float(h.x >> 16);
+    const ScaleMin sm = unpack_scale_min(h.y, h.z, h.w);
+    const uint32_t scw = g < 2 ? sm.sc_lo : sm.sc_hi;
+    const uint32_t mw = g < 2 ? sm.m_lo : sm.m_hi;
+    const int sh = 16 * (g & 1);
+    const float d1 = d * (float)((scw >> sh) & 0xFFu);
+    const float m1 = dmin * (float)((mw >> sh) & 0xFFu);
+    const float d2 = d * (float)((scw >> (sh + 8)) & 0xFFu);
+    const float m2 = dmin * (float)((mw >> (sh + 8)) & 0xFFu);
+    const uint32_t q = *reinterpret_cast<const uint32_t*>(b + 16 + 32 * g + l);
+    float lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t byte = (q >> (8 * k)) & 0xFFu;
+        lo[k] = d1 * (float)(byte & 0x0Fu) - m1;
+        hi[k] = d2 * (float)(byte >> 4) - m2;
+    }
+    float* o = y + blk * QK + 64 * g + l;
+    *reinterpret_cast<float4*>(o) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+    *reinterpret_cast<float4*>(o + 32) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 -> Q4_K. Eight lanes per super-block, lane j fits sub-block j with the
+// reference's weighted search; the eight lanes then agree on d and dmin, lane
+// 0 packs the header and the even lanes pack the nibbles.
+__device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// make_qkx2_quants(32, 15, x, w, L, &the_min, Laux, -1, 0.1, 20, false)
+// (ggml-quants.c:737-816), same operation order.
+__device__ float qkx2_fit32(const float (&x)[32], const float (&w)[32], int (&L)[32], float& neg_min) {
+    constexpr int n = 32, nmax = 15, nstep = 20;
+    const float rmin = -1.0f, rdelta = 0.1f;
+    float lo = x[0], hi = x[0];
+    float sum_w = w[0];
+    float sum_x = sum_w * x[0];
+#pragma unroll
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < lo) lo = x[i];
+        if (x[i] > hi) hi = x[i];
+        sum_w += w[i];
+        sum_x += w[i] * x[i];
+    }
+    if (lo > 0) lo = 0;
+    if (hi == lo) {
+#pragma unroll
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        neg_min = -lo;
+        return 0.0f;
+    }
+    float inv = (float)nmax / (hi - lo);
+    float scale = 1.0f / inv;
+    float best = 0.0f;
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+        const int l = clampi(nearest_int_ref(inv * (x[i] - lo)), 0, nmax);
+        L[i] = l;
+        float diff = scale * (float)l + lo - x[i];
+        diff = diff * diff;
+        best += w[i] * diff;
+    }
+    for (int is = 0; is <= nstep; ++is) {
+        inv = (rmin + rdelta * (float)is + (float)nmax) / (hi - lo);
+        float sl = 0, sl2 = 0, sxl = 0;
+        int La[32];
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+            const int l = clampi(nearest_int_ref(inv * (x[i] - lo)), 0, nmax);
+            La[i] = l;
+            const float fl = (float)l;
+            sl += w[i] * fl;
+            sl2 += w[i] * fl * fl;
+            sxl += w[i] * fl * x[i];
+        }
+        const float D = sum_w * sl2 - sl * sl;
+        if (D > 0) {
+            float cs = (sum_w * sxl - sum_x * sl) / D;
+            float cm = (sl2 * sum_x - sl * sxl) / D;
+            if (cm > 0) {
+                cm = 0;
+                cs = sxl / sl2;
+            }
+            float err = 0;
+#pragma unroll
+            for (int i = 0; i < n; ++i) {
+                float diff = cs * (float)La[i] + cm - x[i];
+                diff = diff * diff;
+                err += w[i] * diff;
+            }
+            if (err < best) {
+#pragma unroll
+                for (int i = 0; i < n; ++i) L[i] = La[i];
+                best = err;
+                scale = cs;
+                lo = cm;
+            }
+        }
+    }
+    neg_min = -lo;
+    return scale;
+}
+
+__device__ __forceinline__ float max8_pos(float v) {
+    // maximum over the 8 lanes of values that are > 0, or +0: the result of the
+    // reference's running `if (v > max) max = v` from max = 0 (NaN never wins)
+    v = (v > 0.0f) ? v : 0.0f;
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        const float o = __shfl_xor(v, off, 8);
+        v = (o > v) ? o : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    const _Float16 h = (_Float16)f;   // v_cvt_f16_f32, round to nearest even
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__global__ __launch_bounds__(256) void quantize_q4k_kernel(const float* __restrict__ xin, uint8_t* __restrict__ y,
+                                                           int64_t nblocks) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t blk = gid >> 3;
+    const int j = (int)(gid & 7);
+    const bool valid = blk < nblocks;   // uniform over each 8-lane group
+
+    float x[32];
+    if (valid) {
+        const float4* src = reinterpret_cast<const float4*>(xin + blk * QK + 32 * j);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 a = src[i];
+            x[4 * i] = a.x; x[4 * i + 1] = a.y; x[4 * i + 2] = a.z; x[4 * i + 3] = a.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = 0.0f;
+    }
+
+    float sum_x2 = 0;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
+    const float av_x = __builtin_sqrtf(sum_x2 / 32);
+    float w[32];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) w[l] = av_x + fabsf(x[l]);
+    int L[32];
+    float neg_min;
+    const float scale = qkx2_fit32(x, w, L, neg_min);
+
+    const float max_scale = max8_pos(scale);
+    const float max_min = max8_pos(neg_min);
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    int ls = nearest_int_ref(inv_scale * scale) & 0xFF;   // (uint8_t) conversion
+    int lm = nearest_int_ref(inv_min * neg_min) & 0xFF;
+    ls = ls < 63 ? ls : 63;
+    lm = lm < 63 ? lm : 63;
+
+    const uint16_t d16 = f32_to_f16_bits(max_scale / 63.f);
+    const uint16_t m16 = f32_to_f16_bits(max_min / 63.f);
+
+    const float d = half_bits_to_float(d16) * (float)ls;
+    if (d != 0.0f) {
+        const float dm = half_bits_to_float(m16) * (float)lm;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) L[i] = clampi(nearest_int_ref((x[i] + dm) / d), 0, 15);
+    }
+
+    // gather (ls, lm) of the 8 sub-blocks into every lane of the group
+    const int mine = ls | (lm << 8);
+    int all[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) all[k] = __shfl(mine, k, 8);
+
+    // pack the low nibbles of this even lane with the high nibbles of lane j+1
+    uint32_t own[8], nbr[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        own[k] = (uint32_t)L[4 * k] | ((uint32_t)L[4 * k + 1] << 8) | ((uint32_t)L[4 * k + 2] << 16) |
+                 ((uint32_t)L[4 * k + 3] << 24);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) nbr[k] = (uint32_t)__shfl_xor((int)own[k], 1, 8);
+
+    if (!valid) return;
+    uint8_t* o = y + blk * Q4K_BYTES;
+    if ((j & 1) == 0) {
+        uint32_t packed[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) packed[k] = own[k] | (nbr[k] << 4);
+        uint4* q = reinterpret_cast<uint4*>(o + 16 + 16 * j);   // qs[32 * (j/2)]
+        q[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        q[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    }
+    if (j == 0) {
+        uint32_t sb[12];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int lsi = all[i] & 0xFF, lmi = all[i] >> 8;
+            const int ls4 = all[i + 4] & 0xFF, lm4 = all[i + 4] >> 8;
+            sb[i] = (uint32_t)(lsi | ((ls4 >> 4) << 6));
+            sb[4 + i] = (uint32_t)(lmi | ((lm4 >> 4) << 6));
+            sb[8 + i] = (uint32_t)((ls4 & 0xF) | ((lm4 & 0xF) << 4));
+        }
+        uint4 hd;
+        hd.x = (uint32_t)d16 | ((uint32_t)m16 << 16);
+        hd.y = sb[0] | (sb[1] << 8) | (sb[2] << 16) | (sb[3] << 24);
+        hd.z = sb[4] | (sb[5] << 8) | (sb[6] << 16) | (sb[7] << 24);
+        hd.w = sb[8] | (sb[9] << 8) | (sb[10] << 16) | (sb[11] << 24);
+        *reinterpret_cast<uint4*>(o) = hd;
+    }
+}
+
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void synth_kernel(float* __restrict__ out, int64_t n, uint64_t seed, int dist,
+                                                    int64_t cols, float mean, float std, float mult,
+                                                    int64_t offset) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        out[i] = spq_synth_value(seed, dist, (uint64_t)(offset + i), (uint64_t)cols, mean, std, mult);
+}
+
+// ---------------------------------------------------------------------------
+// One Q4_K row . one Q8_K row (global 292 B blocks). One wave; four lanes per
+// block as in the GEMV; wave-wide fp32 reduction in a fixed order.
+__global__ __launch_bounds__(64) void vec_dot_q8_kernel(const uint8_t* __restrict__ wx, const uint8_t* __restrict__ q8,
+                                                        int nb, float* __restrict__ out) {
+    const int lane = threadIdx.x;
+    const int l4 = lane & 3;
+    float acc = 0.0f;
+    for (int b = lane >> 2; b < nb; b += 16) {
+        const W4 w = load_w4(wx + (size_t)b * Q4K_BYTES, l4);
+        const BlkC k = block_consts(w.hdr, l4);
+        const Nib n = split_nibbles(w);
+        const uint8_t* yb = q8 + (size_t)b * Q8K_BYTES;
+        const int* qs = reinterpret_cast<const int*>(yb + 4 + 64 * l4);   // 4-byte aligned
+        int S0 = 0, S1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) S0 = dot4(n.lo[i], qs[i], S0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) S1 = dot4(n.hi[i], qs[8 + i], S1);
+        const int16_t* bs = reinterpret_cast<const int16_t*>(yb + 260) + 4 * l4;
+        const int B = k.m0 * ((int)bs[0] + bs[1]) + k.m1 * ((int)bs[2] + bs[3]);
+        const int A = k.sc0 * S0 + k.sc1 * S1;
+        const float d8 = *reinterpret_cast<const float*>(yb);
+        acc = fmaf(k.d * d8, (float)A, acc);
+        acc = fmaf(-(k.dmin * d8), (float)B, acc);
+    }
+    acc = wave_sum_f32(acc);
+    if (lane == 0) *out = acc;
+}
+
+// ---------------------------------------------------------------------------
+hipError_t launch_quantize_q8k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st) {
+    if (nblocks <= 0) return hipSuccess;
+    const int64_t grid = (nblocks + 15) / 16;
+    hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, y, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_q4k(const uint8_t* x, float* y, int64_t nblocks, hipStream_t st) {
+    if (nblocks <= 0) return hipSuccess;
+    const int64_t grid = (nblocks * 32 + 255) / 256;
+    hipLaunchKernelGGL(dequant_q4k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, y, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q4k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st) {
+    if (nblocks <= 0) return hipSuccess;
+    const int64_t grid = (nblocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(quantize_q4k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, y, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_synth(float* out, int64_t n, uint64_t seed, int dist, int64_t cols, float mean, float std,
+                        float outlier_mult, int64_t offset, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    int64_t grid = (n + 255) / 256;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(synth_kernel, dim3((unsigned)grid), dim3(256), 0, st, out, n, seed, dist, cols, mean, std,
+                       outlier_mult, offset);
+    return hipGetLastError();
+}
+
+hipError_t launch_vec_dot_q8(const uint8_t* wx, const uint8_t* q8, int nb, float* out, hipStream_t st) {
+    hipLaunchKernelGGL(vec_dot_q8_kernel, dim3(1), dim3(64), 0, st, wx, q8, nb, out);
+    return hipGetLastError();
+}
+
+}  // namespace spq4k

@@ -1,0 +1,44 @@
+// launch.h — host-side launch interfaces of the gfx950 kernels (internal to
+// libspq4k; the public C ABI is include/spq4k.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace spq4k {
+
+constexpr int GEMV_MAX_SEG = 4;
+
+struct GemvSeg {
+    const uint8_t* W;     // [M][nb] Q4_K blocks, row-major, 16-byte aligned
+    float* Y;             // y[t * y_tstride + r]
+    int64_t y_tstride;
+    int32_t M;
+    int32_t tile_begin;   // first tile index of this segment
+};
+
+struct GemvParams {
+    GemvSeg seg[GEMV_MAX_SEG];
+    int32_t nseg;
+    int32_t nb;           // Q4_K blocks per row (K / 256)
+    const float* X;       // x[t * x_tstride + k], 16-byte aligned rows
+    int64_t x_tstride;
+    int32_t ksplit;       // K splits per row tile
+    int32_t kb_per_split; // blocks per split
+    int32_t chunk_blocks; // blocks staged in LDS at a time
+    float* partial;       // [tiles][ksplit][T][rows] when ksplit > 1
+    uint32_t* counters;   // [tiles], zero between launches
+};
+
+hipError_t launch_gemv(const GemvParams& p, int T, int waves, int ntiles, hipStream_t st);
+hipError_t launch_subblock_sums(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
+
+// element-wise conversions (k_convert.hip)
+hipError_t launch_quantize_q8k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
+hipError_t launch_dequant_q4k(const uint8_t* x, float* y, int64_t nblocks, hipStream_t st);
+hipError_t launch_quantize_q4k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
+hipError_t launch_synth(float* out, int64_t n, uint64_t seed, int dist, int64_t cols, float mean, float std,
+                        float outlier_mult, int64_t offset, hipStream_t st);
+hipError_t launch_vec_dot_q8(const uint8_t* wx, const uint8_t* q8, int nb, float* out, hipStream_t st);
+
+}  // namespace spq4k

@@ -1,0 +1,277 @@
+"""spq4k — Python host binding of libspq4k (the gfx950 Q4_K dequant-matvec).
+
+A thin ctypes layer over the C ABI in include/spq4k.h. The method names
+mirror the reference's operator interface for this path (vendored ggml in
+nihilistau/shannon-prime-burnhard):
+
+    to_float        ggml_type_traits[Q4_K].to_float   (ggml.h:2791-2804)
+    from_float      ggml_type_traits_cpu[Q8_K].from_float (ggml-cpu.h:113-123)
+    quantize_chunk  ggml_quantize_chunk(GGML_TYPE_Q4_K, imatrix=NULL) (ggml.h:2764)
+    vec_dot         ggml_vec_dot_t for Q4_K x Q8_K    (ggml-cpu.h:113)
+    mul_mat         GGML_OP_MUL_MAT                   (ggml.h:1414-1420)
+    mul_mat_id      GGML_OP_MUL_MAT_ID                (ggml.h:1434-1438)
+
+Every call runs on the GPU through libspq4k.so; if the library is missing
+or the device is absent the call raises. There is no CPU fallback.
+Numpy arrays go through the *_host entry points; device work uses raw
+device pointers (e.g. torch tensor .data_ptr()).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import errno
+import os
+
+import numpy as np
+
+QK_K = 256
+Q4K_BLOCK_BYTES = 144
+Q8K_BLOCK_BYTES = 292
+GEMV_MAX_T = 8
+DIST_NORMAL = 0
+DIST_STUDENT_T4 = 1
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libspq4k.so")
+
+_lib = None
+
+
+class Spq4kError(RuntimeError):
+    def __init__(self, fn, rc, msg=""):
+        name = errno.errorcode.get(-rc, str(rc)) if rc < 0 else str(rc)
+        super().__init__(f"{fn} failed: {name} ({rc}) {msg}".rstrip())
+        self.rc = rc
+
+
+def load_library(path: str | None = None):
+    """Load libspq4k.so (built by `make -C shannon-prime-burnhard_amd`)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise FileNotFoundError(f"libspq4k.so not built: {p} (run __graft_entry__.build())")
+    lib = C.CDLL(p)
+    V, I, I64, F, S, U64 = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t, C.c_uint64
+    PV = C.POINTER(C.c_void_p)
+    sig = {
+        "spq4k_init": (I, [I, PV]),
+        "spq4k_free": (None, [V]),
+        "spq4k_set_stream": (I, [V, V]),
+        "spq4k_get_stream": (V, [V]),
+        "spq4k_synchronize": (I, [V]),
+        "spq4k_last_error": (C.c_char_p, [V]),
+        "spq4k_device_count": (I, []),
+        "spq4k_weights_upload": (I, [V, V, I64, I64, I64, PV]),
+        "spq4k_weights_wrap": (I, [V, V, I64, I64, I64, PV]),
+        "spq4k_weights_alloc": (I, [V, I64, I64, I64, PV]),
+        "spq4k_weights_free": (None, [V]),
+        "spq4k_weights_data": (V, [V]),
+        "spq4k_weights_nbytes": (S, [V]),
+        "spq4k_dequant": (I, [V, V, V, I64]),
+        "spq4k_quantize_q8K": (I, [V, V, V, I64]),
+        "spq4k_quantize_q4K": (I, [V, V, V, I64, I64]),
+        "spq4k_vec_dot": (I, [V, I, V, V, V]),
+        "spq4k_dequant_host": (I, [V, V, V, I64]),
+        "spq4k_quantize_q8K_host": (I, [V, V, V, I64]),
+        "spq4k_quantize_q4K_host": (I, [V, V, V, I64, I64]),
+        "spq4k_vec_dot_host": (I, [V, I, V, V, V]),
+        "spq4k_gemv": (I, [V, V, V, V, I64]),
+        "spq4k_gemv_multi": (I, [V, I, V, V, V, I64]),
+        "spq4k_gemm": (I, [V, V, V, V, I64]),
+        "spq4k_mul_mat": (I, [V, V, V, V, I64]),
+        "spq4k_moe": (I, [V, V, V, I64, I64, I64, V, V]),
+        "spq4k_mul_mat_host": (I, [V, V, V, V, I64]),
+        "spq4k_moe_host": (I, [V, V, V, I64, I64, I64, V, V]),
+        "spq4k_subblock_sums": (I, [V, V, I64, I64, V, V]),
+        "spq4k_synth_fill": (I, [V, V, I64, U64, I, I64, F, F, F, I64]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    if isinstance(a, np.ndarray):
+        if not a.flags["C_CONTIGUOUS"]:
+            raise ValueError("array must be C-contiguous")
+        return a.ctypes.data
+    if hasattr(a, "data_ptr"):  # torch tensor
+        return a.data_ptr()
+    raise TypeError(f"cannot take a pointer of {type(a)}")
+
+
+class Weights:
+    """A Q4_K weight matrix (or an E-expert bank) in device memory."""
+
+    def __init__(self, ctx: "Context", handle, M, K, E):
+        self.ctx, self.handle, self.M, self.K, self.E = ctx, handle, M, K, E
+
+    @property
+    def data_ptr(self) -> int:
+        return self.ctx.lib.spq4k_weights_data(self.handle)
+
+    @property
+    def nbytes(self) -> int:
+        return self.ctx.lib.spq4k_weights_nbytes(self.handle)
+
+    def free(self):
+        if self.handle:
+            self.ctx.lib.spq4k_weights_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    """One HIP device + stream (spq4k_ctx)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = C.c_void_p()
+        rc = self.lib.spq4k_init(device, C.byref(h))
+        if rc:
+            raise Spq4kError("spq4k_init", rc)
+        self.handle = h
+        self.device = device
+
+    # -- plumbing
+    def _check(self, fn, rc):
+        if rc:
+            msg = self.lib.spq4k_last_error(self.handle)
+            raise Spq4kError(fn, rc, msg.decode() if msg else "")
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.spq4k_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        """The hipStream_t work is enqueued on (for events and copies)."""
+        return self.lib.spq4k_get_stream(self.handle)
+
+    def set_stream(self, stream_handle: int | None):
+        self._check("spq4k_set_stream", self.lib.spq4k_set_stream(self.handle, stream_handle))
+
+    def synchronize(self):
+        self._check("spq4k_synchronize", self.lib.spq4k_synchronize(self.handle))
+
+    # -- weights
+    def upload(self, q4k: np.ndarray, M: int, K: int, E: int = 1) -> Weights:
+        h = C.c_void_p()
+        self._check("spq4k_weights_upload",
+                    self.lib.spq4k_weights_upload(self.handle, _ptr(np.ascontiguousarray(q4k)), M, K, E, C.byref(h)))
+        return Weights(self, h, M, K, E)
+
+    def wrap(self, dev_ptr: int, M: int, K: int, E: int = 1) -> Weights:
+        h = C.c_void_p()
+        self._check("spq4k_weights_wrap", self.lib.spq4k_weights_wrap(self.handle, dev_ptr, M, K, E, C.byref(h)))
+        return Weights(self, h, M, K, E)
+
+    def alloc_weights(self, M: int, K: int, E: int = 1) -> Weights:
+        h = C.c_void_p()
+        self._check("spq4k_weights_alloc", self.lib.spq4k_weights_alloc(self.handle, M, K, E, C.byref(h)))
+        return Weights(self, h, M, K, E)
+
+    # -- type traits on host arrays (synchronous)
+    def to_float(self, q4k: np.ndarray, k: int) -> np.ndarray:
+        y = np.empty(k, np.float32)
+        self._check("spq4k_dequant_host", self.lib.spq4k_dequant_host(self.handle, _ptr(q4k), _ptr(y), k))
+        return y
+
+    def from_float(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(x.size // QK_K * Q8K_BLOCK_BYTES, np.uint8)
+        self._check("spq4k_quantize_q8K_host",
+                    self.lib.spq4k_quantize_q8K_host(self.handle, _ptr(x), _ptr(y), x.size))
+        return y
+
+    def quantize_chunk(self, src: np.ndarray, nrow: int, n_per_row: int) -> np.ndarray:
+        src = np.ascontiguousarray(src, np.float32).ravel()
+        y = np.zeros(nrow * (n_per_row // QK_K) * Q4K_BLOCK_BYTES, np.uint8)
+        self._check("spq4k_quantize_q4K_host",
+                    self.lib.spq4k_quantize_q4K_host(self.handle, _ptr(src), _ptr(y), nrow, n_per_row))
+        return y
+
+    def vec_dot(self, n: int, vx: np.ndarray, vy: np.ndarray) -> float:
+        s = C.c_float()
+        self._check("spq4k_vec_dot_host",
+                    self.lib.spq4k_vec_dot_host(self.handle, n, C.byref(s), _ptr(vx), _ptr(vy)))
+        return s.value
+
+    def mul_mat(self, W: Weights, X: np.ndarray) -> np.ndarray:
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, W.K)
+        Y = np.empty((X.shape[0], W.M), np.float32)
+        self._check("spq4k_mul_mat_host",
+                    self.lib.spq4k_mul_mat_host(self.handle, W.handle, _ptr(X), _ptr(Y), X.shape[0]))
+        return Y
+
+    def mul_mat_id(self, bank: Weights, X: np.ndarray, ids: np.ndarray) -> np.ndarray:
+        """X: [T, ne11, K] with ne11 in {1, n_used}; ids: [T, n_used] int32 -> Y [T, n_used, M]."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        T, n_used = ids.shape
+        X = np.ascontiguousarray(X, np.float32).reshape(T, -1, bank.K)
+        ne11 = X.shape[1]
+        Y = np.empty((T, n_used, bank.M), np.float32)
+        self._check("spq4k_moe_host", self.lib.spq4k_moe_host(self.handle, bank.handle, _ptr(ids), n_used, ne11, T,
+                                                              _ptr(X), _ptr(Y)))
+        return Y
+
+    def subblock_sums(self, W_dev: int, M: int, K: int, x_dev: int, S_dev: int):
+        self._check("spq4k_subblock_sums", self.lib.spq4k_subblock_sums(self.handle, W_dev, M, K, x_dev, S_dev))
+
+    # -- device-pointer entry points (asynchronous on the context stream)
+    def gemv_dev(self, W: Weights, x_dev: int, y_dev: int, T: int = 1):
+        self._check("spq4k_gemv", self.lib.spq4k_gemv(self.handle, W.handle, x_dev, y_dev, T))
+
+    def gemv_multi_dev(self, Ws, x_dev: int, y_devs, T: int = 1):
+        n = len(Ws)
+        wa = (C.c_void_p * n)(*[w.handle.value if isinstance(w.handle, C.c_void_p) else w.handle for w in Ws])
+        ya = (C.c_void_p * n)(*y_devs)
+        self._check("spq4k_gemv_multi", self.lib.spq4k_gemv_multi(self.handle, n, wa, x_dev, ya, T))
+
+    def gemm_dev(self, W: Weights, X_dev: int, Y_dev: int, T: int):
+        self._check("spq4k_gemm", self.lib.spq4k_gemm(self.handle, W.handle, X_dev, Y_dev, T))
+
+    def mul_mat_dev(self, W: Weights, X_dev: int, Y_dev: int, T: int):
+        self._check("spq4k_mul_mat", self.lib.spq4k_mul_mat(self.handle, W.handle, X_dev, Y_dev, T))
+
+    def moe_dev(self, bank: Weights, ids_dev: int, n_used: int, ne11: int, T: int, X_dev: int, Y_dev: int):
+        self._check("spq4k_moe", self.lib.spq4k_moe(self.handle, bank.handle, ids_dev, n_used, ne11, T, X_dev, Y_dev))
+
+    def dequant_dev(self, vx: int, y: int, k: int):
+        self._check("spq4k_dequant", self.lib.spq4k_dequant(self.handle, vx, y, k))
+
+    def quantize_q8K_dev(self, x: int, vy: int, k: int):
+        self._check("spq4k_quantize_q8K", self.lib.spq4k_quantize_q8K(self.handle, x, vy, k))
+
+    def quantize_q4K_dev(self, src: int, dst: int, nrow: int, n_per_row: int):
+        self._check("spq4k_quantize_q4K", self.lib.spq4k_quantize_q4K(self.handle, src, dst, nrow, n_per_row))
+
+    def synth_fill_dev(self, out: int, n: int, seed: int, dist: int = DIST_NORMAL, cols: int = 0,
+                       mean: float = 0.0, std: float = 1.0, outlier_mult: float = 1.0, offset: int = 0):
+        self._check("spq4k_synth_fill", self.lib.spq4k_synth_fill(self.handle, out, n, seed, dist, cols, mean, std,
+                                                                  outlier_mult, offset))
+
+
+__all__ = ["Context", "Weights", "Spq4kError", "load_library", "LIB_PATH", "QK_K", "Q4K_BLOCK_BYTES",
+           "Q8K_BLOCK_BYTES", "GEMV_MAX_T", "DIST_NORMAL", "DIST_STUDENT_T4"]

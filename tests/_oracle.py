@@ -1,0 +1,212 @@
+"""ctypes access to the CPU checker (oracle/liboracle_q4k.so) and to the
+reference's own ggml CPU library compiled in oracle/_ref/ (test code only)."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(REPO, "oracle", "liboracle_q4k.so")
+REF_DIR = os.path.join(REPO, "oracle", "_ref")
+
+QK_K = 256
+Q4K = 144
+Q8K = 292
+
+V, I, I64, F, U64 = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_uint64
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+class Oracle:
+    """The C restatement of the reference path (oracle/q4k_oracle.c)."""
+
+    def __init__(self, path=ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = C.CDLL(path)
+        for n in ("or_quantize_row_q4K", "or_dequantize_row_q4K", "or_quantize_row_q8K"):
+            getattr(L, n).argtypes = [V, V, I64]
+        L.or_quantize_q4K.argtypes = [V, V, I64, I64]
+        L.or_quantize_q4K.restype = C.c_size_t
+        for n in ("or_vec_dot_generic", "or_vec_dot_avx2order"):
+            getattr(L, n).argtypes = [I, V, V]
+            getattr(L, n).restype = F
+        L.or_vec_dot_exact.argtypes = [I, V, V]
+        L.or_vec_dot_exact.restype = C.c_double
+        L.or_subblock_sums.argtypes = [I, V, V, V]
+        L.or_mul_mat.argtypes = [V, I64, I64, V, I64, V, I]
+        L.or_mul_mat_id.argtypes = [V, I64, I64, I64, V, I64, V, I64, I64, V, I]
+        L.or_mul_mat_id.restype = I
+        L.or_mul_mat_dequant_f64.argtypes = [V, I64, I64, V, I64, V]
+        L.or_synth_fill.argtypes = [V, I64, U64, I, I64, F, F, F, I64]
+        L.or_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.or_fp16_to_fp32.restype = F
+        L.or_fp32_to_fp16.argtypes = [F]
+        L.or_fp32_to_fp16.restype = C.c_uint16
+        L.or_nearest_int.argtypes = [F]
+        L.or_nearest_int.restype = I
+        L.or_scale_min_k4.argtypes = [I, V, V, V]
+        self.L = L
+
+    def quantize_q4K(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(x.size // QK_K * Q4K, np.uint8)
+        self.L.or_quantize_row_q4K(_p(x), _p(y), x.size)
+        return y
+
+    def dequant(self, q: np.ndarray, k: int) -> np.ndarray:
+        y = np.empty(k, np.float32)
+        self.L.or_dequantize_row_q4K(_p(np.ascontiguousarray(q)), _p(y), k)
+        return y
+
+    def quantize_q8K(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(x.size // QK_K * Q8K, np.uint8)
+        self.L.or_quantize_row_q8K(_p(x), _p(y), x.size)
+        return y
+
+    def vec_dot(self, n, qx, qy, order="avx2"):
+        f = self.L.or_vec_dot_avx2order if order == "avx2" else self.L.or_vec_dot_generic
+        return f(n, _p(qx), _p(qy))
+
+    def vec_dot_exact(self, n, qx, qy):
+        return self.L.or_vec_dot_exact(n, _p(qx), _p(qy))
+
+    def subblock_sums(self, n, qx, qy) -> np.ndarray:
+        S = np.zeros(n // QK_K * 8, np.int32)
+        self.L.or_subblock_sums(n, _p(qx), _p(qy), _p(S))
+        return S
+
+    def mul_mat(self, W, M, K, X, order=1):
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+        Y = np.empty((X.shape[0], M), np.float32)
+        self.L.or_mul_mat(_p(W), M, K, _p(X), X.shape[0], _p(Y), order)
+        return Y
+
+    def mul_mat_id(self, bank, M, K, E, X, ids, order=1):
+        ids = np.ascontiguousarray(ids, np.int32)
+        T, k = ids.shape
+        X = np.ascontiguousarray(X, np.float32).reshape(T, -1, K)
+        Y = np.empty((T, k, M), np.float32)
+        rc = self.L.or_mul_mat_id(_p(bank), M, K, E, _p(X), X.shape[1], _p(ids), k, T, _p(Y), order)
+        assert rc == 0
+        return Y
+
+    def mul_mat_f64(self, W, M, K, X):
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+        Y = np.empty((X.shape[0], M), np.float64)
+        self.L.or_mul_mat_dequant_f64(_p(W), M, K, _p(X), X.shape[0], _p(Y))
+        return Y
+
+    def synth(self, n, seed, dist=0, cols=0, mean=0.0, std=1.0, mult=1.0, offset=0) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        self.L.or_synth_fill(_p(out), n, seed, dist, cols, mean, std, mult, offset)
+        return out
+
+
+def cpu_supports_avx512() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            flags = f.read()
+    except OSError:
+        return False
+    return all(t in flags for t in ("avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512cd"))
+
+
+def ref_library_path():
+    for v in (("v4",) if cpu_supports_avx512() else ()) + ("v3",):
+        p = os.path.join(REF_DIR, v, "libggml_ref.so")
+        if os.path.exists(p):
+            return p
+    return None
+
+
+class Ref:
+    """The reference's ggml CPU library built from its own sources (oracle/_ref)."""
+
+    def __init__(self, path=None):
+        path = path or ref_library_path()
+        if not path:
+            raise FileNotFoundError("oracle/_ref not built")
+        L = C.CDLL(path)
+        L.ref_quantize_q4K.argtypes = [V, V, I64, I64]
+        L.ref_quantize_q4K.restype = C.c_size_t
+        L.ref_dequant_q4K.argtypes = [V, V, I64]
+        L.ref_quantize_q8K.argtypes = [V, V, I64]
+        for n in ("ref_vec_dot", "ref_vec_dot_generic"):
+            getattr(L, n).argtypes = [I, V, V]
+            getattr(L, n).restype = F
+        L.ref_mm_create.argtypes = [I, V, V, V, V, V, I64, I]
+        L.ref_mm_create.restype = V
+        L.ref_mmid_create.argtypes = [V, I64, I64, I64, V, I64, V, I64, I64, V, I]
+        L.ref_mmid_create.restype = V
+        L.ref_graph_run.argtypes = [V, I, V]
+        L.ref_graph_run.restype = I
+        L.ref_graph_destroy.argtypes = [V]
+        self.L = L
+        self.path = path
+
+    def quantize_q4K(self, x, nrow, n_per_row):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(nrow * (n_per_row // QK_K) * Q4K, np.uint8)
+        self.L.ref_quantize_q4K(_p(x), _p(y), nrow, n_per_row)
+        return y
+
+    def dequant(self, q, k):
+        y = np.empty(k, np.float32)
+        self.L.ref_dequant_q4K(_p(np.ascontiguousarray(q)), _p(y), k)
+        return y
+
+    def quantize_q8K(self, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(x.size // QK_K * Q8K, np.uint8)
+        self.L.ref_quantize_q8K(_p(x), _p(y), x.size)
+        return y
+
+    def vec_dot(self, n, qx, qy, generic=False):
+        f = self.L.ref_vec_dot_generic if generic else self.L.ref_vec_dot
+        return f(n, _p(qx), _p(qy))
+
+    def mul_mat(self, W, M, K, X, nthreads=1):
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+        T = X.shape[0]
+        Y = np.empty((T, M), np.float32)
+        arr = lambda ctype, vals: (ctype * 1)(*vals)
+        h = self.L.ref_mm_create(1, arr(V, [W.ctypes.data]), arr(I64, [M]), arr(I64, [K]),
+                                 arr(V, [X.ctypes.data]), arr(V, [Y.ctypes.data]), T, nthreads)
+        assert h
+        try:
+            assert self.L.ref_graph_run(h, 1, None) == 0
+        finally:
+            self.L.ref_graph_destroy(h)
+        return Y
+
+    def mul_mat_id(self, bank, M, K, E, X, ids, nthreads=1):
+        ids = np.ascontiguousarray(ids, np.int32)
+        T, k = ids.shape
+        X = np.ascontiguousarray(X, np.float32).reshape(T, -1, K)
+        Y = np.empty((T, k, M), np.float32)
+        h = self.L.ref_mmid_create(_p(bank), M, K, E, _p(X), X.shape[1], _p(ids), k, T, _p(Y), nthreads)
+        assert h
+        try:
+            assert self.L.ref_graph_run(h, 1, None) == 0
+        finally:
+            self.L.ref_graph_destroy(h)
+        return Y
+
+
+def close_enough(a, b, rel=1e-4, abs_=1e-5):
+    """The reference's element tolerance (tests/desktop/test_sp_kernels.cpp:34-48):
+    equal, or |a-b| <= 1e-5, or |a-b| / max(|a|,|b|) <= 1e-4. Returns a bool mask."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    d = np.abs(a - b)
+    scale = np.maximum(np.abs(a), np.abs(b))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        rel_ok = d <= rel * scale
+    return (a == b) | (d <= abs_) | rel_ok
