@@ -7,6 +7,7 @@
 #include <errno.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <hip/hip_runtime.h>
@@ -22,14 +23,11 @@ struct spq4k_ctx {
     int num_cus = 256;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
-    // split-K GEMV
-    float* partial = nullptr;
-    size_t partial_cap = 0;      // floats
-    uint32_t* counters = nullptr;
-    size_t counters_cap = 0;     // entries
     // generic device scratch (Q8_K activations, routing tables)
     uint8_t* scratch = nullptr;
     size_t scratch_cap = 0;
+    int force_bpr = 0;           // tuning override (SPQ4K_GEMV_BPR = 1, 2, 4 or 8)
+    int preq_mode = 0;           // SPQ4K_GEMV_PREQ: 0 auto, 1 always, 2 never
     char err[256] = {0};
 };
 
@@ -72,35 +70,6 @@ int use_device(spq4k_ctx* c) {
     return 0;
 }
 
-int ensure_partial(spq4k_ctx* c, size_t floats, size_t tiles) {
-    if (floats > c->partial_cap) {
-        if (c->partial) hipFree(c->partial);
-        c->partial = nullptr;
-        c->partial_cap = 0;
-        size_t cap = floats < (size_t)(1 << 20) ? (size_t)(1 << 20) : floats;
-        if (hipMalloc(&c->partial, cap * sizeof(float)) != hipSuccess) {
-            c->partial = nullptr;
-            return set_err(c, -ENOMEM, "partial buffer of %zu floats", cap);
-        }
-        c->partial_cap = cap;
-    }
-    if (tiles > c->counters_cap) {
-        // counters must be zero outside a launch; grow only between launches
-        SPQ_HIP(c, hipStreamSynchronize(c->stream));
-        if (c->counters) hipFree(c->counters);
-        c->counters = nullptr;
-        c->counters_cap = 0;
-        size_t cap = tiles < 65536 ? 65536 : tiles;
-        if (hipMalloc(&c->counters, cap * sizeof(uint32_t)) != hipSuccess) {
-            c->counters = nullptr;
-            return set_err(c, -ENOMEM, "counter buffer of %zu", cap);
-        }
-        SPQ_HIP(c, hipMemset(c->counters, 0, cap * sizeof(uint32_t)));
-        c->counters_cap = cap;
-    }
-    return 0;
-}
-
 int ensure_scratch(spq4k_ctx* c, size_t bytes) {
     if (bytes <= c->scratch_cap) return 0;
     SPQ_HIP(c, hipStreamSynchronize(c->stream));
@@ -124,67 +93,83 @@ int check_shape(spq4k_ctx* c, int64_t M, int64_t K, int64_t E) {
     return 0;
 }
 
-// ---- GEMV planning ---------------------------------------------------------
-struct GemvPlan {
-    int waves, ntiles, ksplit, kbps, cb;
-};
+// Quantise T rows of x (row stride x_tstride) into Q8_K planes in the
+// context scratch; Q receives the plane pointers.
+int q8_planes(spq4k_ctx* c, const float* x, int64_t x_tstride, int T, int nb, Q8Planes* Q) {
+    const size_t items = (size_t)T * nb;
+    int rc = ensure_scratch(c, items * 292);
+    if (rc) return rc;
+    int8_t* qs = (int8_t*)c->scratch;
+    int16_t* bs = (int16_t*)(c->scratch + items * 256);
+    float* d = (float*)(c->scratch + items * 288);
+    hipError_t e = launch_quantize_q8k_planes(x, x_tstride, T, nb, qs, bs, d, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "quantize_q8k_planes launch");
+    Q->qs = qs;
+    Q->bs = bs;
+    Q->d = d;
+    return 0;
+}
 
+// ---- GEMV planning ---------------------------------------------------------
 constexpr int LDS_BUDGET = 48 * 1024;
 
-GemvPlan plan_gemv(const spq4k_ctx* c, int64_t total_tiles_64, int nb, int T) {
-    GemvPlan p;
-    p.waves = 4;  // 64 rows per workgroup
-    p.ntiles = (int)total_tiles_64;
-    // enough workgroups for every CU twice over; K splits of >= 2 blocks
-    const int target = 2 * c->num_cus;
-    int ks = 1;
-    if (p.ntiles < target) ks = (target + p.ntiles - 1) / p.ntiles;
-    int max_ks = nb / 2 > 0 ? nb / 2 : 1;
-    if (ks > max_ks) ks = max_ks;
-    if (ks < 1) ks = 1;
-    p.kbps = (nb + ks - 1) / ks;
-    p.ksplit = (nb + p.kbps - 1) / p.kbps;
-    const int cb_max = LDS_BUDGET / (T * 292);
-    p.cb = p.kbps < cb_max ? p.kbps : cb_max;
-    if (p.cb < 1) p.cb = 1;
-    return p;
+// Largest rows-per-workgroup (fewest activation re-quantisations) that still
+// gives at least two workgroups per CU.
+int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
+    if (c->force_bpr) return c->force_bpr;
+    const int64_t target = 2 * (int64_t)c->num_cus;
+    for (int bpr = 1; bpr <= 8; bpr *= 2) {
+        const int rows = gemv_rows_per_tile(bpr);
+        int64_t tiles = 0;
+        for (int i = 0; i < n; ++i) tiles += (M[i] + rows - 1) / rows;
+        if (tiles >= target) return bpr;
+    }
+    return 8;
 }
 
 int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* x, float* const* y, int64_t T) {
     if (n < 1 || n > GEMV_MAX_SEG) return set_err(c, -EINVAL, "gemv: n=%d matrices (1..4)", n);
     if (T < 1 || T > SPQ4K_GEMV_MAX_T) return set_err(c, -EINVAL, "gemv: T=%lld (1..8)", (long long)T);
     if (!x || !aligned(x, 16)) return set_err(c, -EINVAL, "gemv: x null or not 16-byte aligned");
-    const int64_t K = W[0] ? W[0]->K : 0;
-    GemvParams p;
-    memset(&p, 0, sizeof p);
-    int64_t tiles = 0;
+    if (!W[0]) return set_err(c, -EINVAL, "gemv: null weight");
+    const int64_t K = W[0]->K;
+    int64_t Ms[GEMV_MAX_SEG];
     for (int i = 0; i < n; ++i) {
         if (!W[i] || !W[i]->data || !y || !y[i]) return set_err(c, -EINVAL, "gemv: null weight or output");
         if (W[i]->K != K || W[i]->E != 1) return set_err(c, -EINVAL, "gemv: matrices must share K and have E=1");
         if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemv: weights not 16-byte aligned");
+        Ms[i] = W[i]->M;
+    }
+    const int bpr = pick_bpr(c, Ms, n);
+    const int rows = gemv_rows_per_tile(bpr);
+    GemvParams p;
+    memset(&p, 0, sizeof p);
+    int64_t tiles = 0;
+    for (int i = 0; i < n; ++i) {
         p.seg[i].W = W[i]->data;
         p.seg[i].Y = y[i];
         p.seg[i].M = (int32_t)W[i]->M;
         p.seg[i].y_tstride = W[i]->M;
         p.seg[i].tile_begin = (int32_t)tiles;
-        tiles += (W[i]->M + 63) / 64;
+        tiles += (W[i]->M + rows - 1) / rows;
     }
-    if (tiles > (1 << 24)) return set_err(c, -EINVAL, "gemv: too many rows");
+    if (tiles > (1ll << 31) - 1) return set_err(c, -EINVAL, "gemv: too many rows");
     p.nseg = n;
     p.nb = (int32_t)(K / SPQ4K_QK_K);
     p.X = x;
     p.x_tstride = K;
-    const GemvPlan pl = plan_gemv(c, tiles, p.nb, (int)T);
-    p.ksplit = pl.ksplit;
-    p.kb_per_split = pl.kbps;
-    p.chunk_blocks = pl.cb;
-    if (p.ksplit > 1) {
-        int rc = ensure_partial(c, (size_t)tiles * p.ksplit * T * 64, (size_t)tiles);
+    const int cb_max = LDS_BUDGET / ((int)T * 292);
+    p.chunk_blocks = p.nb < cb_max ? p.nb : cb_max;
+    // Quantise the activations once, up front, when re-quantising them in
+    // every workgroup would cost more than the extra launch.
+    bool preq = (int64_t)p.nb * T > 48;
+    if (c->preq_mode == 1) preq = true;
+    if (c->preq_mode == 2) preq = false;
+    if (preq) {
+        int rc = q8_planes(c, x, K, (int)T, p.nb, &p.Q);
         if (rc) return rc;
-        p.partial = c->partial;
-        p.counters = c->counters;
     }
-    hipError_t e = launch_gemv(p, (int)T, pl.waves, (int)tiles, c->stream);
+    hipError_t e = launch_gemv(p, (int)T, bpr, (int)tiles, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "gemv launch");
     return 0;
 }
@@ -214,6 +199,17 @@ int spq4k_init(int device, spq4k_ctx** out) {
         c->num_cus = prop.multiProcessorCount;
     if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) { delete c; return -EIO; }
     c->stream = c->own_stream;
+    if (const char* f = getenv("SPQ4K_GEMV_BPR")) {
+        const int v = atoi(f);
+        if (v == 1 || v == 2 || v == 4 || v == 8) c->force_bpr = v;
+    }
+    if (const char* f = getenv("SPQ4K_GEMV_PREQ")) {
+        const int v = atoi(f);
+        if (v == 1 || v == 2) c->preq_mode = v;
+    }
+    // scratch for Q8_K activation planes: sized for prefill batches up front
+    // so that steady-state calls (and graph capture) never allocate
+    if (ensure_scratch(c, (size_t)16 << 20) != 0) { hipStreamDestroy(c->own_stream); delete c; return -ENOMEM; }
     *out = c;
     return 0;
 }
@@ -222,8 +218,6 @@ void spq4k_free(spq4k_ctx* c) {
     if (!c) return;
     hipSetDevice(c->device);
     if (c->stream) hipStreamSynchronize(c->stream);
-    if (c->partial) hipFree(c->partial);
-    if (c->counters) hipFree(c->counters);
     if (c->scratch) hipFree(c->scratch);
     if (c->own_stream) hipStreamDestroy(c->own_stream);
     delete c;

@@ -1,21 +1,23 @@
 // gemv_core.h — the Q4_K x Q8_K matvec building blocks shared by the dense,
 // grouped and expert-gathered GEMV kernels.
 //
-// Lane mapping (wave64): four lanes per weight row. Lane l4 = lane & 3 of a
-// row's group reads, per 144 B super-block, the 16 B header (d, dmin, scales)
-// and the 32 contiguous bytes qs[32*l4 .. 32*l4+31]. Those bytes carry the
-// whole of sub-blocks j0 = 2*l4 (low nibbles, elements 64*l4 + 0..31) and
-// j1 = 2*l4 + 1 (high nibbles, elements 64*l4 + 32..63), so each lane forms the
-// two exact integer sub-block sums S_{b,j0}, S_{b,j1} with eight v_dot4_i32_i8
-// each, applies its two 6-bit scales and mins, and folds the block into an
-// fp32 accumulator:
+// Lane mapping (wave64): lanes work in quads on a 144 B super-block. Lane
+// l4 = lane & 3 of a quad reads the 16 B header (d, dmin, scales) and the 32
+// contiguous bytes qs[32*l4 .. 32*l4+31]. Those bytes carry the whole of
+// sub-blocks j0 = 2*l4 (low nibbles, elements 64*l4 + 0..31) and j1 = 2*l4 + 1
+// (high nibbles, elements 64*l4 + 32..63), so each lane forms the two exact
+// integer sub-block sums S_{b,j0}, S_{b,j1} with eight v_dot4_i32_i8 each,
+// applies its two 6-bit scales and mins, and folds the block into an fp32
+// accumulator:
 //     acc += (fp16(d) * d8) * (sc0*S0 + sc1*S1) - (fp16(dmin) * d8) * (m0*bs01 + m1*bs23)
 // This is the arithmetic of ggml_vec_dot_q4_K_q8_K
 // (vendor/ggml/src/ggml-cpu/quants.c:645-718, arch/x86/quants.c:1919-1982)
 // with the integer parts exact and only the fp32 summation order changed.
 //
-// Activations are quantised to Q8_K on chip and staged in LDS as
+// Activations are Q8_K, staged in LDS as planes
 //   q8[slot][256] int8 | bsum[slot][16] int16 | d8[slot] f32,  slot = t*CB + block
+// either quantised on chip from fp32 (stage_q8_from_f32) or copied from a
+// Q8_K plane buffer written by quantize_q8k_planes_kernel (stage_q8_from_planes).
 #pragma once
 
 #include "q4k_device.h"
@@ -35,14 +37,6 @@ __device__ __forceinline__ W4 load_w4(const uint8_t* __restrict__ blk, int l4) {
     const uint4* q = reinterpret_cast<const uint4*>(blk + 16 + 32 * l4);
     w.qa = q[0];
     w.qb = q[1];
-    return w;
-}
-
-__device__ __forceinline__ W4 zero_w4() {
-    W4 w;
-    w.hdr = make_uint4(0, 0, 0, 0);
-    w.qa = w.hdr;
-    w.qb = w.hdr;
     return w;
 }
 
@@ -102,6 +96,13 @@ __device__ __forceinline__ Q8Lds q8lds_carve(char* base, int slots) {
     return v;
 }
 
+// Q8_K activations as planes in global memory: T rows of nb blocks.
+struct Q8Planes {
+    const int8_t* qs;    // [T][nb][256], 16-byte aligned
+    const int16_t* bs;   // [T][nb][16]
+    const float* d;      // [T][nb]
+};
+
 // Two integer sub-block sums of one lane against one staged activation block.
 __device__ __forceinline__ void subblock_pair(const Nib& n, const int8_t* q8blk, int l4, int& S0, int& S1) {
     const int4* p = reinterpret_cast<const int4*>(q8blk + 64 * l4);
@@ -128,36 +129,52 @@ __device__ __forceinline__ int min_term(const int16_t* bsblk, int l4, int m0, in
     return m0 * (b0 + b1) + m1 * (b2 + b3);
 }
 
+// One block of one row against T staged activation rows.
+template <int T>
+__device__ __forceinline__ void block_dot(const W4& w, int l4, const Q8Lds& L, int bb, int CB, bool live,
+                                          float (&acc)[T]) {
+    const BlkC k = block_consts(w.hdr, l4);
+    const Nib n = split_nibbles(w);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int slot = t * CB + bb;
+        int S0, S1;
+        subblock_pair(n, L.q8 + slot * 256, l4, S0, S1);
+        int A = k.sc0 * S0 + k.sc1 * S1;
+        int B = min_term(L.bs + slot * 16, l4, k.m0, k.m1);
+        A = live ? A : 0;
+        B = live ? B : 0;
+        const float d8 = L.d8[slot];
+        acc[t] = fmaf(k.d * d8, (float)A, acc[t]);
+        acc[t] = fmaf(-(k.dmin * d8), (float)B, acc[t]);
+    }
+}
+
 // Quantise activation blocks into LDS. Work items are (t, block) pairs,
-// item i -> t = i / nblk, block kb0 + i % nblk. Each 16-lane slice of a wave
+// item i -> t = i / nblk, block kb0 + i % nblk. Each 16-lane row of a wave
 // quantises one item per pass. X rows are 16-byte aligned (checked on host).
 template <int WAVES>
-__device__ __forceinline__ void stage_q8(const float* __restrict__ X, int64_t x_tstride, int T,
-                                         int kb0, int nblk, const Q8Lds& L, int slot_stride) {
+__device__ __forceinline__ void stage_q8_from_f32(const float* __restrict__ X, int64_t x_tstride, int T,
+                                                  int kb0, int nblk, const Q8Lds& L, int slot_stride) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int e = lane & 15;
     const int sub = lane >> 4;  // 0..3
     const int nitems = T * nblk;
     for (int base = 0; base < nitems; base += 4 * WAVES) {
-        const int item = base + wave * 4 + sub;
-        const bool valid = item < nitems;
-        const int t = valid ? item / nblk : 0;
-        const int bb = valid ? item - t * nblk : 0;
+        const int item0 = base + wave * 4 + sub;
+        const bool valid = item0 < nitems;
+        const int item = valid ? item0 : nitems - 1;   // clamp: in-bounds, result discarded
+        const int t = item / nblk;
+        const int bb = item - t * nblk;
         float x[16];
-        if (valid) {
-            const float4* src = reinterpret_cast<const float4*>(X + (int64_t)t * x_tstride +
-                                                                (int64_t)(kb0 + bb) * QK + 16 * e);
+        const float4* src = reinterpret_cast<const float4*>(X + (int64_t)t * x_tstride +
+                                                            (int64_t)(kb0 + bb) * QK + 16 * e);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 v = src[i];
-                x[4 * i + 0] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) x[i] = 0.0f;
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = src[i];
+            x[4 * i + 0] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
         }
-        // all 16 lanes of a slice share `valid`, so the shuffles stay within live lanes
         const Q8Lane q = quantize_q8k_16(x, e);
         if (valid) {
             const int slot = t * slot_stride + bb;
@@ -165,6 +182,25 @@ __device__ __forceinline__ void stage_q8(const float* __restrict__ X, int64_t x_
             L.bs[slot * 16 + e] = (int16_t)q.bsum;
             if (e == 0) L.d8[slot] = q.d;
         }
+    }
+}
+
+// Copy Q8_K planes [t][kb0 .. kb0+nblk) into the LDS layout.
+template <int NT>
+__device__ __forceinline__ void stage_q8_from_planes(const Q8Planes& P, int nb, int T, int kb0, int nblk,
+                                                     const Q8Lds& L, int slot_stride) {
+    const int tid = threadIdx.x;
+    for (int t = 0; t < T; ++t) {
+        // qs: nblk*256 bytes, 16 B per thread per step
+        const uint4* s = reinterpret_cast<const uint4*>(P.qs + ((int64_t)t * nb + kb0) * 256);
+        uint4* d = reinterpret_cast<uint4*>(L.q8 + t * slot_stride * 256);
+        for (int i = tid; i < nblk * 16; i += NT) d[i] = s[i];
+        // bsums: nblk*32 bytes, 4 B per thread per step
+        const uint32_t* sb = reinterpret_cast<const uint32_t*>(P.bs + ((int64_t)t * nb + kb0) * 16);
+        uint32_t* db = reinterpret_cast<uint32_t*>(L.bs + t * slot_stride * 16);
+        for (int i = tid; i < nblk * 8; i += NT) db[i] = sb[i];
+        const float* sd = P.d + (int64_t)t * nb + kb0;
+        for (int i = tid; i < nblk; i += NT) L.d8[t * slot_stride + i] = sd[i];
     }
 }
 

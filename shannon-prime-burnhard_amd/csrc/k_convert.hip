@@ -20,21 +20,16 @@ namespace spq4k {
 // 16 lanes per block, 16 blocks per 256-thread workgroup.
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x, uint8_t* __restrict__ y,
                                                            int64_t nblocks) {
-    const int lane = threadIdx.x & 63;
-    const int e = lane & 15;
-    const int64_t blk = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const bool valid = blk < nblocks;
+    const int e = threadIdx.x & 15;
+    const int64_t blk0 = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool valid = blk0 < nblocks;
+    const int64_t blk = valid ? blk0 : nblocks - 1;   // in-bounds; result discarded
     float v[16];
-    if (valid) {
-        const float4* src = reinterpret_cast<const float4*>(x + blk * QK + 16 * e);
+    const float4* src = reinterpret_cast<const float4*>(x + blk * QK + 16 * e);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 a = src[i];
-            v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+    for (int i = 0; i < 4; ++i) {
+        const float4 a = src[i];
+        v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
     }
     const Q8Lane q = quantize_q8k_16(v, e);
     if (!valid) return;
@@ -43,6 +38,33 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
     qs[0] = q.q[0]; qs[1] = q.q[1]; qs[2] = q.q[2]; qs[3] = q.q[3];
     reinterpret_cast<int16_t*>(o + 260)[e] = (int16_t)q.bsum;
     if (e == 0) *reinterpret_cast<float*>(o) = q.d;
+}
+
+// fp32 rows -> Q8_K planes (qs [T][nb][256], bs [T][nb][16], d [T][nb]): the
+// activation operand of the pre-quantised GEMV/MoE/GEMM paths, one item per
+// (t, block), 16 lanes per item, 16 items per workgroup.
+__global__ __launch_bounds__(256) void quantize_q8k_planes_kernel(const float* __restrict__ x, int64_t x_tstride,
+                                                                  int T, int nb, int8_t* __restrict__ qs,
+                                                                  int16_t* __restrict__ bs, float* __restrict__ d) {
+    const int e = threadIdx.x & 15;
+    const int64_t nitems = (int64_t)T * nb;
+    const int64_t item0 = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool valid = item0 < nitems;
+    const int64_t item = valid ? item0 : nitems - 1;
+    const int64_t t = item / nb;
+    const int64_t b = item - t * nb;
+    const float4* src = reinterpret_cast<const float4*>(x + t * x_tstride + b * QK + 16 * e);
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 a = src[i];
+        v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+    }
+    const Q8Lane q = quantize_q8k_16(v, e);
+    if (!valid) return;
+    *reinterpret_cast<uint4*>(qs + item * 256 + 16 * e) = make_uint4(q.q[0], q.q[1], q.q[2], q.q[3]);
+    bs[item * 16 + e] = (int16_t)q.bsum;
+    if (e == 0) d[item] = q.d;
 }
 
 // ---------------------------------------------------------------------------
@@ -311,7 +333,8 @@ __global__ __launch_bounds__(64) void vec_dot_q8_kernel(const uint8_t* __restric
         acc = fmaf(k.d * d8, (float)A, acc);
         acc = fmaf(-(k.dmin * d8), (float)B, acc);
     }
-    acc = wave_sum_f32(acc);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
     if (lane == 0) *out = acc;
 }
 
@@ -320,6 +343,15 @@ hipError_t launch_quantize_q8k(const float* x, uint8_t* y, int64_t nblocks, hipS
     if (nblocks <= 0) return hipSuccess;
     const int64_t grid = (nblocks + 15) / 16;
     hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, y, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8k_planes(const float* x, int64_t x_tstride, int T, int nb, int8_t* qs, int16_t* bs,
+                                      float* d, hipStream_t st) {
+    const int64_t items = (int64_t)T * nb;
+    if (items <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_q8k_planes_kernel, dim3((unsigned)((items + 15) / 16)), dim3(256), 0, st, x,
+                       x_tstride, T, nb, qs, bs, d);
     return hipGetLastError();
 }
 

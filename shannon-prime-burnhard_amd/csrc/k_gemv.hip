@@ -7,30 +7,34 @@
 // with the CPU path's Q8_K numerics.
 //
 // One launch covers up to four weight matrices that share the same input
-// (e.g. q/k/v or gate/up). Work unit = (row tile of 16*WAVES rows, K split):
-//   1. the workgroup issues the weight loads of its first blocks,
-//   2. quantises its K range of the T input rows to Q8_K into LDS,
-//   3. streams its rows' 144 B blocks and accumulates per lane in fp32,
-//   4. reduces the four lanes of each row; with one K split it stores y,
-//      otherwise it stores a partial and the last workgroup of the tile
-//      (atomic arrival counter) sums the partials in split order and stores y.
-// The arrival counter is reset by that last workgroup, so no per-launch clear
-// is needed and the result does not depend on workgroup timing.
+// (q/k/v or gate/up). A workgroup of WAVES waves owns WAVES * 16/BPR rows and
+// the whole K range:
+//   - 4*BPR lanes work on one row; lane (bsub, l4) takes blocks
+//     b = bsub, bsub + BPR, ... and within each block the 32 qs bytes of
+//     quarter l4 (two whole sub-blocks; see gemv_core.h);
+//   - the workgroup first issues the loads of its first U blocks per lane,
+//     then quantises the T input rows to Q8_K into LDS while they are in
+//     flight, then streams the rest of its rows with U blocks of loads in
+//     flight per lane;
+//   - the 4*BPR lane partials of a row are combined by a butterfly and
+//     stored. No cross-workgroup traffic, no atomics: the result depends
+//     only on the inputs.
+// BPR trades rows per workgroup against redundant activation quantisation:
+// the host picks it so that small matrices still launch >= 2 workgroups
+// per CU and large ones quantise x as few times as possible.
 #include "gemv_core.h"
 #include "launch.h"
 
 namespace spq4k {
 
-template <int T, int WAVES, int U>
+template <int T, int BPR, int WAVES, int U, bool PREQ>
 __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
     extern __shared__ __align__(16) char smem[];
-    constexpr int ROWS = WAVES * 16;
+    constexpr int LPR = 4 * BPR;         // lanes per row
+    constexpr int RPW = 64 / LPR;        // rows per wave
+    constexpr int ROWS = WAVES * RPW;    // rows per workgroup
 
-    const int wg = blockIdx.x;
-    const int tile = wg / p.ksplit;
-    const int split = wg - tile * p.ksplit;
-
-    // segment of this tile
+    const int tile = blockIdx.x;
     int sidx = 0;
 #pragma unroll
     for (int s = 1; s < GEMV_MAX_SEG; ++s)
@@ -44,15 +48,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int l4 = lane & 3;
-    const int grp = lane >> 2;
-    const int row = row0 + wave * 16 + grp;
+    const int bsub = (lane >> 2) & (BPR - 1);
+    const int row = row0 + wave * RPW + lane / LPR;
     const bool row_ok = row < M;
 
     const int nb = p.nb;
-    const int kb0 = split * p.kb_per_split;
-    const int kb1 = min(nb, kb0 + p.kb_per_split);
     const size_t row_bytes = (size_t)nb * Q4K_BYTES;
-    const uint8_t* __restrict__ wrow = W + (size_t)(row_ok ? row : 0) * row_bytes;
+    // rows past M re-read row M-1 (in bounds) and contribute nothing
+    const uint8_t* __restrict__ wrow = W + (size_t)(row_ok ? row : M - 1) * row_bytes;
 
     float acc[T];
 #pragma unroll
@@ -61,96 +64,57 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
     const int CB = p.chunk_blocks;
     const Q8Lds L = q8lds_carve(smem, T * CB);
 
-    for (int c0 = kb0; c0 < kb1; c0 += CB) {
-        const int c1 = min(kb1, c0 + CB);
-        const int nblk = c1 - c0;
+    for (int c0 = 0; c0 < nb; c0 += CB) {
+        const int nblk = min(nb, c0 + CB) - c0;
+        const int niter = (nblk + BPR - 1) / BPR;   // same for every lane
+        const uint8_t* __restrict__ wc = wrow + (size_t)c0 * Q4K_BYTES;
+        auto blk_of = [&](int it) { return min(bsub + BPR * it, nblk - 1); };
 
-        // prefetch the first U blocks of the chunk, then stage activations
-        W4 wr[U];
+        W4 A[U], B[U];
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            wr[u] = (row_ok && u < nblk) ? load_w4(wrow + (size_t)(c0 + u) * Q4K_BYTES, l4) : zero_w4();
+            if (u < niter) A[u] = load_w4(wc + (size_t)blk_of(u) * Q4K_BYTES, l4);
 
         __syncthreads();  // previous chunk's LDS reads are done
-        stage_q8<WAVES>(p.X, p.x_tstride, T, c0, nblk, L, CB);
+        if (PREQ)
+            stage_q8_from_planes<WAVES * 64>(p.Q, nb, T, c0, nblk, L, CB);
+        else
+            stage_q8_from_f32<WAVES>(p.X, p.x_tstride, T, c0, nblk, L, CB);
         __syncthreads();
 
-        for (int b = 0; b < nblk; b += U) {
-            W4 cur[U];
+        for (int i = 0; i < niter; i += 2 * U) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) cur[u] = wr[u];
-            // issue the next group's loads before using this one
+            for (int u = 0; u < U; ++u)
+                if (i + U + u < niter) B[u] = load_w4(wc + (size_t)blk_of(i + U + u) * Q4K_BYTES, l4);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int nbk = b + U + u;
-                wr[u] = (row_ok && nbk < nblk) ? load_w4(wrow + (size_t)(c0 + nbk) * Q4K_BYTES, l4) : zero_w4();
+                const int it = i + u;
+                if (it < niter) {
+                    const int raw = bsub + BPR * it;
+                    block_dot<T>(A[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
+                }
             }
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int bb = b + u;
-                if (bb < nblk) {
-                    const BlkC k = block_consts(cur[u].hdr, l4);
-                    const Nib n = split_nibbles(cur[u]);
+            for (int u = 0; u < U; ++u)
+                if (i + 2 * U + u < niter) A[u] = load_w4(wc + (size_t)blk_of(i + 2 * U + u) * Q4K_BYTES, l4);
 #pragma unroll
-                    for (int t = 0; t < T; ++t) {
-                        const int slot = t * CB + bb;
-                        int S0, S1;
-                        subblock_pair(n, L.q8 + slot * 256, l4, S0, S1);
-                        const int A = k.sc0 * S0 + k.sc1 * S1;
-                        const int B = min_term(L.bs + slot * 16, l4, k.m0, k.m1);
-                        const float d8 = L.d8[slot];
-                        acc[t] = fmaf(k.d * d8, (float)A, acc[t]);
-                        acc[t] = fmaf(-(k.dmin * d8), (float)B, acc[t]);
-                    }
+            for (int u = 0; u < U; ++u) {
+                const int it = i + U + u;
+                if (it < niter) {
+                    const int raw = bsub + BPR * it;
+                    block_dot<T>(B[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
                 }
             }
         }
     }
 
-    // reduce the four lanes of each row
+    // reduce the LPR lanes of each row (DPP, fixed order: deterministic)
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        acc[t] += __shfl_xor(acc[t], 1, 64);
-        acc[t] += __shfl_xor(acc[t], 2, 64);
-    }
-
-    if (p.ksplit == 1) {
-        if (row_ok && l4 == 0) {
+    for (int t = 0; t < T; ++t) acc[t] = group_sum_last<LPR>(acc[t]);
+    if (row_ok && (lane & (LPR - 1)) == LPR - 1) {
 #pragma unroll
-            for (int t = 0; t < T; ++t) Y[(int64_t)t * y_tstride + row] = acc[t];
-        }
-        return;
+        for (int t = 0; t < T; ++t) Y[(int64_t)t * y_tstride + row] = acc[t];
     }
-
-    // split-K: partial[tile][split][t][ROWS]
-    float* part = p.partial + ((size_t)tile * p.ksplit + split) * (size_t)(T * ROWS);
-    const int rit = wave * 16 + grp;
-    if (l4 == 0) {
-#pragma unroll
-        for (int t = 0; t < T; ++t) part[t * ROWS + rit] = acc[t];
-    }
-    __threadfence();
-    __syncthreads();
-    __shared__ int s_last;
-    if (threadIdx.x == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(p.counters + tile, 1u, __ATOMIC_ACQ_REL,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == (unsigned)(p.ksplit - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const float* tbase = p.partial + (size_t)tile * p.ksplit * (size_t)(T * ROWS);
-    for (int i = threadIdx.x; i < T * ROWS; i += WAVES * 64) {
-        const int t = i / ROWS;
-        const int r = row0 + (i - t * ROWS);
-        float s = 0.0f;
-        for (int sp = 0; sp < p.ksplit; ++sp)
-            s += __builtin_nontemporal_load(tbase + (size_t)sp * (T * ROWS) + i);
-        if (r < M) Y[(int64_t)t * y_tstride + r] = s;
-    }
-    if (threadIdx.x == 0)
-        __hip_atomic_store(p.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -171,7 +135,7 @@ __global__ __launch_bounds__(WAVES * 64) void subblock_sums_kernel(const uint8_t
     for (int c0 = 0; c0 < nb; c0 += CB) {
         const int nblk = min(nb, c0 + CB) - c0;
         __syncthreads();
-        stage_q8<WAVES>(X, 0, 1, c0, nblk, L, CB);
+        stage_q8_from_f32<WAVES>(X, 0, 1, c0, nblk, L, CB);
         __syncthreads();
         if (!row_ok) continue;
         for (int bb = 0; bb < nblk; ++bb) {
@@ -187,23 +151,37 @@ __global__ __launch_bounds__(WAVES * 64) void subblock_sums_kernel(const uint8_t
 }
 
 // ---------------------------------------------------------------------------
-template <int T, int WAVES>
-static hipError_t launch_t(const GemvParams& p, int ntiles, hipStream_t st) {
+template <int T, int BPR, bool PREQ>
+static hipError_t launch_tb(const GemvParams& p, int ntiles, hipStream_t st) {
+    constexpr int WAVES = 4;
+    constexpr int U = 2;
     const size_t lds = (size_t)q8lds_bytes(T * p.chunk_blocks);
-    hipLaunchKernelGGL((gemv_q4k_kernel<T, WAVES, 2>), dim3(ntiles * p.ksplit), dim3(WAVES * 64), lds, st, p);
+    hipLaunchKernelGGL((gemv_q4k_kernel<T, BPR, WAVES, U, PREQ>), dim3(ntiles), dim3(WAVES * 64), lds, st, p);
     return hipGetLastError();
 }
 
-hipError_t launch_gemv(const GemvParams& p, int T, int waves, int ntiles, hipStream_t st) {
-#define SPQ_CASE(TT)                                                   \
-    case TT:                                                           \
-        return waves == 2 ? launch_t<TT, 2>(p, ntiles, st) : launch_t<TT, 4>(p, ntiles, st);
-    switch (T) {
-        SPQ_CASE(1) SPQ_CASE(2) SPQ_CASE(3) SPQ_CASE(4)
-        SPQ_CASE(5) SPQ_CASE(6) SPQ_CASE(7) SPQ_CASE(8)
+template <int T, bool PREQ>
+static hipError_t launch_t(const GemvParams& p, int bpr, int ntiles, hipStream_t st) {
+    switch (bpr) {
+        case 1: return launch_tb<T, 1, PREQ>(p, ntiles, st);
+        case 2: return launch_tb<T, 2, PREQ>(p, ntiles, st);
+        case 4: return launch_tb<T, 4, PREQ>(p, ntiles, st);
+        case 8: return launch_tb<T, 8, PREQ>(p, ntiles, st);
         default: return hipErrorInvalidValue;
     }
-#undef SPQ_CASE
+}
+
+int gemv_rows_per_tile(int bpr) { return 4 * (64 / (4 * bpr)); }
+
+hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st) {
+    const bool pq = p.Q.qs != nullptr;
+#define SPQ_T(TT) \
+    case TT: return pq ? launch_t<TT, true>(p, bpr, ntiles, st) : launch_t<TT, false>(p, bpr, ntiles, st);
+    switch (T) {
+        SPQ_T(1) SPQ_T(2) SPQ_T(3) SPQ_T(4) SPQ_T(5) SPQ_T(6) SPQ_T(7) SPQ_T(8)
+        default: return hipErrorInvalidValue;
+    }
+#undef SPQ_T
 }
 
 hipError_t launch_subblock_sums(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st) {

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gemv_core.h"
+
 namespace spq4k {
 
 constexpr int GEMV_MAX_SEG = 4;
@@ -23,18 +25,20 @@ struct GemvParams {
     int32_t nb;           // Q4_K blocks per row (K / 256)
     const float* X;       // x[t * x_tstride + k], 16-byte aligned rows
     int64_t x_tstride;
-    int32_t ksplit;       // K splits per row tile
-    int32_t kb_per_split; // blocks per split
+    Q8Planes Q;           // pre-quantised activations (Q.qs != nullptr) instead of X
     int32_t chunk_blocks; // blocks staged in LDS at a time
-    float* partial;       // [tiles][ksplit][T][rows] when ksplit > 1
-    uint32_t* counters;   // [tiles], zero between launches
 };
 
-hipError_t launch_gemv(const GemvParams& p, int T, int waves, int ntiles, hipStream_t st);
+// rows per workgroup for a lanes-per-row choice of 4*bpr (bpr in 1, 2, 4, 8)
+int gemv_rows_per_tile(int bpr);
+hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st);
 hipError_t launch_subblock_sums(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
 
 // element-wise conversions (k_convert.hip)
 hipError_t launch_quantize_q8k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
+// fp32 rows x[t * x_tstride + k] -> Q8_K planes (T rows of nb blocks)
+hipError_t launch_quantize_q8k_planes(const float* x, int64_t x_tstride, int T, int nb, int8_t* qs, int16_t* bs,
+                                      float* d, hipStream_t st);
 hipError_t launch_dequant_q4k(const uint8_t* x, float* y, int64_t nblocks, hipStream_t st);
 hipError_t launch_quantize_q4k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
 hipError_t launch_synth(float* out, int64_t n, uint64_t seed, int dist, int64_t cols, float mean, float std,

@@ -28,16 +28,10 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
     return (float)h;
 }
 
-// Round to nearest, ties to even, for |v| < 2^22: the value v + 1.5*2^23 has
-// bit pattern 0x4B400000 + round(v). Same result as the reference's
-// nearest_int (ggml-quants.c:559-564) over its valid range.
-__device__ __forceinline__ int nearest_int_small(float v) {
-    float r = v + 12582912.0f;
-    return (int)__float_as_uint(r) - 0x4B400000;
-}
-
-// The reference's nearest_int bit for bit, also outside the valid range
-// (used by the Q4_K encoder, whose call sites clamp the result).
+// The reference's nearest_int (ggml-quants.c:559-564) bit for bit: adding
+// 1.5*2^23 leaves round-to-nearest-even(v) in the low mantissa bits for
+// |v| < 2^22; outside that range the same bit pattern is returned as the
+// reference returns (callers clamp).
 __device__ __forceinline__ int nearest_int_ref(float v) {
     float r = v + 12582912.0f;
     return (int)(__float_as_uint(r) & 0x007FFFFFu) - 0x00400000;
@@ -61,24 +55,55 @@ __device__ __forceinline__ ScaleMin unpack_scale_min(uint32_t s0, uint32_t s1, u
     return r;
 }
 
-__device__ __forceinline__ int byte_of(uint32_t w, int i) {
-    return (int)((w >> (8 * i)) & 0xFFu);
-}
-
 // Signed 4-way int8 dot product with accumulate (v_dot4_i32_i8).
 __device__ __forceinline__ int dot4(int a, int b, int c) {
     return __builtin_amdgcn_sdot4(a, b, c, false);
 }
 
 // -------------------------------------------------------------------------
-// Q8_K quantisation of one 256-value block by 16 lanes (lane e of the 16 owns
-// values 16e .. 16e+15), following quantize_row_q8_K_ref
-// (ggml-quants.c:2692-2729):
+// DPP lane exchange within rows of 16 lanes (gfx9 DPP controls).
+enum : int {
+    DPP_XOR1 = 0xB1,      // quad_perm [1,0,3,2]
+    DPP_XOR2 = 0x4E,      // quad_perm [2,3,0,1]
+    DPP_ROR4 = 0x124,     // row_ror:4
+    DPP_ROR8 = 0x128,     // row_ror:8
+    DPP_SHR4 = 0x114,     // row_shr:4 (lanes 0-3 of a row read 0)
+    DPP_SHR8 = 0x118,     // row_shr:8 (lanes 0-7 of a row read 0)
+    DPP_BCAST15 = 0x142,  // row_bcast:15 (lane 15 of row r -> row r+1)
+    DPP_BCAST31 = 0x143,  // row_bcast:31 (lane 31 -> rows 2 and 3)
+};
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of N lanes (N = 1, 2, 4, 8, 16, 32); the sum is
+// exact in the LAST lane of each group (lane N-1 mod N), other lanes hold
+// partial sums. Fixed combination order: deterministic.
+template <int N>
+__device__ __forceinline__ float group_sum_last(float v) {
+    if (N >= 2) v += dpp_f32<DPP_XOR1>(v);
+    if (N >= 4) v += dpp_f32<DPP_XOR2>(v);
+    if (N >= 8) v += dpp_f32<DPP_SHR4>(v);     // lanes 4-7 (12-15) += lanes 0-3 (8-11)
+    if (N >= 16) v += dpp_f32<DPP_SHR8>(v);    // lane 15 += lane 7
+    if (N >= 32) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_BCAST15, 0xA, 0xF, false));
+    return v;
+}
+
+// -------------------------------------------------------------------------
+// Q8_K quantisation of one 256-value block by an aligned 16-lane row of the
+// wave (lane e of the 16 owns values 16e .. 16e+15), following
+// quantize_row_q8_K_ref (ggml-quants.c:2692-2729):
 //   the first value of largest |x| (ties -> lowest index) gives max, with sign;
-//   iscale = -127/max; q = min(127, nearest_int(iscale*x)); d = 1/iscale;
-//   bsums[e] = sum of the 16 q of lane e. An all-zero (or all-NaN) block gives
-//   d = 0, q = 0 and bsums = 0.
-// The 16 lanes must be an aligned 16-lane slice of the wave.
+//   iscale = -127/max; q = min(127, nearest_int(iscale*x)) stored as int8;
+//   d = 1/iscale; bsums[e] = sum of the 16 stored q of lane e.
+// An all-zero (or all-NaN) block gives d = 0, q = 0 and bsums = 0.
 struct Q8Lane {
     uint32_t q[4];   // 16 int8 values, little-endian
     int bsum;
@@ -92,17 +117,26 @@ __device__ __forceinline__ Q8Lane quantize_q8k_16(const float (&x)[16], int e) {
     for (int i = 0; i < 16; ++i) {
         const uint32_t bits = __float_as_uint(x[i]);
         uint32_t ab = bits & 0x7FFFFFFFu;
-        if (ab > 0x7F800000u) ab = 0;  // NaN never wins (its |x| > amax is false)
-        const uint32_t lo = ((uint32_t)(255 - (16 * e + i)) << 1) | (bits >> 31);
-        // strict '>' on |x| keeps the first index on ties; lo breaks ties the same way
-        if (ab > best_hi || (ab == best_hi && lo > best_lo)) { best_hi = ab; best_lo = lo; }
+        ab = ab > 0x7F800000u ? 0u : ab;  // NaN never wins (|NaN| > amax is false)
+        // within a lane later indices only replace on a strictly larger |x|
+        const bool take = ab > best_hi;
+        best_hi = take ? ab : best_hi;
+        best_lo = take ? (((uint32_t)(255 - (16 * e + i)) << 1) | (bits >> 31)) : best_lo;
     }
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-        const uint32_t oh = __shfl_xor(best_hi, off, 16);
-        const uint32_t ol = __shfl_xor(best_lo, off, 16);
-        if (oh > best_hi || (oh == best_hi && ol > best_lo)) { best_hi = oh; best_lo = ol; }
+    // lexicographic max of (hi, lo) over the 16 lanes
+#define SPQ_KEYMAX(CTRL)                                                  \
+    {                                                                     \
+        const uint32_t oh = dpp_u32<CTRL>(best_hi);                       \
+        const uint32_t ol = dpp_u32<CTRL>(best_lo);                       \
+        const bool t = (oh > best_hi) || (oh == best_hi && ol > best_lo); \
+        best_hi = t ? oh : best_hi;                                       \
+        best_lo = t ? ol : best_lo;                                       \
     }
+    SPQ_KEYMAX(DPP_XOR1)
+    SPQ_KEYMAX(DPP_XOR2)
+    SPQ_KEYMAX(DPP_ROR4)
+    SPQ_KEYMAX(DPP_ROR8)
+#undef SPQ_KEYMAX
     Q8Lane r;
     if (best_hi == 0) {
         r.q[0] = r.q[1] = r.q[2] = r.q[3] = 0;
@@ -132,14 +166,6 @@ __device__ __forceinline__ Q8Lane quantize_q8k_16(const float (&x)[16], int e) {
     r.bsum = s;
     r.d = 1.0f / iscale;
     return r;
-}
-
-// -------------------------------------------------------------------------
-// Wave-level helpers
-__device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
 }
 
 }  // namespace spq4k

@@ -42,6 +42,12 @@ def _lib():
         ("hipGetErrorString", C.c_char_p, [I]),
         ("hipGetDeviceCount", I, [C.POINTER(I)]),
         ("hipMemGetInfo", I, [C.POINTER(S), C.POINTER(S)]),
+        ("hipStreamBeginCapture", I, [V, I]),
+        ("hipStreamEndCapture", I, [V, C.POINTER(V)]),
+        ("hipGraphInstantiate", I, [C.POINTER(V), V, V, V, S]),
+        ("hipGraphLaunch", I, [V, V]),
+        ("hipGraphExecDestroy", I, [V]),
+        ("hipGraphDestroy", I, [V]),
     ):
         f = getattr(h, name)
         f.restype = res
@@ -137,5 +143,49 @@ class Event:
         try:
             if self.h:
                 _lib().hipEventDestroy(self.h)
+        except Exception:
+            pass
+
+
+class Graph:
+    """A HIP graph captured from the work enqueued on `stream` inside
+    `with Graph.capture(stream) as g:`; replay with g.launch()."""
+
+    CAPTURE_RELAXED = 2
+
+    def __init__(self, stream):
+        self.stream = stream
+        self.graph = None
+        self.exec = None
+
+    @classmethod
+    def capture(cls, stream):
+        return cls(stream)
+
+    def __enter__(self):
+        check(_lib().hipStreamBeginCapture(self.stream, self.CAPTURE_RELAXED), "hipStreamBeginCapture")
+        return self
+
+    def __exit__(self, et, ev, tb):
+        g = C.c_void_p()
+        rc = _lib().hipStreamEndCapture(self.stream, C.byref(g))
+        if et is not None:
+            return False
+        check(rc, "hipStreamEndCapture")
+        self.graph = g.value
+        e = C.c_void_p()
+        check(_lib().hipGraphInstantiate(C.byref(e), self.graph, None, None, 0), "hipGraphInstantiate")
+        self.exec = e.value
+        return False
+
+    def launch(self):
+        check(_lib().hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
+
+    def __del__(self):
+        try:
+            if self.exec:
+                _lib().hipGraphExecDestroy(self.exec)
+            if self.graph:
+                _lib().hipGraphDestroy(self.graph)
         except Exception:
             pass
