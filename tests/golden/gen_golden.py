@@ -1,0 +1,133 @@
+#!/usr/bin/env python3
+"""Writes tests/golden/q4k_golden.npz from the reference's own ggml CPU code.
+
+The reference (vendor/ggml of nihilistau/shannon-prime-burnhard) is compiled
+from its sources by oracle/Makefile (`make -C oracle ref`) into oracle/_ref;
+this script calls it through oracle/ref_driver.c and stores small input/output
+vectors. Run only where /root/reference exists; the .npz travels with the
+repository and pins the CPU oracle (tests/test_oracle_golden.py).
+
+Contents (all produced by the reference):
+  enc_x / enc_q    quantize_q4_K (ggml_quantize_chunk, imatrix NULL) bytes
+  deq_q / deq_y    dequantize_row_q4_K
+  q8_x  / q8_y     quantize_row_q8_K blocks; a block with max |x| = 0 keeps
+                   the caller's zero-initialised bsums (the reference does not
+                   write them in that branch)
+  vd_q4 / vd_q8 / vd_K / vd_avx2 / vd_generic
+                   ggml_vec_dot_q4_K_q8_K (x86 kernel) and its portable
+                   ggml_vec_dot_q4_K_q8_K_generic, one row per case
+  mm_*             GGML_OP_MUL_MAT through ggml_graph_compute (1 thread)
+  mmid_*           GGML_OP_MUL_MAT_ID through ggml_graph_compute (1 thread)
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(HERE))
+from _oracle import Ref, ref_library_path  # noqa: E402
+
+QK = 256
+
+
+def encoder_inputs(rng):
+    rows = []
+    rows.append((rng.standard_normal((8, 4096)) * 0.02).astype(np.float32))        # the BASELINE distribution
+    t = (rng.standard_t(4, size=(4, 5120)) * 0.02).astype(np.float32)
+    t[:, ::53] *= 8.0                                                                 # outlier columns
+    rows.append(t)
+    edge = []
+    edge.append(np.zeros(QK, np.float32))                                             # all zero
+    edge.append(np.full(QK, 0.25, np.float32))                                        # constant positive
+    edge.append(np.full(QK, -0.25, np.float32))                                       # constant negative
+    s = np.zeros(QK, np.float32); s[100] = 3.0; edge.append(s)                        # single spike
+    edge.append(np.abs(rng.standard_normal(QK)).astype(np.float32))                   # all >= 0 (min clamps to 0)
+    edge.append(-np.abs(rng.standard_normal(QK)).astype(np.float32))                  # all <= 0
+    edge.append((rng.standard_normal(QK) * 1e-6).astype(np.float32))                  # tiny
+    edge.append((rng.standard_normal(QK) * 100.0).astype(np.float32))                 # large
+    z = rng.standard_normal(QK).astype(np.float32); z[32:64] = 0.0; edge.append(z)    # one zero sub-block
+    a = np.linspace(-1, 1, QK, dtype=np.float32); edge.append(a)                      # ramp
+    rows.append(np.stack(edge))
+    return np.concatenate([r.ravel() for r in rows]).astype(np.float32)
+
+
+def q8_inputs(rng):
+    c = [rng.standard_normal(QK * 8).astype(np.float32)]
+    c.append(np.zeros(QK, np.float32))
+    t = np.zeros(QK, np.float32); t[5] = 2.0; t[77] = -2.0; c.append(t)               # tie, first is +
+    t = np.zeros(QK, np.float32); t[5] = -2.0; t[77] = 2.0; c.append(t)               # tie, first is -
+    c.append(((np.arange(QK) - 128) * 0.5).astype(np.float32))                        # many .5 products
+    c.append((rng.standard_normal(QK) * 1e-20).astype(np.float32))
+    c.append((rng.standard_normal(QK) * 1e20).astype(np.float32))
+    c.append(np.full(QK, 1.0, np.float32))
+    return np.concatenate(c)
+
+
+def main():
+    if ref_library_path() is None:
+        sys.exit("oracle/_ref is not built (make -C oracle ref)")
+    ref = Ref()
+    rng = np.random.default_rng(0xDEADBEEF)
+    out = {}
+
+    x = encoder_inputs(rng)
+    out["enc_x"] = x
+    out["enc_q"] = ref.quantize_q4K(x, 1, x.size)
+
+    q = out["enc_q"].reshape(-1, 144).copy()
+    rb = rng.integers(0, 256, size=(64, 144), dtype=np.uint8)
+    rb[:, 1] &= 0xBF            # finite fp16 d
+    rb[:, 3] &= 0xBF            # finite fp16 dmin
+    q = np.concatenate([q, rb]).ravel()
+    out["deq_q"] = q
+    out["deq_y"] = ref.dequant(q, q.size // 144 * QK)
+
+    xq = q8_inputs(rng)
+    out["q8_x"] = xq
+    out["q8_y"] = ref.quantize_q8K(xq)
+
+    # vec_dot cases: K in {256, 768, 4096, 27648}
+    vq4, vq8, vK, va, vg = [], [], [], [], []
+    for K, n in ((256, 8), (768, 8), (4096, 8), (27648, 4)):
+        for i in range(n):
+            w = ref.quantize_q4K((rng.standard_normal(K) * 0.02).astype(np.float32), 1, K)
+            a = ref.quantize_q8K(rng.standard_normal(K).astype(np.float32))
+            vq4.append(w); vq8.append(a); vK.append(K)
+            va.append(ref.vec_dot(K, w, a)); vg.append(ref.vec_dot(K, w, a, generic=True))
+    out["vd_q4"] = np.concatenate(vq4)
+    out["vd_q8"] = np.concatenate(vq8)
+    out["vd_K"] = np.array(vK, np.int64)
+    out["vd_avx2"] = np.array(va, np.float32)
+    out["vd_generic"] = np.array(vg, np.float32)
+
+    # GGML_OP_MUL_MAT
+    M, K = 64, 512
+    W = ref.quantize_q4K((rng.standard_normal((M, K)) * 0.02).astype(np.float32), M, K)
+    out["mm_W"] = W
+    out["mm_MK"] = np.array([M, K], np.int64)
+    for T in (1, 3, 8, 17):
+        X = rng.standard_normal((T, K)).astype(np.float32)
+        out[f"mm_X{T}"] = X
+        out[f"mm_Y{T}"] = ref.mul_mat(W, M, K, X)
+
+    # GGML_OP_MUL_MAT_ID
+    E, M, K, T = 8, 32, 512, 3
+    bank = ref.quantize_q4K((rng.standard_normal((E * M, K)) * 0.02).astype(np.float32), E * M, K)
+    out["mmid_bank"] = bank
+    out["mmid_EMK"] = np.array([E, M, K], np.int64)
+    for n_used, ne11 in ((2, 1), (4, 4)):
+        ids = np.stack([rng.permutation(E)[:n_used] for _ in range(T)]).astype(np.int32)
+        X = rng.standard_normal((T, ne11, K)).astype(np.float32)
+        tag = f"{n_used}_{ne11}"
+        out[f"mmid_ids_{tag}"] = ids
+        out[f"mmid_X_{tag}"] = X
+        out[f"mmid_Y_{tag}"] = ref.mul_mat_id(bank, M, K, E, X, ids)
+
+    path = os.path.join(HERE, "q4k_golden.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)/1024:.0f} KiB, {len(out)} arrays) using {ref.path}")
+
+
+if __name__ == "__main__":
+    main()

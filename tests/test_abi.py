@@ -1,0 +1,58 @@
+"""The C ABI library: it builds, loads without a GPU, exports every entry
+point that include/*.h declares, and reports a missing device as -ENODEV."""
+import ctypes as C
+import errno
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(REPO, "shannon-prime-burnhard_amd", "libspq4k.so")
+HEADERS = [os.path.join(REPO, "include", h) for h in sorted(os.listdir(os.path.join(REPO, "include")))
+           if h.endswith(".h")]
+
+
+def declared_functions():
+    names = []
+    for h in HEADERS:
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(spq4k_[a-zA-Z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_headers_declare_entry_points():
+    names = declared_functions()
+    assert "spq4k_gemv" in names and "spq4k_moe" in names and "spq4k_gemm" in names
+    assert len(names) >= 30
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(LIB), "build libspq4k.so first (__graft_entry__.build())"
+    lib = C.CDLL(LIB)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"declared in include/*.h but not exported: {missing}"
+
+
+def test_no_device_is_an_error_not_a_fallback():
+    lib = C.CDLL(LIB)
+    lib.spq4k_device_count.restype = C.c_int
+    if lib.spq4k_device_count() > 0:
+        pytest.skip("a GPU is present")
+    h = C.c_void_p()
+    lib.spq4k_init.argtypes = [C.c_int, C.POINTER(C.c_void_p)]
+    assert lib.spq4k_init(0, C.byref(h)) == -errno.ENODEV
+    assert not h.value
+
+
+def test_header_compiles_as_c():
+    import subprocess
+    import tempfile
+    src = "#include <spq4k.h>\n#include <spq4k_synth.h>\nint main(void){return SPQ4K_QK_K == 256 ? 0 : 1;}\n"
+    with tempfile.TemporaryDirectory() as d:
+        f = os.path.join(d, "t.c")
+        open(f, "w").write(src)
+        r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(REPO, "include"), f, "-o",
+                            os.path.join(d, "t")], capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
