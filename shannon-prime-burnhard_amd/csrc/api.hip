@@ -460,8 +460,61 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
               int64_t T, const float* X, float* Y) {
     int rc = use_device(c);
     if (rc) return rc;
-    (void)bank; (void)ids; (void)n_used; (void)ne11; (void)T; (void)X; (void)Y;
-    return set_err(c, -ENOSYS, "moe: not built yet");
+    if (!bank || !bank->data || !ids || !X || !Y) return set_err(c, -EINVAL, "moe: null argument");
+    if (T < 1 || n_used < 1 || n_used > bank->E || (ne11 != 1 && ne11 != n_used))
+        return set_err(c, -EINVAL, "moe: T=%lld n_used=%lld ne11=%lld", (long long)T, (long long)n_used,
+                       (long long)ne11);
+    if (!aligned(X, 16) || !aligned(bank->data, 16) || !aligned(ids, 4))
+        return set_err(c, -EINVAL, "moe: misaligned pointer");
+    if (bank->E > 4096 || T * n_used > (1 << 24)) return set_err(c, -EINVAL, "moe: too many experts or pairs");
+    const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
+    const int64_t rows = T * ne11, n_pairs = T * n_used;
+    // scratch: Q8_K planes | routing tables
+    const size_t q8_bytes = ((size_t)rows * nb * 292 + 255) & ~(size_t)255;
+    const size_t route_bytes = (size_t)(1 + 3 * E + n_pairs) * sizeof(int32_t);
+    rc = ensure_scratch(c, q8_bytes + route_bytes);
+    if (rc) return rc;
+    MoeParams p;
+    memset(&p, 0, sizeof p);
+    const size_t items = (size_t)rows * nb;
+    int8_t* qs = (int8_t*)c->scratch;
+    int16_t* bs = (int16_t*)(c->scratch + items * 256);
+    float* d = (float*)(c->scratch + items * 288);
+    int32_t* rt = (int32_t*)(c->scratch + q8_bytes);
+    p.route.n_act = rt;
+    p.route.act = rt + 1;
+    p.route.act_off = rt + 1 + E;
+    p.route.act_cnt = rt + 1 + 2 * E;
+    p.route.pairs = rt + 1 + 3 * E;
+    hipError_t e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe quantize launch");
+    e = launch_moe_route(ids, (int)n_pairs, E, p.route, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe route launch");
+    p.bank = bank->data;
+    p.expert_bytes = (size_t)M * nb * SPQ4K_Q4K_BLOCK_BYTES;
+    p.Y = Y;
+    p.Q.qs = qs;
+    p.Q.bs = bs;
+    p.Q.d = d;
+    p.M = M;
+    p.nb = nb;
+    p.n_used = (int)n_used;
+    p.ne11 = (int)ne11;
+    // pairs per expert are at most T: chunk width TC, and rows per tile from
+    // the number of experts that can be active
+    const int tc = T >= 8 ? 8 : (T >= 4 ? 4 : (T >= 2 ? 2 : 1));
+    const int64_t max_act = n_pairs < E ? n_pairs : E;
+    int64_t Mtot[1] = {(int64_t)M * max_act};
+    const int bpr = pick_bpr(c, Mtot, 1);
+    const int rows_per_tile = gemv_rows_per_tile(bpr);
+    p.tiles_per_expert = (M + rows_per_tile - 1) / rows_per_tile;
+    const int cb_max = LDS_BUDGET / (tc * 292);
+    p.chunk_blocks = nb < cb_max ? nb : cb_max;
+    const int64_t grid = max_act * p.tiles_per_expert;
+    if (grid > (1ll << 31) - 1) return set_err(c, -EINVAL, "moe: grid too large");
+    e = launch_moe_gemv(p, tc, bpr, (int)grid, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe gemv launch");
+    return 0;
 }
 
 int spq4k_mul_mat_host(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
@@ -486,6 +539,8 @@ int spq4k_moe_host(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, 
     if (rc) return rc;
     if (!bank || !ids || !X || !Y || T < 1 || n_used < 1 || (ne11 != 1 && ne11 != n_used))
         return set_err(c, -EINVAL, "moe_host: bad arguments");
+    for (int64_t i = 0; i < T * n_used; ++i)
+        if (ids[i] < 0 || ids[i] >= bank->E) return set_err(c, -EINVAL, "moe_host: expert id %d out of range", ids[i]);
     const size_t ni = (size_t)T * n_used * sizeof(int32_t);
     const size_t nx = (size_t)T * ne11 * bank->K * sizeof(float);
     const size_t ny = (size_t)T * n_used * bank->M * sizeof(float);

@@ -150,6 +150,57 @@ __device__ __forceinline__ void block_dot(const W4& w, int l4, const Q8Lds& L, i
     }
 }
 
+// Streams one row's super-blocks (this lane's share: blocks bsub, bsub + BPR,
+// ... of each LDS chunk) against the staged activations and accumulates.
+// `stage(c0, nblk)` must fill the LDS slots [t * CB + 0 .. nblk) for the
+// chunk of blocks [c0, c0 + nblk); it is called by the whole workgroup between
+// barriers. Loads are software-pipelined in two register sets of U blocks;
+// addresses are clamped in bounds and out-of-range blocks contribute zero.
+template <int T, int BPR, int U, typename StageFn>
+__device__ __forceinline__ void stream_row(const uint8_t* __restrict__ wrow, bool row_ok, int l4, int bsub, int nb,
+                                           int CB, const Q8Lds& L, float (&acc)[T], StageFn stage) {
+    for (int c0 = 0; c0 < nb; c0 += CB) {
+        const int nblk = min(nb, c0 + CB) - c0;
+        const int niter = (nblk + BPR - 1) / BPR;   // same for every lane
+        const uint8_t* __restrict__ wc = wrow + (size_t)c0 * Q4K_BYTES;
+        auto blk_of = [&](int it) { return min(bsub + BPR * it, nblk - 1); };
+
+        W4 A[U], B[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (u < niter) A[u] = load_w4(wc + (size_t)blk_of(u) * Q4K_BYTES, l4);
+
+        __syncthreads();  // previous chunk's LDS reads are done
+        stage(c0, nblk);
+        __syncthreads();
+
+        for (int i = 0; i < niter; i += 2 * U) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (i + U + u < niter) B[u] = load_w4(wc + (size_t)blk_of(i + U + u) * Q4K_BYTES, l4);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int it = i + u;
+                if (it < niter) {
+                    const int raw = bsub + BPR * it;
+                    block_dot<T>(A[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (i + 2 * U + u < niter) A[u] = load_w4(wc + (size_t)blk_of(i + 2 * U + u) * Q4K_BYTES, l4);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int it = i + U + u;
+                if (it < niter) {
+                    const int raw = bsub + BPR * it;
+                    block_dot<T>(B[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
+                }
+            }
+        }
+    }
+}
+
 // Quantise activation blocks into LDS. Work items are (t, block) pairs,
 // item i -> t = i / nblk, block kb0 + i % nblk. Each 16-lane row of a wave
 // quantises one item per pass. X rows are 16-byte aligned (checked on host).

@@ -63,50 +63,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
 
     const int CB = p.chunk_blocks;
     const Q8Lds L = q8lds_carve(smem, T * CB);
-
-    for (int c0 = 0; c0 < nb; c0 += CB) {
-        const int nblk = min(nb, c0 + CB) - c0;
-        const int niter = (nblk + BPR - 1) / BPR;   // same for every lane
-        const uint8_t* __restrict__ wc = wrow + (size_t)c0 * Q4K_BYTES;
-        auto blk_of = [&](int it) { return min(bsub + BPR * it, nblk - 1); };
-
-        W4 A[U], B[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (u < niter) A[u] = load_w4(wc + (size_t)blk_of(u) * Q4K_BYTES, l4);
-
-        __syncthreads();  // previous chunk's LDS reads are done
+    stream_row<T, BPR, U>(wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int c0, int nblk) {
         if (PREQ)
             stage_q8_from_planes<WAVES * 64>(p.Q, nb, T, c0, nblk, L, CB);
         else
             stage_q8_from_f32<WAVES>(p.X, p.x_tstride, T, c0, nblk, L, CB);
-        __syncthreads();
-
-        for (int i = 0; i < niter; i += 2 * U) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (i + U + u < niter) B[u] = load_w4(wc + (size_t)blk_of(i + U + u) * Q4K_BYTES, l4);
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int it = i + u;
-                if (it < niter) {
-                    const int raw = bsub + BPR * it;
-                    block_dot<T>(A[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (i + 2 * U + u < niter) A[u] = load_w4(wc + (size_t)blk_of(i + 2 * U + u) * Q4K_BYTES, l4);
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int it = i + U + u;
-                if (it < niter) {
-                    const int raw = bsub + BPR * it;
-                    block_dot<T>(B[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
-                }
-            }
-        }
-    }
+    });
 
     // reduce the LPR lanes of each row (DPP, fixed order: deterministic)
 #pragma unroll

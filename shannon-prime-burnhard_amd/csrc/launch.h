@@ -34,6 +34,29 @@ int gemv_rows_per_tile(int bpr);
 hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st);
 hipError_t launch_subblock_sums(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
 
+// expert-gathered matvec (k_moe.hip)
+struct MoeRoute {
+    int32_t* n_act;     // [1] number of experts with at least one pair
+    int32_t* act;       // [E] active expert ids, ascending
+    int32_t* act_off;   // [E] first pair of active expert a in `pairs`
+    int32_t* act_cnt;   // [E] pairs of active expert a
+    int32_t* pairs;     // [T * n_used] pair index t * n_used + s, grouped by expert
+};
+
+struct MoeParams {
+    MoeRoute route;
+    const uint8_t* bank;     // E experts of [M][nb] Q4_K blocks
+    size_t expert_bytes;
+    float* Y;                // [T][n_used][M]
+    Q8Planes Q;              // Q8_K of the T * ne11 input rows
+    int32_t M, nb, n_used, ne11;
+    int32_t tiles_per_expert;
+    int32_t chunk_blocks;
+};
+
+hipError_t launch_moe_route(const int32_t* ids, int n_pairs, int E, const MoeRoute& r, hipStream_t st);
+hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st);
+
 // element-wise conversions (k_convert.hip)
 hipError_t launch_quantize_q8k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
 // fp32 rows x[t * x_tstride + k] -> Q8_K planes (T rows of nb blocks)
