@@ -447,8 +447,21 @@ int spq4k_gemv_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const f
 int spq4k_gemm(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
     int rc = use_device(c);
     if (rc) return rc;
-    (void)W; (void)X; (void)Y; (void)T;
-    return set_err(c, -ENOSYS, "gemm: not built yet");
+    if (!W || !W->data || !X || !Y || T < 1 || W->E != 1) return set_err(c, -EINVAL, "gemm: bad arguments");
+    if (!aligned(X, 16) || !aligned(W->data, 16)) return set_err(c, -EINVAL, "gemm: misaligned pointer");
+    if (T > (1 << 20)) return set_err(c, -EINVAL, "gemm: T too large");
+    GemmParams p;
+    memset(&p, 0, sizeof p);
+    p.W = W->data;
+    p.Y = Y;
+    p.M = (int32_t)W->M;
+    p.T = (int32_t)T;
+    p.nb = (int32_t)(W->K / SPQ4K_QK_K);
+    rc = q8_planes(c, X, W->K, (int)T, p.nb, &p.Q);
+    if (rc) return rc;
+    hipError_t e = launch_gemm(p, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "gemm launch");
+    return 0;
 }
 
 int spq4k_mul_mat(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {

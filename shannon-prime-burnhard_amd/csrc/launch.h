@@ -57,6 +57,15 @@ struct MoeParams {
 hipError_t launch_moe_route(const int32_t* ids, int n_pairs, int E, const MoeRoute& r, hipStream_t st);
 hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st);
 
+// prefill matmul on matrix cores (k_gemm.hip)
+struct GemmParams {
+    const uint8_t* W;   // [M][nb] Q4_K
+    Q8Planes Q;         // Q8_K of the T input rows
+    float* Y;           // [T][M]
+    int32_t M, T, nb;
+};
+hipError_t launch_gemm(const GemmParams& p, hipStream_t st);
+
 // element-wise conversions (k_convert.hip)
 hipError_t launch_quantize_q8k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
 // fp32 rows x[t * x_tstride + k] -> Q8_K planes (T rows of nb blocks)
