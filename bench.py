@@ -300,6 +300,72 @@ def run_single(args, M, K, T, dist, outlier, name):
     print(json.dumps({"metric": f"{name} effective HBM GB/s", "value": round(gbs, 2), "unit": "GB/s",
                       "us_per_call": round(ms * 1e3, 3), "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2),
                       "config": {"workload": name, "M": M, "K": K, "T": T, "weight_copies": copies}}), flush=True)
+    for w in ws:
+        w.free()
+    syn.tmp.free()
+    ctx.close()
+
+
+def run_prefill(args):
+    """the 8B layer shapes as a prefill matmul, T tokens."""
+    ctx = spq4k.Context(0)
+    syn = Synth(ctx, FFN * HID)
+    shapes = [("q", HID, HID), ("k", KV, HID), ("v", KV, HID), ("o", HID, HID), ("gate", FFN, HID),
+              ("up", FFN, HID), ("down", HID, FFN)]
+    ws = [syn.weights(M, K, 300 + i) for i, (_, M, K) in enumerate(shapes)]
+    for T in (16, 128, 512):
+        X = {K: syn.activations(T * K, 9 + K) for K in (HID, FFN)}
+        Y = DeviceArray(T * FFN)
+        with Graph.capture(ctx.stream) as g:
+            for w, (_, M, K) in zip(ws, shapes):
+                ctx.gemm_dev(w, X[K].ptr, Y.ptr, T)
+        ms = time_graph(ctx, g, max(5, args.steps // 5), 2)
+        flops = 2 * T * sum(M * K for _, M, K in shapes)
+        wbytes = sum(q4k_bytes(M, K) for _, M, K in shapes)
+        abytes = wbytes + 4 * T * sum(M + K for _, M, K in shapes)
+        tops = flops / (ms * 1e-3) / 1e12
+        print(json.dumps({"metric": f"Q4_K prefill matmul, one 8B layer, T={T}", "value": round(tops, 2),
+                          "unit": "TOP/s (int8)", "us_per_layer": round(ms * 1e3, 2),
+                          "pct_of_int8_mfma_peak": round(tops / 5000 * 100, 2),
+                          "effective_GBps": round(abytes / (ms * 1e-3) / 1e9, 1),
+                          "tokens_per_s": round(T / (ms * 1e-3 * (LAYERS + 0)), 1),
+                          "config": {"workload": f"8B layer (q,k,v,o,gate,up,down) x T={T} tokens, Q4_K",
+                                     "T": T}}), flush=True)
+    ctx.close()
+
+
+def run_moe(args):
+    """128 experts (gate/up 768x2048, down 2048x768), top-8, T = 1..32."""
+    ctx = spq4k.Context(0)
+    E, k = 128, 8
+    syn = Synth(ctx, E * 768 * 2048)
+    banks = {}
+    for name, M, K in (("gate", 768, 2048), ("up", 768, 2048), ("down", 2048, 768)):
+        w = ctx.alloc_weights(M, K, E)
+        ctx.synth_fill_dev(syn.tmp.ptr, E * M * K, 500 + M, spq4k.DIST_NORMAL, K, 0.0, 0.02, 1.0, 0)
+        ctx.quantize_q4K_dev(syn.tmp.ptr, w.data_ptr, E * M, K)
+        banks[name] = (w, M, K)
+    rng = np.random.default_rng(3)
+    for T in (1, 4, 8, 32):
+        logits = rng.standard_normal((T, E)).astype(np.float32)
+        ids = np.argsort(-logits, axis=1, kind="stable")[:, :k].astype(np.int32)
+        idd = DeviceArray.from_host(ids)
+        xg = syn.activations(T * 2048, 11)
+        xd = syn.activations(T * k * 768, 12)
+        Y = DeviceArray(T * k * 2048)
+        with Graph.capture(ctx.stream) as g:
+            w, M, K = banks["gate"]; ctx.moe_dev(w, idd.ptr, k, 1, T, xg.ptr, Y.ptr)
+            w, M, K = banks["up"]; ctx.moe_dev(w, idd.ptr, k, 1, T, xg.ptr, Y.ptr)
+            w, M, K = banks["down"]; ctx.moe_dev(w, idd.ptr, k, k, T, xd.ptr, Y.ptr)
+        ms = time_graph(ctx, g, max(10, args.steps), 3)
+        uniq = len(np.unique(ids))
+        wbytes = uniq * sum(q4k_bytes(M, K) for (_, M, K) in banks.values())
+        abytes = wbytes + 4 * T * k * (2048 + 768) * 2 + 4 * T * k * (768 + 2048)
+        gbs = abytes / (ms * 1e-3) / 1e9
+        print(json.dumps({"metric": f"Q4_K MoE expert matvec (gate+up+down), T={T}", "value": round(gbs, 1),
+                          "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
+                          "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2), "unique_experts": uniq,
+                          "config": {"workload": "30B-A3B-like MoE layer, 128 experts, top-8", "T": T}}), flush=True)
     ctx.close()
 
 
@@ -308,7 +374,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek"])
+    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -319,6 +385,10 @@ def main():
         run_decode8b(args)
     elif args.config == "gemv4096":
         run_single(args, 4096, 4096, 1, spq4k.DIST_NORMAL, 1.0, "Q4_K GEMV 4096x4096 T=1")
+    elif args.config == "prefill":
+        run_prefill(args)
+    elif args.config == "moe":
+        run_moe(args)
     elif args.config == "largek":
         for (M, K) in ((5120, 27648), (27648, 5120)):
             for T in (1, 4, 8):

@@ -28,11 +28,12 @@ struct spq4k_ctx {
     size_t scratch_cap = 0;
     int force_bpr = 0;           // tuning override (SPQ4K_GEMV_BPR = 1, 2, 4 or 8)
     int preq_mode = 0;           // SPQ4K_GEMV_PREQ: 0 auto, 1 always, 2 never
+    int no_fixed = 0;            // SPQ4K_GEMV_GENERIC=1: skip the compile-time-K kernels
     char err[256] = {0};
 };
 
 struct spq4k_weights {
-    spq4k_ctx* ctx = nullptr;
+    int device = 0;              // weights may outlive the context that made them
     uint8_t* data = nullptr;
     bool owned = false;
     int64_t M = 0, K = 0, E = 0;
@@ -67,13 +68,14 @@ int use_device(spq4k_ctx* c) {
     if (!c) return -EINVAL;
     hipError_t e = hipSetDevice(c->device);
     if (e != hipSuccess) return hip_fail(c, e, "hipSetDevice");
+    (void)hipGetLastError();   // launch errors below are this call's own
     return 0;
 }
 
 int ensure_scratch(spq4k_ctx* c, size_t bytes) {
     if (bytes <= c->scratch_cap) return 0;
     SPQ_HIP(c, hipStreamSynchronize(c->stream));
-    if (c->scratch) hipFree(c->scratch);
+    if (c->scratch) (void)hipFree(c->scratch);
     c->scratch = nullptr;
     c->scratch_cap = 0;
     size_t cap = bytes < (size_t)(4 << 20) ? (size_t)(4 << 20) : bytes;
@@ -138,6 +140,7 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         if (!W[i] || !W[i]->data || !y || !y[i]) return set_err(c, -EINVAL, "gemv: null weight or output");
         if (W[i]->K != K || W[i]->E != 1) return set_err(c, -EINVAL, "gemv: matrices must share K and have E=1");
         if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemv: weights not 16-byte aligned");
+        if (W[i]->device != c->device) return set_err(c, -EINVAL, "gemv: weights live on another device");
         Ms[i] = W[i]->M;
     }
     const int bpr = pick_bpr(c, Ms, n);
@@ -169,6 +172,7 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         int rc = q8_planes(c, x, K, (int)T, p.nb, &p.Q);
         if (rc) return rc;
     }
+    p.fixed_ok = c->no_fixed ? 0 : 1;
     hipError_t e = launch_gemv(p, (int)T, bpr, (int)tiles, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "gemv launch");
     return 0;
@@ -203,23 +207,24 @@ int spq4k_init(int device, spq4k_ctx** out) {
         const int v = atoi(f);
         if (v == 1 || v == 2 || v == 4 || v == 8) c->force_bpr = v;
     }
+    if (const char* f = getenv("SPQ4K_GEMV_GENERIC")) c->no_fixed = atoi(f) == 1;
     if (const char* f = getenv("SPQ4K_GEMV_PREQ")) {
         const int v = atoi(f);
         if (v == 1 || v == 2) c->preq_mode = v;
     }
     // scratch for Q8_K activation planes: sized for prefill batches up front
     // so that steady-state calls (and graph capture) never allocate
-    if (ensure_scratch(c, (size_t)16 << 20) != 0) { hipStreamDestroy(c->own_stream); delete c; return -ENOMEM; }
+    if (ensure_scratch(c, (size_t)16 << 20) != 0) { (void)hipStreamDestroy(c->own_stream); delete c; return -ENOMEM; }
     *out = c;
     return 0;
 }
 
 void spq4k_free(spq4k_ctx* c) {
     if (!c) return;
-    hipSetDevice(c->device);
-    if (c->stream) hipStreamSynchronize(c->stream);
-    if (c->scratch) hipFree(c->scratch);
-    if (c->own_stream) hipStreamDestroy(c->own_stream);
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->scratch) (void)hipFree(c->scratch);
+    if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }
 
@@ -248,7 +253,7 @@ static int weights_new(spq4k_ctx* c, int64_t M, int64_t K, int64_t E, spq4k_weig
     if (rc) return rc;
     spq4k_weights* w = new (std::nothrow) spq4k_weights();
     if (!w) return -ENOMEM;
-    w->ctx = c;
+    w->device = c->device;
     w->M = M;
     w->K = K;
     w->E = E;
@@ -298,9 +303,9 @@ int spq4k_weights_wrap(spq4k_ctx* c, const void* dev, int64_t M, int64_t K, int6
 void spq4k_weights_free(spq4k_weights* w) {
     if (!w) return;
     if (w->owned && w->data) {
-        hipSetDevice(w->ctx->device);
-        hipStreamSynchronize(w->ctx->stream);
-        hipFree(w->data);
+        // hipFree waits for outstanding work on the device that uses the buffer
+        (void)hipSetDevice(w->device);
+        (void)hipFree(w->data);
     }
     delete w;
 }
@@ -354,7 +359,7 @@ int spq4k_vec_dot(spq4k_ctx* c, int n, float* s, const void* vx, const void* vy)
 namespace {
 struct DevBuf {
     void* p = nullptr;
-    ~DevBuf() { if (p) hipFree(p); }
+    ~DevBuf() { if (p) (void)hipFree(p); }
 };
 }  // namespace
 

@@ -152,26 +152,31 @@ __device__ __forceinline__ void block_dot(const W4& w, int l4, const Q8Lds& L, i
 
 // Streams one row's super-blocks (this lane's share: blocks bsub, bsub + BPR,
 // ... of each LDS chunk) against the staged activations and accumulates.
-// `stage(c0, nblk)` must fill the LDS slots [t * CB + 0 .. nblk) for the
-// chunk of blocks [c0, c0 + nblk); it is called by the whole workgroup between
-// barriers. Loads are software-pipelined in two register sets of U blocks;
+// Staging of chunk [c0, c0 + nblk) is split in two so that its global loads
+// are issued before the weight prefetch: `pre(c0, nblk)` issues this lane's
+// first activation loads and returns them in registers, `fin(c0, nblk, r)`
+// turns them into the LDS slots [t * CB + 0 .. nblk) (whole workgroup, between
+// barriers). Loads return in issue order, so an activation load queued behind
+// the weight prefetch would stall staging until every weight byte had landed.
+// Weight loads are software-pipelined in two register sets of U blocks;
 // addresses are clamped in bounds and out-of-range blocks contribute zero.
-template <int T, int BPR, int U, typename StageFn>
+template <int T, int BPR, int U, typename PreFn, typename FinFn>
 __device__ __forceinline__ void stream_row(const uint8_t* __restrict__ wrow, bool row_ok, int l4, int bsub, int nb,
-                                           int CB, const Q8Lds& L, float (&acc)[T], StageFn stage) {
+                                           int CB, const Q8Lds& L, float (&acc)[T], PreFn pre, FinFn fin) {
     for (int c0 = 0; c0 < nb; c0 += CB) {
         const int nblk = min(nb, c0 + CB) - c0;
         const int niter = (nblk + BPR - 1) / BPR;   // same for every lane
         const uint8_t* __restrict__ wc = wrow + (size_t)c0 * Q4K_BYTES;
         auto blk_of = [&](int it) { return min(bsub + BPR * it, nblk - 1); };
 
+        auto xr = pre(c0, nblk);
         W4 A[U], B[U];
 #pragma unroll
         for (int u = 0; u < U; ++u)
             if (u < niter) A[u] = load_w4(wc + (size_t)blk_of(u) * Q4K_BYTES, l4);
 
         __syncthreads();  // previous chunk's LDS reads are done
-        stage(c0, nblk);
+        fin(c0, nblk, xr);
         __syncthreads();
 
         for (int i = 0; i < niter; i += 2 * U) {
@@ -204,36 +209,115 @@ __device__ __forceinline__ void stream_row(const uint8_t* __restrict__ wrow, boo
 // Quantise activation blocks into LDS. Work items are (t, block) pairs,
 // item i -> t = i / nblk, block kb0 + i % nblk. Each 16-lane row of a wave
 // quantises one item per pass. X rows are 16-byte aligned (checked on host).
+// stage_f32_load issues this lane's loads for the first pass; stage_f32_fin
+// quantises them and runs any further passes.
+struct XRegs {
+    float x[16];
+};
+
 template <int WAVES>
-__device__ __forceinline__ void stage_q8_from_f32(const float* __restrict__ X, int64_t x_tstride, int T,
-                                                  int kb0, int nblk, const Q8Lds& L, int slot_stride) {
+__device__ __forceinline__ void stage_f32_item(int pass_base, int nitems, int nblk, int& t, int& bb, bool& valid) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int e = lane & 15;
-    const int sub = lane >> 4;  // 0..3
-    const int nitems = T * nblk;
-    for (int base = 0; base < nitems; base += 4 * WAVES) {
-        const int item0 = base + wave * 4 + sub;
-        const bool valid = item0 < nitems;
-        const int item = valid ? item0 : nitems - 1;   // clamp: in-bounds, result discarded
-        const int t = item / nblk;
-        const int bb = item - t * nblk;
-        float x[16];
-        const float4* src = reinterpret_cast<const float4*>(X + (int64_t)t * x_tstride +
-                                                            (int64_t)(kb0 + bb) * QK + 16 * e);
+    const int item0 = pass_base + wave * 4 + (lane >> 4);
+    valid = item0 < nitems;
+    const int item = valid ? item0 : nitems - 1;   // clamp: in-bounds, result discarded
+    t = item / nblk;
+    bb = item - t * nblk;
+}
+
+__device__ __forceinline__ XRegs load_x16(const float* __restrict__ X, int64_t x_tstride, int t, int kb) {
+    XRegs r;
+    const int e = threadIdx.x & 15;
+    const float4* src = reinterpret_cast<const float4*>(X + (int64_t)t * x_tstride + (int64_t)kb * QK + 16 * e);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 v = src[i];
-            x[4 * i + 0] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
-        }
-        const Q8Lane q = quantize_q8k_16(x, e);
-        if (valid) {
-            const int slot = t * slot_stride + bb;
-            *reinterpret_cast<uint4*>(L.q8 + slot * 256 + 16 * e) = make_uint4(q.q[0], q.q[1], q.q[2], q.q[3]);
-            L.bs[slot * 16 + e] = (int16_t)q.bsum;
-            if (e == 0) L.d8[slot] = q.d;
-        }
+    for (int i = 0; i < 4; ++i) {
+        const float4 v = src[i];
+        r.x[4 * i + 0] = v.x; r.x[4 * i + 1] = v.y; r.x[4 * i + 2] = v.z; r.x[4 * i + 3] = v.w;
     }
+    return r;
+}
+
+__device__ __forceinline__ void store_q8_item(const XRegs& r, bool valid, int slot, const Q8Lds& L) {
+    const int e = threadIdx.x & 15;
+    const Q8Lane q = quantize_q8k_16(r.x, e);
+    if (valid) {
+        *reinterpret_cast<uint4*>(L.q8 + slot * 256 + 16 * e) = make_uint4(q.q[0], q.q[1], q.q[2], q.q[3]);
+        L.bs[slot * 16 + e] = (int16_t)q.bsum;
+        if (e == 0) L.d8[slot] = q.d;
+    }
+}
+
+template <int WAVES>
+__device__ __forceinline__ XRegs stage_f32_load(const float* __restrict__ X, int64_t x_tstride, int T, int kb0,
+                                                int nblk) {
+    int t, bb;
+    bool valid;
+    stage_f32_item<WAVES>(0, T * nblk, nblk, t, bb, valid);
+    return load_x16(X, x_tstride, t, kb0 + bb);
+}
+
+template <int WAVES>
+__device__ __forceinline__ void stage_f32_fin(const float* __restrict__ X, int64_t x_tstride, int T, int kb0,
+                                              int nblk, const Q8Lds& L, int slot_stride, const XRegs& first) {
+    const int nitems = T * nblk;
+    int t, bb;
+    bool valid;
+    stage_f32_item<WAVES>(0, nitems, nblk, t, bb, valid);
+    store_q8_item(first, valid, t * slot_stride + bb, L);
+    for (int base = 4 * WAVES; base < nitems; base += 4 * WAVES) {
+        stage_f32_item<WAVES>(base, nitems, nblk, t, bb, valid);
+        const XRegs r = load_x16(X, x_tstride, t, kb0 + bb);
+        store_q8_item(r, valid, t * slot_stride + bb, L);
+    }
+}
+
+template <int WAVES>
+__device__ __forceinline__ void stage_q8_from_f32(const float* __restrict__ X, int64_t x_tstride, int T, int kb0,
+                                                  int nblk, const Q8Lds& L, int slot_stride) {
+    stage_f32_fin<WAVES>(X, x_tstride, T, kb0, nblk, L, slot_stride, stage_f32_load<WAVES>(X, x_tstride, T, kb0, nblk));
+}
+
+// Compile-time-K variant of stream_row for T = 1 decode with on-chip
+// quantisation (NB blocks per row, all of K staged at once). With the trip
+// counts known, every load is unconditional and the loop is fully unrolled
+// into a rotating pipeline of D register slots, so the compiler's s_waitcnt
+// values are exact: the staging waits only for the activation loads (issued
+// first, all passes), never for weight loads that are still in flight.
+template <int NB, int BPR, int D, int WAVES>
+__device__ __forceinline__ float stream_row_fixed(const uint8_t* __restrict__ wrow, bool row_ok, int l4, int bsub,
+                                                  const float* __restrict__ X, const Q8Lds& L) {
+    constexpr int NIT = (NB + BPR - 1) / BPR;
+    constexpr int DD = NIT < D ? NIT : D;
+    constexpr int PASSES = (NB + 4 * WAVES - 1) / (4 * WAVES);
+    auto blk_of = [&](int it) { return min(bsub + BPR * it, NB - 1); };
+
+    // 1. activation loads for every staging pass
+    XRegs xr[PASSES];
+    int xt[PASSES], xb[PASSES];
+    bool xv[PASSES];
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+        stage_f32_item<WAVES>(ps * 4 * WAVES, NB, NB, xt[ps], xb[ps], xv[ps]);
+        xr[ps] = load_x16(X, 0, 0, xb[ps]);
+    }
+    // 2. weight pipeline fill
+    W4 buf[DD];
+#pragma unroll
+    for (int u = 0; u < DD; ++u) buf[u] = load_w4(wrow + (size_t)blk_of(u) * Q4K_BYTES, l4);
+    // 3. quantise into LDS while the weights are in flight
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) store_q8_item(xr[ps], xv[ps], xb[ps], L);
+    __syncthreads();
+    // 4. stream
+    float acc[1] = {0.0f};
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int raw = bsub + BPR * it;
+        block_dot<1>(buf[it % DD], l4, L, min(raw, NB - 1), NB, row_ok && raw < NB, acc);
+        if (it + DD < NIT) buf[it % DD] = load_w4(wrow + (size_t)blk_of(it + DD) * Q4K_BYTES, l4);
+    }
+    return acc[0];
 }
 
 // Copy Q8_K planes [t][kb0 .. kb0+nblk) into the LDS layout.

@@ -63,12 +63,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
 
     const int CB = p.chunk_blocks;
     const Q8Lds L = q8lds_carve(smem, T * CB);
-    stream_row<T, BPR, U>(wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int c0, int nblk) {
-        if (PREQ)
-            stage_q8_from_planes<WAVES * 64>(p.Q, nb, T, c0, nblk, L, CB);
-        else
-            stage_q8_from_f32<WAVES>(p.X, p.x_tstride, T, c0, nblk, L, CB);
-    });
+    if (PREQ) {
+        stream_row<T, BPR, U>(
+            wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int, int) { return 0; },
+            [&](int c0, int nblk, int) { stage_q8_from_planes<WAVES * 64>(p.Q, nb, T, c0, nblk, L, CB); });
+    } else {
+        stream_row<T, BPR, U>(
+            wrow, row_ok, l4, bsub, nb, CB, L, acc,
+            [&](int c0, int nblk) { return stage_f32_load<WAVES>(p.X, p.x_tstride, T, c0, nblk); },
+            [&](int c0, int nblk, const XRegs& xr) {
+                stage_f32_fin<WAVES>(p.X, p.x_tstride, T, c0, nblk, L, CB, xr);
+            });
+    }
 
     // reduce the LPR lanes of each row (DPP, fixed order: deterministic)
 #pragma unroll
@@ -77,6 +83,36 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
 #pragma unroll
         for (int t = 0; t < T; ++t) Y[(int64_t)t * y_tstride + row] = acc[t];
     }
+}
+
+// T = 1 decode kernel specialised on the number of blocks per row (see
+// stream_row_fixed); same tiling, lane mapping and arithmetic as above.
+template <int NB, int BPR, int WAVES, int D>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_fixed_kernel(GemvParams p) {
+    __shared__ __align__(16) char smem[q8lds_bytes(NB)];
+    constexpr int LPR = 4 * BPR;
+    constexpr int RPW = 64 / LPR;
+    constexpr int ROWS = WAVES * RPW;
+    const int tile = blockIdx.x;
+    int sidx = 0;
+#pragma unroll
+    for (int s = 1; s < GEMV_MAX_SEG; ++s)
+        if (s < p.nseg && tile >= p.seg[s].tile_begin) sidx = s;
+    const uint8_t* __restrict__ W = p.seg[sidx].W;
+    float* __restrict__ Y = p.seg[sidx].Y;
+    const int M = p.seg[sidx].M;
+    const int row0 = (tile - p.seg[sidx].tile_begin) * ROWS;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int l4 = lane & 3;
+    const int bsub = (lane >> 2) & (BPR - 1);
+    const int row = row0 + wave * RPW + lane / LPR;
+    const bool row_ok = row < M;
+    const uint8_t* __restrict__ wrow = W + (size_t)(row_ok ? row : M - 1) * (NB * Q4K_BYTES);
+    const Q8Lds L = q8lds_carve(smem, NB);
+    float acc = stream_row_fixed<NB, BPR, D, WAVES>(wrow, row_ok, l4, bsub, p.X, L);
+    acc = group_sum_last<LPR>(acc);
+    if (row_ok && (lane & (LPR - 1)) == LPR - 1) Y[row] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -135,8 +171,29 @@ static hipError_t launch_t(const GemvParams& p, int bpr, int ntiles, hipStream_t
 
 int gemv_rows_per_tile(int bpr) { return 4 * (64 / (4 * bpr)); }
 
+template <int NB>
+static hipError_t launch_fixed(const GemvParams& p, int bpr, int ntiles, hipStream_t st) {
+    constexpr int WAVES = 4, D = 4;
+    switch (bpr) {
+        case 1: hipLaunchKernelGGL((gemv_q4k_fixed_kernel<NB, 1, WAVES, D>), dim3(ntiles), dim3(256), 0, st, p); break;
+        case 2: hipLaunchKernelGGL((gemv_q4k_fixed_kernel<NB, 2, WAVES, D>), dim3(ntiles), dim3(256), 0, st, p); break;
+        case 4: hipLaunchKernelGGL((gemv_q4k_fixed_kernel<NB, 4, WAVES, D>), dim3(ntiles), dim3(256), 0, st, p); break;
+        case 8: hipLaunchKernelGGL((gemv_q4k_fixed_kernel<NB, 8, WAVES, D>), dim3(ntiles), dim3(256), 0, st, p); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st) {
     const bool pq = p.Q.qs != nullptr;
+    // decode fast path: one token, activations quantised on chip, the K of
+    // the 8B-class shapes (4096 and 12288) known at compile time
+    // (the fully unrolled variants with few lanes per row need too many
+    // registers; those shapes have enough rows for the generic kernel)
+    if (T == 1 && !pq && p.fixed_ok) {
+        if (p.nb == 16 && bpr >= 2) return launch_fixed<16>(p, bpr, ntiles, st);
+        if (p.nb == 48 && bpr >= 4) return launch_fixed<48>(p, bpr, ntiles, st);
+    }
 #define SPQ_T(TT) \
     case TT: return pq ? launch_t<TT, true>(p, bpr, ntiles, st) : launch_t<TT, false>(p, bpr, ntiles, st);
     switch (T) {

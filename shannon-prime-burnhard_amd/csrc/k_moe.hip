@@ -101,7 +101,8 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeParams p) {
         float acc[TC];
 #pragma unroll
         for (int t = 0; t < TC; ++t) acc[t] = 0.0f;
-        stream_row<TC, BPR, U>(wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int c0, int nblk) {
+        stream_row<TC, BPR, U>(wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int, int) { return 0; },
+                               [&](int c0, int nblk, int) {
             // copy the chunk's Q8_K rows (planes) into LDS slots t * CB + b
             for (int t = 0; t < TC; ++t) {
                 const int q8r = s_q8row[t];

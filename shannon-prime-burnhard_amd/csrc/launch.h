@@ -27,6 +27,7 @@ struct GemvParams {
     int64_t x_tstride;
     Q8Planes Q;           // pre-quantised activations (Q.qs != nullptr) instead of X
     int32_t chunk_blocks; // blocks staged in LDS at a time
+    int32_t fixed_ok;     // the compile-time-K decode kernels may be used
 };
 
 // rows per workgroup for a lanes-per-row choice of 4*bpr (bpr in 1, 2, 4, 8)
