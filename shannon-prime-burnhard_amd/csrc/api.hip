@@ -5,6 +5,7 @@
 // entry points. There is no CPU compute path: every result comes from a HIP
 // kernel, and a missing or failing device is an error.
 #include <errno.h>
+#include <limits.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -28,7 +29,9 @@ struct spq4k_ctx {
     size_t scratch_cap = 0;
     int force_bpr = 0;           // tuning override (SPQ4K_GEMV_BPR = 1, 2, 4 or 8)
     int preq_mode = 0;           // SPQ4K_GEMV_PREQ: 0 auto, 1 always, 2 never
-    int no_fixed = 0;            // SPQ4K_GEMV_GENERIC=1: skip the compile-time-K kernels
+    int no_decode = 0;           // SPQ4K_GEMV_GENERIC=1: T = 1 also uses the generic kernel
+    DecodeCfg dec_force = {0, 0, false, 0};   // SPQ4K_DEC_{WAVES,DEPTH,XFIRST,GRID} overrides
+    int dec_xfirst_set = 0;
     char err[256] = {0};
 };
 
@@ -129,6 +132,40 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
     return 8;
 }
 
+// Launch shape of the T = 1 decode kernel. One workgroup per CU, so that x is
+// quantised once per CU, one wave per row; measured on MI355X for the 8B
+// decode shapes (cold weights, graph replay):
+//   K = 4096,  M <= 4096   : 16 waves, x-first         (o projection)
+//   K = 4096,  M <= 8192   : 12 waves = 2 rows a wave   (q/k/v, 6144 rows)
+//   K = 4096,  M <= 32768  : 16 waves                   (gate/up, 24576 rows)
+//   K = 4096,  larger M    : 12 waves, 2 rows in flight, x-first (lm_head)
+//   K = 12288              : 16 waves, x-first: 48 KB of x per CU would
+//                            otherwise queue behind the CU's weight loads
+DecodeCfg plan_decode(const spq4k_ctx* c, int nb, int64_t rows) {
+    DecodeCfg d;
+    if (nb >= 48) {
+        d.waves = 16; d.depth = 1; d.xfirst = true;
+    } else if (rows <= 4096) {
+        d.waves = 16; d.depth = 1; d.xfirst = true;
+    } else if (rows <= 8192) {
+        d.waves = 12; d.depth = 1; d.xfirst = false;
+    } else if (rows <= 32768) {
+        d.waves = 16; d.depth = 1; d.xfirst = false;
+    } else {
+        d.waves = 12; d.depth = 2; d.xfirst = true;
+    }
+    if (c->dec_force.waves) d.waves = c->dec_force.waves;
+    if (c->dec_force.depth) d.depth = c->dec_force.depth;
+    if (c->dec_xfirst_set) d.xfirst = c->dec_force.xfirst;
+    // K = 12288 with two rows in flight needs more than the 128 registers a
+    // 16-wave workgroup allows: one row in flight
+    if (nb >= 48 && d.waves == 16) d.depth = 1;
+    const int64_t wgs = (rows + d.waves - 1) / d.waves;
+    d.grid = (int)(wgs < c->num_cus ? wgs : c->num_cus);
+    if (c->dec_force.grid) d.grid = c->dec_force.grid;
+    return d;
+}
+
 int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* x, float* const* y, int64_t T) {
     if (n < 1 || n > GEMV_MAX_SEG) return set_err(c, -EINVAL, "gemv: n=%d matrices (1..4)", n);
     if (T < 1 || T > SPQ4K_GEMV_MAX_T) return set_err(c, -EINVAL, "gemv: T=%lld (1..8)", (long long)T);
@@ -147,20 +184,34 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
     const int rows = gemv_rows_per_tile(bpr);
     GemvParams p;
     memset(&p, 0, sizeof p);
-    int64_t tiles = 0;
+    int64_t tiles = 0, total = 0;
     for (int i = 0; i < n; ++i) {
         p.seg[i].W = W[i]->data;
         p.seg[i].Y = y[i];
         p.seg[i].M = (int32_t)W[i]->M;
         p.seg[i].y_tstride = W[i]->M;
         p.seg[i].tile_begin = (int32_t)tiles;
+        p.seg[i].row_begin = (int32_t)total;
         tiles += (W[i]->M + rows - 1) / rows;
+        total += W[i]->M;
     }
-    if (tiles > (1ll << 31) - 1) return set_err(c, -EINVAL, "gemv: too many rows");
+    if (tiles > (1ll << 31) - 1 || total > (1ll << 31) - 1) return set_err(c, -EINVAL, "gemv: too many rows");
     p.nseg = n;
     p.nb = (int32_t)(K / SPQ4K_QK_K);
     p.X = x;
     p.x_tstride = K;
+    p.total_rows = (int32_t)total;
+    for (int i = n; i < GEMV_MAX_SEG; ++i) {   // unused segments: never selected
+        p.seg[i] = p.seg[0];
+        p.seg[i].row_begin = INT32_MAX;
+        p.seg[i].tile_begin = INT32_MAX;
+    }
+    if (T == 1 && !c->no_decode && c->preq_mode != 1 && decode_supported(p.nb)) {
+        const DecodeCfg dc = plan_decode(c, p.nb, total);
+        hipError_t e = launch_gemv_decode(p, dc, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemv decode launch");
+        return 0;
+    }
     const int cb_max = LDS_BUDGET / ((int)T * 292);
     p.chunk_blocks = p.nb < cb_max ? p.nb : cb_max;
     // Quantise the activations once, up front, when re-quantising them in
@@ -172,7 +223,6 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         int rc = q8_planes(c, x, K, (int)T, p.nb, &p.Q);
         if (rc) return rc;
     }
-    p.fixed_ok = c->no_fixed ? 0 : 1;
     hipError_t e = launch_gemv(p, (int)T, bpr, (int)tiles, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "gemv launch");
     return 0;
@@ -207,7 +257,23 @@ int spq4k_init(int device, spq4k_ctx** out) {
         const int v = atoi(f);
         if (v == 1 || v == 2 || v == 4 || v == 8) c->force_bpr = v;
     }
-    if (const char* f = getenv("SPQ4K_GEMV_GENERIC")) c->no_fixed = atoi(f) == 1;
+    if (const char* f = getenv("SPQ4K_GEMV_GENERIC")) c->no_decode = atoi(f) == 1;
+    if (const char* f = getenv("SPQ4K_DEC_WAVES")) {
+        const int v = atoi(f);
+        if (v == 8 || v == 12 || v == 16) c->dec_force.waves = v;
+    }
+    if (const char* f = getenv("SPQ4K_DEC_DEPTH")) {
+        const int v = atoi(f);
+        if (v == 1 || v == 2) c->dec_force.depth = v;
+    }
+    if (const char* f = getenv("SPQ4K_DEC_XFIRST")) {
+        c->dec_force.xfirst = atoi(f) == 1;
+        c->dec_xfirst_set = 1;
+    }
+    if (const char* f = getenv("SPQ4K_DEC_GRID")) {
+        const int v = atoi(f);
+        if (v > 0 && v <= 65536) c->dec_force.grid = v;
+    }
     if (const char* f = getenv("SPQ4K_GEMV_PREQ")) {
         const int v = atoi(f);
         if (v == 1 || v == 2) c->preq_mode = v;

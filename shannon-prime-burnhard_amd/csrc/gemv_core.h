@@ -206,6 +206,79 @@ __device__ __forceinline__ void stream_row(const uint8_t* __restrict__ wrow, boo
     }
 }
 
+// ---------------------------------------------------------------------------
+// Register-resident activations (decode kernels). A lane that works on quarter
+// l4 of block b for many rows keeps the Q8_K data that quarter needs in VGPRs:
+//   a[0..7]  = q8[64 l4 + 0 .. 31]   (the low-nibble sub-block 2 l4)
+//   a[8..15] = q8[64 l4 + 32 .. 63]  (the high-nibble sub-block 2 l4 + 1)
+//   bsA = bsums[4 l4] + bsums[4 l4 + 1], bsB = bsums[4 l4 + 2] + bsums[4 l4 + 3]
+struct Q8Reg {
+    int a[16];
+    int bsA, bsB;
+    float d8;
+};
+
+__device__ __forceinline__ void load_q8reg(const Q8Lds& L, int b, int l4, Q8Reg& q) {
+    const int4* p = reinterpret_cast<const int4*>(L.q8 + b * 256 + 64 * l4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int4 v = p[i];
+        q.a[4 * i] = v.x; q.a[4 * i + 1] = v.y; q.a[4 * i + 2] = v.z; q.a[4 * i + 3] = v.w;
+    }
+    const uint2 bs = *reinterpret_cast<const uint2*>(L.bs + b * 16 + 4 * l4);
+    q.bsA = (int)(int16_t)(bs.x & 0xFFFFu) + (int)(int16_t)(bs.x >> 16);
+    q.bsB = (int)(int16_t)(bs.y & 0xFFFFu) + (int)(int16_t)(bs.y >> 16);
+    q.d8 = L.d8[b];
+}
+
+// The two exact integer sub-block sums of quarter l4 of a block:
+// S0 over sub-block 2 l4 (low nibbles), S1 over sub-block 2 l4 + 1 (high).
+__device__ __forceinline__ void subblock_sums_reg(const W4& w, const int (&a)[16], int& S0, int& S1) {
+    const uint32_t qq[8] = {w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w};
+    int s = 0, u = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        s = dot4((int)(qq[i] & 0x0F0F0F0Fu), a[i], s);
+        u = dot4((int)((qq[i] >> 4) & 0x0F0F0F0Fu), a[8 + i], u);
+    }
+    S0 = s;
+    S1 = u;
+}
+
+// Scales and mins of sub-blocks 2 l4 and 2 l4 + 1 (get_scale_min_k4,
+// ggml-quants.c:818-825) from the header words h.y, h.z, h.w.
+__device__ __forceinline__ void scales_of_quarter(const uint4& h, int l4, int& sc0, int& sc1, int& m0, int& m1) {
+    const int sh = 16 * (l4 & 1);
+    const uint32_t s0 = h.y >> sh, s1 = h.z >> sh, s2 = h.w >> sh;
+    uint32_t scp, mp;
+    if (l4 < 2) {
+        scp = s0 & 0x3F3Fu;
+        mp = s1 & 0x3F3Fu;
+    } else {
+        scp = (s2 & 0x0F0Fu) | ((s0 >> 2) & 0x3030u);
+        mp = ((s2 >> 4) & 0x0F0Fu) | ((s1 >> 2) & 0x3030u);
+    }
+    sc0 = (int)(scp & 0xFFu);
+    sc1 = (int)((scp >> 8) & 0xFFu);
+    m0 = (int)(mp & 0xFFu);
+    m1 = (int)((mp >> 8) & 0xFFu);
+}
+
+// acc + this lane's share of ggml_vec_dot_q4_K_q8_K for one block:
+// (d d8) (sc0 S0 + sc1 S1) - (dmin d8) (m0 bsA + m1 bsB), integers exact.
+__device__ __forceinline__ float block_dot_reg(const W4& w, int l4, const Q8Reg& q, float acc) {
+    const float d = half_bits_to_float(w.hdr.x & 0xFFFFu);
+    const float dmin = half_bits_to_float(w.hdr.x >> 16);
+    int sc0, sc1, m0, m1, S0, S1;
+    scales_of_quarter(w.hdr, l4, sc0, sc1, m0, m1);
+    subblock_sums_reg(w, q.a, S0, S1);
+    const int A = sc0 * S0 + sc1 * S1;
+    const int B = m0 * q.bsA + m1 * q.bsB;
+    acc = fmaf(d * q.d8, (float)A, acc);
+    acc = fmaf(-(dmin * q.d8), (float)B, acc);
+    return acc;
+}
+
 // Quantise activation blocks into LDS. Work items are (t, block) pairs,
 // item i -> t = i / nblk, block kb0 + i % nblk. Each 16-lane row of a wave
 // quantises one item per pass. X rows are 16-byte aligned (checked on host).
@@ -276,48 +349,6 @@ template <int WAVES>
 __device__ __forceinline__ void stage_q8_from_f32(const float* __restrict__ X, int64_t x_tstride, int T, int kb0,
                                                   int nblk, const Q8Lds& L, int slot_stride) {
     stage_f32_fin<WAVES>(X, x_tstride, T, kb0, nblk, L, slot_stride, stage_f32_load<WAVES>(X, x_tstride, T, kb0, nblk));
-}
-
-// Compile-time-K variant of stream_row for T = 1 decode with on-chip
-// quantisation (NB blocks per row, all of K staged at once). With the trip
-// counts known, every load is unconditional and the loop is fully unrolled
-// into a rotating pipeline of D register slots, so the compiler's s_waitcnt
-// values are exact: the staging waits only for the activation loads (issued
-// first, all passes), never for weight loads that are still in flight.
-template <int NB, int BPR, int D, int WAVES>
-__device__ __forceinline__ float stream_row_fixed(const uint8_t* __restrict__ wrow, bool row_ok, int l4, int bsub,
-                                                  const float* __restrict__ X, const Q8Lds& L) {
-    constexpr int NIT = (NB + BPR - 1) / BPR;
-    constexpr int DD = NIT < D ? NIT : D;
-    constexpr int PASSES = (NB + 4 * WAVES - 1) / (4 * WAVES);
-    auto blk_of = [&](int it) { return min(bsub + BPR * it, NB - 1); };
-
-    // 1. activation loads for every staging pass
-    XRegs xr[PASSES];
-    int xt[PASSES], xb[PASSES];
-    bool xv[PASSES];
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-        stage_f32_item<WAVES>(ps * 4 * WAVES, NB, NB, xt[ps], xb[ps], xv[ps]);
-        xr[ps] = load_x16(X, 0, 0, xb[ps]);
-    }
-    // 2. weight pipeline fill
-    W4 buf[DD];
-#pragma unroll
-    for (int u = 0; u < DD; ++u) buf[u] = load_w4(wrow + (size_t)blk_of(u) * Q4K_BYTES, l4);
-    // 3. quantise into LDS while the weights are in flight
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) store_q8_item(xr[ps], xv[ps], xb[ps], L);
-    __syncthreads();
-    // 4. stream
-    float acc[1] = {0.0f};
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int raw = bsub + BPR * it;
-        block_dot<1>(buf[it % DD], l4, L, min(raw, NB - 1), NB, row_ok && raw < NB, acc);
-        if (it + DD < NIT) buf[it % DD] = load_w4(wrow + (size_t)blk_of(it + DD) * Q4K_BYTES, l4);
-    }
-    return acc[0];
 }
 
 // Copy Q8_K planes [t][kb0 .. kb0+nblk) into the LDS layout.

@@ -85,39 +85,135 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
     }
 }
 
-// T = 1 decode kernel specialised on the number of blocks per row (see
-// stream_row_fixed); same tiling, lane mapping and arithmetic as above.
-template <int NB, int BPR, int WAVES, int D>
-__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_fixed_kernel(GemvParams p) {
-    __shared__ __align__(16) char smem[q8lds_bytes(NB)];
-    constexpr int LPR = 4 * BPR;
-    constexpr int RPW = 64 / LPR;
-    constexpr int ROWS = WAVES * RPW;
-    const int tile = blockIdx.x;
-    int sidx = 0;
-#pragma unroll
-    for (int s = 1; s < GEMV_MAX_SEG; ++s)
-        if (s < p.nseg && tile >= p.seg[s].tile_begin) sidx = s;
-    const uint8_t* __restrict__ W = p.seg[sidx].W;
-    float* __restrict__ Y = p.seg[sidx].Y;
-    const int M = p.seg[sidx].M;
-    const int row0 = (tile - p.seg[sidx].tile_begin) * ROWS;
+// T = 1 decode kernel. One wave per output row: lane (bsub, l4) = (lane >> 2,
+// lane & 3) takes quarter l4 of blocks bsub, bsub + 16, ... of the row, so the
+// Q8_K data those quarters need is loaded into registers once and reused for
+// every row the wave processes. A workgroup of WAVES waves is one CU's share:
+// x is quantised once per workgroup (by the first ceil(NB/4) waves, four
+// blocks each) into LDS, and wave g = blockIdx * WAVES + w processes the rows
+// g, g + G, g + 2G, ... of the concatenated segments (G = waves in the grid),
+// with D rows of loads in flight. With XFW the quantising waves fetch and
+// quantise x before issuing their own weight loads, so that x is not queued
+// behind the weight requests of the whole CU.
+template <int NB, int WAVES, int D, bool XFW>
+__global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
+    constexpr int NIT = (NB + 15) / 16;           // blocks per lane per row
+    constexpr int QW = (NB + 3) / 4;              // quantising waves
+    constexpr int PASSES = (QW + WAVES - 1) / WAVES;
+    constexpr size_t ROWB = (size_t)NB * Q4K_BYTES;
+    __shared__ __align__(16) char q8s[q8lds_bytes(NB)];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l4 = lane & 3;
-    const int bsub = (lane >> 2) & (BPR - 1);
-    const int row = row0 + wave * RPW + lane / LPR;
-    const bool row_ok = row < M;
-    const uint8_t* __restrict__ wrow = W + (size_t)(row_ok ? row : M - 1) * (NB * Q4K_BYTES);
-    const Q8Lds L = q8lds_carve(smem, NB);
-    float acc = stream_row_fixed<NB, BPR, D, WAVES>(wrow, row_ok, l4, bsub, p.X, L);
-    acc = group_sum_last<LPR>(acc);
-    if (row_ok && (lane & (LPR - 1)) == LPR - 1) Y[row] = acc;
+    const int bsub = lane >> 2;
+    const int Mtot = p.total_rows;
+    const int G = gridDim.x * WAVES;
+    const int g = blockIdx.x * WAVES + wave;
+    const int nrows = g < Mtot ? (Mtot - 1 - g) / G + 1 : 0;
+
+    // segment table read once at kernel start into named scalars (an array
+    // indexed by the segment would be placed in scratch); unused segments
+    // have row_begin = INT32_MAX and are never selected
+    const uint8_t* const W0 = p.seg[0].W;
+    const uint8_t* const W1 = p.seg[1].W;
+    const uint8_t* const W2 = p.seg[2].W;
+    const uint8_t* const W3 = p.seg[3].W;
+    float* const Y0 = p.seg[0].Y;
+    float* const Y1 = p.seg[1].Y;
+    float* const Y2 = p.seg[2].Y;
+    float* const Y3 = p.seg[3].Y;
+    const int R1 = p.seg[1].row_begin, R2 = p.seg[2].row_begin, R3 = p.seg[3].row_begin;
+    struct Loc {
+        const uint8_t* w;
+        float* y;
+        int row;
+    };
+    auto locate = [&](int r) {
+        Loc l;
+        if (r >= R3) { l.w = W3; l.y = Y3; l.row = r - R3; }
+        else if (r >= R2) { l.w = W2; l.y = Y2; l.row = r - R2; }
+        else if (r >= R1) { l.w = W1; l.y = Y1; l.row = r - R1; }
+        else { l.w = W0; l.y = Y0; l.row = r; }
+        return l;
+    };
+    W4 buf[D][NIT];
+    // rows past the end re-read the last row (in bounds; never stored): the
+    // first D loads are unconditional so that the compiler's wait counts for
+    // x stay exact (a load under a branch makes it wait for every load)
+    auto load_row = [&](int i, W4 (&b)[NIT]) {
+        const int r0 = g + i * G;
+        const int r = r0 < Mtot ? r0 : Mtot - 1;
+        const Loc l = locate(r);
+        const uint8_t* wr = l.w + (size_t)l.row * ROWB;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int bb = bsub + 16 * it;
+            b[it] = load_w4(wr + (size_t)(bb < NB ? bb : NB - 1) * Q4K_BYTES, l4);
+        }
+    };
+
+    // activations: quantising waves load x first
+    XRegs xr[PASSES];
+    int xb[PASSES];
+    bool xv[PASSES];
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+        const int qw = ps * WAVES + wave;
+        const int item = qw * 4 + (lane >> 4);
+        xv[ps] = qw < QW && item < NB;
+        xb[ps] = item < NB ? item : NB - 1;
+        if (qw < QW) xr[ps] = load_x16(p.X, 0, 0, xb[ps]);
+    }
+    const Q8Lds L = q8lds_carve(q8s, NB);
+    auto quantise = [&]() {
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps) {
+            if (ps * WAVES + wave < QW) store_q8_item(xr[ps], xv[ps], xb[ps], L);
+        }
+    };
+    if (XFW) {
+        quantise();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int u = 0; u < D; ++u) load_row(u, buf[u]);
+    if (!XFW) quantise();
+    // all quantised blocks visible (LDS writes only: weight loads stay in flight)
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+
+    Q8Reg qr[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int bb = bsub + 16 * it;
+        load_q8reg(L, bb < NB ? bb : NB - 1, l4, qr[it]);
+    }
+    for (int i0 = 0; i0 < nrows; i0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int i = i0 + u;
+            if (i < nrows) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) {
+                    const float a = block_dot_reg(buf[u][it], l4, qr[it], acc);
+                    acc = (bsub + 16 * it < NB) ? a : acc;
+                }
+                acc = group_sum_last<64>(acc);
+                if (lane == 63) {
+                    const Loc l = locate(g + i * G);
+                    l.y[l.row] = acc;
+                }
+                if (i + D < nrows) load_row(i + D, buf[u]);
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
-// Diagnostic: the exact integer sub-block sums S[row][b][j] exactly as the GEMV
-// lanes form them (same loads, unpacking and dot products), for one Q8_K row.
+// Diagnostic: the exact integer sub-block sums S[row][b][j] exactly as the
+// decode kernel's lanes form them (same loads, register layout and dot
+// products: subblock_sums_reg), for one Q8_K row.
 template <int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void subblock_sums_kernel(const uint8_t* __restrict__ W, int M,
                                                                    int nb, const float* __restrict__ X,
@@ -138,9 +234,10 @@ __global__ __launch_bounds__(WAVES * 64) void subblock_sums_kernel(const uint8_t
         if (!row_ok) continue;
         for (int bb = 0; bb < nblk; ++bb) {
             const W4 w = load_w4(W + ((size_t)row * nb + c0 + bb) * Q4K_BYTES, l4);
-            const Nib n = split_nibbles(w);
+            Q8Reg q;
+            load_q8reg(L, bb, l4, q);
             int S0, S1;
-            subblock_pair(n, L.q8 + bb * 256, l4, S0, S1);
+            subblock_sums_reg(w, q.a, S0, S1);
             int32_t* o = S + ((size_t)row * nb + c0 + bb) * 8 + 2 * l4;
             o[0] = S0;
             o[1] = S1;
@@ -171,29 +268,34 @@ static hipError_t launch_t(const GemvParams& p, int bpr, int ntiles, hipStream_t
 
 int gemv_rows_per_tile(int bpr) { return 4 * (64 / (4 * bpr)); }
 
-template <int NB>
-static hipError_t launch_fixed(const GemvParams& p, int bpr, int ntiles, hipStream_t st) {
-    constexpr int WAVES = 4, D = 4;
-    switch (bpr) {
-        case 1: hipLaunchKernelGGL((gemv_q4k_fixed_kernel<NB, 1, WAVES, D>), dim3(ntiles), dim3(256), 0, st, p); break;
-        case 2: hipLaunchKernelGGL((gemv_q4k_fixed_kernel<NB, 2, WAVES, D>), dim3(ntiles), dim3(256), 0, st, p); break;
-        case 4: hipLaunchKernelGGL((gemv_q4k_fixed_kernel<NB, 4, WAVES, D>), dim3(ntiles), dim3(256), 0, st, p); break;
-        case 8: hipLaunchKernelGGL((gemv_q4k_fixed_kernel<NB, 8, WAVES, D>), dim3(ntiles), dim3(256), 0, st, p); break;
-        default: return hipErrorInvalidValue;
-    }
+template <int NB, int WAVES, int D, bool XFW>
+static hipError_t launch_dec(const GemvParams& p, int grid, hipStream_t st) {
+    hipLaunchKernelGGL((gemv_decode_kernel<NB, WAVES, D, XFW>), dim3(grid), dim3(WAVES * 64), 0, st, p);
     return hipGetLastError();
+}
+
+template <int NB>
+static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
+#define SPQ_DEC(W, DD, X)                                                                  \
+    if constexpr (!(NB >= 48 && W == 16 && DD == 2))                                       \
+        if (c.waves == W && c.depth == DD && c.xfirst == X) return launch_dec<NB, W, DD, X>(p, c.grid, st);
+    SPQ_DEC(16, 1, false) SPQ_DEC(16, 1, true) SPQ_DEC(16, 2, false) SPQ_DEC(16, 2, true)
+    SPQ_DEC(12, 1, false) SPQ_DEC(12, 1, true) SPQ_DEC(12, 2, false) SPQ_DEC(12, 2, true)
+    SPQ_DEC(8, 1, false) SPQ_DEC(8, 1, true) SPQ_DEC(8, 2, false) SPQ_DEC(8, 2, true)
+#undef SPQ_DEC
+    return hipErrorInvalidValue;
+}
+
+bool decode_supported(int nb) { return nb == 16 || nb == 48; }
+
+hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
+    if (p.nb == 16) return launch_dec_nb<16>(p, c, st);
+    if (p.nb == 48) return launch_dec_nb<48>(p, c, st);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st) {
     const bool pq = p.Q.qs != nullptr;
-    // decode fast path: one token, activations quantised on chip, the K of
-    // the 8B-class shapes (4096 and 12288) known at compile time
-    // (the fully unrolled variants with few lanes per row need too many
-    // registers; those shapes have enough rows for the generic kernel)
-    if (T == 1 && !pq && p.fixed_ok) {
-        if (p.nb == 16 && bpr >= 2) return launch_fixed<16>(p, bpr, ntiles, st);
-        if (p.nb == 48 && bpr >= 4) return launch_fixed<48>(p, bpr, ntiles, st);
-    }
 #define SPQ_T(TT) \
     case TT: return pq ? launch_t<TT, true>(p, bpr, ntiles, st) : launch_t<TT, false>(p, bpr, ntiles, st);
     switch (T) {

@@ -16,7 +16,8 @@ struct GemvSeg {
     float* Y;             // y[t * y_tstride + r]
     int64_t y_tstride;
     int32_t M;
-    int32_t tile_begin;   // first tile index of this segment
+    int32_t tile_begin;   // first tile index of this segment (generic kernel)
+    int32_t row_begin;    // first row of this segment in the concatenation (decode kernel)
 };
 
 struct GemvParams {
@@ -27,12 +28,22 @@ struct GemvParams {
     int64_t x_tstride;
     Q8Planes Q;           // pre-quantised activations (Q.qs != nullptr) instead of X
     int32_t chunk_blocks; // blocks staged in LDS at a time
-    int32_t fixed_ok;     // the compile-time-K decode kernels may be used
+    int32_t total_rows;   // sum of the segments' M
+};
+
+// Launch shape of the T = 1 decode kernel (gemv_decode_kernel).
+struct DecodeCfg {
+    int waves;    // waves per workgroup: 8, 12 or 16
+    int depth;    // rows of loads in flight per wave: 1 or 2
+    bool xfirst;  // quantising waves fetch and quantise x before their weight loads
+    int grid;     // workgroups
 };
 
 // rows per workgroup for a lanes-per-row choice of 4*bpr (bpr in 1, 2, 4, 8)
 int gemv_rows_per_tile(int bpr);
 hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st);
+bool decode_supported(int nb);
+hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st);
 hipError_t launch_subblock_sums(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
 
 // expert-gathered matvec (k_moe.hip)

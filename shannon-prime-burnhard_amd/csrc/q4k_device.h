@@ -83,8 +83,8 @@ __device__ __forceinline__ float dpp_f32(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-// Sum over each aligned group of N lanes (N = 1, 2, 4, 8, 16, 32); the sum is
-// exact in the LAST lane of each group (lane N-1 mod N), other lanes hold
+// Sum over each aligned group of N lanes (N = 1, 2, 4, 8, 16, 32, 64); the sum
+// is exact in the LAST lane of each group (lane N-1 mod N), other lanes hold
 // partial sums. Fixed combination order: deterministic.
 template <int N>
 __device__ __forceinline__ float group_sum_last(float v) {
@@ -92,7 +92,10 @@ __device__ __forceinline__ float group_sum_last(float v) {
     if (N >= 4) v += dpp_f32<DPP_XOR2>(v);
     if (N >= 8) v += dpp_f32<DPP_SHR4>(v);     // lanes 4-7 (12-15) += lanes 0-3 (8-11)
     if (N >= 16) v += dpp_f32<DPP_SHR8>(v);    // lane 15 += lane 7
+    // rows 1 and 3 add lane 15 of rows 0 and 2: lanes 31 and 63 hold 32-lane sums
     if (N >= 32) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_BCAST15, 0xA, 0xF, false));
+    // rows 2 and 3 add lane 31: lane 63 holds the wave sum
+    if (N >= 64) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_BCAST31, 0xC, 0xF, false));
     return v;
 }
 
@@ -110,14 +113,17 @@ struct Q8Lane {
     float d;         // the block's d (same in all 16 lanes)
 };
 
-__device__ __forceinline__ Q8Lane quantize_q8k_16(const float (&x)[16], int e) {
+// Signed value of the first element of largest |x| over the 16-lane row,
+// found with an exact (|x|, index) key search; NaN never wins, as in the
+// reference's `ax > amax` test. Returns +-0 when every |x| is 0 or NaN.
+__device__ __forceinline__ float first_absmax_16(const float (&x)[16], int e) {
     // key = |x| bits (non-negative floats order as integers) : (255 - idx) : sign
     uint32_t best_hi = 0, best_lo = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const uint32_t bits = __float_as_uint(x[i]);
         uint32_t ab = bits & 0x7FFFFFFFu;
-        ab = ab > 0x7F800000u ? 0u : ab;  // NaN never wins (|NaN| > amax is false)
+        ab = ab > 0x7F800000u ? 0u : ab;
         // within a lane later indices only replace on a strictly larger |x|
         const bool take = ab > best_hi;
         best_hi = take ? ab : best_hi;
@@ -137,32 +143,61 @@ __device__ __forceinline__ Q8Lane quantize_q8k_16(const float (&x)[16], int e) {
     SPQ_KEYMAX(DPP_ROR4)
     SPQ_KEYMAX(DPP_ROR8)
 #undef SPQ_KEYMAX
+    const float amax = __uint_as_float(best_hi);
+    return (best_lo & 1u) ? -amax : amax;
+}
+
+__device__ __forceinline__ Q8Lane quantize_q8k_16(const float (&x)[16], int e) {
+    // Largest and smallest value of the row (fmaxf/fminf skip NaN, as the
+    // reference's comparison does). When the largest |x| occurs with one sign
+    // only, that sign is the max's; when +a and -a both occur (or the row is
+    // all zero / NaN) the first index decides, by the exact key search.
+    float mx = x[0], mn = x[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+        mx = fmaxf(mx, x[i]);
+        mn = fminf(mn, x[i]);
+    }
+    mx = fmaxf(mx, dpp_f32<DPP_XOR1>(mx)); mn = fminf(mn, dpp_f32<DPP_XOR1>(mn));
+    mx = fmaxf(mx, dpp_f32<DPP_XOR2>(mx)); mn = fminf(mn, dpp_f32<DPP_XOR2>(mn));
+    mx = fmaxf(mx, dpp_f32<DPP_ROR4>(mx)); mn = fminf(mn, dpp_f32<DPP_ROR4>(mn));
+    mx = fmaxf(mx, dpp_f32<DPP_ROR8>(mx)); mn = fminf(mn, dpp_f32<DPP_ROR8>(mn));
+    const float neg = -mn;
+    float vmax;
+    if (mx > neg) {
+        vmax = mx;
+    } else if (neg > mx) {
+        vmax = mn;
+    } else {
+        vmax = first_absmax_16(x, e);
+    }
     Q8Lane r;
-    if (best_hi == 0) {
+    if (!(fabsf(vmax) > 0.0f)) {
         r.q[0] = r.q[1] = r.q[2] = r.q[3] = 0;
         r.bsum = 0;
         r.d = 0.0f;
         return r;
     }
-    const float amax = __uint_as_float(best_hi);
-    const float vmax = (best_lo & 1u) ? -amax : amax;
     const float iscale = -127.0f / vmax;
-    int s = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        uint32_t packed = 0;
+        uint32_t v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // the exact reference rounding and int8 store, so that even
             // degenerate blocks (subnormal max, infinities) match bit for bit
-            int v = nearest_int_ref(iscale * x[4 * w + i]);
-            v = v < 127 ? v : 127;
-            const int q8 = (int)(int8_t)(v & 0xFF);
-            s += q8;
-            packed |= ((uint32_t)q8 & 0xFFu) << (8 * i);
+            const int t = nearest_int_ref(iscale * x[4 * w + i]);
+            v[i] = (uint32_t)(t < 127 ? t : 127);
         }
-        r.q[w] = packed;
+        // low bytes packed little-endian: v0 | v1 << 8 | v2 << 16 | v3 << 24
+        const uint32_t p01 = __builtin_amdgcn_perm(v[1], v[0], 0x0C0C0400u);
+        const uint32_t p23 = __builtin_amdgcn_perm(v[3], v[2], 0x04000C0Cu);
+        r.q[w] = p01 | p23;
     }
+    // sum of the 16 stored int8 values
+    int s = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) s = __builtin_amdgcn_sdot4((int)r.q[w], 0x01010101, s, false);
     r.bsum = s;
     r.d = 1.0f / iscale;
     return r;

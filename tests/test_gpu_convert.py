@@ -53,6 +53,16 @@ def _q8k_cases(rng):
     cases.append((rng.standard_normal(256) * 1e30).astype(np.float32))
     h = (np.arange(256, dtype=np.float32) - 128.0) / 2.0; cases.append(h)        # many .5 roundings
     t = rng.standard_normal(256).astype(np.float32); t[3] = np.nan; cases.append(t)
+    t = np.zeros(256, np.float32); t[3] = -2.0; t[10] = 2.0; cases.append(t)      # tie inside one 16-lane share
+    t = np.zeros(256, np.float32); t[9] = 2.0; t[2] = -2.0; cases.append(t)
+    t = rng.standard_normal(256).astype(np.float32); t[40] = np.inf; cases.append(t)
+    t = rng.standard_normal(256).astype(np.float32); t[41] = -np.inf; cases.append(t)
+    t = rng.standard_normal(256).astype(np.float32); t[50] = -np.inf; t[60] = np.inf; cases.append(t)
+    cases.append(np.full(256, np.nan, np.float32))                                # all NaN: d = 0
+    cases.append(np.full(256, -0.0, np.float32))
+    t = np.zeros(256, np.float32); t[255] = -7.0; cases.append(t)                 # max at the last index
+    t = np.zeros(256, np.float32); t[0] = 7.0; t[255] = -7.0; cases.append(t)
+    t = (rng.standard_normal(256) * 0.1).astype(np.float32); t[128] = 3.0; t[129] = -3.0; cases.append(t)
     return np.concatenate(cases)
 
 

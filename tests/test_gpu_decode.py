@@ -1,0 +1,145 @@
+"""GPU parity of the T = 1 decode GEMV (gemv_decode_kernel) and of every launch
+shape the planner can pick, against the CPU oracle.
+
+The decode kernel serves K = 4096 and K = 12288 (the 8B shapes); the generic
+kernel serves every other K and T <= 8. Launch shapes are forced through the
+context's environment overrides (read when a context is created), so each
+(waves, depth, x-first) instantiation and each lanes-per-row choice of the
+generic kernel is checked, not only the ones the planner picks for the sizes
+below. Tolerance: the reference's close_enough (1e-4 relative or 1e-5
+absolute, tests/desktop/test_sp_kernels.cpp:34-48) against the oracle's
+restatement of ggml's x86 path (bit-identical to the reference's own
+ggml_vec_dot_q4_K_q8_K, pinned in test_oracle_golden.py)."""
+import os
+
+import numpy as np
+import pytest
+
+from _oracle import close_enough
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(oracle, rng, M, K, scale=0.02):
+    return oracle.quantize_q4K((rng.standard_normal((M, K)) * scale).astype(np.float32))
+
+
+def _check(got, exp, what):
+    ok = close_enough(got, exp)
+    if not ok.all():
+        i = np.argwhere(~ok)[0]
+        raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} outside tolerance; first {tuple(i)} "
+                             f"got {got[tuple(i)]!r} exp {exp[tuple(i)]!r}")
+
+
+def _context_with(env):
+    """A fresh context created with the given SPQ4K_* overrides in effect."""
+    import spq4k
+    saved = {k: os.environ.get(k) for k in env}
+    try:
+        for k, v in env.items():
+            os.environ[k] = str(v)
+        return spq4k.Context(0)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("M,K", [(1, 4096), (100, 4096), (4096, 4096), (37, 12288), (4096, 12288)])
+def test_decode_single(ctx, oracle, M, K):
+    rng = np.random.default_rng(M * 7 + K)
+    W = _weights(oracle, rng, M, K)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    Wd = ctx.upload(W, M, K)
+    _check(ctx.mul_mat(Wd, x), oracle.mul_mat(W, M, K, x), f"decode M={M} K={K}")
+
+
+@pytest.mark.parametrize("K,shapes", [(4096, (4096, 1024, 1024)), (4096, (12288, 12288)), (12288, (4096,)),
+                                      (4096, (5, 300, 77, 1))])
+def test_decode_grouped(ctx, oracle, K, shapes):
+    """q/k/v and gate/up as one launch: rows of all matrices in one sweep."""
+    from spq4k.hip import DeviceArray
+    rng = np.random.default_rng(sum(shapes) + K)
+    Ws = [_weights(oracle, rng, M, K) for M in shapes]
+    x = rng.standard_normal(K).astype(np.float32)
+    wd = [ctx.upload(w, M, K) for w, M in zip(Ws, shapes)]
+    xd = DeviceArray.from_host(x)
+    ys = [DeviceArray.from_host(np.full(M, np.nan, np.float32)) for M in shapes]
+    ctx.gemv_multi_dev(wd, xd.ptr, [y.ptr for y in ys], 1)
+    ctx.synchronize()
+    for w, M, y in zip(Ws, shapes, ys):
+        _check(y.to_host()[None], oracle.mul_mat(w, M, K, x[None]), f"grouped K={K} M={M}")
+
+
+_CFGS = [(w, d, xf) for w in (8, 12, 16) for d in (1, 2) for xf in (0, 1)]
+
+
+@pytest.mark.parametrize("waves,depth,xfirst", _CFGS)
+def test_decode_launch_shapes(oracle, waves, depth, xfirst):
+    """Every compiled instantiation, with a small grid so that each wave walks
+    several rows (the depth pipeline and its ragged tail) and a full grid."""
+    rng = np.random.default_rng(1000 + waves * 10 + depth * 2 + xfirst)
+    cases = [(1000, 4096), (333, 12288)]
+    data = [(M, K, _weights(oracle, rng, M, K), rng.standard_normal((1, K)).astype(np.float32)) for M, K in cases]
+    for grid in (3, 0):
+        env = {"SPQ4K_DEC_WAVES": waves, "SPQ4K_DEC_DEPTH": depth, "SPQ4K_DEC_XFIRST": xfirst}
+        if grid:
+            env["SPQ4K_DEC_GRID"] = grid
+        c = _context_with(env)
+        try:
+            for M, K, W, x in data:
+                Wd = c.upload(W, M, K)
+                _check(c.mul_mat(Wd, x), oracle.mul_mat(W, M, K, x),
+                       f"decode waves={waves} depth={depth} xfirst={xfirst} grid={grid} M={M} K={K}")
+                Wd.free()
+        finally:
+            c.close()
+
+
+@pytest.mark.parametrize("bpr", [1, 2, 4, 8])
+def test_generic_lanes_per_row(oracle, bpr):
+    """The generic kernel at each lanes-per-row choice (T = 1 and T = 3)."""
+    c = _context_with({"SPQ4K_GEMV_GENERIC": 1, "SPQ4K_GEMV_BPR": bpr})
+    rng = np.random.default_rng(77 + bpr)
+    try:
+        for M, K, T in ((300, 4096, 1), (129, 12288, 1), (64, 5120, 3)):
+            W = _weights(oracle, rng, M, K)
+            x = rng.standard_normal((T, K)).astype(np.float32)
+            Wd = c.upload(W, M, K)
+            _check(c.mul_mat(Wd, x), oracle.mul_mat(W, M, K, x), f"generic bpr={bpr} M={M} K={K} T={T}")
+            Wd.free()
+    finally:
+        c.close()
+
+
+def test_decode_matches_generic(ctx, oracle):
+    """Same bytes through the decode and the generic kernels: both within the
+    tolerance of the oracle and of each other."""
+    rng = np.random.default_rng(31)
+    M, K = 2048, 4096
+    W = _weights(oracle, rng, M, K)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    a = ctx.mul_mat(ctx.upload(W, M, K), x)
+    g = _context_with({"SPQ4K_GEMV_GENERIC": 1})
+    try:
+        b = g.mul_mat(g.upload(W, M, K), x)
+    finally:
+        g.close()
+    exp = oracle.mul_mat(W, M, K, x)
+    _check(a, exp, "decode")
+    _check(b, exp, "generic")
+    _check(a, b, "decode vs generic")
+
+
+def test_decode_repeatable(ctx, oracle):
+    """Fixed combination order: bit-identical reruns."""
+    rng = np.random.default_rng(9)
+    M, K = 1536, 12288
+    Wd = ctx.upload(_weights(oracle, rng, M, K), M, K)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    a = ctx.mul_mat(Wd, x)
+    for _ in range(3):
+        np.testing.assert_array_equal(ctx.mul_mat(Wd, x), a)
