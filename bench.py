@@ -12,12 +12,17 @@ captured once as a HIP graph and replayed.
 
 Metric: effective HBM GB/s = algorithmic bytes of the step (Q4_K weights +
 fp32 x and y of every matvec: 4,268,590,592 B) / step time; also tok/s-equiv
-and % of the 8 TB/s peak. CPU baseline: the reference's own ggml CPU path
-(oracle/_ref, built from /root/reference sources) on a bounded sample of the
-same workload (the first two layers), timed on this host; its outputs are
-checked against the GPU's on identical inputs.
+and % of the 8 TB/s peak. Every launch of the step is gemv_decode_kernel, so
+the HIP events around the timed replays give that kernel's average launch
+duration directly. Each stage kind (q/k/v, o, gate/up, down, lm_head) is also
+replayed on its own for a per-stage breakdown. CPU baseline: the reference's
+own ggml CPU path (oracle/_ref, built from /root/reference sources) on a
+bounded sample of the same workload (layers 0-9, 1.09 GB, larger than the
+host's last-level cache), timed on this host with 16 and with 4 threads;
+its outputs are checked against the GPU's on identical inputs.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--config decode8b|gemv4096|largek]
+  python bench.py [--steps K] [--warmup W] [--gpus 1]
+                  [--config decode8b|gemv4096|largek|prefill|moe|copy]
 """
 from __future__ import annotations
 
@@ -122,6 +127,23 @@ def capture_step(ctx, stages, with_events=False):
     return g, []
 
 
+def time_stage_kinds(ctx, stages, reps=5):
+    """Replay each stage kind (all 36 layers of it, or lm_head) on its own."""
+    kinds = {}
+    for st in stages:
+        kind = st[0].split(".", 1)[-1] if "." in st[0] else st[0]
+        kinds.setdefault(kind, []).append(st)
+    out = {}
+    for kind, sts in kinds.items():
+        with Graph.capture(ctx.stream) as g:
+            enqueue_step(ctx, sts)
+        ms = time_graph(ctx, g, reps, 1)
+        nb = sum(stage_bytes(x) for x in sts)
+        out[kind] = {"us_per_launch": round(ms * 1e3 / len(sts), 3), "launches": len(sts),
+                     "GBps": round(nb / (ms * 1e-3) / 1e9, 1)}
+    return out
+
+
 def time_graph(ctx, g, steps, warmup):
     for _ in range(warmup):
         g.launch()
@@ -138,7 +160,7 @@ def time_graph(ctx, g, steps, warmup):
 
 # ---------------------------------------------------------------------------
 def cpu_baseline_decode(stages, budget_s=10.0):
-    """Reference ggml CPU path (oracle/_ref) on layers 0-1 of the same step."""
+    """Reference ggml CPU path (oracle/_ref) on layers 0-9 of the same step."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
     try:
         from _oracle import Ref, ref_library_path, close_enough
@@ -149,7 +171,8 @@ def cpu_baseline_decode(stages, budget_s=10.0):
         return None, "oracle/_ref not built"
     import ctypes as C
     ref = Ref(path)
-    sample = [s for s in stages if s[0].startswith(("L0.", "L1."))]
+    sample_layers = tuple(f"L{i}." for i in range(10))
+    sample = [s for s in stages if s[0].startswith(sample_layers)]
     Ws, Ms, Ks, Xs, Ys, keep = [], [], [], [], [], []
     gpu_y = []
     nbytes = 0
@@ -167,22 +190,29 @@ def cpu_baseline_decode(stages, budget_s=10.0):
             gpu_y.append((y.to_host(), yh))
             nbytes += q4k_bytes(w.M, w.K) + 4 * w.K + 4 * w.M
     n = len(Ws)
-    nthreads = min(16, os.cpu_count() or 1)
     arr = lambda t, v: (t * n)(*v)
-    h = ref.L.ref_mm_create(n, arr(C.c_void_p, Ws), arr(C.c_int64, Ms), arr(C.c_int64, Ks),
-                            arr(C.c_void_p, Xs), arr(C.c_void_p, Ys), 1, nthreads)
-    if not h:
+
+    def run(nthreads, budget):
+        h = ref.L.ref_mm_create(n, arr(C.c_void_p, Ws), arr(C.c_int64, Ms), arr(C.c_int64, Ks),
+                                arr(C.c_void_p, Xs), arr(C.c_void_p, Ys), 1, nthreads)
+        if not h:
+            return None, 0
+        try:
+            secs = (C.c_double * 1)()
+            ref.L.ref_graph_run(h, 1, secs)          # warm-up
+            first = secs[0]
+            reps = max(5, min(20000, int(budget / max(first, 1e-4))))
+            times = (C.c_double * reps)()
+            ref.L.ref_graph_run(h, reps, times)
+            return float(np.median(np.array(times[:reps]))), reps
+        finally:
+            ref.L.ref_graph_destroy(h)
+
+    nthreads = min(16, os.cpu_count() or 1)
+    med, reps = run(nthreads, budget_s)
+    if med is None:
         return None, "ref graph creation failed"
-    try:
-        secs = (C.c_double * 1)()
-        ref.L.ref_graph_run(h, 1, secs)          # warm-up
-        first = secs[0]
-        reps = max(5, min(20000, int(budget_s / max(first, 1e-4))))
-        times = (C.c_double * reps)()
-        ref.L.ref_graph_run(h, reps, times)
-        med = float(np.median(np.array(times[:reps])))
-    finally:
-        ref.L.ref_graph_destroy(h)
+    med4, reps4 = run(min(4, nthreads), budget_s / 2)
     # parity of the GPU step against the reference on the sampled stages
     worst_bad = 0
     for gy, cy in gpu_y:
@@ -192,9 +222,11 @@ def cpu_baseline_decode(stages, budget_s=10.0):
         "unit": "GB/s",
         "cores": nthreads,
         "kind": "reference",
-        "sample": f"layers 0-1 of the step ({n} ggml mul_mat nodes, {nbytes/1e6:.1f} MB Q4_K+fp32), "
+        "sample": f"layers 0-9 of the step ({n} ggml mul_mat nodes, {nbytes/1e6:.1f} MB Q4_K+fp32), "
                   f"ggml_graph_compute with {nthreads} threads, median of {reps} runs "
                   f"({med*1e3:.2f} ms each); {os.path.basename(os.path.dirname(path))} build",
+        "value_4_threads": round(nbytes / med4 / 1e9, 2) if med4 else None,
+        "tok_s_equiv": round(1.0 / (med * 4268590592 / nbytes), 2),
         "parity_outside_tol": worst_bad,
     }
     return res, None
@@ -227,6 +259,9 @@ def run_decode8b(args):
     achieved = step_bytes / (gemv_ms * 1e-3) / 1e9
     log(f"[bench] step {ms*1e3:.1f} us ({launches} launches), {value:.1f} GB/s = {value*1e9/PEAK_HBM*100:.1f}% "
         f"of 8 TB/s, {1e3/ms:.0f} tok/s-equiv")
+    stages_t = time_stage_kinds(ctx, stages)
+    for k, v in stages_t.items():
+        log(f"[bench]   {k:8s} {v['us_per_launch']:7.2f} us/launch  {v['GBps']:7.1f} GB/s")
     traffic = load_traffic("decode8b")
     cpu, why = (None, "skipped")
     if not args.no_cpu:
@@ -263,15 +298,16 @@ def run_decode8b(args):
         "gflops": round(2 * 7568097280 / (ms * 1e-3) / 1e9, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_q4k_kernel",
+            "kernel": "gemv_decode_kernel",
             "achieved": round(achieved, 2),
             "peak": 8000.0,
             "unit": "GB/s",
             "frac": round(achieved / 8000.0, 4),
-            "traffic": traffic.get("bytes_per_launch") if traffic else None,
+            "traffic": round(traffic["step"]["bytes_per_launch"]) if traffic else None,
             "avg_launch_us": round(gemv_ms * 1e3 / launches, 3),
             "bytes_per_launch": step_bytes // launches,
         },
+        "stages": stages_t,
         "cpu_baseline": cpu,
     }
     if cpu is None:
@@ -369,12 +405,35 @@ def run_moe(args):
     ctx.close()
 
 
+def run_copy(args):
+    """A plain device-to-device copy of 1 GiB (the runtime's blit kernel): the
+    known-size reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE."""
+    from spq4k.hip import _lib, check, D2D
+    ctx = spq4k.Context(0)
+    n = 1 << 30
+    a, b = DeviceArray(n // 4), DeviceArray(n // 4)
+    ctx.synth_fill_dev(a.ptr, n // 4, 1, spq4k.DIST_NORMAL, 0, 0.0, 1.0, 1.0, 0)
+    ctx.synchronize()
+    reps = 3
+    e0, e1 = Event(), Event()
+    e0.record(ctx.stream)
+    for _ in range(reps):
+        check(_lib().hipMemcpyAsync(b.ptr, a.ptr, n, D2D, ctx.stream), "hipMemcpyAsync D2D")
+    e1.record(ctx.stream)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    print(json.dumps({"metric": "device-to-device copy", "bytes_per_copy": n, "copies": reps,
+                      "us_per_copy": round(ms * 1e3, 2), "GBps_read_plus_write": round(2 * n / (ms * 1e-3) / 1e9, 1)}),
+          flush=True)
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe"])
+    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -389,6 +448,8 @@ def main():
         run_prefill(args)
     elif args.config == "moe":
         run_moe(args)
+    elif args.config == "copy":
+        run_copy(args)
     elif args.config == "largek":
         for (M, K) in ((5120, 27648), (27648, 5120)):
             for T in (1, 4, 8):

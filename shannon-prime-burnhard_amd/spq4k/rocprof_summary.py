@@ -1,0 +1,141 @@
+"""Summarise rocprofv3 CSV output of bench.py into the text kept under profiles/.
+
+    python -m spq4k.rocprof_summary --trace DIR --fetch DIR --write DIR \
+        --fetch-copy DIR --write-copy DIR --out profiles/NAME.md --json profiles/NAME.json
+
+--trace holds a `rocprofv3 --kernel-trace --stats --output-format csv` run of
+`bench.py --no-cpu` (decode8b); --fetch / --write hold `--pmc FETCH_SIZE` /
+`--pmc WRITE_SIZE` runs of the same command; --fetch-copy / --write-copy the
+same two counters over `bench.py --config copy` (three 1 GiB device-to-device
+copies), which scale the counters to bytes: factor = copied bytes / counter
+bytes. Per decode stage the summary gives the average launch duration, the
+HBM bytes read and written per launch (scaled) and the algorithmic bytes.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import statistics
+import sys
+
+# The 8B decode step (bench.py build_decode8b): 36 x [qkv, o, gate_up, down], lm_head.
+STAGES = ["qkv", "o", "gate_up", "down"]
+SHAPES = {  # (rows, K) per matrix of each stage
+    "qkv": [(4096, 4096), (1024, 4096), (1024, 4096)],
+    "o": [(4096, 4096)],
+    "gate_up": [(12288, 4096), (12288, 4096)],
+    "down": [(4096, 12288)],
+    "lm_head": [(151936, 4096)],
+}
+COPY_BYTES = 1 << 30
+
+
+def alg_bytes(stage):
+    return sum(M * (K // 256) * 144 + 4 * K + 4 * M for M, K in SHAPES[stage])
+
+
+def _csv(d, suffix):
+    files = glob.glob(os.path.join(d, f"*{suffix}"))
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} in {d}")
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def _gemv(rows):
+    return [r for r in rows if "gemv" in r["Kernel_Name"]]
+
+
+def _staged(rows, key):
+    """Group the GEMV dispatches by decode stage. The first 145 dispatches (in
+    dispatch order) are one decode step, [qkv, o, gate_up, down] x 36 then
+    lm_head; each stage runs its own kernel instantiation, which maps every
+    later dispatch (step replays and per-stage replays alike) to its stage."""
+    rows = sorted(rows, key=lambda r: int(r[key]))
+    name_of = {}
+    for i, r in enumerate(rows[:145]):
+        st = "lm_head" if i == 144 else STAGES[i % 4]
+        if name_of.setdefault(r["Kernel_Name"], st) != st:
+            raise ValueError(f"stages {st} and {name_of[r['Kernel_Name']]} share {r['Kernel_Name']}")
+    out = {s: [] for s in STAGES + ["lm_head"]}
+    for r in rows:
+        out[name_of[r["Kernel_Name"]]].append(r)
+    return out
+
+
+def _copy_factor(d):
+    vals = [float(r["Counter_Value"]) * 1024 for r in _csv(d, "counter_collection.csv")
+            if "copyBuffer" in r["Kernel_Name"]]
+    return COPY_BYTES / statistics.median(vals), statistics.median(vals)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    for a in ("trace", "fetch", "write", "fetch_copy", "write_copy", "out", "json"):
+        ap.add_argument("--" + a.replace("_", "-"), required=True)
+    ap.add_argument("--command", action="append", default=[], help="command line to record (repeatable)")
+    args = ap.parse_args(argv)
+
+    trace = _gemv(_csv(args.trace, "kernel_trace.csv"))
+    by_stage = _staged(trace, "Dispatch_Id" if "Dispatch_Id" in trace[0] else "Start_Timestamp")
+    f_fetch, copy_fetch = _copy_factor(args.fetch_copy)
+    f_write, copy_write = _copy_factor(args.write_copy)
+    fetch = _staged(_gemv(_csv(args.fetch, "counter_collection.csv")), "Dispatch_Id")
+    write = _staged(_gemv(_csv(args.write, "counter_collection.csv")), "Dispatch_Id")
+
+    lines = []
+    tot_us = tot_alg = tot_hbm = 0.0
+    n_launch = 0
+    res = {"copy_calibration": {"bytes": COPY_BYTES, "fetch_counter_bytes": copy_fetch, "fetch_factor": f_fetch,
+                                "write_counter_bytes": copy_write, "write_factor": f_write}, "stages": {}}
+    for st in STAGES + ["lm_head"]:
+        rs = by_stage[st]
+        dur = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000 for r in rs]
+        fb = [float(r["Counter_Value"]) * 1024 * f_fetch for r in fetch[st]]
+        wb = [float(r["Counter_Value"]) * 1024 * f_write for r in write[st]]
+        us = statistics.mean(dur)
+        rd, wr = statistics.mean(fb), statistics.mean(wb)
+        a = alg_bytes(st)
+        per_step = 1 if st == "lm_head" else 36
+        tot_us += us * per_step
+        tot_alg += a * per_step
+        tot_hbm += (rd + wr) * per_step
+        n_launch += per_step
+        kname = rs[0]["Kernel_Name"].replace("spq4k::", "").replace("(spq4k::GemvParams)", "")
+        res["stages"][st] = {"kernel": kname, "launches_measured": len(dur), "avg_us": us, "hbm_read_bytes": rd,
+                             "hbm_write_bytes": wr, "algorithmic_bytes": a}
+        lines.append(f"| {st} | `{kname}` | {len(dur)} | {us:.3f} | {a / 1e6:.3f} | {rd / 1e6:.3f} | {wr / 1e6:.4f} "
+                     f"| {(rd + wr) / a:.3f} | {a / us / 1e3:.0f} |")
+    avg_us = tot_us / n_launch
+    res["step"] = {"launches": n_launch, "sum_of_avg_launch_us": tot_us, "avg_launch_us": avg_us,
+                   "algorithmic_bytes_per_launch": tot_alg / n_launch, "bytes_per_launch": tot_hbm / n_launch,
+                   "hbm_over_algorithmic": tot_hbm / tot_alg, "achieved_GBps": tot_alg / tot_us / 1e3}
+    with open(args.json, "w") as f:
+        json.dump(res, f, indent=1)
+    with open(args.out, "w") as f:
+        f.write("# gemv_decode_kernel — 8B decode sweep (bench.py decode8b), rocprofv3 on MI355X\n\n")
+        f.write("Commands (from the repository root on the GPU box):\n\n```\n")
+        for c in args.command:
+            f.write(c + "\n")
+        f.write("```\n\n")
+        f.write("Per stage: average launch duration from the kernel trace; HBM bytes per launch from FETCH_SIZE / "
+                "WRITE_SIZE (KiB per dispatch) scaled by the copy calibration below; algorithmic bytes = Q4_K "
+                "weights + fp32 x + fp32 y of the launch.\n\n")
+        f.write("| stage | kernel | launches | avg us | algorithmic MB | HBM read MB | HBM write MB | HBM/alg | "
+                "alg GB/s |\n|---|---|---|---|---|---|---|---|---|\n")
+        f.write("\n".join(lines) + "\n\n")
+        f.write(f"Step: {n_launch} launches, sum of average durations {tot_us:.1f} us, average launch "
+                f"{avg_us:.3f} us, algorithmic {tot_alg / n_launch / 1e6:.3f} MB/launch, HBM "
+                f"{tot_hbm / n_launch / 1e6:.3f} MB/launch ({tot_hbm / tot_alg:.3f} x algorithmic), "
+                f"{tot_alg / tot_us / 1e3:.1f} GB/s algorithmic.\n\n")
+        f.write(f"Copy calibration: a {COPY_BYTES} B device-to-device copy reads {copy_fetch:.0f} B by FETCH_SIZE "
+                f"(factor {f_fetch:.4f}) and writes {copy_write:.0f} B by WRITE_SIZE (factor {f_write:.4f}).\n")
+    print(open(args.out).read())
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
