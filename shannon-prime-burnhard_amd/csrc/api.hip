@@ -30,6 +30,8 @@ struct spq4k_ctx {
     int force_bpr = 0;           // tuning override (SPQ4K_GEMV_BPR = 1, 2, 4 or 8)
     int preq_mode = 0;           // SPQ4K_GEMV_PREQ: 0 auto, 1 always, 2 never
     int no_decode = 0;           // SPQ4K_GEMV_GENERIC=1: T = 1 also uses the generic kernel
+    int moe_unfused = 0;         // SPQ4K_MOE_UNFUSED=1: routing pass + Q8_K planes + matvec (3 launches)
+    int moe_mode = 0;            // SPQ4K_MOE_MODE=2: skip the small-batch decode mapping
     DecodeCfg dec_force = {0, 0, false, 0};   // SPQ4K_DEC_{WAVES,DEPTH,XFIRST,GRID} overrides
     int dec_xfirst_set = 0;
     char err[256] = {0};
@@ -258,6 +260,8 @@ int spq4k_init(int device, spq4k_ctx** out) {
         if (v == 1 || v == 2 || v == 4 || v == 8) c->force_bpr = v;
     }
     if (const char* f = getenv("SPQ4K_GEMV_GENERIC")) c->no_decode = atoi(f) == 1;
+    if (const char* f = getenv("SPQ4K_MOE_UNFUSED")) c->moe_unfused = atoi(f) == 1;
+    if (const char* f = getenv("SPQ4K_MOE_MODE")) c->moe_mode = atoi(f);
     if (const char* f = getenv("SPQ4K_DEC_WAVES")) {
         const int v = atoi(f);
         if (v == 8 || v == 12 || v == 16) c->dec_force.waves = v;
@@ -553,6 +557,65 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     if (bank->E > 4096 || T * n_used > (1 << 24)) return set_err(c, -EINVAL, "moe: too many experts or pairs");
     const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
     const int64_t rows = T * ne11, n_pairs = T * n_used;
+    // pairs per expert are at most T: chunk width TC, rows per tile from the
+    // number of experts that can be active
+    const int tc = T >= 8 ? 8 : (T >= 4 ? 4 : (T >= 2 ? 2 : 1));
+    const int64_t max_act = n_pairs < E ? n_pairs : E;
+    int64_t Mtot[1] = {(int64_t)M * max_act};
+    const int bpr = pick_bpr(c, Mtot, 1);
+    const int rows_per_tile = gemv_rows_per_tile(bpr);
+    const int tiles_per_expert = (M + rows_per_tile - 1) / rows_per_tile;
+    const int cb_max = LDS_BUDGET / (tc * 292);
+    const int chunk_blocks = nb < cb_max ? nb : cb_max;
+    // small batches: the decode mapping (every routed pair's rows in one
+    // sweep; an expert chosen twice is streamed twice, so only for T <= 4)
+    if (T <= 4 && n_pairs <= MOE_DEC_MAX_PAIRS && rows <= MOE_DEC_MAX_XROWS && moe_decode_supported(nb) &&
+        !c->moe_unfused && c->moe_mode != 2 &&
+        (size_t)q8lds_bytes((int)rows * nb) <= (size_t)LDS_BUDGET) {
+        MoeFusedParams f;
+        memset(&f, 0, sizeof f);
+        f.ids = ids;
+        f.X = X;
+        f.bank = bank->data;
+        f.expert_bytes = (size_t)M * nb * SPQ4K_Q4K_BLOCK_BYTES;
+        f.Y = Y;
+        f.n_pairs = (int32_t)n_pairs;
+        f.n_used = (int32_t)n_used;
+        f.ne11 = (int32_t)ne11;
+        f.K = (int32_t)bank->K;
+        f.M = M;
+        f.nb = nb;
+        f.E = E;
+        f.n_xrows = (int32_t)rows;
+        const int64_t per_wg = moe_decode_rows_per_wg(nb);
+        const int64_t need = (n_pairs * M + per_wg - 1) / per_wg;
+        const int grid = (int)(need < 2 * c->num_cus ? need : 2 * c->num_cus);
+        hipError_t e = launch_moe_decode(f, grid, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "moe decode launch");
+        return 0;
+    }
+    if (n_pairs <= MOE_FUSED_MAX_PAIRS && !c->moe_unfused) {
+        MoeFusedParams f;
+        memset(&f, 0, sizeof f);
+        f.ids = ids;
+        f.X = X;
+        f.bank = bank->data;
+        f.expert_bytes = (size_t)M * nb * SPQ4K_Q4K_BLOCK_BYTES;
+        f.Y = Y;
+        f.n_pairs = (int32_t)n_pairs;
+        f.n_used = (int32_t)n_used;
+        f.ne11 = (int32_t)ne11;
+        f.K = (int32_t)bank->K;
+        f.M = M;
+        f.nb = nb;
+        f.tiles_per_expert = tiles_per_expert;
+        f.chunk_blocks = chunk_blocks;
+        const int64_t grid = (int64_t)E * tiles_per_expert;
+        if (grid > (1ll << 31) - 1) return set_err(c, -EINVAL, "moe: grid too large");
+        hipError_t e = launch_moe_fused(f, tc, bpr, (int)grid, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "moe fused launch");
+        return 0;
+    }
     // scratch: Q8_K planes | routing tables
     const size_t q8_bytes = ((size_t)rows * nb * 292 + 255) & ~(size_t)255;
     const size_t route_bytes = (size_t)(1 + 3 * E + n_pairs) * sizeof(int32_t);
@@ -584,16 +647,8 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     p.nb = nb;
     p.n_used = (int)n_used;
     p.ne11 = (int)ne11;
-    // pairs per expert are at most T: chunk width TC, and rows per tile from
-    // the number of experts that can be active
-    const int tc = T >= 8 ? 8 : (T >= 4 ? 4 : (T >= 2 ? 2 : 1));
-    const int64_t max_act = n_pairs < E ? n_pairs : E;
-    int64_t Mtot[1] = {(int64_t)M * max_act};
-    const int bpr = pick_bpr(c, Mtot, 1);
-    const int rows_per_tile = gemv_rows_per_tile(bpr);
-    p.tiles_per_expert = (M + rows_per_tile - 1) / rows_per_tile;
-    const int cb_max = LDS_BUDGET / (tc * 292);
-    p.chunk_blocks = nb < cb_max ? nb : cb_max;
+    p.tiles_per_expert = tiles_per_expert;
+    p.chunk_blocks = chunk_blocks;
     const int64_t grid = max_act * p.tiles_per_expert;
     if (grid > (1ll << 31) - 1) return set_err(c, -EINVAL, "moe: grid too large");
     e = launch_moe_gemv(p, tc, bpr, (int)grid, c->stream);

@@ -16,6 +16,8 @@
 //   3. moe_gemv_kernel: workgroup (a, tile) takes active expert a and a tile
 //      of its rows; its pairs are processed TC at a time, each chunk staged
 //      from the Q8_K planes into LDS and streamed with the dense GEMV's code.
+// Calls with at most MOE_FUSED_MAX_PAIRS pairs use moe_fused_kernel instead,
+// which does all three steps in one launch.
 #include "gemv_core.h"
 #include "launch.h"
 
@@ -123,6 +125,231 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeParams p) {
             for (int t = 0; t < TC; ++t)
                 if (t < nt) p.Y[(int64_t)s_pair[t] * M + row] = acc[t];
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Single-launch form (n_pairs <= MOE_FUSED_MAX_PAIRS): workgroup (e, tile)
+// lists the (token, slot) pairs routed to expert e itself (wave 0 scans ids
+// with a ballot compaction that keeps pair order), returns at once when e is
+// unused, and quantises the routed input rows from fp32 into LDS as it
+// streams its rows: no routing pass, no Q8_K planes, one launch per call.
+template <int TC, int BPR, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void moe_fused_kernel(MoeFusedParams p) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int LPR = 4 * BPR;
+    constexpr int RPW = 64 / LPR;
+    constexpr int ROWS = WAVES * RPW;
+    __shared__ int s_cnt;
+    __shared__ int s_pairs[MOE_FUSED_MAX_PAIRS];
+    __shared__ int s_xrow[TC];
+    __shared__ int s_pair[TC];
+
+    const int e = blockIdx.x / p.tiles_per_expert;
+    const int tile = blockIdx.x - e * p.tiles_per_expert;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+
+    if (wave == 0) {
+        int cnt = 0;
+        for (int base = 0; base < p.n_pairs; base += 64) {
+            const int i = base + lane;
+            const bool hit = i < p.n_pairs && p.ids[i] == e;
+            const uint64_t m = __ballot(hit);
+            const int before = __popcll(m & ((1ull << lane) - 1ull));
+            if (hit) s_pairs[cnt + before] = i;
+            cnt += __popcll(m);
+        }
+        if (lane == 0) s_cnt = cnt;
+    }
+    __syncthreads();
+    const int pcnt = s_cnt;
+    if (pcnt == 0) return;   // uniform over the workgroup
+
+    const int l4 = lane & 3;
+    const int bsub = (lane >> 2) & (BPR - 1);
+    const int M = p.M;
+    const int row = tile * ROWS + wave * RPW + lane / LPR;
+    const bool row_ok = row < M;
+    const int nb = p.nb;
+    const uint8_t* __restrict__ wrow =
+        p.bank + (size_t)e * p.expert_bytes + (size_t)(row_ok ? row : M - 1) * ((size_t)nb * Q4K_BYTES);
+    const int CB = p.chunk_blocks;
+    const Q8Lds L = q8lds_carve(smem, TC * CB);
+
+    for (int c = 0; c < pcnt; c += TC) {
+        const int nt = min(TC, pcnt - c);
+        __syncthreads();   // the previous chunk's readers of s_pair / s_xrow are done
+        if (threadIdx.x < TC) {
+            const int i = min((int)threadIdx.x, nt - 1);   // clamp: duplicate slots are computed, not stored
+            const int pair = s_pairs[c + i];
+            const int t = pair / p.n_used;
+            const int sl = pair - t * p.n_used;
+            s_pair[threadIdx.x] = pair;
+            s_xrow[threadIdx.x] = t * p.ne11 + (sl % p.ne11);
+        }
+        __syncthreads();
+        float acc[TC];
+#pragma unroll
+        for (int t = 0; t < TC; ++t) acc[t] = 0.0f;
+        stream_row<TC, BPR, U>(wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int, int) { return 0; },
+                               [&](int c0, int nblk, int) {
+            // quantise block c0 + b of each routed input row into slot t * CB + b
+            const int nitems = TC * nblk;
+            for (int base = 0; base < nitems; base += 4 * WAVES) {
+                const int item0 = base + wave * 4 + (lane >> 4);
+                const bool valid = item0 < nitems;
+                const int item = valid ? item0 : nitems - 1;
+                const int t = item / nblk;
+                const int b = item - t * nblk;
+                const XRegs r = load_x16(p.X, p.K, s_xrow[t], c0 + b);
+                store_q8_item(r, valid, t * CB + b, L);
+            }
+        });
+#pragma unroll
+        for (int t = 0; t < TC; ++t) acc[t] = group_sum_last<LPR>(acc[t]);
+        if (row_ok && (lane & (LPR - 1)) == LPR - 1) {
+#pragma unroll
+            for (int t = 0; t < TC; ++t)
+                if (t < nt) p.Y[(int64_t)s_pair[t] * M + row] = acc[t];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Small-batch form (n_pairs <= MOE_DEC_MAX_PAIRS): the decode mapping. The
+// rows of all routed (token, slot) pairs form one sweep, pair p owning rows
+// [p M, (p + 1) M) of expert ids[p] with input row t * ne11 + s % ne11. Every
+// workgroup quantises the routed input rows once into LDS; LPR = 4 * BSL lanes
+// work on one row (quarter l4 of blocks bsub, bsub + BSL, ...) and waves walk
+// rows g, g + G, ... of the sweep. An expert chosen by several pairs is
+// streamed once per pair, which is why this form is kept to small batches.
+// An id outside [0, E) leaves that pair's outputs untouched.
+template <int NB, int BSL, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int LPR = 4 * BSL;
+    constexpr int RPW = 64 / LPR;
+    constexpr int NIT = (NB + BSL - 1) / BSL;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int l4 = lane & 3;
+    const int bsub = (lane & (LPR - 1)) >> 2;
+    const int M = p.M;
+    const int total = p.n_pairs * M;
+    const int G = gridDim.x * WAVES * RPW;
+    const int g = (blockIdx.x * WAVES + wave) * RPW + lane / LPR;
+    const int nx = p.n_xrows;
+    const Q8Lds L = q8lds_carve(smem, nx * NB);
+
+    // where row r of the sweep lives: expert (or -1), its row, its input row
+    struct Loc {
+        const uint8_t* w;
+        int e, lr, xs;
+    };
+    auto locate = [&](int r) {
+        Loc l;
+        const int rc = r < total ? r : total - 1;
+        const int pr = rc / M;
+        l.lr = rc - pr * M;
+        const int e = p.ids[pr];
+        l.e = (r < total && e >= 0 && e < p.E) ? e : -1;
+        const int t = pr / p.n_used;
+        l.xs = (t * p.ne11 + (pr - t * p.n_used) % p.ne11) * NB;
+        l.w = p.bank + (size_t)(l.e >= 0 ? l.e : 0) * p.expert_bytes + (size_t)l.lr * ((size_t)NB * Q4K_BYTES);
+        return l;
+    };
+    auto load = [&](const Loc& l, W4 (&w)[NIT]) {
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int bb = bsub + BSL * it;
+            w[it] = load_w4(l.w + (size_t)(bb < NB ? bb : NB - 1) * Q4K_BYTES, l4);
+        }
+    };
+    // order of the loads (they complete in order): the expert id of the first
+    // row, the first pass of input rows, then that row's weights, so that the
+    // quantisation waits only for x while the weights are in flight
+    const int item_a = wave * 4 + (lane >> 4);
+    const int ci_a = item_a < nx * NB ? item_a : nx * NB - 1;
+    const int xr_a = ci_a / NB;
+    Loc cur = locate(g);
+    const XRegs xa = load_x16(p.X, p.K, xr_a, ci_a - xr_a * NB);
+    W4 w[NIT];
+    load(cur, w);
+    store_q8_item(xa, item_a < nx * NB, ci_a, L);
+    for (int base = 4 * WAVES; base < nx * NB; base += 4 * WAVES) {
+        const int item0 = base + item_a;
+        const bool valid = item0 < nx * NB;
+        const int item = valid ? item0 : nx * NB - 1;
+        const int xr = item / NB;
+        const XRegs r = load_x16(p.X, p.K, xr, item - xr * NB);
+        store_q8_item(r, valid, item, L);
+    }
+    __syncthreads();
+    for (int r = g; r < total; r += G) {
+        float acc[1] = {0.0f};
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int bb = bsub + BSL * it;
+            block_dot<1>(w[it], l4, L, cur.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && cur.e >= 0, acc);
+        }
+        const float sum = group_sum_last<LPR>(acc[0]);
+        if (cur.e >= 0 && (lane & (LPR - 1)) == LPR - 1) p.Y[(int64_t)(r / M) * M + cur.lr] = sum;
+        if (r + G < total) {
+            cur = locate(r + G);
+            load(cur, w);
+        }
+    }
+}
+
+template <int NB, int BSL>
+static hipError_t launch_mdec(const MoeFusedParams& p, int grid, hipStream_t st) {
+    constexpr int WAVES = 8;
+    const size_t lds = (size_t)q8lds_bytes(p.n_xrows * NB);
+    hipLaunchKernelGGL((moe_decode_kernel<NB, BSL, WAVES>), dim3(grid), dim3(WAVES * 64), lds, st, p);
+    return hipGetLastError();
+}
+
+bool moe_decode_supported(int nb) { return nb == 3 || nb == 8 || nb == 16; }
+
+// rows of the sweep per workgroup pass: WAVES * 64 / (4 * BSL)
+int moe_decode_rows_per_wg(int nb) { return nb == 3 ? 32 : (nb == 8 ? 16 : 8); }
+
+hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st) {
+    switch (p.nb) {
+        case 3: return launch_mdec<3, 4>(p, grid, st);
+        case 8: return launch_mdec<8, 8>(p, grid, st);
+        case 16: return launch_mdec<16, 16>(p, grid, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int TC, int BPR>
+static hipError_t launch_fused_tb(const MoeFusedParams& p, int grid, hipStream_t st) {
+    constexpr int WAVES = 4, U = 2;
+    const size_t lds = (size_t)q8lds_bytes(TC * p.chunk_blocks);
+    hipLaunchKernelGGL((moe_fused_kernel<TC, BPR, WAVES, U>), dim3(grid), dim3(WAVES * 64), lds, st, p);
+    return hipGetLastError();
+}
+
+template <int TC>
+static hipError_t launch_fused_t(const MoeFusedParams& p, int bpr, int grid, hipStream_t st) {
+    switch (bpr) {
+        case 1: return launch_fused_tb<TC, 1>(p, grid, st);
+        case 2: return launch_fused_tb<TC, 2>(p, grid, st);
+        case 4: return launch_fused_tb<TC, 4>(p, grid, st);
+        case 8: return launch_fused_tb<TC, 8>(p, grid, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st) {
+    switch (tc) {
+        case 1: return launch_fused_t<1>(p, bpr, grid, st);
+        case 2: return launch_fused_t<2>(p, bpr, grid, st);
+        case 4: return launch_fused_t<4>(p, bpr, grid, st);
+        case 8: return launch_fused_t<8>(p, bpr, grid, st);
+        default: return hipErrorInvalidValue;
     }
 }
 

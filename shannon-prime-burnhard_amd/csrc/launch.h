@@ -67,6 +67,29 @@ struct MoeParams {
 };
 
 hipError_t launch_moe_route(const int32_t* ids, int n_pairs, int E, const MoeRoute& r, hipStream_t st);
+
+// single-launch MoE (routing and Q8_K quantisation inside the matvec kernel)
+constexpr int MOE_FUSED_MAX_PAIRS = 2048;
+struct MoeFusedParams {
+    const int32_t* ids;      // [n_pairs] = [T][n_used]
+    const float* X;          // [T * ne11][K] fp32, 16-byte aligned rows
+    const uint8_t* bank;     // E experts of [M][nb] Q4_K blocks
+    size_t expert_bytes;
+    float* Y;                // [T][n_used][M]
+    int32_t n_pairs, n_used, ne11, K, M, nb;
+    int32_t tiles_per_expert;
+    int32_t chunk_blocks;
+    int32_t E;          // experts in the bank (moe_decode_kernel)
+    int32_t n_xrows;    // input rows T * ne11 (moe_decode_kernel)
+};
+hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st);
+
+// small-batch MoE in the decode mapping (one sweep over the rows of all pairs)
+constexpr int MOE_DEC_MAX_PAIRS = 64;
+constexpr int MOE_DEC_MAX_XROWS = 64;
+bool moe_decode_supported(int nb);
+int moe_decode_rows_per_wg(int nb);
+hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st);
 hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st);
 
 // prefill matmul on matrix cores (k_gemm.hip)

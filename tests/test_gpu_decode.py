@@ -10,11 +10,10 @@ below. Tolerance: the reference's close_enough (1e-4 relative or 1e-5
 absolute, tests/desktop/test_sp_kernels.cpp:34-48) against the oracle's
 restatement of ggml's x86 path (bit-identical to the reference's own
 ggml_vec_dot_q4_K_q8_K, pinned in test_oracle_golden.py)."""
-import os
-
 import numpy as np
 import pytest
 
+from _envctx import context_with as _context_with
 from _oracle import close_enough
 
 pytestmark = pytest.mark.gpu
@@ -30,22 +29,6 @@ def _check(got, exp, what):
         i = np.argwhere(~ok)[0]
         raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} outside tolerance; first {tuple(i)} "
                              f"got {got[tuple(i)]!r} exp {exp[tuple(i)]!r}")
-
-
-def _context_with(env):
-    """A fresh context created with the given SPQ4K_* overrides in effect."""
-    import spq4k
-    saved = {k: os.environ.get(k) for k in env}
-    try:
-        for k, v in env.items():
-            os.environ[k] = str(v)
-        return spq4k.Context(0)
-    finally:
-        for k, v in saved.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
 
 
 @pytest.mark.parametrize("M,K", [(1, 4096), (100, 4096), (4096, 4096), (37, 12288), (4096, 12288)])

@@ -81,3 +81,52 @@ def test_moe_rejects_bad_ids(ctx):
     X = rng.standard_normal((2, 1, 256)).astype(np.float32)
     with pytest.raises(spq4k.Spq4kError):
         ctx.mul_mat_id(bank, X, np.array([[0, 4], [1, 2]], np.int32))
+
+
+@pytest.mark.parametrize("T,ne11,M,K", [(1, 1, 768, 2048), (1, 8, 2048, 768), (3, 8, 2048, 768), (4, 1, 512, 4096),
+                                        (5, 8, 2048, 768), (32, 1, 768, 2048)])
+def test_moe_paths_agree(oracle, T, ne11, M, K):
+    """Every MoE path against the oracle: the planner's choice, the grouped
+    single-launch kernel (SPQ4K_MOE_MODE=2) and the three-launch path
+    (routing pass, Q8_K planes, matvec)."""
+    from _envctx import context_with
+    E, k = 128, 8
+    ids = _topk_ids(np.random.default_rng(T), T, E, k)
+    X = np.random.default_rng(T + 1).standard_normal((T, ne11, K)).astype(np.float32)
+    outs, host = [], None
+    for env in ({}, {"SPQ4K_MOE_MODE": 2}, {"SPQ4K_MOE_UNFUSED": 1}):
+        c = context_with(env)
+        try:
+            bank, host = _gpu_bank(c, E, M, K, 71)
+            outs.append((env, c.mul_mat_id(bank, X, ids)))
+            bank.free()
+        finally:
+            c.close()
+    exp = oracle.mul_mat_id(host, M, K, E, X, ids)
+    for env, got in outs:
+        _check(got, exp, f"{env} T={T} ne11={ne11} M={M} K={K}")
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_moe_device_ids_out_of_range_leave_outputs(oracle, mode):
+    """Device-pointer entry point: an id outside [0, E) is not routed, so its
+    output rows keep their previous contents (the host entry point rejects it)."""
+    from spq4k.hip import DeviceArray
+    from _envctx import context_with
+    ctx = context_with({"SPQ4K_MOE_MODE": mode})
+    E, M, K, T, k = 16, 256, 2048, 2, 4
+    bank, host = _gpu_bank(ctx, E, M, K, 5)
+    ids = np.array([[3, 99, 7, -1], [1, 2, 3, 4]], np.int32)
+    X = np.random.default_rng(2).standard_normal((T, 1, K)).astype(np.float32)
+    idd, Xd = DeviceArray.from_host(ids), DeviceArray.from_host(X)
+    Yd = DeviceArray.from_host(np.full((T, k, M), 7.0, np.float32))
+    ctx.moe_dev(bank, idd.ptr, k, 1, T, Xd.ptr, Yd.ptr)
+    ctx.synchronize()
+    Y = Yd.to_host().reshape(T, k, M)
+    assert (Y[0, 1] == 7.0).all() and (Y[0, 3] == 7.0).all()
+    ok_ids = ids.copy(); ok_ids[0, 1] = 0; ok_ids[0, 3] = 0
+    exp = oracle.mul_mat_id(host, M, K, E, X, ok_ids)
+    for t, s in ((0, 0), (0, 2), (1, 0), (1, 1), (1, 2), (1, 3)):
+        _check(Y[t, s], exp[t, s], f"slot {t},{s}")
+    bank.free()
+    ctx.close()
