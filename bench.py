@@ -343,65 +343,94 @@ def run_single(args, M, K, T, dist, outlier, name):
 
 
 def run_prefill(args):
-    """the 8B layer shapes as a prefill matmul, T tokens."""
+    """the 8B layer shapes as a prefill matmul, T tokens.
+    Weights are cold (8 distinct layers, 0.9 GB, replayed in one graph); the
+    matrices that share an input run as one call, as in the decode step:
+    [q,k,v] -> o -> [gate,up] -> down."""
     ctx = spq4k.Context(0)
+    NL = 8
     syn = Synth(ctx, FFN * HID)
     shapes = [("q", HID, HID), ("k", KV, HID), ("v", KV, HID), ("o", HID, HID), ("gate", FFN, HID),
               ("up", FFN, HID), ("down", HID, FFN)]
-    ws = [syn.weights(M, K, 300 + i) for i, (_, M, K) in enumerate(shapes)]
+    layers = [[syn.weights(M, K, 300 + 10 * L + i) for i, (_, M, K) in enumerate(shapes)] for L in range(NL)]
+    ctx.synchronize()
     for T in (16, 128, 512):
         X = {K: syn.activations(T * K, 9 + K) for K in (HID, FFN)}
-        Y = DeviceArray(T * FFN)
+        Ys = [DeviceArray(T * M) for (_, M, _) in shapes]
         with Graph.capture(ctx.stream) as g:
-            for w, (_, M, K) in zip(ws, shapes):
-                ctx.gemm_dev(w, X[K].ptr, Y.ptr, T)
-        ms = time_graph(ctx, g, max(5, args.steps // 5), 2)
+            for ws in layers:
+                ctx.gemm_multi_dev(ws[0:3], X[HID].ptr, [y.ptr for y in Ys[0:3]], T)
+                ctx.gemm_dev(ws[3], X[HID].ptr, Ys[3].ptr, T)
+                ctx.gemm_multi_dev(ws[4:6], X[HID].ptr, [y.ptr for y in Ys[4:6]], T)
+                ctx.gemm_dev(ws[6], X[FFN].ptr, Ys[6].ptr, T)
+        ms = time_graph(ctx, g, max(3, args.steps // 10), 1) / NL
         flops = 2 * T * sum(M * K for _, M, K in shapes)
         wbytes = sum(q4k_bytes(M, K) for _, M, K in shapes)
         abytes = wbytes + 4 * T * sum(M + K for _, M, K in shapes)
         tops = flops / (ms * 1e-3) / 1e12
+        bound_us = max(abytes / PEAK_HBM, flops / 5.0e15) * 1e6
         print(json.dumps({"metric": f"Q4_K prefill matmul, one 8B layer, T={T}", "value": round(tops, 2),
                           "unit": "TOP/s (int8)", "us_per_layer": round(ms * 1e3, 2),
                           "pct_of_int8_mfma_peak": round(tops / 5000 * 100, 2),
                           "effective_GBps": round(abytes / (ms * 1e-3) / 1e9, 1),
-                          "tokens_per_s": round(T / (ms * 1e-3 * (LAYERS + 0)), 1),
-                          "config": {"workload": f"8B layer (q,k,v,o,gate,up,down) x T={T} tokens, Q4_K",
-                                     "T": T}}), flush=True)
+                          "roofline_us": round(bound_us, 2), "frac_of_roofline": round(bound_us / (ms * 1e3), 4),
+                          "tokens_per_s_36_layers": round(T / (ms * 1e-3 * LAYERS), 1),
+                          "config": {"workload": f"8B layer (q,k,v,o,gate,up,down) x T={T} tokens, Q4_K, "
+                                                 f"{NL} layers cold", "T": T}}), flush=True)
+        for a in list(X.values()) + Ys:
+            a.free()
+    syn.tmp.free()
     ctx.close()
 
 
 def run_moe(args):
-    """128 experts (gate/up 768x2048, down 2048x768), top-8, T = 1..32."""
+    """128 experts (gate/up 768x2048, down 2048x768), top-8,
+    T = 1..32. Timed cold: 8 layers, each with its own three expert banks
+    (2.7 GB in all, larger than the 256 MB Infinity Cache) and its own routing
+    (top-8 of seeded N(0,1) logits per token), replayed as one graph; a layer
+    is the gate, up and down GGML_OP_MUL_MAT_ID calls."""
     ctx = spq4k.Context(0)
-    E, k = 128, 8
+    E, k, NL = 128, 8, 8
+    shapes = (("gate", 768, 2048), ("up", 768, 2048), ("down", 2048, 768))
     syn = Synth(ctx, E * 768 * 2048)
-    banks = {}
-    for name, M, K in (("gate", 768, 2048), ("up", 768, 2048), ("down", 2048, 768)):
-        w = ctx.alloc_weights(M, K, E)
-        ctx.synth_fill_dev(syn.tmp.ptr, E * M * K, 500 + M, spq4k.DIST_NORMAL, K, 0.0, 0.02, 1.0, 0)
-        ctx.quantize_q4K_dev(syn.tmp.ptr, w.data_ptr, E * M, K)
-        banks[name] = (w, M, K)
+    layers = []
+    for L in range(NL):
+        banks = []
+        for i, (name, M, K) in enumerate(shapes):
+            w = ctx.alloc_weights(M, K, E)
+            ctx.synth_fill_dev(syn.tmp.ptr, E * M * K, 500 + 10 * L + i, spq4k.DIST_NORMAL, K, 0.0, 0.02, 1.0, 0)
+            ctx.quantize_q4K_dev(syn.tmp.ptr, w.data_ptr, E * M, K)
+            banks.append((w, M, K))
+        layers.append(banks)
+    ctx.synchronize()
+    syn.tmp.free()
     rng = np.random.default_rng(3)
     for T in (1, 4, 8, 32):
-        logits = rng.standard_normal((T, E)).astype(np.float32)
-        ids = np.argsort(-logits, axis=1, kind="stable")[:, :k].astype(np.int32)
-        idd = DeviceArray.from_host(ids)
+        ids_l = [np.argsort(-rng.standard_normal((T, E)).astype(np.float32), axis=1, kind="stable")[:, :k]
+                 .astype(np.int32) for _ in range(NL)]
+        idd = [DeviceArray.from_host(i) for i in ids_l]
         xg = syn.activations(T * 2048, 11)
         xd = syn.activations(T * k * 768, 12)
         Y = DeviceArray(T * k * 2048)
         with Graph.capture(ctx.stream) as g:
-            w, M, K = banks["gate"]; ctx.moe_dev(w, idd.ptr, k, 1, T, xg.ptr, Y.ptr)
-            w, M, K = banks["up"]; ctx.moe_dev(w, idd.ptr, k, 1, T, xg.ptr, Y.ptr)
-            w, M, K = banks["down"]; ctx.moe_dev(w, idd.ptr, k, k, T, xd.ptr, Y.ptr)
-        ms = time_graph(ctx, g, max(10, args.steps), 3)
-        uniq = len(np.unique(ids))
-        wbytes = uniq * sum(q4k_bytes(M, K) for (_, M, K) in banks.values())
-        abytes = wbytes + 4 * T * k * (2048 + 768) * 2 + 4 * T * k * (768 + 2048)
+            for L in range(NL):
+                (wg, _, _), (wu, _, _), (wd, _, _) = layers[L]
+                ctx.moe_dev(wg, idd[L].ptr, k, 1, T, xg.ptr, Y.ptr)
+                ctx.moe_dev(wu, idd[L].ptr, k, 1, T, xg.ptr, Y.ptr)
+                ctx.moe_dev(wd, idd[L].ptr, k, k, T, xd.ptr, Y.ptr)
+        ms = time_graph(ctx, g, max(5, args.steps // 5), 2) / NL
+        uniq = float(np.mean([len(np.unique(i)) for i in ids_l]))
+        wbytes = uniq * sum(q4k_bytes(M, K) for (_, M, K) in shapes)
+        abytes = wbytes + 4 * T * (2 * 2048 + 2 * k * 768) + 4 * T * k * (768 + 2048)
         gbs = abytes / (ms * 1e-3) / 1e9
         print(json.dumps({"metric": f"Q4_K MoE expert matvec (gate+up+down), T={T}", "value": round(gbs, 1),
                           "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
                           "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2), "unique_experts": uniq,
-                          "config": {"workload": "30B-A3B-like MoE layer, 128 experts, top-8", "T": T}}), flush=True)
+                          "config": {"workload": "30B-A3B-like MoE layer, 128 experts, top-8, 8 layers of banks (cold)",
+                                     "T": T}}), flush=True)
+        for a in idd:
+            a.free()
+        xg.free(); xd.free(); Y.free()
     ctx.close()
 
 

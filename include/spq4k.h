@@ -107,6 +107,9 @@ int spq4k_vec_dot_host(spq4k_ctx *ctx, int n, float *s, const void *vx, const vo
  *                  1596-1600); y[i] is [T][M_i].
  * spq4k_gemm     : GGML_OP_MUL_MAT for any T (prefill; CUDA mmq.cuh:3478):
  *                  Q8_K activations and int8 MFMA on gfx950.
+ * spq4k_gemm_multi: n <= 4 matrices with the same K and the same input X
+ *                  (q/k/v, gate/up of a prefill batch: forward.cpp:1100-1104,
+ *                  1596-1600): X is quantised once; Y[i] is [T][M_i].
  * spq4k_mul_mat  : dispatch by T, as ggml-cuda.cu:2366-2449 does
  *                  (T <= 8 -> gemv, otherwise gemm).
  * spq4k_moe      : GGML_OP_MUL_MAT_ID (ggml_mul_mat_id(as[K,M,E], b[K,ne11,T],
@@ -119,6 +122,8 @@ int spq4k_gemv(spq4k_ctx *ctx, const spq4k_weights *W, const float *x, float *y,
 int spq4k_gemv_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *W, const float *x,
                      float *const *y, int64_t T);
 int spq4k_gemm(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
+int spq4k_gemm_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *W, const float *X, float *const *Y,
+                     int64_t T);
 int spq4k_mul_mat(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
 int spq4k_moe(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int64_t n_used,
               int64_t ne11, int64_t T, const float *X, float *Y);

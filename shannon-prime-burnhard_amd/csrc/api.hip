@@ -32,6 +32,7 @@ struct spq4k_ctx {
     int no_decode = 0;           // SPQ4K_GEMV_GENERIC=1: T = 1 also uses the generic kernel
     int moe_unfused = 0;         // SPQ4K_MOE_UNFUSED=1: routing pass + Q8_K planes + matvec (3 launches)
     int moe_mode = 0;            // SPQ4K_MOE_MODE=2: skip the small-batch decode mapping
+    int gemm_mode = 0;           // SPQ4K_GEMM_MODE: 0 auto, 1 skinny kernel, 2 tiled kernel
     DecodeCfg dec_force = {0, 0, false, 0};   // SPQ4K_DEC_{WAVES,DEPTH,XFIRST,GRID} overrides
     int dec_xfirst_set = 0;
     char err[256] = {0};
@@ -262,6 +263,7 @@ int spq4k_init(int device, spq4k_ctx** out) {
     if (const char* f = getenv("SPQ4K_GEMV_GENERIC")) c->no_decode = atoi(f) == 1;
     if (const char* f = getenv("SPQ4K_MOE_UNFUSED")) c->moe_unfused = atoi(f) == 1;
     if (const char* f = getenv("SPQ4K_MOE_MODE")) c->moe_mode = atoi(f);
+    if (const char* f = getenv("SPQ4K_GEMM_MODE")) c->gemm_mode = atoi(f);
     if (const char* f = getenv("SPQ4K_DEC_WAVES")) {
         const int v = atoi(f);
         if (v == 8 || v == 12 || v == 16) c->dec_force.waves = v;
@@ -519,24 +521,60 @@ int spq4k_gemv_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const f
     return gemv_launch(c, n, W, x, y, T);
 }
 
-int spq4k_gemm(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
+int spq4k_gemm_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y,
+                     int64_t T) {
     int rc = use_device(c);
     if (rc) return rc;
-    if (!W || !W->data || !X || !Y || T < 1 || W->E != 1) return set_err(c, -EINVAL, "gemm: bad arguments");
-    if (!aligned(X, 16) || !aligned(W->data, 16)) return set_err(c, -EINVAL, "gemm: misaligned pointer");
+    if (!W || !Y || n < 1 || n > GEMM_MAX_SEG) return set_err(c, -EINVAL, "gemm: n=%d matrices (1..4)", n);
+    if (!X || T < 1 || !aligned(X, 16)) return set_err(c, -EINVAL, "gemm: bad activations");
     if (T > (1 << 20)) return set_err(c, -EINVAL, "gemm: T too large");
+    if (!W[0]) return set_err(c, -EINVAL, "gemm: null weight");
+    const int64_t K = W[0]->K;
+    for (int i = 0; i < n; ++i) {
+        if (!W[i] || !W[i]->data || !Y[i] || W[i]->E != 1 || W[i]->K != K)
+            return set_err(c, -EINVAL, "gemm: matrices must be non-null, E=1 and share K");
+        if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemm: misaligned weights");
+        if (W[i]->device != c->device) return set_err(c, -EINVAL, "gemm: weights live on another device");
+    }
     GemmParams p;
     memset(&p, 0, sizeof p);
-    p.W = W->data;
-    p.Y = Y;
-    p.M = (int32_t)W->M;
     p.T = (int32_t)T;
-    p.nb = (int32_t)(W->K / SPQ4K_QK_K);
-    rc = q8_planes(c, X, W->K, (int)T, p.nb, &p.Q);
+    p.nb = (int32_t)(K / SPQ4K_QK_K);
+    p.mode = c->gemm_mode;
+    // the input is quantised once for all the matrices
+    rc = q8_planes(c, X, K, (int)T, p.nb, &p.Q);
     if (rc) return rc;
-    hipError_t e = launch_gemm(p, c->stream);
-    if (e != hipSuccess) return hip_fail(c, e, "gemm launch");
+    hipError_t e;
+    if (gemm_use_skinny((int)T, c->gemm_mode)) {
+        int64_t tiles = 0;
+        for (int i = 0; i < n; ++i) {
+            p.seg[i].W = W[i]->data;
+            p.seg[i].Y = Y[i];
+            p.seg[i].M = (int32_t)W[i]->M;
+            p.seg[i].tile_begin = (int32_t)tiles;
+            tiles += (W[i]->M + 15) / 16;
+        }
+        if (tiles * ((T + 63) / 16) > (1ll << 31) - 1) return set_err(c, -EINVAL, "gemm: grid too large");
+        p.nseg = n;
+        p.total_tiles = (int32_t)tiles;
+        e = launch_gemm_skinny(p, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemm skinny launch");
+        return 0;
+    }
+    for (int i = 0; i < n; ++i) {
+        p.W = W[i]->data;
+        p.Y = Y[i];
+        p.M = (int32_t)W[i]->M;
+        e = launch_gemm(p, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemm launch");
+    }
     return 0;
+}
+
+int spq4k_gemm(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
+    const spq4k_weights* ws[1] = {W};
+    float* ys[1] = {Y};
+    return spq4k_gemm_multi(c, 1, ws, X, ys, T);
 }
 
 int spq4k_mul_mat(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {

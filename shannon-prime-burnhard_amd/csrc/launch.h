@@ -93,13 +93,26 @@ hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st);
 hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st);
 
 // prefill matmul on matrix cores (k_gemm.hip)
+constexpr int GEMM_MAX_SEG = 4;
+struct GemmSeg {
+    const uint8_t* W;     // [M][nb] Q4_K
+    float* Y;             // [T][M]
+    int32_t M;
+    int32_t tile_begin;   // first 16-row tile of this segment (skinny kernel)
+};
 struct GemmParams {
-    const uint8_t* W;   // [M][nb] Q4_K
+    const uint8_t* W;   // [M][nb] Q4_K (tiled kernel: one matrix per launch)
     Q8Planes Q;         // Q8_K of the T input rows
     float* Y;           // [T][M]
     int32_t M, T, nb;
+    int32_t mode;       // 0 auto, 1 skinny kernel at any T, 2 tiled kernel at any T
+    GemmSeg seg[GEMM_MAX_SEG];   // skinny kernel: up to four matrices sharing the input
+    int32_t nseg;
+    int32_t total_tiles;
 };
-hipError_t launch_gemm(const GemmParams& p, hipStream_t st);
+bool gemm_use_skinny(int T, int mode);
+hipError_t launch_gemm(const GemmParams& p, hipStream_t st);          // tiled, one matrix
+hipError_t launch_gemm_skinny(const GemmParams& p, hipStream_t st);   // skinny, all segments
 
 // element-wise conversions (k_convert.hip)
 hipError_t launch_quantize_q8k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);

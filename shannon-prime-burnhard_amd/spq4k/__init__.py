@@ -80,6 +80,7 @@ def load_library(path: str | None = None):
         "spq4k_gemv": (I, [V, V, V, V, I64]),
         "spq4k_gemv_multi": (I, [V, I, V, V, V, I64]),
         "spq4k_gemm": (I, [V, V, V, V, I64]),
+        "spq4k_gemm_multi": (I, [V, I, V, V, V, I64]),
         "spq4k_mul_mat": (I, [V, V, V, V, I64]),
         "spq4k_moe": (I, [V, V, V, I64, I64, I64, V, V]),
         "spq4k_mul_mat_host": (I, [V, V, V, V, I64]),
@@ -251,6 +252,12 @@ class Context:
 
     def gemm_dev(self, W: Weights, X_dev: int, Y_dev: int, T: int):
         self._check("spq4k_gemm", self.lib.spq4k_gemm(self.handle, W.handle, X_dev, Y_dev, T))
+
+    def gemm_multi_dev(self, Ws, X_dev: int, Y_devs, T: int):
+        n = len(Ws)
+        wa = (C.c_void_p * n)(*[w.handle.value if isinstance(w.handle, C.c_void_p) else w.handle for w in Ws])
+        ya = (C.c_void_p * n)(*Y_devs)
+        self._check("spq4k_gemm_multi", self.lib.spq4k_gemm_multi(self.handle, n, wa, X_dev, ya, T))
 
     def mul_mat_dev(self, W: Weights, X_dev: int, Y_dev: int, T: int):
         self._check("spq4k_mul_mat", self.lib.spq4k_mul_mat(self.handle, W.handle, X_dev, Y_dev, T))

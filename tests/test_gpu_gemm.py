@@ -51,3 +51,59 @@ def test_gemm_small_t_matches_gemv(ctx, oracle, T):
     ctx.gemm_dev(Wd, xd.ptr, yd.ptr, T)
     ctx.synchronize()
     _check(yd.to_host(), oracle.mul_mat(W, M, K, X), f"gemm T={T}")
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_gemm_both_kernels(oracle, mode):
+    """The skinny kernel (SPQ4K_GEMM_MODE=1: K split across the workgroup's
+    waves, operands from the Q8_K planes) and the tiled kernel (=2: 64 x 64
+    tiles staged in LDS) at token counts on both sides of their default
+    ranges, with ragged row and token tails."""
+    from _envctx import context_with
+    c = context_with({"SPQ4K_GEMM_MODE": mode})
+    try:
+        for M, K, T in ((70, 4096, 9), (130, 2048, 17), (64, 12288, 31), (50, 768, 47), (96, 4096, 65),
+                        (33, 5120, 130)):
+            rng = np.random.default_rng(M * 3 + T)
+            W = oracle.quantize_q4K((rng.standard_normal((M, K)) * 0.02).astype(np.float32))
+            X = rng.standard_normal((T, K)).astype(np.float32)
+            Wd = c.upload(W, M, K)
+            _check(c.mul_mat(Wd, X), oracle.mul_mat(W, M, K, X), f"mode={mode} M={M} K={K} T={T}")
+            Wd.free()
+    finally:
+        c.close()
+
+
+def test_gemm_repeatable(ctx, oracle):
+    """Fixed reduction order across the workgroup's waves: bit-identical reruns."""
+    rng = np.random.default_rng(4)
+    M, K, T = 200, 12288, 24
+    Wd = ctx.upload(oracle.quantize_q4K((rng.standard_normal((M, K)) * 0.02).astype(np.float32)), M, K)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    a = ctx.mul_mat(Wd, X)
+    for _ in range(3):
+        np.testing.assert_array_equal(ctx.mul_mat(Wd, X), a)
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+@pytest.mark.parametrize("K,shapes,T", [(4096, (256, 64, 64), 16), (2048, (300, 300), 40), (768, (17, 100, 5, 33), 100)])
+def test_gemm_multi(oracle, mode, K, shapes, T):
+    """q/k/v and gate/up of a prefill batch in one call: X quantised once,
+    every matrix within tolerance of the oracle (skinny kernel with segments,
+    or the tiled kernel once per matrix)."""
+    from spq4k.hip import DeviceArray
+    from _envctx import context_with
+    c = context_with({"SPQ4K_GEMM_MODE": mode})
+    try:
+        rng = np.random.default_rng(K + T)
+        Ws = [oracle.quantize_q4K((rng.standard_normal((M, K)) * 0.02).astype(np.float32)) for M in shapes]
+        X = rng.standard_normal((T, K)).astype(np.float32)
+        wd = [c.upload(w, M, K) for w, M in zip(Ws, shapes)]
+        xd = DeviceArray.from_host(X)
+        ys = [DeviceArray.from_host(np.full((T, M), np.nan, np.float32)) for M in shapes]
+        c.gemm_multi_dev(wd, xd.ptr, [y.ptr for y in ys], T)
+        c.synchronize()
+        for w, M, y in zip(Ws, shapes, ys):
+            _check(y.to_host(), oracle.mul_mat(w, M, K, X), f"multi mode={mode} K={K} M={M} T={T}")
+    finally:
+        c.close()
