@@ -29,10 +29,12 @@ struct spq4k_ctx {
     size_t scratch_cap = 0;
     int force_bpr = 0;           // tuning override (SPQ4K_GEMV_BPR = 1, 2, 4 or 8)
     int preq_mode = 0;           // SPQ4K_GEMV_PREQ: 0 auto, 1 always, 2 never
+    int gemv_mfma_min_t = 4;     // SPQ4K_GEMV_MFMA_MIN_T: batches of at least this many tokens use matrix cores
     int no_decode = 0;           // SPQ4K_GEMV_GENERIC=1: T = 1 also uses the generic kernel
     int moe_unfused = 0;         // SPQ4K_MOE_UNFUSED=1: routing pass + Q8_K planes + matvec (3 launches)
     int moe_mode = 0;            // SPQ4K_MOE_MODE=2: skip the small-batch decode mapping
     int gemm_mode = 0;           // SPQ4K_GEMM_MODE: 0 auto, 1 skinny kernel, 2 tiled kernel
+    int gemm_cfg = -1;           // SPQ4K_GEMM_CFG: tiled launch shape, -1 automatic
     DecodeCfg dec_force = {0, 0, false, 0};   // SPQ4K_DEC_{WAVES,DEPTH,XFIRST,GRID} overrides
     int dec_xfirst_set = 0;
     char err[256] = {0};
@@ -103,18 +105,20 @@ int check_shape(spq4k_ctx* c, int64_t M, int64_t K, int64_t E) {
 
 // Quantise T rows of x (row stride x_tstride) into Q8_K planes in the
 // context scratch; Q receives the plane pointers.
-int q8_planes(spq4k_ctx* c, const float* x, int64_t x_tstride, int T, int nb, Q8Planes* Q) {
+int q8_planes(spq4k_ctx* c, const float* x, int64_t x_tstride, int T, int nb, Q8Planes* Q, bool perm = false) {
     const size_t items = (size_t)T * nb;
-    int rc = ensure_scratch(c, items * 292);
+    int rc = ensure_scratch(c, items * (256 + Q8MN_BYTES + 32 + 4));
     if (rc) return rc;
     int8_t* qs = (int8_t*)c->scratch;
-    int16_t* bs = (int16_t*)(c->scratch + items * 256);
-    float* d = (float*)(c->scratch + items * 288);
-    hipError_t e = launch_quantize_q8k_planes(x, x_tstride, T, nb, qs, bs, d, c->stream);
+    uint8_t* mn = c->scratch + items * 256;
+    int16_t* bs = (int16_t*)(c->scratch + items * (256 + Q8MN_BYTES));
+    float* d = (float*)(c->scratch + items * (256 + Q8MN_BYTES + 32));
+    hipError_t e = launch_quantize_q8k_planes(x, x_tstride, T, nb, qs, bs, d, mn, perm, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "quantize_q8k_planes launch");
     Q->qs = qs;
     Q->bs = bs;
     Q->d = d;
+    Q->mn = mn;
     return 0;
 }
 
@@ -215,6 +219,32 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         if (e != hipSuccess) return hip_fail(c, e, "gemv decode launch");
         return 0;
     }
+    if (T >= c->gemv_mfma_min_t && c->force_bpr == 0) {
+        // 4 <= T <= 8: the sdot4 kernel's integer work grows with T while the
+        // matrix cores' 16-token tile costs the same from T = 1 to 16
+        GemmParams g;
+        memset(&g, 0, sizeof g);
+        g.T = (int32_t)T;
+        g.nb = p.nb;
+        g.mode = 1;
+        g.cfg = -1;
+        int rc = q8_planes(c, x, K, (int)T, p.nb, &g.Q);
+        if (rc) return rc;
+        int64_t t16 = 0;
+        for (int i = 0; i < n; ++i) {
+            g.seg[i].W = W[i]->data;
+            g.seg[i].Y = y[i];
+            g.seg[i].M = (int32_t)W[i]->M;
+            g.seg[i].tile_begin = (int32_t)t16;
+            t16 += (W[i]->M + 15) / 16;
+        }
+        for (int i = n; i < GEMM_MAX_SEG; ++i) g.seg[i].tile_begin = INT32_MAX;
+        g.nseg = n;
+        g.total_tiles = (int32_t)t16;
+        hipError_t e = launch_gemm_skinny(g, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemv (matrix cores) launch");
+        return 0;
+    }
     const int cb_max = LDS_BUDGET / ((int)T * 292);
     p.chunk_blocks = p.nb < cb_max ? p.nb : cb_max;
     // Quantise the activations once, up front, when re-quantising them in
@@ -264,6 +294,10 @@ int spq4k_init(int device, spq4k_ctx** out) {
     if (const char* f = getenv("SPQ4K_MOE_UNFUSED")) c->moe_unfused = atoi(f) == 1;
     if (const char* f = getenv("SPQ4K_MOE_MODE")) c->moe_mode = atoi(f);
     if (const char* f = getenv("SPQ4K_GEMM_MODE")) c->gemm_mode = atoi(f);
+    if (const char* f = getenv("SPQ4K_GEMM_CFG")) {
+        const int v = atoi(f);
+        if (v >= 0 && v < gemm_tiled_shapes()) c->gemm_cfg = v;
+    }
     if (const char* f = getenv("SPQ4K_DEC_WAVES")) {
         const int v = atoi(f);
         if (v == 8 || v == 12 || v == 16) c->dec_force.waves = v;
@@ -283,6 +317,10 @@ int spq4k_init(int device, spq4k_ctx** out) {
     if (const char* f = getenv("SPQ4K_GEMV_PREQ")) {
         const int v = atoi(f);
         if (v == 1 || v == 2) c->preq_mode = v;
+    }
+    if (const char* f = getenv("SPQ4K_GEMV_MFMA_MIN_T")) {
+        const int v = atoi(f);
+        if (v >= 2) c->gemv_mfma_min_t = v;
     }
     // scratch for Q8_K activation planes: sized for prefill batches up front
     // so that steady-state calls (and graph capture) never allocate
@@ -541,33 +579,32 @@ int spq4k_gemm_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const f
     p.T = (int32_t)T;
     p.nb = (int32_t)(K / SPQ4K_QK_K);
     p.mode = c->gemm_mode;
+    p.cfg = c->gemm_cfg;
+    int64_t tiles16 = 0;
+    for (int i = 0; i < n; ++i) {
+        p.seg[i].W = W[i]->data;
+        p.seg[i].Y = Y[i];
+        p.seg[i].M = (int32_t)W[i]->M;
+        p.seg[i].tile_begin = (int32_t)tiles16;
+        tiles16 += (W[i]->M + 15) / 16;
+    }
+    for (int i = n; i < GEMM_MAX_SEG; ++i) p.seg[i].tile_begin = INT32_MAX;
+    p.nseg = n;
+    if (tiles16 * ((T + 15) / 16) > (1ll << 31) - 1) return set_err(c, -EINVAL, "gemm: grid too large");
+    const bool skinny = gemm_use_skinny((int)T, c->gemm_mode);
+    if (!skinny) p.cfg = gemm_tiled_pick(p, c->num_cus);
     // the input is quantised once for all the matrices
-    rc = q8_planes(c, X, K, (int)T, p.nb, &p.Q);
+    rc = q8_planes(c, X, K, (int)T, p.nb, &p.Q, !skinny && gemm_tiled_perm(p.cfg));
     if (rc) return rc;
     hipError_t e;
-    if (gemm_use_skinny((int)T, c->gemm_mode)) {
-        int64_t tiles = 0;
-        for (int i = 0; i < n; ++i) {
-            p.seg[i].W = W[i]->data;
-            p.seg[i].Y = Y[i];
-            p.seg[i].M = (int32_t)W[i]->M;
-            p.seg[i].tile_begin = (int32_t)tiles;
-            tiles += (W[i]->M + 15) / 16;
-        }
-        if (tiles * ((T + 63) / 16) > (1ll << 31) - 1) return set_err(c, -EINVAL, "gemm: grid too large");
-        p.nseg = n;
-        p.total_tiles = (int32_t)tiles;
+    if (skinny) {
+        p.total_tiles = (int32_t)tiles16;
         e = launch_gemm_skinny(p, c->stream);
         if (e != hipSuccess) return hip_fail(c, e, "gemm skinny launch");
         return 0;
     }
-    for (int i = 0; i < n; ++i) {
-        p.W = W[i]->data;
-        p.Y = Y[i];
-        p.M = (int32_t)W[i]->M;
-        e = launch_gemm(p, c->stream);
-        if (e != hipSuccess) return hip_fail(c, e, "gemm launch");
-    }
+    e = launch_gemm(p, c->num_cus, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "gemm launch");
     return 0;
 }
 
@@ -655,23 +692,24 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
         return 0;
     }
     // scratch: Q8_K planes | routing tables
-    const size_t q8_bytes = ((size_t)rows * nb * 292 + 255) & ~(size_t)255;
+    const size_t items = (size_t)rows * nb;
+    const size_t q8_bytes = (items * (256 + Q8MN_BYTES + 32 + 4) + 255) & ~(size_t)255;
     const size_t route_bytes = (size_t)(1 + 3 * E + n_pairs) * sizeof(int32_t);
     rc = ensure_scratch(c, q8_bytes + route_bytes);
     if (rc) return rc;
     MoeParams p;
     memset(&p, 0, sizeof p);
-    const size_t items = (size_t)rows * nb;
     int8_t* qs = (int8_t*)c->scratch;
-    int16_t* bs = (int16_t*)(c->scratch + items * 256);
-    float* d = (float*)(c->scratch + items * 288);
+    uint8_t* mn = c->scratch + items * 256;
+    int16_t* bs = (int16_t*)(c->scratch + items * (256 + Q8MN_BYTES));
+    float* d = (float*)(c->scratch + items * (256 + Q8MN_BYTES + 32));
     int32_t* rt = (int32_t*)(c->scratch + q8_bytes);
     p.route.n_act = rt;
     p.route.act = rt + 1;
     p.route.act_off = rt + 1 + E;
     p.route.act_cnt = rt + 1 + 2 * E;
     p.route.pairs = rt + 1 + 3 * E;
-    hipError_t e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, c->stream);
+    hipError_t e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, mn, false, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "moe quantize launch");
     e = launch_moe_route(ids, (int)n_pairs, E, p.route, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "moe route launch");
@@ -681,6 +719,7 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     p.Q.qs = qs;
     p.Q.bs = bs;
     p.Q.d = d;
+    p.Q.mn = mn;
     p.M = M;
     p.nb = nb;
     p.n_used = (int)n_used;

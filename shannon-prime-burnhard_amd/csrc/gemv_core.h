@@ -101,7 +101,12 @@ struct Q8Planes {
     const int8_t* qs;    // [T][nb][256], 16-byte aligned
     const int16_t* bs;   // [T][nb][16]
     const float* d;      // [T][nb]
+    // [T][nb][48 bytes], 16-byte aligned: the min-term operand of the matrix-core
+    // kernels, BS_j = bs[2j] + bs[2j+1] split as 32 hi_j + lo_j (lo_j in 0..31):
+    // fp16 hi_0..hi_7, fp16 lo_0..lo_7, then d as fp32 at byte 32
+    const uint8_t* mn;
 };
+constexpr int Q8MN_BYTES = 48;
 
 // Two integer sub-block sums of one lane against one staged activation block.
 __device__ __forceinline__ void subblock_pair(const Nib& n, const int8_t* q8blk, int l4, int& S0, int& S1) {

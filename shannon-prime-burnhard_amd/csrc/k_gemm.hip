@@ -3,30 +3,24 @@
 // Computes GGML_OP_MUL_MAT for a T-token batch with the numerics of the
 // reference CPU path (ggml_compute_forward_mul_mat, ggml-cpu.c:1241-1439:
 // Q8_K activations, integer sub-block sums exact, fp32 combine):
-//   Y[t][r] = sum_b  d_rb d8_tb I_rbt  -  sum_b sum_j (dmin_rb m_rbj)(d8_tb BS_tbj)
+//   Y[t][r] = sum_b  d8_tb (d_rb I_rbt  -  dmin_rb M_rbt)
 //   I_rbt   = sum_j sc_rbj S_rbtj,    S_rbtj = sum_{k in sub-block j} q4_rk q8_tk
-//   BS_tbj  = bsums_tb[2j] + bsums_tb[2j+1]
+//   M_rbt   = sum_j m_rbj BS_tbj,     BS_tbj = bsums_tb[2j] + bsums_tb[2j+1]
 // The CUDA backend's equivalent is mul_mat_q<Q4_K> (ggml-cuda/mmq.cuh:3478),
-// which uses Q8_1 activations; this kernel keeps Q8_K.
+// which uses Q8_1 activations; these kernels keep Q8_K.
 //
-// Matrix-core mapping (wave64, v_mfma_i32_16x16x64_i8, lane l: row/col l%16,
-// k-quarter q = l/16 holding 16 consecutive k):
+// Matrix-core mapping (wave64, 16x16 output tiles; lane l has column l % 16
+// and k-slot group q = l / 16; the output lane holds rows 4q .. 4q+3):
 //   - a 6-bit scale sc = 8*sh + sl (sh, sl in 0..7) is folded into two int8
-//     A operands A_hi = sh*q4 and A_lo = sl*q4 (both <= 105), so the matrix
-//     cores accumulate H = sum A_hi q8 and L = sum A_lo q8 over a whole
-//     256-value super-block with no per-sub-block VALU work, and I = 8H + L
-//     exactly;
-//   - the min-term integer M = sum_j m_j BS_j of each super-block comes from
-//     v_mfma_f32_16x16x4f32 fed with the integers m_j (<= 63) and BS_j
-//     (|BS| <= 4064): every product and partial sum stays below 2^24, so M is
-//     exact;
-//   - per super-block acc += (d*d8) I - (dmin*d8) M in fp32, the reference's
-//     per-block combine.
-// Workgroup tile: 4 waves x 16 rows, NCT x 16 tokens; activations (Q8_K
-// planes written by quantize_q8k_planes_kernel) staged per super-block in LDS
-// (double-buffered: the next block's loads are issued before this block's
-// MFMAs and stored after them), weights streamed from HBM into registers one
-// super-block ahead.
+//     operands sh*q4 and sl*q4 (both <= 105), so v_mfma_i32_16x16x64_i8
+//     accumulates H = sum sh q4 q8 and L = sum sl q4 q8 over a whole 256-value
+//     super-block with no per-sub-block work, and I = 8H + L exactly;
+//   - the min-term integer M comes from one v_mfma_f32_16x16x16_f16 per tile:
+//     BS_j = 32 hi_j + lo_j (hi_j in -127..127, lo_j in 0..31) and the k slots
+//     hold (32 m_j, hi_j) for j = 0..7 and (m_j, lo_j) for j = 0..7; every
+//     operand, product (<= 2016 * 127) and partial sum (< 2^22) is an integer
+//     that fp16 / fp32 represent exactly, so M is exact;
+//   - per super-block acc += d8 (d I - dmin M) in fp32.
 #include "gemv_core.h"
 #include "launch.h"
 
@@ -35,194 +29,507 @@ namespace spq4k {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
-// per-lane weight registers for one super-block: header + 64 B of qs
+// per-lane weight registers for one super-block: header + 64 B of qs (skinny kernel)
 struct WG4 {
     uint4 hdr;
     uint4 q[4];   // step s: qs[32 s + 16 (q & 1) .. + 16]
 };
 
-template <int NCT>
-__global__ __launch_bounds__(256) void gemm_q4k_kernel(GemmParams p) {
-    constexpr int TOK = NCT * 16;          // tokens per workgroup
-    __shared__ __align__(16) int8_t s_q8[2][TOK * 256];
-    __shared__ float s_d8[2][TOK];
-    __shared__ float s_bm[2][TOK * 8];    // BS_j as exact floats
-    __shared__ float s_dr[2][64];         // d of the workgroup's rows
-    __shared__ float s_dmr[2][64];        // dmin of the workgroup's rows
+// Workgroup i runs on XCD i % 8. Logical tile L numbers the workgroups of one
+// XCD consecutively, so neighbouring tiles (the token tiles of one row tile,
+// which read the same weights) share that XCD's L2.
+__device__ __forceinline__ int xcd_tile(int bid, int G) {
+    const int x = bid & 7;
+    return x * (G >> 3) + min(x, G & 7) + (bid >> 3);
+}
+
+__device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
+    // two 16-bit products (v_pk_mul_lo_u16); each byte of `a` is < 16 and each
+    // 16-bit half of `b` is < 8, so no product carries across a byte
+    u16x2 x, y;
+    __builtin_memcpy(&x, &a, 4);
+    __builtin_memcpy(&y, &b, 4);
+    const u16x2 z = x * y;
+    uint32_t r;
+    __builtin_memcpy(&r, &z, 4);
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// Tiled form. A workgroup of four waves owns ROWS = WR*RT*16 rows of one of up
+// to four matrices sharing the input (row tiles of the segments are numbered
+// one after the other) and TOK = CT*16 tokens; wave (wr, wk) computes RT x CT
+// output tiles of 16x16 over super-blocks wk, wk + WK, ... and the WK partial
+// tiles are summed through LDS in wave order (deterministic).
+//
+// k order inside a super-block: k-slot group q of step s (s = 0..3) holds the
+// low and the high nibbles of bytes 8s .. 8s+7 of the 32-byte nibble group q,
+// i.e. k = 64q + 8s + e and 64q + 32 + 8s + e (e = 0..7): a lane loads its own
+// 32 bytes of qs once per super-block and its two sub-blocks (2q, 2q+1) keep
+// one scale pair for all four steps. The activations are staged in LDS in the
+// same order (a 16-byte read per fragment, rows padded to 272 bytes so that
+// the 16 tokens of a fragment read hit distinct banks), double-buffered: the
+// next iteration's loads are issued before this one's MFMAs and stored after.
+template <int RT, int CT, int WR, int WK>
+__global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
+    static_assert(WR * WK == 4, "four waves per workgroup");
+    constexpr int TOK = CT * 16;
+    constexpr int ROWS = WR * RT * 16;
+    constexpr int QS = 272;     // LDS bytes per token row of q8
+    constexpr int MS = 20;      // LDS halves per token of the min operand (16 used)
+    __shared__ __align__(16) int8_t s_q8[2][WK][TOK * QS];
+    __shared__ __align__(16) _Float16 s_mn[2][WK][TOK * MS];
+    __shared__ __align__(16) float s_d8[2][WK][TOK];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int c16 = lane & 15;             // A row / B column within a 16-tile
-    const int q = lane >> 4;               // k-quarter of a 64-k step; output row group
-    const int M = p.M, T = p.T, nb = p.nb;
-
-    // token tile fastest: the workgroups sharing a weight tile run together
+    const int wr = wave % WR, wk = wave / WR;
+    const int c16 = lane & 15;
+    const int q = lane >> 4;
+    const int T = p.T, nb = p.nb;
     const int ttiles = (T + TOK - 1) / TOK;
-    const int tt = blockIdx.x % ttiles;
-    const int rt = blockIdx.x / ttiles;
-    const int row_a = rt * 64 + wave * 16 + c16;            // this lane's A row
-    const int row_a_c = min(row_a, M - 1);
+    const int L = xcd_tile(blockIdx.x, gridDim.x);
+    const int tt = L % ttiles;
+    const int gt = L / ttiles;                      // row tile over all segments
+    int sidx = 0;
+#pragma unroll
+    for (int k = 1; k < GEMM_MAX_SEG; ++k)
+        if (k < p.nseg && gt >= p.seg[k].tile_begin) sidx = k;
+    const uint8_t* __restrict__ W = p.seg[sidx].W;
+    float* __restrict__ Y = p.seg[sidx].Y;
+    const int M = p.seg[sidx].M;
+    const int row0 = (gt - p.seg[sidx].tile_begin) * ROWS + wr * RT * 16;
     const int tok0 = tt * TOK;
 
-    const uint8_t* __restrict__ wrow = p.W + (size_t)row_a_c * nb * Q4K_BYTES;
-
-    auto load_wblock = [&](int b) {
-        WG4 w;
-        const uint8_t* blk = wrow + (size_t)b * Q4K_BYTES;
-        w.hdr = *reinterpret_cast<const uint4*>(blk);
+    const uint8_t* wrow[RT];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) w.q[s] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * s + 16 * (q & 1));
-        return w;
+    for (int r = 0; r < RT; ++r) wrow[r] = W + (size_t)min(row0 + r * 16 + c16, M - 1) * nb * Q4K_BYTES;
+
+    struct WQ {
+        v4i hdr, lo, hi;   // header; bytes 0..15 and 16..31 of the lane's 32-byte nibble group
+    };
+    auto load_w = [&](int b, WQ* w) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const uint8_t* blk = wrow[r] + (size_t)b * Q4K_BYTES;
+            w[r].hdr = *reinterpret_cast<const v4i*>(blk);
+            w[r].lo = *reinterpret_cast<const v4i*>(blk + 16 + 32 * q);
+            w[r].hi = *reinterpret_cast<const v4i*>(blk + 32 + 32 * q);
+        }
     };
 
-    // staging of super-block b's activations into LDS buffer `buf`, split in
-    // a load half (into registers) and a store half, so that the next
-    // block's loads are in flight during the current block's MFMAs
-    constexpr int QV = (TOK * 16 + 255) / 256;   // uint4 per thread
-    constexpr int BV = (TOK * 8 + 255) / 256;    // bsum pairs per thread
-    struct StageRegs {
-        v4i q[QV];   // native vectors: HIP's uint4 copies go through a stack slot
-        float bm[BV];
-        float d8[BV];
+    // staging of iteration `it` (super-blocks it*WK .. it*WK + WK-1)
+    constexpr int NQ = WK * TOK * 16;   // 16-byte chunks of q8
+    constexpr int NM = WK * TOK * 8;    // (token, sub-block) items of the min operand
+    constexpr int QV = (NQ + 255) / 256;
+    constexpr int MV = (NM + 255) / 256;
+    struct Stage {
+        v4i q[QV];
+        uint32_t bs[MV];
+        float d8[MV];
     };
-    auto stage_load = [&](int b, StageRegs& r) {
+    auto stage_load = [&](int it, Stage& s) {
 #pragma unroll
         for (int k = 0; k < QV; ++k) {
-            const int i = threadIdx.x + 256 * k;
-            const int t = min(i >> 4, TOK - 1), c = i & 15;
-            const int tg = min(tok0 + t, T - 1);
-            r.q[k] = reinterpret_cast<const v4i*>(p.Q.qs + ((int64_t)tg * nb + b) * 256)[c];
+            const int i = min((int)threadIdx.x + 256 * k, NQ - 1);
+            const int kb = i / (TOK * 16), t = (i >> 4) % TOK, c = i & 15;
+            const int b = min(it * WK + kb, nb - 1), tg = min(tok0 + t, T - 1);
+            s.q[k] = reinterpret_cast<const v4i*>(p.Q.qs + ((int64_t)tg * nb + b) * 256)[c];
         }
 #pragma unroll
-        for (int k = 0; k < BV; ++k) {
-            const int i = threadIdx.x + 256 * k;
-            const int t = min(i >> 3, TOK - 1), j = i & 7;
-            const int tg = min(tok0 + t, T - 1);
-            const int16_t* bs = p.Q.bs + ((int64_t)tg * nb + b) * 16;
-            r.bm[k] = (float)((int)bs[2 * j] + (int)bs[2 * j + 1]);
-            r.d8[k] = p.Q.d[(int64_t)tg * nb + b];
+        for (int k = 0; k < MV; ++k) {
+            const int i = min((int)threadIdx.x + 256 * k, NM - 1);
+            const int kb = i / (TOK * 8), t = (i >> 3) % TOK, j = i & 7;
+            const int b = min(it * WK + kb, nb - 1), tg = min(tok0 + t, T - 1);
+            const int64_t ib = (int64_t)tg * nb + b;
+            s.bs[k] = reinterpret_cast<const uint32_t*>(p.Q.bs + ib * 16)[j];
+            s.d8[k] = p.Q.d[ib];
         }
     };
-    auto stage_store = [&](const StageRegs& r, int buf) {
+    auto stage_store = [&](const Stage& s, int buf) {
 #pragma unroll
         for (int k = 0; k < QV; ++k) {
-            const int i = threadIdx.x + 256 * k;
-            if (i < TOK * 16) reinterpret_cast<v4i*>(s_q8[buf])[i] = r.q[k];
+            const int i = (int)threadIdx.x + 256 * k;
+            if (NQ % 256 == 0 || i < NQ) {
+                const int kb = i / (TOK * 16), t = (i >> 4) % TOK, c = i & 15;
+                // chunk c = k 16c .. 16c+15: group c/4, nibble half (c/2)&1, steps 2(c&1), 2(c&1)+1
+                int8_t* dst = s_q8[buf][kb] + t * QS + 64 * (c >> 2) + 32 * (c & 1) + 8 * ((c >> 1) & 1);
+                *reinterpret_cast<uint64_t*>(dst) = (uint64_t)(uint32_t)s.q[k].x | ((uint64_t)(uint32_t)s.q[k].y << 32);
+                *reinterpret_cast<uint64_t*>(dst + 16) =
+                    (uint64_t)(uint32_t)s.q[k].z | ((uint64_t)(uint32_t)s.q[k].w << 32);
+            }
         }
 #pragma unroll
-        for (int k = 0; k < BV; ++k) {
-            const int i = threadIdx.x + 256 * k;
-            if (i < TOK * 8) {
-                s_bm[buf][i] = r.bm[k];
-                if ((i & 7) == 0) s_d8[buf][i >> 3] = r.d8[k];
+        for (int k = 0; k < MV; ++k) {
+            const int i = (int)threadIdx.x + 256 * k;
+            if (NM % 256 == 0 || i < NM) {
+                const int kb = i / (TOK * 8), t = (i >> 3) % TOK, j = i & 7;
+                const int bsum = (int)(int16_t)(s.bs[k] & 0xFFFFu) + (int)(int16_t)(s.bs[k] >> 16);
+                _Float16* m = s_mn[buf][kb] + t * MS;
+                m[j] = (_Float16)(bsum >> 5);          // hi_j (floor division)
+                m[8 + j] = (_Float16)(bsum & 31);      // lo_j
+                if (j == 0) s_d8[buf][kb][t] = s.d8[k];
             }
         }
     };
-    auto stage = [&](int b, int buf) {
-        StageRegs r;
-        stage_load(b, r);
-        stage_store(r, buf);
-    };
 
-    v4f acc[NCT];
+    v4f acc[RT][CT];
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) acc[ct] = v4f{0, 0, 0, 0};
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[r][ct] = v4f{0, 0, 0, 0};
 
-    WG4 wcur = load_wblock(0);
-    stage(0, 0);
-    for (int b = 0; b < nb; ++b) {
-        const int buf = b & 1;
-        // row constants of this super-block (A-lane row)
-        const float d = half_bits_to_float(wcur.hdr.x & 0xFFFFu);
-        const float dmin = half_bits_to_float(wcur.hdr.x >> 16);
-        const ScaleMin sm = unpack_scale_min(wcur.hdr.y, wcur.hdr.z, wcur.hdr.w);
-        if (q == 0) {
-            s_dr[buf][wave * 16 + c16] = d;
-            s_dmr[buf][wave * 16 + c16] = dmin;
-        }
-        __syncthreads();   // stage(b) and s_dr visible; previous block's readers done
-        WG4 wnext;
-        StageRegs snext;
-        if (b + 1 < nb) {
-            wnext = load_wblock(b + 1);
-            stage_load(b + 1, snext);
-        }
+    const int n_it = (nb + WK - 1) / WK;
+    WQ wcur[RT];
+    load_w(min(wk, nb - 1), wcur);
+    {
+        Stage s0;
+        stage_load(0, s0);
+        stage_store(s0, 0);
+    }
+    for (int it = 0; it < n_it; ++it) {
+        const int buf = it & 1;
+        __syncthreads();   // staging of `it` visible; readers of buf ^ 1 (iteration it - 1) done
+        // next iteration's loads (clamped at the end: unconditional, so no wait
+        // is forced at a branch join)
+        WQ wnext[RT];
+        Stage snext;
+        const int itn = min(it + 1, n_it - 1);
+        load_w(min(itn * WK + wk, nb - 1), wnext);
+        stage_load(itn, snext);
 
-        v4i ch[NCT], cl[NCT];
+        if (it * WK + wk < nb) {   // wave-uniform
+            float d[RT], dmin[RT];
+            uint32_t SH0[RT], SL0[RT], SH1[RT], SL1[RT];
+            h4 bm[RT];
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) {
-            ch[ct] = v4i{0, 0, 0, 0};
-            cl[ct] = v4i{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            // sub-block of this lane's 16 k: j = 2s + (q >= 2)
-            const int j = 2 * s + (q >> 1);
-            const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi;
-            const uint32_t sc = (scw >> (8 * (j & 3))) & 0xFFu;
-            const u16x2 sh = {(uint16_t)(sc >> 3), (uint16_t)(sc >> 3)};
-            const u16x2 sl = {(uint16_t)(sc & 7u), (uint16_t)(sc & 7u)};
-            const uint32_t w4[4] = {wcur.q[s].x, wcur.q[s].y, wcur.q[s].z, wcur.q[s].w};
-            int ahs[4], als[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t nib = (q >= 2) ? ((w4[i] >> 4) & 0x0F0F0F0Fu) : (w4[i] & 0x0F0F0F0Fu);
-                // packed 16-bit multiply (v_pk_mul_lo_u16): each byte < 16 times
-                // a factor < 8 stays below 128, so no carry crosses a byte
-                u16x2 n2;
-                __builtin_memcpy(&n2, &nib, 4);
-                const u16x2 h2 = n2 * sh, l2 = n2 * sl;
-                __builtin_memcpy(&ahs[i], &h2, 4);
-                __builtin_memcpy(&als[i], &l2, 4);
+            for (int r = 0; r < RT; ++r) {
+                const uint32_t h0 = (uint32_t)wcur[r].hdr.x;
+                d[r] = half_bits_to_float(h0 & 0xFFFFu);
+                dmin[r] = half_bits_to_float(h0 >> 16);
+                const ScaleMin sm = unpack_scale_min((uint32_t)wcur[r].hdr.y, (uint32_t)wcur[r].hdr.z,
+                                                     (uint32_t)wcur[r].hdr.w);
+                // sub-blocks 2q (low nibbles) and 2q + 1 (high nibbles)
+                const uint32_t sc01 = (q < 2 ? sm.sc_lo : sm.sc_hi) >> (16 * (q & 1));
+                SH0[r] = ((sc01 >> 3) & 7u) * 0x10001u;
+                SL0[r] = (sc01 & 7u) * 0x10001u;
+                SH1[r] = ((sc01 >> 11) & 7u) * 0x10001u;
+                SL1[r] = ((sc01 >> 8) & 7u) * 0x10001u;
+                // min operand: (32 m_j) for slots 0..7, (m_j) for slots 8..15;
+                // 0x6400 | m is the fp16 1024 + m, rescaled exactly
+                const uint32_t mw = (q & 1) ? sm.m_hi : sm.m_lo;
+                const uint32_t x01 = __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u);
+                const uint32_t x23 = __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u);
+                h2 a01, a23;
+                __builtin_memcpy(&a01, &x01, 4);
+                __builtin_memcpy(&a23, &x23, 4);
+                const _Float16 f = q < 2 ? (_Float16)32.0f : (_Float16)1.0f;
+                const _Float16 o = q < 2 ? (_Float16)-32768.0f : (_Float16)-1024.0f;
+                const h2 fv = {f, f}, ov = {o, o};
+                const h2 b01 = a01 * fv + ov, b23 = a23 * fv + ov;
+                bm[r] = h4{b01.x, b01.y, b23.x, b23.y};
             }
-            const v4i ahi = {ahs[0], ahs[1], ahs[2], ahs[3]};
-            const v4i alo = {als[0], als[1], als[2], als[3]};
+
+            v4i ch[RT][CT], cl[RT][CT];
 #pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) {
-                const v4i bv = *reinterpret_cast<const v4i*>(s_q8[buf] + (ct * 16 + c16) * 256 + 64 * s + 16 * q);
-                ch[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, bv, ch[ct], 0, 0, 0);
-                cl[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, bv, cl[ct], 0, 0, 0);
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    ch[r][ct] = v4i{0, 0, 0, 0};
+                    cl[r][ct] = v4i{0, 0, 0, 0};
+                }
+            const int8_t* qb = s_q8[buf][wk] + c16 * QS + 64 * q;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                v4i a[CT];
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct)
+                    a[ct] = *reinterpret_cast<const v4i*>(qb + ct * 16 * QS + 16 * s);
+#pragma unroll
+                for (int r = 0; r < RT; ++r) {
+                    const uint32_t w0 = (uint32_t)(s < 2 ? wcur[r].lo[2 * s] : wcur[r].hi[2 * s - 4]);
+                    const uint32_t w1 = (uint32_t)(s < 2 ? wcur[r].lo[2 * s + 1] : wcur[r].hi[2 * s - 3]);
+                    const uint32_t l0 = w0 & 0x0F0F0F0Fu, l1 = w1 & 0x0F0F0F0Fu;
+                    const uint32_t u0 = (w0 >> 4) & 0x0F0F0F0Fu, u1 = (w1 >> 4) & 0x0F0F0F0Fu;
+                    const v4i bh = {(int)pk_mul_u16(l0, SH0[r]), (int)pk_mul_u16(l1, SH0[r]),
+                                    (int)pk_mul_u16(u0, SH1[r]), (int)pk_mul_u16(u1, SH1[r])};
+                    const v4i bl = {(int)pk_mul_u16(l0, SL0[r]), (int)pk_mul_u16(l1, SL0[r]),
+                                    (int)pk_mul_u16(u0, SL1[r]), (int)pk_mul_u16(u1, SL1[r])};
+#pragma unroll
+                    for (int ct = 0; ct < CT; ++ct) {
+                        ch[r][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[ct], bh, ch[r][ct], 0, 0, 0);
+                        cl[r][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[ct], bl, cl[r][ct], 0, 0, 0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                const h4 am = *reinterpret_cast<const h4*>(s_mn[buf][wk] + (ct * 16 + c16) * MS + 4 * q);
+                const v4f d8 = *reinterpret_cast<const v4f*>(&s_d8[buf][wk][ct * 16 + 4 * q]);
+#pragma unroll
+                for (int r = 0; r < RT; ++r) {
+                    const v4f cm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm[r], v4f{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int I = (ch[r][ct][i] << 3) + cl[r][ct][i];
+                        acc[r][ct][i] = fmaf(d8[i], fmaf(-dmin[r], cm[i], d[r] * (float)I), acc[r][ct][i]);
+                    }
+                }
             }
         }
-        // min-term integers: A_m[r][j] = m_j (k-quarter q holds j = q and j = 4 + q)
-        const float am0 = (float)((sm.m_lo >> (8 * q)) & 0xFFu);
-        const float am1 = (float)((sm.m_hi >> (8 * q)) & 0xFFu);
-        const float4 drow = *reinterpret_cast<const float4*>(&s_dr[buf][wave * 16 + 4 * q]);
-        const float4 dmrow = *reinterpret_cast<const float4*>(&s_dmr[buf][wave * 16 + 4 * q]);
-        const float dd[4] = {drow.x, drow.y, drow.z, drow.w};
-        const float dm[4] = {dmrow.x, dmrow.y, dmrow.z, dmrow.w};
+        // buffer buf ^ 1 was last read in iteration it - 1, before this iteration's barrier
+        stage_store(snext, buf ^ 1);
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) {
-            const int tl = ct * 16 + c16;
-            v4f cm = {0, 0, 0, 0};
-            cm = __builtin_amdgcn_mfma_f32_16x16x4f32(am0, s_bm[buf][tl * 8 + q], cm, 0, 0, 0);
-            cm = __builtin_amdgcn_mfma_f32_16x16x4f32(am1, s_bm[buf][tl * 8 + 4 + q], cm, 0, 0, 0);
-            const float d8 = s_d8[buf][tl];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int I = (ch[ct][i] << 3) + cl[ct][i];
-                acc[ct][i] = fmaf(dd[i] * d8, (float)I, acc[ct][i]);
-                acc[ct][i] = fmaf(-(dm[i] * d8), cm[i], acc[ct][i]);
-            }
-        }
-        if (b + 1 < nb) {
-            // buffer buf ^ 1 was last read in block b - 1, before this block's barrier
-            stage_store(snext, buf ^ 1);
-            wcur = wnext;
-        }
+        for (int r = 0; r < RT; ++r) wcur[r] = wnext[r];
     }
 
-    // output: lane holds rows 4q..4q+3 of its wave tile for token c16 of each column tile
-    const int row_o = rt * 64 + wave * 16 + 4 * q;
+    // output: lane holds tokens 4q .. 4q+3 of each token tile, row c16 of each row tile
+    if constexpr (WK > 1) {
+        __syncthreads();   // every wave is done with the staging buffers
+        v4f* red = reinterpret_cast<v4f*>(&s_q8[0][0][0]);   // [WK-1][WR][RT*CT][64]
+        static_assert((WK - 1) * WR * RT * CT * 64 * 16 <= (int)sizeof(s_q8), "reduction fits the staging LDS");
+        if (wk > 0) {
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
-        const int t = tok0 + ct * 16 + c16;
-        if (t >= T) continue;
-        float* y = p.Y + (int64_t)t * M;
+            for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (row_o + i < M) y[row_o + i] = acc[ct][i];
+                for (int ct = 0; ct < CT; ++ct)
+                    red[(((wk - 1) * WR + wr) * RT * CT + r * CT + ct) * 64 + lane] = acc[r][ct];
+        }
+        __syncthreads();
+        if (wk > 0) return;
+#pragma unroll
+        for (int w = 1; w < WK; ++w)
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) acc[r][ct] += red[(((w - 1) * WR + wr) * RT * CT + r * CT + ct) * 64 + lane];
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int row = row0 + r * 16 + c16;
+        if (row >= M) continue;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = tok0 + ct * 16 + 4 * q + i;
+                if (t < T) Y[(int64_t)t * M + row] = acc[r][ct][i];
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Ring form (large T). Every operand of a super-block reaches LDS through
+// direct global -> LDS loads (global_load_lds_dwordx4), S super-blocks ahead,
+// so a wave's registers hold only accumulators and the operands of one step.
+// A workgroup of NW waves owns ROWS = 16*RT*NW rows of one of up to four
+// matrices sharing the input and TOK = 16*CT tokens; wave w computes rows
+// 16*RT*w .. +16*RT of the tile against all TOK tokens (C = weights x
+// activations: output lane rows 4q .. 4q+3, token c16).
+//
+// A stage holds, as 16-byte slots (64 slots = one wave-wide load):
+//   ROWS x 9 slots   the super-block of each row (144 bytes, row-major);
+//   TOK x 17 slots   the Q8_K values of each token (the permuted order of
+//                    quantize_q8k_planes: one 16-byte read per fragment), one
+//                    spare slot a row so that the 16 tokens of a fragment read
+//                    hit distinct banks;
+//   TOK x 3 slots    the min-term operand and d of each token (Q8Planes::mn);
+// all three counts are whole numbers of loads for CT a multiple of 4, and the
+// NPW loads a wave issues per stage cover them (the surplus loads re-read a
+// valid address into the stage's spare tail). A wave waits for its own loads
+// of a stage with s_waitcnt vmcnt (loads complete in order) before the
+// barrier that publishes the stage to the other waves.
+template <int RT, int CT, int NW, int S>
+__global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
+    static_assert(CT % 4 == 0, "token tile of 64 or 128");
+    constexpr int TOK = CT * 16;
+    constexpr int ROWS = RT * 16 * NW;
+    constexpr int QS = 272;                       // LDS bytes per token of q8
+    constexpr int W_SLOTS = ROWS * 9, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
+    constexpr int NLOAD = (W_SLOTS + Q_SLOTS + M_SLOTS) / 64;
+    constexpr int NPW = (NLOAD + NW - 1) / NW;    // loads per wave per stage
+    constexpr int STAGE = NPW * NW * 1024;
+    constexpr int Q_OFF = W_SLOTS * 16, M_OFF = Q_OFF + Q_SLOTS * 16;
+    static_assert(W_SLOTS % 64 == 0 && Q_SLOTS % 64 == 0 && M_SLOTS % 64 == 0, "whole loads per operand");
+    __shared__ __align__(1024) uint8_t lds[S][STAGE];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c16 = lane & 15;
+    const int q = lane >> 4;
+    const int T = p.T, nb = p.nb;
+    const int ttiles = (T + TOK - 1) / TOK;
+    const int L = xcd_tile(blockIdx.x, gridDim.x);
+    const int tt = L % ttiles;
+    const int gt = L / ttiles;
+    int sidx = 0;
+#pragma unroll
+    for (int k = 1; k < GEMM_MAX_SEG; ++k)
+        if (k < p.nseg && gt >= p.seg[k].tile_begin) sidx = k;
+    const uint8_t* __restrict__ W = p.seg[sidx].W;
+    float* __restrict__ Y = p.seg[sidx].Y;
+    const int M = p.seg[sidx].M;
+    const int row0 = (gt - p.seg[sidx].tile_begin) * ROWS;
+    const int tok0 = tt * TOK;
+
+    // per load: source of super-block 0 and the byte stride between super-blocks
+    const uint8_t* src[NPW];
+    uint32_t stride[NPW];
+#pragma unroll
+    for (int i = 0; i < NPW; ++i) {
+        const int J = NW * i + wave;              // load index within the stage
+        const int slot = J * 64 + lane;
+        if (J * 64 < W_SLOTS) {
+            const int r = min(row0 + slot / 9, M - 1);
+            src[i] = W + (size_t)r * nb * Q4K_BYTES + 16 * (slot % 9);
+            stride[i] = Q4K_BYTES;
+        } else if (J * 64 < W_SLOTS + Q_SLOTS) {
+            const int sl = slot - W_SLOTS;
+            const int tg = min(tok0 + sl / 17, T - 1);
+            src[i] = reinterpret_cast<const uint8_t*>(p.Q.qs) + (size_t)tg * nb * 256 + 16 * min(sl % 17, 15);
+            stride[i] = 256;
+        } else if (J * 64 < W_SLOTS + Q_SLOTS + M_SLOTS) {
+            const int sl = slot - W_SLOTS - Q_SLOTS;
+            const int tg = min(tok0 + sl / 3, T - 1);
+            src[i] = p.Q.mn + (size_t)tg * nb * Q8MN_BYTES + 16 * (sl % 3);
+            stride[i] = Q8MN_BYTES;
+        } else {
+            src[i] = p.Q.mn;                       // surplus load: any valid address
+            stride[i] = 0;
+        }
+    }
+    auto issue = [&](int b, int buf) {
+#pragma unroll
+        for (int i = 0; i < NPW; ++i)
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(src[i] + (size_t)b * stride[i]),
+                (__attribute__((address_space(3))) void*)(lds[buf] + (NW * i + wave) * 1024), 16, 0, 0);
+    };
+
+    v4f acc[RT][CT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[r][ct] = v4f{0, 0, 0, 0};
+
+#pragma unroll
+    for (int k = 0; k < S - 1; ++k) issue(min(k, nb - 1), k);
+    for (int b = 0; b < nb; ++b) {
+        const int buf = b % S;
+        // this wave's loads of stage b are done (the S - 2 later stages may
+        // still be in flight); the barrier publishes everyone's and retires
+        // the readers of the buffer refilled next
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * NPW) : "memory");
+        issue(min(b + S - 1, nb - 1), (b + S - 1) % S);
+
+        const uint8_t* st = lds[buf];
+        const uint8_t* wt = st + (wave * RT * 16) * Q4K_BYTES;
+        v4i ch[RT][CT], cl[RT][CT];
+        uint32_t SH0[RT], SL0[RT], SH1[RT], SL1[RT];
+        v4i wq[RT][2];
+        h4 am[RT];
+        float dr[RT][4], dmr[RT][4];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const uint8_t* wr = wt + (r * 16 + c16) * Q4K_BYTES;
+            const v4i hdr = *reinterpret_cast<const v4i*>(wr);
+            wq[r][0] = *reinterpret_cast<const v4i*>(wr + 16 + 32 * q);
+            wq[r][1] = *reinterpret_cast<const v4i*>(wr + 32 + 32 * q);
+            // d, dmin of output rows 4q .. 4q+3 of this row tile
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t h = *reinterpret_cast<const uint32_t*>(wt + (r * 16 + 4 * q + i) * Q4K_BYTES);
+                dr[r][i] = half_bits_to_float(h & 0xFFFFu);
+                dmr[r][i] = half_bits_to_float(h >> 16);
+            }
+            const ScaleMin sm = unpack_scale_min((uint32_t)hdr.y, (uint32_t)hdr.z, (uint32_t)hdr.w);
+            // this lane's sub-blocks 2q (low nibbles) and 2q + 1 (high nibbles)
+            const uint32_t sc01 = (q < 2 ? sm.sc_lo : sm.sc_hi) >> (16 * (q & 1));
+            SH0[r] = ((sc01 >> 3) & 7u) * 0x10001u;
+            SL0[r] = (sc01 & 7u) * 0x10001u;
+            SH1[r] = ((sc01 >> 11) & 7u) * 0x10001u;
+            SL1[r] = ((sc01 >> 8) & 7u) * 0x10001u;
+            // min operand of row c16: 32 m_j in k slots 0..7, m_j in slots
+            // 8..15 (0x6400 | m is the fp16 1024 + m, rescaled exactly)
+            const uint32_t mw = (q & 1) ? sm.m_hi : sm.m_lo;
+            const uint32_t x01 = __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u);
+            const uint32_t x23 = __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u);
+            h2 a01, a23;
+            __builtin_memcpy(&a01, &x01, 4);
+            __builtin_memcpy(&a23, &x23, 4);
+            const _Float16 f = q < 2 ? (_Float16)32.0f : (_Float16)1.0f;
+            const _Float16 o = q < 2 ? (_Float16)-32768.0f : (_Float16)-1024.0f;
+            const h2 fv = {f, f}, ov = {o, o};
+            const h2 b01 = a01 * fv + ov, b23 = a23 * fv + ov;
+            am[r] = h4{b01.x, b01.y, b23.x, b23.y};
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                ch[r][ct] = v4i{0, 0, 0, 0};
+                cl[r][ct] = v4i{0, 0, 0, 0};
+            }
+        }
+        // activation fragment of token c16, step s: values 64q + 8s .. +7 and
+        // 64q + 32 + 8s .. +7, stored contiguously by the permuted Q8_K planes
+        const uint8_t* qb = st + Q_OFF + c16 * QS + 64 * q;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            v4i bq[CT];
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) bq[ct] = *reinterpret_cast<const v4i*>(qb + ct * 16 * QS + 16 * s);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const uint32_t w0 = (uint32_t)wq[r][s >> 1][2 * (s & 1)];
+                const uint32_t w1 = (uint32_t)wq[r][s >> 1][2 * (s & 1) + 1];
+                const uint32_t l0 = w0 & 0x0F0F0F0Fu, l1 = w1 & 0x0F0F0F0Fu;
+                const uint32_t u0 = (w0 >> 4) & 0x0F0F0F0Fu, u1 = (w1 >> 4) & 0x0F0F0F0Fu;
+                const v4i ah = {(int)pk_mul_u16(l0, SH0[r]), (int)pk_mul_u16(l1, SH0[r]),
+                                (int)pk_mul_u16(u0, SH1[r]), (int)pk_mul_u16(u1, SH1[r])};
+                const v4i al = {(int)pk_mul_u16(l0, SL0[r]), (int)pk_mul_u16(l1, SL0[r]),
+                                (int)pk_mul_u16(u0, SL1[r]), (int)pk_mul_u16(u1, SL1[r])};
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    ch[r][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq[ct], ch[r][ct], 0, 0, 0);
+                    cl[r][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq[ct], cl[r][ct], 0, 0, 0);
+                }
+            }
+        }
+        const uint8_t* mb = st + M_OFF + c16 * Q8MN_BYTES;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            const h4 bm = *reinterpret_cast<const h4*>(mb + ct * 16 * Q8MN_BYTES + 8 * q);
+            const float d8 = *reinterpret_cast<const float*>(mb + ct * 16 * Q8MN_BYTES + 32);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const v4f cm = __builtin_amdgcn_mfma_f32_16x16x16f16(am[r], bm, v4f{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int I = (ch[r][ct][i] << 3) + cl[r][ct][i];
+                    acc[r][ct][i] = fmaf(d8, fmaf(-dmr[r][i], cm[i], dr[r][i] * (float)I), acc[r][ct][i]);
+                }
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the clamped loads past the last stage
+
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int rq = row0 + wave * RT * 16 + r * 16 + 4 * q;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            const int t = tok0 + ct * 16 + c16;
+            if (t >= T) continue;
+            float* y = Y + (int64_t)t * M + rq;
+            if ((M & 3) == 0 && rq + 3 < M) {
+                *reinterpret_cast<v4f*>(y) = acc[r][ct];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (rq + i < M) y[i] = acc[r][ct][i];
+            }
+        }
     }
 }
 
@@ -407,20 +714,65 @@ hipError_t launch_gemm_skinny(const GemmParams& p, hipStream_t st) {
     return longk ? launch_skinny<4, 16, 1>(p, st) : launch_skinny<4, 8, 1>(p, st);
 }
 
-template <int NCT>
-static hipError_t launch_gemm_n(const GemmParams& p, hipStream_t st) {
-    constexpr int TOK = NCT * 16;
-    const int64_t grid = (int64_t)((p.M + 63) / 64) * ((p.T + TOK - 1) / TOK);
-    hipLaunchKernelGGL((gemm_q4k_kernel<NCT>), dim3((unsigned)grid), dim3(256), 0, st, p);
-    return hipGetLastError();
-}
-
 bool gemm_use_skinny(int T, int mode) { return mode == 1 || (mode != 2 && T <= 64); }
 
-hipError_t launch_gemm(const GemmParams& p, hipStream_t st) {
-    if (p.T <= 16) return launch_gemm_n<1>(p, st);
-    if (p.T <= 32) return launch_gemm_n<2>(p, st);
-    return launch_gemm_n<4>(p, st);
+// Tiled-kernel launch shapes, indexed by GemmParams::cfg (-1: chosen here).
+struct TiledShape {
+    int rows, tok;   // workgroup tile
+    bool perm;       // reads the permuted Q8_K values
+    hipError_t (*launch)(const GemmParams&, int grid, hipStream_t);
+};
+template <int RT, int CT, int WR, int WK>
+static hipError_t launch_tiled_(const GemmParams& p, int grid, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_tiled_kernel<RT, CT, WR, WK>), dim3((unsigned)grid), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+template <int RT, int CT, int NW, int S>
+static hipError_t launch_ring_(const GemmParams& p, int grid, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_ring_kernel<RT, CT, NW, S>), dim3((unsigned)grid), dim3(NW * 64), 0, st, p);
+    return hipGetLastError();
+}
+static const TiledShape kTiled[] = {
+    {256, 64, true, launch_ring_<2, 4, 8, 2>},      // 0: ring, 8 waves, 2 stages
+    {128, 64, true, launch_ring_<1, 4, 8, 3>},      // 1: ring, 8 waves, 3 stages
+    {128, 64, true, launch_ring_<2, 4, 4, 3>},      // 2: ring, 4 waves, 3 stages
+    {64, 32, false, launch_tiled_<2, 2, 2, 2>},     // 3: K split in two
+    {32, 16, false, launch_tiled_<2, 1, 1, 4>},     // 4: K split in four
+    {128, 64, false, launch_tiled_<2, 4, 4, 1>},    // 5: register-staged
+};
+constexpr int N_TILED = (int)(sizeof(kTiled) / sizeof(kTiled[0]));
+
+int gemm_tiled_shapes() { return N_TILED; }
+bool gemm_tiled_perm(int cfg) { return cfg >= 0 && cfg < N_TILED && kTiled[cfg].perm; }
+
+static int64_t tiled_grid(const GemmParams& p, const TiledShape& s) {
+    int64_t tiles = 0;
+    for (int i = 0; i < p.nseg; ++i) tiles += (p.seg[i].M + s.rows - 1) / s.rows;
+    return tiles * ((p.T + s.tok - 1) / s.tok);
+}
+
+int gemm_tiled_pick(const GemmParams& p, int num_cus) {
+    if (p.cfg >= 0 && p.cfg < N_TILED) return p.cfg;
+    // the largest tile that still gives every CU a workgroup (measured on
+    // MI355X at T = 512: 256 x 64 for 24576 rows, 128 x 64 for 4096 and 6144)
+    for (int c : {0, 1, 3})
+        if (tiled_grid(p, kTiled[c]) >= num_cus) return c;
+    return 4;
+}
+
+hipError_t launch_gemm(const GemmParams& p0, int num_cus, hipStream_t st) {
+    const int cfg = gemm_tiled_pick(p0, num_cus);
+    const TiledShape& s = kTiled[cfg];
+    GemmParams p = p0;
+    int64_t tiles = 0;
+    for (int i = 0; i < p.nseg; ++i) {
+        p.seg[i].tile_begin = (int32_t)tiles;
+        tiles += (p.seg[i].M + s.rows - 1) / s.rows;
+    }
+    for (int i = p.nseg; i < GEMM_MAX_SEG; ++i) p.seg[i].tile_begin = INT32_MAX;
+    const int64_t grid = tiled_grid(p, s);
+    if (grid > INT32_MAX) return hipErrorInvalidValue;
+    return s.launch(p, (int)grid, st);
 }
 
 }  // namespace spq4k

@@ -98,27 +98,32 @@ struct GemmSeg {
     const uint8_t* W;     // [M][nb] Q4_K
     float* Y;             // [T][M]
     int32_t M;
-    int32_t tile_begin;   // first 16-row tile of this segment (skinny kernel)
+    int32_t tile_begin;   // first row tile of this segment (set by the launcher)
 };
 struct GemmParams {
-    const uint8_t* W;   // [M][nb] Q4_K (tiled kernel: one matrix per launch)
     Q8Planes Q;         // Q8_K of the T input rows
-    float* Y;           // [T][M]
-    int32_t M, T, nb;
+    int32_t T, nb;
     int32_t mode;       // 0 auto, 1 skinny kernel at any T, 2 tiled kernel at any T
-    GemmSeg seg[GEMM_MAX_SEG];   // skinny kernel: up to four matrices sharing the input
+    int32_t cfg;        // tiled launch shape (0 .. gemm_tiled_shapes() - 1), -1 automatic
+    GemmSeg seg[GEMM_MAX_SEG];   // up to four matrices sharing the input
     int32_t nseg;
     int32_t total_tiles;
 };
 bool gemm_use_skinny(int T, int mode);
-hipError_t launch_gemm(const GemmParams& p, hipStream_t st);          // tiled, one matrix
-hipError_t launch_gemm_skinny(const GemmParams& p, hipStream_t st);   // skinny, all segments
+int gemm_tiled_shapes();
+// tiled launch shape for these params (p.cfg if set) and whether it reads the
+// permuted Q8_K values (quantize_q8k_planes with perm)
+int gemm_tiled_pick(const GemmParams& p, int num_cus);
+bool gemm_tiled_perm(int cfg);
+hipError_t launch_gemm(const GemmParams& p, int num_cus, hipStream_t st);   // tiled, all segments
+hipError_t launch_gemm_skinny(const GemmParams& p, hipStream_t st);          // skinny, all segments
 
 // element-wise conversions (k_convert.hip)
 hipError_t launch_quantize_q8k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
-// fp32 rows x[t * x_tstride + k] -> Q8_K planes (T rows of nb blocks)
+// fp32 rows x[t * x_tstride + k] -> Q8_K planes (T rows of nb blocks); perm
+// stores qs in the order of the ring GEMM kernel
 hipError_t launch_quantize_q8k_planes(const float* x, int64_t x_tstride, int T, int nb, int8_t* qs, int16_t* bs,
-                                      float* d, hipStream_t st);
+                                      float* d, uint8_t* mn, bool perm, hipStream_t st);
 hipError_t launch_dequant_q4k(const uint8_t* x, float* y, int64_t nblocks, hipStream_t st);
 hipError_t launch_quantize_q4k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
 hipError_t launch_synth(float* out, int64_t n, uint64_t seed, int dist, int64_t cols, float mean, float std,

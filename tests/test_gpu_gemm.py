@@ -56,8 +56,8 @@ def test_gemm_small_t_matches_gemv(ctx, oracle, T):
 @pytest.mark.parametrize("mode", [1, 2])
 def test_gemm_both_kernels(oracle, mode):
     """The skinny kernel (SPQ4K_GEMM_MODE=1: K split across the workgroup's
-    waves, operands from the Q8_K planes) and the tiled kernel (=2: 64 x 64
-    tiles staged in LDS) at token counts on both sides of their default
+    waves, operands from the Q8_K planes) and the tiled kernel (=2: activations
+    staged in LDS, shape chosen by size) at token counts on both sides of their default
     ranges, with ragged row and token tails."""
     from _envctx import context_with
     c = context_with({"SPQ4K_GEMM_MODE": mode})
@@ -89,8 +89,8 @@ def test_gemm_repeatable(ctx, oracle):
 @pytest.mark.parametrize("K,shapes,T", [(4096, (256, 64, 64), 16), (2048, (300, 300), 40), (768, (17, 100, 5, 33), 100)])
 def test_gemm_multi(oracle, mode, K, shapes, T):
     """q/k/v and gate/up of a prefill batch in one call: X quantised once,
-    every matrix within tolerance of the oracle (skinny kernel with segments,
-    or the tiled kernel once per matrix)."""
+    every matrix within tolerance of the oracle (both kernels take the
+    matrices as segments of one launch)."""
     from spq4k.hip import DeviceArray
     from _envctx import context_with
     c = context_with({"SPQ4K_GEMM_MODE": mode})
@@ -105,5 +105,57 @@ def test_gemm_multi(oracle, mode, K, shapes, T):
         c.synchronize()
         for w, M, y in zip(Ws, shapes, ys):
             _check(y.to_host(), oracle.mul_mat(w, M, K, X), f"multi mode={mode} K={K} M={M} T={T}")
+    finally:
+        c.close()
+
+
+def _extreme_weights(oracle, rng, M, K):
+    """Random Q4_K rows with every fourth super-block replaced by the largest
+    one (d = dmin = 2^-6, all scales and mins 63, all nibbles 15)."""
+    W = oracle.quantize_q4K((rng.standard_normal((M, K)) * 0.02).astype(np.float32)).reshape(M, K // 256, 144)
+    ext = np.full(144, 0xFF, np.uint8)
+    ext[0:2] = ext[2:4] = np.frombuffer(np.float16(2.0 ** -6).tobytes(), np.uint8)
+    W[:, ::4] = ext
+    return W.reshape(-1)
+
+
+def _one_sign_tokens(rng, T, K):
+    X = np.abs(rng.standard_normal((T, K))).astype(np.float32) * np.where(np.arange(T) % 2, -1, 1)[:, None]
+    X[0] = 1.0
+    X[-1] = -1.0
+    X[T // 2, : K // 2] = 3.0 * np.sign(X[T // 2, -1])
+    return X.astype(np.float32)
+
+
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5])
+def test_gemm_tiled_shapes(oracle, cfg):
+    """Every launch shape of the tiled kernel (SPQ4K_GEMM_CFG) with ragged row,
+    token and super-block tails (K = 768 leaves a K-split wave idle), the
+    largest Q4_K blocks against constant +-1 activations (|BS_j| = 4064, the
+    edge of the exact fp16 min-term split), and four matrices in one launch.
+    Each token has one sign: the largest blocks dequantise to 13.78 everywhere,
+    and against mixed-sign tokens their sums would cancel to far below the fp32
+    rounding of the terms, which no summation order can meet at 1e-4."""
+    from spq4k.hip import DeviceArray
+    from _envctx import context_with
+    c = context_with({"SPQ4K_GEMM_MODE": 2, "SPQ4K_GEMM_CFG": cfg})
+    try:
+        rng = np.random.default_rng(500 + cfg)
+        for M, K, T in ((150, 4096, 70), (33, 768, 17), (200, 5120, 100), (64, 12288, 65)):
+            W = _extreme_weights(oracle, rng, M, K)
+            X = _one_sign_tokens(rng, T, K)
+            Wd = c.upload(W, M, K)
+            _check(c.mul_mat(Wd, X), oracle.mul_mat(W, M, K, X), f"cfg={cfg} M={M} K={K} T={T}")
+            Wd.free()
+        K, T, shapes = 2048, 50, (300, 17, 129, 64)
+        Ws = [_extreme_weights(oracle, rng, M, K) for M in shapes]
+        X = _one_sign_tokens(rng, T, K)
+        wd = [c.upload(w, M, K) for w, M in zip(Ws, shapes)]
+        xd = DeviceArray.from_host(X)
+        ys = [DeviceArray.from_host(np.full((T, M), np.nan, np.float32)) for M in shapes]
+        c.gemm_multi_dev(wd, xd.ptr, [y.ptr for y in ys], T)
+        c.synchronize()
+        for w, M, y in zip(Ws, shapes, ys):
+            _check(y.to_host(), oracle.mul_mat(w, M, K, X), f"cfg={cfg} multi M={M}")
     finally:
         c.close()

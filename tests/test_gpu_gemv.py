@@ -55,26 +55,44 @@ def test_gemv_t1(ctx, oracle, M, K):
     _check(got, exp, f"gemv M={M} K={K}")
 
 
+@pytest.mark.parametrize("sdot4", [False, True])
 @pytest.mark.parametrize("T", [2, 3, 4, 5, 8])
-def test_gemv_batched(ctx, oracle, T):
-    rng = np.random.default_rng(100 + T)
-    M, K = 768, 2048
-    W = _weights(oracle, rng, M, K)
-    x = rng.standard_normal((T, K)).astype(np.float32)
-    Wd = ctx.upload(W, M, K)
-    got = ctx.mul_mat(Wd, x)
-    exp = oracle.mul_mat(W, M, K, x)
-    _check(got, exp, f"gemv T={T}")
+def test_gemv_batched(ctx, oracle, T, sdot4):
+    """T <= 8 through spq4k_gemv: the sdot4 kernel below 4 tokens and the
+    matrix-core kernel from 4 (sdot4=True keeps the sdot4 kernel for every T,
+    SPQ4K_GEMV_MFMA_MIN_T=9)."""
+    from _envctx import context_with
+    c = context_with({"SPQ4K_GEMV_MFMA_MIN_T": 9}) if sdot4 else ctx
+    try:
+        rng = np.random.default_rng(100 + T)
+        for M, K in ((768, 2048), (100, 5120)):
+            W = _weights(oracle, rng, M, K)
+            x = rng.standard_normal((T, K)).astype(np.float32)
+            Wd = c.upload(W, M, K)
+            _check(c.mul_mat(Wd, x), oracle.mul_mat(W, M, K, x), f"gemv T={T} M={M} K={K} sdot4={sdot4}")
+            Wd.free()
+    finally:
+        if sdot4:
+            c.close()
 
 
-def test_gemv_large_k_batched(ctx, oracle):
-    # K = 27648 with T = 8 needs several LDS chunks per K split
-    rng = np.random.default_rng(7)
-    M, K, T = 128, 27648, 8
-    W = _weights(oracle, rng, M, K)
-    x = rng.standard_normal((T, K)).astype(np.float32)
-    Wd = ctx.upload(W, M, K)
-    _check(ctx.mul_mat(Wd, x), oracle.mul_mat(W, M, K, x), "gemv K=27648 T=8")
+@pytest.mark.parametrize("sdot4", [False, True])
+def test_gemv_large_k_batched(ctx, oracle, sdot4):
+    # K = 27648 with T = 8: several LDS chunks per K split (sdot4 kernel) or
+    # sixteen waves splitting K (matrix cores)
+    from _envctx import context_with
+    c = context_with({"SPQ4K_GEMV_MFMA_MIN_T": 9}) if sdot4 else ctx
+    try:
+        rng = np.random.default_rng(7)
+        M, K, T = 128, 27648, 8
+        W = _weights(oracle, rng, M, K)
+        x = rng.standard_normal((T, K)).astype(np.float32)
+        Wd = c.upload(W, M, K)
+        _check(c.mul_mat(Wd, x), oracle.mul_mat(W, M, K, x), f"gemv K=27648 T=8 sdot4={sdot4}")
+        Wd.free()
+    finally:
+        if sdot4:
+            c.close()
 
 
 def test_gemv_multi_matches_single(ctx, oracle):
