@@ -105,9 +105,15 @@ int check_shape(spq4k_ctx* c, int64_t M, int64_t K, int64_t E) {
 
 // Quantise T rows of x (row stride x_tstride) into Q8_K planes in the
 // context scratch; Q receives the plane pointers.
-int q8_planes(spq4k_ctx* c, const float* x, int64_t x_tstride, int T, int nb, Q8Planes* Q, bool perm = false) {
+size_t q8_planes_bytes(int T, int nb) {
+    return (((size_t)T * nb * (256 + Q8MN_BYTES + 32 + 4)) + 255) & ~(size_t)255;
+}
+
+// extra: bytes of scratch wanted behind the planes (at q8_planes_bytes)
+int q8_planes(spq4k_ctx* c, const float* x, int64_t x_tstride, int T, int nb, Q8Planes* Q, bool perm = false,
+              size_t extra = 0) {
     const size_t items = (size_t)T * nb;
-    int rc = ensure_scratch(c, items * (256 + Q8MN_BYTES + 32 + 4));
+    int rc = ensure_scratch(c, q8_planes_bytes(T, nb) + extra);
     if (rc) return rc;
     int8_t* qs = (int8_t*)c->scratch;
     uint8_t* mn = c->scratch + items * 256;
@@ -173,6 +179,9 @@ DecodeCfg plan_decode(const spq4k_ctx* c, int nb, int64_t rows) {
     return d;
 }
 
+int gemm_segments(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T,
+                  int mode);
+
 int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* x, float* const* y, int64_t T) {
     if (n < 1 || n > GEMV_MAX_SEG) return set_err(c, -EINVAL, "gemv: n=%d matrices (1..4)", n);
     if (T < 1 || T > SPQ4K_GEMV_MAX_T) return set_err(c, -EINVAL, "gemv: T=%lld (1..8)", (long long)T);
@@ -222,28 +231,7 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
     if (T >= c->gemv_mfma_min_t && c->force_bpr == 0) {
         // 4 <= T <= 8: the sdot4 kernel's integer work grows with T while the
         // matrix cores' 16-token tile costs the same from T = 1 to 16
-        GemmParams g;
-        memset(&g, 0, sizeof g);
-        g.T = (int32_t)T;
-        g.nb = p.nb;
-        g.mode = 1;
-        g.cfg = -1;
-        int rc = q8_planes(c, x, K, (int)T, p.nb, &g.Q);
-        if (rc) return rc;
-        int64_t t16 = 0;
-        for (int i = 0; i < n; ++i) {
-            g.seg[i].W = W[i]->data;
-            g.seg[i].Y = y[i];
-            g.seg[i].M = (int32_t)W[i]->M;
-            g.seg[i].tile_begin = (int32_t)t16;
-            t16 += (W[i]->M + 15) / 16;
-        }
-        for (int i = n; i < GEMM_MAX_SEG; ++i) g.seg[i].tile_begin = INT32_MAX;
-        g.nseg = n;
-        g.total_tiles = (int32_t)t16;
-        hipError_t e = launch_gemm_skinny(g, c->stream);
-        if (e != hipSuccess) return hip_fail(c, e, "gemv (matrix cores) launch");
-        return 0;
+        return gemm_segments(c, n, W, x, y, T, c->gemm_mode == 1 ? 1 : 0);
     }
     const int cb_max = LDS_BUDGET / ((int)T * 292);
     p.chunk_blocks = p.nb < cb_max ? p.nb : cb_max;
@@ -559,6 +547,63 @@ int spq4k_gemv_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const f
     return gemv_launch(c, n, W, x, y, T);
 }
 
+namespace {
+
+// Matrix-core matmul of n matrices sharing the input (shapes checked by the
+// callers): plan, quantise X once into the context scratch (with the partial
+// plane of a K split behind it), launch.
+int gemm_segments(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T,
+                  int mode) {
+    const int64_t K = W[0]->K;
+    GemmParams p;
+    memset(&p, 0, sizeof p);
+    p.T = (int32_t)T;
+    p.nb = (int32_t)(K / SPQ4K_QK_K);
+    p.mode = mode;
+    p.cfg = c->gemm_cfg;
+    int64_t tiles16 = 0, rows = 0;
+    for (int i = 0; i < n; ++i) {
+        p.seg[i].W = W[i]->data;
+        p.seg[i].Y = Y[i];
+        p.seg[i].M = (int32_t)W[i]->M;
+        p.seg[i].tile_begin = (int32_t)tiles16;
+        p.seg[i].row_begin = (int32_t)rows;
+        tiles16 += (W[i]->M + 15) / 16;
+        rows += W[i]->M;
+    }
+    for (int i = n; i < GEMM_MAX_SEG; ++i) p.seg[i].tile_begin = p.seg[i].row_begin = INT32_MAX;
+    p.nseg = n;
+    p.rows = (int32_t)rows;
+    if (tiles16 * ((T + 15) / 16) > (1ll << 31) - 1 || rows > (1ll << 31) - 1)
+        return set_err(c, -EINVAL, "gemm: grid too large");
+    hipError_t e;
+    if (gemm_use_skinny((int)T, mode)) {
+        int rc = q8_planes(c, X, K, (int)T, p.nb, &p.Q);
+        if (rc) return rc;
+        p.total_tiles = (int32_t)tiles16;
+        e = launch_gemm_skinny(p, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemm skinny launch");
+        return 0;
+    }
+    // a K split's partial plane uses the scratch the context already holds,
+    // and at least 8 MB
+    const size_t planes = q8_planes_bytes((int)T, p.nb);
+    size_t room = c->scratch_cap > planes ? c->scratch_cap - planes : 0;
+    if (room < ((size_t)8 << 20)) room = (size_t)8 << 20;
+    const GemmPlan g = gemm_plan(p, c->num_cus, room);
+    p.cfg = g.cfg;
+    p.ksplit = g.ksplit;
+    p.kchunk = g.kchunk;
+    int rc = q8_planes(c, X, K, (int)T, p.nb, &p.Q, g.perm, g.partial_bytes);
+    if (rc) return rc;
+    p.P = g.ksplit > 1 ? reinterpret_cast<float*>(c->scratch + planes) : nullptr;
+    e = launch_gemm(p, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "gemm launch");
+    return 0;
+}
+
+}  // namespace
+
 int spq4k_gemm_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y,
                      int64_t T) {
     int rc = use_device(c);
@@ -574,38 +619,7 @@ int spq4k_gemm_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const f
         if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemm: misaligned weights");
         if (W[i]->device != c->device) return set_err(c, -EINVAL, "gemm: weights live on another device");
     }
-    GemmParams p;
-    memset(&p, 0, sizeof p);
-    p.T = (int32_t)T;
-    p.nb = (int32_t)(K / SPQ4K_QK_K);
-    p.mode = c->gemm_mode;
-    p.cfg = c->gemm_cfg;
-    int64_t tiles16 = 0;
-    for (int i = 0; i < n; ++i) {
-        p.seg[i].W = W[i]->data;
-        p.seg[i].Y = Y[i];
-        p.seg[i].M = (int32_t)W[i]->M;
-        p.seg[i].tile_begin = (int32_t)tiles16;
-        tiles16 += (W[i]->M + 15) / 16;
-    }
-    for (int i = n; i < GEMM_MAX_SEG; ++i) p.seg[i].tile_begin = INT32_MAX;
-    p.nseg = n;
-    if (tiles16 * ((T + 15) / 16) > (1ll << 31) - 1) return set_err(c, -EINVAL, "gemm: grid too large");
-    const bool skinny = gemm_use_skinny((int)T, c->gemm_mode);
-    if (!skinny) p.cfg = gemm_tiled_pick(p, c->num_cus);
-    // the input is quantised once for all the matrices
-    rc = q8_planes(c, X, K, (int)T, p.nb, &p.Q, !skinny && gemm_tiled_perm(p.cfg));
-    if (rc) return rc;
-    hipError_t e;
-    if (skinny) {
-        p.total_tiles = (int32_t)tiles16;
-        e = launch_gemm_skinny(p, c->stream);
-        if (e != hipSuccess) return hip_fail(c, e, "gemm skinny launch");
-        return 0;
-    }
-    e = launch_gemm(p, c->num_cus, c->stream);
-    if (e != hipSuccess) return hip_fail(c, e, "gemm launch");
-    return 0;
+    return gemm_segments(c, n, W, X, Y, T, c->gemm_mode);
 }
 
 int spq4k_gemm(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {

@@ -322,38 +322,40 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Ring form (large T). Every operand of a super-block reaches LDS through
-// direct global -> LDS loads (global_load_lds_dwordx4), S super-blocks ahead,
-// so a wave's registers hold only accumulators and the operands of one step.
+// Ring form. Every operand of a super-block reaches LDS through direct global
+// -> LDS loads (global_load_lds_dwordx4), S - 1 super-blocks ahead, so a
+// wave's registers hold only accumulators and the operands of one step.
 // A workgroup of NW waves owns ROWS = 16*RT*NW rows of one of up to four
-// matrices sharing the input and TOK = 16*CT tokens; wave w computes rows
-// 16*RT*w .. +16*RT of the tile against all TOK tokens (C = weights x
-// activations: output lane rows 4q .. 4q+3, token c16).
+// matrices sharing the input, TOK = 16*CT tokens and one of p.ksplit ranges of
+// p.kchunk super-blocks; wave w computes rows 16*RT*w .. +16*RT of the tile
+// against all TOK tokens (C = weights x activations: output lane rows
+// 4q .. 4q+3, token c16). With one K range the tile is stored to Y; with
+// several, to the partial plane p.P, which gemm_reduce_kernel sums in range
+// order (deterministic).
 //
-// A stage holds, as 16-byte slots (64 slots = one wave-wide load):
+// A stage holds, as 16-byte slots (64 slots = one wave-wide load), each
+// region rounded up to whole loads:
 //   ROWS x 9 slots   the super-block of each row (144 bytes, row-major);
 //   TOK x 17 slots   the Q8_K values of each token (the permuted order of
 //                    quantize_q8k_planes: one 16-byte read per fragment), one
 //                    spare slot a row so that the 16 tokens of a fragment read
 //                    hit distinct banks;
 //   TOK x 3 slots    the min-term operand and d of each token (Q8Planes::mn);
-// all three counts are whole numbers of loads for CT a multiple of 4, and the
-// NPW loads a wave issues per stage cover them (the surplus loads re-read a
-// valid address into the stage's spare tail). A wave waits for its own loads
-// of a stage with s_waitcnt vmcnt (loads complete in order) before the
-// barrier that publishes the stage to the other waves.
+// the NPW loads a wave issues per stage cover them (the surplus and padding
+// slots re-read a valid address). A wave waits for its own loads of a stage
+// with s_waitcnt vmcnt (loads complete in order) before the barrier that
+// publishes the stage to the other waves.
 template <int RT, int CT, int NW, int S>
 __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
-    static_assert(CT % 4 == 0, "token tile of 64 or 128");
     constexpr int TOK = CT * 16;
     constexpr int ROWS = RT * 16 * NW;
     constexpr int QS = 272;                       // LDS bytes per token of q8
     constexpr int W_SLOTS = ROWS * 9, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
-    constexpr int NLOAD = (W_SLOTS + Q_SLOTS + M_SLOTS) / 64;
+    constexpr int W_LOADS = (W_SLOTS + 63) / 64, Q_LOADS = (Q_SLOTS + 63) / 64, M_LOADS = (M_SLOTS + 63) / 64;
+    constexpr int NLOAD = W_LOADS + Q_LOADS + M_LOADS;
     constexpr int NPW = (NLOAD + NW - 1) / NW;    // loads per wave per stage
     constexpr int STAGE = NPW * NW * 1024;
-    constexpr int Q_OFF = W_SLOTS * 16, M_OFF = Q_OFF + Q_SLOTS * 16;
-    static_assert(W_SLOTS % 64 == 0 && Q_SLOTS % 64 == 0 && M_SLOTS % 64 == 0, "whole loads per operand");
+    constexpr int Q_OFF = W_LOADS * 1024, M_OFF = Q_OFF + Q_LOADS * 1024;
     __shared__ __align__(1024) uint8_t lds[S][STAGE];
 
     const int lane = threadIdx.x & 63;
@@ -364,41 +366,47 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
     const int ttiles = (T + TOK - 1) / TOK;
     const int L = xcd_tile(blockIdx.x, gridDim.x);
     const int tt = L % ttiles;
-    const int gt = L / ttiles;
+    const int gt = (L / ttiles) % p.total_tiles;
+    const int ks = L / (ttiles * p.total_tiles);
     int sidx = 0;
 #pragma unroll
     for (int k = 1; k < GEMM_MAX_SEG; ++k)
         if (k < p.nseg && gt >= p.seg[k].tile_begin) sidx = k;
     const uint8_t* __restrict__ W = p.seg[sidx].W;
-    float* __restrict__ Y = p.seg[sidx].Y;
     const int M = p.seg[sidx].M;
     const int row0 = (gt - p.seg[sidx].tile_begin) * ROWS;
     const int tok0 = tt * TOK;
+    const int kb0 = ks * p.kchunk;
+    const int nbl = min(nb - kb0, p.kchunk);       // super-blocks of this range (>= 1)
 
-    // per load: source of super-block 0 and the byte stride between super-blocks
+    // per load: source of the range's first super-block, byte stride between super-blocks
     const uint8_t* src[NPW];
     uint32_t stride[NPW];
 #pragma unroll
     for (int i = 0; i < NPW; ++i) {
         const int J = NW * i + wave;              // load index within the stage
         const int slot = J * 64 + lane;
-        if (J * 64 < W_SLOTS) {
+        src[i] = p.Q.mn;                          // surplus and padding: any valid address
+        stride[i] = 0;
+        if (J < W_LOADS) {
             const int r = min(row0 + slot / 9, M - 1);
-            src[i] = W + (size_t)r * nb * Q4K_BYTES + 16 * (slot % 9);
+            src[i] = W + ((size_t)r * nb + kb0) * Q4K_BYTES + 16 * (slot % 9);
             stride[i] = Q4K_BYTES;
-        } else if (J * 64 < W_SLOTS + Q_SLOTS) {
-            const int sl = slot - W_SLOTS;
-            const int tg = min(tok0 + sl / 17, T - 1);
-            src[i] = reinterpret_cast<const uint8_t*>(p.Q.qs) + (size_t)tg * nb * 256 + 16 * min(sl % 17, 15);
-            stride[i] = 256;
-        } else if (J * 64 < W_SLOTS + Q_SLOTS + M_SLOTS) {
-            const int sl = slot - W_SLOTS - Q_SLOTS;
-            const int tg = min(tok0 + sl / 3, T - 1);
-            src[i] = p.Q.mn + (size_t)tg * nb * Q8MN_BYTES + 16 * (sl % 3);
-            stride[i] = Q8MN_BYTES;
-        } else {
-            src[i] = p.Q.mn;                       // surplus load: any valid address
-            stride[i] = 0;
+        } else if (J < W_LOADS + Q_LOADS) {
+            const int sl = slot - W_LOADS * 64;
+            if (sl < Q_SLOTS) {
+                const int tg = min(tok0 + sl / 17, T - 1);
+                src[i] = reinterpret_cast<const uint8_t*>(p.Q.qs) + ((size_t)tg * nb + kb0) * 256 +
+                         16 * min(sl % 17, 15);
+                stride[i] = 256;
+            }
+        } else if (J < NLOAD) {
+            const int sl = slot - (W_LOADS + Q_LOADS) * 64;
+            if (sl < M_SLOTS) {
+                const int tg = min(tok0 + sl / 3, T - 1);
+                src[i] = p.Q.mn + ((size_t)tg * nb + kb0) * Q8MN_BYTES + 16 * (sl % 3);
+                stride[i] = Q8MN_BYTES;
+            }
         }
     }
     auto issue = [&](int b, int buf) {
@@ -416,14 +424,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
         for (int ct = 0; ct < CT; ++ct) acc[r][ct] = v4f{0, 0, 0, 0};
 
 #pragma unroll
-    for (int k = 0; k < S - 1; ++k) issue(min(k, nb - 1), k);
-    for (int b = 0; b < nb; ++b) {
+    for (int k = 0; k < S - 1; ++k) issue(min(k, nbl - 1), k);
+    for (int b = 0; b < nbl; ++b) {
         const int buf = b % S;
         // this wave's loads of stage b are done (the S - 2 later stages may
         // still be in flight); the barrier publishes everyone's and retires
         // the readers of the buffer refilled next
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * NPW) : "memory");
-        issue(min(b + S - 1, nb - 1), (b + S - 1) % S);
+        issue(min(b + S - 1, nbl - 1), (b + S - 1) % S);
 
         const uint8_t* st = lds[buf];
         const uint8_t* wt = st + (wave * RT * 16) * Q4K_BYTES;
@@ -514,6 +522,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the clamped loads past the last stage
 
+    // destination: Y of the segment, or this range's slice of the partial plane
+    // (rows of all segments one after the other, p.rows in all)
+    float* __restrict__ out;
+    int64_t ld;
+    int rbase;
+    if (p.ksplit > 1) {
+        out = p.P + (int64_t)ks * T * p.rows;
+        ld = p.rows;
+        rbase = p.seg[sidx].row_begin;
+    } else {
+        out = p.seg[sidx].Y;
+        ld = M;
+        rbase = 0;
+    }
+    const bool vec = ((ld | rbase) & 3) == 0;
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         const int rq = row0 + wave * RT * 16 + r * 16 + 4 * q;
@@ -521,8 +544,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
         for (int ct = 0; ct < CT; ++ct) {
             const int t = tok0 + ct * 16 + c16;
             if (t >= T) continue;
-            float* y = Y + (int64_t)t * M + rq;
-            if ((M & 3) == 0 && rq + 3 < M) {
+            float* y = out + (int64_t)t * ld + rbase + rq;
+            if (vec && rq + 3 < M) {
                 *reinterpret_cast<v4f*>(y) = acc[r][ct];
             } else {
 #pragma unroll
@@ -531,6 +554,32 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
             }
         }
     }
+}
+
+// Y[t][r] of each segment = sum over the K ranges, in range order, of the
+// partial plane P[range][t][row_begin + r]: one element a thread, every
+// range's load issued before the sums.
+constexpr int REDUCE_MAX_SPLIT = 32;
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
+    const int64_t n = (int64_t)p.T * p.rows;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int ks = p.ksplit;
+    float part[REDUCE_MAX_SPLIT];
+#pragma unroll
+    for (int k = 0; k < REDUCE_MAX_SPLIT; ++k)
+        if (k < ks) part[k] = p.P[(int64_t)k * n + i];
+    float sum = part[0];
+#pragma unroll
+    for (int k = 1; k < REDUCE_MAX_SPLIT; ++k)
+        if (k < ks) sum += part[k];
+    const int t = (int)(i / p.rows);
+    const int rg = (int)(i - (int64_t)t * p.rows);
+    int sidx = 0;
+#pragma unroll
+    for (int k = 1; k < GEMM_MAX_SEG; ++k)
+        if (k < p.nseg && rg >= p.seg[k].row_begin) sidx = k;
+    p.seg[sidx].Y[(int64_t)t * p.seg[sidx].M + (rg - p.seg[sidx].row_begin)] = sum;
 }
 
 // ---------------------------------------------------------------------------
@@ -714,12 +763,12 @@ hipError_t launch_gemm_skinny(const GemmParams& p, hipStream_t st) {
     return longk ? launch_skinny<4, 16, 1>(p, st) : launch_skinny<4, 8, 1>(p, st);
 }
 
-bool gemm_use_skinny(int T, int mode) { return mode == 1 || (mode != 2 && T <= 64); }
+bool gemm_use_skinny(int T, int mode) { return mode == 1; }
 
 // Tiled-kernel launch shapes, indexed by GemmParams::cfg (-1: chosen here).
 struct TiledShape {
     int rows, tok;   // workgroup tile
-    bool perm;       // reads the permuted Q8_K values
+    bool ring;       // ring kernel: permuted Q8_K values, K ranges
     hipError_t (*launch)(const GemmParams&, int grid, hipStream_t);
 };
 template <int RT, int CT, int WR, int WK>
@@ -736,33 +785,69 @@ static const TiledShape kTiled[] = {
     {256, 64, true, launch_ring_<2, 4, 8, 2>},      // 0: ring, 8 waves, 2 stages
     {128, 64, true, launch_ring_<1, 4, 8, 3>},      // 1: ring, 8 waves, 3 stages
     {128, 64, true, launch_ring_<2, 4, 4, 3>},      // 2: ring, 4 waves, 3 stages
-    {64, 32, false, launch_tiled_<2, 2, 2, 2>},     // 3: K split in two
-    {32, 16, false, launch_tiled_<2, 1, 1, 4>},     // 4: K split in four
+    {64, 32, false, launch_tiled_<2, 2, 2, 2>},     // 3: register-staged, K split in two
+    {32, 16, false, launch_tiled_<2, 1, 1, 4>},     // 4: register-staged, K split in four
     {128, 64, false, launch_tiled_<2, 4, 4, 1>},    // 5: register-staged
+    {128, 16, true, launch_ring_<1, 1, 8, 3>},      // 6: ring, T <= 16
+    {128, 32, true, launch_ring_<1, 2, 8, 3>},      // 7: ring, T <= 32
+    {64, 16, true, launch_ring_<1, 1, 4, 3>},       // 8: ring, T <= 16, 4 waves
 };
 constexpr int N_TILED = (int)(sizeof(kTiled) / sizeof(kTiled[0]));
 
 int gemm_tiled_shapes() { return N_TILED; }
-bool gemm_tiled_perm(int cfg) { return cfg >= 0 && cfg < N_TILED && kTiled[cfg].perm; }
 
-static int64_t tiled_grid(const GemmParams& p, const TiledShape& s) {
+static int64_t row_tiles(const GemmParams& p, int rows) {
     int64_t tiles = 0;
-    for (int i = 0; i < p.nseg; ++i) tiles += (p.seg[i].M + s.rows - 1) / s.rows;
-    return tiles * ((p.T + s.tok - 1) / s.tok);
+    for (int i = 0; i < p.nseg; ++i) tiles += (p.seg[i].M + rows - 1) / rows;
+    return tiles;
 }
 
-int gemm_tiled_pick(const GemmParams& p, int num_cus) {
-    if (p.cfg >= 0 && p.cfg < N_TILED) return p.cfg;
-    // the largest tile that still gives every CU a workgroup (measured on
-    // MI355X at T = 512: 256 x 64 for 24576 rows, 128 x 64 for 4096 and 6144)
-    for (int c : {0, 1, 3})
-        if (tiled_grid(p, kTiled[c]) >= num_cus) return c;
-    return 4;
-}
-
-hipError_t launch_gemm(const GemmParams& p0, int num_cus, hipStream_t st) {
-    const int cfg = gemm_tiled_pick(p0, num_cus);
+GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
+    GemmPlan g;
+    int cfg = p.cfg;
+    if (cfg < 0 || cfg >= N_TILED) {
+        if (p.T <= 16) {
+            cfg = 6;
+        } else if (p.T <= 32) {
+            cfg = 7;
+        } else {
+            // the largest tile that gives every CU a workgroup without a K
+            // split (measured on MI355X at T = 512: 256 x 64 for 24576 rows,
+            // 128 x 64 for 4096 and 6144), else 128 x 64 with one
+            cfg = 1;
+            const int64_t g0 = row_tiles(p, 256) * ((p.T + 63) / 64);
+            if (g0 >= num_cus) cfg = 0;
+        }
+    }
     const TiledShape& s = kTiled[cfg];
+    g.cfg = cfg;
+    g.perm = s.ring;
+    g.ksplit = 1;
+    g.kchunk = p.nb;
+    g.partial_bytes = 0;
+    if (s.ring) {
+        // split K until two workgroups per CU, keeping >= 4 super-blocks a range
+        const int64_t grid0 = row_tiles(p, s.rows) * ((p.T + s.tok - 1) / s.tok);
+        int64_t want = (2 * (int64_t)num_cus + grid0 - 1) / grid0;
+        int64_t most = p.nb / 4 > 1 ? p.nb / 4 : 1;
+        if (most > REDUCE_MAX_SPLIT) most = REDUCE_MAX_SPLIT;
+        if (want > most) want = most;
+        const size_t per_split = (size_t)p.T * p.rows * sizeof(float);
+        while (want > 1 && (size_t)want * per_split > max_partial_bytes) --want;
+        if (want > 1) {
+            g.kchunk = (int)((p.nb + want - 1) / want);
+            g.ksplit = (p.nb + g.kchunk - 1) / g.kchunk;
+            g.partial_bytes = g.ksplit > 1 ? (size_t)g.ksplit * per_split : 0;
+            if (g.ksplit == 1) g.kchunk = p.nb;
+        }
+    }
+    return g;
+}
+
+hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
+    if (p0.cfg < 0 || p0.cfg >= N_TILED) return hipErrorInvalidValue;
+    const TiledShape& s = kTiled[p0.cfg];
+    if (!s.ring && p0.ksplit != 1) return hipErrorInvalidValue;
     GemmParams p = p0;
     int64_t tiles = 0;
     for (int i = 0; i < p.nseg; ++i) {
@@ -770,9 +855,14 @@ hipError_t launch_gemm(const GemmParams& p0, int num_cus, hipStream_t st) {
         tiles += (p.seg[i].M + s.rows - 1) / s.rows;
     }
     for (int i = p.nseg; i < GEMM_MAX_SEG; ++i) p.seg[i].tile_begin = INT32_MAX;
-    const int64_t grid = tiled_grid(p, s);
+    p.total_tiles = (int32_t)tiles;
+    const int64_t grid = tiles * ((p.T + s.tok - 1) / s.tok) * p.ksplit;
     if (grid > INT32_MAX) return hipErrorInvalidValue;
-    return s.launch(p, (int)grid, st);
+    hipError_t e = s.launch(p, (int)grid, st);
+    if (e != hipSuccess || p.ksplit == 1) return e;
+    const int64_t n = (int64_t)p.T * p.rows;
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p);
+    return hipGetLastError();
 }
 
 }  // namespace spq4k

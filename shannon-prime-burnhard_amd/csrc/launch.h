@@ -99,24 +99,35 @@ struct GemmSeg {
     float* Y;             // [T][M]
     int32_t M;
     int32_t tile_begin;   // first row tile of this segment (set by the launcher)
+    int32_t row_begin;    // first row of this segment in the concatenation of all segments
 };
 struct GemmParams {
     Q8Planes Q;         // Q8_K of the T input rows
     int32_t T, nb;
-    int32_t mode;       // 0 auto, 1 skinny kernel at any T, 2 tiled kernel at any T
+    int32_t mode;       // 0 auto, 1 skinny kernel at any T, 2 tiled kernels only
     int32_t cfg;        // tiled launch shape (0 .. gemm_tiled_shapes() - 1), -1 automatic
     GemmSeg seg[GEMM_MAX_SEG];   // up to four matrices sharing the input
     int32_t nseg;
     int32_t total_tiles;
+    int32_t rows;       // sum of the segments' M
+    int32_t ksplit;     // K ranges (ring kernels): 1, or partial sums in P then a reduction
+    int32_t kchunk;     // super-blocks per K range
+    float* P;           // [ksplit][T][rows] partial plane when ksplit > 1
+};
+// Launch plan of the tiled / ring kernels for a GemmParams (T, nb, segments,
+// cfg): shape, K split and the scratch the partial plane needs.
+struct GemmPlan {
+    int cfg;
+    int ksplit, kchunk;
+    bool perm;                 // reads the permuted Q8_K values
+    size_t partial_bytes;      // ksplit * T * rows * 4 when ksplit > 1
 };
 bool gemm_use_skinny(int T, int mode);
 int gemm_tiled_shapes();
-// tiled launch shape for these params (p.cfg if set) and whether it reads the
-// permuted Q8_K values (quantize_q8k_planes with perm)
-int gemm_tiled_pick(const GemmParams& p, int num_cus);
-bool gemm_tiled_perm(int cfg);
-hipError_t launch_gemm(const GemmParams& p, int num_cus, hipStream_t st);   // tiled, all segments
-hipError_t launch_gemm_skinny(const GemmParams& p, hipStream_t st);          // skinny, all segments
+GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes);
+// p.cfg / p.ksplit / p.kchunk / p.P as planned; launches the reduction too
+hipError_t launch_gemm(const GemmParams& p, hipStream_t st);
+hipError_t launch_gemm_skinny(const GemmParams& p, hipStream_t st);   // skinny, all segments
 
 // element-wise conversions (k_convert.hip)
 hipError_t launch_quantize_q8k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
