@@ -32,7 +32,7 @@ struct spq4k_ctx {
     int gemv_mfma_min_t = 4;     // SPQ4K_GEMV_MFMA_MIN_T: batches of at least this many tokens use matrix cores
     int no_decode = 0;           // SPQ4K_GEMV_GENERIC=1: T = 1 also uses the generic kernel
     int moe_unfused = 0;         // SPQ4K_MOE_UNFUSED=1: routing pass + Q8_K planes + matvec (3 launches)
-    int moe_mode = 0;            // SPQ4K_MOE_MODE=2: skip the small-batch decode mapping
+    int moe_mode = 0;            // SPQ4K_MOE_MODE: 2 skips the small-batch decode mapping, 3 takes the single-launch sdot4 kernel
     int gemm_mode = 0;           // SPQ4K_GEMM_MODE: 0 auto, 1 skinny kernel, 2 tiled kernel
     int gemm_cfg = -1;           // SPQ4K_GEMM_CFG: tiled launch shape, -1 automatic
     DecodeCfg dec_force = {0, 0, false, 0};   // SPQ4K_DEC_{WAVES,DEPTH,XFIRST,GRID} overrides
@@ -659,7 +659,7 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     // small batches: the decode mapping (every routed pair's rows in one
     // sweep; an expert chosen twice is streamed twice, so only for T <= 4)
     if (T <= 4 && n_pairs <= MOE_DEC_MAX_PAIRS && rows <= MOE_DEC_MAX_XROWS && moe_decode_supported(nb) &&
-        !c->moe_unfused && c->moe_mode != 2 &&
+        !c->moe_unfused && c->moe_mode == 0 &&
         (size_t)q8lds_bytes((int)rows * nb) <= (size_t)LDS_BUDGET) {
         MoeFusedParams f;
         memset(&f, 0, sizeof f);
@@ -683,7 +683,7 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
         if (e != hipSuccess) return hip_fail(c, e, "moe decode launch");
         return 0;
     }
-    if (n_pairs <= MOE_FUSED_MAX_PAIRS && !c->moe_unfused) {
+    if (c->moe_mode == 3 && n_pairs <= MOE_FUSED_MAX_PAIRS && !c->moe_unfused) {
         MoeFusedParams f;
         memset(&f, 0, sizeof f);
         f.ids = ids;
@@ -723,10 +723,15 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     p.route.act_off = rt + 1 + E;
     p.route.act_cnt = rt + 1 + 2 * E;
     p.route.pairs = rt + 1 + 3 * E;
-    hipError_t e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, mn, false, c->stream);
-    if (e != hipSuccess) return hip_fail(c, e, "moe quantize launch");
-    e = launch_moe_route(ids, (int)n_pairs, E, p.route, c->stream);
-    if (e != hipSuccess) return hip_fail(c, e, "moe route launch");
+    // matrix cores unless the sdot4 kernels are asked for (SPQ4K_MOE_UNFUSED)
+    const bool ring = !c->moe_unfused;
+    hipError_t e;
+    if (!ring) {
+        e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, mn, false, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "moe quantize launch");
+        e = launch_moe_route(ids, (int)n_pairs, E, p.route, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "moe route launch");
+    }
     p.bank = bank->data;
     p.expert_bytes = (size_t)M * nb * SPQ4K_Q4K_BLOCK_BYTES;
     p.Y = Y;
@@ -738,6 +743,21 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     p.nb = nb;
     p.n_used = (int)n_used;
     p.ne11 = (int)ne11;
+    if (ring) {
+        // row tiles a workgroup streams: as many as still leave two
+        // workgroups per CU over the experts that can be active
+        const int64_t ntiles = (M + 127) / 128;
+        int64_t rtw = ntiles * max_act / (2 * (int64_t)c->num_cus);
+        if (rtw < 1) rtw = 1;
+        if (rtw > ntiles) rtw = ntiles;
+        p.ring_rt = (int32_t)rtw;
+        p.tiles_per_expert = (int32_t)((ntiles + rtw - 1) / rtw);
+        if (max_act * p.tiles_per_expert > (1ll << 31) - 1 || rows * nb / 16 > (1ll << 31) - 2)
+            return set_err(c, -EINVAL, "moe: grid too large");
+        e = launch_moe_ring(p, ids, (int)n_pairs, E, X, bank->K, (int)rows, (int)max_act, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "moe ring launch");
+        return 0;
+    }
     p.tiles_per_expert = tiles_per_expert;
     p.chunk_blocks = chunk_blocks;
     const int64_t grid = max_act * p.tiles_per_expert;

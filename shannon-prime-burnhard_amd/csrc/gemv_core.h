@@ -108,6 +108,52 @@ struct Q8Planes {
 };
 constexpr int Q8MN_BYTES = 48;
 
+// fp32 rows -> Q8_K planes (qs [T][nb][256], bs [T][nb][16], d [T][nb] and the
+// min-term operand mn [T][nb][48 B]): the activation operand of the
+// pre-quantised GEMV/MoE/GEMM paths. Items (t, block) 16 * blk .. +15, 16 lanes
+// an item (256 threads). With `perm` each 64-value group g of qs is stored as
+// the matrix-core ring kernels read it: bytes 64g + 16s .. +15 hold values
+// 64g + 8s .. +7 then 64g + 32 + 8s .. +7 (s = 0..3).
+__device__ __forceinline__ void quantize_planes_items(const float* __restrict__ x, int64_t x_tstride, int T, int nb,
+                                                      int8_t* __restrict__ qs, int16_t* __restrict__ bs,
+                                                      float* __restrict__ d, uint8_t* __restrict__ mn, int perm,
+                                                      int64_t blk) {
+    const int e = threadIdx.x & 15;
+    const int64_t nitems = (int64_t)T * nb;
+    const int64_t item0 = blk * 16 + (threadIdx.x >> 4);
+    const bool valid = item0 < nitems;
+    const int64_t item = valid ? item0 : nitems - 1;
+    const int64_t t = item / nb;
+    const int64_t b = item - t * nb;
+    const float4* src = reinterpret_cast<const float4*>(x + t * x_tstride + b * QK + 16 * e);
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 a = src[i];
+        v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+    }
+    const Q8Lane q = quantize_q8k_16(v, e);
+    // sub-block j = e / 2 sums the bsums of lanes 2j and 2j + 1
+    const int bsum_pair = q.bsum + __shfl_xor(q.bsum, 1, 16);
+    if (!valid) return;
+    if (perm) {
+        // values 16e .. 16e+15 = 64g + 32h + 8s .. for g = e/4, h = (e/2)&1, s = 2(e&1), 2(e&1)+1
+        int8_t* dst = qs + item * 256 + 64 * (e >> 2) + 32 * (e & 1) + 8 * ((e >> 1) & 1);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(q.q[0], q.q[1]);
+        *reinterpret_cast<uint2*>(dst + 16) = make_uint2(q.q[2], q.q[3]);
+    } else {
+        *reinterpret_cast<uint4*>(qs + item * 256 + 16 * e) = make_uint4(q.q[0], q.q[1], q.q[2], q.q[3]);
+    }
+    bs[item * 16 + e] = (int16_t)q.bsum;
+    if (e == 0) d[item] = q.d;
+    _Float16* m = reinterpret_cast<_Float16*>(mn + item * Q8MN_BYTES);
+    if ((e & 1) == 0) {
+        m[e >> 1] = (_Float16)(bsum_pair >> 5);       // hi_j, floor division (|BS_j| <= 4064)
+        m[8 + (e >> 1)] = (_Float16)(bsum_pair & 31);  // lo_j
+    }
+    if (e == 1) *reinterpret_cast<float*>(mn + item * Q8MN_BYTES + 32) = q.d;
+}
+
 // Two integer sub-block sums of one lane against one staged activation block.
 __device__ __forceinline__ void subblock_pair(const Nib& n, const int8_t* q8blk, int l4, int& S0, int& S1) {
     const int4* p = reinterpret_cast<const int4*>(q8blk + 64 * l4);

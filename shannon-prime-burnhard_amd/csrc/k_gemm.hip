@@ -23,14 +23,9 @@
 //   - per super-block acc += d8 (d I - dmin M) in fp32.
 #include "gemv_core.h"
 #include "launch.h"
+#include "ring_core.h"
 
 namespace spq4k {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 // per-lane weight registers for one super-block: header + 64 B of qs (skinny kernel)
 struct WG4 {
@@ -46,17 +41,6 @@ __device__ __forceinline__ int xcd_tile(int bid, int G) {
     return x * (G >> 3) + min(x, G & 7) + (bid >> 3);
 }
 
-__device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
-    // two 16-bit products (v_pk_mul_lo_u16); each byte of `a` is < 16 and each
-    // 16-bit half of `b` is < 8, so no product carries across a byte
-    u16x2 x, y;
-    __builtin_memcpy(&x, &a, 4);
-    __builtin_memcpy(&y, &b, 4);
-    const u16x2 z = x * y;
-    uint32_t r;
-    __builtin_memcpy(&r, &z, 4);
-    return r;
-}
 
 // ---------------------------------------------------------------------------
 // Tiled form. A workgroup of four waves owns ROWS = WR*RT*16 rows of one of up
@@ -349,7 +333,6 @@ template <int RT, int CT, int NW, int S>
 __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
     constexpr int TOK = CT * 16;
     constexpr int ROWS = RT * 16 * NW;
-    constexpr int QS = 272;                       // LDS bytes per token of q8
     constexpr int W_SLOTS = ROWS * 9, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
     constexpr int W_LOADS = (W_SLOTS + 63) / 64, Q_LOADS = (Q_SLOTS + 63) / 64, M_LOADS = (M_SLOTS + 63) / 64;
     constexpr int NLOAD = W_LOADS + Q_LOADS + M_LOADS;
@@ -433,92 +416,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * NPW) : "memory");
         issue(min(b + S - 1, nbl - 1), (b + S - 1) % S);
 
-        const uint8_t* st = lds[buf];
-        const uint8_t* wt = st + (wave * RT * 16) * Q4K_BYTES;
-        v4i ch[RT][CT], cl[RT][CT];
-        uint32_t SH0[RT], SL0[RT], SH1[RT], SL1[RT];
-        v4i wq[RT][2];
-        h4 am[RT];
-        float dr[RT][4], dmr[RT][4];
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const uint8_t* wr = wt + (r * 16 + c16) * Q4K_BYTES;
-            const v4i hdr = *reinterpret_cast<const v4i*>(wr);
-            wq[r][0] = *reinterpret_cast<const v4i*>(wr + 16 + 32 * q);
-            wq[r][1] = *reinterpret_cast<const v4i*>(wr + 32 + 32 * q);
-            // d, dmin of output rows 4q .. 4q+3 of this row tile
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t h = *reinterpret_cast<const uint32_t*>(wt + (r * 16 + 4 * q + i) * Q4K_BYTES);
-                dr[r][i] = half_bits_to_float(h & 0xFFFFu);
-                dmr[r][i] = half_bits_to_float(h >> 16);
-            }
-            const ScaleMin sm = unpack_scale_min((uint32_t)hdr.y, (uint32_t)hdr.z, (uint32_t)hdr.w);
-            // this lane's sub-blocks 2q (low nibbles) and 2q + 1 (high nibbles)
-            const uint32_t sc01 = (q < 2 ? sm.sc_lo : sm.sc_hi) >> (16 * (q & 1));
-            SH0[r] = ((sc01 >> 3) & 7u) * 0x10001u;
-            SL0[r] = (sc01 & 7u) * 0x10001u;
-            SH1[r] = ((sc01 >> 11) & 7u) * 0x10001u;
-            SL1[r] = ((sc01 >> 8) & 7u) * 0x10001u;
-            // min operand of row c16: 32 m_j in k slots 0..7, m_j in slots
-            // 8..15 (0x6400 | m is the fp16 1024 + m, rescaled exactly)
-            const uint32_t mw = (q & 1) ? sm.m_hi : sm.m_lo;
-            const uint32_t x01 = __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u);
-            const uint32_t x23 = __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u);
-            h2 a01, a23;
-            __builtin_memcpy(&a01, &x01, 4);
-            __builtin_memcpy(&a23, &x23, 4);
-            const _Float16 f = q < 2 ? (_Float16)32.0f : (_Float16)1.0f;
-            const _Float16 o = q < 2 ? (_Float16)-32768.0f : (_Float16)-1024.0f;
-            const h2 fv = {f, f}, ov = {o, o};
-            const h2 b01 = a01 * fv + ov, b23 = a23 * fv + ov;
-            am[r] = h4{b01.x, b01.y, b23.x, b23.y};
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-                ch[r][ct] = v4i{0, 0, 0, 0};
-                cl[r][ct] = v4i{0, 0, 0, 0};
-            }
-        }
-        // activation fragment of token c16, step s: values 64q + 8s .. +7 and
-        // 64q + 32 + 8s .. +7, stored contiguously by the permuted Q8_K planes
-        const uint8_t* qb = st + Q_OFF + c16 * QS + 64 * q;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            v4i bq[CT];
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) bq[ct] = *reinterpret_cast<const v4i*>(qb + ct * 16 * QS + 16 * s);
-#pragma unroll
-            for (int r = 0; r < RT; ++r) {
-                const uint32_t w0 = (uint32_t)wq[r][s >> 1][2 * (s & 1)];
-                const uint32_t w1 = (uint32_t)wq[r][s >> 1][2 * (s & 1) + 1];
-                const uint32_t l0 = w0 & 0x0F0F0F0Fu, l1 = w1 & 0x0F0F0F0Fu;
-                const uint32_t u0 = (w0 >> 4) & 0x0F0F0F0Fu, u1 = (w1 >> 4) & 0x0F0F0F0Fu;
-                const v4i ah = {(int)pk_mul_u16(l0, SH0[r]), (int)pk_mul_u16(l1, SH0[r]),
-                                (int)pk_mul_u16(u0, SH1[r]), (int)pk_mul_u16(u1, SH1[r])};
-                const v4i al = {(int)pk_mul_u16(l0, SL0[r]), (int)pk_mul_u16(l1, SL0[r]),
-                                (int)pk_mul_u16(u0, SL1[r]), (int)pk_mul_u16(u1, SL1[r])};
-#pragma unroll
-                for (int ct = 0; ct < CT; ++ct) {
-                    ch[r][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq[ct], ch[r][ct], 0, 0, 0);
-                    cl[r][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq[ct], cl[r][ct], 0, 0, 0);
-                }
-            }
-        }
-        const uint8_t* mb = st + M_OFF + c16 * Q8MN_BYTES;
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-            const h4 bm = *reinterpret_cast<const h4*>(mb + ct * 16 * Q8MN_BYTES + 8 * q);
-            const float d8 = *reinterpret_cast<const float*>(mb + ct * 16 * Q8MN_BYTES + 32);
-#pragma unroll
-            for (int r = 0; r < RT; ++r) {
-                const v4f cm = __builtin_amdgcn_mfma_f32_16x16x16f16(am[r], bm, v4f{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int I = (ch[r][ct][i] << 3) + cl[r][ct][i];
-                    acc[r][ct][i] = fmaf(d8, fmaf(-dmr[r][i], cm[i], dr[r][i] * (float)I), acc[r][ct][i]);
-                }
-            }
-        }
+        ring_block<RT, CT>(lds[buf] + (wave * RT * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the clamped loads past the last stage
 

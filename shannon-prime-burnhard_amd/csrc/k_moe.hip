@@ -9,9 +9,9 @@
 // the number of tokens routed to it.
 //
 //   1. moe_route_kernel (one workgroup): per-expert counts, an exclusive scan,
-//      the compacted list of active experts and, per expert, its pairs in
-//      (token, slot) order. Out-of-range ids are not routed (their outputs are
-//      left untouched; the host entry points reject them).
+//      the compacted list of active experts and, per expert, its pairs.
+//      Out-of-range ids are not routed (their outputs are left untouched; the
+//      host entry points reject them).
 //   2. quantize_q8k_planes_kernel: the T*ne11 input rows to Q8_K planes.
 //   3. moe_gemv_kernel: workgroup (a, tile) takes active expert a and a tile
 //      of its rows; its pairs are processed TC at a time, each chunk staged
@@ -20,41 +20,96 @@
 // which does all three steps in one launch.
 #include "gemv_core.h"
 #include "launch.h"
+#include "ring_core.h"
 
 namespace spq4k {
 
+// Routing tables of one call, built by one workgroup of 256 threads: the ids
+// pass through LDS in chunks; per-expert counts by LDS atomics; a parallel
+// scan gives each expert's first pair and the compacted list of active
+// experts (ascending); the pairs are then placed by LDS atomics (their order
+// inside an expert is not fixed, and no output depends on it: every pair's
+// result is computed from its own input row and expert alone).
+// LDS: cnt[E], pos[E], ids[ROUTE_CHUNK], partial[2 * 256] ints.
+constexpr int ROUTE_CHUNK = 2048;
+size_t moe_route_lds_bytes(int E) { return ((size_t)2 * E + ROUTE_CHUNK + 512) * sizeof(int); }
+
+__device__ void route_block(const int32_t* __restrict__ ids, int n_pairs, int E, const MoeRoute& r, int* sh) {
+    int* cnt = sh;
+    int* pos = sh + E;
+    int* idl = sh + 2 * E;
+    int* part = idl + ROUTE_CHUNK;   // [256] pairs, [256] active experts
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += 256) cnt[e] = 0;
+    __syncthreads();
+    for (int base = 0; base < n_pairs; base += ROUTE_CHUNK) {
+        const int n = min(ROUTE_CHUNK, n_pairs - base);
+        for (int i = tid; i < n; i += 256) idl[i] = ids[base + i];
+        __syncthreads();
+        for (int i = tid; i < n; i += 256) {
+            const int e = idl[i];
+            if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+        }
+        __syncthreads();
+    }
+    // thread t scans experts [t * per, (t + 1) * per)
+    const int per = (E + 255) / 256;
+    const int e0 = min(tid * per, E), e1 = min(e0 + per, E);
+    int sp = 0, sa = 0;
+    for (int e = e0; e < e1; ++e) {
+        sp += cnt[e];
+        sa += cnt[e] > 0;
+    }
+    // exclusive scan of (sp, sa) over the 256 threads: within each wave by
+    // shuffles, then the four wave totals
+    const int lane = tid & 63, wv = tid >> 6;
+    int ip = sp, ia = sa;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int tp = __shfl_up(ip, o), ta = __shfl_up(ia, o);
+        if (lane >= o) {
+            ip += tp;
+            ia += ta;
+        }
+    }
+    if (lane == 63) {
+        part[wv] = ip;
+        part[256 + wv] = ia;
+    }
+    __syncthreads();
+    int rp = ip - sp, ra = ia - sa;
+    for (int w = 0; w < wv; ++w) {
+        rp += part[w];
+        ra += part[256 + w];
+    }
+    if (tid == 255) *r.n_act = ra + sa;
+    for (int e = e0; e < e1; ++e) {
+        pos[e] = rp;
+        if (cnt[e] > 0) {
+            r.act[ra] = e;
+            r.act_off[ra] = rp;
+            r.act_cnt[ra] = cnt[e];
+            ++ra;
+        }
+        rp += cnt[e];
+    }
+    __syncthreads();
+    for (int base = 0; base < n_pairs; base += ROUTE_CHUNK) {
+        const int n = min(ROUTE_CHUNK, n_pairs - base);
+        for (int i = tid; i < n; i += 256) idl[i] = ids[base + i];
+        __syncthreads();
+        for (int i = tid; i < n; i += 256) {
+            const int e = idl[i];
+            if (e >= 0 && e < E) r.pairs[atomicAdd(&pos[e], 1)] = base + i;
+        }
+        __syncthreads();
+    }
+}
+
 __global__ __launch_bounds__(256) void moe_route_kernel(const int32_t* __restrict__ ids, int n_pairs, int E,
                                                         MoeRoute r) {
-    extern __shared__ int sh[];   // cnt[E], off[E]
-    int* cnt = sh;
-    int* off = sh + E;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        int c = 0;
-        for (int i = 0; i < n_pairs; ++i) c += (ids[i] == e);
-        cnt[e] = c;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0, act = 0;
-        for (int e = 0; e < E; ++e) {
-            off[e] = run;
-            run += cnt[e];
-            if (cnt[e] > 0) {
-                r.act[act] = e;
-                r.act_off[act] = off[e];
-                r.act_cnt[act] = cnt[e];
-                ++act;
-            }
-        }
-        *r.n_act = act;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        if (cnt[e] == 0) continue;
-        int p = off[e];
-        for (int i = 0; i < n_pairs; ++i)
-            if (ids[i] == e) r.pairs[p++] = i;
-    }
+    extern __shared__ int sh[];
+    route_block(ids, n_pairs, E, r, sh);
 }
 
 template <int TC, int BPR, int WAVES, int U>
@@ -355,7 +410,7 @@ hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, 
 
 // ---------------------------------------------------------------------------
 hipError_t launch_moe_route(const int32_t* ids, int n_pairs, int E, const MoeRoute& r, hipStream_t st) {
-    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), (size_t)2 * E * sizeof(int), st, ids, n_pairs, E, r);
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), moe_route_lds_bytes(E), st, ids, n_pairs, E, r);
     return hipGetLastError();
 }
 
@@ -386,6 +441,144 @@ hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStr
         case 8: return launch_moe_t<8>(p, bpr, grid, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+
+// Matrix-core form for batches whose experts receive several pairs.
+//   moe_prep_kernel: workgroup 0 builds the routing tables (route_block), the
+//   others quantise the input rows into permuted Q8_K planes.
+//   moe_ring_kernel: workgroup (a, g) takes active expert a and its 128-row
+//   tiles g*ring_rt .. +ring_rt; the expert's pairs are gathered 16 at a time
+//   as the tokens of the LDS ring of gemm_ring_kernel (eight waves, one
+//   16-row tile each, direct global -> LDS loads S - 1 super-blocks ahead)
+//   and the row tiles follow each other in one stream, so the ring stays full
+//   across them; each pair's outputs are scattered to Y[pair].
+__global__ __launch_bounds__(256) void moe_prep_kernel(const int32_t* __restrict__ ids, int n_pairs, int E,
+                                                       MoeRoute r, const float* __restrict__ x, int64_t x_tstride,
+                                                       int n_xrows, int nb, Q8Planes Q) {
+    extern __shared__ int sh[];
+    if (blockIdx.x == 0) {
+        route_block(ids, n_pairs, E, r, sh);
+        return;
+    }
+    quantize_planes_items(x, x_tstride, n_xrows, nb, const_cast<int8_t*>(Q.qs), const_cast<int16_t*>(Q.bs),
+                          const_cast<float*>(Q.d), const_cast<uint8_t*>(Q.mn), 1, blockIdx.x - 1);
+}
+
+template <int S>
+__global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
+    constexpr int NW = 8, ROWS = 128, TOK = 16;
+    constexpr int W_SLOTS = ROWS * 9, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
+    constexpr int W_LOADS = W_SLOTS / 64, Q_LOADS = (Q_SLOTS + 63) / 64, M_LOADS = (M_SLOTS + 63) / 64;
+    constexpr int NLOAD = W_LOADS + Q_LOADS + M_LOADS;
+    constexpr int NPW = (NLOAD + NW - 1) / NW;
+    constexpr int STAGE = NPW * NW * 1024;
+    constexpr int Q_OFF = W_LOADS * 1024, M_OFF = Q_OFF + Q_LOADS * 1024;
+    __shared__ __align__(1024) uint8_t lds[S][STAGE];
+
+    const int a = blockIdx.x / p.tiles_per_expert;
+    const int g = blockIdx.x - a * p.tiles_per_expert;
+    if (a >= *p.route.n_act) return;           // uniform over the workgroup
+    const int e = p.route.act[a];
+    const int poff = p.route.act_off[a];
+    const int pcnt = p.route.act_cnt[a];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c16 = lane & 15;
+    const int q = lane >> 4;
+    const int M = p.M, nb = p.nb;
+    const int rt0 = g * p.ring_rt;
+    const int nrt = min(p.ring_rt, (M + ROWS - 1) / ROWS - rt0);
+    const int len = nrt * nb;                  // super-blocks streamed per token tile
+    const uint8_t* __restrict__ W = p.bank + (size_t)e * p.expert_bytes;
+    const size_t row_bytes = (size_t)nb * Q4K_BYTES;
+
+    for (int tile0 = 0; tile0 < pcnt; tile0 += TOK) {
+        // per load: weight slot (row within the tile, 16-byte chunk), or the
+        // activation source of super-block 0 and its stride
+        const uint8_t* src[NPW];
+        uint32_t stride[NPW];
+        int wrow[NPW];
+#pragma unroll
+        for (int i = 0; i < NPW; ++i) {
+            const int J = NW * i + wave;
+            const int slot = J * 64 + lane;
+            src[i] = p.Q.mn;                   // surplus and padding: any valid address
+            stride[i] = 0;
+            wrow[i] = -1;
+            if (J < W_LOADS) {
+                wrow[i] = slot / 9;
+                src[i] = W + 16 * (slot % 9);
+            } else if (J < NLOAD) {
+                const bool isq = J < W_LOADS + Q_LOADS;
+                const int sl = slot - (isq ? W_LOADS : W_LOADS + Q_LOADS) * 64;
+                const int per = isq ? 17 : 3;
+                if (sl < TOK * per) {
+                    const int pid = p.route.pairs[poff + min(tile0 + sl / per, pcnt - 1)];
+                    const int xr = p.ne11 == 1 ? pid / p.n_used : pid;   // input row of the pair
+                    if (isq) {
+                        src[i] = reinterpret_cast<const uint8_t*>(p.Q.qs) + (size_t)xr * nb * 256 + 16 * min(sl % 17, 15);
+                        stride[i] = 256;
+                    } else {
+                        src[i] = p.Q.mn + (size_t)xr * nb * Q8MN_BYTES + 16 * (sl % 3);
+                        stride[i] = Q8MN_BYTES;
+                    }
+                }
+            }
+        }
+        auto issue = [&](int sp, int buf) {
+            const int rt = rt0 + sp / nb, b = sp - (sp / nb) * nb;
+#pragma unroll
+            for (int i = 0; i < NPW; ++i) {
+                const uint8_t* a_ = (NW * i + wave) < W_LOADS
+                                        ? src[i] + (size_t)min(rt * ROWS + wrow[i], M - 1) * row_bytes + (size_t)b * Q4K_BYTES
+                                        : src[i] + (size_t)b * stride[i];
+                __builtin_amdgcn_global_load_lds(
+                    (const void*)a_, (__attribute__((address_space(3))) void*)(lds[buf] + (NW * i + wave) * 1024), 16, 0, 0);
+            }
+        };
+        v4f acc[1][1] = {{v4f{0, 0, 0, 0}}};
+        // the previous token tile's readers are done with every buffer
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < S - 1; ++k) issue(min(k, len - 1), k);
+        for (int sp = 0; sp < len; ++sp) {
+            const int buf = sp % S;
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * NPW) : "memory");
+            issue(min(sp + S - 1, len - 1), (sp + S - 1) % S);
+            ring_block<1, 1>(lds[buf] + (wave * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+            if (sp - (sp / nb) * nb == nb - 1) {
+                // row tile done: lane has rows 4q .. 4q+3 of the wave's 16, pair tile0 + c16
+                if (tile0 + c16 < pcnt) {
+                    const int pid = p.route.pairs[poff + tile0 + c16];
+                    const int rq = (rt0 + sp / nb) * ROWS + wave * 16 + 4 * q;
+                    float* y = p.Y + (int64_t)pid * M + rq;
+                    if ((M & 3) == 0 && rq + 3 < M) {
+                        *reinterpret_cast<v4f*>(y) = acc[0][0];
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (rq + i < M) y[i] = acc[0][0][i];
+                    }
+                }
+                acc[0][0] = v4f{0, 0, 0, 0};
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+}
+
+hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, int E, const float* X,
+                           int64_t x_tstride, int n_xrows, int max_act, hipStream_t st) {
+    const int64_t items = (int64_t)n_xrows * p.nb;
+    hipLaunchKernelGGL(moe_prep_kernel, dim3((unsigned)(1 + (items + 15) / 16)), dim3(256), moe_route_lds_bytes(E), st,
+                       ids, n_pairs, E, p.route, X, x_tstride, n_xrows, p.nb, p.Q);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t grid = (int64_t)max_act * p.tiles_per_expert;
+    hipLaunchKernelGGL(moe_ring_kernel<3>, dim3((unsigned)grid), dim3(512), 0, st, p);
+    return hipGetLastError();
 }
 
 }  // namespace spq4k

@@ -57,6 +57,7 @@ struct MoeRoute {
 
 struct MoeParams {
     MoeRoute route;
+    int32_t ring_rt;         // moe_ring_kernel: 128-row tiles a workgroup streams (tiles_per_expert = groups)
     const uint8_t* bank;     // E experts of [M][nb] Q4_K blocks
     size_t expert_bytes;
     float* Y;                // [T][n_used][M]
@@ -91,6 +92,11 @@ bool moe_decode_supported(int nb);
 int moe_decode_rows_per_wg(int nb);
 hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st);
 hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st);
+// matrix-core form: moe_prep_kernel (routing in workgroup 0, permuted Q8_K
+// planes of the n_xrows input rows X in the others), then the ring kernel
+// over max_act experts x p.tiles_per_expert groups of p.ring_rt row tiles
+hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, int E, const float* X,
+                           int64_t x_tstride, int n_xrows, int max_act, hipStream_t st);
 
 // prefill matmul on matrix cores (k_gemm.hip)
 constexpr int GEMM_MAX_SEG = 4;

@@ -64,14 +64,22 @@ def test_moe_30b_shapes(ctx, oracle, M, K, T, ne11):
     _check(got, exp, f"moe M={M} K={K} T={T} ne11={ne11}")
 
 
-def test_moe_many_tokens_per_expert(ctx, oracle):
-    # every token picks the same 8 experts: 32 pairs per expert, several TC chunks
+@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 3}])
+def test_moe_many_tokens_per_expert(oracle, env):
+    # every token picks the same 8 experts: 32 pairs per expert, two 16-pair
+    # tiles of the ring kernel (several TC chunks of the sdot4 kernel)
+    from _envctx import context_with
+    ctx = context_with(env)
     E, M, K, T, k = 16, 256, 1024, 32, 8
     rng = np.random.default_rng(77)
     bank, host = _gpu_bank(ctx, E, M, K, seed=5)
     ids = np.tile(np.array([3, 1, 4, 15, 9, 2, 6, 5], np.int32), (T, 1))
     X = rng.standard_normal((T, k, K)).astype(np.float32)
-    _check(ctx.mul_mat_id(bank, X, ids), oracle.mul_mat_id(host, M, K, E, X, ids), "moe shared experts")
+    try:
+        _check(ctx.mul_mat_id(bank, X, ids), oracle.mul_mat_id(host, M, K, E, X, ids), f"moe shared experts {env}")
+    finally:
+        bank.free()
+        ctx.close()
 
 
 def test_moe_rejects_bad_ids(ctx):
@@ -84,17 +92,18 @@ def test_moe_rejects_bad_ids(ctx):
 
 
 @pytest.mark.parametrize("T,ne11,M,K", [(1, 1, 768, 2048), (1, 8, 2048, 768), (3, 8, 2048, 768), (4, 1, 512, 4096),
-                                        (5, 8, 2048, 768), (32, 1, 768, 2048)])
+                                        (5, 8, 2048, 768), (32, 1, 768, 2048), (33, 8, 200, 1280)])
 def test_moe_paths_agree(oracle, T, ne11, M, K):
-    """Every MoE path against the oracle: the planner's choice, the grouped
-    single-launch kernel (SPQ4K_MOE_MODE=2) and the three-launch path
-    (routing pass, Q8_K planes, matvec)."""
+    """Every MoE path against the oracle: the planner's choice, the matrix-core
+    path at any batch (SPQ4K_MOE_MODE=2: routing pass, Q8_K planes, ring
+    kernel), the single-launch sdot4 kernel (=3) and the three-launch sdot4
+    path (SPQ4K_MOE_UNFUSED)."""
     from _envctx import context_with
     E, k = 128, 8
     ids = _topk_ids(np.random.default_rng(T), T, E, k)
     X = np.random.default_rng(T + 1).standard_normal((T, ne11, K)).astype(np.float32)
     outs, host = [], None
-    for env in ({}, {"SPQ4K_MOE_MODE": 2}, {"SPQ4K_MOE_UNFUSED": 1}):
+    for env in ({}, {"SPQ4K_MOE_MODE": 2}, {"SPQ4K_MOE_MODE": 3}, {"SPQ4K_MOE_UNFUSED": 1}):
         c = context_with(env)
         try:
             bank, host = _gpu_bank(c, E, M, K, 71)
@@ -107,7 +116,7 @@ def test_moe_paths_agree(oracle, T, ne11, M, K):
         _check(got, exp, f"{env} T={T} ne11={ne11} M={M} K={K}")
 
 
-@pytest.mark.parametrize("mode", [0, 2])
+@pytest.mark.parametrize("mode", [0, 2, 3])
 def test_moe_device_ids_out_of_range_leave_outputs(oracle, mode):
     """Device-pointer entry point: an id outside [0, E) is not routed, so its
     output rows keep their previous contents (the host entry point rejects it)."""
