@@ -3,6 +3,12 @@
     python -m spq4k.rocprof_summary --trace DIR --fetch DIR --write DIR \
         --fetch-copy DIR --write-copy DIR --out profiles/NAME.md --json profiles/NAME.json
 
+    python -m spq4k.rocprof_summary --stats DIR --out profiles/NAME.md --title T --command CMD
+
+The second form turns the kernel_stats.csv of a `rocprofv3 --kernel-trace
+--stats --output-format csv` run into a per-kernel table (calls, average,
+minimum and maximum duration, share of GPU time).
+
 --trace holds a `rocprofv3 --kernel-trace --stats --output-format csv` run of
 `bench.py --no-cpu` (decode8b); --fetch / --write hold `--pmc FETCH_SIZE` /
 `--pmc WRITE_SIZE` runs of the same command; --fetch-copy / --write-copy the
@@ -38,7 +44,8 @@ def alg_bytes(stage):
 
 
 def _csv(d, suffix):
-    files = glob.glob(os.path.join(d, f"*{suffix}"))
+    files = glob.glob(os.path.join(d, f"*{suffix}")) or glob.glob(os.path.join(d, "**", f"*{suffix}"),
+                                                                 recursive=True)
     if not files:
         raise FileNotFoundError(f"no *{suffix} in {d}")
     with open(files[0]) as f:
@@ -72,7 +79,48 @@ def _copy_factor(d):
     return COPY_BYTES / statistics.median(vals), statistics.median(vals)
 
 
+def stats_table(d, out, title, commands):
+    """Per (kernel, grid) launch statistics from the kernel trace, in order of
+    first dispatch (the trace keeps launches of one kernel at different sizes
+    apart, which the stats file merges)."""
+    trace = _csv(d, "kernel_trace.csv")
+    key_id = "Dispatch_Id" if "Dispatch_Id" in trace[0] else "Start_Timestamp"
+    trace.sort(key=lambda r: int(r[key_id]))
+    groups = {}
+    for r in trace:
+        k = (r["Kernel_Name"], r.get("Grid_Size", r.get("Grid_Size_X", "")), r.get("Workgroup_Size",
+                                                                                   r.get("Workgroup_Size_X", "")))
+        groups.setdefault(k, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    total = sum(sum(v) for v in groups.values())
+    with open(out, "w") as f:
+        f.write(f"# {title}\n\nCommands (from the repository root on the GPU box):\n\n```\n")
+        for c in commands:
+            f.write(c + "\n")
+        f.write("```\n\nPer kernel and grid (threads), in order of first launch: durations from the kernel trace.\n\n"
+                "| kernel | grid | wg | launches | avg us | min us | max us | % of GPU time |\n"
+                "|---|---|---|---|---|---|---|---|\n")
+        for (name, grid, wg), v in groups.items():
+            name = name.replace("spq4k::", "").replace("(spq4k::GemmParams)", "").replace(
+                "(spq4k::MoeParams)", "").replace("(spq4k::MoeFusedParams)", "").replace("(spq4k::GemvParams)", "")
+            if "(" in name:
+                name = name[:name.index("(")]
+            f.write(f"| `{name}` | {grid} | {wg} | {len(v)} | {statistics.mean(v):.2f} | {min(v):.2f} | "
+                    f"{max(v):.2f} | {100 * sum(v) / total:.1f} |\n")
+    print(open(out).read())
+
+
 def main(argv=None):
+    if argv is None:
+        argv = sys.argv[1:]
+    if "--stats" in argv:
+        ap = argparse.ArgumentParser()
+        ap.add_argument("--stats", required=True)
+        ap.add_argument("--out", required=True)
+        ap.add_argument("--title", required=True)
+        ap.add_argument("--command", action="append", default=[])
+        a = ap.parse_args(argv)
+        stats_table(a.stats, a.out, a.title, a.command)
+        return 0
     ap = argparse.ArgumentParser()
     for a in ("trace", "fetch", "write", "fetch_copy", "write_copy", "out", "json"):
         ap.add_argument("--" + a.replace("_", "-"), required=True)
