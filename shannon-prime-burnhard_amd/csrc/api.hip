@@ -154,9 +154,12 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
 //   K = 4096,  larger M    : 12 waves, 2 rows in flight, x-first (lm_head)
 //   K = 12288              : 16 waves, x-first: 48 KB of x per CU would
 //                            otherwise queue behind the CU's weight loads
+//   K = 27648              : 8 waves (the registers of 7 Q8_K blocks a lane), x-first
 DecodeCfg plan_decode(const spq4k_ctx* c, int nb, int64_t rows) {
     DecodeCfg d;
-    if (nb >= 48) {
+    if (nb > 48) {
+        d.waves = 8; d.depth = 1; d.xfirst = true;
+    } else if (nb >= 48) {
         d.waves = 16; d.depth = 1; d.xfirst = true;
     } else if (rows <= 4096) {
         d.waves = 16; d.depth = 1; d.xfirst = true;
@@ -171,8 +174,12 @@ DecodeCfg plan_decode(const spq4k_ctx* c, int nb, int64_t rows) {
     if (c->dec_force.depth) d.depth = c->dec_force.depth;
     if (c->dec_xfirst_set) d.xfirst = c->dec_force.xfirst;
     // K = 12288 with two rows in flight needs more than the 128 registers a
-    // 16-wave workgroup allows: one row in flight
+    // 16-wave workgroup allows: one row in flight; K = 27648 runs 8 waves, one row
     if (nb >= 48 && d.waves == 16) d.depth = 1;
+    if (nb > 48) {
+        d.waves = 8;
+        d.depth = 1;
+    }
     const int64_t wgs = (rows + d.waves - 1) / d.waves;
     d.grid = (int)(wgs < c->num_cus ? wgs : c->num_cus);
     if (c->dec_force.grid) d.grid = c->dec_force.grid;

@@ -274,10 +274,17 @@ static hipError_t launch_dec(const GemvParams& p, int grid, hipStream_t st) {
     return hipGetLastError();
 }
 
+// launch shapes that fit the register file: K = 12288 with two rows in flight
+// needs more than a 16-wave workgroup's 128 VGPRs; K = 27648 keeps 7 blocks of
+// Q8_K per lane (133 VGPRs) and fits 8-wave workgroups with one row in flight
+constexpr bool dec_shape_ok(int nb, int waves, int depth) {
+    return !(nb >= 48 && waves == 16 && depth == 2) && !(nb > 48 && (waves > 8 || depth > 1));
+}
+
 template <int NB>
 static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
 #define SPQ_DEC(W, DD, X)                                                                  \
-    if constexpr (!(NB >= 48 && W == 16 && DD == 2))                                       \
+    if constexpr (dec_shape_ok(NB, W, DD))                                                 \
         if (c.waves == W && c.depth == DD && c.xfirst == X) return launch_dec<NB, W, DD, X>(p, c.grid, st);
     SPQ_DEC(16, 1, false) SPQ_DEC(16, 1, true) SPQ_DEC(16, 2, false) SPQ_DEC(16, 2, true)
     SPQ_DEC(12, 1, false) SPQ_DEC(12, 1, true) SPQ_DEC(12, 2, false) SPQ_DEC(12, 2, true)
@@ -286,11 +293,15 @@ static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStre
     return hipErrorInvalidValue;
 }
 
-bool decode_supported(int nb) { return nb == 16 || nb == 48; }
+// K = 4096, 5120, 12288, 27648: the dense shapes of the 8B model and of the
+// large-K configuration
+bool decode_supported(int nb) { return nb == 16 || nb == 20 || nb == 48 || nb == 108; }
 
 hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
     if (p.nb == 16) return launch_dec_nb<16>(p, c, st);
+    if (p.nb == 20) return launch_dec_nb<20>(p, c, st);
     if (p.nb == 48) return launch_dec_nb<48>(p, c, st);
+    if (p.nb == 108) return launch_dec_nb<108>(p, c, st);
     return hipErrorInvalidValue;
 }
 

@@ -1,8 +1,8 @@
 """GPU parity of the T = 1 decode GEMV (gemv_decode_kernel) and of every launch
 shape the planner can pick, against the CPU oracle.
 
-The decode kernel serves K = 4096 and K = 12288 (the 8B shapes); the generic
-kernel serves every other K and T <= 8. Launch shapes are forced through the
+The decode kernel serves K = 4096, 5120, 12288 and 27648 (the 8B and large-K
+shapes); the generic kernel serves every other K at T = 1, and T = 2, 3. Launch shapes are forced through the
 context's environment overrides (read when a context is created), so each
 (waves, depth, x-first) instantiation and each lanes-per-row choice of the
 generic kernel is checked, not only the ones the planner picks for the sizes
@@ -31,7 +31,8 @@ def _check(got, exp, what):
                              f"got {got[tuple(i)]!r} exp {exp[tuple(i)]!r}")
 
 
-@pytest.mark.parametrize("M,K", [(1, 4096), (100, 4096), (4096, 4096), (37, 12288), (4096, 12288)])
+@pytest.mark.parametrize("M,K", [(1, 4096), (100, 4096), (4096, 4096), (37, 12288), (4096, 12288), (300, 5120),
+                                 (3000, 5120), (5, 27648), (700, 27648)])
 def test_decode_single(ctx, oracle, M, K):
     rng = np.random.default_rng(M * 7 + K)
     W = _weights(oracle, rng, M, K)
@@ -63,9 +64,10 @@ _CFGS = [(w, d, xf) for w in (8, 12, 16) for d in (1, 2) for xf in (0, 1)]
 @pytest.mark.parametrize("waves,depth,xfirst", _CFGS)
 def test_decode_launch_shapes(oracle, waves, depth, xfirst):
     """Every compiled instantiation, with a small grid so that each wave walks
-    several rows (the depth pipeline and its ragged tail) and a full grid."""
+    several rows (the depth pipeline and its ragged tail) and a full grid
+    (K = 27648 runs 8 waves and one row in flight whatever is asked)."""
     rng = np.random.default_rng(1000 + waves * 10 + depth * 2 + xfirst)
-    cases = [(1000, 4096), (333, 12288)]
+    cases = [(1000, 4096), (333, 12288), (210, 5120), (77, 27648)]
     data = [(M, K, _weights(oracle, rng, M, K), rng.standard_normal((1, K)).astype(np.float32)) for M, K in cases]
     for grid in (3, 0):
         env = {"SPQ4K_DEC_WAVES": waves, "SPQ4K_DEC_DEPTH": depth, "SPQ4K_DEC_XFIRST": xfirst}
