@@ -1,0 +1,55 @@
+/* spq4k_ggml.h — ggml graph nodes that run Q4_K matmuls through spq4k.
+ *
+ * The engine adapter for the reference's graph builders: a Q4_K weight's
+ * GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID node is replaced by a ggml custom op
+ * (ggml_custom_4d, ggml.h:2610-2623) whose callback runs the product on the
+ * GPU through spq4k. This is the custom-op pattern the engine already uses for
+ * its fp32 CRT matmul (sp_crt_mul_mat, desktop/engine/src/forward.cpp:1266-1281,
+ * whose Q4_K branch is the TODO at :1270-1273) and for BURN_MOE
+ * (burn_moe_op.cpp:377-430): the callback works on ith == 0 only
+ * (forward.cpp:1248, burn_moe_op.cpp:203) and moves tensors with
+ * ggml_backend_tensor_get / _set, or through tensor->data for tensors that
+ * live in a plain ggml context.
+ *
+ * Weights are uploaded to the GPU the first time a weight tensor is seen and
+ * stay resident (keyed by tensor and data pointer); activations and outputs
+ * cross PCIe per call. Built against the host engine's ggml.h.
+ */
+#ifndef SPQ4K_GGML_H
+#define SPQ4K_GGML_H
+
+#include "ggml.h"
+#include "spq4k.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct spq4k_ggml spq4k_ggml;
+
+/* Create a binding on `device` (an spq4k context plus the resident-weight
+ * table). Returns 0 or a negative errno (spq4k_init's codes). */
+int spq4k_ggml_init(int device, spq4k_ggml **out);
+void spq4k_ggml_free(spq4k_ggml *b);
+
+/* GGML_OP_MUL_MAT (ggml_mul_mat, ggml.h:1414-1420) for a Q4_K weight:
+ * W [K, M] Q4_K, x [K, T] f32 contiguous (ne2 = ne3 = 1) -> [M, T] f32. */
+struct ggml_tensor *spq4k_ggml_mul_mat(struct ggml_context *ctx, struct ggml_tensor *W, struct ggml_tensor *x,
+                                       spq4k_ggml *b);
+
+/* GGML_OP_MUL_MAT_ID (ggml_mul_mat_id, ggml.h:1434-1438) for a Q4_K expert
+ * bank: as [K, M, E] Q4_K, x [K, ne11, T] f32 (ne11 = 1 or n_used), ids
+ * [n_used, T] i32 -> [M, n_used, T] f32. */
+struct ggml_tensor *spq4k_ggml_mul_mat_id(struct ggml_context *ctx, struct ggml_tensor *as, struct ggml_tensor *x,
+                                          struct ggml_tensor *ids, spq4k_ggml *b);
+
+/* Custom-op callbacks return nothing: the first failure is kept here (0 when
+ * every node succeeded) and the failed node's output is filled with NaN. */
+int spq4k_ggml_status(const spq4k_ggml *b);
+const char *spq4k_ggml_last_error(const spq4k_ggml *b);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPQ4K_GGML_H */

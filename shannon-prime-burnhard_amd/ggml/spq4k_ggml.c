@@ -1,0 +1,204 @@
+/* spq4k_ggml.c — ggml custom-op nodes for Q4_K GGML_OP_MUL_MAT /
+ * GGML_OP_MUL_MAT_ID, run on the GPU through spq4k (include/spq4k_ggml.h).
+ *
+ * The node is ggml_custom_4d (ggml.h:2610-2623) with the weight, the
+ * activations (and ids) as sources, one task, and the binding as userdata.
+ * Its callback:
+ *   - does all the work on ith == 0, as the engine's own custom ops do
+ *     (desktop/engine/src/forward.cpp:1248, burn_moe_op.cpp:203);
+ *   - finds the weight in the resident table, uploading it on first use
+ *     (spq4k_weights_upload), keyed by tensor and data pointer so that a
+ *     buffer reused for other bytes is uploaded again;
+ *   - reads activations and ids, and writes the output, through
+ *     ggml_backend_tensor_get / _set when the tensor has a backend buffer and
+ *     through tensor->data otherwise;
+ *   - runs spq4k_mul_mat_host / spq4k_moe_host (GGML_OP_MUL_MAT: y[t][m] =
+ *     W[m] . x[t]; GGML_OP_MUL_MAT_ID with the CPU driver's semantics,
+ *     ggml-cpu.c:1521-1690).
+ * A failure is recorded in the binding and the node's output is NaN.
+ */
+#include "spq4k_ggml.h"
+
+#include <errno.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "ggml-backend.h"
+
+struct resident {
+    const struct ggml_tensor *t;
+    const void *data;
+    size_t nbytes;
+    spq4k_weights *w;
+};
+
+struct spq4k_ggml {
+    spq4k_ctx *ctx;
+    struct resident *res;
+    int nres, cap;
+    int status;
+    char err[256];
+};
+
+int spq4k_ggml_init(int device, spq4k_ggml **out) {
+    if (!out) return -EINVAL;
+    *out = NULL;
+    spq4k_ggml *b = (spq4k_ggml *)calloc(1, sizeof *b);
+    if (!b) return -ENOMEM;
+    int rc = spq4k_init(device, &b->ctx);
+    if (rc) {
+        free(b);
+        return rc;
+    }
+    *out = b;
+    return 0;
+}
+
+void spq4k_ggml_free(spq4k_ggml *b) {
+    if (!b) return;
+    for (int i = 0; i < b->nres; ++i) spq4k_weights_free(b->res[i].w);
+    free(b->res);
+    spq4k_free(b->ctx);
+    free(b);
+}
+
+int spq4k_ggml_status(const spq4k_ggml *b) { return b ? b->status : -EINVAL; }
+
+const char *spq4k_ggml_last_error(const spq4k_ggml *b) { return b ? b->err : "null binding"; }
+
+static void fail(spq4k_ggml *b, struct ggml_tensor *dst, int code, const char *what) {
+    if (b->status == 0) {
+        b->status = code;
+        snprintf(b->err, sizeof b->err, "%s: %s", what, code == -EIO ? spq4k_last_error(b->ctx) : strerror(-code));
+    }
+    const size_t n = (size_t)ggml_nelements(dst);
+    float *nan = (float *)malloc(n * sizeof(float));
+    if (!nan) return;
+    for (size_t i = 0; i < n; ++i) nan[i] = NAN;
+    if (dst->buffer)
+        ggml_backend_tensor_set(dst, nan, 0, n * sizeof(float));
+    else
+        memcpy(dst->data, nan, n * sizeof(float));
+    free(nan);
+}
+
+/* tensor bytes in host memory: the tensor's own when it has no backend
+ * buffer (*owned = 0), else a copy (*owned = 1) */
+static void *host_bytes(const struct ggml_tensor *t, int *owned) {
+    const size_t n = ggml_nbytes(t);
+    if (!t->buffer) {
+        *owned = 0;
+        return t->data;
+    }
+    void *p = malloc(n);
+    if (p) ggml_backend_tensor_get(t, p, 0, n);
+    *owned = 1;
+    return p;
+}
+
+static int resident_weight(spq4k_ggml *b, const struct ggml_tensor *W, int64_t M, int64_t K, int64_t E,
+                           spq4k_weights **out) {
+    const size_t nbytes = ggml_nbytes(W);
+    for (int i = 0; i < b->nres; ++i) {
+        if (b->res[i].t == W && b->res[i].data == W->data && b->res[i].nbytes == nbytes) {
+            *out = b->res[i].w;
+            return 0;
+        }
+    }
+    if (b->nres == b->cap) {
+        const int cap = b->cap ? 2 * b->cap : 64;
+        struct resident *r = (struct resident *)realloc(b->res, (size_t)cap * sizeof *r);
+        if (!r) return -ENOMEM;
+        b->res = r;
+        b->cap = cap;
+    }
+    int owned;
+    void *bytes = host_bytes(W, &owned);
+    if (!bytes) return -ENOMEM;
+    spq4k_weights *w = NULL;
+    const int rc = spq4k_weights_upload(b->ctx, bytes, M, K, E, &w);
+    if (owned) free(bytes);
+    if (rc) return rc;
+    b->res[b->nres++] = (struct resident){W, W->data, nbytes, w};
+    *out = w;
+    return 0;
+}
+
+static void run_mul_mat(struct ggml_tensor *dst, int ith, int nth, void *userdata) {
+    (void)nth;
+    if (ith != 0) return;
+    spq4k_ggml *b = (spq4k_ggml *)userdata;
+    const struct ggml_tensor *W = dst->src[0], *x = dst->src[1];
+    const int64_t K = W->ne[0], M = W->ne[1], T = x->ne[1];
+    spq4k_weights *w;
+    int rc = resident_weight(b, W, M, K, 1, &w);
+    if (rc) {
+        fail(b, dst, rc, "spq4k_ggml_mul_mat: weight upload");
+        return;
+    }
+    int ox, oy = 0;
+    const float *X = (const float *)host_bytes(x, &ox);
+    float *Y = dst->buffer ? (float *)malloc((size_t)M * T * sizeof(float)) : (float *)dst->data;
+    if (dst->buffer) oy = 1;
+    if (!X || !Y) {
+        if (ox) free((void *)X);
+        if (oy) free(Y);
+        fail(b, dst, -ENOMEM, "spq4k_ggml_mul_mat");
+        return;
+    }
+    rc = spq4k_mul_mat_host(b->ctx, w, X, Y, T);
+    if (rc == 0 && oy) ggml_backend_tensor_set(dst, Y, 0, (size_t)M * T * sizeof(float));
+    if (ox) free((void *)X);
+    if (oy) free(Y);
+    if (rc) fail(b, dst, rc, "spq4k_ggml_mul_mat");
+}
+
+static void run_mul_mat_id(struct ggml_tensor *dst, int ith, int nth, void *userdata) {
+    (void)nth;
+    if (ith != 0) return;
+    spq4k_ggml *b = (spq4k_ggml *)userdata;
+    const struct ggml_tensor *as = dst->src[0], *x = dst->src[1], *ids = dst->src[2];
+    const int64_t K = as->ne[0], M = as->ne[1], E = as->ne[2];
+    const int64_t ne11 = x->ne[1], T = x->ne[2], n_used = ids->ne[0];
+    spq4k_weights *w;
+    int rc = resident_weight(b, as, M, K, E, &w);
+    if (rc) {
+        fail(b, dst, rc, "spq4k_ggml_mul_mat_id: weight upload");
+        return;
+    }
+    int ox, oi, oy = 0;
+    const float *X = (const float *)host_bytes(x, &ox);
+    const int32_t *I = (const int32_t *)host_bytes(ids, &oi);
+    float *Y = dst->buffer ? (float *)malloc((size_t)M * n_used * T * sizeof(float)) : (float *)dst->data;
+    if (dst->buffer) oy = 1;
+    if (X && I && Y) rc = spq4k_moe_host(b->ctx, w, I, n_used, ne11, T, X, Y);
+    else rc = -ENOMEM;
+    if (rc == 0 && oy) ggml_backend_tensor_set(dst, Y, 0, (size_t)M * n_used * T * sizeof(float));
+    if (ox) free((void *)X);
+    if (oi) free((void *)I);
+    if (oy) free(Y);
+    if (rc) fail(b, dst, rc, "spq4k_ggml_mul_mat_id");
+}
+
+struct ggml_tensor *spq4k_ggml_mul_mat(struct ggml_context *ctx, struct ggml_tensor *W, struct ggml_tensor *x,
+                                       spq4k_ggml *b) {
+    if (!ctx || !W || !x || !b || W->type != GGML_TYPE_Q4_K || x->type != GGML_TYPE_F32 || x->ne[0] != W->ne[0] ||
+        W->ne[2] != 1 || W->ne[3] != 1 || x->ne[2] != 1 || x->ne[3] != 1 || !ggml_is_contiguous(W) ||
+        !ggml_is_contiguous(x))
+        return NULL;
+    struct ggml_tensor *args[2] = {W, x};
+    return ggml_custom_4d(ctx, GGML_TYPE_F32, W->ne[1], x->ne[1], 1, 1, args, 2, run_mul_mat, 1, b);
+}
+
+struct ggml_tensor *spq4k_ggml_mul_mat_id(struct ggml_context *ctx, struct ggml_tensor *as, struct ggml_tensor *x,
+                                          struct ggml_tensor *ids, spq4k_ggml *b) {
+    if (!ctx || !as || !x || !ids || !b || as->type != GGML_TYPE_Q4_K || x->type != GGML_TYPE_F32 ||
+        ids->type != GGML_TYPE_I32 || x->ne[0] != as->ne[0] || ids->ne[1] != x->ne[2] ||
+        (x->ne[1] != 1 && x->ne[1] != ids->ne[0]) || as->ne[3] != 1 || x->ne[3] != 1 || !ggml_is_contiguous(as) ||
+        !ggml_is_contiguous(x) || !ggml_is_contiguous(ids))
+        return NULL;
+    struct ggml_tensor *args[3] = {as, x, ids};
+    return ggml_custom_4d(ctx, GGML_TYPE_F32, as->ne[1], ids->ne[0], ids->ne[1], 1, args, 3, run_mul_mat_id, 1, b);
+}

@@ -1,0 +1,162 @@
+/* ggml_adapter_check.c — test driver for the ggml adapter (include/spq4k_ggml.h).
+ *
+ * Test infrastructure: builds the same ggml graph twice in one context of the
+ * reference's own ggml (compiled from its sources into oracle/_ref) — once with
+ * ggml's GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID nodes, once with the adapter's
+ * spq4k nodes — computes it on the CPU with ggml_graph_compute_with_ctx and
+ * returns both outputs; the Python test compares them with close_enough.
+ * Weights are seeded N(0, 0.02) quantised by ggml_quantize_chunk (Q4_K),
+ * activations seeded N(0, 1).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "ggml-cpu.h"
+#include "ggml.h"
+#include "spq4k_ggml.h"
+
+static uint64_t splitmix(uint64_t *s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static void normal_fill(float *p, int64_t n, uint64_t seed, float std) {
+    uint64_t s = seed;
+    for (int64_t i = 0; i < n; i += 2) {
+        const double u1 = ((splitmix(&s) >> 11) + 1.0) * (1.0 / 9007199254740993.0);
+        const double u2 = (splitmix(&s) >> 11) * (1.0 / 9007199254740992.0);
+        const double r = sqrt(-2.0 * log(u1));
+        p[i] = (float)(std * r * cos(6.283185307179586 * u2));
+        if (i + 1 < n) p[i + 1] = (float)(std * r * sin(6.283185307179586 * u2));
+    }
+}
+
+/* a Q4_K weight [K, M, E] from seeded N(0, 0.02) values */
+static struct ggml_tensor *q4k_weight(struct ggml_context *ctx, int64_t K, int64_t M, int64_t E, uint64_t seed,
+                                      float *scratch) {
+    struct ggml_tensor *w = ggml_new_tensor_3d(ctx, GGML_TYPE_Q4_K, K, M, E);
+    normal_fill(scratch, K * M * E, seed, 0.02f);
+    ggml_quantize_chunk(GGML_TYPE_Q4_K, scratch, w->data, 0, M * E, K, NULL);
+    return w;
+}
+
+static struct ggml_tensor *f32_input(struct ggml_context *ctx, int64_t ne0, int64_t ne1, int64_t ne2, uint64_t seed) {
+    struct ggml_tensor *x = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, ne0, ne1, ne2);
+    normal_fill((float *)x->data, ne0 * ne1 * ne2, seed, 1.0f);
+    return x;
+}
+
+static int finish(struct ggml_context *ctx, spq4k_ggml *b, struct ggml_tensor *yr, struct ggml_tensor *ya,
+                  int nthreads, float *y_ref, float *y_ada, char *err, int errlen) {
+    int rc = 0;
+    if (!yr || !ya) {
+        snprintf(err, errlen, "graph construction failed");
+        rc = -1;
+    } else {
+        struct ggml_cgraph *gf = ggml_new_graph(ctx);
+        ggml_build_forward_expand(gf, yr);
+        ggml_build_forward_expand(gf, ya);
+        if (ggml_graph_compute_with_ctx(ctx, gf, nthreads) != GGML_STATUS_SUCCESS) {
+            snprintf(err, errlen, "ggml_graph_compute failed");
+            rc = -1;
+        } else if (spq4k_ggml_status(b) != 0) {
+            snprintf(err, errlen, "%s", spq4k_ggml_last_error(b));
+            rc = spq4k_ggml_status(b);
+        } else {
+            memcpy(y_ref, yr->data, ggml_nbytes(yr));
+            memcpy(y_ada, ya->data, ggml_nbytes(ya));
+        }
+    }
+    spq4k_ggml_free(b);
+    ggml_free(ctx);
+    return rc;
+}
+
+static struct ggml_context *new_ctx(size_t bytes) {
+    struct ggml_init_params ip = {bytes, NULL, false};
+    return ggml_init(ip);
+}
+
+/* y [M, T] = W [K, M] x x [K, T] */
+int check_mul_mat(int64_t M, int64_t K, int64_t T, uint64_t seed, int nthreads, float *y_ref, float *y_ada,
+                  char *err, int errlen) {
+    spq4k_ggml *b;
+    int rc = spq4k_ggml_init(0, &b);
+    if (rc) {
+        snprintf(err, errlen, "spq4k_ggml_init: %d", rc);
+        return rc;
+    }
+    struct ggml_context *ctx = new_ctx((size_t)M * K * 4 + (size_t)K * T * 16 + (size_t)M * T * 16 + (64 << 20));
+    float *tmp = (float *)malloc((size_t)M * K * sizeof(float));
+    struct ggml_tensor *W = q4k_weight(ctx, K, M, 1, seed, tmp);
+    free(tmp);
+    struct ggml_tensor *x = f32_input(ctx, K, T, 1, seed + 1);
+    return finish(ctx, b, ggml_mul_mat(ctx, W, x), spq4k_ggml_mul_mat(ctx, W, x, b), nthreads, y_ref, y_ada, err,
+                  errlen);
+}
+
+/* a gated feed-forward block, every matmul Q4_K:
+ * y [D, T] = down [F, D] x (silu(gate [D, F] x x) * (up [D, F] x x)).
+ * y_ref: all ggml; y_ada: all three matmuls through the adapter; y_chk:
+ * ggml's down matmul applied to the adapter's own hidden activations (the
+ * per-op comparison for the last node, free of upstream re-quantisation). */
+int check_mlp(int64_t D, int64_t F, int64_t T, uint64_t seed, int nthreads, float *y_ref, float *y_ada, float *y_chk,
+              char *err, int errlen) {
+    spq4k_ggml *b;
+    int rc = spq4k_ggml_init(0, &b);
+    if (rc) {
+        snprintf(err, errlen, "spq4k_ggml_init: %d", rc);
+        return rc;
+    }
+    struct ggml_context *ctx = new_ctx((size_t)3 * D * F * 4 + (size_t)(D + F) * T * 64 + (64 << 20));
+    float *tmp = (float *)malloc((size_t)D * F * sizeof(float));
+    struct ggml_tensor *gate = q4k_weight(ctx, D, F, 1, seed, tmp);
+    struct ggml_tensor *up = q4k_weight(ctx, D, F, 1, seed + 1, tmp);
+    struct ggml_tensor *down = q4k_weight(ctx, F, D, 1, seed + 2, tmp);
+    free(tmp);
+    struct ggml_tensor *x = f32_input(ctx, D, T, 1, seed + 3);
+    struct ggml_tensor *hr = ggml_mul(ctx, ggml_silu(ctx, ggml_mul_mat(ctx, gate, x)), ggml_mul_mat(ctx, up, x));
+    struct ggml_tensor *yr = ggml_mul_mat(ctx, down, hr);
+    struct ggml_tensor *ga = spq4k_ggml_mul_mat(ctx, gate, x, b), *ua = spq4k_ggml_mul_mat(ctx, up, x, b);
+    struct ggml_tensor *ya = NULL, *yc = NULL;
+    if (ga && ua) {
+        struct ggml_tensor *ha = ggml_mul(ctx, ggml_silu(ctx, ga), ua);
+        ya = spq4k_ggml_mul_mat(ctx, down, ha, b);
+        yc = ggml_mul_mat(ctx, down, ha);
+    }
+    if (yc) {
+        struct ggml_cgraph *gf = ggml_new_graph(ctx);
+        ggml_build_forward_expand(gf, yc);
+        ggml_build_forward_expand(gf, ya);
+        ggml_build_forward_expand(gf, yr);
+        if (ggml_graph_compute_with_ctx(ctx, gf, nthreads) != GGML_STATUS_SUCCESS) yc = NULL;
+        else memcpy(y_chk, yc->data, ggml_nbytes(yc));
+    }
+    return finish(ctx, b, yr, yc ? ya : NULL, nthreads, y_ref, y_ada, err, errlen);
+}
+
+/* y [M, n_used, T] = mul_mat_id(as [K, M, E], x [K, ne11, T], ids [n_used, T]) */
+int check_mul_mat_id(int64_t M, int64_t K, int64_t E, int64_t n_used, int64_t ne11, int64_t T, const int32_t *ids_in,
+                     uint64_t seed, int nthreads, float *y_ref, float *y_ada, char *err, int errlen) {
+    spq4k_ggml *b;
+    int rc = spq4k_ggml_init(0, &b);
+    if (rc) {
+        snprintf(err, errlen, "spq4k_ggml_init: %d", rc);
+        return rc;
+    }
+    struct ggml_context *ctx =
+        new_ctx((size_t)M * K * E * 4 + (size_t)K * ne11 * T * 16 + (size_t)M * n_used * T * 16 + (64 << 20));
+    float *tmp = (float *)malloc((size_t)M * K * E * sizeof(float));
+    struct ggml_tensor *as = q4k_weight(ctx, K, M, E, seed, tmp);
+    free(tmp);
+    struct ggml_tensor *x = f32_input(ctx, K, ne11, T, seed + 1);
+    struct ggml_tensor *ids = ggml_new_tensor_2d(ctx, GGML_TYPE_I32, n_used, T);
+    memcpy(ids->data, ids_in, (size_t)n_used * T * sizeof(int32_t));
+    return finish(ctx, b, ggml_mul_mat_id(ctx, as, x, ids), spq4k_ggml_mul_mat_id(ctx, as, x, ids, b), nthreads,
+                  y_ref, y_ada, err, errlen);
+}

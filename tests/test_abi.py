@@ -1,5 +1,6 @@
-"""The C ABI library: it builds, loads without a GPU, exports every entry
-point that include/*.h declares, and reports a missing device as -ENODEV."""
+"""The C ABI libraries: they build, load without a GPU, export every entry
+point that include/*.h declares (spq4k_ggml.h: the ggml adapter library), and
+a missing device is reported as -ENODEV."""
 import ctypes as C
 import errno
 import os
@@ -9,13 +10,15 @@ import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB = os.path.join(REPO, "shannon-prime-burnhard_amd", "libspq4k.so")
+ADAPTER_LIB = os.path.join(REPO, "shannon-prime-burnhard_amd", "libspq4k_ggml.so")
+ADAPTER_HEADER = os.path.join(REPO, "include", "spq4k_ggml.h")
 HEADERS = [os.path.join(REPO, "include", h) for h in sorted(os.listdir(os.path.join(REPO, "include")))
            if h.endswith(".h")]
 
 
-def declared_functions():
+def declared_functions(headers=None):
     names = []
-    for h in HEADERS:
+    for h in headers if headers is not None else [h for h in HEADERS if h != ADAPTER_HEADER]:
         text = open(h).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names += re.findall(r"\b(spq4k_[a-zA-Z0-9_]+)\s*\(", text)
@@ -33,6 +36,23 @@ def test_library_exports_every_declared_symbol():
     lib = C.CDLL(LIB)
     missing = [n for n in declared_functions() if not hasattr(lib, n)]
     assert not missing, f"declared in include/*.h but not exported: {missing}"
+
+
+def test_adapter_exports_every_declared_symbol():
+    if not os.path.exists(ADAPTER_LIB):
+        pytest.skip("the ggml adapter is built only where the host engine's ggml headers are present")
+    # the adapter leaves ggml's symbols to the host process: resolve them from the
+    # reference's ggml build when it is there, else only check the export table
+    ref = os.path.join(REPO, "oracle", "_ref", "v3", "libggml_ref.so")
+    if os.path.exists(ref):
+        C.CDLL(ref, mode=C.RTLD_GLOBAL)
+        lib = C.CDLL(ADAPTER_LIB)
+        missing = [n for n in declared_functions([ADAPTER_HEADER]) if not hasattr(lib, n)]
+    else:
+        import subprocess
+        out = subprocess.run(["nm", "-D", "--defined-only", ADAPTER_LIB], capture_output=True, text=True).stdout
+        missing = [n for n in declared_functions([ADAPTER_HEADER]) if f" {n}\n" not in out + "\n"]
+    assert not missing, f"declared in spq4k_ggml.h but not exported: {missing}"
 
 
 def test_no_device_is_an_error_not_a_fallback():

@@ -1,0 +1,93 @@
+"""The ggml engine adapter (include/spq4k_ggml.h) inside a real ggml graph.
+
+The reference's own ggml (compiled from its sources into oracle/_ref) hosts a
+graph in which the same inputs go through ggml's GGML_OP_MUL_MAT /
+GGML_OP_MUL_MAT_ID on the CPU and through the adapter's spq4k custom-op nodes
+on the GPU (tests/adapter/ggml_adapter_check.c). Every adapter node must be
+within close_enough (1e-4 relative or 1e-5 absolute,
+tests/desktop/test_sp_kernels.cpp:34-48) of ggml's node on the same inputs:
+single projections at decode and prefill batch sizes, the expert-gathered
+matmul, and the last matmul of a gated feed-forward block whose three Q4_K
+matmuls all run on the GPU (SiLU and the product stay ggml CPU ops). The whole
+block is compared normwise: its second and third matmuls re-quantise
+activations that already differ from ggml's in the last fp32 bits, and an
+element that lands on the other side of a Q8_K rounding boundary moves the
+output by d8 * w, far above 1e-5, so element-wise agreement of a chain is not
+a property any reordering of the fp32 sums keeps. This is the engine adapter's
+end-to-end check (the Q4_K branch of sp_crt_mul_mat,
+desktop/engine/src/forward.cpp:1270-1273) at the scale of one block."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from _oracle import close_enough
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+DRIVER = os.path.join(HERE, "adapter", "_build", "libadapter_check.so")
+
+
+@pytest.fixture(scope="module")
+def drv():
+    if not os.path.exists(DRIVER):
+        pytest.skip("adapter test driver not built (needs the reference's ggml sources at build time)")
+    lib = ctypes.CDLL(DRIVER)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    i64, u64, cint = ctypes.c_int64, ctypes.c_uint64, ctypes.c_int
+    lib.check_mul_mat.argtypes = [i64, i64, i64, u64, cint, f32p, f32p, ctypes.c_char_p, cint]
+    lib.check_mlp.argtypes = [i64, i64, i64, u64, cint, f32p, f32p, f32p, ctypes.c_char_p, cint]
+    lib.check_mul_mat_id.argtypes = [i64, i64, i64, i64, i64, i64, ctypes.POINTER(ctypes.c_int32), u64, cint, f32p,
+                                     f32p, ctypes.c_char_p, cint]
+    return lib
+
+
+def _run(fn, n, *args):
+    yr = np.full(n, np.nan, np.float32)
+    ya = np.full(n, np.nan, np.float32)
+    err = ctypes.create_string_buffer(256)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    rc = fn(*args, 8, yr.ctypes.data_as(f32p), ya.ctypes.data_as(f32p), err, 256)
+    assert rc == 0, err.value.decode()
+    return yr, ya
+
+
+def _check(yr, ya, what):
+    assert np.isfinite(yr).all()
+    ok = close_enough(ya, yr)
+    assert ok.all(), (f"{what}: {int((~ok).sum())}/{ok.size} outside tolerance; first {int(np.argmax(~ok))}: "
+                      f"adapter {ya[np.argmax(~ok)]} ggml {yr[np.argmax(~ok)]}")
+
+
+@pytest.mark.parametrize("M,K,T", [(4096, 4096, 1), (300, 2048, 3), (256, 5120, 8), (512, 4096, 64), (128, 12288, 17)])
+def test_adapter_mul_mat(drv, M, K, T):
+    yr, ya = _run(drv.check_mul_mat, M * T, M, K, T, 11 + T)
+    _check(yr, ya, f"mul_mat M={M} K={K} T={T}")
+
+
+FF_NORMWISE = 2e-3   # bound on ||y_adapter - y_ggml|| / ||y_ggml|| for the whole block
+
+
+@pytest.mark.parametrize("D,F,T", [(2048, 5632, 1), (1024, 2816, 6), (1024, 2816, 32)])
+def test_adapter_feed_forward(drv, D, F, T):
+    n = D * T
+    yr, ya, yc = (np.full(n, np.nan, np.float32) for _ in range(3))
+    err = ctypes.create_string_buffer(256)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    rc = drv.check_mlp(D, F, T, 3 + T, 8, yr.ctypes.data_as(f32p), ya.ctypes.data_as(f32p), yc.ctypes.data_as(f32p),
+                       err, 256)
+    assert rc == 0, err.value.decode()
+    _check(yc, ya, f"feed-forward down node D={D} F={F} T={T}")
+    rel = float(np.linalg.norm(ya.astype(np.float64) - yr) / np.linalg.norm(yr.astype(np.float64)))
+    assert rel <= FF_NORMWISE, f"feed-forward block D={D} F={F} T={T}: normwise {rel:.3e} > {FF_NORMWISE}"
+
+
+@pytest.mark.parametrize("T,ne11", [(1, 1), (3, 4), (12, 1)])
+def test_adapter_mul_mat_id(drv, T, ne11):
+    E, M, K, k = 32, 256, 1024, 4
+    rng = np.random.default_rng(T)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    yr, ya = _run(drv.check_mul_mat_id, M * k * T, M, K, E, k, ne11 if ne11 != 4 else k, T,
+                  ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), 21 + T)
+    _check(yr, ya, f"mul_mat_id T={T} ne11={ne11}")
