@@ -686,6 +686,7 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
         const int64_t per_wg = moe_decode_rows_per_wg(nb);
         const int64_t need = (n_pairs * M + per_wg - 1) / per_wg;
         const int grid = (int)(need < 2 * c->num_cus ? need : 2 * c->num_cus);
+        moe_decode_plan(f, grid, &f.rows_per_wg, &f.xwin_rows);
         hipError_t e = launch_moe_decode(f, grid, c->stream);
         if (e != hipSuccess) return hip_fail(c, e, "moe decode launch");
         return 0;

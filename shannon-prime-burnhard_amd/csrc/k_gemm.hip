@@ -25,6 +25,8 @@
 #include "launch.h"
 #include "ring_core.h"
 
+#include <type_traits>
+
 namespace spq4k {
 
 // per-lane weight registers for one super-block: header + 64 B of qs (skinny kernel)
@@ -329,10 +331,11 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 // slots re-read a valid address). A wave waits for its own loads of a stage
 // with s_waitcnt vmcnt (loads complete in order) before the barrier that
 // publishes the stage to the other waves.
-template <int RT, int CT, int NW, int S>
+template <int RT, int CT, int NW, int S, int TW = 16>
 __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
-    constexpr int TOK = CT * 16;
-    constexpr int ROWS = RT * 16 * NW;
+    static_assert(TW == 16 || TW == 32, "16x16 or 32x32 output tiles");
+    constexpr int TOK = CT * TW;
+    constexpr int ROWS = RT * TW * NW;
     constexpr int W_SLOTS = ROWS * 9, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
     constexpr int W_LOADS = (W_SLOTS + 63) / 64, Q_LOADS = (Q_SLOTS + 63) / 64, M_LOADS = (M_SLOTS + 63) / 64;
     constexpr int NLOAD = W_LOADS + Q_LOADS + M_LOADS;
@@ -400,11 +403,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
                 (__attribute__((address_space(3))) void*)(lds[buf] + (NW * i + wave) * 1024), 16, 0, 0);
     };
 
-    v4f acc[RT][CT];
+    typedef typename std::conditional<TW == 16, v4f, v16f>::type acc_t;
+    acc_t acc[RT][CT];
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) acc[r][ct] = v4f{0, 0, 0, 0};
+        for (int ct = 0; ct < CT; ++ct) acc[r][ct] = acc_t{};
 
 #pragma unroll
     for (int k = 0; k < S - 1; ++k) issue(min(k, nbl - 1), k);
@@ -416,7 +420,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * NPW) : "memory");
         issue(min(b + S - 1, nbl - 1), (b + S - 1) % S);
 
-        ring_block<RT, CT>(lds[buf] + (wave * RT * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+        if constexpr (TW == 16)
+            ring_block<RT, CT>(lds[buf] + (wave * RT * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+        else
+            ring_block32<RT, CT>(lds[buf] + (wave * RT * 32) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, lane, acc);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the clamped loads past the last stage
 
@@ -435,20 +442,28 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
         rbase = 0;
     }
     const bool vec = ((ld | rbase) & 3) == 0;
+    // a lane holds runs of 4 consecutive rows of one token: TW = 16, rows
+    // 4q .. 4q+3 of each tile; TW = 32, rows 8j + 4h .. +3 for j = 0..3
+    constexpr int RUNS = TW == 16 ? 1 : 4;
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
-        const int rq = row0 + wave * RT * 16 + r * 16 + 4 * q;
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
-            const int t = tok0 + ct * 16 + c16;
+            const int t = tok0 + ct * TW + (TW == 16 ? c16 : (lane & 31));
             if (t >= T) continue;
-            float* y = out + (int64_t)t * ld + rbase + rq;
-            if (vec && rq + 3 < M) {
-                *reinterpret_cast<v4f*>(y) = acc[r][ct];
-            } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (rq + i < M) y[i] = acc[r][ct][i];
+            for (int j = 0; j < RUNS; ++j) {
+                const int rq = TW == 16 ? row0 + wave * RT * 16 + r * 16 + 4 * q
+                                        : row0 + wave * RT * 32 + r * 32 + 8 * j + 4 * (lane >> 5);
+                float* y = out + (int64_t)t * ld + rbase + rq;
+                const v4f v = {acc[r][ct][4 * j], acc[r][ct][4 * j + 1], acc[r][ct][4 * j + 2], acc[r][ct][4 * j + 3]};
+                if (vec && rq + 3 < M) {
+                    *reinterpret_cast<v4f*>(y) = v;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (rq + i < M) y[i] = v[i];
+                }
             }
         }
     }
@@ -674,13 +689,13 @@ static hipError_t launch_tiled_(const GemmParams& p, int grid, hipStream_t st) {
     hipLaunchKernelGGL((gemm_tiled_kernel<RT, CT, WR, WK>), dim3((unsigned)grid), dim3(256), 0, st, p);
     return hipGetLastError();
 }
-template <int RT, int CT, int NW, int S>
+template <int RT, int CT, int NW, int S, int TW = 16>
 static hipError_t launch_ring_(const GemmParams& p, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_ring_kernel<RT, CT, NW, S>), dim3((unsigned)grid), dim3(NW * 64), 0, st, p);
+    hipLaunchKernelGGL((gemm_ring_kernel<RT, CT, NW, S, TW>), dim3((unsigned)grid), dim3(NW * 64), 0, st, p);
     return hipGetLastError();
 }
 static const TiledShape kTiled[] = {
-    {256, 64, true, launch_ring_<2, 4, 8, 2>},      // 0: ring, 8 waves, 2 stages
+    {256, 64, true, launch_ring_<2, 4, 8, 2>},      // 0: ring 16x16, 8 waves, 2 stages
     {128, 64, true, launch_ring_<1, 4, 8, 3>},      // 1: ring, 8 waves, 3 stages
     {128, 64, true, launch_ring_<2, 4, 4, 3>},      // 2: ring, 4 waves, 3 stages
     {64, 32, false, launch_tiled_<2, 2, 2, 2>},     // 3: register-staged, K split in two
@@ -689,6 +704,11 @@ static const TiledShape kTiled[] = {
     {128, 16, true, launch_ring_<1, 1, 8, 3>},      // 6: ring, T <= 16
     {128, 32, true, launch_ring_<1, 2, 8, 3>},      // 7: ring, T <= 32
     {64, 16, true, launch_ring_<1, 1, 4, 3>},       // 8: ring, T <= 16, 4 waves
+    {256, 128, true, launch_ring_<2, 8, 8, 2>},     // 9: ring, 8 waves, 2 stages of 80 KB
+    {128, 128, true, launch_ring_<1, 8, 8, 2>},     // 10: ring, 8 waves, 2 stages
+    {256, 64, true, launch_ring_<1, 2, 8, 2, 32>},  // 11: ring 32x32, 8 waves, 2 stages
+    {128, 64, true, launch_ring_<1, 2, 4, 3, 32>},  // 12: ring 32x32, 4 waves, 3 stages
+    {128, 32, true, launch_ring_<1, 1, 4, 3, 32>},  // 13: ring 32x32, T <= 32
 };
 constexpr int N_TILED = (int)(sizeof(kTiled) / sizeof(kTiled[0]));
 
@@ -710,11 +730,12 @@ GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
             cfg = 7;
         } else {
             // the largest tile that gives every CU a workgroup without a K
-            // split (measured on MI355X at T = 512: 256 x 64 for 24576 rows,
-            // 128 x 64 for 4096 and 6144), else 128 x 64 with one
+            // split, else 128 x 64 with one. Measured on MI355X at T = 512:
+            // 256 x 64 on 32x32 MFMA tiles for 24576 rows (140 us against 155
+            // on 16x16 tiles), 128 x 64 on 16x16 tiles for 4096 and 6144
             cfg = 1;
             const int64_t g0 = row_tiles(p, 256) * ((p.T + 63) / 64);
-            if (g0 >= num_cus) cfg = 0;
+            if (g0 >= num_cus) cfg = 11;
         }
     }
     const TiledShape& s = kTiled[cfg];

@@ -285,6 +285,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     extern __shared__ __align__(16) char smem[];
     constexpr int LPR = 4 * BSL;
     constexpr int RPW = 64 / LPR;
+    constexpr int RPG = WAVES * RPW;             // rows of one pass of the workgroup
     constexpr int NIT = (NB + BSL - 1) / BSL;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -292,25 +293,34 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     const int bsub = (lane & (LPR - 1)) >> 2;
     const int M = p.M;
     const int total = p.n_pairs * M;
-    const int G = gridDim.x * WAVES * RPW;
-    const int g = (blockIdx.x * WAVES + wave) * RPW + lane / LPR;
-    const int nx = p.n_xrows;
-    const Q8Lds L = q8lds_carve(smem, nx * NB);
+    // this workgroup's rows of the sweep: one contiguous run (one or two
+    // pairs), so it quantises only the input rows those pairs read
+    const int r0 = blockIdx.x * p.rows_per_wg;
+    if (r0 >= total) return;                     // uniform over the workgroup
+    const int r1 = min(total, r0 + p.rows_per_wg);
+    auto xrow = [&](int r) {                     // input row of sweep row r (non-decreasing in r)
+        const int pr = r / M;
+        const int t = pr / p.n_used;
+        return t * p.ne11 + (pr - t * p.n_used) % p.ne11;
+    };
+    const int xlo = xrow(r0);
+    const int nitems = (xrow(r1 - 1) - xlo + 1) * NB;
+    const Q8Lds L = q8lds_carve(smem, p.xwin_rows * NB);
+    const int g0 = r0 + wave * RPW + lane / LPR;
 
-    // where row r of the sweep lives: expert (or -1), its row, its input row
+    // where row r of the sweep lives: expert (or -1), its row, its input window slot
     struct Loc {
         const uint8_t* w;
         int e, lr, xs;
     };
     auto locate = [&](int r) {
         Loc l;
-        const int rc = r < total ? r : total - 1;
+        const int rc = r < r1 ? r : r1 - 1;
         const int pr = rc / M;
         l.lr = rc - pr * M;
         const int e = p.ids[pr];
-        l.e = (r < total && e >= 0 && e < p.E) ? e : -1;
-        const int t = pr / p.n_used;
-        l.xs = (t * p.ne11 + (pr - t * p.n_used) % p.ne11) * NB;
+        l.e = (r < r1 && e >= 0 && e < p.E) ? e : -1;
+        l.xs = (xrow(rc) - xlo) * NB;
         l.w = p.bank + (size_t)(l.e >= 0 ? l.e : 0) * p.expert_bytes + (size_t)l.lr * ((size_t)NB * Q4K_BYTES);
         return l;
     };
@@ -325,23 +335,21 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     // row, the first pass of input rows, then that row's weights, so that the
     // quantisation waits only for x while the weights are in flight
     const int item_a = wave * 4 + (lane >> 4);
-    const int ci_a = item_a < nx * NB ? item_a : nx * NB - 1;
-    const int xr_a = ci_a / NB;
-    Loc cur = locate(g);
-    const XRegs xa = load_x16(p.X, p.K, xr_a, ci_a - xr_a * NB);
+    const int ci_a = item_a < nitems ? item_a : nitems - 1;
+    Loc cur = locate(g0);
+    const XRegs xa = load_x16(p.X, p.K, xlo + ci_a / NB, ci_a % NB);
     W4 w[NIT];
     load(cur, w);
-    store_q8_item(xa, item_a < nx * NB, ci_a, L);
-    for (int base = 4 * WAVES; base < nx * NB; base += 4 * WAVES) {
+    store_q8_item(xa, item_a < nitems, ci_a, L);
+    for (int base = 4 * WAVES; base < nitems; base += 4 * WAVES) {
         const int item0 = base + item_a;
-        const bool valid = item0 < nx * NB;
-        const int item = valid ? item0 : nx * NB - 1;
-        const int xr = item / NB;
-        const XRegs r = load_x16(p.X, p.K, xr, item - xr * NB);
+        const bool valid = item0 < nitems;
+        const int item = valid ? item0 : nitems - 1;
+        const XRegs r = load_x16(p.X, p.K, xlo + item / NB, item % NB);
         store_q8_item(r, valid, item, L);
     }
     __syncthreads();
-    for (int r = g; r < total; r += G) {
+    for (int r = g0; r < r1; r += RPG) {
         float acc[1] = {0.0f};
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
@@ -350,8 +358,8 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
         }
         const float sum = group_sum_last<LPR>(acc[0]);
         if (cur.e >= 0 && (lane & (LPR - 1)) == LPR - 1) p.Y[(int64_t)(r / M) * M + cur.lr] = sum;
-        if (r + G < total) {
-            cur = locate(r + G);
+        if (r + RPG < r1) {
+            cur = locate(r + RPG);
             load(cur, w);
         }
     }
@@ -360,7 +368,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
 template <int NB, int BSL>
 static hipError_t launch_mdec(const MoeFusedParams& p, int grid, hipStream_t st) {
     constexpr int WAVES = 8;
-    const size_t lds = (size_t)q8lds_bytes(p.n_xrows * NB);
+    const size_t lds = (size_t)q8lds_bytes(p.xwin_rows * NB);
     hipLaunchKernelGGL((moe_decode_kernel<NB, BSL, WAVES>), dim3(grid), dim3(WAVES * 64), lds, st, p);
     return hipGetLastError();
 }
@@ -369,6 +377,19 @@ bool moe_decode_supported(int nb) { return nb == 3 || nb == 8 || nb == 16; }
 
 // rows of the sweep per workgroup pass: WAVES * 64 / (4 * BSL)
 int moe_decode_rows_per_wg(int nb) { return nb == 3 ? 32 : (nb == 8 ? 16 : 8); }
+
+// rows per workgroup (a whole number of passes) and the input rows the
+// largest run of that many sweep rows can read
+void moe_decode_plan(const MoeFusedParams& p, int grid, int32_t* rows_per_wg, int32_t* xwin_rows) {
+    const int64_t total = (int64_t)p.n_pairs * p.M;
+    const int64_t pass = moe_decode_rows_per_wg(p.nb);
+    int64_t rw = (total + grid - 1) / grid;
+    rw = (rw + pass - 1) / pass * pass;
+    *rows_per_wg = (int32_t)rw;
+    // a run of rw rows touches at most rw / M + 2 pairs, so as many input rows
+    const int64_t w = rw / p.M + 2;
+    *xwin_rows = (int32_t)(w < p.n_xrows ? w : p.n_xrows);
+}
 
 hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st) {
     switch (p.nb) {

@@ -82,6 +82,8 @@ struct MoeFusedParams {
     int32_t chunk_blocks;
     int32_t E;          // experts in the bank (moe_decode_kernel)
     int32_t n_xrows;    // input rows T * ne11 (moe_decode_kernel)
+    int32_t rows_per_wg;   // moe_decode_kernel: contiguous sweep rows a workgroup (moe_decode_plan)
+    int32_t xwin_rows;     // moe_decode_kernel: input rows quantised by a workgroup at most
 };
 hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st);
 
@@ -90,6 +92,7 @@ constexpr int MOE_DEC_MAX_PAIRS = 64;
 constexpr int MOE_DEC_MAX_XROWS = 64;
 bool moe_decode_supported(int nb);
 int moe_decode_rows_per_wg(int nb);
+void moe_decode_plan(const MoeFusedParams& p, int grid, int32_t* rows_per_wg, int32_t* xwin_rows);
 hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st);
 hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st);
 // matrix-core form: moe_prep_kernel (routing in workgroup 0, permuted Q8_K

@@ -50,7 +50,6 @@ __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
 template <int RT, int CT>
 __device__ __forceinline__ void ring_block(const uint8_t* wt, const uint8_t* qreg, const uint8_t* mreg, int c16, int q,
                                            v4f (&acc)[RT][CT]) {
-    v4i ch[RT][CT], cl[RT][CT];
     uint32_t SH0[RT], SL0[RT], SH1[RT], SL1[RT];
     v4i wq[RT][2];
     h4 am[RT];
@@ -88,48 +87,150 @@ __device__ __forceinline__ void ring_block(const uint8_t* wt, const uint8_t* qre
         const h2 fv = {f, f}, ov = {o, o};
         const h2 b01 = a01 * fv + ov, b23 = a23 * fv + ov;
         am[r] = h4{b01.x, b01.y, b23.x, b23.y};
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-            ch[r][ct] = v4i{0, 0, 0, 0};
-            cl[r][ct] = v4i{0, 0, 0, 0};
-        }
     }
     // activation fragment of token c16, step s: values 64q + 8s .. +7 and
     // 64q + 32 + 8s .. +7, stored contiguously by the permuted Q8_K planes
-    const uint8_t* qb = qreg + c16 * RING_QS + 64 * q;
+    // folded weight operands of every step, made once for all token tiles
+    v4i ah[RT][4], al[RT][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        v4i bq[CT];
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) bq[ct] = *reinterpret_cast<const v4i*>(qb + ct * 16 * RING_QS + 16 * s);
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
+        for (int s = 0; s < 4; ++s) {
             const uint32_t w0 = (uint32_t)wq[r][s >> 1][2 * (s & 1)];
             const uint32_t w1 = (uint32_t)wq[r][s >> 1][2 * (s & 1) + 1];
             const uint32_t l0 = w0 & 0x0F0F0F0Fu, l1 = w1 & 0x0F0F0F0Fu;
             const uint32_t u0 = (w0 >> 4) & 0x0F0F0F0Fu, u1 = (w1 >> 4) & 0x0F0F0F0Fu;
-            const v4i ah = {(int)pk_mul_u16(l0, SH0[r]), (int)pk_mul_u16(l1, SH0[r]),
-                            (int)pk_mul_u16(u0, SH1[r]), (int)pk_mul_u16(u1, SH1[r])};
-            const v4i al = {(int)pk_mul_u16(l0, SL0[r]), (int)pk_mul_u16(l1, SL0[r]),
-                            (int)pk_mul_u16(u0, SL1[r]), (int)pk_mul_u16(u1, SL1[r])};
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-                ch[r][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bq[ct], ch[r][ct], 0, 0, 0);
-                cl[r][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bq[ct], cl[r][ct], 0, 0, 0);
-            }
+            ah[r][s] = v4i{(int)pk_mul_u16(l0, SH0[r]), (int)pk_mul_u16(l1, SH0[r]), (int)pk_mul_u16(u0, SH1[r]),
+                           (int)pk_mul_u16(u1, SH1[r])};
+            al[r][s] = v4i{(int)pk_mul_u16(l0, SL0[r]), (int)pk_mul_u16(l1, SL0[r]), (int)pk_mul_u16(u0, SL1[r]),
+                           (int)pk_mul_u16(u1, SL1[r])};
         }
-    }
+    // tile by tile: a tile's eight-MFMA chain is followed by its combine, so
+    // the combine's VALU work overlaps the next tile's MFMAs and only a few
+    // tiles' integer sums are live at a time
+    const uint8_t* qb = qreg + c16 * RING_QS + 64 * q;
     const uint8_t* mb = mreg + c16 * Q8MN_BYTES;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
+        v4i bq[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bq[s] = *reinterpret_cast<const v4i*>(qb + ct * 16 * RING_QS + 16 * s);
         const h4 bm = *reinterpret_cast<const h4*>(mb + ct * 16 * Q8MN_BYTES + 8 * q);
         const float d8 = *reinterpret_cast<const float*>(mb + ct * 16 * Q8MN_BYTES + 32);
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
+            v4i ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[r][0], bq[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            v4i cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[r][0], bq[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int s = 1; s < 4; ++s) {
+                ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[r][s], bq[s], ch, 0, 0, 0);
+                cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[r][s], bq[s], cl, 0, 0, 0);
+            }
             const v4f cm = __builtin_amdgcn_mfma_f32_16x16x16f16(am[r], bm, v4f{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int I = (ch[r][ct][i] << 3) + cl[r][ct][i];
+                const int I = (ch[i] << 3) + cl[i];
+                acc[r][ct][i] = fmaf(d8, fmaf(-dmr[r][i], cm[i], dr[r][i] * (float)I), acc[r][ct][i]);
+            }
+        }
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// The same super-block on 32x32 tiles: v_mfma_i32_32x32x32_i8, which sustains
+// 1.7x the int8 rate of the 16x16x64 form on gfx950 (4.7 against 2.8 POP/s
+// measured), and v_mfma_f32_32x32x16_f16 for the min term.
+// Lane (c32, h) = (lane & 31, lane >> 5). Operand k slots: step s (0..7) of
+// lane half h holds the low and the high nibbles of bytes 8*(s&3) .. +7 of
+// nibble group 2h + (s >> 2) (sub-blocks 4h + 2(s>>2) and +1), i.e. values
+// 64g + 8(s&3) .. +7 and 64g + 32 + 8(s&3) .. +7 of group g = 2h + (s>>2),
+// which the permuted Q8_K row stores at 64g + 16(s&3) (one 16-byte read).
+// Min-term slots: half 0 holds (32 m_j, hi_j), half 1 (m_j, lo_j), j = 0..7.
+// Output element i of lane (c32, h): row 8(i/4) + 4h + (i%4) of the 32-row
+// tile, token c32 of the 32-token tile.
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+template <int RT, int CT>
+__device__ __forceinline__ void ring_block32(const uint8_t* wt, const uint8_t* qreg, const uint8_t* mreg, int lane,
+                                             v16f (&acc)[RT][CT]) {
+    const int c32 = lane & 31, h = lane >> 5;
+    v4i ah[RT][8], al[RT][8];
+    h8 am[RT];
+    float dr[RT][16], dmr[RT][16];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const uint8_t* wr = wt + (r * 32 + c32) * Q4K_BYTES;
+        const v4i hdr = *reinterpret_cast<const v4i*>(wr);
+        v4i wq[4];   // groups 2h, 2h + 1 of qs
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wq[k] = *reinterpret_cast<const v4i*>(wr + 16 + 64 * h + 16 * k);
+        // d, dmin of output rows 8(i/4) + 4h + (i%4)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t hd =
+                *reinterpret_cast<const uint32_t*>(wt + (r * 32 + 8 * (i >> 2) + 4 * h + (i & 3)) * Q4K_BYTES);
+            dr[r][i] = half_bits_to_float(hd & 0xFFFFu);
+            dmr[r][i] = half_bits_to_float(hd >> 16);
+        }
+        const ScaleMin sm = unpack_scale_min((uint32_t)hdr.y, (uint32_t)hdr.z, (uint32_t)hdr.w);
+        const uint32_t scw = h ? sm.sc_hi : sm.sc_lo;   // sub-blocks 4h .. 4h+3
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int gl = s >> 2;
+            const uint32_t sc01 = scw >> (16 * gl);      // sub-blocks 4h + 2gl (low nibbles), +1 (high)
+            const uint32_t SH0 = ((sc01 >> 3) & 7u) * 0x10001u, SL0 = (sc01 & 7u) * 0x10001u;
+            const uint32_t SH1 = ((sc01 >> 11) & 7u) * 0x10001u, SL1 = ((sc01 >> 8) & 7u) * 0x10001u;
+            const v4i& g = wq[2 * gl + ((s & 3) >> 1)];
+            const uint32_t w0 = (uint32_t)g[2 * (s & 1)], w1 = (uint32_t)g[2 * (s & 1) + 1];
+            const uint32_t l0 = w0 & 0x0F0F0F0Fu, l1 = w1 & 0x0F0F0F0Fu;
+            const uint32_t u0 = (w0 >> 4) & 0x0F0F0F0Fu, u1 = (w1 >> 4) & 0x0F0F0F0Fu;
+            ah[r][s] = v4i{(int)pk_mul_u16(l0, SH0), (int)pk_mul_u16(l1, SH0), (int)pk_mul_u16(u0, SH1),
+                           (int)pk_mul_u16(u1, SH1)};
+            al[r][s] = v4i{(int)pk_mul_u16(l0, SL0), (int)pk_mul_u16(l1, SL0), (int)pk_mul_u16(u0, SL1),
+                           (int)pk_mul_u16(u1, SL1)};
+        }
+        // min operand of row c32: 32 m_j (half 0) or m_j (half 1), j = 0..7;
+        // 0x6400 | m is the fp16 1024 + m, rescaled exactly
+        const _Float16 f = h == 0 ? (_Float16)32.0f : (_Float16)1.0f;
+        const _Float16 o = h == 0 ? (_Float16)-32768.0f : (_Float16)-1024.0f;
+        const h2 fv = {f, f}, ov = {o, o};
+        h2 mh[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t mw = k < 2 ? sm.m_lo : sm.m_hi;
+            const uint32_t x = __builtin_amdgcn_perm(0x64646464u, mw, (k & 1) ? 0x04030402u : 0x04010400u);
+            h2 a;
+            __builtin_memcpy(&a, &x, 4);
+            mh[k] = a * fv + ov;
+        }
+        am[r] = h8{mh[0].x, mh[0].y, mh[1].x, mh[1].y, mh[2].x, mh[2].y, mh[3].x, mh[3].y};
+    }
+    const uint8_t* qb = qreg + c32 * RING_QS + 128 * h;
+    const uint8_t* mb = mreg + c32 * Q8MN_BYTES + 16 * h;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+        v4i bq[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            bq[s] = *reinterpret_cast<const v4i*>(qb + ct * 32 * RING_QS + 64 * (s >> 2) + 16 * (s & 3));
+        const h8 bm = *reinterpret_cast<const h8*>(mb + ct * 32 * Q8MN_BYTES);
+        const float d8 = *reinterpret_cast<const float*>(mb - 16 * h + ct * 32 * Q8MN_BYTES + 32);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            v16i ch = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah[r][0], bq[0], v16i{}, 0, 0, 0);
+            v16i cl = __builtin_amdgcn_mfma_i32_32x32x32_i8(al[r][0], bq[0], v16i{}, 0, 0, 0);
+#pragma unroll
+            for (int s = 1; s < 8; ++s) {
+                ch = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah[r][s], bq[s], ch, 0, 0, 0);
+                cl = __builtin_amdgcn_mfma_i32_32x32x32_i8(al[r][s], bq[s], cl, 0, 0, 0);
+            }
+            const v16f cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[r], bm, v16f{}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int I = (ch[i] << 3) + cl[i];
                 acc[r][ct][i] = fmaf(d8, fmaf(-dmr[r][i], cm[i], dr[r][i] * (float)I), acc[r][ct][i]);
             }
         }
