@@ -429,35 +429,52 @@ double or_vec_dot_exact(int n, const void *vx, const void *vy) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Row geometry and vec_dot of a weight type (ggml-cpu/ggml-cpu.c:297-316:
+ * both types take Q8_K activations). */
+static size_t block_bytes(int type) {
+    return type == OR_TYPE_Q4_K ? OR_Q4K_BLOCK_BYTES : type == OR_TYPE_Q6_K ? OR_Q6K_BLOCK_BYTES : 0;
+}
+
+static float type_dot(int type, int order, int n, const void *wr, const void *q8) {
+    if (type == OR_TYPE_Q6_K)
+        return order ? or_vec_dot_q6K_avx2order(n, wr, q8) : or_vec_dot_q6K_generic(n, wr, q8);
+    return order ? or_vec_dot_avx2order(n, wr, q8) : or_vec_dot_generic(n, wr, q8);
+}
+
 /* Dense driver. Follows ggml-cpu/ggml-cpu.c:1241-1439
  * (ggml_compute_forward_mul_mat): each activation row is converted to Q8_K
- * (vec_dot_type of Q4_K, ggml-cpu.c:297-305), then dst[t][r] = vec_dot(K,
- * W row r, Q8_K row t). Thread chunking does not change any value. */
-void or_mul_mat(const void *W, int64_t M, int64_t K, const float *X, int64_t T,
-                float *Y, int order) {
+ * (the vec_dot_type of Q4_K and Q6_K, ggml-cpu.c:297-316), then dst[t][r] =
+ * vec_dot(K, W row r, Q8_K row t). Thread chunking does not change any value. */
+int or_mul_mat_type(int type, const void *W, int64_t M, int64_t K, const float *X, int64_t T,
+                    float *Y, int order) {
     const int64_t nb = K / OR_QK_K;
-    const size_t row_bytes = (size_t)nb * OR_Q4K_BLOCK_BYTES;
+    const size_t row_bytes = (size_t)nb * block_bytes(type);
+    if (!row_bytes) return -22;
     or_block_q8K *q8 = (or_block_q8K *)malloc((size_t)nb * sizeof(or_block_q8K));
     for (int64_t t = 0; t < T; ++t) {
         or_quantize_row_q8K(X + t * K, q8, K);
-        for (int64_t r = 0; r < M; ++r) {
-            const void *wr = (const uint8_t *)W + (size_t)r * row_bytes;
-            Y[t * M + r] = order ? or_vec_dot_avx2order((int)K, wr, q8)
-                                 : or_vec_dot_generic((int)K, wr, q8);
-        }
+        for (int64_t r = 0; r < M; ++r)
+            Y[t * M + r] = type_dot(type, order, (int)K, (const uint8_t *)W + (size_t)r * row_bytes, q8);
     }
     free(q8);
+    return 0;
+}
+
+void or_mul_mat(const void *W, int64_t M, int64_t K, const float *X, int64_t T,
+                float *Y, int order) {
+    (void)or_mul_mat_type(OR_TYPE_Q4_K, W, M, K, X, T, Y, order);
 }
 
 /* Expert-gathered driver. Follows ggml-cpu/ggml-cpu.c:1441-1511 and
  * 1521-1690 (ggml_compute_forward_mul_mat_id): for token t and slot s the
  * expert is ids[t][s]; its input row is X[t][s % ne11] (ne11 == 1 broadcasts
  * one row to every slot); dst[t][s][r] = vec_dot(expert row r, Q8_K(input)). */
-int or_mul_mat_id(const void *as, int64_t M, int64_t K, int64_t E,
-                  const float *X, int64_t ne11, const int32_t *ids, int64_t k,
-                  int64_t T, float *Y, int order) {
+int or_mul_mat_id_type(int type, const void *as, int64_t M, int64_t K, int64_t E,
+                       const float *X, int64_t ne11, const int32_t *ids, int64_t k,
+                       int64_t T, float *Y, int order) {
     const int64_t nb = K / OR_QK_K;
-    const size_t row_bytes = (size_t)nb * OR_Q4K_BLOCK_BYTES;
+    const size_t row_bytes = (size_t)nb * block_bytes(type);
+    if (!row_bytes) return -22;
     const size_t expert_bytes = row_bytes * (size_t)M;
     or_block_q8K *q8 = (or_block_q8K *)malloc((size_t)nb * sizeof(or_block_q8K));
     for (int64_t t = 0; t < T; ++t) {
@@ -466,26 +483,32 @@ int or_mul_mat_id(const void *as, int64_t M, int64_t K, int64_t E,
             if (e < 0 || e >= E) { free(q8); return -22; }
             or_quantize_row_q8K(X + (t * ne11 + (s % ne11)) * K, q8, K);
             const uint8_t *base = (const uint8_t *)as + (size_t)e * expert_bytes;
-            for (int64_t r = 0; r < M; ++r) {
-                const void *wr = base + (size_t)r * row_bytes;
-                Y[(t * k + s) * M + r] = order ? or_vec_dot_avx2order((int)K, wr, q8)
-                                               : or_vec_dot_generic((int)K, wr, q8);
-            }
+            for (int64_t r = 0; r < M; ++r)
+                Y[(t * k + s) * M + r] = type_dot(type, order, (int)K, base + (size_t)r * row_bytes, q8);
         }
     }
     free(q8);
     return 0;
 }
 
-/* Dequant-then-dot in double (the fp32 weights of or_dequantize_row_q4K times
+int or_mul_mat_id(const void *as, int64_t M, int64_t K, int64_t E,
+                  const float *X, int64_t ne11, const int32_t *ids, int64_t k,
+                  int64_t T, float *Y, int order) {
+    return or_mul_mat_id_type(OR_TYPE_Q4_K, as, M, K, E, X, ne11, ids, k, T, Y, order);
+}
+
+/* Dequant-then-dot in double (the fp32 weights of the type's to_float times
  * the fp32 activations, accumulated in double); the reference's scalar
  * dequant-then-dot path is desktop/beast_canyon/sp_beast_canyon.c:1122-1134. */
-void or_mul_mat_dequant_f64(const void *W, int64_t M, int64_t K, const float *X,
-                            int64_t T, double *Y) {
-    const size_t row_bytes = (size_t)(K / OR_QK_K) * OR_Q4K_BLOCK_BYTES;
+int or_mul_mat_dequant_f64_type(int type, const void *W, int64_t M, int64_t K, const float *X,
+                                int64_t T, double *Y) {
+    const size_t row_bytes = (size_t)(K / OR_QK_K) * block_bytes(type);
+    if (!row_bytes) return -22;
     float *wrow = (float *)malloc((size_t)K * sizeof(float));
     for (int64_t r = 0; r < M; ++r) {
-        or_dequantize_row_q4K((const uint8_t *)W + (size_t)r * row_bytes, wrow, K);
+        const uint8_t *src = (const uint8_t *)W + (size_t)r * row_bytes;
+        if (type == OR_TYPE_Q6_K) or_dequantize_row_q6K(src, wrow, K);
+        else or_dequantize_row_q4K(src, wrow, K);
         for (int64_t t = 0; t < T; ++t) {
             double acc = 0;
             const float *xt = X + t * K;
@@ -494,6 +517,12 @@ void or_mul_mat_dequant_f64(const void *W, int64_t M, int64_t K, const float *X,
         }
     }
     free(wrow);
+    return 0;
+}
+
+void or_mul_mat_dequant_f64(const void *W, int64_t M, int64_t K, const float *X,
+                            int64_t T, double *Y) {
+    (void)or_mul_mat_dequant_f64_type(OR_TYPE_Q4_K, W, M, K, X, T, Y);
 }
 
 /* ------------------------------------------------------------------------ */

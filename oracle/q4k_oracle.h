@@ -11,6 +11,8 @@
  * compiled with -ffp-contract=off so that each floating-point operation is
  * rounded exactly once, as in ggml-base (which is built without FMA flags).
  *
+ * q6k_oracle.c restates the Q6_K functions the same way.
+ *
  * Parity pins (see tests/): golden fixtures written by tests/golden/gen_golden.py
  * from the reference compiled in oracle/_ref, exhaustive and closed-form checks
  * of the scale unpacker, dequantiser and Q8_K quantiser, and brute-force
@@ -42,6 +44,18 @@ typedef struct {
     int8_t  qs[256];
     int16_t bsums[16];
 } or_block_q8K;
+
+#define OR_Q6K_BLOCK_BYTES 210   /* ql[128], qh[64], scales[16] (i8), d (fp16) */
+typedef struct {
+    uint8_t  ql[128];
+    uint8_t  qh[64];
+    int8_t   scales[16];
+    uint16_t d;
+} or_block_q6K;
+
+/* weight types, numbered as ggml.h:402-404 numbers them */
+#define OR_TYPE_Q4_K 12
+#define OR_TYPE_Q6_K 14
 
 /* scalar helpers */
 float    or_fp16_to_fp32(uint16_t h);
@@ -75,6 +89,26 @@ int  or_mul_mat_id(const void *as, int64_t M, int64_t K, int64_t E,
 /* dequant-then-dot in double: the "dequant-then-dot" branch of the parity bar */
 void or_mul_mat_dequant_f64(const void *W, int64_t M, int64_t K, const float *X,
                             int64_t T, double *Y);
+
+/* Q6_K (q6k_oracle.c) */
+void   or_quantize_row_q6K(const float *x, void *y, int64_t k);
+size_t or_quantize_q6K(const float *src, void *dst, int64_t nrow, int64_t n_per_row);
+void   or_dequantize_row_q6K(const void *x, float *y, int64_t k);
+float  or_vec_dot_q6K_generic(int n, const void *vx, const void *vy);
+float  or_vec_dot_q6K_avx2order(int n, const void *vx, const void *vy);
+double or_vec_dot_q6K_exact(int n, const void *vx, const void *vy);
+/* S[b*16 + j] = sum over the 16 weights of sub-block j of block b of (q-32)*q8 */
+void   or_subblock_sums_q6K(int n, const void *vx, const void *vy, int32_t *S);
+
+/* the drivers above for a weight type (OR_TYPE_Q4_K or OR_TYPE_Q6_K);
+ * return -22 for another type or a bad expert id */
+int or_mul_mat_type(int type, const void *W, int64_t M, int64_t K, const float *X, int64_t T,
+                    float *Y, int order);
+int or_mul_mat_id_type(int type, const void *as, int64_t M, int64_t K, int64_t E,
+                       const float *X, int64_t ne11, const int32_t *ids, int64_t k,
+                       int64_t T, float *Y, int order);
+int or_mul_mat_dequant_f64_type(int type, const void *W, int64_t M, int64_t K, const float *X,
+                                int64_t T, double *Y);
 
 /* synthetic data, bit-identical with the device generator */
 void or_synth_fill(float *out, int64_t n, uint64_t seed, int dist, int64_t cols,

@@ -7,7 +7,8 @@
  *
  * Everything below calls the reference's public API (ggml.h, ggml-cpu.h);
  * no reference arithmetic is re-implemented here.
- *   - type traits: ggml_get_type_traits(Q4_K)->to_float (dequantize_row_q4_K),
+ *   - type traits (Q4_K, and Q6_K through the *_type forms):
+ *     ggml_get_type_traits(Q4_K)->to_float (dequantize_row_q4_K),
  *     ggml_get_type_traits_cpu(Q8_K)->from_float (quantize_row_q8_K),
  *     ggml_get_type_traits_cpu(Q4_K)->vec_dot (ggml_vec_dot_q4_K_q8_K),
  *     ggml_quantize_chunk(Q4_K, ..., imatrix = NULL)
@@ -26,6 +27,8 @@
 
 /* declared in ggml-cpu/quants.h (internal); exported by the library */
 void ggml_vec_dot_q4_K_q8_K_generic(int n, float *s, size_t bs, const void *vx, size_t bx,
+                                    const void *vy, size_t by, int nrc);
+void ggml_vec_dot_q6_K_q8_K_generic(int n, float *s, size_t bs, const void *vx, size_t bx,
                                     const void *vy, size_t by, int nrc);
 
 static int g_inited = 0;
@@ -59,6 +62,26 @@ float ref_vec_dot_generic(int n, const void *vx, const void *vy) {
     ensure_init();
     float s = 0;
     ggml_vec_dot_q4_K_q8_K_generic(n, &s, 0, vx, 0, vy, 0, 1);
+    return s;
+}
+
+/* the same traits for any weight type (GGML_TYPE_Q4_K = 12, Q6_K = 14) */
+size_t ref_quantize_type(int type, const float *src, void *dst, int64_t nrow, int64_t n_per_row) {
+    ensure_init();
+    return ggml_quantize_chunk((enum ggml_type)type, src, dst, 0, nrow, n_per_row, NULL);
+}
+
+void ref_dequant_type(int type, const void *x, float *y, int64_t k) {
+    ensure_init();
+    ggml_get_type_traits((enum ggml_type)type)->to_float(x, y, k);
+}
+
+float ref_vec_dot_type(int type, int n, const void *vx, const void *vy, int generic) {
+    ensure_init();
+    float s = 0;
+    if (generic && type == GGML_TYPE_Q6_K) ggml_vec_dot_q6_K_q8_K_generic(n, &s, 0, vx, 0, vy, 0, 1);
+    else if (generic) ggml_vec_dot_q4_K_q8_K_generic(n, &s, 0, vx, 0, vy, 0, 1);
+    else ggml_get_type_traits_cpu((enum ggml_type)type)->vec_dot(n, &s, 0, vx, 0, vy, 0, 1);
     return s;
 }
 
@@ -110,11 +133,11 @@ void ref_graph_destroy(void *h) {
 /* n dense matmuls dst_i[T][M_i] = W_i[M_i x K_i] * X_i[T][K_i], all in one
  * graph (computed node after node, as ggml's CPU backend does for a layer).
  * Buffers are the caller's and are used in place. */
-void *ref_mm_create(int n, const void *const *W, const int64_t *M, const int64_t *K,
-                    const float *const *X, float *const *Y, int64_t T, int nthreads) {
+void *ref_mm_create_type(int type, int n, const void *const *W, const int64_t *M, const int64_t *K,
+                         const float *const *X, float *const *Y, int64_t T, int nthreads) {
     ref_graph *g = graph_begin(n);
     for (int i = 0; i < n; ++i) {
-        struct ggml_tensor *w = ggml_new_tensor_2d(g->ctx, GGML_TYPE_Q4_K, K[i], M[i]);
+        struct ggml_tensor *w = ggml_new_tensor_2d(g->ctx, (enum ggml_type)type, K[i], M[i]);
         struct ggml_tensor *x = ggml_new_tensor_2d(g->ctx, GGML_TYPE_F32, K[i], T);
         w->data = (void *)W[i];
         x->data = (void *)X[i];
@@ -126,12 +149,17 @@ void *ref_mm_create(int n, const void *const *W, const int64_t *M, const int64_t
     return g;
 }
 
+void *ref_mm_create(int n, const void *const *W, const int64_t *M, const int64_t *K,
+                    const float *const *X, float *const *Y, int64_t T, int nthreads) {
+    return ref_mm_create_type(GGML_TYPE_Q4_K, n, W, M, K, X, Y, T, nthreads);
+}
+
 /* dst[T][k][M] = mul_mat_id(as[E][M][K], X[T][ne11][K], ids[T][k]) */
-void *ref_mmid_create(const void *as, int64_t M, int64_t K, int64_t E, const float *X,
-                      int64_t ne11, const int32_t *ids, int64_t k, int64_t T, float *Y,
-                      int nthreads) {
+void *ref_mmid_create_type(int type, const void *as, int64_t M, int64_t K, int64_t E, const float *X,
+                           int64_t ne11, const int32_t *ids, int64_t k, int64_t T, float *Y,
+                           int nthreads) {
     ref_graph *g = graph_begin(1);
-    struct ggml_tensor *a = ggml_new_tensor_3d(g->ctx, GGML_TYPE_Q4_K, K, M, E);
+    struct ggml_tensor *a = ggml_new_tensor_3d(g->ctx, (enum ggml_type)type, K, M, E);
     struct ggml_tensor *b = ggml_new_tensor_3d(g->ctx, GGML_TYPE_F32, K, ne11, T);
     struct ggml_tensor *id = ggml_new_tensor_2d(g->ctx, GGML_TYPE_I32, k, T);
     a->data = (void *)as;
@@ -142,6 +170,12 @@ void *ref_mmid_create(const void *as, int64_t M, int64_t K, int64_t E, const flo
     ggml_build_forward_expand(g->gf, y);
     if (graph_finish(g, nthreads) != 0) { ref_graph_destroy(g); return NULL; }
     return g;
+}
+
+void *ref_mmid_create(const void *as, int64_t M, int64_t K, int64_t E, const float *X,
+                      int64_t ne11, const int32_t *ids, int64_t k, int64_t T, float *Y,
+                      int nthreads) {
+    return ref_mmid_create_type(GGML_TYPE_Q4_K, as, M, K, E, X, ne11, ids, k, T, Y, nthreads);
 }
 
 /* Runs the graph iters times; returns the wall seconds of each run in secs. */

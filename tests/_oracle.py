@@ -13,7 +13,10 @@ REF_DIR = os.path.join(REPO, "oracle", "_ref")
 
 QK_K = 256
 Q4K = 144
+Q6K = 210
 Q8K = 292
+TYPE_Q4_K, TYPE_Q6_K = 12, 14            # ggml.h:402-404
+BLOCK_BYTES = {TYPE_Q4_K: Q4K, TYPE_Q6_K: Q6K}
 
 V, I, I64, F, U64 = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_uint64
 
@@ -51,6 +54,19 @@ class Oracle:
         L.or_nearest_int.argtypes = [F]
         L.or_nearest_int.restype = I
         L.or_scale_min_k4.argtypes = [I, V, V, V]
+        for n in ("or_quantize_row_q6K", "or_dequantize_row_q6K"):
+            getattr(L, n).argtypes = [V, V, I64]
+        for n in ("or_vec_dot_q6K_generic", "or_vec_dot_q6K_avx2order"):
+            getattr(L, n).argtypes = [I, V, V]
+            getattr(L, n).restype = F
+        L.or_vec_dot_q6K_exact.argtypes = [I, V, V]
+        L.or_vec_dot_q6K_exact.restype = C.c_double
+        L.or_subblock_sums_q6K.argtypes = [I, V, V, V]
+        L.or_mul_mat_type.argtypes = [I, V, I64, I64, V, I64, V, I]
+        L.or_mul_mat_id_type.argtypes = [I, V, I64, I64, I64, V, I64, V, I64, I64, V, I]
+        L.or_mul_mat_dequant_f64_type.argtypes = [I, V, I64, I64, V, I64, V]
+        for n in ("or_mul_mat_type", "or_mul_mat_id_type", "or_mul_mat_dequant_f64_type"):
+            getattr(L, n).restype = I
         self.L = L
 
     def quantize_q4K(self, x: np.ndarray) -> np.ndarray:
@@ -103,6 +119,57 @@ class Oracle:
         self.L.or_mul_mat_dequant_f64(_p(W), M, K, _p(X), X.shape[0], _p(Y))
         return Y
 
+    # ---- Q6_K (oracle/q6k_oracle.c) and type-generic drivers ----
+    def quantize_q6K(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(x.size // QK_K * Q6K, np.uint8)
+        self.L.or_quantize_row_q6K(_p(x), _p(y), x.size)
+        return y
+
+    def dequant_q6K(self, q: np.ndarray, k: int) -> np.ndarray:
+        y = np.empty(k, np.float32)
+        self.L.or_dequantize_row_q6K(_p(np.ascontiguousarray(q)), _p(y), k)
+        return y
+
+    def vec_dot_q6K(self, n, qx, qy, order="avx2"):
+        f = self.L.or_vec_dot_q6K_avx2order if order == "avx2" else self.L.or_vec_dot_q6K_generic
+        return f(n, _p(qx), _p(qy))
+
+    def vec_dot_q6K_exact(self, n, qx, qy):
+        return self.L.or_vec_dot_q6K_exact(n, _p(qx), _p(qy))
+
+    def subblock_sums_q6K(self, n, qx, qy) -> np.ndarray:
+        S = np.zeros(n // QK_K * 16, np.int32)
+        self.L.or_subblock_sums_q6K(n, _p(qx), _p(qy), _p(S))
+        return S
+
+    def quantize(self, qtype, x):
+        return self.quantize_q6K(x) if qtype == TYPE_Q6_K else self.quantize_q4K(x)
+
+    def to_float(self, qtype, q, k):
+        return self.dequant_q6K(q, k) if qtype == TYPE_Q6_K else self.dequant(q, k)
+
+    def mul_mat_type(self, qtype, W, M, K, X, order=1):
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+        Y = np.empty((X.shape[0], M), np.float32)
+        assert self.L.or_mul_mat_type(qtype, _p(W), M, K, _p(X), X.shape[0], _p(Y), order) == 0
+        return Y
+
+    def mul_mat_id_type(self, qtype, bank, M, K, E, X, ids, order=1):
+        ids = np.ascontiguousarray(ids, np.int32)
+        T, k = ids.shape
+        X = np.ascontiguousarray(X, np.float32).reshape(T, -1, K)
+        Y = np.empty((T, k, M), np.float32)
+        rc = self.L.or_mul_mat_id_type(qtype, _p(bank), M, K, E, _p(X), X.shape[1], _p(ids), k, T, _p(Y), order)
+        assert rc == 0
+        return Y
+
+    def mul_mat_f64_type(self, qtype, W, M, K, X):
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+        Y = np.empty((X.shape[0], M), np.float64)
+        assert self.L.or_mul_mat_dequant_f64_type(qtype, _p(W), M, K, _p(X), X.shape[0], _p(Y)) == 0
+        return Y
+
     def synth(self, n, seed, dist=0, cols=0, mean=0.0, std=1.0, mult=1.0, offset=0) -> np.ndarray:
         out = np.empty(n, np.float32)
         self.L.or_synth_fill(_p(out), n, seed, dist, cols, mean, std, mult, offset)
@@ -145,6 +212,15 @@ class Ref:
         L.ref_mm_create.restype = V
         L.ref_mmid_create.argtypes = [V, I64, I64, I64, V, I64, V, I64, I64, V, I]
         L.ref_mmid_create.restype = V
+        L.ref_quantize_type.argtypes = [I, V, V, I64, I64]
+        L.ref_quantize_type.restype = C.c_size_t
+        L.ref_dequant_type.argtypes = [I, V, V, I64]
+        L.ref_vec_dot_type.argtypes = [I, I, V, V, I]
+        L.ref_vec_dot_type.restype = F
+        L.ref_mm_create_type.argtypes = [I, I, V, V, V, V, V, I64, I]
+        L.ref_mm_create_type.restype = V
+        L.ref_mmid_create_type.argtypes = [I, V, I64, I64, I64, V, I64, V, I64, I64, V, I]
+        L.ref_mmid_create_type.restype = V
         L.ref_graph_run.argtypes = [V, I, V]
         L.ref_graph_run.restype = I
         L.ref_graph_destroy.argtypes = [V]
@@ -172,13 +248,27 @@ class Ref:
         f = self.L.ref_vec_dot_generic if generic else self.L.ref_vec_dot
         return f(n, _p(qx), _p(qy))
 
-    def mul_mat(self, W, M, K, X, nthreads=1):
+    def quantize_type(self, qtype, x, nrow, n_per_row):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(nrow * (n_per_row // QK_K) * BLOCK_BYTES[qtype], np.uint8)
+        self.L.ref_quantize_type(qtype, _p(x), _p(y), nrow, n_per_row)
+        return y
+
+    def dequant_type(self, qtype, q, k):
+        y = np.empty(k, np.float32)
+        self.L.ref_dequant_type(qtype, _p(np.ascontiguousarray(q)), _p(y), k)
+        return y
+
+    def vec_dot_type(self, qtype, n, qx, qy, generic=False):
+        return self.L.ref_vec_dot_type(qtype, n, _p(qx), _p(qy), int(generic))
+
+    def mul_mat(self, W, M, K, X, nthreads=1, qtype=TYPE_Q4_K):
         X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
         T = X.shape[0]
         Y = np.empty((T, M), np.float32)
         arr = lambda ctype, vals: (ctype * 1)(*vals)
-        h = self.L.ref_mm_create(1, arr(V, [W.ctypes.data]), arr(I64, [M]), arr(I64, [K]),
-                                 arr(V, [X.ctypes.data]), arr(V, [Y.ctypes.data]), T, nthreads)
+        h = self.L.ref_mm_create_type(qtype, 1, arr(V, [W.ctypes.data]), arr(I64, [M]), arr(I64, [K]),
+                                      arr(V, [X.ctypes.data]), arr(V, [Y.ctypes.data]), T, nthreads)
         assert h
         try:
             assert self.L.ref_graph_run(h, 1, None) == 0
@@ -186,12 +276,13 @@ class Ref:
             self.L.ref_graph_destroy(h)
         return Y
 
-    def mul_mat_id(self, bank, M, K, E, X, ids, nthreads=1):
+    def mul_mat_id(self, bank, M, K, E, X, ids, nthreads=1, qtype=TYPE_Q4_K):
         ids = np.ascontiguousarray(ids, np.int32)
         T, k = ids.shape
         X = np.ascontiguousarray(X, np.float32).reshape(T, -1, K)
         Y = np.empty((T, k, M), np.float32)
-        h = self.L.ref_mmid_create(_p(bank), M, K, E, _p(X), X.shape[1], _p(ids), k, T, _p(Y), nthreads)
+        h = self.L.ref_mmid_create_type(qtype, _p(bank), M, K, E, _p(X), X.shape[1], _p(ids), k, T, _p(Y),
+                                        nthreads)
         assert h
         try:
             assert self.L.ref_graph_run(h, 1, None) == 0

@@ -1,5 +1,6 @@
 #!/usr/bin/env python3
-"""Writes tests/golden/q4k_golden.npz from the reference's own ggml CPU code.
+"""Writes tests/golden/q4k_golden.npz and q6k_golden.npz from the reference's
+own ggml CPU code.
 
 The reference (vendor/ggml of nihilistau/shannon-prime-burnhard) is compiled
 from its sources by oracle/Makefile (`make -C oracle ref`) into oracle/_ref;
@@ -18,6 +19,13 @@ Contents (all produced by the reference):
                    ggml_vec_dot_q4_K_q8_K_generic, one row per case
   mm_*             GGML_OP_MUL_MAT through ggml_graph_compute (1 thread)
   mmid_*           GGML_OP_MUL_MAT_ID through ggml_graph_compute (1 thread)
+
+q6k_golden.npz holds the same kinds of vectors for GGML_TYPE_Q6_K
+(quantize_q6_K / quantize_row_q6_K_ref, dequantize_row_q6_K,
+ggml_vec_dot_q6_K_q8_K and its _generic form, MUL_MAT, MUL_MAT_ID), plus
+vec_dot cases on random block bytes that reach every scale and 6-bit value.
+
+Usage: gen_golden.py [q4k] [q6k]   (default: both)
 """
 import os
 import sys
@@ -26,7 +34,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
-from _oracle import Ref, ref_library_path  # noqa: E402
+from _oracle import TYPE_Q6_K, Q6K, Ref, ref_library_path  # noqa: E402
 
 QK = 256
 
@@ -64,10 +72,99 @@ def q8_inputs(rng):
     return np.concatenate(c)
 
 
+def q6k_encoder_inputs(rng):
+    rows = [(rng.standard_normal((8, 4096)) * 0.02).astype(np.float32).ravel()]
+    t = (rng.standard_t(4, size=(4, 5120)) * 0.02).astype(np.float32)
+    t[:, ::53] *= 8.0
+    rows.append(t.ravel())
+    edge = [np.zeros(QK, np.float32), np.full(QK, 0.25, np.float32), np.full(QK, -0.25, np.float32)]
+    s = np.zeros(QK, np.float32); s[100] = 3.0; edge.append(s)                        # single spike
+    s = np.zeros(QK, np.float32); s[7] = -3.0; edge.append(s)                         # negative spike
+    edge.append(np.abs(rng.standard_normal(QK)).astype(np.float32))                   # all >= 0
+    edge.append(-np.abs(rng.standard_normal(QK)).astype(np.float32))                  # all <= 0
+    edge.append((rng.standard_normal(QK) * 1e-6).astype(np.float32))                  # tiny
+    edge.append((rng.standard_normal(QK) * 1e-17).astype(np.float32))                 # below the 1e-15 cut
+    edge.append((rng.standard_normal(QK) * 100.0).astype(np.float32))                 # large
+    z = rng.standard_normal(QK).astype(np.float32); z[48:64] = 0.0; edge.append(z)    # one zero sub-block
+    z = rng.standard_normal(QK).astype(np.float32); z[::16] *= 50; edge.append(z)     # one spike per sub-block
+    edge.append(np.linspace(-1, 1, QK, dtype=np.float32))                             # ramp
+    rows.append(np.stack(edge).ravel())
+    return np.concatenate(rows).astype(np.float32)
+
+
+def gen_q6k(ref, rng):
+    out = {}
+    x = q6k_encoder_inputs(rng)
+    out["enc_x"] = x
+    out["enc_q"] = ref.quantize_type(TYPE_Q6_K, x, 1, x.size)
+
+    rb = rng.integers(0, 256, size=(64, Q6K), dtype=np.uint8)
+    rb[:, 209] &= 0xBF                                                                  # finite fp16 d
+    q = np.concatenate([out["enc_q"].reshape(-1, Q6K), rb]).ravel()
+    out["deq_q"] = q
+    out["deq_y"] = ref.dequant_type(TYPE_Q6_K, q, q.size // Q6K * QK)
+
+    # vec_dot: encoder output at K in {256, 768, 4096, 27648}, then random
+    # block bytes (every scale -128..127 and 6-bit value) against Q8_K of
+    # N(0,1) and of one-sign inputs
+    vq6, vq8, vK, va, vg = [], [], [], [], []
+    cases = [(K, n, "enc") for K, n in ((256, 8), (768, 8), (4096, 8), (27648, 4))]
+    cases += [(K, n, "rand") for K, n in ((256, 8), (4096, 8))]
+    for K, n, kind in cases:
+        for i in range(n):
+            if kind == "enc":
+                w = ref.quantize_type(TYPE_Q6_K, (rng.standard_normal(K) * 0.02).astype(np.float32), 1, K)
+            else:
+                w = rng.integers(0, 256, size=(K // QK, Q6K), dtype=np.uint8)
+                w[:, 209] &= 0x3B                                                       # |d| < 2^-1
+                w = w.ravel()
+            xa = rng.standard_normal(K).astype(np.float32)
+            if kind == "rand" and i % 2:
+                xa = np.abs(xa)
+            a = ref.quantize_q8K(xa)
+            vq6.append(w); vq8.append(a); vK.append(K)
+            va.append(ref.vec_dot_type(TYPE_Q6_K, K, w, a)); vg.append(ref.vec_dot_type(TYPE_Q6_K, K, w, a, True))
+    out["vd_q6"] = np.concatenate(vq6)
+    out["vd_q8"] = np.concatenate(vq8)
+    out["vd_K"] = np.array(vK, np.int64)
+    out["vd_avx2"] = np.array(va, np.float32)
+    out["vd_generic"] = np.array(vg, np.float32)
+
+    M, K = 64, 512
+    W = ref.quantize_type(TYPE_Q6_K, (rng.standard_normal((M, K)) * 0.02).astype(np.float32), M, K)
+    out["mm_W"] = W
+    out["mm_MK"] = np.array([M, K], np.int64)
+    for T in (1, 3, 8, 17):
+        X = rng.standard_normal((T, K)).astype(np.float32)
+        out[f"mm_X{T}"] = X
+        out[f"mm_Y{T}"] = ref.mul_mat(W, M, K, X, qtype=TYPE_Q6_K)
+
+    E, M, K, T = 8, 32, 512, 3
+    bank = ref.quantize_type(TYPE_Q6_K, (rng.standard_normal((E * M, K)) * 0.02).astype(np.float32), E * M, K)
+    out["mmid_bank"] = bank
+    out["mmid_EMK"] = np.array([E, M, K], np.int64)
+    for n_used, ne11 in ((2, 1), (4, 4)):
+        ids = np.stack([rng.permutation(E)[:n_used] for _ in range(T)]).astype(np.int32)
+        X = rng.standard_normal((T, ne11, K)).astype(np.float32)
+        tag = f"{n_used}_{ne11}"
+        out[f"mmid_ids_{tag}"] = ids
+        out[f"mmid_X_{tag}"] = X
+        out[f"mmid_Y_{tag}"] = ref.mul_mat_id(bank, M, K, E, X, ids, qtype=TYPE_Q6_K)
+    return out
+
+
 def main():
     if ref_library_path() is None:
         sys.exit("oracle/_ref is not built (make -C oracle ref)")
+    which = set(sys.argv[1:]) or {"q4k", "q6k"}
     ref = Ref()
+    if "q6k" in which:
+        out = gen_q6k(ref, np.random.default_rng(0x6B6B))
+        path = os.path.join(HERE, "q6k_golden.npz")
+        np.savez_compressed(path, **out)
+        print(f"wrote {path} ({os.path.getsize(path)/1024:.0f} KiB, {len(out)} arrays) using {ref.path}")
+    if "q4k" not in which:
+        return
     rng = np.random.default_rng(0xDEADBEEF)
     out = {}
 
