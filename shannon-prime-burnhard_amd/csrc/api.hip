@@ -44,6 +44,8 @@ struct spq4k_weights {
     int device = 0;              // weights may outlive the context that made them
     uint8_t* data = nullptr;
     bool owned = false;
+    int type = SPQ4K_TYPE_Q4_K;  // ggml type id
+    int fmt = WF_Q4K;            // kernel format of that type
     int64_t M = 0, K = 0, E = 0;
     size_t nbytes = 0;
 };
@@ -71,6 +73,14 @@ int hip_fail(spq4k_ctx* c, hipError_t e, const char* what) {
     } while (0)
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// weight types the kernels take: kernel format and block bytes, -1 / 0 otherwise
+int type_fmt(int type) {
+    return type == SPQ4K_TYPE_Q4_K ? WF_Q4K : type == SPQ4K_TYPE_Q6_K ? WF_Q6K : -1;
+}
+size_t type_block_bytes(int type) {
+    return type == SPQ4K_TYPE_Q4_K ? SPQ4K_Q4K_BLOCK_BYTES : type == SPQ4K_TYPE_Q6_K ? SPQ4K_Q6K_BLOCK_BYTES : 0;
+}
 
 int use_device(spq4k_ctx* c) {
     if (!c) return -EINVAL;
@@ -155,7 +165,7 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
 //   K = 12288              : 16 waves, x-first: 48 KB of x per CU would
 //                            otherwise queue behind the CU's weight loads
 //   K = 27648              : 8 waves (the registers of 7 Q8_K blocks a lane), x-first
-DecodeCfg plan_decode(const spq4k_ctx* c, int nb, int64_t rows) {
+DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb, int64_t rows) {
     DecodeCfg d;
     if (nb > 48) {
         d.waves = 8; d.depth = 1; d.xfirst = true;
@@ -180,6 +190,11 @@ DecodeCfg plan_decode(const spq4k_ctx* c, int nb, int64_t rows) {
         d.waves = 8;
         d.depth = 1;
     }
+    // Q6_K at K = 12288 (15 + 21 registers a block): 12 waves, one row in flight
+    if (fmt == WF_Q6K && nb >= 48 && (d.waves == 16 || (d.waves == 12 && d.depth == 2))) {
+        d.waves = 12;
+        d.depth = 1;
+    }
     const int64_t wgs = (rows + d.waves - 1) / d.waves;
     d.grid = (int)(wgs < c->num_cus ? wgs : c->num_cus);
     if (c->dec_force.grid) d.grid = c->dec_force.grid;
@@ -199,6 +214,7 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
     for (int i = 0; i < n; ++i) {
         if (!W[i] || !W[i]->data || !y || !y[i]) return set_err(c, -EINVAL, "gemv: null weight or output");
         if (W[i]->K != K || W[i]->E != 1) return set_err(c, -EINVAL, "gemv: matrices must share K and have E=1");
+        if (W[i]->type != W[0]->type) return set_err(c, -EINVAL, "gemv: matrices must share the weight type");
         if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemv: weights not 16-byte aligned");
         if (W[i]->device != c->device) return set_err(c, -EINVAL, "gemv: weights live on another device");
         Ms[i] = W[i]->M;
@@ -224,18 +240,19 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
     p.X = x;
     p.x_tstride = K;
     p.total_rows = (int32_t)total;
+    p.fmt = W[0]->fmt;
     for (int i = n; i < GEMV_MAX_SEG; ++i) {   // unused segments: never selected
         p.seg[i] = p.seg[0];
         p.seg[i].row_begin = INT32_MAX;
         p.seg[i].tile_begin = INT32_MAX;
     }
-    if (T == 1 && !c->no_decode && c->preq_mode != 1 && decode_supported(p.nb)) {
-        const DecodeCfg dc = plan_decode(c, p.nb, total);
+    if (T == 1 && !c->no_decode && c->preq_mode != 1 && decode_supported(p.fmt, p.nb)) {
+        const DecodeCfg dc = plan_decode(c, p.fmt, p.nb, total);
         hipError_t e = launch_gemv_decode(p, dc, c->stream);
         if (e != hipSuccess) return hip_fail(c, e, "gemv decode launch");
         return 0;
     }
-    if (T >= c->gemv_mfma_min_t && c->force_bpr == 0) {
+    if (p.fmt == WF_Q4K && T >= c->gemv_mfma_min_t && c->force_bpr == 0) {
         // 4 <= T <= 8: the sdot4 kernel's integer work grows with T while the
         // matrix cores' 16-token tile costs the same from T = 1 to 16
         return gemm_segments(c, n, W, x, y, T, c->gemm_mode == 1 ? 1 : 0);
@@ -253,6 +270,57 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
     }
     hipError_t e = launch_gemv(p, (int)T, bpr, (int)tiles, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "gemv launch");
+    return 0;
+}
+
+// Batches of more than SPQ4K_GEMV_MAX_T tokens for formats without a
+// matrix-core kernel (Q6_K): X is quantised once into Q8_K planes, then the
+// sdot4 GEMV runs over slices of 8 tokens of those planes.
+int gemv_chunked(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T) {
+    const int64_t K = W[0]->K;
+    const int nb = (int)(K / SPQ4K_QK_K);
+    int64_t Ms[GEMV_MAX_SEG];
+    for (int i = 0; i < n; ++i) Ms[i] = W[i]->M;
+    const int bpr = pick_bpr(c, Ms, n);
+    const int rows = gemv_rows_per_tile(bpr);
+    GemvParams p;
+    memset(&p, 0, sizeof p);
+    int64_t tiles = 0, total = 0;
+    for (int i = 0; i < n; ++i) {
+        p.seg[i].W = W[i]->data;
+        p.seg[i].M = (int32_t)W[i]->M;
+        p.seg[i].y_tstride = W[i]->M;
+        p.seg[i].tile_begin = (int32_t)tiles;
+        p.seg[i].row_begin = (int32_t)total;
+        tiles += (W[i]->M + rows - 1) / rows;
+        total += W[i]->M;
+    }
+    if (tiles > (1ll << 31) - 1 || total > (1ll << 31) - 1) return set_err(c, -EINVAL, "gemv: too many rows");
+    for (int i = n; i < GEMV_MAX_SEG; ++i) {
+        p.seg[i] = p.seg[0];
+        p.seg[i].row_begin = INT32_MAX;
+        p.seg[i].tile_begin = INT32_MAX;
+    }
+    p.nseg = n;
+    p.nb = nb;
+    p.x_tstride = K;
+    p.total_rows = (int32_t)total;
+    p.fmt = W[0]->fmt;
+    const int cb_max = LDS_BUDGET / (SPQ4K_GEMV_MAX_T * 292);
+    p.chunk_blocks = nb < cb_max ? nb : cb_max;
+    Q8Planes Q;
+    int rc = q8_planes(c, X, K, (int)T, nb, &Q);
+    if (rc) return rc;
+    for (int64_t t0 = 0; t0 < T; t0 += SPQ4K_GEMV_MAX_T) {
+        const int tc = (int)(T - t0 < SPQ4K_GEMV_MAX_T ? T - t0 : SPQ4K_GEMV_MAX_T);
+        p.Q.qs = Q.qs + t0 * nb * 256;
+        p.Q.bs = Q.bs + t0 * nb * 16;
+        p.Q.d = Q.d + t0 * nb;
+        for (int i = 0; i < n; ++i) p.seg[i].Y = Y[i] + t0 * W[i]->M;
+        for (int i = n; i < GEMV_MAX_SEG; ++i) p.seg[i].Y = p.seg[0].Y;
+        hipError_t e = launch_gemv(p, tc, bpr, (int)tiles, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemv launch");
+    }
     return 0;
 }
 
@@ -351,27 +419,34 @@ int spq4k_synchronize(spq4k_ctx* c) {
 const char* spq4k_last_error(const spq4k_ctx* c) { return c ? c->err : "null context"; }
 
 // ---- weights -----------------------------------------------------------------
-static int weights_new(spq4k_ctx* c, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
+static int weights_new(spq4k_ctx* c, int type, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
     if (!out) return set_err(c, -EINVAL, "weights: null out");
     *out = nullptr;
+    if (type_fmt(type) < 0) return set_err(c, -EINVAL, "weights: unsupported type %d (Q4_K = 12, Q6_K = 14)", type);
     int rc = check_shape(c, M, K, E);
     if (rc) return rc;
     spq4k_weights* w = new (std::nothrow) spq4k_weights();
     if (!w) return -ENOMEM;
     w->device = c->device;
+    w->type = type;
+    w->fmt = type_fmt(type);
     w->M = M;
     w->K = K;
     w->E = E;
-    w->nbytes = (size_t)E * (size_t)M * (size_t)(K / SPQ4K_QK_K) * SPQ4K_Q4K_BLOCK_BYTES;
+    w->nbytes = (size_t)E * (size_t)M * (size_t)(K / SPQ4K_QK_K) * type_block_bytes(type);
     *out = w;
     return 0;
 }
 
 int spq4k_weights_alloc(spq4k_ctx* c, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
+    return spq4k_weights_alloc_type(c, SPQ4K_TYPE_Q4_K, M, K, E, out);
+}
+
+int spq4k_weights_alloc_type(spq4k_ctx* c, int type, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
     int rc = use_device(c);
     if (rc) return rc;
     spq4k_weights* w;
-    rc = weights_new(c, M, K, E, &w);
+    rc = weights_new(c, type, M, K, E, &w);
     if (rc) return rc;
     if (hipMalloc(&w->data, w->nbytes) != hipSuccess) {
         delete w;
@@ -383,8 +458,13 @@ int spq4k_weights_alloc(spq4k_ctx* c, int64_t M, int64_t K, int64_t E, spq4k_wei
 }
 
 int spq4k_weights_upload(spq4k_ctx* c, const void* host, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
+    return spq4k_weights_upload_type(c, SPQ4K_TYPE_Q4_K, host, M, K, E, out);
+}
+
+int spq4k_weights_upload_type(spq4k_ctx* c, int type, const void* host, int64_t M, int64_t K, int64_t E,
+                              spq4k_weights** out) {
     if (!host) return set_err(c, -EINVAL, "weights_upload: null host pointer");
-    int rc = spq4k_weights_alloc(c, M, K, E, out);
+    int rc = spq4k_weights_alloc_type(c, type, M, K, E, out);
     if (rc) return rc;
     hipError_t e = hipMemcpyAsync((*out)->data, host, (*out)->nbytes, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
@@ -397,8 +477,13 @@ int spq4k_weights_upload(spq4k_ctx* c, const void* host, int64_t M, int64_t K, i
 }
 
 int spq4k_weights_wrap(spq4k_ctx* c, const void* dev, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
+    return spq4k_weights_wrap_type(c, SPQ4K_TYPE_Q4_K, dev, M, K, E, out);
+}
+
+int spq4k_weights_wrap_type(spq4k_ctx* c, int type, const void* dev, int64_t M, int64_t K, int64_t E,
+                            spq4k_weights** out) {
     if (!dev || !aligned(dev, 16)) return set_err(c, -EINVAL, "weights_wrap: null or not 16-byte aligned");
-    int rc = weights_new(c, M, K, E, out);
+    int rc = weights_new(c, type, M, K, E, out);
     if (rc) return rc;
     (*out)->data = (uint8_t*)dev;
     (*out)->owned = false;
@@ -416,6 +501,7 @@ void spq4k_weights_free(spq4k_weights* w) {
 }
 
 void* spq4k_weights_data(const spq4k_weights* w) { return w ? (void*)w->data : nullptr; }
+int spq4k_weights_type(const spq4k_weights* w) { return w ? w->type : -EINVAL; }
 size_t spq4k_weights_nbytes(const spq4k_weights* w) { return w ? w->nbytes : 0; }
 
 // ---- type traits ---------------------------------------------------------------
@@ -537,6 +623,100 @@ int spq4k_vec_dot_host(spq4k_ctx* c, int n, float* s, const void* vx, const void
     return 0;
 }
 
+// ---- type traits of any supported weight type ------------------------------------
+int spq4k_to_float(spq4k_ctx* c, int type, const void* vx, float* y, int64_t k) {
+    if (type == SPQ4K_TYPE_Q4_K) return spq4k_dequant(c, vx, y, k);
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (type != SPQ4K_TYPE_Q6_K) return set_err(c, -EINVAL, "to_float: unsupported type %d", type);
+    if (!vx || !y || k < 0 || k % SPQ4K_QK_K || !aligned(vx, 2) || !aligned(y, 16))
+        return set_err(c, -EINVAL, "to_float: bad arguments");
+    hipError_t e = launch_dequant_q6k((const uint8_t*)vx, y, k / SPQ4K_QK_K, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "dequant_q6k launch");
+    return 0;
+}
+
+int spq4k_quantize_chunk(spq4k_ctx* c, int type, const float* src, void* dst, int64_t nrow, int64_t n_per_row) {
+    if (type == SPQ4K_TYPE_Q4_K) return spq4k_quantize_q4K(c, src, dst, nrow, n_per_row);
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (type != SPQ4K_TYPE_Q6_K) return set_err(c, -EINVAL, "quantize_chunk: unsupported type %d", type);
+    if (!src || !dst || nrow < 0 || n_per_row <= 0 || n_per_row % SPQ4K_QK_K || !aligned(src, 16) ||
+        !aligned(dst, 2))
+        return set_err(c, -EINVAL, "quantize_chunk: bad arguments");
+    hipError_t e = launch_quantize_q6k(src, (uint8_t*)dst, nrow * (n_per_row / SPQ4K_QK_K), c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "quantize_q6k launch");
+    return 0;
+}
+
+int spq4k_vec_dot_q8K(spq4k_ctx* c, int type, int n, float* s, const void* vx, const void* vy) {
+    if (type == SPQ4K_TYPE_Q4_K) return spq4k_vec_dot(c, n, s, vx, vy);
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (type != SPQ4K_TYPE_Q6_K) return set_err(c, -EINVAL, "vec_dot_q8K: unsupported type %d", type);
+    if (!s || !vx || !vy || n <= 0 || n % SPQ4K_QK_K || !aligned(vx, 2) || !aligned(vy, 4))
+        return set_err(c, -EINVAL, "vec_dot_q8K: bad arguments");
+    hipError_t e = launch_vec_dot_q6k((const uint8_t*)vx, (const uint8_t*)vy, n / SPQ4K_QK_K, s, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "vec_dot_q6k launch");
+    return 0;
+}
+
+int spq4k_to_float_host(spq4k_ctx* c, int type, const void* vx, float* y, int64_t k) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    const size_t bb = type_block_bytes(type);
+    if (!vx || !y || k < 0 || k % SPQ4K_QK_K || !bb) return set_err(c, -EINVAL, "to_float_host: bad arguments");
+    const size_t nin = (size_t)(k / SPQ4K_QK_K) * bb, nout = (size_t)k * sizeof(float);
+    DevBuf a, b;
+    if (hipMalloc(&a.p, nin + 16) != hipSuccess || hipMalloc(&b.p, nout + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "to_float_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, vx, nin, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_to_float(c, type, a.p, (float*)b.p, k);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(y, b.p, nout, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int spq4k_quantize_chunk_host(spq4k_ctx* c, int type, const float* src, void* dst, int64_t nrow, int64_t n_per_row) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    const size_t bb = type_block_bytes(type);
+    if (!src || !dst || nrow < 0 || n_per_row <= 0 || n_per_row % SPQ4K_QK_K || !bb)
+        return set_err(c, -EINVAL, "quantize_chunk_host: bad arguments");
+    const int64_t k = nrow * n_per_row;
+    const size_t nin = (size_t)k * sizeof(float), nout = (size_t)(k / SPQ4K_QK_K) * bb;
+    DevBuf a, b;
+    if (hipMalloc(&a.p, nin + 16) != hipSuccess || hipMalloc(&b.p, nout + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "quantize_chunk_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, src, nin, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_quantize_chunk(c, type, (const float*)a.p, b.p, nrow, n_per_row);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(dst, b.p, nout, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int spq4k_vec_dot_q8K_host(spq4k_ctx* c, int type, int n, float* s, const void* vx, const void* vy) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    const size_t bb = type_block_bytes(type);
+    if (!s || !vx || !vy || n <= 0 || n % SPQ4K_QK_K || !bb) return set_err(c, -EINVAL, "vec_dot_q8K_host: bad arguments");
+    const size_t nx = (size_t)(n / SPQ4K_QK_K) * bb;
+    const size_t ny = (size_t)(n / SPQ4K_QK_K) * SPQ4K_Q8K_BLOCK_BYTES;
+    DevBuf a, b, o;
+    if (hipMalloc(&a.p, nx + 16) != hipSuccess || hipMalloc(&b.p, ny + 16) != hipSuccess ||
+        hipMalloc(&o.p, 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "vec_dot_q8K_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, vx, nx, hipMemcpyHostToDevice, c->stream));
+    SPQ_HIP(c, hipMemcpyAsync(b.p, vy, ny, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_vec_dot_q8K(c, type, n, (float*)o.p, a.p, b.p);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(s, o.p, sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
 // ---- matmul ----------------------------------------------------------------------
 int spq4k_gemv(spq4k_ctx* c, const spq4k_weights* W, const float* x, float* y, int64_t T) {
     int rc = use_device(c);
@@ -623,8 +803,13 @@ int spq4k_gemm_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const f
     for (int i = 0; i < n; ++i) {
         if (!W[i] || !W[i]->data || !Y[i] || W[i]->E != 1 || W[i]->K != K)
             return set_err(c, -EINVAL, "gemm: matrices must be non-null, E=1 and share K");
+        if (W[i]->type != W[0]->type) return set_err(c, -EINVAL, "gemm: matrices must share the weight type");
         if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemm: misaligned weights");
         if (W[i]->device != c->device) return set_err(c, -EINVAL, "gemm: weights live on another device");
+    }
+    if (W[0]->fmt == WF_Q6K) {
+        if (T <= SPQ4K_GEMV_MAX_T) return gemv_launch(c, n, W, X, Y, T);
+        return gemv_chunked(c, n, W, X, Y, T);
     }
     return gemm_segments(c, n, W, X, Y, T, c->gemm_mode);
 }
@@ -652,6 +837,7 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
         return set_err(c, -EINVAL, "moe: misaligned pointer");
     if (bank->E > 4096 || T * n_used > (1 << 24)) return set_err(c, -EINVAL, "moe: too many experts or pairs");
     const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
+    const size_t bb = type_block_bytes(bank->type);
     const int64_t rows = T * ne11, n_pairs = T * n_used;
     // pairs per expert are at most T: chunk width TC, rows per tile from the
     // number of experts that can be active
@@ -673,7 +859,8 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
         f.ids = ids;
         f.X = X;
         f.bank = bank->data;
-        f.expert_bytes = (size_t)M * nb * SPQ4K_Q4K_BLOCK_BYTES;
+        f.expert_bytes = (size_t)M * nb * bb;
+        f.fmt = bank->fmt;
         f.Y = Y;
         f.n_pairs = (int32_t)n_pairs;
         f.n_used = (int32_t)n_used;
@@ -697,7 +884,8 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
         f.ids = ids;
         f.X = X;
         f.bank = bank->data;
-        f.expert_bytes = (size_t)M * nb * SPQ4K_Q4K_BLOCK_BYTES;
+        f.expert_bytes = (size_t)M * nb * bb;
+        f.fmt = bank->fmt;
         f.Y = Y;
         f.n_pairs = (int32_t)n_pairs;
         f.n_used = (int32_t)n_used;
@@ -731,8 +919,8 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     p.route.act_off = rt + 1 + E;
     p.route.act_cnt = rt + 1 + 2 * E;
     p.route.pairs = rt + 1 + 3 * E;
-    // matrix cores unless the sdot4 kernels are asked for (SPQ4K_MOE_UNFUSED)
-    const bool ring = !c->moe_unfused;
+    // matrix cores (Q4_K) unless the sdot4 kernels are asked for (SPQ4K_MOE_UNFUSED)
+    const bool ring = !c->moe_unfused && bank->fmt == WF_Q4K;
     hipError_t e;
     if (!ring) {
         e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, mn, false, c->stream);
@@ -741,7 +929,8 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
         if (e != hipSuccess) return hip_fail(c, e, "moe route launch");
     }
     p.bank = bank->data;
-    p.expert_bytes = (size_t)M * nb * SPQ4K_Q4K_BLOCK_BYTES;
+    p.expert_bytes = (size_t)M * nb * bb;
+    p.fmt = bank->fmt;
     p.Y = Y;
     p.Q.qs = qs;
     p.Q.bs = bs;
@@ -824,6 +1013,20 @@ int spq4k_subblock_sums(spq4k_ctx* c, const void* W, int64_t M, int64_t K, const
     if (!W || !x || !S || !aligned(W, 16) || !aligned(x, 16)) return set_err(c, -EINVAL, "subblock_sums: bad pointers");
     hipError_t e = launch_subblock_sums((const uint8_t*)W, (int)M, (int)(K / SPQ4K_QK_K), x, S, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "subblock_sums launch");
+    return 0;
+}
+
+int spq4k_subblock_sums_type(spq4k_ctx* c, int type, const void* W, int64_t M, int64_t K, const float* x,
+                             int32_t* S) {
+    if (type == SPQ4K_TYPE_Q4_K) return spq4k_subblock_sums(c, W, M, K, x, S);
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (type != SPQ4K_TYPE_Q6_K) return set_err(c, -EINVAL, "subblock_sums: unsupported type %d", type);
+    rc = check_shape(c, M, K, 1);
+    if (rc) return rc;
+    if (!W || !x || !S || !aligned(W, 2) || !aligned(x, 16)) return set_err(c, -EINVAL, "subblock_sums: bad pointers");
+    hipError_t e = launch_subblock_sums_q6k((const uint8_t*)W, (int)M, (int)(K / SPQ4K_QK_K), x, S, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "subblock_sums_q6k launch");
     return 0;
 }
 

@@ -211,20 +211,23 @@ __device__ __forceinline__ void block_dot(const W4& w, int l4, const Q8Lds& L, i
 // the weight prefetch would stall staging until every weight byte had landed.
 // Weight loads are software-pipelined in two register sets of U blocks;
 // addresses are clamped in bounds and out-of-range blocks contribute zero.
-template <int T, int BPR, int U, typename PreFn, typename FinFn>
+// Fmt is the weight format (FmtQ4K below, FmtQ6K in q6k_core.h): its block
+// size, lane loads and the per-block dot against staged activations.
+template <typename Fmt, int T, int BPR, int U, typename PreFn, typename FinFn>
 __device__ __forceinline__ void stream_row(const uint8_t* __restrict__ wrow, bool row_ok, int l4, int bsub, int nb,
                                            int CB, const Q8Lds& L, float (&acc)[T], PreFn pre, FinFn fin) {
+    using W = typename Fmt::W;
     for (int c0 = 0; c0 < nb; c0 += CB) {
         const int nblk = min(nb, c0 + CB) - c0;
         const int niter = (nblk + BPR - 1) / BPR;   // same for every lane
-        const uint8_t* __restrict__ wc = wrow + (size_t)c0 * Q4K_BYTES;
+        const uint8_t* __restrict__ wc = wrow + (size_t)c0 * Fmt::BYTES;
         auto blk_of = [&](int it) { return min(bsub + BPR * it, nblk - 1); };
 
         auto xr = pre(c0, nblk);
-        W4 A[U], B[U];
+        W A[U], B[U];
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            if (u < niter) A[u] = load_w4(wc + (size_t)blk_of(u) * Q4K_BYTES, l4);
+            if (u < niter) A[u] = Fmt::load(wc + (size_t)blk_of(u) * Fmt::BYTES, l4);
 
         __syncthreads();  // previous chunk's LDS reads are done
         fin(c0, nblk, xr);
@@ -233,24 +236,24 @@ __device__ __forceinline__ void stream_row(const uint8_t* __restrict__ wrow, boo
         for (int i = 0; i < niter; i += 2 * U) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                if (i + U + u < niter) B[u] = load_w4(wc + (size_t)blk_of(i + U + u) * Q4K_BYTES, l4);
+                if (i + U + u < niter) B[u] = Fmt::load(wc + (size_t)blk_of(i + U + u) * Fmt::BYTES, l4);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int it = i + u;
                 if (it < niter) {
                     const int raw = bsub + BPR * it;
-                    block_dot<T>(A[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
+                    Fmt::template dot<T>(A[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
                 }
             }
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                if (i + 2 * U + u < niter) A[u] = load_w4(wc + (size_t)blk_of(i + 2 * U + u) * Q4K_BYTES, l4);
+                if (i + 2 * U + u < niter) A[u] = Fmt::load(wc + (size_t)blk_of(i + 2 * U + u) * Fmt::BYTES, l4);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int it = i + U + u;
                 if (it < niter) {
                     const int raw = bsub + BPR * it;
-                    block_dot<T>(B[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
+                    Fmt::template dot<T>(B[u], l4, L, min(raw, nblk - 1), CB, row_ok && raw < nblk, acc);
                 }
             }
         }
@@ -420,5 +423,25 @@ __device__ __forceinline__ void stage_q8_from_planes(const Q8Planes& P, int nb, 
         for (int i = tid; i < nblk; i += NT) L.d8[t * slot_stride + i] = sd[i];
     }
 }
+
+// ---------------------------------------------------------------------------
+// Weight-format policy of Q4_K for the kernels shared with other formats
+// (stream_row, the decode kernels): block bytes, a lane's loads, the
+// register-activation dot and the LDS-activation dot over T tokens.
+struct FmtQ4K {
+    static constexpr int BYTES = Q4K_BYTES;
+    using W = W4;
+    using R = Q8Reg;
+    static __device__ __forceinline__ W load(const uint8_t* blk, int l4) { return load_w4(blk, l4); }
+    static __device__ __forceinline__ void load_reg(const Q8Lds& L, int b, int l4, R& q) { load_q8reg(L, b, l4, q); }
+    static __device__ __forceinline__ float dot_reg(const W& w, int l4, const R& q, float acc) {
+        return block_dot_reg(w, l4, q, acc);
+    }
+    template <int T>
+    static __device__ __forceinline__ void dot(const W& w, int l4, const Q8Lds& L, int bb, int CB, bool live,
+                                               float (&acc)[T]) {
+        block_dot<T>(w, l4, L, bb, CB, live, acc);
+    }
+};
 
 }  // namespace spq4k

@@ -1,4 +1,4 @@
-// k_gemv.hip — fused Q4_K GEMV for decode (T <= 8 tokens) on gfx950.
+// k_gemv.hip — fused Q4_K / Q6_K GEMV for decode (T <= 8 tokens) on gfx950.
 //
 // Replaces, for GGML_TYPE_Q4_K, the work of ggml_compute_forward_mul_mat
 // (vendor/ggml/src/ggml-cpu/ggml-cpu.c:1241-1439: Q8_K conversion of src1, then
@@ -22,13 +22,17 @@
 // BPR trades rows per workgroup against redundant activation quantisation:
 // the host picks it so that small matrices still launch >= 2 workgroups
 // per CU and large ones quantise x as few times as possible.
+// The kernels are templates over the weight format (FmtQ4K, FmtQ6K): the same
+// lane mapping serves Q6_K blocks (q6k_core.h), whose CPU counterpart is
+// ggml_vec_dot_q6_K_q8_K (ggml-cpu/arch/x86/quants.c:2288).
 #include "gemv_core.h"
 #include "launch.h"
+#include "q6k_core.h"
 
 namespace spq4k {
 
-template <int T, int BPR, int WAVES, int U, bool PREQ>
-__global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
+template <typename Fmt, int T, int BPR, int WAVES, int U, bool PREQ>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
     extern __shared__ __align__(16) char smem[];
     constexpr int LPR = 4 * BPR;         // lanes per row
     constexpr int RPW = 64 / LPR;        // rows per wave
@@ -53,7 +57,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
     const bool row_ok = row < M;
 
     const int nb = p.nb;
-    const size_t row_bytes = (size_t)nb * Q4K_BYTES;
+    const size_t row_bytes = (size_t)nb * Fmt::BYTES;
     // rows past M re-read row M-1 (in bounds) and contribute nothing
     const uint8_t* __restrict__ wrow = W + (size_t)(row_ok ? row : M - 1) * row_bytes;
 
@@ -64,11 +68,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
     const int CB = p.chunk_blocks;
     const Q8Lds L = q8lds_carve(smem, T * CB);
     if (PREQ) {
-        stream_row<T, BPR, U>(
+        stream_row<Fmt, T, BPR, U>(
             wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int, int) { return 0; },
             [&](int c0, int nblk, int) { stage_q8_from_planes<WAVES * 64>(p.Q, nb, T, c0, nblk, L, CB); });
     } else {
-        stream_row<T, BPR, U>(
+        stream_row<Fmt, T, BPR, U>(
             wrow, row_ok, l4, bsub, nb, CB, L, acc,
             [&](int c0, int nblk) { return stage_f32_load<WAVES>(p.X, p.x_tstride, T, c0, nblk); },
             [&](int c0, int nblk, const XRegs& xr) {
@@ -95,12 +99,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q4k_kernel(GemvParams p) {
 // with D rows of loads in flight. With XFW the quantising waves fetch and
 // quantise x before issuing their own weight loads, so that x is not queued
 // behind the weight requests of the whole CU.
-template <int NB, int WAVES, int D, bool XFW>
+template <typename Fmt, int NB, int WAVES, int D, bool XFW>
 __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
+    using W = typename Fmt::W;
     constexpr int NIT = (NB + 15) / 16;           // blocks per lane per row
     constexpr int QW = (NB + 3) / 4;              // quantising waves
     constexpr int PASSES = (QW + WAVES - 1) / WAVES;
-    constexpr size_t ROWB = (size_t)NB * Q4K_BYTES;
+    constexpr size_t ROWB = (size_t)NB * Fmt::BYTES;
     __shared__ __align__(16) char q8s[q8lds_bytes(NB)];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -136,11 +141,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
         else { l.w = W0; l.y = Y0; l.row = r; }
         return l;
     };
-    W4 buf[D][NIT];
+    W buf[D][NIT];
     // rows past the end re-read the last row (in bounds; never stored): the
     // first D loads are unconditional so that the compiler's wait counts for
     // x stay exact (a load under a branch makes it wait for every load)
-    auto load_row = [&](int i, W4 (&b)[NIT]) {
+    auto load_row = [&](int i, W (&b)[NIT]) {
         const int r0 = g + i * G;
         const int r = r0 < Mtot ? r0 : Mtot - 1;
         const Loc l = locate(r);
@@ -148,7 +153,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int bb = bsub + 16 * it;
-            b[it] = load_w4(wr + (size_t)(bb < NB ? bb : NB - 1) * Q4K_BYTES, l4);
+            b[it] = Fmt::load(wr + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
         }
     };
 
@@ -182,11 +187,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
 
-    Q8Reg qr[NIT];
+    typename Fmt::R qr[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int bb = bsub + 16 * it;
-        load_q8reg(L, bb < NB ? bb : NB - 1, l4, qr[it]);
+        Fmt::load_reg(L, bb < NB ? bb : NB - 1, l4, qr[it]);
     }
     for (int i0 = 0; i0 < nrows; i0 += D) {
 #pragma unroll
@@ -196,7 +201,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
                 float acc = 0.0f;
 #pragma unroll
                 for (int it = 0; it < NIT; ++it) {
-                    const float a = block_dot_reg(buf[u][it], l4, qr[it], acc);
+                    const float a = Fmt::dot_reg(buf[u][it], l4, qr[it], acc);
                     acc = (bsub + 16 * it < NB) ? a : acc;
                 }
                 acc = group_sum_last<64>(acc);
@@ -246,31 +251,31 @@ __global__ __launch_bounds__(WAVES * 64) void subblock_sums_kernel(const uint8_t
 }
 
 // ---------------------------------------------------------------------------
-template <int T, int BPR, bool PREQ>
+template <typename Fmt, int T, int BPR, bool PREQ>
 static hipError_t launch_tb(const GemvParams& p, int ntiles, hipStream_t st) {
     constexpr int WAVES = 4;
     constexpr int U = 2;
     const size_t lds = (size_t)q8lds_bytes(T * p.chunk_blocks);
-    hipLaunchKernelGGL((gemv_q4k_kernel<T, BPR, WAVES, U, PREQ>), dim3(ntiles), dim3(WAVES * 64), lds, st, p);
+    hipLaunchKernelGGL((gemv_kernel<Fmt, T, BPR, WAVES, U, PREQ>), dim3(ntiles), dim3(WAVES * 64), lds, st, p);
     return hipGetLastError();
 }
 
-template <int T, bool PREQ>
+template <typename Fmt, int T, bool PREQ>
 static hipError_t launch_t(const GemvParams& p, int bpr, int ntiles, hipStream_t st) {
     switch (bpr) {
-        case 1: return launch_tb<T, 1, PREQ>(p, ntiles, st);
-        case 2: return launch_tb<T, 2, PREQ>(p, ntiles, st);
-        case 4: return launch_tb<T, 4, PREQ>(p, ntiles, st);
-        case 8: return launch_tb<T, 8, PREQ>(p, ntiles, st);
+        case 1: return launch_tb<Fmt, T, 1, PREQ>(p, ntiles, st);
+        case 2: return launch_tb<Fmt, T, 2, PREQ>(p, ntiles, st);
+        case 4: return launch_tb<Fmt, T, 4, PREQ>(p, ntiles, st);
+        case 8: return launch_tb<Fmt, T, 8, PREQ>(p, ntiles, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 int gemv_rows_per_tile(int bpr) { return 4 * (64 / (4 * bpr)); }
 
-template <int NB, int WAVES, int D, bool XFW>
+template <typename Fmt, int NB, int WAVES, int D, bool XFW>
 static hipError_t launch_dec(const GemvParams& p, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_decode_kernel<NB, WAVES, D, XFW>), dim3(grid), dim3(WAVES * 64), 0, st, p);
+    hipLaunchKernelGGL((gemv_decode_kernel<Fmt, NB, WAVES, D, XFW>), dim3(grid), dim3(WAVES * 64), 0, st, p);
     return hipGetLastError();
 }
 
@@ -280,12 +285,19 @@ static hipError_t launch_dec(const GemvParams& p, int grid, hipStream_t st) {
 constexpr bool dec_shape_ok(int nb, int waves, int depth) {
     return !(nb >= 48 && waves == 16 && depth == 2) && !(nb > 48 && (waves > 8 || depth > 1));
 }
+// Q6_K holds 15 + 21 registers a block (Q4_K 12 + 19): at K = 12288 a 16-wave
+// workgroup (128 registers) or two rows in flight at 12 waves would spill
+template <typename Fmt>
+constexpr bool dec_shape_ok_fmt(int nb, int waves, int depth) {
+    if (Fmt::BYTES == Q6K_BYTES && nb >= 48 && (waves == 16 || (waves == 12 && depth == 2))) return false;
+    return dec_shape_ok(nb, waves, depth);
+}
 
-template <int NB>
+template <typename Fmt, int NB>
 static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
 #define SPQ_DEC(W, DD, X)                                                                  \
-    if constexpr (dec_shape_ok(NB, W, DD))                                                 \
-        if (c.waves == W && c.depth == DD && c.xfirst == X) return launch_dec<NB, W, DD, X>(p, c.grid, st);
+    if constexpr (dec_shape_ok_fmt<Fmt>(NB, W, DD))                                        \
+        if (c.waves == W && c.depth == DD && c.xfirst == X) return launch_dec<Fmt, NB, W, DD, X>(p, c.grid, st);
     SPQ_DEC(16, 1, false) SPQ_DEC(16, 1, true) SPQ_DEC(16, 2, false) SPQ_DEC(16, 2, true)
     SPQ_DEC(12, 1, false) SPQ_DEC(12, 1, true) SPQ_DEC(12, 2, false) SPQ_DEC(12, 2, true)
     SPQ_DEC(8, 1, false) SPQ_DEC(8, 1, true) SPQ_DEC(8, 2, false) SPQ_DEC(8, 2, true)
@@ -293,27 +305,43 @@ static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStre
     return hipErrorInvalidValue;
 }
 
-// K = 4096, 5120, 12288, 27648: the dense shapes of the 8B model and of the
-// large-K configuration
-bool decode_supported(int nb) { return nb == 16 || nb == 20 || nb == 48 || nb == 108; }
+// Q4_K: K = 4096, 5120, 12288, 27648, the dense shapes of the 8B model and of
+// the large-K configuration. Q6_K (15 weight and 21 activation registers a
+// block a lane): K = 4096 and 12288; at K = 27648 its seven blocks a lane
+// would not fit the register file, and the generic kernel runs.
+bool decode_supported(int fmt, int nb) {
+    if (fmt == WF_Q6K) return nb == 16 || nb == 48;
+    return nb == 16 || nb == 20 || nb == 48 || nb == 108;
+}
 
 hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
-    if (p.nb == 16) return launch_dec_nb<16>(p, c, st);
-    if (p.nb == 20) return launch_dec_nb<20>(p, c, st);
-    if (p.nb == 48) return launch_dec_nb<48>(p, c, st);
-    if (p.nb == 108) return launch_dec_nb<108>(p, c, st);
+    if (p.fmt == WF_Q6K) {
+        if (p.nb == 16) return launch_dec_nb<FmtQ6K, 16>(p, c, st);
+        if (p.nb == 48) return launch_dec_nb<FmtQ6K, 48>(p, c, st);
+        return hipErrorInvalidValue;
+    }
+    if (p.nb == 16) return launch_dec_nb<FmtQ4K, 16>(p, c, st);
+    if (p.nb == 20) return launch_dec_nb<FmtQ4K, 20>(p, c, st);
+    if (p.nb == 48) return launch_dec_nb<FmtQ4K, 48>(p, c, st);
+    if (p.nb == 108) return launch_dec_nb<FmtQ4K, 108>(p, c, st);
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st) {
+template <typename Fmt>
+static hipError_t launch_gemv_fmt(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st) {
     const bool pq = p.Q.qs != nullptr;
 #define SPQ_T(TT) \
-    case TT: return pq ? launch_t<TT, true>(p, bpr, ntiles, st) : launch_t<TT, false>(p, bpr, ntiles, st);
+    case TT: return pq ? launch_t<Fmt, TT, true>(p, bpr, ntiles, st) : launch_t<Fmt, TT, false>(p, bpr, ntiles, st);
     switch (T) {
         SPQ_T(1) SPQ_T(2) SPQ_T(3) SPQ_T(4) SPQ_T(5) SPQ_T(6) SPQ_T(7) SPQ_T(8)
         default: return hipErrorInvalidValue;
     }
 #undef SPQ_T
+}
+
+hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st) {
+    return p.fmt == WF_Q6K ? launch_gemv_fmt<FmtQ6K>(p, T, bpr, ntiles, st)
+                           : launch_gemv_fmt<FmtQ4K>(p, T, bpr, ntiles, st);
 }
 
 hipError_t launch_subblock_sums(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st) {

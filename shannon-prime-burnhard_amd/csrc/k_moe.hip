@@ -17,9 +17,12 @@
 //      of its rows; its pairs are processed TC at a time, each chunk staged
 //      from the Q8_K planes into LDS and streamed with the dense GEMV's code.
 // Calls with at most MOE_FUSED_MAX_PAIRS pairs use moe_fused_kernel instead,
-// which does all three steps in one launch.
+// which does all three steps in one launch. The sdot4 kernels (moe_gemv,
+// moe_fused, moe_decode) are templates over the weight format and also run
+// Q6_K expert banks (FmtQ6K, q6k_core.h); the matrix-core ring is Q4_K only.
 #include "gemv_core.h"
 #include "launch.h"
+#include "q6k_core.h"
 #include "ring_core.h"
 
 namespace spq4k {
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const int32_t* __restric
     route_block(ids, n_pairs, E, r, sh);
 }
 
-template <int TC, int BPR, int WAVES, int U>
+template <typename Fmt, int TC, int BPR, int WAVES, int U>
 __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeParams p) {
     extern __shared__ __align__(16) char smem[];
     constexpr int LPR = 4 * BPR;
@@ -134,7 +137,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeParams p) {
     const int row = tile * ROWS + wave * RPW + lane / LPR;
     const bool row_ok = row < M;
     const int nb = p.nb;
-    const size_t row_bytes = (size_t)nb * Q4K_BYTES;
+    const size_t row_bytes = (size_t)nb * Fmt::BYTES;
     const uint8_t* __restrict__ wrow =
         p.bank + (size_t)e * p.expert_bytes + (size_t)(row_ok ? row : M - 1) * row_bytes;
 
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeParams p) {
         float acc[TC];
 #pragma unroll
         for (int t = 0; t < TC; ++t) acc[t] = 0.0f;
-        stream_row<TC, BPR, U>(wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int, int) { return 0; },
+        stream_row<Fmt, TC, BPR, U>(wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int, int) { return 0; },
                                [&](int c0, int nblk, int) {
             // copy the chunk's Q8_K rows (planes) into LDS slots t * CB + b
             for (int t = 0; t < TC; ++t) {
@@ -189,7 +192,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeParams p) {
 // with a ballot compaction that keeps pair order), returns at once when e is
 // unused, and quantises the routed input rows from fp32 into LDS as it
 // streams its rows: no routing pass, no Q8_K planes, one launch per call.
-template <int TC, int BPR, int WAVES, int U>
+template <typename Fmt, int TC, int BPR, int WAVES, int U>
 __global__ __launch_bounds__(WAVES * 64) void moe_fused_kernel(MoeFusedParams p) {
     extern __shared__ __align__(16) char smem[];
     constexpr int LPR = 4 * BPR;
@@ -228,7 +231,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_fused_kernel(MoeFusedParams p)
     const bool row_ok = row < M;
     const int nb = p.nb;
     const uint8_t* __restrict__ wrow =
-        p.bank + (size_t)e * p.expert_bytes + (size_t)(row_ok ? row : M - 1) * ((size_t)nb * Q4K_BYTES);
+        p.bank + (size_t)e * p.expert_bytes + (size_t)(row_ok ? row : M - 1) * ((size_t)nb * Fmt::BYTES);
     const int CB = p.chunk_blocks;
     const Q8Lds L = q8lds_carve(smem, TC * CB);
 
@@ -247,7 +250,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_fused_kernel(MoeFusedParams p)
         float acc[TC];
 #pragma unroll
         for (int t = 0; t < TC; ++t) acc[t] = 0.0f;
-        stream_row<TC, BPR, U>(wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int, int) { return 0; },
+        stream_row<Fmt, TC, BPR, U>(wrow, row_ok, l4, bsub, nb, CB, L, acc, [&](int, int) { return 0; },
                                [&](int c0, int nblk, int) {
             // quantise block c0 + b of each routed input row into slot t * CB + b
             const int nitems = TC * nblk;
@@ -280,8 +283,9 @@ __global__ __launch_bounds__(WAVES * 64) void moe_fused_kernel(MoeFusedParams p)
 // rows g, g + G, ... of the sweep. An expert chosen by several pairs is
 // streamed once per pair, which is why this form is kept to small batches.
 // An id outside [0, E) leaves that pair's outputs untouched.
-template <int NB, int BSL, int WAVES>
+template <typename Fmt, int NB, int BSL, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p) {
+    using W = typename Fmt::W;
     extern __shared__ __align__(16) char smem[];
     constexpr int LPR = 4 * BSL;
     constexpr int RPW = 64 / LPR;
@@ -321,14 +325,14 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
         const int e = p.ids[pr];
         l.e = (r < r1 && e >= 0 && e < p.E) ? e : -1;
         l.xs = (xrow(rc) - xlo) * NB;
-        l.w = p.bank + (size_t)(l.e >= 0 ? l.e : 0) * p.expert_bytes + (size_t)l.lr * ((size_t)NB * Q4K_BYTES);
+        l.w = p.bank + (size_t)(l.e >= 0 ? l.e : 0) * p.expert_bytes + (size_t)l.lr * ((size_t)NB * Fmt::BYTES);
         return l;
     };
-    auto load = [&](const Loc& l, W4 (&w)[NIT]) {
+    auto load = [&](const Loc& l, W (&w)[NIT]) {
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int bb = bsub + BSL * it;
-            w[it] = load_w4(l.w + (size_t)(bb < NB ? bb : NB - 1) * Q4K_BYTES, l4);
+            w[it] = Fmt::load(l.w + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
         }
     };
     // order of the loads (they complete in order): the expert id of the first
@@ -338,7 +342,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     const int ci_a = item_a < nitems ? item_a : nitems - 1;
     Loc cur = locate(g0);
     const XRegs xa = load_x16(p.X, p.K, xlo + ci_a / NB, ci_a % NB);
-    W4 w[NIT];
+    W w[NIT];
     load(cur, w);
     store_q8_item(xa, item_a < nitems, ci_a, L);
     for (int base = 4 * WAVES; base < nitems; base += 4 * WAVES) {
@@ -354,7 +358,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int bb = bsub + BSL * it;
-            block_dot<1>(w[it], l4, L, cur.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && cur.e >= 0, acc);
+            Fmt::template dot<1>(w[it], l4, L, cur.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && cur.e >= 0, acc);
         }
         const float sum = group_sum_last<LPR>(acc[0]);
         if (cur.e >= 0 && (lane & (LPR - 1)) == LPR - 1) p.Y[(int64_t)(r / M) * M + cur.lr] = sum;
@@ -365,11 +369,11 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     }
 }
 
-template <int NB, int BSL>
+template <typename Fmt, int NB, int BSL>
 static hipError_t launch_mdec(const MoeFusedParams& p, int grid, hipStream_t st) {
     constexpr int WAVES = 8;
     const size_t lds = (size_t)q8lds_bytes(p.xwin_rows * NB);
-    hipLaunchKernelGGL((moe_decode_kernel<NB, BSL, WAVES>), dim3(grid), dim3(WAVES * 64), lds, st, p);
+    hipLaunchKernelGGL((moe_decode_kernel<Fmt, NB, BSL, WAVES>), dim3(grid), dim3(WAVES * 64), lds, st, p);
     return hipGetLastError();
 }
 
@@ -391,42 +395,53 @@ void moe_decode_plan(const MoeFusedParams& p, int grid, int32_t* rows_per_wg, in
     *xwin_rows = (int32_t)(w < p.n_xrows ? w : p.n_xrows);
 }
 
-hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st) {
+template <typename Fmt>
+static hipError_t launch_moe_decode_fmt(const MoeFusedParams& p, int grid, hipStream_t st) {
     switch (p.nb) {
-        case 3: return launch_mdec<3, 4>(p, grid, st);
-        case 8: return launch_mdec<8, 8>(p, grid, st);
-        case 16: return launch_mdec<16, 16>(p, grid, st);
+        case 3: return launch_mdec<Fmt, 3, 4>(p, grid, st);
+        case 8: return launch_mdec<Fmt, 8, 8>(p, grid, st);
+        case 16: return launch_mdec<Fmt, 16, 16>(p, grid, st);
         default: return hipErrorInvalidValue;
     }
 }
 
-template <int TC, int BPR>
+hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st) {
+    return p.fmt == WF_Q6K ? launch_moe_decode_fmt<FmtQ6K>(p, grid, st) : launch_moe_decode_fmt<FmtQ4K>(p, grid, st);
+}
+
+template <typename Fmt, int TC, int BPR>
 static hipError_t launch_fused_tb(const MoeFusedParams& p, int grid, hipStream_t st) {
     constexpr int WAVES = 4, U = 2;
     const size_t lds = (size_t)q8lds_bytes(TC * p.chunk_blocks);
-    hipLaunchKernelGGL((moe_fused_kernel<TC, BPR, WAVES, U>), dim3(grid), dim3(WAVES * 64), lds, st, p);
+    hipLaunchKernelGGL((moe_fused_kernel<Fmt, TC, BPR, WAVES, U>), dim3(grid), dim3(WAVES * 64), lds, st, p);
     return hipGetLastError();
 }
 
-template <int TC>
+template <typename Fmt, int TC>
 static hipError_t launch_fused_t(const MoeFusedParams& p, int bpr, int grid, hipStream_t st) {
     switch (bpr) {
-        case 1: return launch_fused_tb<TC, 1>(p, grid, st);
-        case 2: return launch_fused_tb<TC, 2>(p, grid, st);
-        case 4: return launch_fused_tb<TC, 4>(p, grid, st);
-        case 8: return launch_fused_tb<TC, 8>(p, grid, st);
+        case 1: return launch_fused_tb<Fmt, TC, 1>(p, grid, st);
+        case 2: return launch_fused_tb<Fmt, TC, 2>(p, grid, st);
+        case 4: return launch_fused_tb<Fmt, TC, 4>(p, grid, st);
+        case 8: return launch_fused_tb<Fmt, TC, 8>(p, grid, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <typename Fmt>
+static hipError_t launch_moe_fused_fmt(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st) {
+    switch (tc) {
+        case 1: return launch_fused_t<Fmt, 1>(p, bpr, grid, st);
+        case 2: return launch_fused_t<Fmt, 2>(p, bpr, grid, st);
+        case 4: return launch_fused_t<Fmt, 4>(p, bpr, grid, st);
+        case 8: return launch_fused_t<Fmt, 8>(p, bpr, grid, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st) {
-    switch (tc) {
-        case 1: return launch_fused_t<1>(p, bpr, grid, st);
-        case 2: return launch_fused_t<2>(p, bpr, grid, st);
-        case 4: return launch_fused_t<4>(p, bpr, grid, st);
-        case 8: return launch_fused_t<8>(p, bpr, grid, st);
-        default: return hipErrorInvalidValue;
-    }
+    return p.fmt == WF_Q6K ? launch_moe_fused_fmt<FmtQ6K>(p, tc, bpr, grid, st)
+                           : launch_moe_fused_fmt<FmtQ4K>(p, tc, bpr, grid, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -435,33 +450,39 @@ hipError_t launch_moe_route(const int32_t* ids, int n_pairs, int E, const MoeRou
     return hipGetLastError();
 }
 
-template <int TC, int BPR>
+template <typename Fmt, int TC, int BPR>
 static hipError_t launch_moe_tb(const MoeParams& p, int grid, hipStream_t st) {
     constexpr int WAVES = 4, U = 2;
     const size_t lds = (size_t)q8lds_bytes(TC * p.chunk_blocks);
-    hipLaunchKernelGGL((moe_gemv_kernel<TC, BPR, WAVES, U>), dim3(grid), dim3(WAVES * 64), lds, st, p);
+    hipLaunchKernelGGL((moe_gemv_kernel<Fmt, TC, BPR, WAVES, U>), dim3(grid), dim3(WAVES * 64), lds, st, p);
     return hipGetLastError();
 }
 
-template <int TC>
+template <typename Fmt, int TC>
 static hipError_t launch_moe_t(const MoeParams& p, int bpr, int grid, hipStream_t st) {
     switch (bpr) {
-        case 1: return launch_moe_tb<TC, 1>(p, grid, st);
-        case 2: return launch_moe_tb<TC, 2>(p, grid, st);
-        case 4: return launch_moe_tb<TC, 4>(p, grid, st);
-        case 8: return launch_moe_tb<TC, 8>(p, grid, st);
+        case 1: return launch_moe_tb<Fmt, TC, 1>(p, grid, st);
+        case 2: return launch_moe_tb<Fmt, TC, 2>(p, grid, st);
+        case 4: return launch_moe_tb<Fmt, TC, 4>(p, grid, st);
+        case 8: return launch_moe_tb<Fmt, TC, 8>(p, grid, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <typename Fmt>
+static hipError_t launch_moe_gemv_fmt(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st) {
+    switch (tc) {
+        case 1: return launch_moe_t<Fmt, 1>(p, bpr, grid, st);
+        case 2: return launch_moe_t<Fmt, 2>(p, bpr, grid, st);
+        case 4: return launch_moe_t<Fmt, 4>(p, bpr, grid, st);
+        case 8: return launch_moe_t<Fmt, 8>(p, bpr, grid, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st) {
-    switch (tc) {
-        case 1: return launch_moe_t<1>(p, bpr, grid, st);
-        case 2: return launch_moe_t<2>(p, bpr, grid, st);
-        case 4: return launch_moe_t<4>(p, bpr, grid, st);
-        case 8: return launch_moe_t<8>(p, bpr, grid, st);
-        default: return hipErrorInvalidValue;
-    }
+    return p.fmt == WF_Q6K ? launch_moe_gemv_fmt<FmtQ6K>(p, tc, bpr, grid, st)
+                           : launch_moe_gemv_fmt<FmtQ4K>(p, tc, bpr, grid, st);
 }
 
 

@@ -11,8 +11,14 @@ namespace spq4k {
 
 constexpr int GEMV_MAX_SEG = 4;
 
+// weight formats of the matvec kernels
+enum WFmt : int32_t {
+    WF_Q4K = 0,   // GGML_TYPE_Q4_K, 144-byte blocks
+    WF_Q6K = 1,   // GGML_TYPE_Q6_K, 210-byte blocks
+};
+
 struct GemvSeg {
-    const uint8_t* W;     // [M][nb] Q4_K blocks, row-major, 16-byte aligned
+    const uint8_t* W;     // [M][nb] blocks of the format, row-major
     float* Y;             // y[t * y_tstride + r]
     int64_t y_tstride;
     int32_t M;
@@ -29,6 +35,7 @@ struct GemvParams {
     Q8Planes Q;           // pre-quantised activations (Q.qs != nullptr) instead of X
     int32_t chunk_blocks; // blocks staged in LDS at a time
     int32_t total_rows;   // sum of the segments' M
+    int32_t fmt;          // WFmt of every segment
 };
 
 // Launch shape of the T = 1 decode kernel (gemv_decode_kernel).
@@ -42,7 +49,7 @@ struct DecodeCfg {
 // rows per workgroup for a lanes-per-row choice of 4*bpr (bpr in 1, 2, 4, 8)
 int gemv_rows_per_tile(int bpr);
 hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st);
-bool decode_supported(int nb);
+bool decode_supported(int fmt, int nb);
 hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st);
 hipError_t launch_subblock_sums(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
 
@@ -65,6 +72,7 @@ struct MoeParams {
     int32_t M, nb, n_used, ne11;
     int32_t tiles_per_expert;
     int32_t chunk_blocks;
+    int32_t fmt;             // WFmt of the bank (moe_gemv_kernel; the ring is Q4_K only)
 };
 
 hipError_t launch_moe_route(const int32_t* ids, int n_pairs, int E, const MoeRoute& r, hipStream_t st);
@@ -84,6 +92,7 @@ struct MoeFusedParams {
     int32_t n_xrows;    // input rows T * ne11 (moe_decode_kernel)
     int32_t rows_per_wg;   // moe_decode_kernel: contiguous sweep rows a workgroup (moe_decode_plan)
     int32_t xwin_rows;     // moe_decode_kernel: input rows quantised by a workgroup at most
+    int32_t fmt;           // WFmt of the bank
 };
 hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st);
 
@@ -149,5 +158,12 @@ hipError_t launch_quantize_q4k(const float* x, uint8_t* y, int64_t nblocks, hipS
 hipError_t launch_synth(float* out, int64_t n, uint64_t seed, int dist, int64_t cols, float mean, float std,
                         float outlier_mult, int64_t offset, hipStream_t st);
 hipError_t launch_vec_dot_q8(const uint8_t* wx, const uint8_t* q8, int nb, float* out, hipStream_t st);
+
+// Q6_K conversions (k_q6k.hip); the Q6_K matvecs are the FmtQ6K instances of
+// launch_gemv / launch_gemv_decode / launch_moe_* (fmt = WF_Q6K)
+hipError_t launch_dequant_q6k(const uint8_t* x, float* y, int64_t nblocks, hipStream_t st);
+hipError_t launch_quantize_q6k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
+hipError_t launch_vec_dot_q6k(const uint8_t* wx, const uint8_t* q8, int nb, float* out, hipStream_t st);
+hipError_t launch_subblock_sums_q6k(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
 
 }  // namespace spq4k

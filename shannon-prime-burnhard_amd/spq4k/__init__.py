@@ -4,12 +4,14 @@ A thin ctypes layer over the C ABI in include/spq4k.h. The method names
 mirror the reference's operator interface for this path (vendored ggml in
 nihilistau/shannon-prime-burnhard):
 
-    to_float        ggml_type_traits[Q4_K].to_float   (ggml.h:2791-2804)
+    to_float        ggml_type_traits[type].to_float   (ggml.h:2791-2804)
     from_float      ggml_type_traits_cpu[Q8_K].from_float (ggml-cpu.h:113-123)
-    quantize_chunk  ggml_quantize_chunk(GGML_TYPE_Q4_K, imatrix=NULL) (ggml.h:2764)
-    vec_dot         ggml_vec_dot_t for Q4_K x Q8_K    (ggml-cpu.h:113)
+    quantize_chunk  ggml_quantize_chunk(type, imatrix=NULL) (ggml.h:2764)
+    vec_dot         ggml_vec_dot_t for type x Q8_K    (ggml-cpu.h:113)
     mul_mat         GGML_OP_MUL_MAT                   (ggml.h:1414-1420)
     mul_mat_id      GGML_OP_MUL_MAT_ID                (ggml.h:1434-1438)
+
+`type` is ggml's type id: TYPE_Q4_K (12, the default) or TYPE_Q6_K (14).
 
 Every call runs on the GPU through libspq4k.so; if the library is missing
 or the device is absent the call raises. There is no CPU fallback.
@@ -26,7 +28,11 @@ import numpy as np
 
 QK_K = 256
 Q4K_BLOCK_BYTES = 144
+Q6K_BLOCK_BYTES = 210
 Q8K_BLOCK_BYTES = 292
+TYPE_Q4_K = 12
+TYPE_Q6_K = 14
+BLOCK_BYTES = {TYPE_Q4_K: Q4K_BLOCK_BYTES, TYPE_Q6_K: Q6K_BLOCK_BYTES}
 GEMV_MAX_T = 8
 DIST_NORMAL = 0
 DIST_STUDENT_T4 = 1
@@ -86,6 +92,17 @@ def load_library(path: str | None = None):
         "spq4k_mul_mat_host": (I, [V, V, V, V, I64]),
         "spq4k_moe_host": (I, [V, V, V, I64, I64, I64, V, V]),
         "spq4k_subblock_sums": (I, [V, V, I64, I64, V, V]),
+        "spq4k_weights_upload_type": (I, [V, I, V, I64, I64, I64, PV]),
+        "spq4k_weights_wrap_type": (I, [V, I, V, I64, I64, I64, PV]),
+        "spq4k_weights_alloc_type": (I, [V, I, I64, I64, I64, PV]),
+        "spq4k_weights_type": (I, [V]),
+        "spq4k_to_float": (I, [V, I, V, V, I64]),
+        "spq4k_quantize_chunk": (I, [V, I, V, V, I64, I64]),
+        "spq4k_vec_dot_q8K": (I, [V, I, I, V, V, V]),
+        "spq4k_to_float_host": (I, [V, I, V, V, I64]),
+        "spq4k_quantize_chunk_host": (I, [V, I, V, V, I64, I64]),
+        "spq4k_vec_dot_q8K_host": (I, [V, I, I, V, V, V]),
+        "spq4k_subblock_sums_type": (I, [V, I, V, I64, I64, V, V]),
         "spq4k_synth_fill": (I, [V, V, I64, U64, I, I64, F, F, F, I64]),
     }
     for name, (res, args) in sig.items():
@@ -111,10 +128,10 @@ def _ptr(a):
 
 
 class Weights:
-    """A Q4_K weight matrix (or an E-expert bank) in device memory."""
+    """A Q4_K or Q6_K weight matrix (or an E-expert bank) in device memory."""
 
-    def __init__(self, ctx: "Context", handle, M, K, E):
-        self.ctx, self.handle, self.M, self.K, self.E = ctx, handle, M, K, E
+    def __init__(self, ctx: "Context", handle, M, K, E, type=TYPE_Q4_K):
+        self.ctx, self.handle, self.M, self.K, self.E, self.type = ctx, handle, M, K, E, type
 
     @property
     def data_ptr(self) -> int:
@@ -177,26 +194,29 @@ class Context:
         self._check("spq4k_synchronize", self.lib.spq4k_synchronize(self.handle))
 
     # -- weights
-    def upload(self, q4k: np.ndarray, M: int, K: int, E: int = 1) -> Weights:
+    def upload(self, q: np.ndarray, M: int, K: int, E: int = 1, type: int = TYPE_Q4_K) -> Weights:
         h = C.c_void_p()
-        self._check("spq4k_weights_upload",
-                    self.lib.spq4k_weights_upload(self.handle, _ptr(np.ascontiguousarray(q4k)), M, K, E, C.byref(h)))
-        return Weights(self, h, M, K, E)
+        self._check("spq4k_weights_upload_type",
+                    self.lib.spq4k_weights_upload_type(self.handle, type, _ptr(np.ascontiguousarray(q)), M, K, E,
+                                                       C.byref(h)))
+        return Weights(self, h, M, K, E, type)
 
-    def wrap(self, dev_ptr: int, M: int, K: int, E: int = 1) -> Weights:
+    def wrap(self, dev_ptr: int, M: int, K: int, E: int = 1, type: int = TYPE_Q4_K) -> Weights:
         h = C.c_void_p()
-        self._check("spq4k_weights_wrap", self.lib.spq4k_weights_wrap(self.handle, dev_ptr, M, K, E, C.byref(h)))
-        return Weights(self, h, M, K, E)
+        self._check("spq4k_weights_wrap_type",
+                    self.lib.spq4k_weights_wrap_type(self.handle, type, dev_ptr, M, K, E, C.byref(h)))
+        return Weights(self, h, M, K, E, type)
 
-    def alloc_weights(self, M: int, K: int, E: int = 1) -> Weights:
+    def alloc_weights(self, M: int, K: int, E: int = 1, type: int = TYPE_Q4_K) -> Weights:
         h = C.c_void_p()
-        self._check("spq4k_weights_alloc", self.lib.spq4k_weights_alloc(self.handle, M, K, E, C.byref(h)))
-        return Weights(self, h, M, K, E)
+        self._check("spq4k_weights_alloc_type",
+                    self.lib.spq4k_weights_alloc_type(self.handle, type, M, K, E, C.byref(h)))
+        return Weights(self, h, M, K, E, type)
 
     # -- type traits on host arrays (synchronous)
-    def to_float(self, q4k: np.ndarray, k: int) -> np.ndarray:
+    def to_float(self, q: np.ndarray, k: int, type: int = TYPE_Q4_K) -> np.ndarray:
         y = np.empty(k, np.float32)
-        self._check("spq4k_dequant_host", self.lib.spq4k_dequant_host(self.handle, _ptr(q4k), _ptr(y), k))
+        self._check("spq4k_to_float_host", self.lib.spq4k_to_float_host(self.handle, type, _ptr(q), _ptr(y), k))
         return y
 
     def from_float(self, x: np.ndarray) -> np.ndarray:
@@ -206,17 +226,17 @@ class Context:
                     self.lib.spq4k_quantize_q8K_host(self.handle, _ptr(x), _ptr(y), x.size))
         return y
 
-    def quantize_chunk(self, src: np.ndarray, nrow: int, n_per_row: int) -> np.ndarray:
+    def quantize_chunk(self, src: np.ndarray, nrow: int, n_per_row: int, type: int = TYPE_Q4_K) -> np.ndarray:
         src = np.ascontiguousarray(src, np.float32).ravel()
-        y = np.zeros(nrow * (n_per_row // QK_K) * Q4K_BLOCK_BYTES, np.uint8)
-        self._check("spq4k_quantize_q4K_host",
-                    self.lib.spq4k_quantize_q4K_host(self.handle, _ptr(src), _ptr(y), nrow, n_per_row))
+        y = np.zeros(nrow * (n_per_row // QK_K) * BLOCK_BYTES[type], np.uint8)
+        self._check("spq4k_quantize_chunk_host",
+                    self.lib.spq4k_quantize_chunk_host(self.handle, type, _ptr(src), _ptr(y), nrow, n_per_row))
         return y
 
-    def vec_dot(self, n: int, vx: np.ndarray, vy: np.ndarray) -> float:
+    def vec_dot(self, n: int, vx: np.ndarray, vy: np.ndarray, type: int = TYPE_Q4_K) -> float:
         s = C.c_float()
-        self._check("spq4k_vec_dot_host",
-                    self.lib.spq4k_vec_dot_host(self.handle, n, C.byref(s), _ptr(vx), _ptr(vy)))
+        self._check("spq4k_vec_dot_q8K_host",
+                    self.lib.spq4k_vec_dot_q8K_host(self.handle, type, n, C.byref(s), _ptr(vx), _ptr(vy)))
         return s.value
 
     def mul_mat(self, W: Weights, X: np.ndarray) -> np.ndarray:
@@ -237,8 +257,9 @@ class Context:
                                                               _ptr(X), _ptr(Y)))
         return Y
 
-    def subblock_sums(self, W_dev: int, M: int, K: int, x_dev: int, S_dev: int):
-        self._check("spq4k_subblock_sums", self.lib.spq4k_subblock_sums(self.handle, W_dev, M, K, x_dev, S_dev))
+    def subblock_sums(self, W_dev: int, M: int, K: int, x_dev: int, S_dev: int, type: int = TYPE_Q4_K):
+        self._check("spq4k_subblock_sums_type",
+                    self.lib.spq4k_subblock_sums_type(self.handle, type, W_dev, M, K, x_dev, S_dev))
 
     # -- device-pointer entry points (asynchronous on the context stream)
     def gemv_dev(self, W: Weights, x_dev: int, y_dev: int, T: int = 1):
@@ -274,6 +295,15 @@ class Context:
     def quantize_q4K_dev(self, src: int, dst: int, nrow: int, n_per_row: int):
         self._check("spq4k_quantize_q4K", self.lib.spq4k_quantize_q4K(self.handle, src, dst, nrow, n_per_row))
 
+    def to_float_dev(self, type: int, vx: int, y: int, k: int):
+        self._check("spq4k_to_float", self.lib.spq4k_to_float(self.handle, type, vx, y, k))
+
+    def quantize_chunk_dev(self, type: int, src: int, dst: int, nrow: int, n_per_row: int):
+        self._check("spq4k_quantize_chunk", self.lib.spq4k_quantize_chunk(self.handle, type, src, dst, nrow, n_per_row))
+
+    def vec_dot_q8K_dev(self, type: int, n: int, s_dev: int, vx: int, vy: int):
+        self._check("spq4k_vec_dot_q8K", self.lib.spq4k_vec_dot_q8K(self.handle, type, n, s_dev, vx, vy))
+
     def synth_fill_dev(self, out: int, n: int, seed: int, dist: int = DIST_NORMAL, cols: int = 0,
                        mean: float = 0.0, std: float = 1.0, outlier_mult: float = 1.0, offset: int = 0):
         self._check("spq4k_synth_fill", self.lib.spq4k_synth_fill(self.handle, out, n, seed, dist, cols, mean, std,
@@ -281,4 +311,5 @@ class Context:
 
 
 __all__ = ["Context", "Weights", "Spq4kError", "load_library", "LIB_PATH", "QK_K", "Q4K_BLOCK_BYTES",
-           "Q8K_BLOCK_BYTES", "GEMV_MAX_T", "DIST_NORMAL", "DIST_STUDENT_T4"]
+           "Q6K_BLOCK_BYTES", "Q8K_BLOCK_BYTES", "TYPE_Q4_K", "TYPE_Q6_K", "BLOCK_BYTES", "GEMV_MAX_T",
+           "DIST_NORMAL", "DIST_STUDENT_T4"]
