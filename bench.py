@@ -22,7 +22,11 @@ host's last-level cache), timed on this host with 16 and with 4 threads;
 its outputs are checked against the GPU's on identical inputs.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
-                  [--config decode8b|gemv4096|largek|prefill|moe|copy]
+                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|copy]
+
+--config q6k measures the Q6_K tensors a Q4_K model carries beside its Q4_K
+ones (attn_v, ffn_down, output; the MoE down-projection bank) with the same
+cold-weight method.
 """
 from __future__ import annotations
 
@@ -42,6 +46,7 @@ from spq4k.hip import DeviceArray, Event, Graph, mem_info  # noqa: E402
 
 PEAK_HBM = 8.0e12
 Q4K_B = 144
+Q6K_B = 210
 
 # 8B dense layer (Qwen3-8B-like)
 HID, KV, FFN, VOCAB, LAYERS = 4096, 1024, 12288, 151936, 36
@@ -55,6 +60,10 @@ def q4k_bytes(M, K):
     return M * (K // 256) * Q4K_B
 
 
+def q6k_bytes(M, K):
+    return M * (K // 256) * Q6K_B
+
+
 class Synth:
     """Seeded weights synthesised and Q4_K-encoded on the device."""
 
@@ -62,10 +71,10 @@ class Synth:
         self.ctx = ctx
         self.tmp = DeviceArray(max_elems, np.float32)
 
-    def weights(self, M, K, seed, dist=spq4k.DIST_NORMAL, outlier=1.0):
-        w = self.ctx.alloc_weights(M, K)
-        self.ctx.synth_fill_dev(self.tmp.ptr, M * K, seed, dist, K, 0.0, 0.02, outlier, 0)
-        self.ctx.quantize_q4K_dev(self.tmp.ptr, w.data_ptr, M, K)
+    def weights(self, M, K, seed, dist=spq4k.DIST_NORMAL, outlier=1.0, qtype=spq4k.TYPE_Q4_K, E=1):
+        w = self.ctx.alloc_weights(M, K, E, type=qtype)
+        self.ctx.synth_fill_dev(self.tmp.ptr, E * M * K, seed, dist, K, 0.0, 0.02, outlier, 0)
+        self.ctx.quantize_chunk_dev(qtype, self.tmp.ptr, w.data_ptr, E * M, K)
         return w
 
     def activations(self, n, seed):
@@ -316,13 +325,13 @@ def run_decode8b(args):
     ctx.close()
 
 
-def run_single(args, M, K, T, dist, outlier, name):
+def run_single(args, M, K, T, dist, outlier, name, qtype=spq4k.TYPE_Q4_K):
     """A single matrix shape, timed cold (rotating >= 1 GiB of weight copies)."""
     ctx = spq4k.Context(0)
     syn = Synth(ctx, M * K)
-    nb = q4k_bytes(M, K)
+    nb = q6k_bytes(M, K) if qtype == spq4k.TYPE_Q6_K else q4k_bytes(M, K)
     copies = max(2, min(128, (1 << 30) // nb + 1))
-    ws = [syn.weights(M, K, 77 + i, dist, outlier) for i in range(copies)]
+    ws = [syn.weights(M, K, 77 + i, dist, outlier, qtype) for i in range(copies)]
     x = syn.activations(T * K, 5)
     y = DeviceArray(T * M)
     ctx.synchronize()
@@ -434,6 +443,46 @@ def run_moe(args):
     ctx.close()
 
 
+def run_q6k(args):
+    """Q6_K: the sibling K-quant a Q4_K model stores some tensors in. Dense
+    decode shapes of the 8B model at T = 1 (and a T = 8 batch), cold, then the
+    MoE down-projection bank (128 experts of 2048x768) at T = 1..32, 8 layers
+    of banks cold, as in run_moe."""
+    for name, M, K, T in (("Q6_K attn_v 1024x4096", 1024, 4096, 1), ("Q6_K 4096x4096", 4096, 4096, 1),
+                          ("Q6_K ffn_down 4096x12288", 4096, 12288, 1),
+                          ("Q6_K output 151936x4096", 151936, 4096, 1), ("Q6_K 4096x4096 T=8", 4096, 4096, 8)):
+        run_single(args, M, K, T, spq4k.DIST_NORMAL, 1.0, name, spq4k.TYPE_Q6_K)
+    ctx = spq4k.Context(0)
+    E, k, NL, M, K = 128, 8, 8, 2048, 768
+    syn = Synth(ctx, E * M * K)
+    banks = [syn.weights(M, K, 900 + L, qtype=spq4k.TYPE_Q6_K, E=E) for L in range(NL)]
+    ctx.synchronize()
+    syn.tmp.free()
+    rng = np.random.default_rng(4)
+    for T in (1, 4, 8, 32):
+        ids_l = [np.argsort(-rng.standard_normal((T, E)).astype(np.float32), axis=1, kind="stable")[:, :k]
+                 .astype(np.int32) for _ in range(NL)]
+        idd = [DeviceArray.from_host(i) for i in ids_l]
+        xd = syn.activations(T * k * K, 12)
+        Y = DeviceArray(T * k * M)
+        with Graph.capture(ctx.stream) as g:
+            for L in range(NL):
+                ctx.moe_dev(banks[L], idd[L].ptr, k, k, T, xd.ptr, Y.ptr)
+        ms = time_graph(ctx, g, max(5, args.steps // 5), 2) / NL
+        uniq = float(np.mean([len(np.unique(i)) for i in ids_l]))
+        abytes = uniq * q6k_bytes(M, K) + 4 * T * k * (K + M)
+        gbs = abytes / (ms * 1e-3) / 1e9
+        print(json.dumps({"metric": f"Q6_K MoE down-projection matvec, T={T}", "value": round(gbs, 1),
+                          "unit": "GB/s", "us_per_call": round(ms * 1e3, 2),
+                          "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2), "unique_experts": uniq,
+                          "config": {"workload": "128 experts of 2048x768 Q6_K, top-8, 8 banks (cold)", "T": T}}),
+              flush=True)
+        for a in idd:
+            a.free()
+        xd.free(); Y.free()
+    ctx.close()
+
+
 def run_copy(args):
     """A plain device-to-device copy of 1 GiB (the runtime's blit kernel): the
     known-size reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE."""
@@ -462,7 +511,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "copy"])
+    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -477,6 +526,8 @@ def main():
         run_prefill(args)
     elif args.config == "moe":
         run_moe(args)
+    elif args.config == "q6k":
+        run_q6k(args)
     elif args.config == "copy":
         run_copy(args)
     elif args.config == "largek":

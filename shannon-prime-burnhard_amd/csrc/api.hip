@@ -839,10 +839,13 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
     const size_t bb = type_block_bytes(bank->type);
     const int64_t rows = T * ne11, n_pairs = T * n_used;
-    // pairs per expert are at most T: chunk width TC, rows per tile from the
-    // number of experts that can be active
-    const int tc = T >= 8 ? 8 : (T >= 4 ? 4 : (T >= 2 ? 2 : 1));
+    // chunk width TC of the sdot4 expert kernels: about twice the mean number
+    // of pairs an active expert receives (they are uneven), at most 8; every
+    // pair of a chunk costs its integer work even when the chunk is not full
     const int64_t max_act = n_pairs < E ? n_pairs : E;
+    const int64_t mean_pairs = (n_pairs + max_act - 1) / max_act;
+    int tc = 1;
+    while (tc < 8 && tc < 2 * mean_pairs) tc *= 2;
     int64_t Mtot[1] = {(int64_t)M * max_act};
     const int bpr = pick_bpr(c, Mtot, 1);
     const int rows_per_tile = gemv_rows_per_tile(bpr);

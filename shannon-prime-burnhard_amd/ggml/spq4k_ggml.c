@@ -1,4 +1,4 @@
-/* spq4k_ggml.c — ggml custom-op nodes for Q4_K GGML_OP_MUL_MAT /
+/* spq4k_ggml.c — ggml custom-op nodes for Q4_K / Q6_K GGML_OP_MUL_MAT /
  * GGML_OP_MUL_MAT_ID, run on the GPU through spq4k (include/spq4k_ggml.h).
  *
  * The node is ggml_custom_4d (ggml.h:2610-2623) with the weight, the
@@ -7,8 +7,9 @@
  *   - does all the work on ith == 0, as the engine's own custom ops do
  *     (desktop/engine/src/forward.cpp:1248, burn_moe_op.cpp:203);
  *   - finds the weight in the resident table, uploading it on first use
- *     (spq4k_weights_upload), keyed by tensor and data pointer so that a
- *     buffer reused for other bytes is uploaded again;
+ *     (spq4k_weights_upload_type with the tensor's ggml type), keyed by
+ *     tensor and data pointer so that a buffer reused for other bytes is
+ *     uploaded again;
  *   - reads activations and ids, and writes the output, through
  *     ggml_backend_tensor_get / _set when the tensor has a backend buffer and
  *     through tensor->data otherwise;
@@ -118,7 +119,7 @@ static int resident_weight(spq4k_ggml *b, const struct ggml_tensor *W, int64_t M
     void *bytes = host_bytes(W, &owned);
     if (!bytes) return -ENOMEM;
     spq4k_weights *w = NULL;
-    const int rc = spq4k_weights_upload(b->ctx, bytes, M, K, E, &w);
+    const int rc = spq4k_weights_upload_type(b->ctx, (int)W->type, bytes, M, K, E, &w);
     if (owned) free(bytes);
     if (rc) return rc;
     b->res[b->nres++] = (struct resident){W, W->data, nbytes, w};
@@ -182,9 +183,12 @@ static void run_mul_mat_id(struct ggml_tensor *dst, int ith, int nth, void *user
     if (rc) fail(b, dst, rc, "spq4k_ggml_mul_mat_id");
 }
 
+/* weight types the library runs (spq4k.h: SPQ4K_TYPE_Q4_K, SPQ4K_TYPE_Q6_K) */
+static int supported(enum ggml_type t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q6_K; }
+
 struct ggml_tensor *spq4k_ggml_mul_mat(struct ggml_context *ctx, struct ggml_tensor *W, struct ggml_tensor *x,
                                        spq4k_ggml *b) {
-    if (!ctx || !W || !x || !b || W->type != GGML_TYPE_Q4_K || x->type != GGML_TYPE_F32 || x->ne[0] != W->ne[0] ||
+    if (!ctx || !W || !x || !b || !supported(W->type) || x->type != GGML_TYPE_F32 || x->ne[0] != W->ne[0] ||
         W->ne[2] != 1 || W->ne[3] != 1 || x->ne[2] != 1 || x->ne[3] != 1 || !ggml_is_contiguous(W) ||
         !ggml_is_contiguous(x))
         return NULL;
@@ -194,7 +198,7 @@ struct ggml_tensor *spq4k_ggml_mul_mat(struct ggml_context *ctx, struct ggml_ten
 
 struct ggml_tensor *spq4k_ggml_mul_mat_id(struct ggml_context *ctx, struct ggml_tensor *as, struct ggml_tensor *x,
                                           struct ggml_tensor *ids, spq4k_ggml *b) {
-    if (!ctx || !as || !x || !ids || !b || as->type != GGML_TYPE_Q4_K || x->type != GGML_TYPE_F32 ||
+    if (!ctx || !as || !x || !ids || !b || !supported(as->type) || x->type != GGML_TYPE_F32 ||
         ids->type != GGML_TYPE_I32 || x->ne[0] != as->ne[0] || ids->ne[1] != x->ne[2] ||
         (x->ne[1] != 1 && x->ne[1] != ids->ne[0]) || as->ne[3] != 1 || x->ne[3] != 1 || !ggml_is_contiguous(as) ||
         !ggml_is_contiguous(x) || !ggml_is_contiguous(ids))

@@ -5,8 +5,8 @@
  * ggml's GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID nodes, once with the adapter's
  * spq4k nodes — computes it on the CPU with ggml_graph_compute_with_ctx and
  * returns both outputs; the Python test compares them with close_enough.
- * Weights are seeded N(0, 0.02) quantised by ggml_quantize_chunk (Q4_K),
- * activations seeded N(0, 1).
+ * Weights are seeded N(0, 0.02) quantised by ggml_quantize_chunk (Q4_K or
+ * Q6_K, as the caller asks), activations seeded N(0, 1).
  */
 #include <math.h>
 #include <stdint.h>
@@ -36,12 +36,12 @@ static void normal_fill(float *p, int64_t n, uint64_t seed, float std) {
     }
 }
 
-/* a Q4_K weight [K, M, E] from seeded N(0, 0.02) values */
-static struct ggml_tensor *q4k_weight(struct ggml_context *ctx, int64_t K, int64_t M, int64_t E, uint64_t seed,
-                                      float *scratch) {
-    struct ggml_tensor *w = ggml_new_tensor_3d(ctx, GGML_TYPE_Q4_K, K, M, E);
+/* a weight [K, M, E] of ggml type `type` from seeded N(0, 0.02) values */
+static struct ggml_tensor *q_weight(struct ggml_context *ctx, int type, int64_t K, int64_t M, int64_t E,
+                                    uint64_t seed, float *scratch) {
+    struct ggml_tensor *w = ggml_new_tensor_3d(ctx, (enum ggml_type)type, K, M, E);
     normal_fill(scratch, K * M * E, seed, 0.02f);
-    ggml_quantize_chunk(GGML_TYPE_Q4_K, scratch, w->data, 0, M * E, K, NULL);
+    ggml_quantize_chunk((enum ggml_type)type, scratch, w->data, 0, M * E, K, NULL);
     return w;
 }
 
@@ -82,8 +82,8 @@ static struct ggml_context *new_ctx(size_t bytes) {
     return ggml_init(ip);
 }
 
-/* y [M, T] = W [K, M] x x [K, T] */
-int check_mul_mat(int64_t M, int64_t K, int64_t T, uint64_t seed, int nthreads, float *y_ref, float *y_ada,
+/* y [M, T] = W [K, M] x x [K, T], W of ggml type `type` */
+int check_mul_mat(int type, int64_t M, int64_t K, int64_t T, uint64_t seed, int nthreads, float *y_ref, float *y_ada,
                   char *err, int errlen) {
     spq4k_ggml *b;
     int rc = spq4k_ggml_init(0, &b);
@@ -93,20 +93,21 @@ int check_mul_mat(int64_t M, int64_t K, int64_t T, uint64_t seed, int nthreads, 
     }
     struct ggml_context *ctx = new_ctx((size_t)M * K * 4 + (size_t)K * T * 16 + (size_t)M * T * 16 + (64 << 20));
     float *tmp = (float *)malloc((size_t)M * K * sizeof(float));
-    struct ggml_tensor *W = q4k_weight(ctx, K, M, 1, seed, tmp);
+    struct ggml_tensor *W = q_weight(ctx, type, K, M, 1, seed, tmp);
     free(tmp);
     struct ggml_tensor *x = f32_input(ctx, K, T, 1, seed + 1);
     return finish(ctx, b, ggml_mul_mat(ctx, W, x), spq4k_ggml_mul_mat(ctx, W, x, b), nthreads, y_ref, y_ada, err,
                   errlen);
 }
 
-/* a gated feed-forward block, every matmul Q4_K:
+/* a gated feed-forward block, gate and up Q4_K, down of type down_type (a
+ * Q4_K_M model stores some ffn_down tensors as Q6_K):
  * y [D, T] = down [F, D] x (silu(gate [D, F] x x) * (up [D, F] x x)).
  * y_ref: all ggml; y_ada: all three matmuls through the adapter; y_chk:
  * ggml's down matmul applied to the adapter's own hidden activations (the
  * per-op comparison for the last node, free of upstream re-quantisation). */
-int check_mlp(int64_t D, int64_t F, int64_t T, uint64_t seed, int nthreads, float *y_ref, float *y_ada, float *y_chk,
-              char *err, int errlen) {
+int check_mlp(int down_type, int64_t D, int64_t F, int64_t T, uint64_t seed, int nthreads, float *y_ref,
+              float *y_ada, float *y_chk, char *err, int errlen) {
     spq4k_ggml *b;
     int rc = spq4k_ggml_init(0, &b);
     if (rc) {
@@ -115,9 +116,9 @@ int check_mlp(int64_t D, int64_t F, int64_t T, uint64_t seed, int nthreads, floa
     }
     struct ggml_context *ctx = new_ctx((size_t)3 * D * F * 4 + (size_t)(D + F) * T * 64 + (64 << 20));
     float *tmp = (float *)malloc((size_t)D * F * sizeof(float));
-    struct ggml_tensor *gate = q4k_weight(ctx, D, F, 1, seed, tmp);
-    struct ggml_tensor *up = q4k_weight(ctx, D, F, 1, seed + 1, tmp);
-    struct ggml_tensor *down = q4k_weight(ctx, F, D, 1, seed + 2, tmp);
+    struct ggml_tensor *gate = q_weight(ctx, GGML_TYPE_Q4_K, D, F, 1, seed, tmp);
+    struct ggml_tensor *up = q_weight(ctx, GGML_TYPE_Q4_K, D, F, 1, seed + 1, tmp);
+    struct ggml_tensor *down = q_weight(ctx, down_type, F, D, 1, seed + 2, tmp);
     free(tmp);
     struct ggml_tensor *x = f32_input(ctx, D, T, 1, seed + 3);
     struct ggml_tensor *hr = ggml_mul(ctx, ggml_silu(ctx, ggml_mul_mat(ctx, gate, x)), ggml_mul_mat(ctx, up, x));
@@ -140,9 +141,10 @@ int check_mlp(int64_t D, int64_t F, int64_t T, uint64_t seed, int nthreads, floa
     return finish(ctx, b, yr, yc ? ya : NULL, nthreads, y_ref, y_ada, err, errlen);
 }
 
-/* y [M, n_used, T] = mul_mat_id(as [K, M, E], x [K, ne11, T], ids [n_used, T]) */
-int check_mul_mat_id(int64_t M, int64_t K, int64_t E, int64_t n_used, int64_t ne11, int64_t T, const int32_t *ids_in,
-                     uint64_t seed, int nthreads, float *y_ref, float *y_ada, char *err, int errlen) {
+/* y [M, n_used, T] = mul_mat_id(as [K, M, E], x [K, ne11, T], ids [n_used, T]), as of type `type` */
+int check_mul_mat_id(int type, int64_t M, int64_t K, int64_t E, int64_t n_used, int64_t ne11, int64_t T,
+                     const int32_t *ids_in, uint64_t seed, int nthreads, float *y_ref, float *y_ada, char *err,
+                     int errlen) {
     spq4k_ggml *b;
     int rc = spq4k_ggml_init(0, &b);
     if (rc) {
@@ -152,7 +154,7 @@ int check_mul_mat_id(int64_t M, int64_t K, int64_t E, int64_t n_used, int64_t ne
     struct ggml_context *ctx =
         new_ctx((size_t)M * K * E * 4 + (size_t)K * ne11 * T * 16 + (size_t)M * n_used * T * 16 + (64 << 20));
     float *tmp = (float *)malloc((size_t)M * K * E * sizeof(float));
-    struct ggml_tensor *as = q4k_weight(ctx, K, M, E, seed, tmp);
+    struct ggml_tensor *as = q_weight(ctx, type, K, M, E, seed, tmp);
     free(tmp);
     struct ggml_tensor *x = f32_input(ctx, K, ne11, T, seed + 1);
     struct ggml_tensor *ids = ggml_new_tensor_2d(ctx, GGML_TYPE_I32, n_used, T);

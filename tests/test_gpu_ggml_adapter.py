@@ -1,4 +1,5 @@
-"""The ggml engine adapter (include/spq4k_ggml.h) inside a real ggml graph.
+"""The ggml engine adapter (include/spq4k_ggml.h) inside a real ggml graph,
+for Q4_K weights and for the Q6_K tensors a Q4_K model carries beside them.
 
 The reference's own ggml (compiled from its sources into oracle/_ref) hosts a
 graph in which the same inputs go through ggml's GGML_OP_MUL_MAT /
@@ -22,7 +23,7 @@ import os
 import numpy as np
 import pytest
 
-from _oracle import close_enough
+from _oracle import TYPE_Q4_K, TYPE_Q6_K, close_enough
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -36,10 +37,10 @@ def drv():
     lib = ctypes.CDLL(DRIVER)
     f32p = ctypes.POINTER(ctypes.c_float)
     i64, u64, cint = ctypes.c_int64, ctypes.c_uint64, ctypes.c_int
-    lib.check_mul_mat.argtypes = [i64, i64, i64, u64, cint, f32p, f32p, ctypes.c_char_p, cint]
-    lib.check_mlp.argtypes = [i64, i64, i64, u64, cint, f32p, f32p, f32p, ctypes.c_char_p, cint]
-    lib.check_mul_mat_id.argtypes = [i64, i64, i64, i64, i64, i64, ctypes.POINTER(ctypes.c_int32), u64, cint, f32p,
-                                     f32p, ctypes.c_char_p, cint]
+    lib.check_mul_mat.argtypes = [cint, i64, i64, i64, u64, cint, f32p, f32p, ctypes.c_char_p, cint]
+    lib.check_mlp.argtypes = [cint, i64, i64, i64, u64, cint, f32p, f32p, f32p, ctypes.c_char_p, cint]
+    lib.check_mul_mat_id.argtypes = [cint, i64, i64, i64, i64, i64, i64, ctypes.POINTER(ctypes.c_int32), u64, cint,
+                                     f32p, f32p, ctypes.c_char_p, cint]
     return lib
 
 
@@ -60,34 +61,37 @@ def _check(yr, ya, what):
                       f"adapter {ya[np.argmax(~ok)]} ggml {yr[np.argmax(~ok)]}")
 
 
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q6_K])
 @pytest.mark.parametrize("M,K,T", [(4096, 4096, 1), (300, 2048, 3), (256, 5120, 8), (512, 4096, 64), (128, 12288, 17)])
-def test_adapter_mul_mat(drv, M, K, T):
-    yr, ya = _run(drv.check_mul_mat, M * T, M, K, T, 11 + T)
-    _check(yr, ya, f"mul_mat M={M} K={K} T={T}")
+def test_adapter_mul_mat(drv, qtype, M, K, T):
+    yr, ya = _run(drv.check_mul_mat, M * T, qtype, M, K, T, 11 + T)
+    _check(yr, ya, f"mul_mat type={qtype} M={M} K={K} T={T}")
 
 
 FF_NORMWISE = 2e-3   # bound on ||y_adapter - y_ggml|| / ||y_ggml|| for the whole block
 
 
+@pytest.mark.parametrize("down_type", [TYPE_Q4_K, TYPE_Q6_K])
 @pytest.mark.parametrize("D,F,T", [(2048, 5632, 1), (1024, 2816, 6), (1024, 2816, 32)])
-def test_adapter_feed_forward(drv, D, F, T):
+def test_adapter_feed_forward(drv, down_type, D, F, T):
     n = D * T
     yr, ya, yc = (np.full(n, np.nan, np.float32) for _ in range(3))
     err = ctypes.create_string_buffer(256)
     f32p = ctypes.POINTER(ctypes.c_float)
-    rc = drv.check_mlp(D, F, T, 3 + T, 8, yr.ctypes.data_as(f32p), ya.ctypes.data_as(f32p), yc.ctypes.data_as(f32p),
-                       err, 256)
+    rc = drv.check_mlp(down_type, D, F, T, 3 + T, 8, yr.ctypes.data_as(f32p), ya.ctypes.data_as(f32p),
+                       yc.ctypes.data_as(f32p), err, 256)
     assert rc == 0, err.value.decode()
     _check(yc, ya, f"feed-forward down node D={D} F={F} T={T}")
     rel = float(np.linalg.norm(ya.astype(np.float64) - yr) / np.linalg.norm(yr.astype(np.float64)))
     assert rel <= FF_NORMWISE, f"feed-forward block D={D} F={F} T={T}: normwise {rel:.3e} > {FF_NORMWISE}"
 
 
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q6_K])
 @pytest.mark.parametrize("T,ne11", [(1, 1), (3, 4), (12, 1)])
-def test_adapter_mul_mat_id(drv, T, ne11):
+def test_adapter_mul_mat_id(drv, qtype, T, ne11):
     E, M, K, k = 32, 256, 1024, 4
     rng = np.random.default_rng(T)
     ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
-    yr, ya = _run(drv.check_mul_mat_id, M * k * T, M, K, E, k, ne11 if ne11 != 4 else k, T,
+    yr, ya = _run(drv.check_mul_mat_id, M * k * T, qtype, M, K, E, k, ne11 if ne11 != 4 else k, T,
                   ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), 21 + T)
-    _check(yr, ya, f"mul_mat_id T={T} ne11={ne11}")
+    _check(yr, ya, f"mul_mat_id type={qtype} T={T} ne11={ne11}")
