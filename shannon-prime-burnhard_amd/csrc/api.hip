@@ -252,7 +252,8 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         if (e != hipSuccess) return hip_fail(c, e, "gemv decode launch");
         return 0;
     }
-    if (p.fmt == WF_Q4K && T >= c->gemv_mfma_min_t && c->force_bpr == 0) {
+    // SPQ4K_GEMM_MODE=1 keeps Q6_K batches on the sdot4 kernels (gemv_chunked)
+    if (T >= c->gemv_mfma_min_t && c->force_bpr == 0 && !(p.fmt == WF_Q6K && c->gemm_mode == 1)) {
         // 4 <= T <= 8: the sdot4 kernel's integer work grows with T while the
         // matrix cores' 16-token tile costs the same from T = 1 to 16
         return gemm_segments(c, n, W, x, y, T, c->gemm_mode == 1 ? 1 : 0);
@@ -761,8 +762,13 @@ int gemm_segments(spq4k_ctx* c, int n, const spq4k_weights* const* W, const floa
     for (int i = n; i < GEMM_MAX_SEG; ++i) p.seg[i].tile_begin = p.seg[i].row_begin = INT32_MAX;
     p.nseg = n;
     p.rows = (int32_t)rows;
+    p.fmt = W[0]->fmt;
     if (tiles16 * ((T + 15) / 16) > (1ll << 31) - 1 || rows > (1ll << 31) - 1)
         return set_err(c, -EINVAL, "gemm: grid too large");
+    if (p.fmt == WF_Q6K && mode == 1) {   // sdot4 kernels over 8-token slices
+        if (T <= SPQ4K_GEMV_MAX_T) return gemv_launch(c, n, W, X, Y, T);
+        return gemv_chunked(c, n, W, X, Y, T);
+    }
     hipError_t e;
     if (gemm_use_skinny((int)T, mode)) {
         int rc = q8_planes(c, X, K, (int)T, p.nb, &p.Q);
@@ -806,10 +812,6 @@ int spq4k_gemm_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const f
         if (W[i]->type != W[0]->type) return set_err(c, -EINVAL, "gemm: matrices must share the weight type");
         if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemm: misaligned weights");
         if (W[i]->device != c->device) return set_err(c, -EINVAL, "gemm: weights live on another device");
-    }
-    if (W[0]->fmt == WF_Q6K) {
-        if (T <= SPQ4K_GEMV_MAX_T) return gemv_launch(c, n, W, X, Y, T);
-        return gemv_chunked(c, n, W, X, Y, T);
     }
     return gemm_segments(c, n, W, X, Y, T, c->gemm_mode);
 }

@@ -23,6 +23,7 @@
 //   - per super-block acc += d8 (d I - dmin M) in fp32.
 #include "gemv_core.h"
 #include "launch.h"
+#include "q6k_core.h"
 #include "ring_core.h"
 
 #include <type_traits>
@@ -331,12 +332,22 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 // slots re-read a valid address). A wave waits for its own loads of a stage
 // with s_waitcnt vmcnt (loads complete in order) before the barrier that
 // publishes the stage to the other waves.
-template <int RT, int CT, int NW, int S, int TW = 16>
+//
+// F selects the weight format: 0 = Q4_K (9 slots a row, ring_block /
+// ring_block32), 1 = Q6_K (14 slots a row of Q6K_LDS = 224 bytes: slots 0..12
+// are block bytes 0..207 and slot 13 re-reads bytes 194..209, so no load
+// leaves its 210-byte block; ring_block_q6, 16x16 tiles). Q6_K block starts
+// are 2-byte aligned; global loads on gfx950 take unaligned addresses.
+template <int RT, int CT, int NW, int S, int TW = 16, int F = 0>
 __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
     static_assert(TW == 16 || TW == 32, "16x16 or 32x32 output tiles");
+    static_assert(F == 0 || TW == 16, "Q6_K runs on 16x16 tiles");
+    constexpr int WSL = F ? 14 : 9;                  // 16-byte slots of a row's block
+    constexpr int BB = F ? Q6K_BYTES : Q4K_BYTES;    // block bytes in memory
+    constexpr int ROWB = 16 * WSL;                   // bytes of a row in the stage
     constexpr int TOK = CT * TW;
     constexpr int ROWS = RT * TW * NW;
-    constexpr int W_SLOTS = ROWS * 9, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
+    constexpr int W_SLOTS = ROWS * WSL, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
     constexpr int W_LOADS = (W_SLOTS + 63) / 64, Q_LOADS = (Q_SLOTS + 63) / 64, M_LOADS = (M_SLOTS + 63) / 64;
     constexpr int NLOAD = W_LOADS + Q_LOADS + M_LOADS;
     constexpr int NPW = (NLOAD + NW - 1) / NW;    // loads per wave per stage
@@ -375,9 +386,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
         src[i] = p.Q.mn;                          // surplus and padding: any valid address
         stride[i] = 0;
         if (J < W_LOADS) {
-            const int r = min(row0 + slot / 9, M - 1);
-            src[i] = W + ((size_t)r * nb + kb0) * Q4K_BYTES + 16 * (slot % 9);
-            stride[i] = Q4K_BYTES;
+            const int r = min(row0 + slot / WSL, M - 1);
+            const int sub = slot % WSL;
+            src[i] = W + ((size_t)r * nb + kb0) * BB + (F && sub == 13 ? 194 : 16 * sub);
+            stride[i] = BB;
         } else if (J < W_LOADS + Q_LOADS) {
             const int sl = slot - W_LOADS * 64;
             if (sl < Q_SLOTS) {
@@ -420,7 +432,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * NPW) : "memory");
         issue(min(b + S - 1, nbl - 1), (b + S - 1) % S);
 
-        if constexpr (TW == 16)
+        if constexpr (F == 1)
+            ring_block_q6<RT, CT>(lds[buf] + (wave * RT * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+        else if constexpr (TW == 16)
             ring_block<RT, CT>(lds[buf] + (wave * RT * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
         else
             ring_block32<RT, CT>(lds[buf] + (wave * RT * 32) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, lane, acc);
@@ -683,15 +697,16 @@ struct TiledShape {
     int rows, tok;   // workgroup tile
     bool ring;       // ring kernel: permuted Q8_K values, K ranges
     hipError_t (*launch)(const GemmParams&, int grid, hipStream_t);
+    int fmt = WF_Q4K;   // weight format the shape runs
 };
 template <int RT, int CT, int WR, int WK>
 static hipError_t launch_tiled_(const GemmParams& p, int grid, hipStream_t st) {
     hipLaunchKernelGGL((gemm_tiled_kernel<RT, CT, WR, WK>), dim3((unsigned)grid), dim3(256), 0, st, p);
     return hipGetLastError();
 }
-template <int RT, int CT, int NW, int S, int TW = 16>
+template <int RT, int CT, int NW, int S, int TW = 16, int F = 0>
 static hipError_t launch_ring_(const GemmParams& p, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_ring_kernel<RT, CT, NW, S, TW>), dim3((unsigned)grid), dim3(NW * 64), 0, st, p);
+    hipLaunchKernelGGL((gemm_ring_kernel<RT, CT, NW, S, TW, F>), dim3((unsigned)grid), dim3(NW * 64), 0, st, p);
     return hipGetLastError();
 }
 static const TiledShape kTiled[] = {
@@ -709,6 +724,12 @@ static const TiledShape kTiled[] = {
     {256, 64, true, launch_ring_<1, 2, 8, 2, 32>},  // 11: ring 32x32, 8 waves, 2 stages
     {128, 64, true, launch_ring_<1, 2, 4, 3, 32>},  // 12: ring 32x32, 4 waves, 3 stages
     {128, 32, true, launch_ring_<1, 1, 4, 3, 32>},  // 13: ring 32x32, T <= 32
+    // Q6_K (ring_block_q6)
+    {128, 64, true, launch_ring_<1, 4, 8, 3, 16, 1>, WF_Q6K},   // 14: 8 waves, 3 stages of 48 KB
+    {128, 16, true, launch_ring_<1, 1, 8, 3, 16, 1>, WF_Q6K},   // 15: T <= 16
+    {128, 32, true, launch_ring_<1, 2, 8, 3, 16, 1>, WF_Q6K},   // 16: T <= 32
+    {256, 64, true, launch_ring_<2, 4, 8, 2, 16, 1>, WF_Q6K},   // 17: 8 waves, 2 stages of 80 KB
+    {64, 64, true, launch_ring_<1, 4, 4, 3, 16, 1>, WF_Q6K},    // 18: 4 waves
 };
 constexpr int N_TILED = (int)(sizeof(kTiled) / sizeof(kTiled[0]));
 
@@ -723,7 +744,10 @@ static int64_t row_tiles(const GemmParams& p, int rows) {
 GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
     GemmPlan g;
     int cfg = p.cfg;
-    if (cfg < 0 || cfg >= N_TILED) {
+    if (cfg >= 0 && cfg < N_TILED && kTiled[cfg].fmt != p.fmt) cfg = -1;   // a shape of the other format
+    if ((cfg < 0 || cfg >= N_TILED) && p.fmt == WF_Q6K) {
+        cfg = p.T <= 16 ? 15 : (p.T <= 32 ? 16 : 14);
+    } else if (cfg < 0 || cfg >= N_TILED) {
         if (p.T <= 16) {
             cfg = 6;
         } else if (p.T <= 32) {
@@ -766,6 +790,7 @@ GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
 hipError_t launch_gemm(const GemmParams& p0, hipStream_t st) {
     if (p0.cfg < 0 || p0.cfg >= N_TILED) return hipErrorInvalidValue;
     const TiledShape& s = kTiled[p0.cfg];
+    if (s.fmt != p0.fmt) return hipErrorInvalidValue;
     if (!s.ring && p0.ksplit != 1) return hipErrorInvalidValue;
     GemmParams p = p0;
     int64_t tiles = 0;

@@ -131,6 +131,7 @@ struct GemmParams {
     int32_t ksplit;     // K ranges (ring kernels): 1, or partial sums in P then a reduction
     int32_t kchunk;     // super-blocks per K range
     float* P;           // [ksplit][T][rows] partial plane when ksplit > 1
+    int32_t fmt;        // WFmt of every segment (shapes are per format)
 };
 // Launch plan of the tiled / ring kernels for a GemmParams (T, nb, segments,
 // cfg): shape, K split and the scratch the partial plane needs.

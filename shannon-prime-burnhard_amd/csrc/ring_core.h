@@ -1,6 +1,6 @@
-// ring_core.h — one Q4_K super-block x Q8_K activations on gfx950 matrix
-// cores, read from an LDS stage (device code shared by the ring kernels of
-// k_gemm.hip and k_moe.hip).
+// ring_core.h — one Q4_K super-block (or one Q6_K block, ring_block_q6 below)
+// x Q8_K activations on gfx950 matrix cores, read from an LDS stage (device
+// code shared by the ring kernels of k_gemm.hip and k_moe.hip).
 //
 // Numerics are those of the reference CPU path (ggml_vec_dot_q4_K_q8_K,
 // ggml-cpu/arch/x86/quants.c:1900-1982), with the integer sums exact:
@@ -232,6 +232,123 @@ __device__ __forceinline__ void ring_block32(const uint8_t* wt, const uint8_t* q
             for (int i = 0; i < 16; ++i) {
                 const int I = (ch[i] << 3) + cl[i];
                 acc[r][ct][i] = fmaf(d8, fmaf(-dmr[r][i], cm[i], dr[r][i] * (float)I), acc[r][ct][i]);
+            }
+        }
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// One Q6_K block (ggml-common.h:348-357) on 16x16 tiles, for the ring kernel
+// with F = 1. Numerics of ggml_vec_dot_q6_K_q8_K
+// (ggml-cpu/arch/x86/quants.c:2288-2366) with the integer sums exact:
+//   acc[row][t] += (d_row d8_t) I,   I = sum_j scale_j sum_{k in j} (q_k - 32) q8_k
+// The int8 scale (-128..127) is folded into the weight operand:
+// w = scale * (q - 32) lies in -4096..4096, written w = 256 a + b with
+// b = w - 256 round(w / 256) in -128..127 and a in -16..16, two int8
+// operands; v_mfma_i32_16x16x64_i8 gives A = sum a q8 and B = sum b q8 over
+// the block and I = 256 A + B exactly (|256 A| < 2^27).
+// Lane (c16, q), step s: the k slots are those of the Q4_K ring (values
+// 64q + 8s .. +7 and 64q + 32 + 8s .. +7, the permuted Q8_K order), which in
+// Q6_K are quarters h0 = 2 (q & 1) and h0 + 1 of half n = q >> 1 at
+// l = 8s .. 8s+7: nibble q & 1 of ql[64n + l] and ql[64n + 32 + l] and bits
+// 4 (q & 1) .. +3 of qh[32n + l]; their sub-blocks 8n + 2 h0 + s / 2 and
+// 8n + 2 h0 + 2 + s / 2.
+// Stage rows are Q6K_LDS = 224 bytes: block bytes 0..207, then 194..209 (the
+// last 16-byte load of a block reads its final 16 bytes), so d is at 222.
+constexpr int Q6K_LDS = 224;
+
+// u16 lanes w0 = v0 * sc + c, w1 = v2 * sc + c of bytes v0..v3 (v_pk_mad_u16)
+__device__ __forceinline__ uint32_t pk_mad_u16(uint32_t a, uint32_t b, uint32_t c) {
+    u16x2 x, y, z;
+    __builtin_memcpy(&x, &a, 4);
+    __builtin_memcpy(&y, &b, 4);
+    __builtin_memcpy(&z, &c, 4);
+    const u16x2 r = x * y + z;
+    uint32_t o;
+    __builtin_memcpy(&o, &r, 4);
+    return o;
+}
+
+// Four 6-bit values (bytes of v) times a scale, split into the two int8
+// operands: sc2 = scale in both u16 halves, c2 = 128 - 32 scale in both.
+// u = w + 128 = 256 a + (b + 128) with b + 128 in 0..255: a is the high byte
+// of u, b its low byte minus 128.
+__device__ __forceinline__ void q6_fold(uint32_t v, uint32_t sc2, uint32_t c2, uint32_t& ahi, uint32_t& blo) {
+    const uint32_t ev = __builtin_amdgcn_perm(0u, v, 0x0C020C00u);   // bytes 0, 2 -> u16 lanes
+    const uint32_t od = __builtin_amdgcn_perm(0u, v, 0x0C030C01u);   // bytes 1, 3
+    const uint32_t ue = pk_mad_u16(ev, sc2, c2), uo = pk_mad_u16(od, sc2, c2);
+    blo = __builtin_amdgcn_perm(uo, ue, 0x06020400u) ^ 0x80808080u;   // low bytes: e0 o0 e1 o1
+    ahi = __builtin_amdgcn_perm(uo, ue, 0x07030501u);                 // high bytes
+}
+
+template <int RT, int CT>
+__device__ __forceinline__ void ring_block_q6(const uint8_t* wt, const uint8_t* qreg, const uint8_t* mreg, int c16,
+                                              int q, v4f (&acc)[RT][CT]) {
+    const int n = q >> 1, ns = 4 * (q & 1);
+    v4i aa[RT][4], ab[RT][4];
+    float dr[RT][4];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const uint8_t* wr = wt + (r * 16 + c16) * Q6K_LDS;
+        v4i ql[4], qh[2];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ql[k] = *reinterpret_cast<const v4i*>(wr + 64 * n + 16 * k);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) qh[k] = *reinterpret_cast<const v4i*>(wr + 128 + 32 * n + 16 * k);
+        // scales 8n + 2h0 + {0, 1, 2, 3}: (h0, l < 16), (h0, l >= 16), (h0 + 1, l < 16), (h0 + 1, l >= 16)
+        const uint32_t scw = *reinterpret_cast<const uint32_t*>(wr + 192 + 8 * n + 4 * (q & 1));
+        uint32_t sc2[4], c2[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int sv = (int)(int8_t)((scw >> (8 * k)) & 0xFFu);
+            sc2[k] = ((uint32_t)sv & 0xFFFFu) * 0x10001u;
+            c2[k] = ((uint32_t)(128 - 32 * sv) & 0xFFFFu) * 0x10001u;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint16_t hd = *reinterpret_cast<const uint16_t*>(wt + (r * 16 + 4 * q + i) * Q6K_LDS + 222);
+            dr[r][i] = half_bits_to_float(hd);
+        }
+        // dword position p (l = 4p .. 4p+3): quarter h0 from ql[p], h0 + 1 from ql[8 + p]
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            uint32_t av[4], bv[4];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int pp = 2 * s + e;
+                const uint32_t lo = (uint32_t)ql[pp >> 2][pp & 3], hi = (uint32_t)ql[2 + (pp >> 2)][pp & 3];
+                const uint32_t hb = (uint32_t)qh[pp >> 2][pp & 3] >> ns;
+                const uint32_t v0 = ((lo >> ns) & 0x0F0F0F0Fu) | ((hb & 0x03030303u) << 4);
+                const uint32_t v1 = ((hi >> ns) & 0x0F0F0F0Fu) | (((hb >> 2) & 0x03030303u) << 4);
+                q6_fold(v0, sc2[s >> 1], c2[s >> 1], av[e], bv[e]);
+                q6_fold(v1, sc2[2 + (s >> 1)], c2[2 + (s >> 1)], av[2 + e], bv[2 + e]);
+            }
+            aa[r][s] = v4i{(int)av[0], (int)av[1], (int)av[2], (int)av[3]};
+            ab[r][s] = v4i{(int)bv[0], (int)bv[1], (int)bv[2], (int)bv[3]};
+        }
+    }
+    const uint8_t* qb = qreg + c16 * RING_QS + 64 * q;
+    const uint8_t* mb = mreg + c16 * Q8MN_BYTES;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+        v4i bq[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bq[s] = *reinterpret_cast<const v4i*>(qb + ct * 16 * RING_QS + 16 * s);
+        const float d8 = *reinterpret_cast<const float*>(mb + ct * 16 * Q8MN_BYTES + 32);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            v4i ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(aa[r][0], bq[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            v4i cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(ab[r][0], bq[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int s = 1; s < 4; ++s) {
+                ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(aa[r][s], bq[s], ca, 0, 0, 0);
+                cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(ab[r][s], bq[s], cb, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int I = (ca[i] << 8) + cb[i];
+                acc[r][ct][i] = fmaf(dr[r][i] * d8, (float)I, acc[r][ct][i]);
             }
         }
     }

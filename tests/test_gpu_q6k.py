@@ -6,8 +6,9 @@ test_oracle_q6k.py):
   - dequantisation (dequantize_row_q6_K) and the encoder (quantize_q6_K):
     bit-exact;
   - integer sub-block sums: bit-exact against the oracle's brute force;
-  - vec_dot, GEMV (T = 1 decode kernel and the T <= 8 kernel), batches above
-    8 tokens, expert-gathered matvec (every MoE path): every element within
+  - vec_dot, GEMV (T = 1 decode kernel and the sdot4 kernel), batches on the
+    matrix-core ring (every Q6_K launch shape, K split, ragged edges) and on
+    the sdot4 slices, expert-gathered matvec (every MoE path): every element within
     close_enough (1e-4 relative or 1e-5 absolute,
     tests/desktop/test_sp_kernels.cpp:34-48) of ggml's x86 order.
 Weights are encoder output (N(0, 0.02)) or arbitrary block bytes, which reach
@@ -211,6 +212,80 @@ def test_mul_mat_batched(ctx, oracle, T):
         X = rng.standard_normal((T, K)).astype(np.float32)
         got = ctx.mul_mat(ctx.upload(W, M, K, type=TYPE_Q6_K), X)
         _check(got, oracle.mul_mat_type(TYPE_Q6_K, W, M, K, X), f"q6k mul_mat T={T} M={M} K={K}")
+
+
+@pytest.mark.parametrize("cfg", [14, 15, 16, 17, 18])
+def test_ring_launch_shapes(oracle, cfg):
+    """Every Q6_K matrix-core launch shape, on ragged rows and tokens and on
+    rows of an odd number of blocks (2-byte-aligned block starts)."""
+    rng = np.random.default_rng(610 + cfg)
+    c = context_with({"SPQ4K_GEMM_CFG": cfg})
+    try:
+        for M, K, T in ((300, 768, 5), (200, 4096, 33), (1000, 2048, 100)):
+            W = _enc(oracle, rng, M, K)
+            X = rng.standard_normal((T, K)).astype(np.float32)
+            got = c.mul_mat(c.upload(W, M, K, type=TYPE_Q6_K), X)
+            _check(got, oracle.mul_mat_type(TYPE_Q6_K, W, M, K, X), f"cfg={cfg} M={M} K={K} T={T}")
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("M,K,T", [(64, 27648, 64), (4096, 4096, 128), (512, 12288, 256), (96, 5120, 7)])
+def test_ring_planned(ctx, oracle, M, K, T):
+    """The planner's choice, including K splits (few rows, long K) and the
+    reduction of their partial sums."""
+    rng = np.random.default_rng(M + K + T)
+    W = _gpu_enc(ctx, rng, M, K)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    got = ctx.mul_mat(ctx.upload(W, M, K, type=TYPE_Q6_K), X)
+    _check(got, oracle.mul_mat_type(TYPE_Q6_K, W, M, K, X), f"planned M={M} K={K} T={T}")
+
+
+def test_ring_extreme_operands(ctx, oracle):
+    """Blocks at the ends of the folded operand range: scale -128 or 127 with
+    6-bit values 0 or 63 (w = scale (q - 32) from -4064 to 4096), every
+    combination, one combination a row so that with one-sign activations a
+    row's blocks add up without cancellation; and arbitrary blocks held to the
+    summation bound."""
+    rng = np.random.default_rng(620)
+    M, K, T = 64, 1024, 48
+    nb = K // QK
+    blk = np.zeros((M, nb, Q6K), np.uint8)
+    for r in range(M):
+        for b in range(nb):
+            v = r % 4
+            s = -128 if v < 2 else 127
+            qv = 0 if v % 2 == 0 else 63
+            blk[r, b, 0:128] = (qv & 15) | ((qv & 15) << 4)
+            hb = qv >> 4
+            blk[r, b, 128:192] = hb | (hb << 2) | (hb << 4) | (hb << 6)
+            blk[r, b, 192:208] = np.array([s] * 16, np.int8).view(np.uint8)
+            blk[r, b, 208:210] = np.array([2.0 ** -12 * (1 + r % 5)], np.float16).view(np.uint8)
+    W = blk.ravel()
+    X = np.abs(rng.standard_normal((T, K))).astype(np.float32)
+    Wd = ctx.upload(W, M, K, type=TYPE_Q6_K)
+    _check(ctx.mul_mat(Wd, X), oracle.mul_mat_type(TYPE_Q6_K, W, M, K, X), "extreme one-sign")
+    W2 = _rand_blocks(rng, M * nb)
+    X2 = rng.standard_normal((T, K)).astype(np.float32)
+    exact, mag = _exact_rows(oracle, W2, M, K, X2)
+    _check_bounded(ctx.mul_mat(ctx.upload(W2, M, K, type=TYPE_Q6_K), X2), exact, mag, nb, "arbitrary blocks")
+
+
+@pytest.mark.parametrize("T", [4, 40])
+def test_ring_matches_sdot4_slices(oracle, T):
+    """SPQ4K_GEMM_MODE=1 keeps Q6_K batches on the sdot4 kernels: both paths
+    within tolerance of the oracle on the same inputs."""
+    rng = np.random.default_rng(630 + T)
+    M, K = 384, 4096
+    W = _enc(oracle, rng, M, K)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    exp = oracle.mul_mat_type(TYPE_Q6_K, W, M, K, X)
+    for env in ({}, {"SPQ4K_GEMM_MODE": 1}):
+        c = context_with(env)
+        try:
+            _check(c.mul_mat(c.upload(W, M, K, type=TYPE_Q6_K), X), exp, f"{env} T={T}")
+        finally:
+            c.close()
 
 
 @pytest.mark.parametrize("T", [1, 4, 12])
