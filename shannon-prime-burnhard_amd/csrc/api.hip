@@ -924,8 +924,11 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     p.route.act_off = rt + 1 + E;
     p.route.act_cnt = rt + 1 + 2 * E;
     p.route.pairs = rt + 1 + 3 * E;
-    // matrix cores (Q4_K) unless the sdot4 kernels are asked for (SPQ4K_MOE_UNFUSED)
-    const bool ring = !c->moe_unfused && bank->fmt == WF_Q4K;
+    // matrix cores unless the sdot4 kernels are asked for (SPQ4K_MOE_UNFUSED);
+    // a Q6_K bank's operand preparation costs more, so its experts go to the
+    // matrix cores only once they receive two pairs on average (measured on
+    // the 2048 x 768 down bank: T = 8 sdot4 31 us against 36, T = 32 65 against 61)
+    const bool ring = !c->moe_unfused && (bank->fmt == WF_Q4K || mean_pairs >= 2);
     hipError_t e;
     if (!ring) {
         e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, mn, false, c->stream);

@@ -19,7 +19,7 @@
 // Calls with at most MOE_FUSED_MAX_PAIRS pairs use moe_fused_kernel instead,
 // which does all three steps in one launch. The sdot4 kernels (moe_gemv,
 // moe_fused, moe_decode) are templates over the weight format and also run
-// Q6_K expert banks (FmtQ6K, q6k_core.h); the matrix-core ring is Q4_K only.
+// Q6_K expert banks (FmtQ6K, q6k_core.h); so is the matrix-core ring (F = 1).
 #include "gemv_core.h"
 #include "launch.h"
 #include "q6k_core.h"
@@ -507,10 +507,13 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(const int32_t* __restrict
                           const_cast<float*>(Q.d), const_cast<uint8_t*>(Q.mn), 1, blockIdx.x - 1);
 }
 
-template <int S>
+// F = 1: Q6_K banks (14 slots a row, the last re-reading block bytes
+// 194..209; ring_block_q6), as in gemm_ring_kernel.
+template <int S, int F = 0>
 __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
     constexpr int NW = 8, ROWS = 128, TOK = 16;
-    constexpr int W_SLOTS = ROWS * 9, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
+    constexpr int WSL = F ? 14 : 9, BB = F ? Q6K_BYTES : Q4K_BYTES, ROWB = 16 * WSL;
+    constexpr int W_SLOTS = ROWS * WSL, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
     constexpr int W_LOADS = W_SLOTS / 64, Q_LOADS = (Q_SLOTS + 63) / 64, M_LOADS = (M_SLOTS + 63) / 64;
     constexpr int NLOAD = W_LOADS + Q_LOADS + M_LOADS;
     constexpr int NPW = (NLOAD + NW - 1) / NW;
@@ -534,7 +537,7 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
     const int nrt = min(p.ring_rt, (M + ROWS - 1) / ROWS - rt0);
     const int len = nrt * nb;                  // super-blocks streamed per token tile
     const uint8_t* __restrict__ W = p.bank + (size_t)e * p.expert_bytes;
-    const size_t row_bytes = (size_t)nb * Q4K_BYTES;
+    const size_t row_bytes = (size_t)nb * BB;
 
     for (int tile0 = 0; tile0 < pcnt; tile0 += TOK) {
         // per load: weight slot (row within the tile, 16-byte chunk), or the
@@ -550,8 +553,9 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
             stride[i] = 0;
             wrow[i] = -1;
             if (J < W_LOADS) {
-                wrow[i] = slot / 9;
-                src[i] = W + 16 * (slot % 9);
+                wrow[i] = slot / WSL;
+                const int sub = slot % WSL;
+                src[i] = W + (F && sub == 13 ? 194 : 16 * sub);
             } else if (J < NLOAD) {
                 const bool isq = J < W_LOADS + Q_LOADS;
                 const int sl = slot - (isq ? W_LOADS : W_LOADS + Q_LOADS) * 64;
@@ -574,7 +578,7 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
 #pragma unroll
             for (int i = 0; i < NPW; ++i) {
                 const uint8_t* a_ = (NW * i + wave) < W_LOADS
-                                        ? src[i] + (size_t)min(rt * ROWS + wrow[i], M - 1) * row_bytes + (size_t)b * Q4K_BYTES
+                                        ? src[i] + (size_t)min(rt * ROWS + wrow[i], M - 1) * row_bytes + (size_t)b * BB
                                         : src[i] + (size_t)b * stride[i];
                 __builtin_amdgcn_global_load_lds(
                     (const void*)a_, (__attribute__((address_space(3))) void*)(lds[buf] + (NW * i + wave) * 1024), 16, 0, 0);
@@ -589,7 +593,10 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
             const int buf = sp % S;
             asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * NPW) : "memory");
             issue(min(sp + S - 1, len - 1), (sp + S - 1) % S);
-            ring_block<1, 1>(lds[buf] + (wave * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+            if constexpr (F == 1)
+                ring_block_q6<1, 1>(lds[buf] + (wave * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+            else
+                ring_block<1, 1>(lds[buf] + (wave * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
             if (sp - (sp / nb) * nb == nb - 1) {
                 // row tile done: lane has rows 4q .. 4q+3 of the wave's 16, pair tile0 + c16
                 if (tile0 + c16 < pcnt) {
@@ -619,7 +626,10 @@ hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t grid = (int64_t)max_act * p.tiles_per_expert;
-    hipLaunchKernelGGL(moe_ring_kernel<3>, dim3((unsigned)grid), dim3(512), 0, st, p);
+    if (p.fmt == WF_Q6K)
+        hipLaunchKernelGGL((moe_ring_kernel<3, 1>), dim3((unsigned)grid), dim3(512), 0, st, p);
+    else
+        hipLaunchKernelGGL((moe_ring_kernel<3, 0>), dim3((unsigned)grid), dim3(512), 0, st, p);
     return hipGetLastError();
 }
 

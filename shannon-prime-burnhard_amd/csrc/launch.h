@@ -72,7 +72,7 @@ struct MoeParams {
     int32_t M, nb, n_used, ne11;
     int32_t tiles_per_expert;
     int32_t chunk_blocks;
-    int32_t fmt;             // WFmt of the bank (moe_gemv_kernel; the ring is Q4_K only)
+    int32_t fmt;             // WFmt of the bank
 };
 
 hipError_t launch_moe_route(const int32_t* ids, int n_pairs, int E, const MoeRoute& r, hipStream_t st);
