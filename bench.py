@@ -344,6 +344,7 @@ def run_single(args, M, K, T, dist, outlier, name, qtype=spq4k.TYPE_Q4_K):
     gbs = alg / (ms * 1e-3) / 1e9
     print(json.dumps({"metric": f"{name} effective HBM GB/s", "value": round(gbs, 2), "unit": "GB/s",
                       "us_per_call": round(ms * 1e3, 3), "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2),
+                      "TOPs_int8": round(2 * M * K * T / (ms * 1e-3) / 1e12, 1),
                       "config": {"workload": name, "M": M, "K": K, "T": T, "weight_copies": copies}}), flush=True)
     for w in ws:
         w.free()
@@ -445,13 +446,19 @@ def run_moe(args):
 
 def run_q6k(args):
     """Q6_K: the sibling K-quant a Q4_K model stores some tensors in. Dense
-    decode shapes of the 8B model at T = 1 (and a T = 8 batch), cold, then the
-    MoE down-projection bank (128 experts of 2048x768) at T = 1..32, 8 layers
-    of banks cold, as in run_moe."""
+    decode shapes of the 8B model at T = 1, a T = 8 batch and the down
+    projection as a prefill matmul (T = 16, 128, 512; the same shape in Q4_K
+    beside it), cold, then the MoE down-projection bank (128 experts of
+    2048x768) at T = 1..32, 8 layers of banks cold, as in run_moe."""
     for name, M, K, T in (("Q6_K attn_v 1024x4096", 1024, 4096, 1), ("Q6_K 4096x4096", 4096, 4096, 1),
                           ("Q6_K ffn_down 4096x12288", 4096, 12288, 1),
-                          ("Q6_K output 151936x4096", 151936, 4096, 1), ("Q6_K 4096x4096 T=8", 4096, 4096, 8)):
-        run_single(args, M, K, T, spq4k.DIST_NORMAL, 1.0, name, spq4k.TYPE_Q6_K)
+                          ("Q6_K output 151936x4096", 151936, 4096, 1), ("Q6_K 4096x4096 T=8", 4096, 4096, 8),
+                          ("Q6_K ffn_down 4096x12288 T=16", 4096, 12288, 16),
+                          ("Q6_K ffn_down 4096x12288 T=128", 4096, 12288, 128),
+                          ("Q6_K ffn_down 4096x12288 T=512", 4096, 12288, 512),
+                          ("Q4_K ffn_down 4096x12288 T=512 (same shape, Q4_K)", 4096, 12288, 512)):
+        qt = spq4k.TYPE_Q4_K if name.startswith("Q4_K") else spq4k.TYPE_Q6_K
+        run_single(args, M, K, T, spq4k.DIST_NORMAL, 1.0, name, qt)
     ctx = spq4k.Context(0)
     E, k, NL, M, K = 128, 8, 8, 2048, 768
     syn = Synth(ctx, E * M * K)
