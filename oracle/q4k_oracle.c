@@ -90,8 +90,8 @@ void or_scale_min_k4(int j, const uint8_t *s, uint8_t *sc, uint8_t *m) {
  * least-squares (scale, min) for its rounding; the lowest weighted squared
  * error wins. The operation order matches the reference so that the chosen
  * L, scale and min are bit-identical. Returns scale, writes -min. */
-static float qkx2_fit(int n, int nmax, const float *x, const float *w, uint8_t *L,
-                      float *neg_min, uint8_t *Laux, float rmin, float rdelta, int nstep) {
+float or_qkx2_fit(int n, int nmax, const float *x, const float *w, uint8_t *L,
+                 float *neg_min, uint8_t *Laux, float rmin, float rdelta, int nstep) {
     float lo = x[0], hi = x[0];
     float sum_w = w[0];
     float sum_x = sum_w * x[0];
@@ -184,7 +184,7 @@ void or_quantize_row_q4K(const float *x, void *vy, int64_t k) {
             for (int l = 0; l < 32; ++l) sum_x2 += xs[l] * xs[l];
             float av_x = sqrtf(sum_x2 / 32);
             for (int l = 0; l < 32; ++l) wts[l] = av_x + fabsf(xs[l]);
-            scales[j] = qkx2_fit(32, 15, xs, wts, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
+            scales[j] = or_qkx2_fit(32, 15, xs, wts, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
             if (scales[j] > max_scale) max_scale = scales[j];
             if (mins[j] > max_min) max_min = mins[j];
         }
@@ -432,12 +432,16 @@ double or_vec_dot_exact(int n, const void *vx, const void *vy) {
 /* Row geometry and vec_dot of a weight type (ggml-cpu/ggml-cpu.c:297-316:
  * both types take Q8_K activations). */
 static size_t block_bytes(int type) {
-    return type == OR_TYPE_Q4_K ? OR_Q4K_BLOCK_BYTES : type == OR_TYPE_Q6_K ? OR_Q6K_BLOCK_BYTES : 0;
+    return type == OR_TYPE_Q4_K ? OR_Q4K_BLOCK_BYTES
+         : type == OR_TYPE_Q5_K ? OR_Q5K_BLOCK_BYTES
+         : type == OR_TYPE_Q6_K ? OR_Q6K_BLOCK_BYTES : 0;
 }
 
 static float type_dot(int type, int order, int n, const void *wr, const void *q8) {
     if (type == OR_TYPE_Q6_K)
         return order ? or_vec_dot_q6K_avx2order(n, wr, q8) : or_vec_dot_q6K_generic(n, wr, q8);
+    if (type == OR_TYPE_Q5_K)
+        return order ? or_vec_dot_q5K_avx2order(n, wr, q8) : or_vec_dot_q5K_generic(n, wr, q8);
     return order ? or_vec_dot_avx2order(n, wr, q8) : or_vec_dot_generic(n, wr, q8);
 }
 
@@ -508,6 +512,7 @@ int or_mul_mat_dequant_f64_type(int type, const void *W, int64_t M, int64_t K, c
     for (int64_t r = 0; r < M; ++r) {
         const uint8_t *src = (const uint8_t *)W + (size_t)r * row_bytes;
         if (type == OR_TYPE_Q6_K) or_dequantize_row_q6K(src, wrow, K);
+        else if (type == OR_TYPE_Q5_K) or_dequantize_row_q5K(src, wrow, K);
         else or_dequantize_row_q4K(src, wrow, K);
         for (int64_t t = 0; t < T; ++t) {
             double acc = 0;

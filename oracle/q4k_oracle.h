@@ -11,7 +11,8 @@
  * compiled with -ffp-contract=off so that each floating-point operation is
  * rounded exactly once, as in ggml-base (which is built without FMA flags).
  *
- * q6k_oracle.c restates the Q6_K functions the same way.
+ * q6k_oracle.c and q5k_oracle.c restate the Q6_K and Q5_K functions the
+ * same way.
  *
  * Parity pins (see tests/): golden fixtures written by tests/golden/gen_golden.py
  * from the reference compiled in oracle/_ref, exhaustive and closed-form checks
@@ -53,8 +54,18 @@ typedef struct {
     uint16_t d;
 } or_block_q6K;
 
+#define OR_Q5K_BLOCK_BYTES 176   /* d, dmin (fp16), scales[12], qh[32], qs[128] */
+typedef struct {
+    uint16_t d;
+    uint16_t dmin;
+    uint8_t  scales[12];
+    uint8_t  qh[32];
+    uint8_t  qs[128];
+} or_block_q5K;
+
 /* weight types, numbered as ggml.h:402-404 numbers them */
 #define OR_TYPE_Q4_K 12
+#define OR_TYPE_Q5_K 13
 #define OR_TYPE_Q6_K 14
 
 /* scalar helpers */
@@ -100,7 +111,21 @@ double or_vec_dot_q6K_exact(int n, const void *vx, const void *vy);
 /* S[b*16 + j] = sum over the 16 weights of sub-block j of block b of (q-32)*q8 */
 void   or_subblock_sums_q6K(int n, const void *vx, const void *vy, int32_t *S);
 
-/* the drivers above for a weight type (OR_TYPE_Q4_K or OR_TYPE_Q6_K);
+/* Q5_K (q5k_oracle.c) */
+void   or_quantize_row_q5K(const float *x, void *y, int64_t k);
+size_t or_quantize_q5K(const float *src, void *dst, int64_t nrow, int64_t n_per_row);
+void   or_dequantize_row_q5K(const void *x, float *y, int64_t k);
+float  or_vec_dot_q5K_generic(int n, const void *vx, const void *vy);
+float  or_vec_dot_q5K_avx2order(int n, const void *vx, const void *vy);
+double or_vec_dot_q5K_exact(int n, const void *vx, const void *vy);
+/* S[b*8 + j] = sum over the 32 weights of sub-block j of block b of q5*q8 */
+void   or_subblock_sums_q5K(int n, const void *vx, const void *vy, int32_t *S);
+
+/* make_qkx2_quants (q4k_oracle.c), shared by the Q4_K and Q5_K encoders */
+float or_qkx2_fit(int n, int nmax, const float *x, const float *w, uint8_t *L,
+                  float *neg_min, uint8_t *Laux, float rmin, float rdelta, int nstep);
+
+/* the drivers above for a weight type (OR_TYPE_Q4_K, _Q5_K or _Q6_K);
  * return -22 for another type or a bad expert id */
 int or_mul_mat_type(int type, const void *W, int64_t M, int64_t K, const float *X, int64_t T,
                     float *Y, int order);

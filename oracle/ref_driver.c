@@ -7,7 +7,7 @@
  *
  * Everything below calls the reference's public API (ggml.h, ggml-cpu.h);
  * no reference arithmetic is re-implemented here.
- *   - type traits (Q4_K, and Q6_K through the *_type forms):
+ *   - type traits (Q4_K, and Q5_K / Q6_K through the *_type forms):
  *     ggml_get_type_traits(Q4_K)->to_float (dequantize_row_q4_K),
  *     ggml_get_type_traits_cpu(Q8_K)->from_float (quantize_row_q8_K),
  *     ggml_get_type_traits_cpu(Q4_K)->vec_dot (ggml_vec_dot_q4_K_q8_K),
@@ -29,6 +29,8 @@
 void ggml_vec_dot_q4_K_q8_K_generic(int n, float *s, size_t bs, const void *vx, size_t bx,
                                     const void *vy, size_t by, int nrc);
 void ggml_vec_dot_q6_K_q8_K_generic(int n, float *s, size_t bs, const void *vx, size_t bx,
+                                    const void *vy, size_t by, int nrc);
+void ggml_vec_dot_q5_K_q8_K_generic(int n, float *s, size_t bs, const void *vx, size_t bx,
                                     const void *vy, size_t by, int nrc);
 
 static int g_inited = 0;
@@ -65,7 +67,7 @@ float ref_vec_dot_generic(int n, const void *vx, const void *vy) {
     return s;
 }
 
-/* the same traits for any weight type (GGML_TYPE_Q4_K = 12, Q6_K = 14) */
+/* the same traits for any weight type (GGML_TYPE_Q4_K = 12, Q5_K = 13, Q6_K = 14) */
 size_t ref_quantize_type(int type, const float *src, void *dst, int64_t nrow, int64_t n_per_row) {
     ensure_init();
     return ggml_quantize_chunk((enum ggml_type)type, src, dst, 0, nrow, n_per_row, NULL);
@@ -80,6 +82,7 @@ float ref_vec_dot_type(int type, int n, const void *vx, const void *vy, int gene
     ensure_init();
     float s = 0;
     if (generic && type == GGML_TYPE_Q6_K) ggml_vec_dot_q6_K_q8_K_generic(n, &s, 0, vx, 0, vy, 0, 1);
+    else if (generic && type == GGML_TYPE_Q5_K) ggml_vec_dot_q5_K_q8_K_generic(n, &s, 0, vx, 0, vy, 0, 1);
     else if (generic) ggml_vec_dot_q4_K_q8_K_generic(n, &s, 0, vx, 0, vy, 0, 1);
     else ggml_get_type_traits_cpu((enum ggml_type)type)->vec_dot(n, &s, 0, vx, 0, vy, 0, 1);
     return s;

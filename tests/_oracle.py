@@ -13,10 +13,11 @@ REF_DIR = os.path.join(REPO, "oracle", "_ref")
 
 QK_K = 256
 Q4K = 144
+Q5K = 176
 Q6K = 210
 Q8K = 292
-TYPE_Q4_K, TYPE_Q6_K = 12, 14            # ggml.h:402-404
-BLOCK_BYTES = {TYPE_Q4_K: Q4K, TYPE_Q6_K: Q6K}
+TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 12, 13, 14            # ggml.h:402-404
+BLOCK_BYTES = {TYPE_Q4_K: Q4K, TYPE_Q5_K: Q5K, TYPE_Q6_K: Q6K}
 
 V, I, I64, F, U64 = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_uint64
 
@@ -62,6 +63,14 @@ class Oracle:
         L.or_vec_dot_q6K_exact.argtypes = [I, V, V]
         L.or_vec_dot_q6K_exact.restype = C.c_double
         L.or_subblock_sums_q6K.argtypes = [I, V, V, V]
+        for n in ("or_quantize_row_q5K", "or_dequantize_row_q5K"):
+            getattr(L, n).argtypes = [V, V, I64]
+        for n in ("or_vec_dot_q5K_generic", "or_vec_dot_q5K_avx2order"):
+            getattr(L, n).argtypes = [I, V, V]
+            getattr(L, n).restype = F
+        L.or_vec_dot_q5K_exact.argtypes = [I, V, V]
+        L.or_vec_dot_q5K_exact.restype = C.c_double
+        L.or_subblock_sums_q5K.argtypes = [I, V, V, V]
         L.or_mul_mat_type.argtypes = [I, V, I64, I64, V, I64, V, I]
         L.or_mul_mat_id_type.argtypes = [I, V, I64, I64, I64, V, I64, V, I64, I64, V, I]
         L.or_mul_mat_dequant_f64_type.argtypes = [I, V, I64, I64, V, I64, V]
@@ -143,11 +152,35 @@ class Oracle:
         self.L.or_subblock_sums_q6K(n, _p(qx), _p(qy), _p(S))
         return S
 
+    # ---- Q5_K (oracle/q5k_oracle.c) ----
+    def quantize_q5K(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(x.size // QK_K * Q5K, np.uint8)
+        self.L.or_quantize_row_q5K(_p(x), _p(y), x.size)
+        return y
+
+    def dequant_q5K(self, q: np.ndarray, k: int) -> np.ndarray:
+        y = np.empty(k, np.float32)
+        self.L.or_dequantize_row_q5K(_p(np.ascontiguousarray(q)), _p(y), k)
+        return y
+
+    def vec_dot_q5K(self, n, qx, qy, order="avx2"):
+        f = self.L.or_vec_dot_q5K_avx2order if order == "avx2" else self.L.or_vec_dot_q5K_generic
+        return f(n, _p(qx), _p(qy))
+
+    def vec_dot_q5K_exact(self, n, qx, qy):
+        return self.L.or_vec_dot_q5K_exact(n, _p(qx), _p(qy))
+
+    def subblock_sums_q5K(self, n, qx, qy) -> np.ndarray:
+        S = np.zeros(n // QK_K * 8, np.int32)
+        self.L.or_subblock_sums_q5K(n, _p(qx), _p(qy), _p(S))
+        return S
+
     def quantize(self, qtype, x):
-        return self.quantize_q6K(x) if qtype == TYPE_Q6_K else self.quantize_q4K(x)
+        return {TYPE_Q4_K: self.quantize_q4K, TYPE_Q5_K: self.quantize_q5K, TYPE_Q6_K: self.quantize_q6K}[qtype](x)
 
     def to_float(self, qtype, q, k):
-        return self.dequant_q6K(q, k) if qtype == TYPE_Q6_K else self.dequant(q, k)
+        return {TYPE_Q4_K: self.dequant, TYPE_Q5_K: self.dequant_q5K, TYPE_Q6_K: self.dequant_q6K}[qtype](q, k)
 
     def mul_mat_type(self, qtype, W, M, K, X, order=1):
         X = np.ascontiguousarray(X, np.float32).reshape(-1, K)

@@ -20,12 +20,13 @@ Contents (all produced by the reference):
   mm_*             GGML_OP_MUL_MAT through ggml_graph_compute (1 thread)
   mmid_*           GGML_OP_MUL_MAT_ID through ggml_graph_compute (1 thread)
 
-q6k_golden.npz holds the same kinds of vectors for GGML_TYPE_Q6_K
-(quantize_q6_K / quantize_row_q6_K_ref, dequantize_row_q6_K,
-ggml_vec_dot_q6_K_q8_K and its _generic form, MUL_MAT, MUL_MAT_ID), plus
-vec_dot cases on random block bytes that reach every scale and 6-bit value.
+q6k_golden.npz and q5k_golden.npz hold the same kinds of vectors for
+GGML_TYPE_Q6_K and GGML_TYPE_Q5_K (quantize_q6_K / quantize_q5_K,
+dequantize_row_q6_K / _q5_K, ggml_vec_dot_q6_K_q8_K / _q5_K_q8_K and their
+_generic forms, MUL_MAT, MUL_MAT_ID), plus vec_dot cases on random block bytes
+that reach every scale and quant value.
 
-Usage: gen_golden.py [q4k] [q6k]   (default: both)
+Usage: gen_golden.py [q4k] [q5k] [q6k]   (default: all)
 """
 import os
 import sys
@@ -34,7 +35,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
-from _oracle import TYPE_Q6_K, Q6K, Ref, ref_library_path  # noqa: E402
+from _oracle import TYPE_Q5_K, TYPE_Q6_K, Q5K, Q6K, Ref, ref_library_path  # noqa: E402
 
 QK = 256
 
@@ -92,55 +93,61 @@ def q6k_encoder_inputs(rng):
     return np.concatenate(rows).astype(np.float32)
 
 
-def gen_q6k(ref, rng):
+def _finite_blocks(rng, n, qtype, bb, tame):
+    """Random block bytes with finite fp16 scales (tame: |d| < 2^-1)."""
+    b = rng.integers(0, 256, size=(n, bb), dtype=np.uint8)
+    mask = 0x3B if tame else 0xBF
+    for hi in ((209,) if qtype == TYPE_Q6_K else (1, 3)):     # high bytes of d (and dmin)
+        b[:, hi] &= mask
+    return b
+
+
+def gen_kquant(ref, rng, qtype, bb):
+    """Golden vectors of one K-quant weight type with Q8_K activations."""
     out = {}
     x = q6k_encoder_inputs(rng)
     out["enc_x"] = x
-    out["enc_q"] = ref.quantize_type(TYPE_Q6_K, x, 1, x.size)
+    out["enc_q"] = ref.quantize_type(qtype, x, 1, x.size)
 
-    rb = rng.integers(0, 256, size=(64, Q6K), dtype=np.uint8)
-    rb[:, 209] &= 0xBF                                                                  # finite fp16 d
-    q = np.concatenate([out["enc_q"].reshape(-1, Q6K), rb]).ravel()
+    q = np.concatenate([out["enc_q"].reshape(-1, bb), _finite_blocks(rng, 64, qtype, bb, False)]).ravel()
     out["deq_q"] = q
-    out["deq_y"] = ref.dequant_type(TYPE_Q6_K, q, q.size // Q6K * QK)
+    out["deq_y"] = ref.dequant_type(qtype, q, q.size // bb * QK)
 
     # vec_dot: encoder output at K in {256, 768, 4096, 27648}, then random
-    # block bytes (every scale -128..127 and 6-bit value) against Q8_K of
-    # N(0,1) and of one-sign inputs
-    vq6, vq8, vK, va, vg = [], [], [], [], []
+    # block bytes (every scale and quant value) against Q8_K of N(0,1) and of
+    # one-sign inputs
+    vw, vq8, vK, va, vg = [], [], [], [], []
     cases = [(K, n, "enc") for K, n in ((256, 8), (768, 8), (4096, 8), (27648, 4))]
     cases += [(K, n, "rand") for K, n in ((256, 8), (4096, 8))]
     for K, n, kind in cases:
         for i in range(n):
             if kind == "enc":
-                w = ref.quantize_type(TYPE_Q6_K, (rng.standard_normal(K) * 0.02).astype(np.float32), 1, K)
+                w = ref.quantize_type(qtype, (rng.standard_normal(K) * 0.02).astype(np.float32), 1, K)
             else:
-                w = rng.integers(0, 256, size=(K // QK, Q6K), dtype=np.uint8)
-                w[:, 209] &= 0x3B                                                       # |d| < 2^-1
-                w = w.ravel()
+                w = _finite_blocks(rng, K // QK, qtype, bb, True).ravel()
             xa = rng.standard_normal(K).astype(np.float32)
             if kind == "rand" and i % 2:
                 xa = np.abs(xa)
             a = ref.quantize_q8K(xa)
-            vq6.append(w); vq8.append(a); vK.append(K)
-            va.append(ref.vec_dot_type(TYPE_Q6_K, K, w, a)); vg.append(ref.vec_dot_type(TYPE_Q6_K, K, w, a, True))
-    out["vd_q6"] = np.concatenate(vq6)
+            vw.append(w); vq8.append(a); vK.append(K)
+            va.append(ref.vec_dot_type(qtype, K, w, a)); vg.append(ref.vec_dot_type(qtype, K, w, a, True))
+    out["vd_w"] = np.concatenate(vw)
     out["vd_q8"] = np.concatenate(vq8)
     out["vd_K"] = np.array(vK, np.int64)
     out["vd_avx2"] = np.array(va, np.float32)
     out["vd_generic"] = np.array(vg, np.float32)
 
     M, K = 64, 512
-    W = ref.quantize_type(TYPE_Q6_K, (rng.standard_normal((M, K)) * 0.02).astype(np.float32), M, K)
+    W = ref.quantize_type(qtype, (rng.standard_normal((M, K)) * 0.02).astype(np.float32), M, K)
     out["mm_W"] = W
     out["mm_MK"] = np.array([M, K], np.int64)
     for T in (1, 3, 8, 17):
         X = rng.standard_normal((T, K)).astype(np.float32)
         out[f"mm_X{T}"] = X
-        out[f"mm_Y{T}"] = ref.mul_mat(W, M, K, X, qtype=TYPE_Q6_K)
+        out[f"mm_Y{T}"] = ref.mul_mat(W, M, K, X, qtype=qtype)
 
     E, M, K, T = 8, 32, 512, 3
-    bank = ref.quantize_type(TYPE_Q6_K, (rng.standard_normal((E * M, K)) * 0.02).astype(np.float32), E * M, K)
+    bank = ref.quantize_type(qtype, (rng.standard_normal((E * M, K)) * 0.02).astype(np.float32), E * M, K)
     out["mmid_bank"] = bank
     out["mmid_EMK"] = np.array([E, M, K], np.int64)
     for n_used, ne11 in ((2, 1), (4, 4)):
@@ -149,18 +156,27 @@ def gen_q6k(ref, rng):
         tag = f"{n_used}_{ne11}"
         out[f"mmid_ids_{tag}"] = ids
         out[f"mmid_X_{tag}"] = X
-        out[f"mmid_Y_{tag}"] = ref.mul_mat_id(bank, M, K, E, X, ids, qtype=TYPE_Q6_K)
+        out[f"mmid_Y_{tag}"] = ref.mul_mat_id(bank, M, K, E, X, ids, qtype=qtype)
+    return out
+
+
+def gen_q6k(ref, rng):
+    out = gen_kquant(ref, rng, TYPE_Q6_K, Q6K)
+    out["vd_q6"] = out.pop("vd_w")
     return out
 
 
 def main():
     if ref_library_path() is None:
         sys.exit("oracle/_ref is not built (make -C oracle ref)")
-    which = set(sys.argv[1:]) or {"q4k", "q6k"}
+    which = set(sys.argv[1:]) or {"q4k", "q5k", "q6k"}
     ref = Ref()
-    if "q6k" in which:
-        out = gen_q6k(ref, np.random.default_rng(0x6B6B))
-        path = os.path.join(HERE, "q6k_golden.npz")
+    for tag, fn in (("q6k", lambda: gen_q6k(ref, np.random.default_rng(0x6B6B))),
+                    ("q5k", lambda: gen_kquant(ref, np.random.default_rng(0x5B5B), TYPE_Q5_K, Q5K))):
+        if tag not in which:
+            continue
+        out = fn()
+        path = os.path.join(HERE, f"{tag}_golden.npz")
         np.savez_compressed(path, **out)
         print(f"wrote {path} ({os.path.getsize(path)/1024:.0f} KiB, {len(out)} arrays) using {ref.path}")
     if "q4k" not in which:
