@@ -6,10 +6,11 @@
  * paths below relative to vendor/ggml/): activations are quantised to Q8_K
  * exactly as quantize_row_q8_K does, integer sub-block sums are exact, and
  * outputs agree with ggml_vec_dot_q4_K_q8_K to fp32 summation order.
- * GGML_TYPE_Q6_K weights (the sibling K-quant that Q4_K models carry for some
- * tensors) take the same Q8_K activations and go through the same entry
- * points once uploaded with their type (spq4k_weights_upload_type); their
- * outputs agree with ggml_vec_dot_q6_K_q8_K the same way.
+ * GGML_TYPE_Q6_K and GGML_TYPE_Q5_K weights (the sibling K-quants that Q4_K
+ * models carry for some tensors) take the same Q8_K activations and go
+ * through the same entry points once uploaded with their type
+ * (spq4k_weights_upload_type); their outputs agree with
+ * ggml_vec_dot_q6_K_q8_K / ggml_vec_dot_q5_K_q8_K the same way.
  *
  * Conventions
  *   - Every function returns 0 on success or a negative errno value:
@@ -44,12 +45,14 @@ extern "C" {
 
 #define SPQ4K_QK_K 256
 #define SPQ4K_Q4K_BLOCK_BYTES 144
+#define SPQ4K_Q5K_BLOCK_BYTES 176
 #define SPQ4K_Q6K_BLOCK_BYTES 210
 #define SPQ4K_Q8K_BLOCK_BYTES 292
 #define SPQ4K_GEMV_MAX_T 8
 
 /* weight types, with ggml's numbers (enum ggml_type, ggml.h:402-404) */
 #define SPQ4K_TYPE_Q4_K 12
+#define SPQ4K_TYPE_Q5_K 13
 #define SPQ4K_TYPE_Q6_K 14
 
 typedef struct spq4k_ctx spq4k_ctx;
@@ -85,12 +88,14 @@ void   spq4k_weights_free(spq4k_weights *w);
 void  *spq4k_weights_data(const spq4k_weights *w);
 size_t spq4k_weights_nbytes(const spq4k_weights *w);
 
-/* The same for a weight of ggml type `type` (SPQ4K_TYPE_Q4_K or
+/* The same for a weight of ggml type `type` (SPQ4K_TYPE_Q4_K, SPQ4K_TYPE_Q5_K:
+ * GGML_TYPE_Q5_K blocks of 176 bytes, ggml-common.h:334-346, or
  * SPQ4K_TYPE_Q6_K: GGML_TYPE_Q6_K blocks of 210 bytes, ggml-common.h:348-357),
  * as ggml_backend_tensor_set uploads a tensor of any type
  * (llama_weights.cpp:483-560). The plain forms above are type Q4_K. Every
- * matmul entry point below takes weights of either type; matrices passed
- * together (the *_multi forms) must share it. */
+ * matmul entry point below takes weights of any of these types (Q5_K
+ * batches run on the sdot4 kernels, Q4_K and Q6_K ones on the matrix
+ * cores); matrices passed together (the *_multi forms) must share it. */
 int spq4k_weights_upload_type(spq4k_ctx *ctx, int type, const void *host, int64_t M, int64_t K, int64_t E,
                               spq4k_weights **out);
 int spq4k_weights_wrap_type(spq4k_ctx *ctx, int type, const void *dev, int64_t M, int64_t K, int64_t E,
@@ -119,16 +124,21 @@ int spq4k_vec_dot(spq4k_ctx *ctx, int n, float *s, const void *vx, const void *v
 /* Type traits of any supported weight type (ggml_get_type_traits(type),
  * ggml.c:768-791; ggml_get_type_traits_cpu(type), ggml-cpu.c:297-322):
  * spq4k_to_float       : to_float           (Q6_K: dequantize_row_q6_K,
- *                        ggml-quants.c:1877-1906; bit-exact fp32)
+ *                        ggml-quants.c:1877-1906; Q5_K: dequantize_row_q5_K,
+ *                        :1669-1694; bit-exact fp32)
  * spq4k_quantize_chunk : ggml_quantize_chunk(type, ..., imatrix = NULL)
  *                        (ggml.h:2764; Q6_K: quantize_q6_K ->
  *                        quantize_row_q6_K_ref, ggml-quants.c:1992-1996,
- *                        :1807-1875; bit-exact bytes)
+ *                        :1807-1875; Q5_K: quantize_q5_K ->
+ *                        quantize_row_q5_K_ref, :1789-1793, :1582-1667;
+ *                        bit-exact bytes)
  * spq4k_vec_dot_q8K    : vec_dot with vec_dot_type Q8_K, nrc = 1 (Q6_K:
- *                        ggml_vec_dot_q6_K_q8_K, arch/x86/quants.c:2288);
- *                        *s is a device float.
+ *                        ggml_vec_dot_q6_K_q8_K, arch/x86/quants.c:2288;
+ *                        Q5_K: ggml_vec_dot_q5_K_q8_K, :2078); *s is a
+ *                        device float.
  * Q6_K block pointers need only 2-byte alignment (ggml rows of an odd number
- * of 210-byte blocks). Type Q4_K gives the Q4_K entry points above. */
+ * of 210-byte blocks), Q5_K ones 16. Type Q4_K gives the Q4_K entry points
+ * above. */
 int spq4k_to_float(spq4k_ctx *ctx, int type, const void *vx, float *y, int64_t k);
 int spq4k_quantize_chunk(spq4k_ctx *ctx, int type, const float *src, void *dst, int64_t nrow, int64_t n_per_row);
 int spq4k_vec_dot_q8K(spq4k_ctx *ctx, int type, int n, float *s, const void *vx, const void *vy);
@@ -182,9 +192,11 @@ int spq4k_moe_host(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids
  * code as the GEMV. No reference function returns them; they are the integer
  * core of ggml_vec_dot_q4_K_q8_K (ggml-cpu/quants.c:645-718). */
 int spq4k_subblock_sums(spq4k_ctx *ctx, const void *W, int64_t M, int64_t K, const float *x, int32_t *S);
-/* The same for a weight type: Q4_K as above; Q6_K gives S[r][b][j], j < 16,
- * the sum over the 16 weights of sub-block j of (q - 32) * q8, the integer
- * core of ggml_vec_dot_q6_K_q8_K (ggml-cpu/quants.c:800-852). */
+/* The same for a weight type: Q4_K as above; Q5_K gives S[r][b][j], j < 8,
+ * the sum of q5 * q8 over sub-block j (ggml-cpu/quants.c:720-798); Q6_K gives
+ * S[r][b][j], j < 16, the sum over the 16 weights of sub-block j of
+ * (q - 32) * q8, the integer core of ggml_vec_dot_q6_K_q8_K
+ * (ggml-cpu/quants.c:800-852). */
 int spq4k_subblock_sums_type(spq4k_ctx *ctx, int type, const void *W, int64_t M, int64_t K, const float *x,
                              int32_t *S);
 

@@ -76,11 +76,17 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 // weight types the kernels take: kernel format and block bytes, -1 / 0 otherwise
 int type_fmt(int type) {
-    return type == SPQ4K_TYPE_Q4_K ? WF_Q4K : type == SPQ4K_TYPE_Q6_K ? WF_Q6K : -1;
+    return type == SPQ4K_TYPE_Q4_K ? WF_Q4K
+         : type == SPQ4K_TYPE_Q5_K ? WF_Q5K
+         : type == SPQ4K_TYPE_Q6_K ? WF_Q6K : -1;
 }
 size_t type_block_bytes(int type) {
-    return type == SPQ4K_TYPE_Q4_K ? SPQ4K_Q4K_BLOCK_BYTES : type == SPQ4K_TYPE_Q6_K ? SPQ4K_Q6K_BLOCK_BYTES : 0;
+    return type == SPQ4K_TYPE_Q4_K ? SPQ4K_Q4K_BLOCK_BYTES
+         : type == SPQ4K_TYPE_Q5_K ? SPQ4K_Q5K_BLOCK_BYTES
+         : type == SPQ4K_TYPE_Q6_K ? SPQ4K_Q6K_BLOCK_BYTES : 0;
 }
+// formats with a matrix-core kernel (the others run batches on the sdot4 kernels)
+bool fmt_has_mfma(int fmt) { return fmt == WF_Q4K || fmt == WF_Q6K; }
 
 int use_device(spq4k_ctx* c) {
     if (!c) return -EINVAL;
@@ -190,8 +196,9 @@ DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb, int64_t rows) {
         d.waves = 8;
         d.depth = 1;
     }
-    // Q6_K at K = 12288 (15 + 21 registers a block): 12 waves, one row in flight
-    if (fmt == WF_Q6K && nb >= 48 && (d.waves == 16 || (d.waves == 12 && d.depth == 2))) {
+    // Q6_K and Q5_K at K = 12288 (15 + 21 and 20 + 19 registers a block):
+    // 12 waves, one row in flight
+    if (fmt != WF_Q4K && nb >= 48 && (d.waves == 16 || (d.waves == 12 && d.depth == 2))) {
         d.waves = 12;
         d.depth = 1;
     }
@@ -253,7 +260,8 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         return 0;
     }
     // SPQ4K_GEMM_MODE=1 keeps Q6_K batches on the sdot4 kernels (gemv_chunked)
-    if (T >= c->gemv_mfma_min_t && c->force_bpr == 0 && !(p.fmt == WF_Q6K && c->gemm_mode == 1)) {
+    if (T >= c->gemv_mfma_min_t && c->force_bpr == 0 && fmt_has_mfma(p.fmt) &&
+        !(p.fmt == WF_Q6K && c->gemm_mode == 1)) {
         // 4 <= T <= 8: the sdot4 kernel's integer work grows with T while the
         // matrix cores' 16-token tile costs the same from T = 1 to 16
         return gemm_segments(c, n, W, x, y, T, c->gemm_mode == 1 ? 1 : 0);
@@ -423,7 +431,8 @@ const char* spq4k_last_error(const spq4k_ctx* c) { return c ? c->err : "null con
 static int weights_new(spq4k_ctx* c, int type, int64_t M, int64_t K, int64_t E, spq4k_weights** out) {
     if (!out) return set_err(c, -EINVAL, "weights: null out");
     *out = nullptr;
-    if (type_fmt(type) < 0) return set_err(c, -EINVAL, "weights: unsupported type %d (Q4_K = 12, Q6_K = 14)", type);
+    if (type_fmt(type) < 0)
+        return set_err(c, -EINVAL, "weights: unsupported type %d (Q4_K = 12, Q5_K = 13, Q6_K = 14)", type);
     int rc = check_shape(c, M, K, E);
     if (rc) return rc;
     spq4k_weights* w = new (std::nothrow) spq4k_weights();
@@ -629,10 +638,12 @@ int spq4k_to_float(spq4k_ctx* c, int type, const void* vx, float* y, int64_t k) 
     if (type == SPQ4K_TYPE_Q4_K) return spq4k_dequant(c, vx, y, k);
     int rc = use_device(c);
     if (rc) return rc;
-    if (type != SPQ4K_TYPE_Q6_K) return set_err(c, -EINVAL, "to_float: unsupported type %d", type);
-    if (!vx || !y || k < 0 || k % SPQ4K_QK_K || !aligned(vx, 2) || !aligned(y, 16))
+    if (type != SPQ4K_TYPE_Q6_K && type != SPQ4K_TYPE_Q5_K)
+        return set_err(c, -EINVAL, "to_float: unsupported type %d", type);
+    if (!vx || !y || k < 0 || k % SPQ4K_QK_K || !aligned(vx, type == SPQ4K_TYPE_Q5_K ? 16 : 2) || !aligned(y, 16))
         return set_err(c, -EINVAL, "to_float: bad arguments");
-    hipError_t e = launch_dequant_q6k((const uint8_t*)vx, y, k / SPQ4K_QK_K, c->stream);
+    hipError_t e = type == SPQ4K_TYPE_Q5_K ? launch_dequant_q5k((const uint8_t*)vx, y, k / SPQ4K_QK_K, c->stream)
+                                           : launch_dequant_q6k((const uint8_t*)vx, y, k / SPQ4K_QK_K, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "dequant_q6k launch");
     return 0;
 }
@@ -641,11 +652,14 @@ int spq4k_quantize_chunk(spq4k_ctx* c, int type, const float* src, void* dst, in
     if (type == SPQ4K_TYPE_Q4_K) return spq4k_quantize_q4K(c, src, dst, nrow, n_per_row);
     int rc = use_device(c);
     if (rc) return rc;
-    if (type != SPQ4K_TYPE_Q6_K) return set_err(c, -EINVAL, "quantize_chunk: unsupported type %d", type);
+    if (type != SPQ4K_TYPE_Q6_K && type != SPQ4K_TYPE_Q5_K)
+        return set_err(c, -EINVAL, "quantize_chunk: unsupported type %d", type);
     if (!src || !dst || nrow < 0 || n_per_row <= 0 || n_per_row % SPQ4K_QK_K || !aligned(src, 16) ||
-        !aligned(dst, 2))
+        !aligned(dst, type == SPQ4K_TYPE_Q5_K ? 16 : 2))
         return set_err(c, -EINVAL, "quantize_chunk: bad arguments");
-    hipError_t e = launch_quantize_q6k(src, (uint8_t*)dst, nrow * (n_per_row / SPQ4K_QK_K), c->stream);
+    const int64_t nblk = nrow * (n_per_row / SPQ4K_QK_K);
+    hipError_t e = type == SPQ4K_TYPE_Q5_K ? launch_quantize_q5k(src, (uint8_t*)dst, nblk, c->stream)
+                                           : launch_quantize_q6k(src, (uint8_t*)dst, nblk, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "quantize_q6k launch");
     return 0;
 }
@@ -654,10 +668,14 @@ int spq4k_vec_dot_q8K(spq4k_ctx* c, int type, int n, float* s, const void* vx, c
     if (type == SPQ4K_TYPE_Q4_K) return spq4k_vec_dot(c, n, s, vx, vy);
     int rc = use_device(c);
     if (rc) return rc;
-    if (type != SPQ4K_TYPE_Q6_K) return set_err(c, -EINVAL, "vec_dot_q8K: unsupported type %d", type);
-    if (!s || !vx || !vy || n <= 0 || n % SPQ4K_QK_K || !aligned(vx, 2) || !aligned(vy, 4))
+    if (type != SPQ4K_TYPE_Q6_K && type != SPQ4K_TYPE_Q5_K)
+        return set_err(c, -EINVAL, "vec_dot_q8K: unsupported type %d", type);
+    if (!s || !vx || !vy || n <= 0 || n % SPQ4K_QK_K || !aligned(vx, type == SPQ4K_TYPE_Q5_K ? 16 : 2) ||
+        !aligned(vy, 4))
         return set_err(c, -EINVAL, "vec_dot_q8K: bad arguments");
-    hipError_t e = launch_vec_dot_q6k((const uint8_t*)vx, (const uint8_t*)vy, n / SPQ4K_QK_K, s, c->stream);
+    hipError_t e = type == SPQ4K_TYPE_Q5_K
+                       ? launch_vec_dot_q5k((const uint8_t*)vx, (const uint8_t*)vy, n / SPQ4K_QK_K, s, c->stream)
+                       : launch_vec_dot_q6k((const uint8_t*)vx, (const uint8_t*)vy, n / SPQ4K_QK_K, s, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "vec_dot_q6k launch");
     return 0;
 }
@@ -765,7 +783,7 @@ int gemm_segments(spq4k_ctx* c, int n, const spq4k_weights* const* W, const floa
     p.fmt = W[0]->fmt;
     if (tiles16 * ((T + 15) / 16) > (1ll << 31) - 1 || rows > (1ll << 31) - 1)
         return set_err(c, -EINVAL, "gemm: grid too large");
-    if (p.fmt == WF_Q6K && mode == 1) {   // sdot4 kernels over 8-token slices
+    if (!fmt_has_mfma(p.fmt) || (p.fmt == WF_Q6K && mode == 1)) {   // sdot4 kernels over 8-token slices
         if (T <= SPQ4K_GEMV_MAX_T) return gemv_launch(c, n, W, X, Y, T);
         return gemv_chunked(c, n, W, X, Y, T);
     }
@@ -928,7 +946,7 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     // a Q6_K bank's operand preparation costs more, so its experts go to the
     // matrix cores only once they receive two pairs on average (measured on
     // the 2048 x 768 down bank: T = 8 sdot4 31 us against 36, T = 32 65 against 61)
-    const bool ring = !c->moe_unfused && (bank->fmt == WF_Q4K || mean_pairs >= 2);
+    const bool ring = !c->moe_unfused && fmt_has_mfma(bank->fmt) && (bank->fmt == WF_Q4K || mean_pairs >= 2);
     hipError_t e;
     if (!ring) {
         e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, mn, false, c->stream);
@@ -1029,11 +1047,15 @@ int spq4k_subblock_sums_type(spq4k_ctx* c, int type, const void* W, int64_t M, i
     if (type == SPQ4K_TYPE_Q4_K) return spq4k_subblock_sums(c, W, M, K, x, S);
     int rc = use_device(c);
     if (rc) return rc;
-    if (type != SPQ4K_TYPE_Q6_K) return set_err(c, -EINVAL, "subblock_sums: unsupported type %d", type);
+    if (type != SPQ4K_TYPE_Q6_K && type != SPQ4K_TYPE_Q5_K)
+        return set_err(c, -EINVAL, "subblock_sums: unsupported type %d", type);
     rc = check_shape(c, M, K, 1);
     if (rc) return rc;
-    if (!W || !x || !S || !aligned(W, 2) || !aligned(x, 16)) return set_err(c, -EINVAL, "subblock_sums: bad pointers");
-    hipError_t e = launch_subblock_sums_q6k((const uint8_t*)W, (int)M, (int)(K / SPQ4K_QK_K), x, S, c->stream);
+    if (!W || !x || !S || !aligned(W, type == SPQ4K_TYPE_Q5_K ? 16 : 2) || !aligned(x, 16))
+        return set_err(c, -EINVAL, "subblock_sums: bad pointers");
+    hipError_t e = type == SPQ4K_TYPE_Q5_K
+                       ? launch_subblock_sums_q5k((const uint8_t*)W, (int)M, (int)(K / SPQ4K_QK_K), x, S, c->stream)
+                       : launch_subblock_sums_q6k((const uint8_t*)W, (int)M, (int)(K / SPQ4K_QK_K), x, S, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "subblock_sums_q6k launch");
     return 0;
 }

@@ -1,9 +1,12 @@
-// k_convert.hip — format conversions of the Q4_K path on gfx950:
+// k_convert.hip — format conversions of the Q4_K and Q5_K paths on gfx950:
 //   fp32 -> Q8_K     (quantize_row_q8_K_ref, ggml-quants.c:2692-2729)
 //   Q4_K -> fp32     (dequantize_row_q4_K, ggml-quants.c:1467-1489)
 //   fp32 -> Q4_K     (quantize_row_q4_K_ref + make_qkx2_quants,
 //                     ggml-quants.c:1395-1465, :737-816)
 //   Q4_K . Q8_K      (ggml_vec_dot_q4_K_q8_K shape, one row)
+//   Q5_K -> fp32, fp32 -> Q5_K, Q5_K . Q8_K and its integer sub-block sums
+//                    (dequantize_row_q5_K, quantize_row_q5_K_ref,
+//                     ggml-quants.c:1669-1694, :1582-1667)
 //   synthetic data   (synth_math.h)
 // Every kernel reproduces the reference's rounding step for step (compiled
 // with -ffp-contract=off, IEEE division and square root), so the outputs are
@@ -11,6 +14,7 @@
 #include "q4k_device.h"
 #include "gemv_core.h"
 #include "launch.h"
+#include "q5k_core.h"
 #include "synth_math.h"
 
 namespace spq4k {
@@ -93,11 +97,13 @@ __global__ __launch_bounds__(256) void dequant_q4k_kernel(const uint8_t* __restr
 // 0 packs the header and the even lanes pack the nibbles.
 __device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
-// make_qkx2_quants(32, 15, x, w, L, &the_min, Laux, -1, 0.1, 20, false)
-// (ggml-quants.c:737-816), same operation order.
-__device__ float qkx2_fit32(const float (&x)[32], const float (&w)[32], int (&L)[32], float& neg_min) {
-    constexpr int n = 32, nmax = 15, nstep = 20;
-    const float rmin = -1.0f, rdelta = 0.1f;
+// make_qkx2_quants(32, NMAX, x, w, L, &the_min, Laux, rmin, 0.1, NSTEP, false)
+// (ggml-quants.c:737-816), same operation order: Q4_K calls it with
+// (15, -1, 20), Q5_K with (31, -0.5, 15).
+template <int NMAX, int NSTEP>
+__device__ float qkx2_fit32(const float (&x)[32], const float (&w)[32], int (&L)[32], float& neg_min, float rmin) {
+    constexpr int n = 32, nmax = NMAX, nstep = NSTEP;
+    const float rdelta = 0.1f;
     float lo = x[0], hi = x[0];
     float sum_w = w[0];
     float sum_x = sum_w * x[0];
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(256) void quantize_q4k_kernel(const float* __restri
     for (int l = 0; l < 32; ++l) w[l] = av_x + fabsf(x[l]);
     int L[32];
     float neg_min;
-    const float scale = qkx2_fit32(x, w, L, neg_min);
+    const float scale = qkx2_fit32<15, 20>(x, w, L, neg_min, -1.0f);
 
     const float max_scale = max8_pos(scale);
     const float max_min = max8_pos(neg_min);
@@ -277,6 +283,210 @@ __global__ __launch_bounds__(256) void quantize_q4k_kernel(const float* __restri
         hd.z = sb[4] | (sb[5] << 8) | (sb[6] << 16) | (sb[7] << 24);
         hd.w = sb[8] | (sb[9] << 8) | (sb[10] << 16) | (sb[11] << 24);
         *reinterpret_cast<uint4*>(o) = hd;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 -> Q5_K (quantize_row_q5_K_ref, ggml-quants.c:1582-1667): the Q4_K
+// encoder's lanes with 5-bit values; eight lanes per block, lane j fits
+// sub-block j; the even lanes pack the low nibbles, and the eight lanes OR
+// their high bits (bit j of qh[l]) together.
+__global__ __launch_bounds__(256) void quantize_q5k_kernel(const float* __restrict__ xin, uint8_t* __restrict__ y,
+                                                           int64_t nblocks) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t blk = gid >> 3;
+    const int j = (int)(gid & 7);
+    const bool valid = blk < nblocks;   // uniform over each 8-lane group
+
+    float x[32];
+    if (valid) {
+        const float4* src = reinterpret_cast<const float4*>(xin + blk * QK + 32 * j);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 a = src[i];
+            x[4 * i] = a.x; x[4 * i + 1] = a.y; x[4 * i + 2] = a.z; x[4 * i + 3] = a.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = 0.0f;
+    }
+    float sum_x2 = 0;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
+    const float av_x = __builtin_sqrtf(sum_x2 / 32);
+    float w[32];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) w[l] = av_x + fabsf(x[l]);
+    int L[32];
+    float neg_min;
+    const float scale = qkx2_fit32<31, 15>(x, w, L, neg_min, -0.5f);
+
+    const float max_scale = max8_pos(scale);
+    const float max_min = max8_pos(neg_min);
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    int ls = nearest_int_ref(inv_scale * scale) & 0xFF;
+    int lm = nearest_int_ref(inv_min * neg_min) & 0xFF;
+    ls = ls < 63 ? ls : 63;
+    lm = lm < 63 ? lm : 63;
+    const uint16_t d16 = f32_to_f16_bits(max_scale / 63.f);
+    const uint16_t m16 = f32_to_f16_bits(max_min / 63.f);
+    const float d = half_bits_to_float(d16) * (float)ls;
+    if (d != 0.0f) {
+        const float dm = half_bits_to_float(m16) * (float)lm;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) L[i] = clampi(nearest_int_ref((x[i] + dm) / d), 0, 31);
+    }
+    const int mine = ls | (lm << 8);
+    int all[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) all[k] = __shfl(mine, k, 8);
+
+    uint32_t own[8], nbr[8], hb[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        own[k] = (uint32_t)L[4 * k] | ((uint32_t)L[4 * k + 1] << 8) | ((uint32_t)L[4 * k + 2] << 16) |
+                 ((uint32_t)L[4 * k + 3] << 24);
+        hb[k] = ((own[k] >> 4) & 0x01010101u) << j;   // this lane's bit j of qh[4k .. 4k+3]
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) nbr[k] = (uint32_t)__shfl_xor((int)own[k], 1, 8);
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) hb[k] |= (uint32_t)__shfl_xor((int)hb[k], off, 8);
+
+    if (!valid) return;
+    uint8_t* o = y + blk * Q5K_BYTES;
+    if ((j & 1) == 0) {
+        uint32_t packed[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) packed[k] = (own[k] & 0x0F0F0F0Fu) | ((nbr[k] & 0x0F0F0F0Fu) << 4);
+        uint4* q = reinterpret_cast<uint4*>(o + 48 + 16 * j);   // qs[32 * (j/2)]
+        q[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        q[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    }
+    if (j == 1) {
+        uint4* h = reinterpret_cast<uint4*>(o + 16);
+        h[0] = make_uint4(hb[0], hb[1], hb[2], hb[3]);
+        h[1] = make_uint4(hb[4], hb[5], hb[6], hb[7]);
+    }
+    if (j == 0) {
+        uint32_t sb[12];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int lsi = all[i] & 0xFF, lmi = all[i] >> 8;
+            const int ls4 = all[i + 4] & 0xFF, lm4 = all[i + 4] >> 8;
+            sb[i] = (uint32_t)(lsi | ((ls4 >> 4) << 6));
+            sb[4 + i] = (uint32_t)(lmi | ((lm4 >> 4) << 6));
+            sb[8 + i] = (uint32_t)((ls4 & 0xF) | ((lm4 & 0xF) << 4));
+        }
+        uint4 hd;
+        hd.x = (uint32_t)d16 | ((uint32_t)m16 << 16);
+        hd.y = sb[0] | (sb[1] << 8) | (sb[2] << 16) | (sb[3] << 24);
+        hd.z = sb[4] | (sb[5] << 8) | (sb[6] << 16) | (sb[7] << 24);
+        hd.w = sb[8] | (sb[9] << 8) | (sb[10] << 16) | (sb[11] << 24);
+        *reinterpret_cast<uint4*>(o) = hd;
+    }
+}
+
+// Q5_K -> fp32: thread i of a block's 32 handles qs bytes 4i .. 4i+3 of group
+// g = i / 8 (four low-nibble and four high-nibble outputs) with their qh bits;
+// y = (d * sc) * q - (dmin * m), each step rounded once.
+__global__ __launch_bounds__(256) void dequant_q5k_kernel(const uint8_t* __restrict__ x, float* __restrict__ y,
+                                                          int64_t nblocks) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t blk = gid >> 5;
+    if (blk >= nblocks) return;
+    const int i = (int)(gid & 31);
+    const int g = i >> 3;
+    const int l = 4 * (i & 7);
+    const uint8_t* b = x + blk * Q5K_BYTES;
+    const uint4 h = *reinterpret_cast<const uint4*>(b);
+    const float d = half_bits_to_float(h.x & 0xFFFFu);
+    const float dmin = half_bits_to_float(h.x >> 16);
+    const ScaleMin sm = unpack_scale_min(h.y, h.z, h.w);
+    const uint32_t scw = g < 2 ? sm.sc_lo : sm.sc_hi;
+    const uint32_t mw = g < 2 ? sm.m_lo : sm.m_hi;
+    const int sh = 16 * (g & 1);
+    const float d1 = d * (float)((scw >> sh) & 0xFFu);
+    const float m1 = dmin * (float)((mw >> sh) & 0xFFu);
+    const float d2 = d * (float)((scw >> (sh + 8)) & 0xFFu);
+    const float m2 = dmin * (float)((mw >> (sh + 8)) & 0xFFu);
+    const uint32_t q = *reinterpret_cast<const uint32_t*>(b + 48 + 32 * g + l);
+    const uint32_t hq = *reinterpret_cast<const uint32_t*>(b + 16 + l);
+    float lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t byte = (q >> (8 * k)) & 0xFFu, hbyte = (hq >> (8 * k)) & 0xFFu;
+        lo[k] = d1 * (float)((byte & 0x0Fu) + (((hbyte >> (2 * g)) & 1u) << 4)) - m1;
+        hi[k] = d2 * (float)((byte >> 4) + (((hbyte >> (2 * g + 1)) & 1u) << 4)) - m2;
+    }
+    float* o = y + blk * QK + 64 * g + l;
+    *reinterpret_cast<float4*>(o) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+    *reinterpret_cast<float4*>(o + 32) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+}
+
+// One Q5_K row . one Q8_K row (global 292 B blocks), one wave.
+__global__ __launch_bounds__(64) void vec_dot_q5k_kernel(const uint8_t* __restrict__ wx,
+                                                         const uint8_t* __restrict__ q8, int nb,
+                                                         float* __restrict__ out) {
+    const int lane = threadIdx.x;
+    const int l4 = lane & 3;
+    float acc = 0.0f;
+    for (int b = lane >> 2; b < nb; b += 16) {
+        const W5 w = load_w5(wx + (size_t)b * Q5K_BYTES, l4);
+        const uint8_t* yb = q8 + (size_t)b * Q8K_BYTES;
+        const int* qs = reinterpret_cast<const int*>(yb + 4 + 64 * l4);   // 4-byte aligned
+        Q8Reg r;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r.a[i] = qs[i];
+        const int16_t* bs = reinterpret_cast<const int16_t*>(yb + 260) + 4 * l4;
+        r.bsA = (int)bs[0] + bs[1];
+        r.bsB = (int)bs[2] + bs[3];
+        r.d8 = *reinterpret_cast<const float*>(yb);
+        acc = block_dot5_reg(w, l4, r, acc);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) *out = acc;
+}
+
+// Diagnostic: exact integer sub-block sums S[row][b][j] of Q5_K rows against
+// Q8_K(x), formed by the GEMV's lane code (split_q5 + dot4).
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void subblock_sums_q5k_kernel(const uint8_t* __restrict__ W, int M, int nb,
+                                                                       const float* __restrict__ X,
+                                                                       int32_t* __restrict__ S, int CB) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int ROWS = WAVES * 16;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int l4 = lane & 3;
+    const int row = blockIdx.x * ROWS + wave * 16 + (lane >> 2);
+    const bool row_ok = row < M;
+    const Q8Lds L = q8lds_carve(smem, CB);
+    for (int c0 = 0; c0 < nb; c0 += CB) {
+        const int nblk = min(nb, c0 + CB) - c0;
+        __syncthreads();
+        stage_q8_from_f32<WAVES>(X, 0, 1, c0, nblk, L, CB);
+        __syncthreads();
+        if (!row_ok) continue;
+        for (int bb = 0; bb < nblk; ++bb) {
+            const W5 w = load_w5(W + ((size_t)row * nb + c0 + bb) * Q5K_BYTES, l4);
+            Q8Reg q;
+            load_q8reg(L, bb, l4, q);
+            const Nib n = split_q5(w, l4);
+            int S0 = 0, S1 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                S0 = dot4(n.lo[i], q.a[i], S0);
+                S1 = dot4(n.hi[i], q.a[8 + i], S1);
+            }
+            int32_t* o = S + ((size_t)row * nb + c0 + bb) * 8 + 2 * l4;
+            o[0] = S0;
+            o[1] = S1;
+        }
     }
 }
 
@@ -348,6 +558,34 @@ hipError_t launch_quantize_q4k(const float* x, uint8_t* y, int64_t nblocks, hipS
     if (nblocks <= 0) return hipSuccess;
     const int64_t grid = (nblocks * 8 + 255) / 256;
     hipLaunchKernelGGL(quantize_q4k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, y, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q5k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st) {
+    if (nblocks <= 0) return hipSuccess;
+    const int64_t grid = (nblocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(quantize_q5k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, y, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_q5k(const uint8_t* x, float* y, int64_t nblocks, hipStream_t st) {
+    if (nblocks <= 0) return hipSuccess;
+    const int64_t grid = (nblocks * 32 + 255) / 256;
+    hipLaunchKernelGGL(dequant_q5k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, y, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_vec_dot_q5k(const uint8_t* wx, const uint8_t* q8, int nb, float* out, hipStream_t st) {
+    hipLaunchKernelGGL(vec_dot_q5k_kernel, dim3(1), dim3(64), 0, st, wx, q8, nb, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_subblock_sums_q5k(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st) {
+    constexpr int WAVES = 4;
+    const int CB = nb < 64 ? nb : 64;
+    const size_t lds = (size_t)q8lds_bytes(CB);
+    const int grid = (M + WAVES * 16 - 1) / (WAVES * 16);
+    hipLaunchKernelGGL((subblock_sums_q5k_kernel<WAVES>), dim3(grid), dim3(WAVES * 64), lds, st, W, M, nb, X, S, CB);
     return hipGetLastError();
 }
 

@@ -22,11 +22,13 @@
 // BPR trades rows per workgroup against redundant activation quantisation:
 // the host picks it so that small matrices still launch >= 2 workgroups
 // per CU and large ones quantise x as few times as possible.
-// The kernels are templates over the weight format (FmtQ4K, FmtQ6K): the same
-// lane mapping serves Q6_K blocks (q6k_core.h), whose CPU counterpart is
-// ggml_vec_dot_q6_K_q8_K (ggml-cpu/arch/x86/quants.c:2288).
+// The kernels are templates over the weight format (FmtQ4K, FmtQ5K, FmtQ6K):
+// the same lane mapping serves Q5_K and Q6_K blocks (q5k_core.h, q6k_core.h),
+// whose CPU counterparts are ggml_vec_dot_q5_K_q8_K and _q6_K_q8_K
+// (ggml-cpu/arch/x86/quants.c:2078, :2288).
 #include "gemv_core.h"
 #include "launch.h"
+#include "q5k_core.h"
 #include "q6k_core.h"
 
 namespace spq4k {
@@ -285,11 +287,12 @@ static hipError_t launch_dec(const GemvParams& p, int grid, hipStream_t st) {
 constexpr bool dec_shape_ok(int nb, int waves, int depth) {
     return !(nb >= 48 && waves == 16 && depth == 2) && !(nb > 48 && (waves > 8 || depth > 1));
 }
-// Q6_K holds 15 + 21 registers a block (Q4_K 12 + 19): at K = 12288 a 16-wave
-// workgroup (128 registers) or two rows in flight at 12 waves would spill
+// Q6_K holds 15 + 21 registers a block, Q5_K 20 + 19 (Q4_K 12 + 19): at
+// K = 12288 a 16-wave workgroup (128 registers) or two rows in flight at 12
+// waves would spill
 template <typename Fmt>
 constexpr bool dec_shape_ok_fmt(int nb, int waves, int depth) {
-    if (Fmt::BYTES == Q6K_BYTES && nb >= 48 && (waves == 16 || (waves == 12 && depth == 2))) return false;
+    if (Fmt::BYTES != Q4K_BYTES && nb >= 48 && (waves == 16 || (waves == 12 && depth == 2))) return false;
     return dec_shape_ok(nb, waves, depth);
 }
 
@@ -310,7 +313,7 @@ static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStre
 // block a lane): K = 4096 and 12288; at K = 27648 its seven blocks a lane
 // would not fit the register file, and the generic kernel runs.
 bool decode_supported(int fmt, int nb) {
-    if (fmt == WF_Q6K) return nb == 16 || nb == 48;
+    if (fmt == WF_Q6K || fmt == WF_Q5K) return nb == 16 || nb == 48;
     return nb == 16 || nb == 20 || nb == 48 || nb == 108;
 }
 
@@ -318,6 +321,11 @@ hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream
     if (p.fmt == WF_Q6K) {
         if (p.nb == 16) return launch_dec_nb<FmtQ6K, 16>(p, c, st);
         if (p.nb == 48) return launch_dec_nb<FmtQ6K, 48>(p, c, st);
+        return hipErrorInvalidValue;
+    }
+    if (p.fmt == WF_Q5K) {
+        if (p.nb == 16) return launch_dec_nb<FmtQ5K, 16>(p, c, st);
+        if (p.nb == 48) return launch_dec_nb<FmtQ5K, 48>(p, c, st);
         return hipErrorInvalidValue;
     }
     if (p.nb == 16) return launch_dec_nb<FmtQ4K, 16>(p, c, st);
@@ -340,8 +348,9 @@ static hipError_t launch_gemv_fmt(const GemvParams& p, int T, int bpr, int ntile
 }
 
 hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st) {
-    return p.fmt == WF_Q6K ? launch_gemv_fmt<FmtQ6K>(p, T, bpr, ntiles, st)
-                           : launch_gemv_fmt<FmtQ4K>(p, T, bpr, ntiles, st);
+    if (p.fmt == WF_Q6K) return launch_gemv_fmt<FmtQ6K>(p, T, bpr, ntiles, st);
+    if (p.fmt == WF_Q5K) return launch_gemv_fmt<FmtQ5K>(p, T, bpr, ntiles, st);
+    return launch_gemv_fmt<FmtQ4K>(p, T, bpr, ntiles, st);
 }
 
 hipError_t launch_subblock_sums(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st) {

@@ -19,9 +19,11 @@
 // Calls with at most MOE_FUSED_MAX_PAIRS pairs use moe_fused_kernel instead,
 // which does all three steps in one launch. The sdot4 kernels (moe_gemv,
 // moe_fused, moe_decode) are templates over the weight format and also run
-// Q6_K expert banks (FmtQ6K, q6k_core.h); so is the matrix-core ring (F = 1).
+// Q6_K and Q5_K expert banks (FmtQ6K, FmtQ5K); the matrix-core ring runs
+// Q4_K and Q6_K (F = 1).
 #include "gemv_core.h"
 #include "launch.h"
+#include "q5k_core.h"
 #include "q6k_core.h"
 #include "ring_core.h"
 
@@ -406,7 +408,9 @@ static hipError_t launch_moe_decode_fmt(const MoeFusedParams& p, int grid, hipSt
 }
 
 hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st) {
-    return p.fmt == WF_Q6K ? launch_moe_decode_fmt<FmtQ6K>(p, grid, st) : launch_moe_decode_fmt<FmtQ4K>(p, grid, st);
+    if (p.fmt == WF_Q6K) return launch_moe_decode_fmt<FmtQ6K>(p, grid, st);
+    if (p.fmt == WF_Q5K) return launch_moe_decode_fmt<FmtQ5K>(p, grid, st);
+    return launch_moe_decode_fmt<FmtQ4K>(p, grid, st);
 }
 
 template <typename Fmt, int TC, int BPR>
@@ -440,8 +444,9 @@ static hipError_t launch_moe_fused_fmt(const MoeFusedParams& p, int tc, int bpr,
 }
 
 hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st) {
-    return p.fmt == WF_Q6K ? launch_moe_fused_fmt<FmtQ6K>(p, tc, bpr, grid, st)
-                           : launch_moe_fused_fmt<FmtQ4K>(p, tc, bpr, grid, st);
+    if (p.fmt == WF_Q6K) return launch_moe_fused_fmt<FmtQ6K>(p, tc, bpr, grid, st);
+    if (p.fmt == WF_Q5K) return launch_moe_fused_fmt<FmtQ5K>(p, tc, bpr, grid, st);
+    return launch_moe_fused_fmt<FmtQ4K>(p, tc, bpr, grid, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -481,8 +486,9 @@ static hipError_t launch_moe_gemv_fmt(const MoeParams& p, int tc, int bpr, int g
 }
 
 hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st) {
-    return p.fmt == WF_Q6K ? launch_moe_gemv_fmt<FmtQ6K>(p, tc, bpr, grid, st)
-                           : launch_moe_gemv_fmt<FmtQ4K>(p, tc, bpr, grid, st);
+    if (p.fmt == WF_Q6K) return launch_moe_gemv_fmt<FmtQ6K>(p, tc, bpr, grid, st);
+    if (p.fmt == WF_Q5K) return launch_moe_gemv_fmt<FmtQ5K>(p, tc, bpr, grid, st);
+    return launch_moe_gemv_fmt<FmtQ4K>(p, tc, bpr, grid, st);
 }
 
 
@@ -620,6 +626,7 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
 
 hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, int E, const float* X,
                            int64_t x_tstride, int n_xrows, int max_act, hipStream_t st) {
+    if (p.fmt == WF_Q5K) return hipErrorInvalidValue;   // no matrix-core form
     const int64_t items = (int64_t)n_xrows * p.nb;
     hipLaunchKernelGGL(moe_prep_kernel, dim3((unsigned)(1 + (items + 15) / 16)), dim3(256), moe_route_lds_bytes(E), st,
                        ids, n_pairs, E, p.route, X, x_tstride, n_xrows, p.nb, p.Q);

@@ -15,6 +15,7 @@ constexpr int GEMV_MAX_SEG = 4;
 enum WFmt : int32_t {
     WF_Q4K = 0,   // GGML_TYPE_Q4_K, 144-byte blocks
     WF_Q6K = 1,   // GGML_TYPE_Q6_K, 210-byte blocks
+    WF_Q5K = 2,   // GGML_TYPE_Q5_K, 176-byte blocks (sdot4 kernels only)
 };
 
 struct GemvSeg {
@@ -166,5 +167,12 @@ hipError_t launch_dequant_q6k(const uint8_t* x, float* y, int64_t nblocks, hipSt
 hipError_t launch_quantize_q6k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
 hipError_t launch_vec_dot_q6k(const uint8_t* wx, const uint8_t* q8, int nb, float* out, hipStream_t st);
 hipError_t launch_subblock_sums_q6k(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
+
+// Q5_K conversions (k_convert.hip); the Q5_K matvecs are the FmtQ5K instances
+// of launch_gemv / launch_gemv_decode / launch_moe_decode / _fused / _gemv
+hipError_t launch_quantize_q5k(const float* x, uint8_t* y, int64_t nblocks, hipStream_t st);
+hipError_t launch_dequant_q5k(const uint8_t* x, float* y, int64_t nblocks, hipStream_t st);
+hipError_t launch_vec_dot_q5k(const uint8_t* wx, const uint8_t* q8, int nb, float* out, hipStream_t st);
+hipError_t launch_subblock_sums_q5k(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
 
 }  // namespace spq4k

@@ -183,8 +183,8 @@ static void run_mul_mat_id(struct ggml_tensor *dst, int ith, int nth, void *user
     if (rc) fail(b, dst, rc, "spq4k_ggml_mul_mat_id");
 }
 
-/* weight types the library runs (spq4k.h: SPQ4K_TYPE_Q4_K, SPQ4K_TYPE_Q6_K) */
-static int supported(enum ggml_type t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q6_K; }
+/* weight types the library runs (spq4k.h: SPQ4K_TYPE_Q4_K, _Q5_K, _Q6_K) */
+static int supported(enum ggml_type t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K; }
 
 struct ggml_tensor *spq4k_ggml_mul_mat(struct ggml_context *ctx, struct ggml_tensor *W, struct ggml_tensor *x,
                                        spq4k_ggml *b) {

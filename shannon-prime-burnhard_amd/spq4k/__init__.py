@@ -11,7 +11,8 @@ nihilistau/shannon-prime-burnhard):
     mul_mat         GGML_OP_MUL_MAT                   (ggml.h:1414-1420)
     mul_mat_id      GGML_OP_MUL_MAT_ID                (ggml.h:1434-1438)
 
-`type` is ggml's type id: TYPE_Q4_K (12, the default) or TYPE_Q6_K (14).
+`type` is ggml's type id: TYPE_Q4_K (12, the default), TYPE_Q5_K (13) or
+TYPE_Q6_K (14).
 
 Every call runs on the GPU through libspq4k.so; if the library is missing
 or the device is absent the call raises. There is no CPU fallback.
@@ -28,11 +29,13 @@ import numpy as np
 
 QK_K = 256
 Q4K_BLOCK_BYTES = 144
+Q5K_BLOCK_BYTES = 176
 Q6K_BLOCK_BYTES = 210
 Q8K_BLOCK_BYTES = 292
 TYPE_Q4_K = 12
+TYPE_Q5_K = 13
 TYPE_Q6_K = 14
-BLOCK_BYTES = {TYPE_Q4_K: Q4K_BLOCK_BYTES, TYPE_Q6_K: Q6K_BLOCK_BYTES}
+BLOCK_BYTES = {TYPE_Q4_K: Q4K_BLOCK_BYTES, TYPE_Q5_K: Q5K_BLOCK_BYTES, TYPE_Q6_K: Q6K_BLOCK_BYTES}
 GEMV_MAX_T = 8
 DIST_NORMAL = 0
 DIST_STUDENT_T4 = 1
@@ -311,5 +314,6 @@ class Context:
 
 
 __all__ = ["Context", "Weights", "Spq4kError", "load_library", "LIB_PATH", "QK_K", "Q4K_BLOCK_BYTES",
-           "Q6K_BLOCK_BYTES", "Q8K_BLOCK_BYTES", "TYPE_Q4_K", "TYPE_Q6_K", "BLOCK_BYTES", "GEMV_MAX_T",
+           "Q5K_BLOCK_BYTES", "Q6K_BLOCK_BYTES", "Q8K_BLOCK_BYTES", "TYPE_Q4_K", "TYPE_Q5_K", "TYPE_Q6_K",
+           "BLOCK_BYTES", "GEMV_MAX_T",
            "DIST_NORMAL", "DIST_STUDENT_T4"]
