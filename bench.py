@@ -22,11 +22,11 @@ host's last-level cache), timed on this host with 16 and with 4 threads;
 its outputs are checked against the GPU's on identical inputs.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
-                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|copy]
+                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|q5k|copy]
 
---config q6k measures the Q6_K tensors a Q4_K model carries beside its Q4_K
-ones (attn_v, ffn_down, output; the MoE down-projection bank) with the same
-cold-weight method.
+--config q6k / q5k measure the Q6_K / Q5_K tensors a K-quant model carries
+beside its Q4_K ones (attn_v, ffn_down, output; the MoE down-projection bank)
+with the same cold-weight method.
 """
 from __future__ import annotations
 
@@ -46,7 +46,6 @@ from spq4k.hip import DeviceArray, Event, Graph, mem_info  # noqa: E402
 
 PEAK_HBM = 8.0e12
 Q4K_B = 144
-Q6K_B = 210
 
 # 8B dense layer (Qwen3-8B-like)
 HID, KV, FFN, VOCAB, LAYERS = 4096, 1024, 12288, 151936, 36
@@ -59,9 +58,6 @@ def log(msg):
 def q4k_bytes(M, K):
     return M * (K // 256) * Q4K_B
 
-
-def q6k_bytes(M, K):
-    return M * (K // 256) * Q6K_B
 
 
 class Synth:
@@ -329,7 +325,7 @@ def run_single(args, M, K, T, dist, outlier, name, qtype=spq4k.TYPE_Q4_K):
     """A single matrix shape, timed cold (rotating >= 1 GiB of weight copies)."""
     ctx = spq4k.Context(0)
     syn = Synth(ctx, M * K)
-    nb = q6k_bytes(M, K) if qtype == spq4k.TYPE_Q6_K else q4k_bytes(M, K)
+    nb = M * (K // 256) * spq4k.BLOCK_BYTES[qtype]
     copies = max(2, min(128, (1 << 30) // nb + 1))
     ws = [syn.weights(M, K, 77 + i, dist, outlier, qtype) for i in range(copies)]
     x = syn.activations(T * K, 5)
@@ -444,27 +440,30 @@ def run_moe(args):
     ctx.close()
 
 
-def run_q6k(args):
-    """Q6_K: the sibling K-quant a Q4_K model stores some tensors in. Dense
-    decode shapes of the 8B model at T = 1, a T = 8 batch and the down
-    projection as a prefill matmul (T = 16, 128, 512; the same shape in Q4_K
-    beside it), cold, then the MoE down-projection bank (128 experts of
-    2048x768) at T = 1..32, 8 layers of banks cold, as in run_moe."""
-    for name, M, K, T in (("Q6_K attn_v 1024x4096", 1024, 4096, 1), ("Q6_K 4096x4096", 4096, 4096, 1),
-                          ("Q6_K ffn_down 4096x12288", 4096, 12288, 1),
-                          ("Q6_K output 151936x4096", 151936, 4096, 1), ("Q6_K 4096x4096 T=8", 4096, 4096, 8),
-                          ("Q6_K ffn_down 4096x12288 T=16", 4096, 12288, 16),
-                          ("Q6_K ffn_down 4096x12288 T=128", 4096, 12288, 128),
-                          ("Q6_K ffn_down 4096x12288 T=512", 4096, 12288, 512),
+def run_kquant(args, qtype):
+    """The sibling K-quants a Q4_K model file stores some tensors in (Q6_K:
+    attn_v, ffn_down, output; Q5_K in Q5_K_M files). Dense decode shapes of the
+    8B model at T = 1, a T = 8 batch and the down projection as a prefill
+    matmul (T = 16, 128, 512; the same shape in Q4_K beside it), cold, then the
+    MoE down-projection bank (128 experts of 2048x768) at T = 1..32, 8 layers
+    of banks cold, as in run_moe."""
+    tag = "Q6_K" if qtype == spq4k.TYPE_Q6_K else "Q5_K"
+    for name, M, K, T in ((f"{tag} attn_v 1024x4096", 1024, 4096, 1), (f"{tag} 4096x4096", 4096, 4096, 1),
+                          (f"{tag} ffn_down 4096x12288", 4096, 12288, 1),
+                          (f"{tag} output 151936x4096", 151936, 4096, 1), (f"{tag} 4096x4096 T=8", 4096, 4096, 8),
+                          (f"{tag} ffn_down 4096x12288 T=16", 4096, 12288, 16),
+                          (f"{tag} ffn_down 4096x12288 T=128", 4096, 12288, 128),
+                          (f"{tag} ffn_down 4096x12288 T=512", 4096, 12288, 512),
                           ("Q4_K ffn_down 4096x12288 T=512 (same shape, Q4_K)", 4096, 12288, 512)):
-        qt = spq4k.TYPE_Q4_K if name.startswith("Q4_K") else spq4k.TYPE_Q6_K
+        qt = spq4k.TYPE_Q4_K if name.startswith("Q4_K") else qtype
         run_single(args, M, K, T, spq4k.DIST_NORMAL, 1.0, name, qt)
     ctx = spq4k.Context(0)
     E, k, NL, M, K = 128, 8, 8, 2048, 768
     syn = Synth(ctx, E * M * K)
-    banks = [syn.weights(M, K, 900 + L, qtype=spq4k.TYPE_Q6_K, E=E) for L in range(NL)]
+    banks = [syn.weights(M, K, 900 + L, qtype=qtype, E=E) for L in range(NL)]
     ctx.synchronize()
     syn.tmp.free()
+    bb = spq4k.BLOCK_BYTES[qtype]
     rng = np.random.default_rng(4)
     for T in (1, 4, 8, 32):
         ids_l = [np.argsort(-rng.standard_normal((T, E)).astype(np.float32), axis=1, kind="stable")[:, :k]
@@ -477,12 +476,12 @@ def run_q6k(args):
                 ctx.moe_dev(banks[L], idd[L].ptr, k, k, T, xd.ptr, Y.ptr)
         ms = time_graph(ctx, g, max(5, args.steps // 5), 2) / NL
         uniq = float(np.mean([len(np.unique(i)) for i in ids_l]))
-        abytes = uniq * q6k_bytes(M, K) + 4 * T * k * (K + M)
+        abytes = uniq * M * (K // 256) * bb + 4 * T * k * (K + M)
         gbs = abytes / (ms * 1e-3) / 1e9
-        print(json.dumps({"metric": f"Q6_K MoE down-projection matvec, T={T}", "value": round(gbs, 1),
+        print(json.dumps({"metric": f"{tag} MoE down-projection matvec, T={T}", "value": round(gbs, 1),
                           "unit": "GB/s", "us_per_call": round(ms * 1e3, 2),
                           "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2), "unique_experts": uniq,
-                          "config": {"workload": "128 experts of 2048x768 Q6_K, top-8, 8 banks (cold)", "T": T}}),
+                          "config": {"workload": f"128 experts of 2048x768 {tag}, top-8, 8 banks (cold)", "T": T}}),
               flush=True)
         for a in idd:
             a.free()
@@ -518,7 +517,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "copy"])
+    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -534,7 +533,9 @@ def main():
     elif args.config == "moe":
         run_moe(args)
     elif args.config == "q6k":
-        run_q6k(args)
+        run_kquant(args, spq4k.TYPE_Q6_K)
+    elif args.config == "q5k":
+        run_kquant(args, spq4k.TYPE_Q5_K)
     elif args.config == "copy":
         run_copy(args)
     elif args.config == "largek":
