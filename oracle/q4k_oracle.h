@@ -11,8 +11,8 @@
  * compiled with -ffp-contract=off so that each floating-point operation is
  * rounded exactly once, as in ggml-base (which is built without FMA flags).
  *
- * q6k_oracle.c and q5k_oracle.c restate the Q6_K and Q5_K functions the
- * same way.
+ * q6k_oracle.c, q5k_oracle.c and q8_0_oracle.c restate the Q6_K, Q5_K and
+ * Q8_0 functions the same way.
  *
  * Parity pins (see tests/): golden fixtures written by tests/golden/gen_golden.py
  * from the reference compiled in oracle/_ref, exhaustive and closed-form checks
@@ -63,7 +63,15 @@ typedef struct {
     uint8_t  qs[128];
 } or_block_q5K;
 
-/* weight types, numbered as ggml.h:402-404 numbers them */
+#define OR_QK8_0 32
+#define OR_Q8_0_BLOCK_BYTES 34   /* d (fp16), qs[32] (i8) */
+typedef struct {
+    uint16_t d;
+    int8_t   qs[32];
+} or_block_q8_0;
+
+/* weight types, numbered as ggml.h:392-404 numbers them */
+#define OR_TYPE_Q8_0 8
 #define OR_TYPE_Q4_K 12
 #define OR_TYPE_Q5_K 13
 #define OR_TYPE_Q6_K 14
@@ -120,6 +128,18 @@ float  or_vec_dot_q5K_avx2order(int n, const void *vx, const void *vy);
 double or_vec_dot_q5K_exact(int n, const void *vx, const void *vy);
 /* S[b*8 + j] = sum over the 32 weights of sub-block j of block b of q5*q8 */
 void   or_subblock_sums_q5K(int n, const void *vx, const void *vy, int32_t *S);
+
+/* Q8_0 (q8_0_oracle.c): weights and their Q8_0 activations, 32 values a block */
+void   or_quantize_row_q8_0(const float *x, void *y, int64_t k);        /* activations: x86 CPU backend */
+void   or_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);    /* weights: model-file encoder */
+void   or_dequantize_row_q8_0(const void *x, float *y, int64_t k);
+float  or_vec_dot_q8_0_generic(int n, const void *vx, const void *vy);
+float  or_vec_dot_q8_0_avx2order(int n, const void *vx, const void *vy);
+double or_vec_dot_q8_0_exact(int n, const void *vx, const void *vy);
+void   or_block_sums_q8_0(int n, const void *vx, const void *vy, int32_t *S);
+int    or_mul_mat_q8_0(const void *W, int64_t M, int64_t K, const float *X, int64_t T, float *Y, int order);
+int    or_mul_mat_id_q8_0(const void *as, int64_t M, int64_t K, int64_t E, const float *X, int64_t ne11,
+                          const int32_t *ids, int64_t k, int64_t T, float *Y, int order);
 
 /* make_qkx2_quants (q4k_oracle.c), shared by the Q4_K and Q5_K encoders */
 float or_qkx2_fit(int n, int nmax, const float *x, const float *w, uint8_t *L,

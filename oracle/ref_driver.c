@@ -32,6 +32,8 @@ void ggml_vec_dot_q6_K_q8_K_generic(int n, float *s, size_t bs, const void *vx, 
                                     const void *vy, size_t by, int nrc);
 void ggml_vec_dot_q5_K_q8_K_generic(int n, float *s, size_t bs, const void *vx, size_t bx,
                                     const void *vy, size_t by, int nrc);
+void ggml_vec_dot_q8_0_q8_0_generic(int n, float *s, size_t bs, const void *vx, size_t bx,
+                                    const void *vy, size_t by, int nrc);
 
 static int g_inited = 0;
 static void ensure_init(void) {
@@ -67,7 +69,7 @@ float ref_vec_dot_generic(int n, const void *vx, const void *vy) {
     return s;
 }
 
-/* the same traits for any weight type (GGML_TYPE_Q4_K = 12, Q5_K = 13, Q6_K = 14) */
+/* the same traits for any weight type (GGML_TYPE_Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14) */
 size_t ref_quantize_type(int type, const float *src, void *dst, int64_t nrow, int64_t n_per_row) {
     ensure_init();
     return ggml_quantize_chunk((enum ggml_type)type, src, dst, 0, nrow, n_per_row, NULL);
@@ -83,9 +85,18 @@ float ref_vec_dot_type(int type, int n, const void *vx, const void *vy, int gene
     float s = 0;
     if (generic && type == GGML_TYPE_Q6_K) ggml_vec_dot_q6_K_q8_K_generic(n, &s, 0, vx, 0, vy, 0, 1);
     else if (generic && type == GGML_TYPE_Q5_K) ggml_vec_dot_q5_K_q8_K_generic(n, &s, 0, vx, 0, vy, 0, 1);
+    else if (generic && type == GGML_TYPE_Q8_0) ggml_vec_dot_q8_0_q8_0_generic(n, &s, 0, vx, 0, vy, 0, 1);
     else if (generic) ggml_vec_dot_q4_K_q8_K_generic(n, &s, 0, vx, 0, vy, 0, 1);
     else ggml_get_type_traits_cpu((enum ggml_type)type)->vec_dot(n, &s, 0, vx, 0, vy, 0, 1);
     return s;
+}
+
+/* the CPU backend's activation quantiser for a weight type's vec_dot_type
+ * (Q8_K for the K-quants, Q8_0 for Q8_0): ggml_get_type_traits_cpu(vdt)->from_float */
+void ref_quantize_vec_dot_type(int type, const float *x, void *y, int64_t k) {
+    ensure_init();
+    const enum ggml_type vdt = ggml_get_type_traits_cpu((enum ggml_type)type)->vec_dot_type;
+    ggml_get_type_traits_cpu(vdt)->from_float(x, y, k);
 }
 
 int ref_has_avx512(void) { return ggml_cpu_has_avx512(); }

@@ -16,8 +16,10 @@ Q4K = 144
 Q5K = 176
 Q6K = 210
 Q8K = 292
-TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 12, 13, 14            # ggml.h:402-404
+Q8_0 = 34
+TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 8, 12, 13, 14            # ggml.h:392-404
 BLOCK_BYTES = {TYPE_Q4_K: Q4K, TYPE_Q5_K: Q5K, TYPE_Q6_K: Q6K}
+BLOCK_VALUES = {TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q5_K: 256, TYPE_Q6_K: 256}
 
 V, I, I64, F, U64 = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_uint64
 
@@ -71,6 +73,18 @@ class Oracle:
         L.or_vec_dot_q5K_exact.argtypes = [I, V, V]
         L.or_vec_dot_q5K_exact.restype = C.c_double
         L.or_subblock_sums_q5K.argtypes = [I, V, V, V]
+        for n in ("or_quantize_row_q8_0", "or_quantize_row_q8_0_ref", "or_dequantize_row_q8_0"):
+            getattr(L, n).argtypes = [V, V, I64]
+        for n in ("or_vec_dot_q8_0_generic", "or_vec_dot_q8_0_avx2order"):
+            getattr(L, n).argtypes = [I, V, V]
+            getattr(L, n).restype = F
+        L.or_vec_dot_q8_0_exact.argtypes = [I, V, V]
+        L.or_vec_dot_q8_0_exact.restype = C.c_double
+        L.or_block_sums_q8_0.argtypes = [I, V, V, V]
+        L.or_mul_mat_q8_0.argtypes = [V, I64, I64, V, I64, V, I]
+        L.or_mul_mat_q8_0.restype = I
+        L.or_mul_mat_id_q8_0.argtypes = [V, I64, I64, I64, V, I64, V, I64, I64, V, I]
+        L.or_mul_mat_id_q8_0.restype = I
         L.or_mul_mat_type.argtypes = [I, V, I64, I64, V, I64, V, I]
         L.or_mul_mat_id_type.argtypes = [I, V, I64, I64, I64, V, I64, V, I64, I64, V, I]
         L.or_mul_mat_dequant_f64_type.argtypes = [I, V, I64, I64, V, I64, V]
@@ -176,6 +190,47 @@ class Oracle:
         self.L.or_subblock_sums_q5K(n, _p(qx), _p(qy), _p(S))
         return S
 
+    # ---- Q8_0 (oracle/q8_0_oracle.c) ----
+    def quantize_q8_0(self, x: np.ndarray, ref_encoder=False) -> np.ndarray:
+        """Activations (the CPU backend's quantize_row_q8_0), or with
+        ref_encoder the model-file encoder quantize_row_q8_0_ref."""
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(x.size // 32 * Q8_0, np.uint8)
+        f = self.L.or_quantize_row_q8_0_ref if ref_encoder else self.L.or_quantize_row_q8_0
+        f(_p(x), _p(y), x.size)
+        return y
+
+    def dequant_q8_0(self, q: np.ndarray, k: int) -> np.ndarray:
+        y = np.empty(k, np.float32)
+        self.L.or_dequantize_row_q8_0(_p(np.ascontiguousarray(q)), _p(y), k)
+        return y
+
+    def vec_dot_q8_0(self, n, qx, qy, order="avx2"):
+        f = self.L.or_vec_dot_q8_0_avx2order if order == "avx2" else self.L.or_vec_dot_q8_0_generic
+        return f(n, _p(qx), _p(qy))
+
+    def vec_dot_q8_0_exact(self, n, qx, qy):
+        return self.L.or_vec_dot_q8_0_exact(n, _p(qx), _p(qy))
+
+    def block_sums_q8_0(self, n, qx, qy) -> np.ndarray:
+        S = np.zeros(n // 32, np.int32)
+        self.L.or_block_sums_q8_0(n, _p(qx), _p(qy), _p(S))
+        return S
+
+    def mul_mat_q8_0(self, W, M, K, X, order=1):
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+        Y = np.empty((X.shape[0], M), np.float32)
+        assert self.L.or_mul_mat_q8_0(_p(W), M, K, _p(X), X.shape[0], _p(Y), order) == 0
+        return Y
+
+    def mul_mat_id_q8_0(self, bank, M, K, E, X, ids, order=1):
+        ids = np.ascontiguousarray(ids, np.int32)
+        T, k = ids.shape
+        X = np.ascontiguousarray(X, np.float32).reshape(T, -1, K)
+        Y = np.empty((T, k, M), np.float32)
+        assert self.L.or_mul_mat_id_q8_0(_p(bank), M, K, E, _p(X), X.shape[1], _p(ids), k, T, _p(Y), order) == 0
+        return Y
+
     def quantize(self, qtype, x):
         return {TYPE_Q4_K: self.quantize_q4K, TYPE_Q5_K: self.quantize_q5K, TYPE_Q6_K: self.quantize_q6K}[qtype](x)
 
@@ -250,6 +305,7 @@ class Ref:
         L.ref_dequant_type.argtypes = [I, V, V, I64]
         L.ref_vec_dot_type.argtypes = [I, I, V, V, I]
         L.ref_vec_dot_type.restype = F
+        L.ref_quantize_vec_dot_type.argtypes = [I, V, V, I64]
         L.ref_mm_create_type.argtypes = [I, I, V, V, V, V, V, I64, I]
         L.ref_mm_create_type.restype = V
         L.ref_mmid_create_type.argtypes = [I, V, I64, I64, I64, V, I64, V, I64, I64, V, I]
@@ -283,13 +339,21 @@ class Ref:
 
     def quantize_type(self, qtype, x, nrow, n_per_row):
         x = np.ascontiguousarray(x, np.float32).ravel()
-        y = np.zeros(nrow * (n_per_row // QK_K) * BLOCK_BYTES[qtype], np.uint8)
+        nbytes = nrow * n_per_row // 32 * Q8_0 if qtype == TYPE_Q8_0 else nrow * (n_per_row // QK_K) * BLOCK_BYTES[qtype]
+        y = np.zeros(nbytes, np.uint8)
         self.L.ref_quantize_type(qtype, _p(x), _p(y), nrow, n_per_row)
         return y
 
     def dequant_type(self, qtype, q, k):
         y = np.empty(k, np.float32)
         self.L.ref_dequant_type(qtype, _p(np.ascontiguousarray(q)), _p(y), k)
+        return y
+
+    def quantize_q8_0_act(self, x):
+        """The CPU backend's activation quantiser for Q8_0 weights."""
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.zeros(x.size // 32 * Q8_0, np.uint8)
+        self.L.ref_quantize_vec_dot_type(TYPE_Q8_0, _p(x), _p(y), x.size)
         return y
 
     def vec_dot_type(self, qtype, n, qx, qy, generic=False):

@@ -26,7 +26,13 @@ dequantize_row_q6_K / _q5_K, ggml_vec_dot_q6_K_q8_K / _q5_K_q8_K and their
 _generic forms, MUL_MAT, MUL_MAT_ID), plus vec_dot cases on random block bytes
 that reach every scale and quant value.
 
-Usage: gen_golden.py [q4k] [q5k] [q6k]   (default: all)
+q8_0_golden.npz holds GGML_TYPE_Q8_0 vectors: the model-file encoder
+(quantize_q8_0 -> quantize_row_q8_0_ref), dequantize_row_q8_0, the CPU
+backend's activation quantiser (quantize_row_q8_0, which rounds half to even
+where the encoder rounds half away from zero: tie cases included),
+ggml_vec_dot_q8_0_q8_0 and its _generic form, MUL_MAT, MUL_MAT_ID.
+
+Usage: gen_golden.py [q4k] [q5k] [q6k] [q8_0]   (default: all)
 """
 import os
 import sys
@@ -35,7 +41,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
-from _oracle import TYPE_Q5_K, TYPE_Q6_K, Q5K, Q6K, Ref, ref_library_path  # noqa: E402
+from _oracle import TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, Q5K, Q6K, Q8_0, Ref, ref_library_path  # noqa: E402
 
 QK = 256
 
@@ -160,6 +166,70 @@ def gen_kquant(ref, rng, qtype, bb):
     return out
 
 
+def q8_0_act_inputs(rng):
+    c = [rng.standard_normal(32 * 64).astype(np.float32)]
+    t = np.zeros(32, np.float32); t[0] = 127.0; t[1:9] = [2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5, -3.5]
+    c.append(t)                                                                   # exact ties after scaling
+    c.append(np.zeros(32, np.float32))                                           # d = 0
+    c.append((np.arange(32) - 16).astype(np.float32) * 0.25)
+    c.append((rng.standard_normal(32) * 1e-30).astype(np.float32))
+    c.append((rng.standard_normal(32) * 1e30).astype(np.float32))
+    c.append(np.full(32, -7.0, np.float32))
+    return np.concatenate(c)
+
+
+def gen_q8_0(ref, rng):
+    out = {}
+    x = np.concatenate([q6k_encoder_inputs(rng), q8_0_act_inputs(rng)])
+    out["enc_x"] = x
+    out["enc_q"] = ref.quantize_type(TYPE_Q8_0, x, 1, x.size)
+    rb = rng.integers(0, 256, size=(256, Q8_0), dtype=np.uint8)
+    rb[:, 1] &= 0xBF                                                              # finite fp16 d
+    q = np.concatenate([out["enc_q"].reshape(-1, Q8_0), rb]).ravel()
+    out["deq_q"] = q
+    out["deq_y"] = ref.dequant_type(TYPE_Q8_0, q, q.size // Q8_0 * 32)
+    xa = q8_0_act_inputs(rng)
+    out["act_x"] = xa
+    out["act_q"] = ref.quantize_q8_0_act(xa)
+    vw, va8, vK, va, vg = [], [], [], [], []
+    for K, n, kind in ((32, 8, "enc"), (768, 8, "enc"), (4096, 8, "enc"), (27648, 4, "enc"), (4096, 8, "rand")):
+        for i in range(n):
+            if kind == "enc":
+                w = ref.quantize_type(TYPE_Q8_0, (rng.standard_normal(K) * 0.02).astype(np.float32), 1, K)
+            else:
+                w = rng.integers(0, 256, size=(K // 32, Q8_0), dtype=np.uint8)
+                w[:, 1] &= 0x3B
+                w = w.ravel()
+            a = ref.quantize_q8_0_act(rng.standard_normal(K).astype(np.float32))
+            vw.append(w); va8.append(a); vK.append(K)
+            va.append(ref.vec_dot_type(TYPE_Q8_0, K, w, a)); vg.append(ref.vec_dot_type(TYPE_Q8_0, K, w, a, True))
+    out["vd_w"] = np.concatenate(vw)
+    out["vd_a"] = np.concatenate(va8)
+    out["vd_K"] = np.array(vK, np.int64)
+    out["vd_avx2"] = np.array(va, np.float32)
+    out["vd_generic"] = np.array(vg, np.float32)
+    M, K = 64, 512
+    W = ref.quantize_type(TYPE_Q8_0, (rng.standard_normal((M, K)) * 0.02).astype(np.float32), M, K)
+    out["mm_W"] = W
+    out["mm_MK"] = np.array([M, K], np.int64)
+    for T in (1, 3, 8, 17):
+        X = rng.standard_normal((T, K)).astype(np.float32)
+        out[f"mm_X{T}"] = X
+        out[f"mm_Y{T}"] = ref.mul_mat(W, M, K, X, qtype=TYPE_Q8_0)
+    E, M, K, T = 8, 32, 512, 3
+    bank = ref.quantize_type(TYPE_Q8_0, (rng.standard_normal((E * M, K)) * 0.02).astype(np.float32), E * M, K)
+    out["mmid_bank"] = bank
+    out["mmid_EMK"] = np.array([E, M, K], np.int64)
+    for n_used, ne11 in ((2, 1), (4, 4)):
+        ids = np.stack([rng.permutation(E)[:n_used] for _ in range(T)]).astype(np.int32)
+        Xm = rng.standard_normal((T, ne11, K)).astype(np.float32)
+        tag = f"{n_used}_{ne11}"
+        out[f"mmid_ids_{tag}"] = ids
+        out[f"mmid_X_{tag}"] = Xm
+        out[f"mmid_Y_{tag}"] = ref.mul_mat_id(bank, M, K, E, Xm, ids, qtype=TYPE_Q8_0)
+    return out
+
+
 def gen_q6k(ref, rng):
     out = gen_kquant(ref, rng, TYPE_Q6_K, Q6K)
     out["vd_q6"] = out.pop("vd_w")
@@ -169,10 +239,11 @@ def gen_q6k(ref, rng):
 def main():
     if ref_library_path() is None:
         sys.exit("oracle/_ref is not built (make -C oracle ref)")
-    which = set(sys.argv[1:]) or {"q4k", "q5k", "q6k"}
+    which = set(sys.argv[1:]) or {"q4k", "q5k", "q6k", "q8_0"}
     ref = Ref()
     for tag, fn in (("q6k", lambda: gen_q6k(ref, np.random.default_rng(0x6B6B))),
-                    ("q5k", lambda: gen_kquant(ref, np.random.default_rng(0x5B5B), TYPE_Q5_K, Q5K))):
+                    ("q5k", lambda: gen_kquant(ref, np.random.default_rng(0x5B5B), TYPE_Q5_K, Q5K)),
+                    ("q8_0", lambda: gen_q8_0(ref, np.random.default_rng(0x8080)))):
         if tag not in which:
             continue
         out = fn()
