@@ -22,11 +22,14 @@ host's last-level cache), timed on this host with 16 and with 4 threads;
 its outputs are checked against the GPU's on identical inputs.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
-                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|q5k|copy]
+                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|q5k|q8_0|single|copy]
+                  [--M M --K K --T T --qtype TYPE]   (--config single)
 
---config q6k / q5k measure the Q6_K / Q5_K tensors a K-quant model carries
-beside its Q4_K ones (attn_v, ffn_down, output; the MoE down-projection bank)
-with the same cold-weight method.
+--config q6k / q5k / q8_0 measure the Q6_K / Q5_K / Q8_0 tensors a Q4_K model
+file can carry beside its Q4_K ones (attn_v, ffn_down, output; the MoE
+down-projection bank) with the same cold-weight method. --config single
+times one matrix shape of one weight type (ggml type id: 8 Q8_0, 12 Q4_K,
+13 Q5_K, 14 Q6_K) the same way, for profiling one kernel.
 """
 from __future__ import annotations
 
@@ -325,7 +328,7 @@ def run_single(args, M, K, T, dist, outlier, name, qtype=spq4k.TYPE_Q4_K):
     """A single matrix shape, timed cold (rotating >= 1 GiB of weight copies)."""
     ctx = spq4k.Context(0)
     syn = Synth(ctx, M * K)
-    nb = M * (K // 256) * spq4k.BLOCK_BYTES[qtype]
+    nb = M * (K // spq4k.BLOCK_VALUES[qtype]) * spq4k.BLOCK_BYTES[qtype]
     copies = max(2, min(128, (1 << 30) // nb + 1))
     ws = [syn.weights(M, K, 77 + i, dist, outlier, qtype) for i in range(copies)]
     x = syn.activations(T * K, 5)
@@ -441,13 +444,14 @@ def run_moe(args):
 
 
 def run_kquant(args, qtype):
-    """The sibling K-quants a Q4_K model file stores some tensors in (Q6_K:
-    attn_v, ffn_down, output; Q5_K in Q5_K_M files). Dense decode shapes of the
+    """The other types a Q4_K model file stores some tensors in (Q6_K:
+    attn_v, ffn_down, output; Q5_K in Q5_K_M files; Q8_0 for small or
+    sensitive tensors). Dense decode shapes of the
     8B model at T = 1, a T = 8 batch and the down projection as a prefill
     matmul (T = 16, 128, 512; the same shape in Q4_K beside it), cold, then the
     MoE down-projection bank (128 experts of 2048x768) at T = 1..32, 8 layers
     of banks cold, as in run_moe."""
-    tag = "Q6_K" if qtype == spq4k.TYPE_Q6_K else "Q5_K"
+    tag = {spq4k.TYPE_Q6_K: "Q6_K", spq4k.TYPE_Q5_K: "Q5_K", spq4k.TYPE_Q8_0: "Q8_0"}[qtype]
     for name, M, K, T in ((f"{tag} attn_v 1024x4096", 1024, 4096, 1), (f"{tag} 4096x4096", 4096, 4096, 1),
                           (f"{tag} ffn_down 4096x12288", 4096, 12288, 1),
                           (f"{tag} output 151936x4096", 151936, 4096, 1), (f"{tag} 4096x4096 T=8", 4096, 4096, 8),
@@ -464,6 +468,7 @@ def run_kquant(args, qtype):
     ctx.synchronize()
     syn.tmp.free()
     bb = spq4k.BLOCK_BYTES[qtype]
+    qk = spq4k.BLOCK_VALUES[qtype]
     rng = np.random.default_rng(4)
     for T in (1, 4, 8, 32):
         ids_l = [np.argsort(-rng.standard_normal((T, E)).astype(np.float32), axis=1, kind="stable")[:, :k]
@@ -476,7 +481,7 @@ def run_kquant(args, qtype):
                 ctx.moe_dev(banks[L], idd[L].ptr, k, k, T, xd.ptr, Y.ptr)
         ms = time_graph(ctx, g, max(5, args.steps // 5), 2) / NL
         uniq = float(np.mean([len(np.unique(i)) for i in ids_l]))
-        abytes = uniq * M * (K // 256) * bb + 4 * T * k * (K + M)
+        abytes = uniq * M * (K // qk) * bb + 4 * T * k * (K + M)
         gbs = abytes / (ms * 1e-3) / 1e9
         print(json.dumps({"metric": f"{tag} MoE down-projection matvec, T={T}", "value": round(gbs, 1),
                           "unit": "GB/s", "us_per_call": round(ms * 1e3, 2),
@@ -517,7 +522,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "copy"])
+    ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "q8_0",
+                                                          "single", "copy"])
+    ap.add_argument("--M", type=int, default=4096, help="rows (--config single)")
+    ap.add_argument("--K", type=int, default=4096, help="inputs (--config single)")
+    ap.add_argument("--T", type=int, default=1, help="tokens (--config single)")
+    ap.add_argument("--qtype", type=int, default=spq4k.TYPE_Q4_K, help="ggml weight type (--config single)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -536,6 +546,12 @@ def main():
         run_kquant(args, spq4k.TYPE_Q6_K)
     elif args.config == "q5k":
         run_kquant(args, spq4k.TYPE_Q5_K)
+    elif args.config == "q8_0":
+        run_kquant(args, spq4k.TYPE_Q8_0)
+    elif args.config == "single":
+        tag = {spq4k.TYPE_Q4_K: "Q4_K", spq4k.TYPE_Q5_K: "Q5_K", spq4k.TYPE_Q6_K: "Q6_K", spq4k.TYPE_Q8_0: "Q8_0"}
+        run_single(args, args.M, args.K, args.T, spq4k.DIST_NORMAL, 1.0,
+                   f"{tag[args.qtype]} {args.M}x{args.K} T={args.T}", args.qtype)
     elif args.config == "copy":
         run_copy(args)
     elif args.config == "largek":

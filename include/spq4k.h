@@ -11,6 +11,9 @@
  * through the same entry points once uploaded with their type
  * (spq4k_weights_upload_type); their outputs agree with
  * ggml_vec_dot_q6_K_q8_K / ggml_vec_dot_q5_K_q8_K the same way.
+ * GGML_TYPE_Q8_0 weights (32-value blocks; K a multiple of 32) take Q8_0
+ * activations made as the CPU backend's quantize_row_q8_0 makes them, and
+ * agree with ggml_vec_dot_q8_0_q8_0 the same way.
  *
  * Conventions
  *   - Every function returns 0 on success or a negative errno value:
@@ -48,9 +51,12 @@ extern "C" {
 #define SPQ4K_Q5K_BLOCK_BYTES 176
 #define SPQ4K_Q6K_BLOCK_BYTES 210
 #define SPQ4K_Q8K_BLOCK_BYTES 292
+#define SPQ4K_QK8_0 32
+#define SPQ4K_Q8_0_BLOCK_BYTES 34
 #define SPQ4K_GEMV_MAX_T 8
 
-/* weight types, with ggml's numbers (enum ggml_type, ggml.h:402-404) */
+/* weight types, with ggml's numbers (enum ggml_type, ggml.h:398, :402-404) */
+#define SPQ4K_TYPE_Q8_0 8
 #define SPQ4K_TYPE_Q4_K 12
 #define SPQ4K_TYPE_Q5_K 13
 #define SPQ4K_TYPE_Q6_K 14
@@ -89,13 +95,16 @@ void  *spq4k_weights_data(const spq4k_weights *w);
 size_t spq4k_weights_nbytes(const spq4k_weights *w);
 
 /* The same for a weight of ggml type `type` (SPQ4K_TYPE_Q4_K, SPQ4K_TYPE_Q5_K:
- * GGML_TYPE_Q5_K blocks of 176 bytes, ggml-common.h:334-346, or
- * SPQ4K_TYPE_Q6_K: GGML_TYPE_Q6_K blocks of 210 bytes, ggml-common.h:348-357),
- * as ggml_backend_tensor_set uploads a tensor of any type
- * (llama_weights.cpp:483-560). The plain forms above are type Q4_K. Every
- * matmul entry point below takes weights of any of these types (Q5_K
- * batches run on the sdot4 kernels, Q4_K and Q6_K ones on the matrix
- * cores); matrices passed together (the *_multi forms) must share it. */
+ * GGML_TYPE_Q5_K blocks of 176 bytes, ggml-common.h:334-346,
+ * SPQ4K_TYPE_Q6_K: GGML_TYPE_Q6_K blocks of 210 bytes, ggml-common.h:348-357,
+ * or SPQ4K_TYPE_Q8_0: GGML_TYPE_Q8_0 blocks of 34 bytes per 32 values,
+ * ggml-common.h:241-245, K a multiple of 32), as ggml_backend_tensor_set
+ * uploads a tensor of any type (llama_weights.cpp:483-560). The plain forms
+ * above are type Q4_K. Every matmul entry point below takes weights of any
+ * of these types (Q5_K and Q8_0 batches run on the sdot4 kernels, Q4_K and
+ * Q6_K ones on the matrix cores); matrices passed together (the *_multi
+ * forms) must share it. Q6_K and Q8_0 data need 2-byte alignment, Q4_K and
+ * Q5_K 16. */
 int spq4k_weights_upload_type(spq4k_ctx *ctx, int type, const void *host, int64_t M, int64_t K, int64_t E,
                               spq4k_weights **out);
 int spq4k_weights_wrap_type(spq4k_ctx *ctx, int type, const void *dev, int64_t M, int64_t K, int64_t E,
@@ -135,10 +144,13 @@ int spq4k_vec_dot(spq4k_ctx *ctx, int n, float *s, const void *vx, const void *v
  * spq4k_vec_dot_q8K    : vec_dot with vec_dot_type Q8_K, nrc = 1 (Q6_K:
  *                        ggml_vec_dot_q6_K_q8_K, arch/x86/quants.c:2288;
  *                        Q5_K: ggml_vec_dot_q5_K_q8_K, :2078); *s is a
- *                        device float.
- * Q6_K block pointers need only 2-byte alignment (ggml rows of an odd number
- * of 210-byte blocks), Q5_K ones 16. Type Q4_K gives the Q4_K entry points
- * above. */
+ *                        device float. Not for Q8_0 (see below).
+ * Q8_0 (k a multiple of 32): to_float is dequantize_row_q8_0
+ * (ggml-quants.c:491-505, bit-exact); quantize_chunk is quantize_q8_0 ->
+ * quantize_row_q8_0_ref (ggml-quants.c:2219, :234-257; bit-exact bytes).
+ * Q6_K and Q8_0 block pointers need only 2-byte alignment (ggml rows of an
+ * odd number of 210- or 34-byte blocks), Q5_K ones 16. Type Q4_K gives the
+ * Q4_K entry points above. */
 int spq4k_to_float(spq4k_ctx *ctx, int type, const void *vx, float *y, int64_t k);
 int spq4k_quantize_chunk(spq4k_ctx *ctx, int type, const float *src, void *dst, int64_t nrow, int64_t n_per_row);
 int spq4k_vec_dot_q8K(spq4k_ctx *ctx, int type, int n, float *s, const void *vx, const void *vy);
@@ -146,6 +158,20 @@ int spq4k_to_float_host(spq4k_ctx *ctx, int type, const void *vx, float *y, int6
 int spq4k_quantize_chunk_host(spq4k_ctx *ctx, int type, const float *src, void *dst, int64_t nrow,
                               int64_t n_per_row);
 int spq4k_vec_dot_q8K_host(spq4k_ctx *ctx, int type, int n, float *s, const void *vx, const void *vy);
+
+/* Q8_0's CPU type traits (ggml-cpu.c:258-261), k and n multiples of 32:
+ * spq4k_quantize_q8_0 : ggml_from_float_t for Q8_0 = quantize_row_q8_0 of the
+ *                       CPU backend (arch/x86/quants.c:302-367: d = max|x| /
+ *                       127 as fp16, q = round-half-even(x * 127 / max|x|));
+ *                       bit-exact blocks. It differs from the model-file
+ *                       encoder (spq4k_quantize_chunk) on rounding ties.
+ * spq4k_vec_dot_q8_0  : ggml_vec_dot_q8_0_q8_0 with nrc = 1
+ *                       (arch/x86/quants.c:1170-1204); vx Q8_0 weights, vy
+ *                       Q8_0 activations; *s is a device float. */
+int spq4k_quantize_q8_0(spq4k_ctx *ctx, const float *x, void *vy, int64_t k);
+int spq4k_vec_dot_q8_0(spq4k_ctx *ctx, int n, float *s, const void *vx, const void *vy);
+int spq4k_quantize_q8_0_host(spq4k_ctx *ctx, const float *x, void *vy, int64_t k);
+int spq4k_vec_dot_q8_0_host(spq4k_ctx *ctx, int n, float *s, const void *vx, const void *vy);
 
 int spq4k_dequant_host(spq4k_ctx *ctx, const void *vx, float *y, int64_t k);
 int spq4k_quantize_q8K_host(spq4k_ctx *ctx, const float *x, void *vy, int64_t k);
@@ -171,7 +197,9 @@ int spq4k_vec_dot_host(spq4k_ctx *ctx, int n, float *s, const void *vx, const vo
  *                  Y[t][s][r] = row r of expert ids[t][s] . Q8_K(X[t][s % ne11]),
  *                  ne11 in {1, n_used}; ids are device int32 [T][n_used].
  *                  Tokens are grouped per expert so each selected expert's
- *                  weights stream once per call. */
+ *                  weights stream once per call.
+ * For Q8_0 weights every matmul above quantises X to Q8_0 as
+ * spq4k_quantize_q8_0 does (the vec_dot_type of Q8_0) in place of Q8_K. */
 int spq4k_gemv(spq4k_ctx *ctx, const spq4k_weights *W, const float *x, float *y, int64_t T);
 int spq4k_gemv_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *W, const float *x,
                      float *const *y, int64_t T);
@@ -196,7 +224,9 @@ int spq4k_subblock_sums(spq4k_ctx *ctx, const void *W, int64_t M, int64_t K, con
  * the sum of q5 * q8 over sub-block j (ggml-cpu/quants.c:720-798); Q6_K gives
  * S[r][b][j], j < 16, the sum over the 16 weights of sub-block j of
  * (q - 32) * q8, the integer core of ggml_vec_dot_q6_K_q8_K
- * (ggml-cpu/quants.c:800-852). */
+ * (ggml-cpu/quants.c:800-852); Q8_0 gives S[r][b], b < K/32, the sum of
+ * qw * qx over block b against spq4k_quantize_q8_0(x), the integer core of
+ * ggml_vec_dot_q8_0_q8_0 (ggml-cpu/quants.c:400-428). */
 int spq4k_subblock_sums_type(spq4k_ctx *ctx, int type, const void *W, int64_t M, int64_t K, const float *x,
                              int32_t *S);
 

@@ -1,7 +1,7 @@
-/* spq4k_ggml.h — ggml graph nodes that run Q4_K / Q6_K matmuls through spq4k.
+/* spq4k_ggml.h — ggml graph nodes that run quantised matmuls through spq4k.
  *
- * The engine adapter for the reference's graph builders: a Q4_K (or Q6_K,
- * the sibling K-quant a Q4_K model stores some tensors in) weight's
+ * The engine adapter for the reference's graph builders: a Q4_K (or Q5_K,
+ * Q6_K or Q8_0, the types a Q4_K model stores some tensors in) weight's
  * GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID node is replaced by a ggml custom op
  * (ggml_custom_4d, ggml.h:2610-2623) whose callback runs the product on the
  * GPU through spq4k. This is the custom-op pattern the engine already uses for
@@ -33,14 +33,14 @@ typedef struct spq4k_ggml spq4k_ggml;
 int spq4k_ggml_init(int device, spq4k_ggml **out);
 void spq4k_ggml_free(spq4k_ggml *b);
 
-/* GGML_OP_MUL_MAT (ggml_mul_mat, ggml.h:1414-1420) for a Q4_K or Q6_K weight:
- * W [K, M] Q4_K / Q6_K, x [K, T] f32 contiguous (ne2 = ne3 = 1) -> [M, T] f32.
+/* GGML_OP_MUL_MAT (ggml_mul_mat, ggml.h:1414-1420) for a Q4_K, Q5_K, Q6_K or
+ * Q8_0 weight: W [K, M], x [K, T] f32 contiguous (ne2 = ne3 = 1) -> [M, T] f32.
  * Returns NULL (build ggml's own node instead) for any other type or shape. */
 struct ggml_tensor *spq4k_ggml_mul_mat(struct ggml_context *ctx, struct ggml_tensor *W, struct ggml_tensor *x,
                                        spq4k_ggml *b);
 
-/* GGML_OP_MUL_MAT_ID (ggml_mul_mat_id, ggml.h:1434-1438) for a Q4_K or Q6_K
- * expert bank: as [K, M, E], x [K, ne11, T] f32 (ne11 = 1 or n_used), ids
+/* GGML_OP_MUL_MAT_ID (ggml_mul_mat_id, ggml.h:1434-1438) for an expert bank
+ * of one of those types: as [K, M, E], x [K, ne11, T] f32 (ne11 = 1 or n_used), ids
  * [n_used, T] i32 -> [M, n_used, T] f32. */
 struct ggml_tensor *spq4k_ggml_mul_mat_id(struct ggml_context *ctx, struct ggml_tensor *as, struct ggml_tensor *x,
                                           struct ggml_tensor *ids, spq4k_ggml *b);

@@ -22,6 +22,7 @@ using namespace spq4k;
 struct spq4k_ctx {
     int device = 0;
     int num_cus = 256;
+    size_t lds_max = 64 * 1024;  // LDS a workgroup may allocate (the device's limit, at most Q80_LDS_MAX)
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     // generic device scratch (Q8_K activations, routing tables)
@@ -37,6 +38,8 @@ struct spq4k_ctx {
     int gemm_cfg = -1;           // SPQ4K_GEMM_CFG: tiled launch shape, -1 automatic
     DecodeCfg dec_force = {0, 0, false, 0};   // SPQ4K_DEC_{WAVES,DEPTH,XFIRST,GRID} overrides
     int dec_xfirst_set = 0;
+    int q80_grid = 0;            // SPQ4K_Q80_GRID: workgroups of the Q8_0 matvec, 0 automatic
+    int q80_preq = 0;            // SPQ4K_Q80_PREQ: 0 auto, 1 always quantise x once up front, 2 never
     char err[256] = {0};
 };
 
@@ -78,13 +81,19 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 int type_fmt(int type) {
     return type == SPQ4K_TYPE_Q4_K ? WF_Q4K
          : type == SPQ4K_TYPE_Q5_K ? WF_Q5K
-         : type == SPQ4K_TYPE_Q6_K ? WF_Q6K : -1;
+         : type == SPQ4K_TYPE_Q6_K ? WF_Q6K
+         : type == SPQ4K_TYPE_Q8_0 ? WF_Q80 : -1;
 }
 size_t type_block_bytes(int type) {
     return type == SPQ4K_TYPE_Q4_K ? SPQ4K_Q4K_BLOCK_BYTES
          : type == SPQ4K_TYPE_Q5_K ? SPQ4K_Q5K_BLOCK_BYTES
-         : type == SPQ4K_TYPE_Q6_K ? SPQ4K_Q6K_BLOCK_BYTES : 0;
+         : type == SPQ4K_TYPE_Q6_K ? SPQ4K_Q6K_BLOCK_BYTES
+         : type == SPQ4K_TYPE_Q8_0 ? SPQ4K_Q8_0_BLOCK_BYTES : 0;
 }
+// values per block (ggml's blck_size): 32 for Q8_0, 256 for the K-quants
+int64_t type_block_values(int type) { return type == SPQ4K_TYPE_Q8_0 ? SPQ4K_QK8_0 : SPQ4K_QK_K; }
+// alignment the kernels need of a block pointer of the type
+size_t type_align(int type) { return type == SPQ4K_TYPE_Q4_K || type == SPQ4K_TYPE_Q5_K ? 16 : 2; }
 // formats with a matrix-core kernel (the others run batches on the sdot4 kernels)
 bool fmt_has_mfma(int fmt) { return fmt == WF_Q4K || fmt == WF_Q6K; }
 
@@ -111,10 +120,10 @@ int ensure_scratch(spq4k_ctx* c, size_t bytes) {
     return 0;
 }
 
-int check_shape(spq4k_ctx* c, int64_t M, int64_t K, int64_t E) {
+int check_shape(spq4k_ctx* c, int64_t M, int64_t K, int64_t E, int64_t qk = SPQ4K_QK_K) {
     if (M <= 0 || K <= 0 || E <= 0) return set_err(c, -EINVAL, "non-positive shape M=%lld K=%lld E=%lld",
                                                    (long long)M, (long long)K, (long long)E);
-    if (K % SPQ4K_QK_K) return set_err(c, -EINVAL, "K=%lld is not a multiple of 256", (long long)K);
+    if (K % qk) return set_err(c, -EINVAL, "K=%lld is not a multiple of %lld", (long long)K, (long long)qk);
     if (M > (1ll << 30) || K > (1ll << 30)) return set_err(c, -EINVAL, "shape too large");
     return 0;
 }
@@ -211,6 +220,95 @@ DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb, int64_t rows) {
 int gemm_segments(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T,
                   int mode);
 
+// ---- Q8_0 planning ------------------------------------------------------------
+// Q8_0 planes of `rows` activation rows in the context scratch: values
+// [rows][K] int8, then scales [rows][nb] fp32; `extra` bytes behind them.
+size_t q80_planes_bytes(int64_t rows, int nb) { return (((size_t)rows * nb * 36) + 255) & ~(size_t)255; }
+
+int q80_planes(spq4k_ctx* c, const float* x, int64_t x_tstride, int64_t rows, int nb, Q80Params* p,
+               size_t extra = 0) {
+    int rc = ensure_scratch(c, q80_planes_bytes(rows, nb) + extra);
+    if (rc) return rc;
+    int8_t* q = (int8_t*)c->scratch;
+    float* d = (float*)(c->scratch + (size_t)rows * nb * 32);
+    hipError_t e = launch_quantize_q8_0_planes(x, x_tstride, (int)rows, nb, q, d, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "quantize_q8_0_planes launch");
+    p->Aq = q;
+    p->Ad = d;
+    return 0;
+}
+
+// Workgroups of a Q8_0 matvec over `rows` weight rows: one or two per CU,
+// never more than there are row groups. Two when the activation rows a
+// workgroup stages are small (36 KB or less), one otherwise.
+int q80_grid(const spq4k_ctx* c, int64_t rows, int nb, int64_t xrows) {
+    if (c->q80_grid) return c->q80_grid;
+    const int64_t per_wg = q80_rows_per_wg(nb);
+    const int64_t need = (rows + per_wg - 1) / per_wg;
+    const int64_t cap = (q80_lds_bytes((int)xrows, nb) <= 36 * 1024 ? 2 : 1) * (int64_t)c->num_cus;
+    return (int)(need < cap ? need : cap);
+}
+
+// GGML_OP_MUL_MAT for Q8_0 weights, any T: n matrices sharing the input x
+// (rows of K floats). T <= 8 tokens go in one launch with the activations
+// quantised in every workgroup (T = 1) or once up front into planes that the
+// workgroups copy to LDS; larger T run over slices of those planes, as many
+// tokens a launch as LDS holds (at most 8); a row too long for LDS reads its
+// one token from the planes directly.
+int q80_dense(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T) {
+    const int64_t K = W[0]->K;
+    const int nb = (int)(K / SPQ4K_QK8_0);
+    Q80Params p;
+    memset(&p, 0, sizeof p);
+    int64_t total = 0;
+    for (int i = 0; i < n; ++i) {
+        p.seg[i].W = W[i]->data;
+        p.seg[i].Y = Y[i];
+        p.seg[i].M = (int32_t)W[i]->M;
+        p.seg[i].y_tstride = W[i]->M;
+        p.seg[i].row_begin = (int32_t)total;
+        total += W[i]->M;
+    }
+    if (total > (1ll << 31) - 1) return set_err(c, -EINVAL, "gemv: too many rows");
+    for (int i = n; i < GEMV_MAX_SEG; ++i) {   // unused segments: never selected
+        p.seg[i] = p.seg[0];
+        p.seg[i].row_begin = INT32_MAX;
+    }
+    p.nseg = n;
+    p.nb = nb;
+    p.total_rows = (int32_t)total;
+    p.X = X;
+    p.x_tstride = K;
+    const size_t per_tok = q80_lds_bytes(1, nb);
+    const int64_t fit = (int64_t)(c->lds_max / per_tok);   // tokens whose planes fit in LDS
+    const int64_t tmax = fit < SPQ4K_GEMV_MAX_T ? fit : SPQ4K_GEMV_MAX_T;
+    bool preq = T > 1 || tmax < 1;
+    if (c->q80_preq == 1) preq = true;
+    if (c->q80_preq == 2 && T <= tmax) preq = false;
+    if (!preq) {
+        p.n_xrows = (int32_t)T;
+        hipError_t e = launch_gemv_q8_0(p, (int)T, false, q80_grid(c, total, nb, T), c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemv_q8_0 launch");
+        return 0;
+    }
+    int rc = q80_planes(c, X, K, T, nb, &p);
+    if (rc) return rc;
+    const int8_t* q0 = p.Aq;
+    const float* d0 = p.Ad;
+    const int64_t step = tmax >= 1 ? tmax : 1;
+    for (int64_t t0 = 0; t0 < T; t0 += step) {
+        const int tc = (int)(T - t0 < step ? T - t0 : step);
+        p.Aq = q0 + t0 * K;
+        p.Ad = d0 + t0 * nb;
+        p.n_xrows = tc;
+        for (int i = 0; i < n; ++i) p.seg[i].Y = Y[i] + t0 * W[i]->M;
+        for (int i = n; i < GEMV_MAX_SEG; ++i) p.seg[i].Y = p.seg[0].Y;
+        hipError_t e = launch_gemv_q8_0(p, tc, tmax < 1, q80_grid(c, total, nb, tmax < 1 ? 0 : tc), c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemv_q8_0 launch");
+    }
+    return 0;
+}
+
 int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* x, float* const* y, int64_t T) {
     if (n < 1 || n > GEMV_MAX_SEG) return set_err(c, -EINVAL, "gemv: n=%d matrices (1..4)", n);
     if (T < 1 || T > SPQ4K_GEMV_MAX_T) return set_err(c, -EINVAL, "gemv: T=%lld (1..8)", (long long)T);
@@ -222,10 +320,11 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         if (!W[i] || !W[i]->data || !y || !y[i]) return set_err(c, -EINVAL, "gemv: null weight or output");
         if (W[i]->K != K || W[i]->E != 1) return set_err(c, -EINVAL, "gemv: matrices must share K and have E=1");
         if (W[i]->type != W[0]->type) return set_err(c, -EINVAL, "gemv: matrices must share the weight type");
-        if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemv: weights not 16-byte aligned");
+        if (!aligned(W[i]->data, type_align(W[i]->type))) return set_err(c, -EINVAL, "gemv: weights misaligned");
         if (W[i]->device != c->device) return set_err(c, -EINVAL, "gemv: weights live on another device");
         Ms[i] = W[i]->M;
     }
+    if (W[0]->fmt == WF_Q80) return q80_dense(c, n, W, x, y, T);
     const int bpr = pick_bpr(c, Ms, n);
     const int rows = gemv_rows_per_tile(bpr);
     GemvParams p;
@@ -354,8 +453,10 @@ int spq4k_init(int device, spq4k_ctx** out) {
     c->device = device;
     if (hipSetDevice(device) != hipSuccess) { delete c; return -ENODEV; }
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0) {
         c->num_cus = prop.multiProcessorCount;
+        c->lds_max = prop.sharedMemPerBlock < Q80_LDS_MAX ? prop.sharedMemPerBlock : Q80_LDS_MAX;
+    }
     if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) { delete c; return -EIO; }
     c->stream = c->own_stream;
     if (const char* f = getenv("SPQ4K_GEMV_BPR")) {
@@ -393,6 +494,14 @@ int spq4k_init(int device, spq4k_ctx** out) {
     if (const char* f = getenv("SPQ4K_GEMV_MFMA_MIN_T")) {
         const int v = atoi(f);
         if (v >= 2) c->gemv_mfma_min_t = v;
+    }
+    if (const char* f = getenv("SPQ4K_Q80_GRID")) {
+        const int v = atoi(f);
+        if (v > 0 && v <= 65536) c->q80_grid = v;
+    }
+    if (const char* f = getenv("SPQ4K_Q80_PREQ")) {
+        const int v = atoi(f);
+        if (v == 1 || v == 2) c->q80_preq = v;
     }
     // scratch for Q8_K activation planes: sized for prefill batches up front
     // so that steady-state calls (and graph capture) never allocate
@@ -432,8 +541,8 @@ static int weights_new(spq4k_ctx* c, int type, int64_t M, int64_t K, int64_t E, 
     if (!out) return set_err(c, -EINVAL, "weights: null out");
     *out = nullptr;
     if (type_fmt(type) < 0)
-        return set_err(c, -EINVAL, "weights: unsupported type %d (Q4_K = 12, Q5_K = 13, Q6_K = 14)", type);
-    int rc = check_shape(c, M, K, E);
+        return set_err(c, -EINVAL, "weights: unsupported type %d (Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14)", type);
+    int rc = check_shape(c, M, K, E, type_block_values(type));
     if (rc) return rc;
     spq4k_weights* w = new (std::nothrow) spq4k_weights();
     if (!w) return -ENOMEM;
@@ -443,7 +552,7 @@ static int weights_new(spq4k_ctx* c, int type, int64_t M, int64_t K, int64_t E, 
     w->M = M;
     w->K = K;
     w->E = E;
-    w->nbytes = (size_t)E * (size_t)M * (size_t)(K / SPQ4K_QK_K) * type_block_bytes(type);
+    w->nbytes = (size_t)E * (size_t)M * (size_t)(K / type_block_values(type)) * type_block_bytes(type);
     *out = w;
     return 0;
 }
@@ -638,6 +747,13 @@ int spq4k_to_float(spq4k_ctx* c, int type, const void* vx, float* y, int64_t k) 
     if (type == SPQ4K_TYPE_Q4_K) return spq4k_dequant(c, vx, y, k);
     int rc = use_device(c);
     if (rc) return rc;
+    if (type == SPQ4K_TYPE_Q8_0) {
+        if (!vx || !y || k < 0 || k % SPQ4K_QK8_0 || !aligned(vx, 2) || !aligned(y, 16))
+            return set_err(c, -EINVAL, "to_float: bad arguments");
+        hipError_t e = launch_dequant_q8_0((const uint8_t*)vx, y, k / SPQ4K_QK8_0, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "dequant_q8_0 launch");
+        return 0;
+    }
     if (type != SPQ4K_TYPE_Q6_K && type != SPQ4K_TYPE_Q5_K)
         return set_err(c, -EINVAL, "to_float: unsupported type %d", type);
     if (!vx || !y || k < 0 || k % SPQ4K_QK_K || !aligned(vx, type == SPQ4K_TYPE_Q5_K ? 16 : 2) || !aligned(y, 16))
@@ -652,6 +768,14 @@ int spq4k_quantize_chunk(spq4k_ctx* c, int type, const float* src, void* dst, in
     if (type == SPQ4K_TYPE_Q4_K) return spq4k_quantize_q4K(c, src, dst, nrow, n_per_row);
     int rc = use_device(c);
     if (rc) return rc;
+    if (type == SPQ4K_TYPE_Q8_0) {
+        if (!src || !dst || nrow < 0 || n_per_row <= 0 || n_per_row % SPQ4K_QK8_0 || !aligned(src, 16) ||
+            !aligned(dst, 2))
+            return set_err(c, -EINVAL, "quantize_chunk: bad arguments");
+        hipError_t e = launch_quantize_q8_0(src, (uint8_t*)dst, nrow * (n_per_row / SPQ4K_QK8_0), true, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "quantize_q8_0 launch");
+        return 0;
+    }
     if (type != SPQ4K_TYPE_Q6_K && type != SPQ4K_TYPE_Q5_K)
         return set_err(c, -EINVAL, "quantize_chunk: unsupported type %d", type);
     if (!src || !dst || nrow < 0 || n_per_row <= 0 || n_per_row % SPQ4K_QK_K || !aligned(src, 16) ||
@@ -680,12 +804,67 @@ int spq4k_vec_dot_q8K(spq4k_ctx* c, int type, int n, float* s, const void* vx, c
     return 0;
 }
 
+int spq4k_quantize_q8_0(spq4k_ctx* c, const float* x, void* vy, int64_t k) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!x || !vy || k < 0 || k % SPQ4K_QK8_0 || !aligned(x, 16) || !aligned(vy, 2))
+        return set_err(c, -EINVAL, "quantize_q8_0: bad arguments");
+    hipError_t e = launch_quantize_q8_0(x, (uint8_t*)vy, k / SPQ4K_QK8_0, false, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "quantize_q8_0 launch");
+    return 0;
+}
+
+int spq4k_vec_dot_q8_0(spq4k_ctx* c, int n, float* s, const void* vx, const void* vy) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!s || !vx || !vy || n <= 0 || n % SPQ4K_QK8_0 || !aligned(vx, 2) || !aligned(vy, 2))
+        return set_err(c, -EINVAL, "vec_dot_q8_0: bad arguments");
+    hipError_t e = launch_vec_dot_q8_0((const uint8_t*)vx, (const uint8_t*)vy, n / SPQ4K_QK8_0, s, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "vec_dot_q8_0 launch");
+    return 0;
+}
+
+int spq4k_quantize_q8_0_host(spq4k_ctx* c, const float* x, void* vy, int64_t k) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!x || !vy || k < 0 || k % SPQ4K_QK8_0) return set_err(c, -EINVAL, "quantize_q8_0_host: bad arguments");
+    const size_t nin = (size_t)k * sizeof(float), nout = (size_t)(k / SPQ4K_QK8_0) * SPQ4K_Q8_0_BLOCK_BYTES;
+    DevBuf a, b;
+    if (hipMalloc(&a.p, nin + 16) != hipSuccess || hipMalloc(&b.p, nout + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "quantize_q8_0_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, x, nin, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_quantize_q8_0(c, (const float*)a.p, b.p, k);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(vy, b.p, nout, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int spq4k_vec_dot_q8_0_host(spq4k_ctx* c, int n, float* s, const void* vx, const void* vy) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!s || !vx || !vy || n <= 0 || n % SPQ4K_QK8_0) return set_err(c, -EINVAL, "vec_dot_q8_0_host: bad arguments");
+    const size_t nx = (size_t)(n / SPQ4K_QK8_0) * SPQ4K_Q8_0_BLOCK_BYTES;
+    DevBuf a, b, o;
+    if (hipMalloc(&a.p, nx + 16) != hipSuccess || hipMalloc(&b.p, nx + 16) != hipSuccess ||
+        hipMalloc(&o.p, 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "vec_dot_q8_0_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, vx, nx, hipMemcpyHostToDevice, c->stream));
+    SPQ_HIP(c, hipMemcpyAsync(b.p, vy, nx, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_vec_dot_q8_0(c, n, (float*)o.p, a.p, b.p);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(s, o.p, sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
 int spq4k_to_float_host(spq4k_ctx* c, int type, const void* vx, float* y, int64_t k) {
     int rc = use_device(c);
     if (rc) return rc;
     const size_t bb = type_block_bytes(type);
-    if (!vx || !y || k < 0 || k % SPQ4K_QK_K || !bb) return set_err(c, -EINVAL, "to_float_host: bad arguments");
-    const size_t nin = (size_t)(k / SPQ4K_QK_K) * bb, nout = (size_t)k * sizeof(float);
+    const int64_t qk = type_block_values(type);
+    if (!vx || !y || k < 0 || k % qk || !bb) return set_err(c, -EINVAL, "to_float_host: bad arguments");
+    const size_t nin = (size_t)(k / qk) * bb, nout = (size_t)k * sizeof(float);
     DevBuf a, b;
     if (hipMalloc(&a.p, nin + 16) != hipSuccess || hipMalloc(&b.p, nout + 16) != hipSuccess)
         return set_err(c, -ENOMEM, "to_float_host");
@@ -701,10 +880,11 @@ int spq4k_quantize_chunk_host(spq4k_ctx* c, int type, const float* src, void* ds
     int rc = use_device(c);
     if (rc) return rc;
     const size_t bb = type_block_bytes(type);
-    if (!src || !dst || nrow < 0 || n_per_row <= 0 || n_per_row % SPQ4K_QK_K || !bb)
+    const int64_t qk = type_block_values(type);
+    if (!src || !dst || nrow < 0 || n_per_row <= 0 || n_per_row % qk || !bb)
         return set_err(c, -EINVAL, "quantize_chunk_host: bad arguments");
     const int64_t k = nrow * n_per_row;
-    const size_t nin = (size_t)k * sizeof(float), nout = (size_t)(k / SPQ4K_QK_K) * bb;
+    const size_t nin = (size_t)k * sizeof(float), nout = (size_t)(k / qk) * bb;
     DevBuf a, b;
     if (hipMalloc(&a.p, nin + 16) != hipSuccess || hipMalloc(&b.p, nout + 16) != hipSuccess)
         return set_err(c, -ENOMEM, "quantize_chunk_host");
@@ -760,6 +940,7 @@ namespace {
 // plane of a K split behind it), launch.
 int gemm_segments(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T,
                   int mode) {
+    if (W[0]->fmt == WF_Q80) return q80_dense(c, n, W, X, Y, T);
     const int64_t K = W[0]->K;
     GemmParams p;
     memset(&p, 0, sizeof p);
@@ -828,7 +1009,7 @@ int spq4k_gemm_multi(spq4k_ctx* c, int n, const spq4k_weights* const* W, const f
         if (!W[i] || !W[i]->data || !Y[i] || W[i]->E != 1 || W[i]->K != K)
             return set_err(c, -EINVAL, "gemm: matrices must be non-null, E=1 and share K");
         if (W[i]->type != W[0]->type) return set_err(c, -EINVAL, "gemm: matrices must share the weight type");
-        if (!aligned(W[i]->data, 16)) return set_err(c, -EINVAL, "gemm: misaligned weights");
+        if (!aligned(W[i]->data, type_align(W[i]->type))) return set_err(c, -EINVAL, "gemm: misaligned weights");
         if (W[i]->device != c->device) return set_err(c, -EINVAL, "gemm: weights live on another device");
     }
     return gemm_segments(c, n, W, X, Y, T, c->gemm_mode);
@@ -845,6 +1026,75 @@ int spq4k_mul_mat(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y
     return spq4k_gemm(c, W, X, Y, T);
 }
 
+namespace {
+
+// GGML_OP_MUL_MAT_ID for a Q8_0 bank (arguments checked by spq4k_moe).
+// Small batches sweep the rows of every routed pair in one launch with the
+// input rows quantised into each workgroup's LDS; larger ones quantise the
+// input rows once into planes, route the pairs by expert and stream each
+// active expert once, its pairs TC at a time.
+int q80_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t n_used, int64_t ne11, int64_t T,
+            const float* X, float* Y) {
+    const int E = (int)bank->E, M = (int)bank->M, nb = (int)(bank->K / SPQ4K_QK8_0);
+    const int64_t rows = T * ne11, n_pairs = T * n_used;
+    Q80Params p;
+    memset(&p, 0, sizeof p);
+    p.nb = nb;
+    p.bank = bank->data;
+    p.expert_bytes = (size_t)M * nb * SPQ4K_Q8_0_BLOCK_BYTES;
+    p.Y = Y;
+    p.E = E;
+    p.M = M;
+    p.n_used = (int32_t)n_used;
+    p.ne11 = (int32_t)ne11;
+    p.X = X;
+    p.x_tstride = bank->K;
+    if (T <= 4 && n_pairs <= MOE_DEC_MAX_PAIRS && q80_lds_bytes((int)rows, nb) <= 64 * 1024 && c->moe_mode == 0 &&
+        !c->moe_unfused && n_pairs * M <= INT32_MAX) {
+        p.ids = ids;
+        p.n_xrows = (int32_t)rows;
+        p.total_rows = (int32_t)(n_pairs * M);
+        hipError_t e = launch_moe_q8_0_sweep(p, q80_grid(c, n_pairs * M, nb, rows), c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "moe_q8_0 sweep launch");
+        return 0;
+    }
+    if (rows * nb > INT32_MAX) return set_err(c, -EINVAL, "moe: too many input rows");
+    // scratch: Q8_0 planes | routing tables
+    const size_t planes = q80_planes_bytes(rows, nb);
+    const size_t route_bytes = (size_t)(1 + 3 * E + n_pairs) * sizeof(int32_t);
+    int rc = q80_planes(c, X, bank->K, rows, nb, &p, route_bytes);
+    if (rc) return rc;
+    int32_t* rt = (int32_t*)(c->scratch + planes);
+    p.route.n_act = rt;
+    p.route.act = rt + 1;
+    p.route.act_off = rt + 1 + E;
+    p.route.act_cnt = rt + 1 + 2 * E;
+    p.route.pairs = rt + 1 + 3 * E;
+    hipError_t e = launch_moe_route(ids, (int)n_pairs, E, p.route, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe route launch");
+    // pairs a row is dotted with at a time: about twice the mean an active
+    // expert receives, at most 8
+    const int64_t max_act = n_pairs < E ? n_pairs : E;
+    const int64_t mean_pairs = (n_pairs + max_act - 1) / max_act;
+    int tc = 1;
+    while (tc < 8 && tc < 2 * mean_pairs) tc *= 2;
+    // rows of an expert a workgroup takes: whole passes of its waves, as few
+    // as still give two workgroups per CU over the experts that can be active
+    const int64_t pass = q80_rows_per_wg(nb);
+    const int64_t passes = (M + pass - 1) / pass;
+    int64_t groups = (2 * (int64_t)c->num_cus + max_act - 1) / max_act;
+    if (groups > passes) groups = passes;
+    const int64_t per_wg = (passes + groups - 1) / groups * pass;
+    p.rows_per_wg = (int32_t)per_wg;
+    p.groups = (int32_t)((M + per_wg - 1) / per_wg);
+    if (max_act * p.groups > INT32_MAX) return set_err(c, -EINVAL, "moe: grid too large");
+    e = launch_moe_q8_0_grouped(p, tc, (int)(max_act * p.groups), c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe_q8_0 grouped launch");
+    return 0;
+}
+
+}  // namespace
+
 int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t n_used, int64_t ne11,
               int64_t T, const float* X, float* Y) {
     int rc = use_device(c);
@@ -853,9 +1103,10 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     if (T < 1 || n_used < 1 || n_used > bank->E || (ne11 != 1 && ne11 != n_used))
         return set_err(c, -EINVAL, "moe: T=%lld n_used=%lld ne11=%lld", (long long)T, (long long)n_used,
                        (long long)ne11);
-    if (!aligned(X, 16) || !aligned(bank->data, 16) || !aligned(ids, 4))
+    if (!aligned(X, 16) || !aligned(bank->data, type_align(bank->type)) || !aligned(ids, 4))
         return set_err(c, -EINVAL, "moe: misaligned pointer");
     if (bank->E > 4096 || T * n_used > (1 << 24)) return set_err(c, -EINVAL, "moe: too many experts or pairs");
+    if (bank->fmt == WF_Q80) return q80_moe(c, bank, ids, n_used, ne11, T, X, Y);
     const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
     const size_t bb = type_block_bytes(bank->type);
     const int64_t rows = T * ne11, n_pairs = T * n_used;
@@ -1047,6 +1298,14 @@ int spq4k_subblock_sums_type(spq4k_ctx* c, int type, const void* W, int64_t M, i
     if (type == SPQ4K_TYPE_Q4_K) return spq4k_subblock_sums(c, W, M, K, x, S);
     int rc = use_device(c);
     if (rc) return rc;
+    if (type == SPQ4K_TYPE_Q8_0) {
+        rc = check_shape(c, M, K, 1, SPQ4K_QK8_0);
+        if (rc) return rc;
+        if (!W || !x || !S || !aligned(W, 2) || !aligned(x, 16)) return set_err(c, -EINVAL, "subblock_sums: bad pointers");
+        hipError_t e = launch_block_sums_q8_0((const uint8_t*)W, (int)M, (int)(K / SPQ4K_QK8_0), x, S, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "block_sums_q8_0 launch");
+        return 0;
+    }
     if (type != SPQ4K_TYPE_Q6_K && type != SPQ4K_TYPE_Q5_K)
         return set_err(c, -EINVAL, "subblock_sums: unsupported type %d", type);
     rc = check_shape(c, M, K, 1);

@@ -16,6 +16,7 @@ enum WFmt : int32_t {
     WF_Q4K = 0,   // GGML_TYPE_Q4_K, 144-byte blocks
     WF_Q6K = 1,   // GGML_TYPE_Q6_K, 210-byte blocks
     WF_Q5K = 2,   // GGML_TYPE_Q5_K, 176-byte blocks (sdot4 kernels only)
+    WF_Q80 = 3,   // GGML_TYPE_Q8_0, 34-byte blocks of 32 (kernels of k_q8_0.hip)
 };
 
 struct GemvSeg {
@@ -174,5 +175,43 @@ hipError_t launch_quantize_q5k(const float* x, uint8_t* y, int64_t nblocks, hipS
 hipError_t launch_dequant_q5k(const uint8_t* x, float* y, int64_t nblocks, hipStream_t st);
 hipError_t launch_vec_dot_q5k(const uint8_t* wx, const uint8_t* q8, int nb, float* out, hipStream_t st);
 hipError_t launch_subblock_sums_q5k(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
+
+// Q8_0 weights (k_q8_0.hip): Q8_0 activations, one group of lanes per row
+constexpr size_t Q80_LDS_MAX = 160 * 1024;   // LDS of one workgroup on gfx950
+struct Q80Params {
+    GemvSeg seg[GEMV_MAX_SEG];   // dense: matrices sharing the input (W, Y, y_tstride, row_begin)
+    int32_t nseg;
+    int32_t nb;                  // Q8_0 blocks per row (K / 32)
+    int32_t total_rows;          // dense: rows of all segments; sweep: n_pairs * M
+    // activations: p.X quantised into LDS, or Q8_0 planes Aq [row][K], Ad [row][nb]
+    const float* X;              // fp32 rows x[r * x_tstride + k], 16-byte aligned
+    int64_t x_tstride;
+    int32_t n_xrows;             // activation rows the kernel stages in LDS
+    const int8_t* Aq;
+    const float* Ad;
+    // expert-gathered forms
+    const uint8_t* bank;         // E experts of [M][nb] blocks
+    size_t expert_bytes;
+    float* Y;                    // [T][n_used][M]
+    const int32_t* ids;          // sweep: [T][n_used]
+    int32_t E, M, n_used, ne11;
+    MoeRoute route;              // grouped: routing tables (launch_moe_route)
+    int32_t groups;              // grouped: workgroups per active expert
+    int32_t rows_per_wg;         // grouped: rows of the expert a workgroup takes
+};
+size_t q80_lds_bytes(int xrows, int nb);
+int q80_lanes_per_row(int nb);
+int q80_rows_per_wg(int nb);
+hipError_t launch_quantize_q8_0(const float* x, uint8_t* y, int64_t nblocks, bool ref_encoder, hipStream_t st);
+hipError_t launch_dequant_q8_0(const uint8_t* x, float* y, int64_t nblocks, hipStream_t st);
+hipError_t launch_quantize_q8_0_planes(const float* x, int64_t x_tstride, int rows, int nb, int8_t* q, float* d,
+                                       hipStream_t st);
+hipError_t launch_block_sums_q8_0(const uint8_t* W, int M, int nb, const float* x, int32_t* S, hipStream_t st);
+hipError_t launch_vec_dot_q8_0(const uint8_t* wx, const uint8_t* a, int nb, float* out, hipStream_t st);
+// T tokens (p.n_xrows == T), LDS-staged activations, or with global_acts
+// (T = 1) read from p.Aq / p.Ad
+hipError_t launch_gemv_q8_0(const Q80Params& p, int T, bool global_acts, int grid, hipStream_t st);
+hipError_t launch_moe_q8_0_sweep(const Q80Params& p, int grid, hipStream_t st);
+hipError_t launch_moe_q8_0_grouped(const Q80Params& p, int tc, int grid, hipStream_t st);
 
 }  // namespace spq4k

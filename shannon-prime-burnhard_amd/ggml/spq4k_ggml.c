@@ -1,4 +1,4 @@
-/* spq4k_ggml.c — ggml custom-op nodes for Q4_K / Q6_K GGML_OP_MUL_MAT /
+/* spq4k_ggml.c — ggml custom-op nodes for Q4_K / Q5_K / Q6_K / Q8_0 GGML_OP_MUL_MAT /
  * GGML_OP_MUL_MAT_ID, run on the GPU through spq4k (include/spq4k_ggml.h).
  *
  * The node is ggml_custom_4d (ggml.h:2610-2623) with the weight, the
@@ -183,8 +183,10 @@ static void run_mul_mat_id(struct ggml_tensor *dst, int ith, int nth, void *user
     if (rc) fail(b, dst, rc, "spq4k_ggml_mul_mat_id");
 }
 
-/* weight types the library runs (spq4k.h: SPQ4K_TYPE_Q4_K, _Q5_K, _Q6_K) */
-static int supported(enum ggml_type t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K; }
+/* weight types the library runs (spq4k.h: SPQ4K_TYPE_Q4_K, _Q5_K, _Q6_K, _Q8_0) */
+static int supported(enum ggml_type t) {
+    return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K || t == GGML_TYPE_Q8_0;
+}
 
 struct ggml_tensor *spq4k_ggml_mul_mat(struct ggml_context *ctx, struct ggml_tensor *W, struct ggml_tensor *x,
                                        spq4k_ggml *b) {

@@ -5,14 +5,15 @@ mirror the reference's operator interface for this path (vendored ggml in
 nihilistau/shannon-prime-burnhard):
 
     to_float        ggml_type_traits[type].to_float   (ggml.h:2791-2804)
-    from_float      ggml_type_traits_cpu[Q8_K].from_float (ggml-cpu.h:113-123)
+    from_float      ggml_type_traits_cpu[vec_dot_type].from_float (ggml-cpu.h:113-123)
     quantize_chunk  ggml_quantize_chunk(type, imatrix=NULL) (ggml.h:2764)
-    vec_dot         ggml_vec_dot_t for type x Q8_K    (ggml-cpu.h:113)
+    vec_dot         ggml_vec_dot_t for type x vec_dot_type (ggml-cpu.h:113)
     mul_mat         GGML_OP_MUL_MAT                   (ggml.h:1414-1420)
     mul_mat_id      GGML_OP_MUL_MAT_ID                (ggml.h:1434-1438)
 
-`type` is ggml's type id: TYPE_Q4_K (12, the default), TYPE_Q5_K (13) or
-TYPE_Q6_K (14).
+`type` is ggml's type id: TYPE_Q4_K (12, the default), TYPE_Q5_K (13),
+TYPE_Q6_K (14) or TYPE_Q8_0 (8). The K-quants' vec_dot_type is Q8_K
+(256-value blocks); Q8_0's is Q8_0 (32-value blocks).
 
 Every call runs on the GPU through libspq4k.so; if the library is missing
 or the device is absent the call raises. There is no CPU fallback.
@@ -32,10 +33,15 @@ Q4K_BLOCK_BYTES = 144
 Q5K_BLOCK_BYTES = 176
 Q6K_BLOCK_BYTES = 210
 Q8K_BLOCK_BYTES = 292
+QK8_0 = 32
+Q8_0_BLOCK_BYTES = 34
+TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
 TYPE_Q5_K = 13
 TYPE_Q6_K = 14
-BLOCK_BYTES = {TYPE_Q4_K: Q4K_BLOCK_BYTES, TYPE_Q5_K: Q5K_BLOCK_BYTES, TYPE_Q6_K: Q6K_BLOCK_BYTES}
+BLOCK_BYTES = {TYPE_Q4_K: Q4K_BLOCK_BYTES, TYPE_Q5_K: Q5K_BLOCK_BYTES, TYPE_Q6_K: Q6K_BLOCK_BYTES,
+               TYPE_Q8_0: Q8_0_BLOCK_BYTES}
+BLOCK_VALUES = {TYPE_Q4_K: QK_K, TYPE_Q5_K: QK_K, TYPE_Q6_K: QK_K, TYPE_Q8_0: QK8_0}
 GEMV_MAX_T = 8
 DIST_NORMAL = 0
 DIST_STUDENT_T4 = 1
@@ -106,6 +112,10 @@ def load_library(path: str | None = None):
         "spq4k_quantize_chunk_host": (I, [V, I, V, V, I64, I64]),
         "spq4k_vec_dot_q8K_host": (I, [V, I, I, V, V, V]),
         "spq4k_subblock_sums_type": (I, [V, I, V, I64, I64, V, V]),
+        "spq4k_quantize_q8_0": (I, [V, V, V, I64]),
+        "spq4k_vec_dot_q8_0": (I, [V, I, V, V, V]),
+        "spq4k_quantize_q8_0_host": (I, [V, V, V, I64]),
+        "spq4k_vec_dot_q8_0_host": (I, [V, I, V, V, V]),
         "spq4k_synth_fill": (I, [V, V, I64, U64, I, I64, F, F, F, I64]),
     }
     for name, (res, args) in sig.items():
@@ -131,7 +141,7 @@ def _ptr(a):
 
 
 class Weights:
-    """A Q4_K or Q6_K weight matrix (or an E-expert bank) in device memory."""
+    """A quantised weight matrix (or an E-expert bank) of one type in device memory."""
 
     def __init__(self, ctx: "Context", handle, M, K, E, type=TYPE_Q4_K):
         self.ctx, self.handle, self.M, self.K, self.E, self.type = ctx, handle, M, K, E, type
@@ -222,8 +232,14 @@ class Context:
         self._check("spq4k_to_float_host", self.lib.spq4k_to_float_host(self.handle, type, _ptr(q), _ptr(y), k))
         return y
 
-    def from_float(self, x: np.ndarray) -> np.ndarray:
+    def from_float(self, x: np.ndarray, type: int = TYPE_Q4_K) -> np.ndarray:
+        """Activations to the vec_dot_type of weight type `type` (Q8_K, or Q8_0 for TYPE_Q8_0)."""
         x = np.ascontiguousarray(x, np.float32).ravel()
+        if type == TYPE_Q8_0:
+            y = np.zeros(x.size // QK8_0 * Q8_0_BLOCK_BYTES, np.uint8)
+            self._check("spq4k_quantize_q8_0_host",
+                        self.lib.spq4k_quantize_q8_0_host(self.handle, _ptr(x), _ptr(y), x.size))
+            return y
         y = np.zeros(x.size // QK_K * Q8K_BLOCK_BYTES, np.uint8)
         self._check("spq4k_quantize_q8K_host",
                     self.lib.spq4k_quantize_q8K_host(self.handle, _ptr(x), _ptr(y), x.size))
@@ -231,13 +247,17 @@ class Context:
 
     def quantize_chunk(self, src: np.ndarray, nrow: int, n_per_row: int, type: int = TYPE_Q4_K) -> np.ndarray:
         src = np.ascontiguousarray(src, np.float32).ravel()
-        y = np.zeros(nrow * (n_per_row // QK_K) * BLOCK_BYTES[type], np.uint8)
+        y = np.zeros(nrow * (n_per_row // BLOCK_VALUES[type]) * BLOCK_BYTES[type], np.uint8)
         self._check("spq4k_quantize_chunk_host",
                     self.lib.spq4k_quantize_chunk_host(self.handle, type, _ptr(src), _ptr(y), nrow, n_per_row))
         return y
 
     def vec_dot(self, n: int, vx: np.ndarray, vy: np.ndarray, type: int = TYPE_Q4_K) -> float:
         s = C.c_float()
+        if type == TYPE_Q8_0:
+            self._check("spq4k_vec_dot_q8_0_host",
+                        self.lib.spq4k_vec_dot_q8_0_host(self.handle, n, C.byref(s), _ptr(vx), _ptr(vy)))
+            return s.value
         self._check("spq4k_vec_dot_q8K_host",
                     self.lib.spq4k_vec_dot_q8K_host(self.handle, type, n, C.byref(s), _ptr(vx), _ptr(vy)))
         return s.value
@@ -307,6 +327,12 @@ class Context:
     def vec_dot_q8K_dev(self, type: int, n: int, s_dev: int, vx: int, vy: int):
         self._check("spq4k_vec_dot_q8K", self.lib.spq4k_vec_dot_q8K(self.handle, type, n, s_dev, vx, vy))
 
+    def quantize_q8_0_dev(self, x: int, vy: int, k: int):
+        self._check("spq4k_quantize_q8_0", self.lib.spq4k_quantize_q8_0(self.handle, x, vy, k))
+
+    def vec_dot_q8_0_dev(self, n: int, s_dev: int, vx: int, vy: int):
+        self._check("spq4k_vec_dot_q8_0", self.lib.spq4k_vec_dot_q8_0(self.handle, n, s_dev, vx, vy))
+
     def synth_fill_dev(self, out: int, n: int, seed: int, dist: int = DIST_NORMAL, cols: int = 0,
                        mean: float = 0.0, std: float = 1.0, outlier_mult: float = 1.0, offset: int = 0):
         self._check("spq4k_synth_fill", self.lib.spq4k_synth_fill(self.handle, out, n, seed, dist, cols, mean, std,
@@ -314,6 +340,6 @@ class Context:
 
 
 __all__ = ["Context", "Weights", "Spq4kError", "load_library", "LIB_PATH", "QK_K", "Q4K_BLOCK_BYTES",
-           "Q5K_BLOCK_BYTES", "Q6K_BLOCK_BYTES", "Q8K_BLOCK_BYTES", "TYPE_Q4_K", "TYPE_Q5_K", "TYPE_Q6_K",
-           "BLOCK_BYTES", "GEMV_MAX_T",
+           "Q5K_BLOCK_BYTES", "Q6K_BLOCK_BYTES", "Q8K_BLOCK_BYTES", "QK8_0", "Q8_0_BLOCK_BYTES", "TYPE_Q8_0",
+           "TYPE_Q4_K", "TYPE_Q5_K", "TYPE_Q6_K", "BLOCK_BYTES", "BLOCK_VALUES", "GEMV_MAX_T",
            "DIST_NORMAL", "DIST_STUDENT_T4"]

@@ -5,8 +5,8 @@
  * ggml's GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID nodes, once with the adapter's
  * spq4k nodes — computes it on the CPU with ggml_graph_compute_with_ctx and
  * returns both outputs; the Python test compares them with close_enough.
- * Weights are seeded N(0, 0.02) quantised by ggml_quantize_chunk (Q4_K or
- * Q6_K, as the caller asks), activations seeded N(0, 1).
+ * Weights are seeded N(0, 0.02) quantised by ggml_quantize_chunk (of the type
+ * the caller asks), activations seeded N(0, 1).
  */
 #include <math.h>
 #include <stdint.h>

@@ -1,6 +1,6 @@
 """The ggml engine adapter (include/spq4k_ggml.h) inside a real ggml graph,
-for Q4_K weights and for the Q5_K / Q6_K tensors K-quant models carry beside
-them.
+for Q4_K weights and for the Q5_K / Q6_K / Q8_0 tensors Q4_K models carry
+beside them.
 
 The reference's own ggml (compiled from its sources into oracle/_ref) hosts a
 graph in which the same inputs go through ggml's GGML_OP_MUL_MAT /
@@ -24,7 +24,7 @@ import os
 import numpy as np
 import pytest
 
-from _oracle import TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, close_enough
+from _oracle import TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, close_enough
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -62,7 +62,7 @@ def _check(yr, ya, what):
                       f"adapter {ya[np.argmax(~ok)]} ggml {yr[np.argmax(~ok)]}")
 
 
-@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K])
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0])
 @pytest.mark.parametrize("M,K,T", [(4096, 4096, 1), (300, 2048, 3), (256, 5120, 8), (512, 4096, 64), (128, 12288, 17)])
 def test_adapter_mul_mat(drv, qtype, M, K, T):
     yr, ya = _run(drv.check_mul_mat, M * T, qtype, M, K, T, 11 + T)
@@ -72,7 +72,7 @@ def test_adapter_mul_mat(drv, qtype, M, K, T):
 FF_NORMWISE = 2e-3   # bound on ||y_adapter - y_ggml|| / ||y_ggml|| for the whole block
 
 
-@pytest.mark.parametrize("down_type", [TYPE_Q4_K, TYPE_Q6_K])
+@pytest.mark.parametrize("down_type", [TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0])
 @pytest.mark.parametrize("D,F,T", [(2048, 5632, 1), (1024, 2816, 6), (1024, 2816, 32)])
 def test_adapter_feed_forward(drv, down_type, D, F, T):
     n = D * T
@@ -87,7 +87,7 @@ def test_adapter_feed_forward(drv, down_type, D, F, T):
     assert rel <= FF_NORMWISE, f"feed-forward block D={D} F={F} T={T}: normwise {rel:.3e} > {FF_NORMWISE}"
 
 
-@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K])
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0])
 @pytest.mark.parametrize("T,ne11", [(1, 1), (3, 4), (12, 1)])
 def test_adapter_mul_mat_id(drv, qtype, T, ne11):
     E, M, K, k = 32, 256, 1024, 4
