@@ -22,14 +22,18 @@ host's last-level cache), timed on this host with 16 and with 4 threads;
 its outputs are checked against the GPU's on identical inputs.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
-                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|q5k|q8_0|single|copy]
+                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|q5k|q8_0|single|gguf|copy]
                   [--M M --K K --T T --qtype TYPE]   (--config single)
 
 --config q6k / q5k / q8_0 measure the Q6_K / Q5_K / Q8_0 tensors a Q4_K model
 file can carry beside its Q4_K ones (attn_v, ffn_down, output; the MoE
 down-projection bank) with the same cold-weight method. --config single
 times one matrix shape of one weight type (ggml type id: 8 Q8_0, 12 Q4_K,
-13 Q5_K, 14 Q6_K) the same way, for profiling one kernel.
+13 Q5_K, 14 Q6_K) the same way, for profiling one kernel. --config gguf writes
+a synthetic GGUF file of 8B-model Q4_K / Q6_K tensors (12 layers and the
+output matrix, 1.66 GB) to the temporary directory and times making it
+resident (spq4k_model_load) against a per-tensor hipMemcpy from the file
+mapping.
 """
 from __future__ import annotations
 
@@ -494,6 +498,99 @@ def run_kquant(args, qtype):
     ctx.close()
 
 
+def _write_gguf(path, spec, rng):
+    """A GGUF v3 file (default alignment 32) of tensors [(name, ggml type,
+    ne)] with random bytes, written in chunks."""
+    import struct
+    bb = {spq4k.TYPE_Q4_K: (256, 144), spq4k.TYPE_Q6_K: (256, 210)}
+    def gstr(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+    head = bytearray(b"GGUF") + struct.pack("<Iqq", 3, len(spec), 1)
+    head += gstr("general.architecture") + struct.pack("<i", 8) + gstr("llama")
+    off, sizes = 0, []
+    for name, t, ne in spec:
+        n = int(np.prod(ne)) // bb[t][0] * bb[t][1]
+        head += gstr(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<q", x) for x in ne)
+        head += struct.pack("<iQ", t, off)
+        sizes.append(n)
+        off += (n + 31) // 32 * 32
+    head += b"\0" * ((-len(head)) % 32)
+    with open(path, "wb") as f:
+        f.write(head)
+        for n in sizes:
+            left = n
+            while left:
+                c = min(left, 64 << 20)
+                f.write(rng.bytes(c))
+                left -= c
+            f.write(b"\0" * ((-n) % 32))
+    return sum(sizes)
+
+
+def run_gguf(args):
+    """GGUF residency: LlamaWeights::load_backend_offload_'s upload
+    (desktop/engine/src/llama_weights.cpp:483-720) of 12 layers of the 8B
+    shapes plus the output matrix, warm page cache (the file was just
+    written). Roofline: the host link, PCIe 5.0 x16, 64 GB/s a direction."""
+    import tempfile
+    from spq4k.hip import _lib, check, H2D
+    spec = []
+    for L in range(12):
+        spec += [(f"blk.{L}.attn_q.weight", spq4k.TYPE_Q4_K, (HID, HID)),
+                 (f"blk.{L}.attn_k.weight", spq4k.TYPE_Q4_K, (HID, KV)),
+                 (f"blk.{L}.attn_v.weight", spq4k.TYPE_Q6_K, (HID, KV)),
+                 (f"blk.{L}.attn_output.weight", spq4k.TYPE_Q4_K, (HID, HID)),
+                 (f"blk.{L}.ffn_gate.weight", spq4k.TYPE_Q4_K, (HID, FFN)),
+                 (f"blk.{L}.ffn_up.weight", spq4k.TYPE_Q4_K, (HID, FFN)),
+                 (f"blk.{L}.ffn_down.weight", spq4k.TYPE_Q6_K, (FFN, HID))]
+    spec.append(("output.weight", spq4k.TYPE_Q6_K, (HID, VOCAB)))
+    path = os.path.join(tempfile.gettempdir(), f"spq4k_bench_{os.getpid()}.gguf")
+    rng = np.random.default_rng(5)
+    try:
+        t0 = time.perf_counter()
+        total = _write_gguf(path, spec, rng)
+        log(f"gguf: wrote {total / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s")
+        ctx = spq4k.Context(0)
+        g = spq4k.Gguf(path)
+        best = None
+        for _ in range(3):
+            t0 = time.perf_counter()
+            m = ctx.load_model(g)
+            dt = time.perf_counter() - t0
+            assert m.nbytes >= total
+            m.free()
+            best = dt if best is None else min(best, dt)
+        # per-tensor copies from the mapping (pageable host memory)
+        tens = g.tensors()
+        dev = DeviceArray(sum((t[5] + 255) // 256 * 256 for t in tens), np.uint8)
+        base = None
+        for _ in range(2):
+            ctx.synchronize()
+            t0 = time.perf_counter()
+            off = 0
+            for i, t in enumerate(tens):
+                src = g.lib.spq4k_gguf_tensor_data(g.handle, i)
+                check(_lib().hipMemcpy(dev.ptr + off, src, t[5], H2D), "hipMemcpy H2D")
+                off += (t[5] + 255) // 256 * 256
+            dt = time.perf_counter() - t0
+            base = dt if base is None else min(base, dt)
+        dev.free()
+        g.close()
+        ctx.close()
+        gbs = total / best / 1e9
+        print(json.dumps({"metric": "GGUF weight residency (spq4k_model_load), host to HBM", "value": round(gbs, 2),
+                          "unit": "GB/s", "seconds": round(best, 3), "bytes": total, "tensors": len(spec),
+                          "roofline": {"bound": "pcie", "achieved": round(gbs, 2), "peak": 64.0, "unit": "GB/s",
+                                       "frac": round(gbs / 64.0, 3)},
+                          "per_tensor_hipMemcpy_GBps": round(total / base / 1e9, 2),
+                          "config": {"workload": "12 layers of 8B shapes + output, Q4_K / Q6_K, warm page cache"}}),
+              flush=True)
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+
+
 def run_copy(args):
     """A plain device-to-device copy of 1 GiB (the runtime's blit kernel): the
     known-size reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE."""
@@ -523,7 +620,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "q8_0",
-                                                          "single", "copy"])
+                                                          "single", "gguf", "copy"])
     ap.add_argument("--M", type=int, default=4096, help="rows (--config single)")
     ap.add_argument("--K", type=int, default=4096, help="inputs (--config single)")
     ap.add_argument("--T", type=int, default=1, help="tokens (--config single)")
@@ -548,6 +645,8 @@ def main():
         run_kquant(args, spq4k.TYPE_Q5_K)
     elif args.config == "q8_0":
         run_kquant(args, spq4k.TYPE_Q8_0)
+    elif args.config == "gguf":
+        run_gguf(args)
     elif args.config == "single":
         tag = {spq4k.TYPE_Q4_K: "Q4_K", spq4k.TYPE_Q5_K: "Q5_K", spq4k.TYPE_Q6_K: "Q6_K", spq4k.TYPE_Q8_0: "Q8_0"}
         run_single(args, args.M, args.K, args.T, spq4k.DIST_NORMAL, 1.0,

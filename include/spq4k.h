@@ -74,6 +74,8 @@ void        spq4k_free(spq4k_ctx *ctx);
 /* Use the caller's hipStream_t (NULL restores the context's own stream). */
 int         spq4k_set_stream(spq4k_ctx *ctx, void *hip_stream);
 void       *spq4k_get_stream(spq4k_ctx *ctx);
+/* the HIP device of the context */
+int         spq4k_get_device(const spq4k_ctx *ctx);
 int         spq4k_synchronize(spq4k_ctx *ctx);
 const char *spq4k_last_error(const spq4k_ctx *ctx);
 int         spq4k_device_count(void);
@@ -112,6 +114,8 @@ int spq4k_weights_wrap_type(spq4k_ctx *ctx, int type, const void *dev, int64_t M
 int spq4k_weights_alloc_type(spq4k_ctx *ctx, int type, int64_t M, int64_t K, int64_t E, spq4k_weights **out);
 /* the ggml type id of w, or -EINVAL for NULL */
 int spq4k_weights_type(const spq4k_weights *w);
+/* the shape of w (rows M, inputs K, experts E); -EINVAL for NULL */
+int spq4k_weights_shape(const spq4k_weights *w, int64_t *M, int64_t *K, int64_t *E);
 
 /* ---- type traits (ggml.h:2791-2804, ggml-cpu.h:113-123) -----------------
  * spq4k_dequant      : ggml_to_float_t for Q4_K   = dequantize_row_q4_K

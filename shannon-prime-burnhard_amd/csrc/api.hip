@@ -526,6 +526,7 @@ int spq4k_set_stream(spq4k_ctx* c, void* s) {
 }
 
 void* spq4k_get_stream(spq4k_ctx* c) { return c ? (void*)c->stream : nullptr; }
+int spq4k_get_device(const spq4k_ctx* c) { return c ? c->device : -EINVAL; }
 
 int spq4k_synchronize(spq4k_ctx* c) {
     int rc = use_device(c);
@@ -621,6 +622,13 @@ void spq4k_weights_free(spq4k_weights* w) {
 
 void* spq4k_weights_data(const spq4k_weights* w) { return w ? (void*)w->data : nullptr; }
 int spq4k_weights_type(const spq4k_weights* w) { return w ? w->type : -EINVAL; }
+int spq4k_weights_shape(const spq4k_weights* w, int64_t* M, int64_t* K, int64_t* E) {
+    if (!w) return -EINVAL;
+    if (M) *M = w->M;
+    if (K) *K = w->K;
+    if (E) *E = w->E;
+    return 0;
+}
 size_t spq4k_weights_nbytes(const spq4k_weights* w) { return w ? w->nbytes : 0; }
 
 // ---- type traits ---------------------------------------------------------------

@@ -112,6 +112,39 @@ def load_library(path: str | None = None):
         "spq4k_quantize_chunk_host": (I, [V, I, V, V, I64, I64]),
         "spq4k_vec_dot_q8K_host": (I, [V, I, I, V, V, V]),
         "spq4k_subblock_sums_type": (I, [V, I, V, I64, I64, V, V]),
+        "spq4k_get_device": (I, [V]),
+        "spq4k_weights_shape": (I, [V, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64)]),
+        "spq4k_gguf_open": (I, [C.c_char_p, PV]),
+        "spq4k_gguf_close": (None, [V]),
+        "spq4k_gguf_strerror": (C.c_char_p, []),
+        "spq4k_gguf_version": (C.c_uint32, [V]),
+        "spq4k_gguf_alignment": (S, [V]),
+        "spq4k_gguf_data_offset": (S, [V]),
+        "spq4k_gguf_data_size": (S, [V]),
+        "spq4k_gguf_file_size": (S, [V]),
+        "spq4k_gguf_n_kv": (I64, [V]),
+        "spq4k_gguf_find_key": (I64, [V, C.c_char_p]),
+        "spq4k_gguf_key": (C.c_char_p, [V, I64]),
+        "spq4k_gguf_kv_type": (I, [V, I64]),
+        "spq4k_gguf_arr_type": (I, [V, I64]),
+        "spq4k_gguf_arr_n": (I64, [V, I64]),
+        "spq4k_gguf_val_data": (V, [V, I64]),
+        "spq4k_gguf_val_str": (C.c_char_p, [V, I64, I64]),
+        "spq4k_gguf_n_tensors": (I64, [V]),
+        "spq4k_gguf_find_tensor": (I64, [V, C.c_char_p]),
+        "spq4k_gguf_tensor_name": (C.c_char_p, [V, I64]),
+        "spq4k_gguf_tensor_type": (I, [V, I64]),
+        "spq4k_gguf_tensor_shape": (I, [V, I64, C.POINTER(C.c_int64)]),
+        "spq4k_gguf_tensor_offset": (S, [V, I64]),
+        "spq4k_gguf_tensor_nbytes": (S, [V, I64]),
+        "spq4k_gguf_tensor_data": (V, [V, I64]),
+        "spq4k_model_load": (I, [V, V, I, I, PV]),
+        "spq4k_model_free": (None, [V]),
+        "spq4k_model_weights": (V, [V, C.c_char_p]),
+        "spq4k_model_expert_base": (I, [V, C.c_char_p]),
+        "spq4k_model_n_tensors": (I64, [V]),
+        "spq4k_model_tensor_name": (C.c_char_p, [V, I64]),
+        "spq4k_model_nbytes": (S, [V]),
         "spq4k_quantize_q8_0": (I, [V, V, V, I64]),
         "spq4k_vec_dot_q8_0": (I, [V, I, V, V, V]),
         "spq4k_quantize_q8_0_host": (I, [V, V, V, I64]),
@@ -140,6 +173,146 @@ def _ptr(a):
     raise TypeError(f"cannot take a pointer of {type(a)}")
 
 
+GGUF_SCALAR = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32, 6: np.float32,
+               7: np.uint8, 10: np.uint64, 11: np.int64, 12: np.float64}
+GGUF_STRING, GGUF_ARRAY = 8, 9
+
+
+class Gguf:
+    """A GGUF model file mapped read-only (include/spq4k_gguf.h): the metadata
+    and tensor tables of gguf_init_from_file, tensor bytes as views of the
+    mapping. Host only."""
+
+    def __init__(self, path: str):
+        self.lib = load_library()
+        h = C.c_void_p()
+        rc = self.lib.spq4k_gguf_open(os.fsencode(path), C.byref(h))
+        if rc != 0:
+            raise Spq4kError("spq4k_gguf_open", rc, self.lib.spq4k_gguf_strerror().decode(errors="replace"))
+        self.handle = h
+        self.path = path
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.spq4k_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def version(self) -> int:
+        return self.lib.spq4k_gguf_version(self.handle)
+
+    @property
+    def alignment(self) -> int:
+        return self.lib.spq4k_gguf_alignment(self.handle)
+
+    @property
+    def data_offset(self) -> int:
+        return self.lib.spq4k_gguf_data_offset(self.handle)
+
+    @property
+    def data_size(self) -> int:
+        return self.lib.spq4k_gguf_data_size(self.handle)
+
+    def kv(self) -> list:
+        """[(key, type, arr_type, value)]: value a numpy array (non-string
+        types, scalars of one element) or a list of str."""
+        out = []
+        for i in range(self.lib.spq4k_gguf_n_kv(self.handle)):
+            key = self.lib.spq4k_gguf_key(self.handle, i).decode()
+            t = self.lib.spq4k_gguf_kv_type(self.handle, i)
+            at = self.lib.spq4k_gguf_arr_type(self.handle, i) if t == GGUF_ARRAY else -1
+            et = at if t == GGUF_ARRAY else t
+            n = self.lib.spq4k_gguf_arr_n(self.handle, i)
+            if et == GGUF_STRING:
+                val = [self.lib.spq4k_gguf_val_str(self.handle, i, j).decode("utf-8", "surrogateescape") for j in range(n)]
+            else:
+                dt = np.dtype(GGUF_SCALAR[et])
+                ptr = self.lib.spq4k_gguf_val_data(self.handle, i)
+                val = (np.ctypeslib.as_array((C.c_uint8 * (n * dt.itemsize)).from_address(ptr)).view(dt).copy()
+                       if n else np.zeros(0, dt))
+            out.append((key, t, at, val))
+        return out
+
+    def tensors(self) -> list:
+        """[(name, ggml type, ne (4), n_dims, offset, nbytes)] in file order."""
+        out = []
+        ne = (C.c_int64 * 4)()
+        for i in range(self.lib.spq4k_gguf_n_tensors(self.handle)):
+            nd = self.lib.spq4k_gguf_tensor_shape(self.handle, i, ne)
+            out.append((self.lib.spq4k_gguf_tensor_name(self.handle, i).decode(),
+                        self.lib.spq4k_gguf_tensor_type(self.handle, i), tuple(ne), nd,
+                        self.lib.spq4k_gguf_tensor_offset(self.handle, i),
+                        self.lib.spq4k_gguf_tensor_nbytes(self.handle, i)))
+        return out
+
+    def find_tensor(self, name: str) -> int:
+        return self.lib.spq4k_gguf_find_tensor(self.handle, name.encode())
+
+    def tensor_bytes(self, i: int) -> np.ndarray:
+        """The tensor's bytes as a read-only view of the mapping."""
+        n = self.lib.spq4k_gguf_tensor_nbytes(self.handle, i)
+        ptr = self.lib.spq4k_gguf_tensor_data(self.handle, i)
+        if n == 0:
+            return np.zeros(0, np.uint8)
+        a = np.ctypeslib.as_array((C.c_uint8 * n).from_address(ptr))
+        a.flags.writeable = False
+        return a
+
+
+class Model:
+    """Weights of a GGUF file resident on the GPU (spq4k_model_load)."""
+
+    def __init__(self, ctx: "Context", gguf: Gguf, n_gpu_layers: int = -1, experts_on_cpu: int = 0):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        h = C.c_void_p()
+        rc = self.lib.spq4k_model_load(ctx.handle, gguf.handle, n_gpu_layers, experts_on_cpu, C.byref(h))
+        if rc != 0:
+            raise Spq4kError("spq4k_model_load", rc, self.lib.spq4k_gguf_strerror().decode(errors="replace"))
+        self.handle = h
+
+    def names(self) -> list:
+        return [self.lib.spq4k_model_tensor_name(self.handle, i).decode()
+                for i in range(self.lib.spq4k_model_n_tensors(self.handle))]
+
+    @property
+    def nbytes(self) -> int:
+        return self.lib.spq4k_model_nbytes(self.handle)
+
+    def weights(self, name: str):
+        """Weights view of resident tensor `name` (owned by the model), or None."""
+        h = self.lib.spq4k_model_weights(self.handle, name.encode())
+        if not h:
+            return None
+        return _ModelWeights(self, h)
+
+    def expert_base(self, name: str) -> int:
+        return self.lib.spq4k_model_expert_base(self.handle, name.encode())
+
+    def free(self):
+        if getattr(self, "handle", None):
+            self.lib.spq4k_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Weights:
     """A quantised weight matrix (or an E-expert bank) of one type in device memory."""
 
@@ -164,6 +337,20 @@ class Weights:
             self.free()
         except Exception:
             pass
+
+
+class _ModelWeights(Weights):
+    """Weights owned by a Model: freed with it, never by this object."""
+
+    def __init__(self, model: "Model", handle):
+        lib = model.lib
+        M, K, E = C.c_int64(), C.c_int64(), C.c_int64()
+        lib.spq4k_weights_shape(handle, C.byref(M), C.byref(K), C.byref(E))
+        super().__init__(model.ctx, C.c_void_p(handle), M.value, K.value, E.value, lib.spq4k_weights_type(handle))
+        self.model = model   # keeps the model alive while the view is used
+
+    def free(self):
+        self.handle = None
 
 
 class Context:
@@ -225,6 +412,9 @@ class Context:
         self._check("spq4k_weights_alloc_type",
                     self.lib.spq4k_weights_alloc_type(self.handle, type, M, K, E, C.byref(h)))
         return Weights(self, h, M, K, E, type)
+
+    def load_model(self, gguf: Gguf, n_gpu_layers: int = -1, experts_on_cpu: int = 0) -> Model:
+        return Model(self, gguf, n_gpu_layers, experts_on_cpu)
 
     # -- type traits on host arrays (synchronous)
     def to_float(self, q: np.ndarray, k: int, type: int = TYPE_Q4_K) -> np.ndarray:
@@ -341,5 +531,5 @@ class Context:
 
 __all__ = ["Context", "Weights", "Spq4kError", "load_library", "LIB_PATH", "QK_K", "Q4K_BLOCK_BYTES",
            "Q5K_BLOCK_BYTES", "Q6K_BLOCK_BYTES", "Q8K_BLOCK_BYTES", "QK8_0", "Q8_0_BLOCK_BYTES", "TYPE_Q8_0",
-           "TYPE_Q4_K", "TYPE_Q5_K", "TYPE_Q6_K", "BLOCK_BYTES", "BLOCK_VALUES", "GEMV_MAX_T",
+           "TYPE_Q4_K", "TYPE_Q5_K", "TYPE_Q6_K", "BLOCK_BYTES", "BLOCK_VALUES", "GEMV_MAX_T", "Gguf", "Model",
            "DIST_NORMAL", "DIST_STUDENT_T4"]

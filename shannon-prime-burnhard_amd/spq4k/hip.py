@@ -79,6 +79,14 @@ def synchronize():
     check(_lib().hipDeviceSynchronize(), "hipDeviceSynchronize")
 
 
+def download(ptr: int, nbytes: int) -> np.ndarray:
+    """nbytes of device memory at ptr, as uint8 (synchronous)."""
+    out = np.empty(nbytes, np.uint8)
+    if nbytes:
+        check(_lib().hipMemcpy(out.ctypes.data, ptr, nbytes, D2H), "hipMemcpy D2H")
+    return out
+
+
 class DeviceArray:
     """A device allocation with a numpy dtype/shape (no arithmetic)."""
 
