@@ -22,7 +22,7 @@ host's last-level cache), timed on this host with 16 and with 4 threads;
 its outputs are checked against the GPU's on identical inputs.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
-                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|q5k|q8_0|single|gguf|copy]
+                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|q5k|q8_0|single|gguf|fusion|copy]
                   [--M M --K K --T T --qtype TYPE]   (--config single)
 
 --config q6k / q5k / q8_0 measure the Q6_K / Q5_K / Q8_0 tensors a Q4_K model
@@ -33,7 +33,9 @@ times one matrix shape of one weight type (ggml type id: 8 Q8_0, 12 Q4_K,
 a synthetic GGUF file of 8B-model Q4_K / Q6_K tensors (12 layers and the
 output matrix, 1.66 GB) to the temporary directory and times making it
 resident (spq4k_model_load) against a per-tensor hipMemcpy from the file
-mapping.
+mapping. --config fusion times the decode (T = 1) pre-norm projections and
+SwiGLU front half of the 8B layer fused (one launch) and unfused (the norm,
+the matvec, the element-wise pass), cold.
 """
 from __future__ import annotations
 
@@ -591,6 +593,66 @@ def run_gguf(args):
             os.remove(path)
 
 
+def run_fusion(args):
+    """Decode-step neighbours of the matvec, 8B shapes, Q4_K, cold weights:
+    the attention pre-norm + q/k/v (spq4k_mul_mat_rms_norm) and the FFN
+    pre-norm + gate/up + SiLU * up (spq4k_mul_mat_swiglu), each fused into
+    one launch and unfused (spq4k_rms_norm, the grouped matvec, spq4k_swiglu),
+    captured in a graph. Algorithmic bytes: weights + x + norm weights + y."""
+    ctx = spq4k.Context(0)
+    K = HID
+    syn = Synth(ctx, FFN * K)
+    x = syn.activations(K, 3)
+    nw = syn.activations(K, 4)
+    xn = DeviceArray(K)
+    eps = 1e-6
+    cases = {
+        "qkv": [(HID, K), (KV, K), (KV, K)],
+        "gate_up": [(FFN, K), (FFN, K)],
+    }
+    for name, shapes in cases.items():
+        wb = sum(q4k_bytes(M, K) for M, _ in shapes)
+        copies = max(2, min(64, (1 << 30) // wb + 1))
+        sets = [[syn.weights(M, K, 300 + 10 * i + j) for j, (M, _) in enumerate(shapes)] for i in range(copies)]
+        ys = [DeviceArray(M) for M, _ in shapes]
+        y = DeviceArray(shapes[0][0])
+        ctx.synchronize()
+        n = max(args.steps, copies)
+        out_bytes = 4 * (shapes[0][0] if name == "gate_up" else sum(M for M, _ in shapes))
+        alg = wb + 8 * K + out_bytes
+        res = {}
+        for fused in (True, False):
+            with Graph.capture(ctx.stream) as g:
+                for i in range(n):
+                    W = sets[i % copies]
+                    if name == "qkv":
+                        if fused:
+                            ctx.mul_mat_rms_norm_dev(W, x.ptr, nw.ptr, eps, [a.ptr for a in ys], 1)
+                        else:
+                            ctx.rms_norm_dev(x.ptr, nw.ptr, eps, xn.ptr, K, 1)
+                            ctx.gemv_multi_dev(W, xn.ptr, [a.ptr for a in ys], 1)
+                    else:
+                        if fused:
+                            ctx.mul_mat_swiglu_dev(W[0], W[1], x.ptr, nw.ptr, eps, y.ptr, 1)
+                        else:
+                            ctx.rms_norm_dev(x.ptr, nw.ptr, eps, xn.ptr, K, 1)
+                            ctx.gemv_multi_dev(W, xn.ptr, [ys[0].ptr, ys[1].ptr], 1)
+                            ctx.swiglu_dev(ys[0].ptr, ys[1].ptr, y.ptr, FFN)
+            ms = time_graph(ctx, g, 1, max(1, args.warmup // 10)) / n
+            res[fused] = ms
+        print(json.dumps({"metric": f"decode {name} with its pre-norm" + (" and SwiGLU" if name == "gate_up" else ""),
+                          "fused_us": round(res[True] * 1e3, 2), "unfused_us": round(res[False] * 1e3, 2),
+                          "fused_GBps": round(alg / (res[True] * 1e-3) / 1e9, 1),
+                          "unfused_GBps": round(alg / (res[False] * 1e-3) / 1e9, 1),
+                          "speedup": round(res[False] / res[True], 3),
+                          "config": {"workload": f"8B {name}, Q4_K, T=1, {copies} weight copies (cold)",
+                                     "algorithmic_bytes": alg}}), flush=True)
+        for ws in sets:
+            for w in ws:
+                w.free()
+    ctx.close()
+
+
 def run_copy(args):
     """A plain device-to-device copy of 1 GiB (the runtime's blit kernel): the
     known-size reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE."""
@@ -620,7 +682,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "q8_0",
-                                                          "single", "gguf", "copy"])
+                                                          "single", "gguf", "fusion", "copy"])
     ap.add_argument("--M", type=int, default=4096, help="rows (--config single)")
     ap.add_argument("--K", type=int, default=4096, help="inputs (--config single)")
     ap.add_argument("--T", type=int, default=1, help="tokens (--config single)")
@@ -647,6 +709,8 @@ def main():
         run_kquant(args, spq4k.TYPE_Q8_0)
     elif args.config == "gguf":
         run_gguf(args)
+    elif args.config == "fusion":
+        run_fusion(args)
     elif args.config == "single":
         tag = {spq4k.TYPE_Q4_K: "Q4_K", spq4k.TYPE_Q5_K: "Q5_K", spq4k.TYPE_Q6_K: "Q6_K", spq4k.TYPE_Q8_0: "Q8_0"}
         run_single(args, args.M, args.K, args.T, spq4k.DIST_NORMAL, 1.0,

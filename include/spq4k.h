@@ -214,6 +214,36 @@ int spq4k_mul_mat(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float 
 int spq4k_moe(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int64_t n_used,
               int64_t ne11, int64_t T, const float *X, float *Y);
 
+/* ---- the operations either side of the matvec ---------------------------
+ * spq4k_rms_norm         : ggml_mul(ggml_rms_norm(x, eps), w) over T rows of K
+ *                          (ggml-cpu/ops.cpp:3724-3784): y = x * s * w with
+ *                          s = 1 / sqrtf(mean + eps), mean = (float)(sum of
+ *                          the fp32 squares in double / K). Bit-exact but for
+ *                          the double sum's order (a different mean needs the
+ *                          sum within ~2^-40 of a float rounding boundary).
+ * spq4k_mul_mat_rms_norm : y_i = W_i . rms_norm(x) * norm_w for n <= 4
+ *                          matrices sharing the input (the attention and FFN
+ *                          pre-norms, forward.cpp:1693-1696): at T = 1 one
+ *                          launch, the norm in the matvec's prologue;
+ *                          otherwise the norm pass, then spq4k_mul_mat's path.
+ * spq4k_mul_mat_swiglu   : y = silu(Wg . xb) * (Wu . xb), xb = x, or
+ *                          rms_norm(x) * norm_w when norm_w is not NULL (the
+ *                          dense SwiGLU front half, forward.cpp:1703-1706;
+ *                          ggml-cuda fuses the same gate in mmvq.cu:437-470):
+ *                          at T = 1 one launch (gate row and up row side by
+ *                          side, SiLU and the product in the epilogue);
+ *                          otherwise gate and up, then one element-wise pass.
+ *                          Wg and Wu share type, K and M; y is [T][M].
+ * Device pointers; x, norm_w 16-byte aligned; eps >= 0. */
+int spq4k_rms_norm(spq4k_ctx *ctx, const float *x, const float *w, float eps, float *y, int64_t K, int64_t T);
+/* y = silu(g) * u over n values (ggml_silu then ggml_mul; ggml_swiglu_split's
+ * ggml_vec_swiglu_f32, ggml-cpu/vec.cpp:433): the unfused epilogue */
+int spq4k_swiglu(spq4k_ctx *ctx, const float *g, const float *u, float *y, int64_t n);
+int spq4k_mul_mat_rms_norm(spq4k_ctx *ctx, int n, const spq4k_weights *const *W, const float *x,
+                           const float *norm_w, float eps, float *const *y, int64_t T);
+int spq4k_mul_mat_swiglu(spq4k_ctx *ctx, const spq4k_weights *Wg, const spq4k_weights *Wu, const float *x,
+                         const float *norm_w, float eps, float *y, int64_t T);
+
 int spq4k_mul_mat_host(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
 int spq4k_moe_host(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int64_t n_used,
                    int64_t ne11, int64_t T, const float *X, float *Y);

@@ -159,6 +159,10 @@ int or_mul_mat_dequant_f64_type(int type, const void *W, int64_t M, int64_t K, c
 void or_synth_fill(float *out, int64_t n, uint64_t seed, int dist, int64_t cols,
                    float mean, float std, float outlier_mult, int64_t offset);
 
+/* fused neighbours of the matvec (fusion_oracle.c) */
+void or_rms_norm(const float *x, int64_t K, int64_t T, const float *w, float eps, float *y);
+void or_swiglu(const float *g, const float *u, int64_t n, float *y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -205,3 +205,93 @@ int ref_graph_run(void *h, int iters, double *secs) {
     }
     return 0;
 }
+
+/* ---- the operations fused around the matvec ------------------------------ */
+/* owned intermediate buffers of a graph (freed with it) */
+typedef struct {
+    ref_graph g;
+    void *bufs[8];
+    int nbufs;
+} ref_graph_b;
+
+static float *graph_buf(ref_graph_b *gb, size_t n) {
+    float *p = (float *)malloc(n * sizeof(float));
+    gb->bufs[gb->nbufs++] = p;
+    return p;
+}
+
+void ref_graph_b_destroy(void *h) {
+    ref_graph_b *gb = (ref_graph_b *)h;
+    if (!gb) return;
+    for (int i = 0; i < gb->nbufs; ++i) free(gb->bufs[i]);
+    if (gb->g.tp) ggml_threadpool_free(gb->g.tp);
+    free(gb->g.work);
+    ggml_free(gb->g.ctx);
+    free(gb);
+}
+
+static ref_graph_b *graph_b_begin(int n_nodes) {
+    ref_graph *g = graph_begin(n_nodes);
+    ref_graph_b *gb = (ref_graph_b *)calloc(1, sizeof(ref_graph_b));
+    gb->g = *g;
+    free(g);
+    return gb;
+}
+
+/* Xn[T][K] = ggml_mul(ggml_rms_norm(X, eps), w) */
+void *ref_rms_norm_create(const float *X, int64_t K, int64_t T, const float *w, float eps, float *Xn,
+                          int nthreads) {
+    ref_graph_b *gb = graph_b_begin(2);
+    struct ggml_context *c = gb->g.ctx;
+    struct ggml_tensor *x = ggml_new_tensor_2d(c, GGML_TYPE_F32, K, T);
+    struct ggml_tensor *wt = ggml_new_tensor_1d(c, GGML_TYPE_F32, K);
+    x->data = (void *)X;
+    wt->data = (void *)w;
+    struct ggml_tensor *n = ggml_rms_norm(c, x, eps);
+    n->data = graph_buf(gb, (size_t)K * T);
+    struct ggml_tensor *m = ggml_mul(c, n, wt);
+    m->data = Xn;
+    ggml_build_forward_expand(gb->g.gf, m);
+    if (graph_finish(&gb->g, nthreads) != 0) { ref_graph_b_destroy(gb); return NULL; }
+    return gb;
+}
+
+/* The dense SwiGLU front half of forward.cpp:1693-1706: xb = x, or
+ * ggml_mul(ggml_rms_norm(x, eps), w) when w is given; Y[T][M] =
+ * ggml_mul(ggml_silu(mul_mat(Wg, xb)), mul_mat(Wu, xb)). */
+void *ref_swiglu_create(int type, const void *Wg, const void *Wu, int64_t M, int64_t K, const float *X, int64_t T,
+                        const float *w, float eps, float *Y, int nthreads) {
+    ref_graph_b *gb = graph_b_begin(6);
+    struct ggml_context *c = gb->g.ctx;
+    struct ggml_tensor *x = ggml_new_tensor_2d(c, GGML_TYPE_F32, K, T);
+    x->data = (void *)X;
+    struct ggml_tensor *xb = x;
+    if (w) {
+        struct ggml_tensor *wt = ggml_new_tensor_1d(c, GGML_TYPE_F32, K);
+        wt->data = (void *)w;
+        struct ggml_tensor *n = ggml_rms_norm(c, x, eps);
+        n->data = graph_buf(gb, (size_t)K * T);
+        xb = ggml_mul(c, n, wt);
+        xb->data = graph_buf(gb, (size_t)K * T);
+    }
+    struct ggml_tensor *wg = ggml_new_tensor_2d(c, (enum ggml_type)type, K, M);
+    struct ggml_tensor *wu = ggml_new_tensor_2d(c, (enum ggml_type)type, K, M);
+    wg->data = (void *)Wg;
+    wu->data = (void *)Wu;
+    struct ggml_tensor *g = ggml_mul_mat(c, wg, xb);
+    g->data = graph_buf(gb, (size_t)M * T);
+    struct ggml_tensor *u = ggml_mul_mat(c, wu, xb);
+    u->data = graph_buf(gb, (size_t)M * T);
+    struct ggml_tensor *s = ggml_silu(c, g);
+    s->data = graph_buf(gb, (size_t)M * T);
+    struct ggml_tensor *y = ggml_mul(c, s, u);
+    y->data = Y;
+    ggml_build_forward_expand(gb->g.gf, y);
+    if (graph_finish(&gb->g, nthreads) != 0) { ref_graph_b_destroy(gb); return NULL; }
+    return gb;
+}
+
+int ref_graph_b_run(void *h) {
+    ref_graph_b *gb = (ref_graph_b *)h;
+    return ggml_graph_compute(gb->g.gf, &gb->g.plan) == GGML_STATUS_SUCCESS ? 0 : -1;
+}

@@ -28,6 +28,9 @@ struct spq4k_ctx {
     // generic device scratch (Q8_K activations, routing tables)
     uint8_t* scratch = nullptr;
     size_t scratch_cap = 0;
+    // intermediates of the fused entry points (normalised rows, gate / up outputs)
+    uint8_t* scratch2 = nullptr;
+    size_t scratch2_cap = 0;
     int force_bpr = 0;           // tuning override (SPQ4K_GEMV_BPR = 1, 2, 4 or 8)
     int preq_mode = 0;           // SPQ4K_GEMV_PREQ: 0 auto, 1 always, 2 never
     int gemv_mfma_min_t = 4;     // SPQ4K_GEMV_MFMA_MIN_T: batches of at least this many tokens use matrix cores
@@ -120,6 +123,20 @@ int ensure_scratch(spq4k_ctx* c, size_t bytes) {
     return 0;
 }
 
+int ensure_scratch2(spq4k_ctx* c, size_t bytes) {
+    if (bytes <= c->scratch2_cap) return 0;
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    if (c->scratch2) (void)hipFree(c->scratch2);
+    c->scratch2 = nullptr;
+    c->scratch2_cap = 0;
+    if (hipMalloc(&c->scratch2, bytes) != hipSuccess) {
+        c->scratch2 = nullptr;
+        return set_err(c, -ENOMEM, "scratch of %zu bytes", bytes);
+    }
+    c->scratch2_cap = bytes;
+    return 0;
+}
+
 int check_shape(spq4k_ctx* c, int64_t M, int64_t K, int64_t E, int64_t qk = SPQ4K_QK_K) {
     if (M <= 0 || K <= 0 || E <= 0) return set_err(c, -EINVAL, "non-positive shape M=%lld K=%lld E=%lld",
                                                    (long long)M, (long long)K, (long long)E);
@@ -181,7 +198,7 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
 //                            otherwise queue behind the CU's weight loads
 //   K = 27648              : 8 waves (the registers of 7 Q8_K blocks a lane), x-first
 DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb, int64_t rows) {
-    DecodeCfg d;
+    DecodeCfg d{};
     if (nb > 48) {
         d.waves = 8; d.depth = 1; d.xfirst = true;
     } else if (nb >= 48) {
@@ -219,6 +236,16 @@ DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb, int64_t rows) {
 
 int gemm_segments(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T,
                   int mode);
+
+// A fusion asked of gemv_launch: the decode kernel's RMS-norm prologue
+// (norm_w) and / or its gate-up SiLU epilogue (glu: W[0] gate, W[1] up, y[0]
+// the output). gemv_launch returns 1 when the fused kernel does not apply
+// (the caller then runs the unfused steps).
+struct Fuse {
+    const float* norm_w = nullptr;
+    float eps = 0.0f;
+    bool glu = false;
+};
 
 // ---- Q8_0 planning ------------------------------------------------------------
 // Q8_0 planes of `rows` activation rows in the context scratch: values
@@ -309,7 +336,8 @@ int q80_dense(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X
     return 0;
 }
 
-int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* x, float* const* y, int64_t T) {
+int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* x, float* const* y, int64_t T,
+                const Fuse* fuse = nullptr) {
     if (n < 1 || n > GEMV_MAX_SEG) return set_err(c, -EINVAL, "gemv: n=%d matrices (1..4)", n);
     if (T < 1 || T > SPQ4K_GEMV_MAX_T) return set_err(c, -EINVAL, "gemv: T=%lld (1..8)", (long long)T);
     if (!x || !aligned(x, 16)) return set_err(c, -EINVAL, "gemv: x null or not 16-byte aligned");
@@ -324,6 +352,7 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         if (W[i]->device != c->device) return set_err(c, -EINVAL, "gemv: weights live on another device");
         Ms[i] = W[i]->M;
     }
+    if (fuse && (W[0]->fmt == WF_Q80 || T != 1)) return 1;
     if (W[0]->fmt == WF_Q80) return q80_dense(c, n, W, x, y, T);
     const int bpr = pick_bpr(c, Ms, n);
     const int rows = gemv_rows_per_tile(bpr);
@@ -351,6 +380,29 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         p.seg[i] = p.seg[0];
         p.seg[i].row_begin = INT32_MAX;
         p.seg[i].tile_begin = INT32_MAX;
+    }
+    if (fuse) {
+        if (c->no_decode || !decode_supported(p.fmt, p.nb)) return 1;
+        DecodeCfg dc = plan_decode(c, p.fmt, p.nb, fuse->glu ? W[0]->M : total);
+        dc.norm = fuse->norm_w != nullptr;
+        dc.glu = fuse->glu;
+        dc.xfirst = true;
+        if (dc.glu) {
+            dc.depth = 2;
+            if (!c->dec_force.waves)
+                for (int w : {16, 12, 8}) {
+                    dc.waves = w;
+                    if (decode_fused_supported(p.fmt, p.nb, dc)) break;
+                }
+            const int64_t wgs = (W[0]->M + dc.waves - 1) / dc.waves;
+            dc.grid = c->dec_force.grid ? c->dec_force.grid : (int)(wgs < c->num_cus ? wgs : c->num_cus);
+        }
+        if (!decode_fused_supported(p.fmt, p.nb, dc)) return 1;
+        p.norm_w = fuse->norm_w;
+        p.eps = fuse->eps;
+        hipError_t e = launch_gemv_decode(p, dc, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemv decode (fused) launch");
+        return 0;
     }
     if (T == 1 && !c->no_decode && c->preq_mode != 1 && decode_supported(p.fmt, p.nb)) {
         const DecodeCfg dc = plan_decode(c, p.fmt, p.nb, total);
@@ -515,6 +567,7 @@ void spq4k_free(spq4k_ctx* c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->scratch) (void)hipFree(c->scratch);
+    if (c->scratch2) (void)hipFree(c->scratch2);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }
@@ -1102,6 +1155,120 @@ int q80_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t
 }
 
 }  // namespace
+
+// ---- the operations fused around the matvec -------------------------------------
+int spq4k_rms_norm(spq4k_ctx* c, const float* x, const float* w, float eps, float* y, int64_t K, int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!x || !w || !y || K <= 0 || K > (1 << 30) || T < 1 || T > (1 << 24) || !(eps >= 0.0f) || !aligned(x, 4) ||
+        !aligned(y, 4) || !aligned(w, 4))
+        return set_err(c, -EINVAL, "rms_norm: bad arguments");
+    hipError_t e = launch_rms_norm(x, K, (int)T, (int)K, w, eps, y, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "rms_norm launch");
+    return 0;
+}
+
+int spq4k_swiglu(spq4k_ctx* c, const float* g, const float* u, float* y, int64_t n) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!g || !u || !y || n < 0 || !aligned(g, 4) || !aligned(u, 4) || !aligned(y, 4))
+        return set_err(c, -EINVAL, "swiglu: bad arguments");
+    hipError_t e = launch_swiglu(g, u, y, n, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "swiglu launch");
+    return 0;
+}
+
+namespace {
+
+// matmul of n matrices sharing X, any T (spq4k_mul_mat's dispatch)
+int mul_mat_n(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T) {
+    if (T <= SPQ4K_GEMV_MAX_T) return gemv_launch(c, n, W, X, Y, T);
+    return gemm_segments(c, n, W, X, Y, T, c->gemm_mode);
+}
+
+int check_fused_args(spq4k_ctx* c, const char* what, int n, const spq4k_weights* const* W, const float* x,
+                     const float* norm_w, float eps, int64_t T) {
+    if (!W || n < 1 || n > GEMV_MAX_SEG || !W[0]) return set_err(c, -EINVAL, "%s: bad matrices", what);
+    if (!x || !aligned(x, 16) || T < 1 || T > (1 << 20)) return set_err(c, -EINVAL, "%s: bad activations", what);
+    if (norm_w && (!aligned(norm_w, 16) || !(eps >= 0.0f))) return set_err(c, -EINVAL, "%s: bad norm weights", what);
+    for (int i = 0; i < n; ++i) {
+        if (!W[i] || !W[i]->data || W[i]->E != 1 || W[i]->K != W[0]->K || W[i]->type != W[0]->type)
+            return set_err(c, -EINVAL, "%s: matrices must be non-null, E = 1, and share K and type", what);
+        if (!aligned(W[i]->data, type_align(W[i]->type))) return set_err(c, -EINVAL, "%s: misaligned weights", what);
+        if (W[i]->device != c->device) return set_err(c, -EINVAL, "%s: weights live on another device", what);
+    }
+    return 0;
+}
+
+}  // namespace
+
+int spq4k_mul_mat_rms_norm(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* x, const float* norm_w,
+                           float eps, float* const* y, int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!norm_w) return set_err(c, -EINVAL, "mul_mat_rms_norm: null norm weights");
+    rc = check_fused_args(c, "mul_mat_rms_norm", n, W, x, norm_w, eps, T);
+    if (rc) return rc;
+    if (!y) return set_err(c, -EINVAL, "mul_mat_rms_norm: null outputs");
+    for (int i = 0; i < n; ++i)
+        if (!y[i]) return set_err(c, -EINVAL, "mul_mat_rms_norm: null output");
+    if (T == 1) {
+        Fuse f;
+        f.norm_w = norm_w;
+        f.eps = eps;
+        rc = gemv_launch(c, n, W, x, y, T, &f);
+        if (rc <= 0) return rc;
+    }
+    // unfused: the normalised rows, then the matmul on them
+    const int64_t K = W[0]->K;
+    rc = ensure_scratch2(c, (size_t)T * K * sizeof(float));
+    if (rc) return rc;
+    float* xn = reinterpret_cast<float*>(c->scratch2);
+    hipError_t e = launch_rms_norm(x, K, (int)T, (int)K, norm_w, eps, xn, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "rms_norm launch");
+    return mul_mat_n(c, n, W, xn, y, T);
+}
+
+int spq4k_mul_mat_swiglu(spq4k_ctx* c, const spq4k_weights* Wg, const spq4k_weights* Wu, const float* x,
+                         const float* norm_w, float eps, float* y, int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    const spq4k_weights* W[2] = {Wg, Wu};
+    rc = check_fused_args(c, "mul_mat_swiglu", 2, W, x, norm_w, eps, T);
+    if (rc) return rc;
+    if (!y || Wg->M != Wu->M) return set_err(c, -EINVAL, "mul_mat_swiglu: null output or gate / up rows differ");
+    if (T == 1) {
+        Fuse f;
+        f.norm_w = norm_w;
+        f.eps = eps;
+        f.glu = true;
+        float* ys[2] = {y, y};
+        rc = gemv_launch(c, 2, W, x, ys, T, &f);
+        if (rc <= 0) return rc;
+    }
+    // unfused: [normalised rows], gate and up, then silu(gate) * up
+    const int64_t K = Wg->K, M = Wg->M;
+    const size_t xb = norm_w ? (((size_t)T * K * sizeof(float) + 255) & ~(size_t)255) : 0;
+    const size_t gb = (((size_t)T * M * sizeof(float)) + 255) & ~(size_t)255;
+    rc = ensure_scratch2(c, xb + 2 * gb);
+    if (rc) return rc;
+    const float* xin = x;
+    hipError_t e;
+    if (norm_w) {
+        float* xn = reinterpret_cast<float*>(c->scratch2);
+        e = launch_rms_norm(x, K, (int)T, (int)K, norm_w, eps, xn, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "rms_norm launch");
+        xin = xn;
+    }
+    float* G = reinterpret_cast<float*>(c->scratch2 + xb);
+    float* U = reinterpret_cast<float*>(c->scratch2 + xb + gb);
+    float* gu[2] = {G, U};
+    rc = mul_mat_n(c, 2, W, xin, gu, T);
+    if (rc) return rc;
+    e = launch_swiglu(G, U, y, T * M, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "swiglu launch");
+    return 0;
+}
 
 int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t n_used, int64_t ne11,
               int64_t T, const float* X, float* Y) {

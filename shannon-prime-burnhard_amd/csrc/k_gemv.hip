@@ -91,6 +91,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
     }
 }
 
+// Sum of squares of the lane's 16 x values in double (ggml_float), as the
+// CPU's rms_norm accumulates them (ops.cpp:3757-3761: each square rounded to
+// fp32, then added in double).
+__device__ __forceinline__ double sumsq16(const XRegs& r) {
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s += (double)(r.x[j] * r.x[j]);
+    return s;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// silu(x) = x / (1 + e^-x) (ggml_silu_f32, ggml-cpu/vec.h:1064-1066)
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
 // T = 1 decode kernel. One wave per output row: lane (bsub, l4) = (lane >> 2,
 // lane & 3) takes quarter l4 of blocks bsub, bsub + 16, ... of the row, so the
 // Q8_K data those quarters need is loaded into registers once and reused for
@@ -101,8 +120,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
 // with D rows of loads in flight. With XFW the quantising waves fetch and
 // quantise x before issuing their own weight loads, so that x is not queued
 // behind the weight requests of the whole CU.
-template <typename Fmt, int NB, int WAVES, int D, bool XFW>
+// NORM: x is RMS-normalised and multiplied by p.norm_w before quantisation
+// (ggml_rms_norm + ggml_mul, ggml-cpu/ops.cpp:3724-3784): the quantising
+// waves reduce the sum of squares in double across the workgroup (one more
+// barrier), then scale their values as (x * s) * w.
+// GLU (D = 2): segments 0 and 1 are the gate and up matrices of equal M; wave
+// g takes rows g, g + G, ... of both (the two rows in flight are gate r and
+// up r) and stores silu(gate r . x) * (up r . x) to segment 0's output
+// (ggml_silu + ggml_mul, forward.cpp:1703-1706).
+template <typename Fmt, int NB, int WAVES, int D, bool XFW, bool NORM, bool GLU>
 __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
+    static_assert(!GLU || D == 2, "the fused gate/up pair is the two rows in flight");
     using W = typename Fmt::W;
     constexpr int NIT = (NB + 15) / 16;           // blocks per lane per row
     constexpr int QW = (NB + 3) / 4;              // quantising waves
@@ -113,7 +141,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l4 = lane & 3;
     const int bsub = lane >> 2;
-    const int Mtot = p.total_rows;
+    const int Mtot = GLU ? p.seg[0].M : p.total_rows;   // logical rows
     const int G = gridDim.x * WAVES;
     const int g = blockIdx.x * WAVES + wave;
     const int nrows = g < Mtot ? (Mtot - 1 - g) / G + 1 : 0;
@@ -158,9 +186,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
             b[it] = Fmt::load(wr + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
         }
     };
+    // GLU: row r of gate (which = 0) or up (which = 1)
+    auto load_glu = [&](int i, int which, W (&b)[NIT]) {
+        const int r0 = g + i * G;
+        const int r = r0 < Mtot ? r0 : Mtot - 1;
+        const uint8_t* wr = (which ? W1 : W0) + (size_t)r * ROWB;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int bb = bsub + 16 * it;
+            b[it] = Fmt::load(wr + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
+        }
+    };
 
     // activations: quantising waves load x first
     XRegs xr[PASSES];
+    XRegs nw[NORM ? PASSES : 1];
     int xb[PASSES];
     bool xv[PASSES];
 #pragma unroll
@@ -170,8 +210,31 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
         xv[ps] = qw < QW && item < NB;
         xb[ps] = item < NB ? item : NB - 1;
         if (qw < QW) xr[ps] = load_x16(p.X, 0, 0, xb[ps]);
+        if (NORM && qw < QW) nw[NORM ? ps : 0] = load_x16(p.norm_w, 0, 0, xb[ps]);
     }
     const Q8Lds L = q8lds_carve(q8s, NB);
+    if (NORM) {
+        // sum of squares of x over the workgroup, in double; every wave adds
+        // the WAVES partials in the same order, so all get the same scale
+        __shared__ double ssq[WAVES];
+        double s = 0.0;
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps)
+            if (ps * WAVES + wave < QW && xv[ps]) s += sumsq16(xr[ps]);
+        s = wave_sum_f64(s);
+        if (lane == 0) ssq[wave] = s;
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        double S = 0.0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) S += ssq[w];
+        const float mean = (float)(S / (double)(NB * QK));
+        const float scale = 1.0f / sqrtf(mean + p.eps);
+#pragma unroll
+        for (int ps = 0; ps < PASSES; ++ps)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) xr[ps].x[j] = xr[ps].x[j] * scale * nw[NORM ? ps : 0].x[j];
+    }
     auto quantise = [&]() {
 #pragma unroll
         for (int ps = 0; ps < PASSES; ++ps) {
@@ -182,8 +245,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
         quantise();
         __builtin_amdgcn_sched_barrier(0);
     }
+    if (GLU) {
+        load_glu(0, 0, buf[0]);
+        load_glu(0, 1, buf[D - 1]);
+    } else {
 #pragma unroll
-    for (int u = 0; u < D; ++u) load_row(u, buf[u]);
+        for (int u = 0; u < D; ++u) load_row(u, buf[u]);
+    }
     if (!XFW) quantise();
     // all quantised blocks visible (LDS writes only: weight loads stay in flight)
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
@@ -194,6 +262,27 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     for (int it = 0; it < NIT; ++it) {
         const int bb = bsub + 16 * it;
         Fmt::load_reg(L, bb < NB ? bb : NB - 1, l4, qr[it]);
+    }
+    if (GLU) {
+        for (int i = 0; i < nrows; ++i) {
+            float a2[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) {
+                    const float a = Fmt::dot_reg(buf[u * (D - 1)][it], l4, qr[it], acc);
+                    acc = (bsub + 16 * it < NB) ? a : acc;
+                }
+                a2[u] = group_sum_last<64>(acc);
+            }
+            if (lane == 63) Y0[g + i * G] = silu_f32(a2[0]) * a2[1];
+            if (i + 1 < nrows) {
+                load_glu(i + 1, 0, buf[0]);
+                load_glu(i + 1, 1, buf[D - 1]);
+            }
+        }
+        return;
     }
     for (int i0 = 0; i0 < nrows; i0 += D) {
 #pragma unroll
@@ -215,6 +304,46 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
             }
         }
     }
+}
+
+// RMS norm of T rows (one workgroup of 256 threads a row): the squares
+// (fp32) summed in double by a fixed tree, mean = (float)(sum / K),
+// s = 1 / sqrtf(mean + eps), y = (x * s) * w (ggml-cpu/ops.cpp:3757-3779).
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, int64_t x_tstride, int K,
+                                                       const float* __restrict__ w, float eps,
+                                                       float* __restrict__ y) {
+    __shared__ double part[4];
+    const int t = blockIdx.x;
+    const float* xr = x + (int64_t)t * x_tstride;
+    double s = 0.0;
+    for (int k = threadIdx.x; k < K; k += 256) s += (double)(xr[k] * xr[k]);
+    s = wave_sum_f64(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const double S = ((part[0] + part[1]) + part[2]) + part[3];
+    const float mean = (float)(S / (double)K);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    float* yr = y + (int64_t)t * K;
+    for (int k = threadIdx.x; k < K; k += 256) yr[k] = xr[k] * scale * w[k];
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                     float* __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) y[i] = silu_f32(g[i]) * u[i];
+}
+
+hipError_t launch_rms_norm(const float* x, int64_t x_tstride, int T, int K, const float* w, float eps, float* y,
+                           hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(T), dim3(256), 0, st, x, x_tstride, K, w, eps, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float* g, const float* u, float* y, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, y, n);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -275,9 +404,10 @@ static hipError_t launch_t(const GemvParams& p, int bpr, int ntiles, hipStream_t
 
 int gemv_rows_per_tile(int bpr) { return 4 * (64 / (4 * bpr)); }
 
-template <typename Fmt, int NB, int WAVES, int D, bool XFW>
+template <typename Fmt, int NB, int WAVES, int D, bool XFW, bool NORM = false, bool GLU = false>
 static hipError_t launch_dec(const GemvParams& p, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_decode_kernel<Fmt, NB, WAVES, D, XFW>), dim3(grid), dim3(WAVES * 64), 0, st, p);
+    hipLaunchKernelGGL((gemv_decode_kernel<Fmt, NB, WAVES, D, XFW, NORM, GLU>), dim3(grid), dim3(WAVES * 64), 0, st,
+                       p);
     return hipGetLastError();
 }
 
@@ -298,6 +428,20 @@ constexpr bool dec_shape_ok_fmt(int nb, int waves, int depth) {
 
 template <typename Fmt, int NB>
 static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
+    if (c.glu || c.norm) {
+        // the fused forms run x first; the gate/up pair is the two rows in flight
+        if (!c.xfirst || (c.glu && c.depth != 2)) return hipErrorInvalidValue;
+#define SPQ_DECF(W, DD)                                                                             \
+        if constexpr (dec_shape_ok_fmt<Fmt>(NB, W, DD))                                             \
+            if (c.waves == W && c.depth == DD) {                                                     \
+                if (c.glu && c.norm) return launch_dec<Fmt, NB, W, DD, true, true, DD == 2>(p, c.grid, st); \
+                if (c.glu) return launch_dec<Fmt, NB, W, DD, true, false, DD == 2>(p, c.grid, st);  \
+                return launch_dec<Fmt, NB, W, DD, true, true, false>(p, c.grid, st);                \
+            }
+        SPQ_DECF(16, 1) SPQ_DECF(16, 2) SPQ_DECF(12, 1) SPQ_DECF(12, 2) SPQ_DECF(8, 1) SPQ_DECF(8, 2)
+#undef SPQ_DECF
+        return hipErrorInvalidValue;
+    }
 #define SPQ_DEC(W, DD, X)                                                                  \
     if constexpr (dec_shape_ok_fmt<Fmt>(NB, W, DD))                                        \
         if (c.waves == W && c.depth == DD && c.xfirst == X) return launch_dec<Fmt, NB, W, DD, X>(p, c.grid, st);
@@ -306,6 +450,26 @@ static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStre
     SPQ_DEC(8, 1, false) SPQ_DEC(8, 1, true) SPQ_DEC(8, 2, false) SPQ_DEC(8, 2, true)
 #undef SPQ_DEC
     return hipErrorInvalidValue;
+}
+
+template <typename Fmt>
+static bool dec_fused_ok(int nb, const DecodeCfg& c) {
+    if (!c.xfirst || (c.glu && c.depth != 2)) return false;
+    auto ok = [&](int n) {
+        for (int w : {16, 12, 8})
+            for (int d : {1, 2})
+                if (c.waves == w && c.depth == d) return dec_shape_ok_fmt<Fmt>(n, w, d);
+        return false;
+    };
+    return ok(nb);
+}
+
+bool decode_fused_supported(int fmt, int nb, const DecodeCfg& c) {
+    if (!decode_supported(fmt, nb)) return false;
+    if (fmt == WF_Q6K) return dec_fused_ok<FmtQ6K>(nb, c);
+    if (fmt == WF_Q5K) return dec_fused_ok<FmtQ5K>(nb, c);
+    if (fmt == WF_Q4K) return dec_fused_ok<FmtQ4K>(nb, c);
+    return false;
 }
 
 // Q4_K: K = 4096, 5120, 12288, 27648, the dense shapes of the 8B model and of

@@ -38,6 +38,9 @@ struct GemvParams {
     int32_t chunk_blocks; // blocks staged in LDS at a time
     int32_t total_rows;   // sum of the segments' M
     int32_t fmt;          // WFmt of every segment
+    // fusions of the T = 1 decode kernel (DecodeCfg.norm / .glu)
+    const float* norm_w;  // x -> (x * 1/sqrt(mean(x^2) + eps)) * norm_w before quantisation
+    float eps;
 };
 
 // Launch shape of the T = 1 decode kernel (gemv_decode_kernel).
@@ -46,6 +49,8 @@ struct DecodeCfg {
     int depth;    // rows of loads in flight per wave: 1 or 2
     bool xfirst;  // quantising waves fetch and quantise x before their weight loads
     int grid;     // workgroups
+    bool norm;    // RMS-normalise x (p.norm_w, p.eps) before quantising it (xfirst)
+    bool glu;     // segments 0 and 1 are gate and up: y0 = silu(gate . x) * (up . x) (depth 2, xfirst)
 };
 
 // rows per workgroup for a lanes-per-row choice of 4*bpr (bpr in 1, 2, 4, 8)
@@ -53,6 +58,14 @@ int gemv_rows_per_tile(int bpr);
 hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st);
 bool decode_supported(int fmt, int nb);
 hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st);
+// whether the decode kernel has the fused form c (norm / glu) for this format and row length
+bool decode_fused_supported(int fmt, int nb, const DecodeCfg& c);
+// ggml_rms_norm then ggml_mul by w (ggml-cpu/ops.cpp:3724-3784): y[t] = (x[t] * s_t) * w,
+// s_t = 1 / sqrt(mean(x[t]^2) + eps), one workgroup a row
+hipError_t launch_rms_norm(const float* x, int64_t x_tstride, int T, int K, const float* w, float eps, float* y,
+                           hipStream_t st);
+// y = silu(g) * u element-wise (ggml_silu then ggml_mul, ggml_vec_swiglu_f32)
+hipError_t launch_swiglu(const float* g, const float* u, float* y, int64_t n, hipStream_t st);
 hipError_t launch_subblock_sums(const uint8_t* W, int M, int nb, const float* X, int32_t* S, hipStream_t st);
 
 // expert-gathered matvec (k_moe.hip)

@@ -145,6 +145,10 @@ def load_library(path: str | None = None):
         "spq4k_model_n_tensors": (I64, [V]),
         "spq4k_model_tensor_name": (C.c_char_p, [V, I64]),
         "spq4k_model_nbytes": (S, [V]),
+        "spq4k_rms_norm": (I, [V, V, V, F, V, I64, I64]),
+        "spq4k_swiglu": (I, [V, V, V, V, I64]),
+        "spq4k_mul_mat_rms_norm": (I, [V, I, V, V, V, F, V, I64]),
+        "spq4k_mul_mat_swiglu": (I, [V, V, V, V, V, F, V, I64]),
         "spq4k_quantize_q8_0": (I, [V, V, V, I64]),
         "spq4k_vec_dot_q8_0": (I, [V, I, V, V, V]),
         "spq4k_quantize_q8_0_host": (I, [V, V, V, I64]),
@@ -516,6 +520,23 @@ class Context:
 
     def vec_dot_q8K_dev(self, type: int, n: int, s_dev: int, vx: int, vy: int):
         self._check("spq4k_vec_dot_q8K", self.lib.spq4k_vec_dot_q8K(self.handle, type, n, s_dev, vx, vy))
+
+    def rms_norm_dev(self, x: int, w: int, eps: float, y: int, K: int, T: int = 1):
+        self._check("spq4k_rms_norm", self.lib.spq4k_rms_norm(self.handle, x, w, eps, y, K, T))
+
+    def swiglu_dev(self, g: int, u: int, y: int, n: int):
+        self._check("spq4k_swiglu", self.lib.spq4k_swiglu(self.handle, g, u, y, n))
+
+    def mul_mat_rms_norm_dev(self, Ws, x_dev: int, norm_w_dev: int, eps: float, y_devs, T: int = 1):
+        n = len(Ws)
+        wa = (C.c_void_p * n)(*[w.handle.value if isinstance(w.handle, C.c_void_p) else w.handle for w in Ws])
+        ya = (C.c_void_p * n)(*y_devs)
+        self._check("spq4k_mul_mat_rms_norm",
+                    self.lib.spq4k_mul_mat_rms_norm(self.handle, n, wa, x_dev, norm_w_dev, eps, ya, T))
+
+    def mul_mat_swiglu_dev(self, Wg, Wu, x_dev: int, norm_w_dev, eps: float, y_dev: int, T: int = 1):
+        self._check("spq4k_mul_mat_swiglu",
+                    self.lib.spq4k_mul_mat_swiglu(self.handle, Wg.handle, Wu.handle, x_dev, norm_w_dev, eps, y_dev, T))
 
     def quantize_q8_0_dev(self, x: int, vy: int, k: int):
         self._check("spq4k_quantize_q8_0", self.lib.spq4k_quantize_q8_0(self.handle, x, vy, k))

@@ -50,6 +50,8 @@ class Oracle:
         L.or_mul_mat_id.restype = I
         L.or_mul_mat_dequant_f64.argtypes = [V, I64, I64, V, I64, V]
         L.or_synth_fill.argtypes = [V, I64, U64, I, I64, F, F, F, I64]
+        L.or_rms_norm.argtypes = [V, I64, I64, V, F, V]
+        L.or_swiglu.argtypes = [V, V, I64, V]
         L.or_fp16_to_fp32.argtypes = [C.c_uint16]
         L.or_fp16_to_fp32.restype = F
         L.or_fp32_to_fp16.argtypes = [F]
@@ -258,6 +260,23 @@ class Oracle:
         assert self.L.or_mul_mat_dequant_f64_type(qtype, _p(W), M, K, _p(X), X.shape[0], _p(Y)) == 0
         return Y
 
+    # ---- fused neighbours (oracle/fusion_oracle.c) ----
+    def rms_norm(self, X, w, eps) -> np.ndarray:
+        """ggml_mul(ggml_rms_norm(X, eps), w), rows of X."""
+        X = np.ascontiguousarray(X, np.float32)
+        K = X.shape[-1]
+        Y = np.empty_like(X)
+        self.L.or_rms_norm(_p(X), K, X.size // K, None if w is None else _p(np.ascontiguousarray(w, np.float32)),
+                           eps, _p(Y))
+        return Y
+
+    def swiglu(self, g, u) -> np.ndarray:
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        y = np.empty_like(g)
+        self.L.or_swiglu(_p(g), _p(u), g.size, _p(y))
+        return y
+
     def synth(self, n, seed, dist=0, cols=0, mean=0.0, std=1.0, mult=1.0, offset=0) -> np.ndarray:
         out = np.empty(n, np.float32)
         self.L.or_synth_fill(_p(out), n, seed, dist, cols, mean, std, mult, offset)
@@ -313,6 +332,13 @@ class Ref:
         L.ref_graph_run.argtypes = [V, I, V]
         L.ref_graph_run.restype = I
         L.ref_graph_destroy.argtypes = [V]
+        L.ref_rms_norm_create.argtypes = [V, I64, I64, V, F, V, I]
+        L.ref_rms_norm_create.restype = V
+        L.ref_swiglu_create.argtypes = [I, V, V, I64, I64, V, I64, V, F, V, I]
+        L.ref_swiglu_create.restype = V
+        L.ref_graph_b_run.argtypes = [V]
+        L.ref_graph_b_run.restype = I
+        L.ref_graph_b_destroy.argtypes = [V]
         self.L = L
         self.path = path
 
@@ -386,6 +412,41 @@ class Ref:
         finally:
             self.L.ref_graph_destroy(h)
         return Y
+
+
+def _ref_rms_norm(self, X, w, eps, nthreads=1):
+    X = np.ascontiguousarray(X, np.float32)
+    K = X.shape[-1]
+    Y = np.empty_like(X)
+    w = np.ascontiguousarray(w, np.float32)
+    h = self.L.ref_rms_norm_create(_p(X), K, X.size // K, _p(w), eps, _p(Y), nthreads)
+    assert h
+    try:
+        assert self.L.ref_graph_b_run(h) == 0
+    finally:
+        self.L.ref_graph_b_destroy(h)
+    return Y
+
+
+def _ref_swiglu_ffn(self, qtype, Wg, Wu, M, K, X, w=None, eps=1e-6, nthreads=1):
+    """silu(Wg . xb) * (Wu . xb), xb = X or rms_norm(X) * w, through a ggml graph."""
+    X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+    Y = np.empty((X.shape[0], M), np.float32)
+    wp = None if w is None else _p(np.ascontiguousarray(w, np.float32))
+    keep = None if w is None else np.ascontiguousarray(w, np.float32)
+    if keep is not None:
+        wp = _p(keep)
+    h = self.L.ref_swiglu_create(qtype, _p(Wg), _p(Wu), M, K, _p(X), X.shape[0], wp, eps, _p(Y), nthreads)
+    assert h
+    try:
+        assert self.L.ref_graph_b_run(h) == 0
+    finally:
+        self.L.ref_graph_b_destroy(h)
+    return Y
+
+
+Ref.rms_norm = _ref_rms_norm
+Ref.swiglu_ffn = _ref_swiglu_ffn
 
 
 def close_enough(a, b, rel=1e-4, abs_=1e-5):
