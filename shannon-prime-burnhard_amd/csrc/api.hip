@@ -98,7 +98,9 @@ int64_t type_block_values(int type) { return type == SPQ4K_TYPE_Q8_0 ? SPQ4K_QK8
 // alignment the kernels need of a block pointer of the type
 size_t type_align(int type) { return type == SPQ4K_TYPE_Q4_K || type == SPQ4K_TYPE_Q5_K ? 16 : 2; }
 // formats with a matrix-core kernel (the others run batches on the sdot4 kernels)
-bool fmt_has_mfma(int fmt) { return fmt == WF_Q4K || fmt == WF_Q6K; }
+bool fmt_has_mfma(int fmt) { return fmt == WF_Q4K || fmt == WF_Q6K || fmt == WF_Q5K; }
+// formats of the expert-gathered ring kernel (moe_ring_kernel)
+bool fmt_has_moe_ring(int fmt) { return fmt == WF_Q4K || fmt == WF_Q6K || fmt == WF_Q5K; }
 
 int use_device(spq4k_ctx* c) {
     if (!c) return -EINVAL;
@@ -410,9 +412,9 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
         if (e != hipSuccess) return hip_fail(c, e, "gemv decode launch");
         return 0;
     }
-    // SPQ4K_GEMM_MODE=1 keeps Q6_K batches on the sdot4 kernels (gemv_chunked)
+    // SPQ4K_GEMM_MODE=1 keeps Q6_K and Q5_K batches on the sdot4 kernels (gemv_chunked)
     if (T >= c->gemv_mfma_min_t && c->force_bpr == 0 && fmt_has_mfma(p.fmt) &&
-        !(p.fmt == WF_Q6K && c->gemm_mode == 1)) {
+        !(p.fmt != WF_Q4K && c->gemm_mode == 1)) {
         // 4 <= T <= 8: the sdot4 kernel's integer work grows with T while the
         // matrix cores' 16-token tile costs the same from T = 1 to 16
         return gemm_segments(c, n, W, x, y, T, c->gemm_mode == 1 ? 1 : 0);
@@ -1025,7 +1027,7 @@ int gemm_segments(spq4k_ctx* c, int n, const spq4k_weights* const* W, const floa
     p.fmt = W[0]->fmt;
     if (tiles16 * ((T + 15) / 16) > (1ll << 31) - 1 || rows > (1ll << 31) - 1)
         return set_err(c, -EINVAL, "gemm: grid too large");
-    if (!fmt_has_mfma(p.fmt) || (p.fmt == WF_Q6K && mode == 1)) {   // sdot4 kernels over 8-token slices
+    if (!fmt_has_mfma(p.fmt) || (p.fmt != WF_Q4K && mode == 1)) {   // sdot4 kernels over 8-token slices
         if (T <= SPQ4K_GEMV_MAX_T) return gemv_launch(c, n, W, X, Y, T);
         return gemv_chunked(c, n, W, X, Y, T);
     }
@@ -1369,10 +1371,11 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     p.route.act_cnt = rt + 1 + 2 * E;
     p.route.pairs = rt + 1 + 3 * E;
     // matrix cores unless the sdot4 kernels are asked for (SPQ4K_MOE_UNFUSED);
-    // a Q6_K bank's operand preparation costs more, so its experts go to the
-    // matrix cores only once they receive two pairs on average (measured on
-    // the 2048 x 768 down bank: T = 8 sdot4 31 us against 36, T = 32 65 against 61)
-    const bool ring = !c->moe_unfused && fmt_has_mfma(bank->fmt) && (bank->fmt == WF_Q4K || mean_pairs >= 2);
+    // a Q6_K or Q5_K bank's operand preparation costs more, so its experts go
+    // to the matrix cores only once they receive two pairs on average
+    // (measured on the Q6_K 2048 x 768 down bank: T = 8 sdot4 31 us against
+    // 36, T = 32 65 against 61)
+    const bool ring = !c->moe_unfused && fmt_has_moe_ring(bank->fmt) && (bank->fmt == WF_Q4K || mean_pairs >= 2);
     hipError_t e;
     if (!ring) {
         e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, mn, false, c->stream);

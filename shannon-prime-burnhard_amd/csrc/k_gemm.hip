@@ -338,12 +338,13 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 // are block bytes 0..207 and slot 13 re-reads bytes 194..209, so no load
 // leaves its 210-byte block; ring_block_q6, 16x16 tiles). Q6_K block starts
 // are 2-byte aligned; global loads on gfx950 take unaligned addresses.
+// 2 = Q5_K (11 slots of its 176-byte block; ring_block_q5, 16x16 tiles).
 template <int RT, int CT, int NW, int S, int TW = 16, int F = 0>
 __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
     static_assert(TW == 16 || TW == 32, "16x16 or 32x32 output tiles");
-    static_assert(F == 0 || TW == 16, "Q6_K runs on 16x16 tiles");
-    constexpr int WSL = F ? 14 : 9;                  // 16-byte slots of a row's block
-    constexpr int BB = F ? Q6K_BYTES : Q4K_BYTES;    // block bytes in memory
+    static_assert(F == 0 || TW == 16, "Q6_K and Q5_K run on 16x16 tiles");
+    constexpr int WSL = F == 1 ? 14 : F == 2 ? 11 : 9;                               // 16-byte slots of a row's block
+    constexpr int BB = F == 1 ? Q6K_BYTES : F == 2 ? Q5K_BYTES : Q4K_BYTES;          // block bytes in memory
     constexpr int ROWB = 16 * WSL;                   // bytes of a row in the stage
     constexpr int TOK = CT * TW;
     constexpr int ROWS = RT * TW * NW;
@@ -388,7 +389,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
         if (J < W_LOADS) {
             const int r = min(row0 + slot / WSL, M - 1);
             const int sub = slot % WSL;
-            src[i] = W + ((size_t)r * nb + kb0) * BB + (F && sub == 13 ? 194 : 16 * sub);
+            src[i] = W + ((size_t)r * nb + kb0) * BB + (F == 1 && sub == 13 ? 194 : 16 * sub);
             stride[i] = BB;
         } else if (J < W_LOADS + Q_LOADS) {
             const int sl = slot - W_LOADS * 64;
@@ -434,6 +435,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
 
         if constexpr (F == 1)
             ring_block_q6<RT, CT>(lds[buf] + (wave * RT * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+        else if constexpr (F == 2)
+            ring_block_q5<RT, CT>(lds[buf] + (wave * RT * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
         else if constexpr (TW == 16)
             ring_block<RT, CT>(lds[buf] + (wave * RT * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
         else
@@ -730,6 +733,12 @@ static const TiledShape kTiled[] = {
     {128, 32, true, launch_ring_<1, 2, 8, 3, 16, 1>, WF_Q6K},   // 16: T <= 32
     {256, 64, true, launch_ring_<2, 4, 8, 2, 16, 1>, WF_Q6K},   // 17: 8 waves, 2 stages of 80 KB
     {64, 64, true, launch_ring_<1, 4, 4, 3, 16, 1>, WF_Q6K},    // 18: 4 waves
+    // Q5_K (ring_block_q5)
+    {128, 64, true, launch_ring_<1, 4, 8, 3, 16, 2>, WF_Q5K},   // 19: 8 waves, 3 stages
+    {128, 16, true, launch_ring_<1, 1, 8, 3, 16, 2>, WF_Q5K},   // 20: T <= 16
+    {128, 32, true, launch_ring_<1, 2, 8, 3, 16, 2>, WF_Q5K},   // 21: T <= 32
+    {128, 64, true, launch_ring_<1, 4, 8, 2, 16, 2>, WF_Q5K},   // 22: 8 waves, 2 stages
+    {64, 64, true, launch_ring_<1, 4, 4, 3, 16, 2>, WF_Q5K},    // 23: 4 waves
 };
 constexpr int N_TILED = (int)(sizeof(kTiled) / sizeof(kTiled[0]));
 
@@ -747,6 +756,8 @@ GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
     if (cfg >= 0 && cfg < N_TILED && kTiled[cfg].fmt != p.fmt) cfg = -1;   // a shape of the other format
     if ((cfg < 0 || cfg >= N_TILED) && p.fmt == WF_Q6K) {
         cfg = p.T <= 16 ? 15 : (p.T <= 32 ? 16 : 14);
+    } else if ((cfg < 0 || cfg >= N_TILED) && p.fmt == WF_Q5K) {
+        cfg = p.T <= 16 ? 20 : (p.T <= 32 ? 21 : 19);
     } else if (cfg < 0 || cfg >= N_TILED) {
         if (p.T <= 16) {
             cfg = 6;

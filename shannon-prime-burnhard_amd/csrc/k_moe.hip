@@ -514,11 +514,13 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(const int32_t* __restrict
 }
 
 // F = 1: Q6_K banks (14 slots a row, the last re-reading block bytes
-// 194..209; ring_block_q6), as in gemm_ring_kernel.
+// 194..209; ring_block_q6); F = 2: Q5_K banks (11 slots, ring_block_q5); as
+// in gemm_ring_kernel.
 template <int S, int F = 0>
 __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
     constexpr int NW = 8, ROWS = 128, TOK = 16;
-    constexpr int WSL = F ? 14 : 9, BB = F ? Q6K_BYTES : Q4K_BYTES, ROWB = 16 * WSL;
+    constexpr int WSL = F == 1 ? 14 : F == 2 ? 11 : 9;
+    constexpr int BB = F == 1 ? Q6K_BYTES : F == 2 ? Q5K_BYTES : Q4K_BYTES, ROWB = 16 * WSL;
     constexpr int W_SLOTS = ROWS * WSL, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
     constexpr int W_LOADS = W_SLOTS / 64, Q_LOADS = (Q_SLOTS + 63) / 64, M_LOADS = (M_SLOTS + 63) / 64;
     constexpr int NLOAD = W_LOADS + Q_LOADS + M_LOADS;
@@ -561,7 +563,7 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
             if (J < W_LOADS) {
                 wrow[i] = slot / WSL;
                 const int sub = slot % WSL;
-                src[i] = W + (F && sub == 13 ? 194 : 16 * sub);
+                src[i] = W + (F == 1 && sub == 13 ? 194 : 16 * sub);
             } else if (J < NLOAD) {
                 const bool isq = J < W_LOADS + Q_LOADS;
                 const int sl = slot - (isq ? W_LOADS : W_LOADS + Q_LOADS) * 64;
@@ -601,6 +603,8 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
             issue(min(sp + S - 1, len - 1), (sp + S - 1) % S);
             if constexpr (F == 1)
                 ring_block_q6<1, 1>(lds[buf] + (wave * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+            else if constexpr (F == 2)
+                ring_block_q5<1, 1>(lds[buf] + (wave * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
             else
                 ring_block<1, 1>(lds[buf] + (wave * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
             if (sp - (sp / nb) * nb == nb - 1) {
@@ -626,7 +630,6 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
 
 hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, int E, const float* X,
                            int64_t x_tstride, int n_xrows, int max_act, hipStream_t st) {
-    if (p.fmt == WF_Q5K) return hipErrorInvalidValue;   // no matrix-core form
     const int64_t items = (int64_t)n_xrows * p.nb;
     hipLaunchKernelGGL(moe_prep_kernel, dim3((unsigned)(1 + (items + 15) / 16)), dim3(256), moe_route_lds_bytes(E), st,
                        ids, n_pairs, E, p.route, X, x_tstride, n_xrows, p.nb, p.Q);
@@ -635,6 +638,8 @@ hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, 
     const int64_t grid = (int64_t)max_act * p.tiles_per_expert;
     if (p.fmt == WF_Q6K)
         hipLaunchKernelGGL((moe_ring_kernel<3, 1>), dim3((unsigned)grid), dim3(512), 0, st, p);
+    else if (p.fmt == WF_Q5K)
+        hipLaunchKernelGGL((moe_ring_kernel<3, 2>), dim3((unsigned)grid), dim3(512), 0, st, p);
     else
         hipLaunchKernelGGL((moe_ring_kernel<3, 0>), dim3((unsigned)grid), dim3(512), 0, st, p);
     return hipGetLastError();

@@ -24,6 +24,7 @@
 #pragma once
 
 #include "gemv_core.h"
+#include "q5k_core.h"
 
 namespace spq4k {
 
@@ -349,6 +350,103 @@ __device__ __forceinline__ void ring_block_q6(const uint8_t* wt, const uint8_t* 
             for (int i = 0; i < 4; ++i) {
                 const int I = (ca[i] << 8) + cb[i];
                 acc[r][ct][i] = fmaf(dr[r][i] * d8, (float)I, acc[r][ct][i]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// One Q5_K super-block (176 bytes: d, dmin, the Q4_K scale/min packing,
+// qh[32] at 16, qs[128] at 48) x Q8_K activations on 16x16 tiles, with the
+// Q4_K lane mapping and the same permuted Q8_K stage. A weight value is
+// q5 = nibble + 16 * bit of qh (ggml_vec_dot_q5_K_q8_K,
+// ggml-cpu/arch/x86/quants.c:2078-2174): lane (c16, q) takes nibble group q
+// and bits 2q (low nibbles) and 2q + 1 (high nibbles) of the 32 qh bytes.
+// q5 reaches 31, so the 6-bit scale is split in three, sc = 16a + 4b + c with
+// a, b, c in 0..3: the int8 operands a*q5, b*q5, c*q5 (<= 93) feed three MFMA
+// chains A, B, C and I = sum_j sc_j S_j = 16A + 4B + C exactly; the min term
+// is Q4_K's (one f16 MFMA, exact).
+template <int RT, int CT>
+__device__ __forceinline__ void ring_block_q5(const uint8_t* wt, const uint8_t* qreg, const uint8_t* mreg, int c16,
+                                              int q, v4f (&acc)[RT][CT]) {
+    v4i aa[RT][4], ab[RT][4], ac[RT][4];
+    h4 am[RT];
+    float dr[RT][4], dmr[RT][4];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const uint8_t* wr = wt + (r * 16 + c16) * Q5K_BYTES;
+        const v4i hdr = *reinterpret_cast<const v4i*>(wr);
+        const v4i qh0 = *reinterpret_cast<const v4i*>(wr + 16);
+        const v4i qh1 = *reinterpret_cast<const v4i*>(wr + 32);
+        v4i wq[2];
+        wq[0] = *reinterpret_cast<const v4i*>(wr + 48 + 32 * q);
+        wq[1] = *reinterpret_cast<const v4i*>(wr + 64 + 32 * q);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t h = *reinterpret_cast<const uint32_t*>(wt + (r * 16 + 4 * q + i) * Q5K_BYTES);
+            dr[r][i] = half_bits_to_float(h & 0xFFFFu);
+            dmr[r][i] = half_bits_to_float(h >> 16);
+        }
+        const ScaleMin sm = unpack_scale_min((uint32_t)hdr.y, (uint32_t)hdr.z, (uint32_t)hdr.w);
+        const uint32_t sc01 = (q < 2 ? sm.sc_lo : sm.sc_hi) >> (16 * (q & 1));
+        const uint32_t s0 = sc01 & 63u, s1 = (sc01 >> 8) & 63u;
+        const uint32_t A0 = (s0 >> 4) * 0x10001u, B0 = ((s0 >> 2) & 3u) * 0x10001u, C0 = (s0 & 3u) * 0x10001u;
+        const uint32_t A1 = (s1 >> 4) * 0x10001u, B1 = ((s1 >> 2) & 3u) * 0x10001u, C1 = (s1 & 3u) * 0x10001u;
+        const uint32_t mw = (q & 1) ? sm.m_hi : sm.m_lo;
+        const uint32_t x01 = __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u);
+        const uint32_t x23 = __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u);
+        h2 a01, a23;
+        __builtin_memcpy(&a01, &x01, 4);
+        __builtin_memcpy(&a23, &x23, 4);
+        const _Float16 f = q < 2 ? (_Float16)32.0f : (_Float16)1.0f;
+        const _Float16 o = q < 2 ? (_Float16)-32768.0f : (_Float16)-1024.0f;
+        const h2 fv = {f, f}, ov = {o, o};
+        const h2 b01 = a01 * fv + ov, b23 = a23 * fv + ov;
+        am[r] = h4{b01.x, b01.y, b23.x, b23.y};
+        const uint32_t qh[8] = {(uint32_t)qh0.x, (uint32_t)qh0.y, (uint32_t)qh0.z, (uint32_t)qh0.w,
+                                (uint32_t)qh1.x, (uint32_t)qh1.y, (uint32_t)qh1.z, (uint32_t)qh1.w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint32_t w0 = (uint32_t)wq[s >> 1][2 * (s & 1)];
+            const uint32_t w1 = (uint32_t)wq[s >> 1][2 * (s & 1) + 1];
+            const uint32_t h0 = qh[2 * s], h1 = qh[2 * s + 1];
+            const uint32_t l0 = (w0 & 0x0F0F0F0Fu) | (((h0 >> (2 * q)) & 0x01010101u) << 4);
+            const uint32_t l1 = (w1 & 0x0F0F0F0Fu) | (((h1 >> (2 * q)) & 0x01010101u) << 4);
+            const uint32_t u0 = ((w0 >> 4) & 0x0F0F0F0Fu) | (((h0 >> (2 * q + 1)) & 0x01010101u) << 4);
+            const uint32_t u1 = ((w1 >> 4) & 0x0F0F0F0Fu) | (((h1 >> (2 * q + 1)) & 0x01010101u) << 4);
+            aa[r][s] = v4i{(int)pk_mul_u16(l0, A0), (int)pk_mul_u16(l1, A0), (int)pk_mul_u16(u0, A1),
+                           (int)pk_mul_u16(u1, A1)};
+            ab[r][s] = v4i{(int)pk_mul_u16(l0, B0), (int)pk_mul_u16(l1, B0), (int)pk_mul_u16(u0, B1),
+                           (int)pk_mul_u16(u1, B1)};
+            ac[r][s] = v4i{(int)pk_mul_u16(l0, C0), (int)pk_mul_u16(l1, C0), (int)pk_mul_u16(u0, C1),
+                           (int)pk_mul_u16(u1, C1)};
+        }
+    }
+    const uint8_t* qb = qreg + c16 * RING_QS + 64 * q;
+    const uint8_t* mb = mreg + c16 * Q8MN_BYTES;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+        v4i bq[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bq[s] = *reinterpret_cast<const v4i*>(qb + ct * 16 * RING_QS + 16 * s);
+        const h4 bm = *reinterpret_cast<const h4*>(mb + ct * 16 * Q8MN_BYTES + 8 * q);
+        const float d8 = *reinterpret_cast<const float*>(mb + ct * 16 * Q8MN_BYTES + 32);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            v4i ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(aa[r][0], bq[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            v4i cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(ab[r][0], bq[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+            v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(ac[r][0], bq[0], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int s = 1; s < 4; ++s) {
+                ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(aa[r][s], bq[s], ca, 0, 0, 0);
+                cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(ab[r][s], bq[s], cb, 0, 0, 0);
+                cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(ac[r][s], bq[s], cc, 0, 0, 0);
+            }
+            const v4f cm = __builtin_amdgcn_mfma_f32_16x16x16f16(am[r], bm, v4f{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int I = (ca[i] << 4) + (cb[i] << 2) + cc[i];
+                acc[r][ct][i] = fmaf(d8, fmaf(-dmr[r][i], cm[i], dr[r][i] * (float)I), acc[r][ct][i]);
             }
         }
     }

@@ -7,9 +7,10 @@ test_oracle_q5k.py):
     bit-exact;
   - integer sub-block sums: bit-exact against the oracle's brute force;
   - vec_dot, GEMV (T = 1 decode kernel and the sdot4 kernel), batches (the
-    sdot4 GEMV over 8-token slices: Q5_K has no matrix-core kernel) and the
-    expert-gathered matvec (decode mapping, single-launch and grouped sdot4
-    kernels): every element within close_enough (1e-4 relative or 1e-5
+    matrix-core ring for T >= 4, every launch shape; the sdot4 GEMV over
+    8-token slices under SPQ4K_GEMM_MODE=1) and the expert-gathered matvec
+    (decode mapping, single-launch and grouped sdot4 kernels, the matrix-core
+    expert kernel): every element within close_enough (1e-4 relative or 1e-5
     absolute, tests/desktop/test_sp_kernels.cpp:34-48) of ggml's x86 order.
 Weights are encoder output (N(0, 0.02)) or arbitrary block bytes; outputs of
 arbitrary bytes are held to the fp32 summation bound around the exact result
@@ -213,6 +214,90 @@ def test_mul_mat_batched(ctx, oracle, T):
         _check(got, oracle.mul_mat_type(TYPE_Q5_K, W, M, K, X), f"q5k mul_mat T={T} M={M} K={K}")
 
 
+@pytest.mark.parametrize("cfg", [19, 20, 21, 22, 23])
+def test_ring_launch_shapes(oracle, cfg):
+    """Every Q5_K matrix-core launch shape, on ragged rows and tokens."""
+    rng = np.random.default_rng(510 + cfg)
+    c = context_with({"SPQ4K_GEMM_CFG": cfg})
+    try:
+        for M, K, T in ((300, 768, 5), (200, 4096, 33), (1000, 2048, 100)):
+            W = _enc(oracle, rng, M, K)
+            X = rng.standard_normal((T, K)).astype(np.float32)
+            got = c.mul_mat(c.upload(W, M, K, type=TYPE_Q5_K), X)
+            _check(got, oracle.mul_mat_type(TYPE_Q5_K, W, M, K, X), f"cfg={cfg} M={M} K={K} T={T}")
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("M,K,T", [(64, 27648, 64), (4096, 4096, 128), (512, 12288, 256), (96, 5120, 7)])
+def test_ring_planned(ctx, oracle, M, K, T):
+    """The planner's choice, including K splits (few rows, long K) and the
+    reduction of their partial sums."""
+    rng = np.random.default_rng(M + K + T + 5)
+    W = _gpu_enc(ctx, rng, M, K)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    got = ctx.mul_mat(ctx.upload(W, M, K, type=TYPE_Q5_K), X)
+    _check(got, oracle.mul_mat_type(TYPE_Q5_K, W, M, K, X), f"planned M={M} K={K} T={T}")
+
+
+def _const_block(sc, mn, q5, d, dmin):
+    """One Q5_K block whose 8 sub-blocks all hold scale sc, min mn (6-bit)
+    and value q5 (5-bit), packed as get_scale_min_k4 and dequantize_row_q5_K
+    unpack them (ggml-quants.c)."""
+    b = np.zeros(Q5K, np.uint8)
+    b[0:4] = np.array([d, dmin], np.float16).view(np.uint8)
+    b[4:8] = (sc & 63) | ((sc >> 4) << 6)
+    b[8:12] = (mn & 63) | ((mn >> 4) << 6)
+    b[12:16] = (sc & 15) | ((mn & 15) << 4)
+    b[16:48] = 0xFF if q5 >> 4 else 0
+    b[48:176] = (q5 & 15) | ((q5 & 15) << 4)
+    return b
+
+
+def test_ring_extreme_operands(ctx, oracle):
+    """Blocks at the ends of the split operand range: scale 63 (every part of
+    sc = 16a + 4b + c at 3, operands a q5 up to 93) and the single-part
+    scales 48, 12, 3, with value 0 or 31 and min 0 or 63, one combination a
+    row; dmin < 0 so that with one-sign activations the scale and min terms
+    add (every Q8_K block holds -128 at its largest magnitude). Then
+    arbitrary blocks, held to the summation bound."""
+    rng = np.random.default_rng(520)
+    M, K, T = 64, 1024, 48
+    nb = K // QK
+    blk = np.zeros((M, nb, Q5K), np.uint8)
+    for r in range(M):
+        v = r % 16
+        sc, q5, mn = (63, 48, 12, 3)[v % 4], (0, 31)[(v >> 2) & 1], (0, 63)[(v >> 3) & 1]
+        for b in range(nb):
+            blk[r, b] = _const_block(sc, mn, q5, 2.0 ** -12 * (1 + r % 5), -2.0 ** -13 * (1 + r % 3))
+    W = blk.ravel()
+    for X in (np.abs(rng.standard_normal((T, K))), -np.abs(rng.standard_normal((T, K)))):
+        X = X.astype(np.float32)
+        _check(ctx.mul_mat(ctx.upload(W, M, K, type=TYPE_Q5_K), X),
+               oracle.mul_mat_type(TYPE_Q5_K, W, M, K, X), "extreme one-sign")
+    W2 = _rand_blocks(rng, M * nb)
+    X2 = rng.standard_normal((T, K)).astype(np.float32)
+    exact, mag = _exact_rows(oracle, W2, M, K, X2)
+    _check_bounded(ctx.mul_mat(ctx.upload(W2, M, K, type=TYPE_Q5_K), X2), exact, mag, nb, "arbitrary blocks")
+
+
+@pytest.mark.parametrize("T", [4, 40])
+def test_ring_matches_sdot4_slices(oracle, T):
+    """SPQ4K_GEMM_MODE=1 keeps Q5_K batches on the sdot4 kernels: both paths
+    within tolerance of the oracle on the same inputs."""
+    rng = np.random.default_rng(530 + T)
+    M, K = 384, 4096
+    W = _enc(oracle, rng, M, K)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    exp = oracle.mul_mat_type(TYPE_Q5_K, W, M, K, X)
+    for env in ({}, {"SPQ4K_GEMM_MODE": 1}):
+        c = context_with(env)
+        try:
+            _check(c.mul_mat(c.upload(W, M, K, type=TYPE_Q5_K), X), exp, f"{env} T={T}")
+        finally:
+            c.close()
+
+
 @pytest.mark.parametrize("T", [1, 4, 12])
 def test_gemv_multi_device(ctx, oracle, T):
     from spq4k.hip import DeviceArray
@@ -241,7 +326,7 @@ def test_mul_mat_id_golden(ctx, tag):
     _check(got, GOLD[f"mmid_Y_{tag}"], f"golden mul_mat_id {tag}")
 
 
-@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 3}, {"SPQ4K_MOE_MODE": 2}])
+@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 3}, {"SPQ4K_MOE_UNFUSED": 1}, {"SPQ4K_MOE_MODE": 2}])
 @pytest.mark.parametrize("T,ne11", [(1, 1), (3, 8), (12, 1), (32, 8)])
 def test_moe(oracle, env, T, ne11):
     rng = np.random.default_rng(508 + T)
@@ -255,5 +340,25 @@ def test_moe(oracle, env, T, ne11):
             got = c.mul_mat_id(c.upload(bank, M, K, E, type=TYPE_Q5_K), X, ids)
             _check(got, oracle.mul_mat_id_type(TYPE_Q5_K, bank, M, K, E, X, ids),
                    f"q5k moe {env} T={T} ne11={ne11} M={M} K={K}")
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_UNFUSED": 1}])
+def test_moe_ring_ragged(oracle, env):
+    """The matrix-core expert kernel on a bank whose rows are not a multiple
+    of its 128-row tile, with one expert chosen by every token (pairs over
+    several 16-token tiles, the last one partial) and the rest spread; the
+    sdot4 grouped kernels on the same inputs."""
+    rng = np.random.default_rng(540)
+    E, n_used, M, K, T = 16, 4, 200, 1024, 70
+    bank = _enc(oracle, rng, E * M, K)
+    ids = np.stack([np.concatenate([[0], rng.choice(np.arange(1, E), n_used - 1, replace=False)])
+                    for _ in range(T)]).astype(np.int32)
+    X = rng.standard_normal((T, 1, K)).astype(np.float32)
+    c = context_with(env)
+    try:
+        got = c.mul_mat_id(c.upload(bank, M, K, E, type=TYPE_Q5_K), X, ids)
+        _check(got, oracle.mul_mat_id_type(TYPE_Q5_K, bank, M, K, E, X, ids), f"q5k moe ring {env}")
     finally:
         c.close()
