@@ -192,7 +192,7 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
 // Launch shape of the T = 1 decode kernel. One workgroup per CU, so that x is
 // quantised once per CU, one wave per row; measured on MI355X for the 8B
 // decode shapes (cold weights, graph replay):
-//   K = 4096,  M <= 4096   : 16 waves, x-first         (o projection)
+//   K = 4096,  M <= 4096   : 16 waves                   (o projection)
 //   K = 4096,  M <= 8192   : 12 waves = 2 rows a wave   (q/k/v, 6144 rows)
 //   K = 4096,  M <= 32768  : 16 waves                   (gate/up, 24576 rows)
 //   K = 4096,  larger M    : 12 waves, 2 rows in flight, x-first (lm_head)
@@ -206,7 +206,7 @@ DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb, int64_t rows) {
     } else if (nb >= 48) {
         d.waves = 16; d.depth = 1; d.xfirst = true;
     } else if (rows <= 4096) {
-        d.waves = 16; d.depth = 1; d.xfirst = true;
+        d.waves = 16; d.depth = 1; d.xfirst = false;
     } else if (rows <= 8192) {
         d.waves = 12; d.depth = 1; d.xfirst = false;
     } else if (rows <= 32768) {
