@@ -284,9 +284,56 @@ int q80_grid(const spq4k_ctx* c, int64_t rows, int nb, int64_t xrows) {
 // workgroups copy to LDS; larger T run over slices of those planes, as many
 // tokens a launch as LDS holds (at most 8); a row too long for LDS reads its
 // one token from the planes directly.
+// Q8_0 batches on the matrix cores (gemm_ring_kernel, F = 3): the Q8_0
+// planes of X in the scratch with the partial plane of a K split behind them,
+// then the ring launch (and the reduction of the K ranges).
+int q80_gemm(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T) {
+    const int64_t K = W[0]->K;
+    const int nb = (int)(K / SPQ4K_QK8_0);
+    GemmParams p;
+    memset(&p, 0, sizeof p);
+    p.T = (int32_t)T;
+    p.nb = (int32_t)(K / SPQ4K_QK_K);
+    p.cfg = c->gemm_cfg;
+    int64_t rows = 0;
+    for (int i = 0; i < n; ++i) {
+        p.seg[i].W = W[i]->data;
+        p.seg[i].Y = Y[i];
+        p.seg[i].M = (int32_t)W[i]->M;
+        p.seg[i].row_begin = (int32_t)rows;
+        rows += W[i]->M;
+    }
+    for (int i = n; i < GEMM_MAX_SEG; ++i) p.seg[i].tile_begin = p.seg[i].row_begin = INT32_MAX;
+    p.nseg = n;
+    p.rows = (int32_t)rows;
+    p.fmt = WF_Q80;
+    if ((rows + 15) / 16 * ((T + 15) / 16) > (1ll << 31) - 1 || rows > (1ll << 31) - 1)
+        return set_err(c, -EINVAL, "gemm: grid too large");
+    const size_t planes = q80_planes_bytes(T, nb);
+    size_t room = c->scratch_cap > planes ? c->scratch_cap - planes : 0;
+    if (room < ((size_t)8 << 20)) room = (size_t)8 << 20;
+    const GemmPlan g = gemm_plan(p, c->num_cus, room);
+    p.cfg = g.cfg;
+    p.ksplit = g.ksplit;
+    p.kchunk = g.kchunk;
+    Q80Params qp;
+    memset(&qp, 0, sizeof qp);
+    int rc = q80_planes(c, X, K, T, nb, &qp, g.partial_bytes);
+    if (rc) return rc;
+    p.Q.qs = qp.Aq;
+    p.Q.d = qp.Ad;
+    p.Q.mn = reinterpret_cast<const uint8_t*>(qp.Aq);   // no min-term plane: a valid address for stray reads
+    p.P = g.ksplit > 1 ? reinterpret_cast<float*>(c->scratch + planes) : nullptr;
+    const hipError_t e = launch_gemm(p, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "gemm (Q8_0) launch");
+    return 0;
+}
+
 int q80_dense(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X, float* const* Y, int64_t T) {
     const int64_t K = W[0]->K;
     const int nb = (int)(K / SPQ4K_QK8_0);
+    // batches beyond the matvec's 8 tokens, K a multiple of 256: matrix cores
+    if (T > SPQ4K_GEMV_MAX_T && K % SPQ4K_QK_K == 0 && c->gemm_mode != 1) return q80_gemm(c, n, W, X, Y, T);
     Q80Params p;
     memset(&p, 0, sizeof p);
     int64_t total = 0;

@@ -339,12 +339,16 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 // leaves its 210-byte block; ring_block_q6, 16x16 tiles). Q6_K block starts
 // are 2-byte aligned; global loads on gfx950 take unaligned addresses.
 // 2 = Q5_K (11 slots of its 176-byte block; ring_block_q5, 16x16 tiles).
+// 3 = Q8_0 with K a multiple of 256: a super-block is eight 34-byte blocks,
+// 272 bytes = 17 slots a row; the activations are Q8_0 planes (p.Q.qs int8
+// [T][K], p.Q.d fp32 [T][K/32]): the token's values as for Q8_K, its eight
+// scales in the first two of its three min-term slots (ring_block_q80).
 template <int RT, int CT, int NW, int S, int TW = 16, int F = 0>
 __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
     static_assert(TW == 16 || TW == 32, "16x16 or 32x32 output tiles");
-    static_assert(F == 0 || TW == 16, "Q6_K and Q5_K run on 16x16 tiles");
-    constexpr int WSL = F == 1 ? 14 : F == 2 ? 11 : 9;                               // 16-byte slots of a row's block
-    constexpr int BB = F == 1 ? Q6K_BYTES : F == 2 ? Q5K_BYTES : Q4K_BYTES;          // block bytes in memory
+    static_assert(F == 0 || TW == 16, "Q6_K, Q5_K and Q8_0 run on 16x16 tiles");
+    constexpr int WSL = F == 1 ? 14 : F == 2 ? 11 : F == 3 ? 17 : 9;                 // 16-byte slots of a row's block
+    constexpr int BB = F == 1 ? Q6K_BYTES : F == 2 ? Q5K_BYTES : F == 3 ? Q80_RING_ROW : Q4K_BYTES;   // bytes in memory
     constexpr int ROWB = 16 * WSL;                   // bytes of a row in the stage
     constexpr int TOK = CT * TW;
     constexpr int ROWS = RT * TW * NW;
@@ -384,7 +388,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
     for (int i = 0; i < NPW; ++i) {
         const int J = NW * i + wave;              // load index within the stage
         const int slot = J * 64 + lane;
-        src[i] = p.Q.mn;                          // surplus and padding: any valid address
+        // surplus and padding: any valid address (Q8_0 planes have no min-term plane)
+        src[i] = F == 3 ? reinterpret_cast<const uint8_t*>(p.Q.qs) : p.Q.mn;
         stride[i] = 0;
         if (J < W_LOADS) {
             const int r = min(row0 + slot / WSL, M - 1);
@@ -403,8 +408,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
             const int sl = slot - (W_LOADS + Q_LOADS) * 64;
             if (sl < M_SLOTS) {
                 const int tg = min(tok0 + sl / 3, T - 1);
-                src[i] = p.Q.mn + ((size_t)tg * nb + kb0) * Q8MN_BYTES + 16 * (sl % 3);
-                stride[i] = Q8MN_BYTES;
+                if constexpr (F == 3) {
+                    src[i] = reinterpret_cast<const uint8_t*>(p.Q.d) + ((size_t)tg * nb + kb0) * 32 + 16 * min(sl % 3, 1);
+                    stride[i] = 32;
+                } else {
+                    src[i] = p.Q.mn + ((size_t)tg * nb + kb0) * Q8MN_BYTES + 16 * (sl % 3);
+                    stride[i] = Q8MN_BYTES;
+                }
             }
         }
     }
@@ -437,6 +447,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmParams p) {
             ring_block_q6<RT, CT>(lds[buf] + (wave * RT * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
         else if constexpr (F == 2)
             ring_block_q5<RT, CT>(lds[buf] + (wave * RT * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+        else if constexpr (F == 3)
+            ring_block_q80<RT, CT>(lds[buf] + (wave * RT * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
         else if constexpr (TW == 16)
             ring_block<RT, CT>(lds[buf] + (wave * RT * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
         else
@@ -739,6 +751,12 @@ static const TiledShape kTiled[] = {
     {128, 32, true, launch_ring_<1, 2, 8, 3, 16, 2>, WF_Q5K},   // 21: T <= 32
     {128, 64, true, launch_ring_<1, 4, 8, 2, 16, 2>, WF_Q5K},   // 22: 8 waves, 2 stages
     {64, 64, true, launch_ring_<1, 4, 4, 3, 16, 2>, WF_Q5K},    // 23: 4 waves
+    // Q8_0, K a multiple of 256 (F = 3)
+    {128, 16, true, launch_ring_<1, 1, 8, 3, 16, 3>, WF_Q80},   // 24: T <= 16
+    {128, 32, true, launch_ring_<1, 2, 8, 3, 16, 3>, WF_Q80},   // 25: T <= 32
+    {128, 64, true, launch_ring_<1, 4, 8, 2, 16, 3>, WF_Q80},   // 26: 8 waves, 2 stages of 56 KB
+    {64, 64, true, launch_ring_<1, 4, 4, 3, 16, 3>, WF_Q80},    // 27: 4 waves, 3 stages
+    {128, 16, true, launch_ring_<1, 1, 8, 2, 16, 3>, WF_Q80},   // 28: T <= 16, 2 stages (two workgroups a CU)
 };
 constexpr int N_TILED = (int)(sizeof(kTiled) / sizeof(kTiled[0]));
 
@@ -758,6 +776,10 @@ GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
         cfg = p.T <= 16 ? 15 : (p.T <= 32 ? 16 : 14);
     } else if ((cfg < 0 || cfg >= N_TILED) && p.fmt == WF_Q5K) {
         cfg = p.T <= 16 ? 20 : (p.T <= 32 ? 21 : 19);
+    } else if ((cfg < 0 || cfg >= N_TILED) && p.fmt == WF_Q80) {
+        // measured on 4096 x 12288: T = 16 28.7 us (2 stages, two workgroups a
+        // CU) against 35.3 (3 stages, one); T = 512 227 us on 128 x 64 tiles
+        cfg = p.T <= 32 ? 28 : 26;
     } else if (cfg < 0 || cfg >= N_TILED) {
         if (p.T <= 16) {
             cfg = 6;

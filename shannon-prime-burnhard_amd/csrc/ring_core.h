@@ -452,4 +452,48 @@ __device__ __forceinline__ void ring_block_q5(const uint8_t* wt, const uint8_t* 
     }
 }
 
+// ---------------------------------------------------------------------------
+// One 256-value chunk of Q8_0 rows (eight 34-byte blocks, fp16 d then 32
+// int8 values: 272 bytes a row, 17 stage slots) x Q8_0 activations (the
+// token's int8 values in natural order, RING_QS bytes a token row; its eight
+// fp32 block scales at the start of its Q8MN_BYTES of mreg) on 16x16 tiles.
+// Block j is one v_mfma_i32_16x16x32_i8 (lane (c16, q) holds values 8q .. 8q+7
+// of row c16 and of token c16) giving the exact integer dot of every (row,
+// token) pair, then y += (d_w * d_x) * (float)sum: the per-block combine of
+// ggml_vec_dot_q8_0_q8_0 (ggml-cpu/arch/x86/quants.c). A row's values start 2
+// bytes into its block: the 8-byte LDS reads are 2-byte aligned (gfx950 LDS
+// takes unaligned addresses).
+constexpr int Q80_RING_ROW = 272;
+template <int RT, int CT>
+__device__ __forceinline__ void ring_block_q80(const uint8_t* wt, const uint8_t* qreg, const uint8_t* mreg, int c16,
+                                               int q, v4f (&acc)[RT][CT]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        long a[RT];
+        float dw[RT][4];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            __builtin_memcpy(&a[r], wt + (r * 16 + c16) * Q80_RING_ROW + 34 * j + 2 + 8 * q, 8);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint16_t h;
+                __builtin_memcpy(&h, wt + (r * 16 + 4 * q + i) * Q80_RING_ROW + 34 * j, 2);
+                dw[r][i] = half_bits_to_float(h);
+            }
+        }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            long b;
+            __builtin_memcpy(&b, qreg + (ct * 16 + c16) * RING_QS + 32 * j + 8 * q, 8);
+            const float dx = *reinterpret_cast<const float*>(mreg + (ct * 16 + c16) * Q8MN_BYTES + 4 * j);
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const v4i s = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[r], b, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[r][ct][i] = fmaf(dw[r][i] * dx, (float)s[i], acc[r][ct][i]);
+            }
+        }
+    }
+}
+
 }  // namespace spq4k

@@ -9,9 +9,11 @@ reference in test_oracle_q8_0.py):
     them away from zero): bit-exact;
   - integer block sums: bit-exact against the oracle's brute force;
   - vec_dot, the matvec at every lanes-per-row shape (K from 32 to 147456,
-    the last too long for LDS), batches over token slices, several matrices
-    in one launch and the expert-gathered matvec (one sweep for small
-    batches, grouped by expert otherwise): every element within close_enough
+    the last too long for LDS), batches (over 8 tokens and K a multiple of
+    256: the matrix-core ring, every launch shape, K splits, the int8 ends;
+    otherwise the matvec over token slices), several matrices in one launch
+    and the expert-gathered matvec (one sweep for small batches, grouped by
+    expert otherwise): every element within close_enough
     (1e-4 relative or 1e-5 absolute, tests/desktop/test_sp_kernels.cpp:34-48)
     of ggml's x86 order.
 Weights are encoder output (N(0, 0.02)) or arbitrary block bytes; outputs of
@@ -232,6 +234,76 @@ def test_mul_mat_batched(ctx, oracle, T):
         X = rng.standard_normal((T, K)).astype(np.float32)
         got = ctx.mul_mat(ctx.upload(W, M, K, type=TYPE_Q8_0), X)
         _check(got, oracle.mul_mat_q8_0(W, M, K, X), f"q8_0 mul_mat T={T} M={M} K={K}")
+
+
+@pytest.mark.parametrize("cfg", [24, 25, 26, 27, 28])
+def test_ring_launch_shapes(oracle, cfg):
+    """Every Q8_0 matrix-core launch shape (K a multiple of 256), on ragged
+    rows and tokens."""
+    rng = np.random.default_rng(820 + cfg)
+    c = context_with({"SPQ4K_GEMM_CFG": cfg})
+    try:
+        for M, K, T in ((300, 768, 17), (200, 4096, 33), (1000, 2048, 100)):
+            W = _enc(oracle, rng, M, K)
+            X = rng.standard_normal((T, K)).astype(np.float32)
+            got = c.mul_mat(c.upload(W, M, K, type=TYPE_Q8_0), X)
+            _check(got, oracle.mul_mat_q8_0(W, M, K, X), f"cfg={cfg} M={M} K={K} T={T}")
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("M,K,T", [(64, 27648, 64), (4096, 4096, 128), (512, 12288, 256), (96, 5120, 9)])
+def test_ring_planned(ctx, oracle, M, K, T):
+    """The planner's choice, including K splits (few rows, long K) and the
+    reduction of their partial sums."""
+    rng = np.random.default_rng(M + K + T + 8)
+    W = ctx.quantize_chunk((rng.standard_normal((M, K)) * 0.02).astype(np.float32), M, K, type=TYPE_Q8_0)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    got = ctx.mul_mat(ctx.upload(W, M, K, type=TYPE_Q8_0), X)
+    _check(got, oracle.mul_mat_q8_0(W, M, K, X), f"planned M={M} K={K} T={T}")
+
+
+def test_ring_extreme_operands(ctx, oracle):
+    """Blocks of values -128 or 127 throughout (the int8 ends, every block of
+    a row alike; d of either sign, one sign a row), one-sign activations so
+    that a row's blocks add up without cancellation; then arbitrary blocks,
+    held to the summation bound."""
+    rng = np.random.default_rng(830)
+    M, K, T = 64, 1024, 40
+    nb = K // QK
+    blk = np.zeros((M, nb, Q8_0), np.uint8)
+    for r in range(M):
+        v = -128 if r % 2 == 0 else 127
+        d = (2.0 ** -12) * (1 + r % 5) * (1 if (r >> 1) % 2 == 0 else -1)
+        blk[r, :, 0:2] = np.array([d], np.float16).view(np.uint8)
+        blk[r, :, 2:] = np.array([v], np.int8).view(np.uint8)
+    W = blk.ravel()
+    Wd = ctx.upload(W, M, K, type=TYPE_Q8_0)
+    for X in (np.abs(rng.standard_normal((T, K))), -np.abs(rng.standard_normal((T, K)))):
+        X = X.astype(np.float32)
+        _check(ctx.mul_mat(Wd, X), oracle.mul_mat_q8_0(W, M, K, X), "extreme one-sign")
+    W2 = _rand_blocks(rng, M * nb)
+    X2 = rng.standard_normal((T, K)).astype(np.float32)
+    exact, mag = _exact_rows(oracle, W2, M, K, X2)
+    _check_bounded(ctx.mul_mat(ctx.upload(W2, M, K, type=TYPE_Q8_0), X2), exact, mag, nb, "arbitrary blocks")
+
+
+@pytest.mark.parametrize("T", [9, 40])
+def test_ring_matches_matvec_slices(oracle, T):
+    """SPQ4K_GEMM_MODE=1 keeps Q8_0 batches on the matvec over token slices;
+    K = 800 (not a multiple of 256) always does. Both paths within tolerance
+    of the oracle on the same inputs."""
+    rng = np.random.default_rng(840 + T)
+    for M, K in ((384, 4096), (256, 800)):
+        W = _enc(oracle, rng, M, K)
+        X = rng.standard_normal((T, K)).astype(np.float32)
+        exp = oracle.mul_mat_q8_0(W, M, K, X)
+        for env in ({}, {"SPQ4K_GEMM_MODE": 1}):
+            c = context_with(env)
+            try:
+                _check(c.mul_mat(c.upload(W, M, K, type=TYPE_Q8_0), X), exp, f"{env} M={M} K={K} T={T}")
+            finally:
+                c.close()
 
 
 @pytest.mark.parametrize("T", [1, 3])
