@@ -347,9 +347,18 @@ def run_single(args, M, K, T, dist, outlier, name, qtype=spq4k.TYPE_Q4_K):
     ms = time_graph(ctx, g, 1, max(1, args.warmup // 10)) / n
     alg = nb + 4 * K * T + 4 * M * T
     gbs = alg / (ms * 1e-3) / 1e9
+    # reported beside it, never as the value: the same weights every call,
+    # resident in the 256 MB Infinity Cache when they fit
+    with Graph.capture(ctx.stream) as gh:
+        for i in range(n):
+            ctx.mul_mat_dev(ws[0], x.ptr, y.ptr, T)
+    ms_hot = time_graph(ctx, gh, 1, 1) / n
     print(json.dumps({"metric": f"{name} effective HBM GB/s", "value": round(gbs, 2), "unit": "GB/s",
                       "us_per_call": round(ms * 1e3, 3), "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2),
                       "TOPs_int8": round(2 * M * K * T / (ms * 1e-3) / 1e12, 1),
+                      "hot_cache": {"us_per_call": round(ms_hot * 1e3, 3),
+                                    "GBps": round(alg / (ms_hot * 1e-3) / 1e9, 1),
+                                    "note": "same weights every call (Infinity Cache resident when under 256 MB)"},
                       "config": {"workload": name, "M": M, "K": K, "T": T, "weight_copies": copies}}), flush=True)
     for w in ws:
         w.free()
@@ -434,6 +443,14 @@ def run_moe(args):
                 ctx.moe_dev(wu, idd[L].ptr, k, 1, T, xg.ptr, Y.ptr)
                 ctx.moe_dev(wd, idd[L].ptr, k, k, T, xd.ptr, Y.ptr)
         ms = time_graph(ctx, g, max(5, args.steps // 5), 2) / NL
+        # beside it, never as the value: layer 0's banks and routing every time
+        with Graph.capture(ctx.stream) as gh:
+            for L in range(NL):
+                (wg, _, _), (wu, _, _), (wd, _, _) = layers[0]
+                ctx.moe_dev(wg, idd[0].ptr, k, 1, T, xg.ptr, Y.ptr)
+                ctx.moe_dev(wu, idd[0].ptr, k, 1, T, xg.ptr, Y.ptr)
+                ctx.moe_dev(wd, idd[0].ptr, k, k, T, xd.ptr, Y.ptr)
+        ms_hot = time_graph(ctx, gh, max(5, args.steps // 5), 2) / NL
         uniq = float(np.mean([len(np.unique(i)) for i in ids_l]))
         wbytes = uniq * sum(q4k_bytes(M, K) for (_, M, K) in shapes)
         abytes = wbytes + 4 * T * (2 * 2048 + 2 * k * 768) + 4 * T * k * (768 + 2048)
@@ -441,6 +458,8 @@ def run_moe(args):
         print(json.dumps({"metric": f"Q4_K MoE expert matvec (gate+up+down), T={T}", "value": round(gbs, 1),
                           "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
                           "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2), "unique_experts": uniq,
+                          "hot_cache": {"us_per_layer": round(ms_hot * 1e3, 2),
+                                        "note": "one layer's banks and routing every time (Infinity Cache resident)"},
                           "config": {"workload": "30B-A3B-like MoE layer, 128 experts, top-8, 8 layers of banks (cold)",
                                      "T": T}}), flush=True)
         for a in idd:
