@@ -1182,10 +1182,38 @@ int q80_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t
     p.route.pairs = rt + 1 + 3 * E;
     hipError_t e = launch_moe_route(ids, (int)n_pairs, E, p.route, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "moe route launch");
-    // pairs a row is dotted with at a time: about twice the mean an active
-    // expert receives, at most 8
     const int64_t max_act = n_pairs < E ? n_pairs : E;
     const int64_t mean_pairs = (n_pairs + max_act - 1) / max_act;
+    // matrix cores once the active experts receive two pairs on average (K a
+    // multiple of 256): moe_ring_kernel streams each expert once per 16 pairs
+    if (!c->moe_unfused && bank->K % SPQ4K_QK_K == 0 && mean_pairs >= 2) {
+        MoeParams mp;
+        memset(&mp, 0, sizeof mp);
+        mp.route = p.route;
+        mp.bank = bank->data;
+        mp.expert_bytes = p.expert_bytes;
+        mp.Y = Y;
+        mp.Q.qs = p.Aq;
+        mp.Q.d = p.Ad;
+        mp.Q.mn = reinterpret_cast<const uint8_t*>(p.Aq);   // no min-term plane: a valid address for stray reads
+        mp.M = M;
+        mp.nb = (int32_t)(bank->K / SPQ4K_QK_K);
+        mp.n_used = (int32_t)n_used;
+        mp.ne11 = (int32_t)ne11;
+        mp.fmt = WF_Q80;
+        const int64_t ntiles = (M + 127) / 128;
+        int64_t rtw = ntiles * max_act / (2 * (int64_t)c->num_cus);
+        if (rtw < 1) rtw = 1;
+        if (rtw > ntiles) rtw = ntiles;
+        mp.ring_rt = (int32_t)rtw;
+        mp.tiles_per_expert = (int32_t)((ntiles + rtw - 1) / rtw);
+        if (max_act * mp.tiles_per_expert > (1ll << 31) - 1) return set_err(c, -EINVAL, "moe: grid too large");
+        e = launch_moe_ring_q80(mp, (int)max_act, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "moe ring (Q8_0) launch");
+        return 0;
+    }
+    // pairs a row is dotted with at a time: about twice the mean an active
+    // expert receives, at most 8
     int tc = 1;
     while (tc < 8 && tc < 2 * mean_pairs) tc *= 2;
     // rows of an expert a workgroup takes: whole passes of its waves, as few

@@ -514,13 +514,16 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(const int32_t* __restrict
 }
 
 // F = 1: Q6_K banks (14 slots a row, the last re-reading block bytes
-// 194..209; ring_block_q6); F = 2: Q5_K banks (11 slots, ring_block_q5); as
-// in gemm_ring_kernel.
+// 194..209; ring_block_q6); F = 2: Q5_K banks (11 slots, ring_block_q5);
+// F = 3: Q8_0 banks with K a multiple of 256 (17 slots: eight 34-byte
+// blocks; Q8_0 planes, the token's eight scales in its min-term slots;
+// ring_block_q80); as in gemm_ring_kernel.
 template <int S, int F = 0>
 __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
     constexpr int NW = 8, ROWS = 128, TOK = 16;
-    constexpr int WSL = F == 1 ? 14 : F == 2 ? 11 : 9;
-    constexpr int BB = F == 1 ? Q6K_BYTES : F == 2 ? Q5K_BYTES : Q4K_BYTES, ROWB = 16 * WSL;
+    constexpr int WSL = F == 1 ? 14 : F == 2 ? 11 : F == 3 ? 17 : 9;
+    constexpr int BB = F == 1 ? Q6K_BYTES : F == 2 ? Q5K_BYTES : F == 3 ? Q80_RING_ROW : Q4K_BYTES;
+    constexpr int ROWB = 16 * WSL;
     constexpr int W_SLOTS = ROWS * WSL, Q_SLOTS = TOK * 17, M_SLOTS = TOK * 3;
     constexpr int W_LOADS = W_SLOTS / 64, Q_LOADS = (Q_SLOTS + 63) / 64, M_LOADS = (M_SLOTS + 63) / 64;
     constexpr int NLOAD = W_LOADS + Q_LOADS + M_LOADS;
@@ -557,7 +560,8 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
         for (int i = 0; i < NPW; ++i) {
             const int J = NW * i + wave;
             const int slot = J * 64 + lane;
-            src[i] = p.Q.mn;                   // surplus and padding: any valid address
+            // surplus and padding: any valid address (Q8_0 planes have no min-term plane)
+            src[i] = F == 3 ? reinterpret_cast<const uint8_t*>(p.Q.qs) : p.Q.mn;
             stride[i] = 0;
             wrow[i] = -1;
             if (J < W_LOADS) {
@@ -574,6 +578,9 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
                     if (isq) {
                         src[i] = reinterpret_cast<const uint8_t*>(p.Q.qs) + (size_t)xr * nb * 256 + 16 * min(sl % 17, 15);
                         stride[i] = 256;
+                    } else if (F == 3) {
+                        src[i] = reinterpret_cast<const uint8_t*>(p.Q.d) + (size_t)xr * nb * 32 + 16 * min(sl % 3, 1);
+                        stride[i] = 32;
                     } else {
                         src[i] = p.Q.mn + (size_t)xr * nb * Q8MN_BYTES + 16 * (sl % 3);
                         stride[i] = Q8MN_BYTES;
@@ -605,6 +612,8 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
                 ring_block_q6<1, 1>(lds[buf] + (wave * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
             else if constexpr (F == 2)
                 ring_block_q5<1, 1>(lds[buf] + (wave * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
+            else if constexpr (F == 3)
+                ring_block_q80<1, 1>(lds[buf] + (wave * 16) * ROWB, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
             else
                 ring_block<1, 1>(lds[buf] + (wave * 16) * Q4K_BYTES, lds[buf] + Q_OFF, lds[buf] + M_OFF, c16, q, acc);
             if (sp - (sp / nb) * nb == nb - 1) {
@@ -626,6 +635,15 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
+}
+
+// Q8_0 banks: the routing tables and Q8_0 planes are already in place
+// (launch_moe_route, the Q8_0 planes quantiser); the ring alone.
+hipError_t launch_moe_ring_q80(const MoeParams& p, int max_act, hipStream_t st) {
+    if (p.fmt != WF_Q80) return hipErrorInvalidValue;
+    const int64_t grid = (int64_t)max_act * p.tiles_per_expert;
+    hipLaunchKernelGGL((moe_ring_kernel<2, 3>), dim3((unsigned)grid), dim3(512), 0, st, p);
+    return hipGetLastError();
 }
 
 hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, int E, const float* X,

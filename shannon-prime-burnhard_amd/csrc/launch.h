@@ -124,6 +124,9 @@ hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStr
 // over max_act experts x p.tiles_per_expert groups of p.ring_rt row tiles
 hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, int E, const float* X,
                            int64_t x_tstride, int n_xrows, int max_act, hipStream_t st);
+// Q8_0 banks (K a multiple of 256; p.Q.qs / p.Q.d the Q8_0 planes, p.route
+// filled): the ring kernel only
+hipError_t launch_moe_ring_q80(const MoeParams& p, int max_act, hipStream_t st);
 
 // prefill matmul on matrix cores (k_gemm.hip)
 constexpr int GEMM_MAX_SEG = 4;

@@ -361,9 +361,12 @@ def test_mul_mat_id_golden(ctx, tag):
     _check(got, GOLD[f"mmid_Y_{tag}"], f"golden mul_mat_id {tag}")
 
 
-@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 2}])
+@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 2}, {"SPQ4K_MOE_UNFUSED": 1}])
 @pytest.mark.parametrize("T,ne11", [(1, 1), (3, 8), (12, 1), (32, 8), (200, 1)])
 def test_moe(oracle, env, T, ne11):
+    """Every MoE path: the one-launch sweep (small batches), the matrix-core
+    expert kernel (two pairs an expert on average, K a multiple of 256) and
+    the grouped matvec (K = 96, or SPQ4K_MOE_UNFUSED)."""
     rng = np.random.default_rng(811 + T)
     E, n_used = 32, 8
     c = context_with(env)
@@ -379,17 +382,43 @@ def test_moe(oracle, env, T, ne11):
         c.close()
 
 
-def test_moe_rand_blocks(ctx, oracle):
-    """Arbitrary expert bytes, grouped kernel: the summation bound per pair."""
+@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_UNFUSED": 1}])
+def test_moe_rand_blocks(oracle, env):
+    """Arbitrary expert bytes, matrix-core expert kernel and grouped matvec:
+    the summation bound per pair."""
     rng = np.random.default_rng(812)
     E, n_used, T, M, K = 16, 4, 24, 96, 2048
     bank = _rand_blocks(rng, E * M * K // QK)
     ids = np.stack([rng.choice(E, n_used, replace=False) for _ in range(T)]).astype(np.int32)
     X = rng.standard_normal((T, 1, K)).astype(np.float32)
-    got = ctx.mul_mat_id(ctx.upload(bank, M, K, E, type=TYPE_Q8_0), X, ids)
+    c = context_with(env)
+    try:
+        got = c.mul_mat_id(c.upload(bank, M, K, E, type=TYPE_Q8_0), X, ids)
+    finally:
+        c.close()
     rb = M * K // QK * Q8_0
     for t in range(T):
         for s in range(n_used):
             e = ids[t, s]
             exact, mag = _exact_rows(oracle, bank[e * rb:(e + 1) * rb], M, K, X[t])
             _check_bounded(got[t, s][None], exact, mag, K // QK, f"pair ({t}, {s})")
+
+
+@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_UNFUSED": 1}])
+def test_moe_ring_ragged(oracle, env):
+    """The matrix-core expert kernel on a bank whose rows are not a multiple
+    of its 128-row tile, one expert chosen by every token (pairs over several
+    16-token tiles, the last partial) and the rest spread; the grouped matvec
+    on the same inputs."""
+    rng = np.random.default_rng(850)
+    E, n_used, M, K, T = 16, 4, 200, 1024, 70
+    bank = _enc(oracle, rng, E * M, K)
+    ids = np.stack([np.concatenate([[0], rng.choice(np.arange(1, E), n_used - 1, replace=False)])
+                    for _ in range(T)]).astype(np.int32)
+    X = rng.standard_normal((T, 1, K)).astype(np.float32)
+    c = context_with(env)
+    try:
+        got = c.mul_mat_id(c.upload(bank, M, K, E, type=TYPE_Q8_0), X, ids)
+        _check(got, oracle.mul_mat_id_q8_0(bank, M, K, E, X, ids), f"q8_0 moe ring {env}")
+    finally:
+        c.close()
