@@ -57,19 +57,24 @@ def _gemv(rows):
 
 
 def _staged(rows, key):
-    """Group the GEMV dispatches by decode stage. The first 145 dispatches (in
-    dispatch order) are one decode step, [qkv, o, gate_up, down] x 36 then
-    lm_head; each stage runs its own kernel instantiation, which maps every
-    later dispatch (step replays and per-stage replays alike) to its stage."""
+    """Group the GEMV dispatches of the step replays by decode stage. The
+    first 145 dispatches (in dispatch order) are one decode step, [qkv, o,
+    gate_up, down] x 36 then lm_head; every following block of 145 whose
+    kernel names repeat that sequence is another replay of the step, its
+    dispatches mapped to stages by position (two stages may run the same
+    kernel instantiation). Dispatches after the last such block (the
+    per-stage replays) are left out."""
     rows = sorted(rows, key=lambda r: int(r[key]))
-    name_of = {}
-    for i, r in enumerate(rows[:145]):
-        st = "lm_head" if i == 144 else STAGES[i % 4]
-        if name_of.setdefault(r["Kernel_Name"], st) != st:
-            raise ValueError(f"stages {st} and {name_of[r['Kernel_Name']]} share {r['Kernel_Name']}")
+    pattern = [r["Kernel_Name"] for r in rows[:145]]
+    if len(pattern) < 145:
+        raise ValueError(f"{len(pattern)} GEMV dispatches: fewer than one decode step")
     out = {s: [] for s in STAGES + ["lm_head"]}
-    for r in rows:
-        out[name_of[r["Kernel_Name"]]].append(r)
+    for b in range(0, len(rows) - 144, 145):
+        block = rows[b:b + 145]
+        if [r["Kernel_Name"] for r in block] != pattern:
+            break
+        for i, r in enumerate(block):
+            out["lm_head" if i == 144 else STAGES[i % 4]].append(r)
     return out
 
 
@@ -169,7 +174,7 @@ def main(argv=None):
         for c in args.command:
             f.write(c + "\n")
         f.write("```\n\n")
-        f.write("Per stage: average launch duration from the kernel trace; HBM bytes per launch from FETCH_SIZE / "
+        f.write("Per stage: average launch duration from the kernel trace over the step replays; HBM bytes per launch from FETCH_SIZE / "
                 "WRITE_SIZE (KiB per dispatch) scaled by the copy calibration below; algorithmic bytes = Q4_K "
                 "weights + fp32 x + fp32 y of the launch.\n\n")
         f.write("| stage | kernel | launches | avg us | algorithmic MB | HBM read MB | HBM write MB | HBM/alg | "
