@@ -412,7 +412,8 @@ def run_moe(args):
     T = 1..32. Timed cold: 8 layers, each with its own three expert banks
     (2.7 GB in all, larger than the 256 MB Infinity Cache) and its own routing
     (top-8 of seeded N(0,1) logits per token), replayed as one graph; a layer
-    is the gate, up and down GGML_OP_MUL_MAT_ID calls."""
+    is the gate, up and down GGML_OP_MUL_MAT_ID nodes: gate and up (same ids
+    and input) as one spq4k_moe_multi call, then down."""
     ctx = spq4k.Context(0)
     E, k, NL = 128, 8, 8
     shapes = (("gate", 768, 2048), ("up", 768, 2048), ("down", 2048, 768))
@@ -436,19 +437,19 @@ def run_moe(args):
         xg = syn.activations(T * 2048, 11)
         xd = syn.activations(T * k * 768, 12)
         Y = DeviceArray(T * k * 2048)
+        Y2 = DeviceArray(T * k * 768)
         with Graph.capture(ctx.stream) as g:
             for L in range(NL):
                 (wg, _, _), (wu, _, _), (wd, _, _) = layers[L]
-                ctx.moe_dev(wg, idd[L].ptr, k, 1, T, xg.ptr, Y.ptr)
-                ctx.moe_dev(wu, idd[L].ptr, k, 1, T, xg.ptr, Y.ptr)
+                # gate and up share ids and input: one spq4k_moe_multi call
+                ctx.moe_multi_dev([wg, wu], idd[L].ptr, k, 1, T, xg.ptr, [Y.ptr, Y2.ptr])
                 ctx.moe_dev(wd, idd[L].ptr, k, k, T, xd.ptr, Y.ptr)
         ms = time_graph(ctx, g, max(5, args.steps // 5), 2) / NL
         # beside it, never as the value: layer 0's banks and routing every time
         with Graph.capture(ctx.stream) as gh:
             for L in range(NL):
                 (wg, _, _), (wu, _, _), (wd, _, _) = layers[0]
-                ctx.moe_dev(wg, idd[0].ptr, k, 1, T, xg.ptr, Y.ptr)
-                ctx.moe_dev(wu, idd[0].ptr, k, 1, T, xg.ptr, Y.ptr)
+                ctx.moe_multi_dev([wg, wu], idd[0].ptr, k, 1, T, xg.ptr, [Y.ptr, Y2.ptr])
                 ctx.moe_dev(wd, idd[0].ptr, k, k, T, xd.ptr, Y.ptr)
         ms_hot = time_graph(ctx, gh, max(5, args.steps // 5), 2) / NL
         uniq = float(np.mean([len(np.unique(i)) for i in ids_l]))
@@ -464,7 +465,7 @@ def run_moe(args):
                                      "T": T}}), flush=True)
         for a in idd:
             a.free()
-        xg.free(); xd.free(); Y.free()
+        xg.free(); xd.free(); Y.free(); Y2.free()
     ctx.close()
 
 

@@ -213,6 +213,15 @@ int spq4k_gemm_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *W, const
 int spq4k_mul_mat(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
 int spq4k_moe(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int64_t n_used,
               int64_t ne11, int64_t T, const float *X, float *Y);
+/* spq4k_moe_multi: the n (1 or 2) GGML_OP_MUL_MAT_ID nodes of one MoE layer
+ * that share ids and input, the expert up and gate banks
+ * (desktop/engine/src/forward.cpp:1100-1101: ggml_mul_mat_id(ffn_up_exps,
+ * cur, selected) and ggml_mul_mat_id(ffn_gate_exps, cur, selected)). Banks
+ * share type, K and E (M may differ); Y[i] is [T][n_used][M_i], each equal
+ * to spq4k_moe(banks[i], ...). Small batches of K-quant banks sweep both
+ * banks in one launch; otherwise the banks run one after the other. */
+int spq4k_moe_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *banks, const int32_t *ids,
+                    int64_t n_used, int64_t ne11, int64_t T, const float *X, float *const *Y);
 
 /* ---- the operations either side of the matvec ---------------------------
  * spq4k_rms_norm         : ggml_mul(ggml_rms_norm(x, eps), w) over T rows of K

@@ -1347,10 +1347,10 @@ int spq4k_mul_mat_swiglu(spq4k_ctx* c, const spq4k_weights* Wg, const spq4k_weig
     return 0;
 }
 
-int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t n_used, int64_t ne11,
-              int64_t T, const float* X, float* Y) {
-    int rc = use_device(c);
-    if (rc) return rc;
+namespace {
+
+int moe_check(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t n_used, int64_t ne11,
+              int64_t T, const float* X, const float* Y) {
     if (!bank || !bank->data || !ids || !X || !Y) return set_err(c, -EINVAL, "moe: null argument");
     if (T < 1 || n_used < 1 || n_used > bank->E || (ne11 != 1 && ne11 != n_used))
         return set_err(c, -EINVAL, "moe: T=%lld n_used=%lld ne11=%lld", (long long)T, (long long)n_used,
@@ -1358,6 +1358,150 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     if (!aligned(X, 16) || !aligned(bank->data, type_align(bank->type)) || !aligned(ids, 4))
         return set_err(c, -EINVAL, "moe: misaligned pointer");
     if (bank->E > 4096 || T * n_used > (1 << 24)) return set_err(c, -EINVAL, "moe: too many experts or pairs");
+    return 0;
+}
+
+// Small batches of a K-quant bank, or of two banks of one type, K and E
+// sharing ids and X (gate and up): the decode mapping, every routed pair's
+// rows (of both banks) in one sweep and one launch. An expert chosen twice
+// is streamed twice, so only for T <= 4. Returns 1 when it does not apply.
+int moe_decode_try(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, const int32_t* ids,
+                   int64_t n_used, int64_t ne11, int64_t T, const float* X, float* const* Y) {
+    const spq4k_weights* bank = banks[0];
+    const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
+    const int M1 = nbank > 1 ? (int)banks[1]->M : 0;
+    const size_t bb = type_block_bytes(bank->type);
+    const int64_t rows = T * ne11, n_pairs = T * n_used;
+    if (!(T <= 4 && n_pairs <= MOE_DEC_MAX_PAIRS && rows <= MOE_DEC_MAX_XROWS && moe_decode_supported(nb) &&
+          !c->moe_unfused && c->moe_mode == 0 && (size_t)q8lds_bytes((int)rows * nb) <= (size_t)LDS_BUDGET &&
+          n_pairs * (M + M1) <= INT32_MAX))
+        return 1;
+    MoeFusedParams f;
+    memset(&f, 0, sizeof f);
+    f.ids = ids;
+    f.X = X;
+    f.bank = bank->data;
+    f.expert_bytes = (size_t)M * nb * bb;
+    f.fmt = bank->fmt;
+    f.Y = Y[0];
+    f.n_pairs = (int32_t)n_pairs;
+    f.n_used = (int32_t)n_used;
+    f.ne11 = (int32_t)ne11;
+    f.K = (int32_t)bank->K;
+    f.M = M;
+    f.nb = nb;
+    f.E = E;
+    f.n_xrows = (int32_t)rows;
+    if (nbank > 1) {
+        f.bank1 = banks[1]->data;
+        f.expert_bytes1 = (size_t)M1 * nb * bb;
+        f.Y1 = Y[1];
+        f.M1 = M1;
+    }
+    const int64_t per_wg = moe_decode_rows_per_wg(nb);
+    const int64_t need = (n_pairs * (M + M1) + per_wg - 1) / per_wg;
+    const int grid = (int)(need < 2 * c->num_cus ? need : 2 * c->num_cus);
+    moe_decode_plan(f, grid, &f.rows_per_wg, &f.xwin_rows);
+    hipError_t e = launch_moe_decode(f, grid, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe decode launch");
+    return 0;
+}
+
+bool moe_ring_chosen(const spq4k_ctx* c, const spq4k_weights* bank, int64_t mean_pairs) {
+    return !c->moe_unfused && fmt_has_moe_ring(bank->fmt) && (bank->fmt == WF_Q4K || mean_pairs >= 2);
+}
+
+// The matrix-core expert kernel over one bank, or two of one type, K, E and M
+// sharing ids and X (gate and up): one prep launch (routing and the permuted
+// Q8_K planes), then one ring launch whose grid covers every bank.
+int moe_ring_run(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, const int32_t* ids, int64_t n_used,
+                 int64_t ne11, int64_t T, const float* X, float* const* Y) {
+    const spq4k_weights* bank = banks[0];
+    const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
+    const size_t bb = type_block_bytes(bank->type);
+    const int64_t rows = T * ne11, n_pairs = T * n_used;
+    const int64_t max_act = n_pairs < E ? n_pairs : E;
+    // scratch: Q8_K planes | routing tables
+    const size_t items = (size_t)rows * nb;
+    const size_t q8_bytes = (items * (256 + Q8MN_BYTES + 32 + 4) + 255) & ~(size_t)255;
+    const size_t route_bytes = (size_t)(1 + 3 * E + n_pairs) * sizeof(int32_t);
+    int rc = ensure_scratch(c, q8_bytes + route_bytes);
+    if (rc) return rc;
+    MoeParams p;
+    memset(&p, 0, sizeof p);
+    int32_t* rt = (int32_t*)(c->scratch + q8_bytes);
+    p.route.n_act = rt;
+    p.route.act = rt + 1;
+    p.route.act_off = rt + 1 + E;
+    p.route.act_cnt = rt + 1 + 2 * E;
+    p.route.pairs = rt + 1 + 3 * E;
+    p.bank = bank->data;
+    p.expert_bytes = (size_t)M * nb * bb;
+    p.fmt = bank->fmt;
+    p.Y = Y[0];
+    p.Q.qs = (int8_t*)c->scratch;
+    p.Q.mn = c->scratch + items * 256;
+    p.Q.bs = (int16_t*)(c->scratch + items * (256 + Q8MN_BYTES));
+    p.Q.d = (float*)(c->scratch + items * (256 + Q8MN_BYTES + 32));
+    p.M = M;
+    p.nb = nb;
+    p.n_used = (int)n_used;
+    p.ne11 = (int)ne11;
+    p.nbank = nbank;
+    p.max_act = (int32_t)max_act;
+    if (nbank > 1) {
+        p.bank1 = banks[1]->data;
+        p.Y1 = Y[1];
+    }
+    // row tiles a workgroup streams: as many as still leave two workgroups
+    // per CU over the experts (of every bank) that can be active
+    const int64_t ntiles = (M + 127) / 128;
+    int64_t rtw = ntiles * max_act * nbank / (2 * (int64_t)c->num_cus);
+    if (rtw < 1) rtw = 1;
+    if (rtw > ntiles) rtw = ntiles;
+    p.ring_rt = (int32_t)rtw;
+    p.tiles_per_expert = (int32_t)((ntiles + rtw - 1) / rtw);
+    if (max_act * p.tiles_per_expert * nbank > (1ll << 31) - 1 || rows * nb / 16 > (1ll << 31) - 2)
+        return set_err(c, -EINVAL, "moe: grid too large");
+    const hipError_t e = launch_moe_ring(p, ids, (int)n_pairs, E, X, bank->K, (int)rows, (int)max_act, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe ring launch");
+    return 0;
+}
+
+}  // namespace
+
+int spq4k_moe_multi(spq4k_ctx* c, int n, const spq4k_weights* const* banks, const int32_t* ids, int64_t n_used,
+                    int64_t ne11, int64_t T, const float* X, float* const* Y) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (n < 1 || n > 2 || !banks || !Y) return set_err(c, -EINVAL, "moe_multi: n=%d banks (1..2)", n);
+    for (int i = 0; i < n; ++i) {
+        rc = moe_check(c, banks[i], ids, n_used, ne11, T, X, Y[i]);
+        if (rc) return rc;
+        if (banks[i]->type != banks[0]->type || banks[i]->K != banks[0]->K || banks[i]->E != banks[0]->E)
+            return set_err(c, -EINVAL, "moe_multi: banks must share type, K and E");
+    }
+    if (n == 2 && banks[0]->fmt != WF_Q80) {
+        rc = moe_decode_try(c, banks, 2, ids, n_used, ne11, T, X, Y);
+        if (rc <= 0) return rc;
+        const int64_t n_pairs = T * n_used, max_act = n_pairs < banks[0]->E ? n_pairs : banks[0]->E;
+        if (banks[1]->M == banks[0]->M && c->moe_mode != 3 &&
+            moe_ring_chosen(c, banks[0], (n_pairs + max_act - 1) / max_act))
+            return moe_ring_run(c, banks, 2, ids, n_used, ne11, T, X, Y);
+    }
+    for (int i = 0; i < n; ++i) {
+        rc = spq4k_moe(c, banks[i], ids, n_used, ne11, T, X, Y[i]);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t n_used, int64_t ne11,
+              int64_t T, const float* X, float* Y) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    rc = moe_check(c, bank, ids, n_used, ne11, T, X, Y);
+    if (rc) return rc;
     if (bank->fmt == WF_Q80) return q80_moe(c, bank, ids, n_used, ne11, T, X, Y);
     const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
     const size_t bb = type_block_bytes(bank->type);
@@ -1375,34 +1519,12 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     const int tiles_per_expert = (M + rows_per_tile - 1) / rows_per_tile;
     const int cb_max = LDS_BUDGET / (tc * 292);
     const int chunk_blocks = nb < cb_max ? nb : cb_max;
-    // small batches: the decode mapping (every routed pair's rows in one
-    // sweep; an expert chosen twice is streamed twice, so only for T <= 4)
-    if (T <= 4 && n_pairs <= MOE_DEC_MAX_PAIRS && rows <= MOE_DEC_MAX_XROWS && moe_decode_supported(nb) &&
-        !c->moe_unfused && c->moe_mode == 0 &&
-        (size_t)q8lds_bytes((int)rows * nb) <= (size_t)LDS_BUDGET) {
-        MoeFusedParams f;
-        memset(&f, 0, sizeof f);
-        f.ids = ids;
-        f.X = X;
-        f.bank = bank->data;
-        f.expert_bytes = (size_t)M * nb * bb;
-        f.fmt = bank->fmt;
-        f.Y = Y;
-        f.n_pairs = (int32_t)n_pairs;
-        f.n_used = (int32_t)n_used;
-        f.ne11 = (int32_t)ne11;
-        f.K = (int32_t)bank->K;
-        f.M = M;
-        f.nb = nb;
-        f.E = E;
-        f.n_xrows = (int32_t)rows;
-        const int64_t per_wg = moe_decode_rows_per_wg(nb);
-        const int64_t need = (n_pairs * M + per_wg - 1) / per_wg;
-        const int grid = (int)(need < 2 * c->num_cus ? need : 2 * c->num_cus);
-        moe_decode_plan(f, grid, &f.rows_per_wg, &f.xwin_rows);
-        hipError_t e = launch_moe_decode(f, grid, c->stream);
-        if (e != hipSuccess) return hip_fail(c, e, "moe decode launch");
-        return 0;
+    // small batches: the decode mapping
+    {
+        const spq4k_weights* b1[1] = {bank};
+        float* y1[1] = {Y};
+        rc = moe_decode_try(c, b1, 1, ids, n_used, ne11, T, X, y1);
+        if (rc <= 0) return rc;
     }
     if (c->moe_mode == 3 && n_pairs <= MOE_FUSED_MAX_PAIRS && !c->moe_unfused) {
         MoeFusedParams f;
@@ -1427,6 +1549,16 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
         if (e != hipSuccess) return hip_fail(c, e, "moe fused launch");
         return 0;
     }
+    // matrix cores unless the sdot4 kernels are asked for (SPQ4K_MOE_UNFUSED);
+    // a Q6_K or Q5_K bank's operand preparation costs more, so its experts go
+    // to the matrix cores only once they receive two pairs on average
+    // (measured on the Q6_K 2048 x 768 down bank: T = 8 sdot4 31 us against
+    // 36, T = 32 65 against 61)
+    if (moe_ring_chosen(c, bank, mean_pairs)) {
+        const spq4k_weights* b1[1] = {bank};
+        float* y1[1] = {Y};
+        return moe_ring_run(c, b1, 1, ids, n_used, ne11, T, X, y1);
+    }
     // scratch: Q8_K planes | routing tables
     const size_t items = (size_t)rows * nb;
     const size_t q8_bytes = (items * (256 + Q8MN_BYTES + 32 + 4) + 255) & ~(size_t)255;
@@ -1445,19 +1577,10 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     p.route.act_off = rt + 1 + E;
     p.route.act_cnt = rt + 1 + 2 * E;
     p.route.pairs = rt + 1 + 3 * E;
-    // matrix cores unless the sdot4 kernels are asked for (SPQ4K_MOE_UNFUSED);
-    // a Q6_K or Q5_K bank's operand preparation costs more, so its experts go
-    // to the matrix cores only once they receive two pairs on average
-    // (measured on the Q6_K 2048 x 768 down bank: T = 8 sdot4 31 us against
-    // 36, T = 32 65 against 61)
-    const bool ring = !c->moe_unfused && fmt_has_moe_ring(bank->fmt) && (bank->fmt == WF_Q4K || mean_pairs >= 2);
-    hipError_t e;
-    if (!ring) {
-        e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, mn, false, c->stream);
-        if (e != hipSuccess) return hip_fail(c, e, "moe quantize launch");
-        e = launch_moe_route(ids, (int)n_pairs, E, p.route, c->stream);
-        if (e != hipSuccess) return hip_fail(c, e, "moe route launch");
-    }
+    hipError_t e = launch_quantize_q8k_planes(X, bank->K, (int)rows, nb, qs, bs, d, mn, false, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe quantize launch");
+    e = launch_moe_route(ids, (int)n_pairs, E, p.route, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe route launch");
     p.bank = bank->data;
     p.expert_bytes = (size_t)M * nb * bb;
     p.fmt = bank->fmt;
@@ -1470,21 +1593,6 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     p.nb = nb;
     p.n_used = (int)n_used;
     p.ne11 = (int)ne11;
-    if (ring) {
-        // row tiles a workgroup streams: as many as still leave two
-        // workgroups per CU over the experts that can be active
-        const int64_t ntiles = (M + 127) / 128;
-        int64_t rtw = ntiles * max_act / (2 * (int64_t)c->num_cus);
-        if (rtw < 1) rtw = 1;
-        if (rtw > ntiles) rtw = ntiles;
-        p.ring_rt = (int32_t)rtw;
-        p.tiles_per_expert = (int32_t)((ntiles + rtw - 1) / rtw);
-        if (max_act * p.tiles_per_expert > (1ll << 31) - 1 || rows * nb / 16 > (1ll << 31) - 2)
-            return set_err(c, -EINVAL, "moe: grid too large");
-        e = launch_moe_ring(p, ids, (int)n_pairs, E, X, bank->K, (int)rows, (int)max_act, c->stream);
-        if (e != hipSuccess) return hip_fail(c, e, "moe ring launch");
-        return 0;
-    }
     p.tiles_per_expert = tiles_per_expert;
     p.chunk_blocks = chunk_blocks;
     const int64_t grid = max_act * p.tiles_per_expert;

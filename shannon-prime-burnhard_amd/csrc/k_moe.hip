@@ -284,7 +284,10 @@ __global__ __launch_bounds__(WAVES * 64) void moe_fused_kernel(MoeFusedParams p)
 // work on one row (quarter l4 of blocks bsub, bsub + BSL, ...) and waves walk
 // rows g, g + G, ... of the sweep. An expert chosen by several pairs is
 // streamed once per pair, which is why this form is kept to small batches.
-// An id outside [0, E) leaves that pair's outputs untouched.
+// An id outside [0, E) leaves that pair's outputs untouched. With a second
+// bank (p.M1 > 0: the up projection beside the gate, the same ids and input)
+// pair p owns rows [p (M + M1), (p + 1)(M + M1)): M rows of the first bank,
+// then M1 of the second, so both go in one launch and one quantisation.
 template <typename Fmt, int NB, int BSL, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p) {
     using W = typename Fmt::W;
@@ -297,15 +300,17 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     const int wave = threadIdx.x >> 6;
     const int l4 = lane & 3;
     const int bsub = (lane & (LPR - 1)) >> 2;
-    const int M = p.M;
-    const int total = p.n_pairs * M;
+    // a pair's sweep rows: the M rows of the bank, then the M1 rows of the
+    // second bank when there is one (same expert, same input row)
+    const int M = p.M, MV = p.M + p.M1;
+    const int total = p.n_pairs * MV;
     // this workgroup's rows of the sweep: one contiguous run (one or two
     // pairs), so it quantises only the input rows those pairs read
     const int r0 = blockIdx.x * p.rows_per_wg;
     if (r0 >= total) return;                     // uniform over the workgroup
     const int r1 = min(total, r0 + p.rows_per_wg);
     auto xrow = [&](int r) {                     // input row of sweep row r (non-decreasing in r)
-        const int pr = r / M;
+        const int pr = r / MV;
         const int t = pr / p.n_used;
         return t * p.ne11 + (pr - t * p.n_used) % p.ne11;
     };
@@ -314,20 +319,27 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     const Q8Lds L = q8lds_carve(smem, p.xwin_rows * NB);
     const int g0 = r0 + wave * RPW + lane / LPR;
 
-    // where row r of the sweep lives: expert (or -1), its row, its input window slot
+    // where row r of the sweep lives: expert (or -1), its weights and output,
+    // its input window slot
     struct Loc {
         const uint8_t* w;
-        int e, lr, xs;
+        float* y;
+        int e, xs;
     };
     auto locate = [&](int r) {
         Loc l;
         const int rc = r < r1 ? r : r1 - 1;
-        const int pr = rc / M;
-        l.lr = rc - pr * M;
+        const int pr = rc / MV;
+        const int v = rc - pr * MV;
+        const bool second = v >= M;
+        const int lr = second ? v - M : v;
         const int e = p.ids[pr];
         l.e = (r < r1 && e >= 0 && e < p.E) ? e : -1;
         l.xs = (xrow(rc) - xlo) * NB;
-        l.w = p.bank + (size_t)(l.e >= 0 ? l.e : 0) * p.expert_bytes + (size_t)l.lr * ((size_t)NB * Fmt::BYTES);
+        const size_t eo = (size_t)(l.e >= 0 ? l.e : 0);
+        l.w = (second ? p.bank1 + eo * p.expert_bytes1 : p.bank + eo * p.expert_bytes) +
+              (size_t)lr * ((size_t)NB * Fmt::BYTES);
+        l.y = second ? p.Y1 + (int64_t)pr * p.M1 + lr : p.Y + (int64_t)pr * M + lr;
         return l;
     };
     auto load = [&](const Loc& l, W (&w)[NIT]) {
@@ -363,7 +375,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
             Fmt::template dot<1>(w[it], l4, L, cur.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && cur.e >= 0, acc);
         }
         const float sum = group_sum_last<LPR>(acc[0]);
-        if (cur.e >= 0 && (lane & (LPR - 1)) == LPR - 1) p.Y[(int64_t)(r / M) * M + cur.lr] = sum;
+        if (cur.e >= 0 && (lane & (LPR - 1)) == LPR - 1) *cur.y = sum;
         if (r + RPG < r1) {
             cur = locate(r + RPG);
             load(cur, w);
@@ -387,13 +399,14 @@ int moe_decode_rows_per_wg(int nb) { return nb == 3 ? 32 : (nb == 8 ? 16 : 8); }
 // rows per workgroup (a whole number of passes) and the input rows the
 // largest run of that many sweep rows can read
 void moe_decode_plan(const MoeFusedParams& p, int grid, int32_t* rows_per_wg, int32_t* xwin_rows) {
-    const int64_t total = (int64_t)p.n_pairs * p.M;
+    const int64_t MV = (int64_t)p.M + p.M1;
+    const int64_t total = (int64_t)p.n_pairs * MV;
     const int64_t pass = moe_decode_rows_per_wg(p.nb);
     int64_t rw = (total + grid - 1) / grid;
     rw = (rw + pass - 1) / pass * pass;
     *rows_per_wg = (int32_t)rw;
-    // a run of rw rows touches at most rw / M + 2 pairs, so as many input rows
-    const int64_t w = rw / p.M + 2;
+    // a run of rw rows touches at most rw / MV + 2 pairs, so as many input rows
+    const int64_t w = rw / MV + 2;
     *xwin_rows = (int32_t)(w < p.n_xrows ? w : p.n_xrows);
 }
 
@@ -532,8 +545,12 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
     constexpr int Q_OFF = W_LOADS * 1024, M_OFF = Q_OFF + Q_LOADS * 1024;
     __shared__ __align__(1024) uint8_t lds[S][STAGE];
 
-    const int a = blockIdx.x / p.tiles_per_expert;
-    const int g = blockIdx.x - a * p.tiles_per_expert;
+    // workgroups of the second bank (if any) follow the first bank's
+    const int half = p.max_act * p.tiles_per_expert;
+    const bool second = p.nbank > 1 && (int)blockIdx.x >= half;
+    const int bid = (int)blockIdx.x - (second ? half : 0);
+    const int a = bid / p.tiles_per_expert;
+    const int g = bid - a * p.tiles_per_expert;
     if (a >= *p.route.n_act) return;           // uniform over the workgroup
     const int e = p.route.act[a];
     const int poff = p.route.act_off[a];
@@ -547,7 +564,8 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
     const int rt0 = g * p.ring_rt;
     const int nrt = min(p.ring_rt, (M + ROWS - 1) / ROWS - rt0);
     const int len = nrt * nb;                  // super-blocks streamed per token tile
-    const uint8_t* __restrict__ W = p.bank + (size_t)e * p.expert_bytes;
+    const uint8_t* __restrict__ W = (second ? p.bank1 : p.bank) + (size_t)e * p.expert_bytes;
+    float* __restrict__ Yb = second ? p.Y1 : p.Y;
     const size_t row_bytes = (size_t)nb * BB;
 
     for (int tile0 = 0; tile0 < pcnt; tile0 += TOK) {
@@ -621,7 +639,7 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
                 if (tile0 + c16 < pcnt) {
                     const int pid = p.route.pairs[poff + tile0 + c16];
                     const int rq = (rt0 + sp / nb) * ROWS + wave * 16 + 4 * q;
-                    float* y = p.Y + (int64_t)pid * M + rq;
+                    float* y = Yb + (int64_t)pid * M + rq;
                     if ((M & 3) == 0 && rq + 3 < M) {
                         *reinterpret_cast<v4f*>(y) = acc[0][0];
                     } else {
@@ -653,7 +671,7 @@ hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, 
                        ids, n_pairs, E, p.route, X, x_tstride, n_xrows, p.nb, p.Q);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int64_t grid = (int64_t)max_act * p.tiles_per_expert;
+    const int64_t grid = (int64_t)max_act * p.tiles_per_expert * (p.nbank > 1 ? 2 : 1);
     if (p.fmt == WF_Q6K)
         hipLaunchKernelGGL((moe_ring_kernel<3, 1>), dim3((unsigned)grid), dim3(512), 0, st, p);
     else if (p.fmt == WF_Q5K)

@@ -88,6 +88,12 @@ struct MoeParams {
     int32_t tiles_per_expert;
     int32_t chunk_blocks;
     int32_t fmt;             // WFmt of the bank
+    // moe_ring_kernel: a second bank of the same type, K, E and M sharing the
+    // routing and planes (gate and up); its workgroups follow the first
+    // bank's max_act * tiles_per_expert. nbank 0 or 1: one bank.
+    const uint8_t* bank1;
+    float* Y1;
+    int32_t nbank, max_act;
 };
 
 hipError_t launch_moe_route(const int32_t* ids, int n_pairs, int E, const MoeRoute& r, hipStream_t st);
@@ -108,6 +114,12 @@ struct MoeFusedParams {
     int32_t rows_per_wg;   // moe_decode_kernel: contiguous sweep rows a workgroup (moe_decode_plan)
     int32_t xwin_rows;     // moe_decode_kernel: input rows quantised by a workgroup at most
     int32_t fmt;           // WFmt of the bank
+    // moe_decode_kernel only: a second bank of the same type, K and E (the up
+    // projection beside the gate) swept in the same launch; M1 = 0 for none
+    const uint8_t* bank1;
+    size_t expert_bytes1;
+    float* Y1;               // [T][n_used][M1]
+    int32_t M1;
 };
 hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st);
 

@@ -98,6 +98,7 @@ def load_library(path: str | None = None):
         "spq4k_gemm_multi": (I, [V, I, V, V, V, I64]),
         "spq4k_mul_mat": (I, [V, V, V, V, I64]),
         "spq4k_moe": (I, [V, V, V, I64, I64, I64, V, V]),
+        "spq4k_moe_multi": (I, [V, I, PV, V, I64, I64, I64, V, PV]),
         "spq4k_mul_mat_host": (I, [V, V, V, V, I64]),
         "spq4k_moe_host": (I, [V, V, V, I64, I64, I64, V, V]),
         "spq4k_subblock_sums": (I, [V, V, I64, I64, V, V]),
@@ -502,6 +503,14 @@ class Context:
 
     def moe_dev(self, bank: Weights, ids_dev: int, n_used: int, ne11: int, T: int, X_dev: int, Y_dev: int):
         self._check("spq4k_moe", self.lib.spq4k_moe(self.handle, bank.handle, ids_dev, n_used, ne11, T, X_dev, Y_dev))
+
+    def moe_multi_dev(self, banks, ids_dev: int, n_used: int, ne11: int, T: int, X_dev: int, Y_devs):
+        """spq4k_moe_multi: banks sharing ids and input (gate and up), Y_devs[i] per bank."""
+        n = len(banks)
+        hb = (C.c_void_p * n)(*[b.handle.value if isinstance(b.handle, C.c_void_p) else b.handle for b in banks])
+        yb = (C.c_void_p * n)(*Y_devs)
+        self._check("spq4k_moe_multi", self.lib.spq4k_moe_multi(self.handle, n, hb, ids_dev, n_used, ne11, T,
+                                                               X_dev, yb))
 
     def dequant_dev(self, vx: int, y: int, k: int):
         self._check("spq4k_dequant", self.lib.spq4k_dequant(self.handle, vx, y, k))

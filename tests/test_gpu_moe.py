@@ -139,3 +139,57 @@ def test_moe_device_ids_out_of_range_leave_outputs(oracle, mode):
         _check(Y[t, s], exp[t, s], f"slot {t},{s}")
     bank.free()
     ctx.close()
+
+
+@pytest.mark.parametrize("qtype", [12, 13, 14, 8])
+@pytest.mark.parametrize("T,ne11", [(1, 1), (3, 8), (4, 1), (8, 1), (32, 8)])
+@pytest.mark.parametrize("shapes", [(768, 768), (768, 512)])
+def test_moe_multi(ctx, oracle, qtype, T, ne11, shapes):
+    """spq4k_moe_multi: two banks sharing ids and input (gate and up of 768
+    rows; a second bank of 512 rows) in one call, each output bit for bit the
+    one spq4k_moe gives that bank alone (both the two-bank sweep and the
+    two-bank expert ring run every row with the same arithmetic), and within
+    tolerance of the oracle. K-quant banks: T <= 4 sweeps both banks in one
+    launch; larger batches of banks of equal rows share one prep and one
+    ring launch; the rest run the banks one after the other."""
+    from spq4k.hip import DeviceArray
+    E, k, K = 32, 8, 2048
+    rng = np.random.default_rng(900 + 10 * T + ne11 + qtype + shapes[1])
+    hosts, banks = [], []
+    for M in shapes:
+        # the GPU encoder (bit-exact with ggml's, pinned in the per-type tests)
+        x = (rng.standard_normal((E * M, K)) * 0.02).astype(np.float32)
+        h = ctx.quantize_chunk(x, E * M, K, type=qtype)
+        hosts.append(h)
+        banks.append(ctx.upload(h, M, K, E, type=qtype))
+    ids = _topk_ids(rng, T, E, k)
+    X = rng.standard_normal((T, ne11, K)).astype(np.float32)
+    idd, xd = DeviceArray.from_host(ids), DeviceArray.from_host(X)
+    ym = [DeviceArray((T, k, M)) for M in shapes]
+    ys = [DeviceArray((T, k, M)) for M in shapes]
+    ctx.moe_multi_dev(banks, idd.ptr, k, ne11, T, xd.ptr, [y.ptr for y in ym])
+    for b, y in zip(banks, ys):
+        ctx.moe_dev(b, idd.ptr, k, ne11, T, xd.ptr, y.ptr)
+    ctx.synchronize()
+    for i, (M, h) in enumerate(zip(shapes, hosts)):
+        got, alone = ym[i].to_host(), ys[i].to_host()
+        np.testing.assert_array_equal(got.view(np.uint32), alone.view(np.uint32), err_msg=f"bank {i} M={M}")
+        if i == 0:
+            exp = (oracle.mul_mat_id_q8_0(h, M, K, E, X, ids) if qtype == 8
+                   else oracle.mul_mat_id_type(qtype, h, M, K, E, X, ids))
+            _check(got, exp, f"type {qtype} T={T} ne11={ne11} bank {i}")
+
+
+def test_moe_multi_errors(ctx, oracle):
+    from spq4k import Spq4kError
+    from spq4k.hip import DeviceArray
+    rng = np.random.default_rng(7)
+    E, M, K = 4, 64, 256
+    a = ctx.upload(oracle.quantize(12, (rng.standard_normal((E * M, K)) * 0.02).astype(np.float32)), M, K, E)
+    b = ctx.upload(oracle.quantize(14, (rng.standard_normal((E * M, K)) * 0.02).astype(np.float32)), M, K, E,
+                   type=14)
+    ids, x, y = DeviceArray.from_host(np.zeros((1, 2), np.int32)), DeviceArray(K), DeviceArray(2 * M)
+    with pytest.raises(Spq4kError):   # types differ
+        ctx.moe_multi_dev([a, b], ids.ptr, 2, 1, 1, x.ptr, [y.ptr, y.ptr])
+    with pytest.raises(Spq4kError):   # three banks
+        ctx.moe_multi_dev([a, a, a], ids.ptr, 2, 1, 1, x.ptr, [y.ptr, y.ptr, y.ptr])
