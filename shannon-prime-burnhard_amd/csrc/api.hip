@@ -43,6 +43,7 @@ struct spq4k_ctx {
     int dec_xfirst_set = 0;
     int q80_grid = 0;            // SPQ4K_Q80_GRID: workgroups of the Q8_0 matvec, 0 automatic
     int q80_preq = 0;            // SPQ4K_Q80_PREQ: 0 auto, 1 always quantise x once up front, 2 never
+    int q80_staged = 1;          // SPQ4K_Q80_STAGED: 0 direct block loads only, 1 staging where it measured faster, 2 staging wherever it fits
     char err[256] = {0};
 };
 
@@ -361,6 +362,25 @@ int q80_dense(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X
     bool preq = T > 1 || tmax < 1;
     if (c->q80_preq == 1) preq = true;
     if (c->q80_preq == 2 && T <= tmax) preq = false;
+    // decode, K a multiple of 256: the weight-staging kernel (contiguous
+    // loads) where it measured faster on MI355X (cold, us, staged / direct):
+    // 151936 x 4096 128.6 / 149.7, 1024 x 4096 6.2 / 7.5, 2048 x 4096
+    // 6.7 / 7.6; not for the mid shapes (4096 x 4096 8.6 / 8.2, 12288 x 4096
+    // 16.4 / 15.3, 4096 x 12288 19.3 / 18.6, 1024 x 12288 12.8 / 11.3) nor
+    // T > 1 (its LDS then leaves one workgroup a CU: T = 8 15.3 / 13.8)
+    const bool staged_wins = total >= 65536 || (total <= 2048 && nb <= 128);
+    if (c->q80_staged && T == 1 && (staged_wins || c->q80_staged == 2) && q80_staged_fits((int)T, nb) &&
+        q80_staged_lds_bytes((int)T, nb) <= c->lds_max) {
+        if (preq) {
+            int rc = q80_planes(c, X, K, T, nb, &p);
+            if (rc) return rc;
+        }
+        p.n_xrows = (int32_t)T;
+        const int grid = q80_staged_grid(total, (int)T, nb, c->num_cus, c->lds_max);
+        hipError_t e = launch_gemv_q8_0_staged(p, (int)T, grid, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "gemv_q8_0 (staged) launch");
+        return 0;
+    }
     if (!preq) {
         p.n_xrows = (int32_t)T;
         hipError_t e = launch_gemv_q8_0(p, (int)T, false, q80_grid(c, total, nb, T), c->stream);
@@ -599,6 +619,10 @@ int spq4k_init(int device, spq4k_ctx** out) {
     if (const char* f = getenv("SPQ4K_Q80_GRID")) {
         const int v = atoi(f);
         if (v > 0 && v <= 65536) c->q80_grid = v;
+    }
+    if (const char* f = getenv("SPQ4K_Q80_STAGED")) {
+        const int v = atoi(f);
+        if (v >= 0 && v <= 2) c->q80_staged = v;
     }
     if (const char* f = getenv("SPQ4K_Q80_PREQ")) {
         const int v = atoi(f);

@@ -335,6 +335,100 @@ __device__ __forceinline__ void q80_dense_store(const Q80Params& p, int r, int t
     }
 }
 
+// Dense, K a multiple of 256 (eight-block chunks of a row start 16-byte
+// aligned): the weights stream through a double buffer of each wave in LDS,
+// Q80S_CB blocks (2176 bytes) at a time, by contiguous 16-byte
+// global_load_lds, and are read back with unaligned LDS reads. The 34-byte
+// block stride of direct loads keeps the texture addresser busy (each
+// wave-wide 16-byte load spans 2 KB); contiguous lanes do not. A wave takes
+// one row at a time, lane g block g of each chunk; its (row, chunk) items
+// form one stream with the next item always in flight, across rows too.
+// Activations in LDS as in gemv_q8_0_kernel; the per-block combine is its.
+constexpr int Q80S_CB = 64;
+constexpr int Q80S_SLOTS = Q80S_CB * Q80_BYTES / 16;          // 136
+constexpr int Q80S_LOADS = (Q80S_SLOTS + 63) / 64;             // 3 wave-wide loads a chunk
+constexpr int Q80S_BUF = Q80S_LOADS * 1024;
+size_t q80s_weight_lds() { return (size_t)Q80_WAVES * 2 * Q80S_BUF; }
+
+template <int T>
+__global__ __launch_bounds__(Q80_WAVES * 64) void gemv_q8_0_staged_kernel(Q80Params p) {
+    extern __shared__ __align__(1024) char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = p.nb;
+    const size_t row_bytes = (size_t)nb * Q80_BYTES;
+    const int total = p.total_rows;
+    const int S = gridDim.x * Q80_WAVES;
+    const int rw0 = blockIdx.x * Q80_WAVES + wave;
+    const int nch = (nb + Q80S_CB - 1) / Q80S_CB;
+    const int nrow = rw0 < total ? (total - 1 - rw0) / S + 1 : 0;
+    const int nitem = nrow * nch;
+    // the weight buffers sit behind the activations, at a 1 KB boundary
+    const size_t act = ((size_t)p.n_xrows * nb * (QK80 + 4) + 1023) & ~(size_t)1023;   // q80_lds_bytes
+    uint8_t* wbuf = reinterpret_cast<uint8_t*>(smem) + act + (size_t)wave * 2 * Q80S_BUF;
+    auto issue = [&](int i) {
+        const int ri = i / nch, c = i - ri * nch;
+        const uint8_t* wr = q80_dense_row(p, rw0 + ri * S, row_bytes);
+        const size_t lim = row_bytes - 16;
+#pragma unroll
+        for (int k = 0; k < Q80S_LOADS; ++k) {
+            size_t o = (size_t)c * (Q80S_CB * Q80_BYTES) + (size_t)(k * 64 + lane) * 16;
+            o = o < lim ? o : lim;                 // past the row's end: a valid address, never read back
+            __builtin_amdgcn_global_load_lds((const void*)(wr + o),
+                                             (__attribute__((address_space(3))) void*)(wbuf + (i & 1) * Q80S_BUF + k * 1024),
+                                             16, 0, 0);
+        }
+    };
+    q80_stage(p, smem);
+    const int8_t* aq = reinterpret_cast<const int8_t*>(smem);
+    const float* ad = reinterpret_cast<const float*>(smem + (size_t)p.n_xrows * nb * QK80);
+    const int64_t K = (int64_t)nb * QK80;
+    if (nitem > 0) issue(0);
+    float acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = 0.0f;
+    for (int i = 0; i < nitem; ++i) {
+        // the buffer refilled next was read in the previous item (its LDS
+        // reads have returned: their values were used)
+        if (i + 1 < nitem) {
+            issue(i + 1);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Q80S_LOADS) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        const int ri = i / nch, c = i - ri * nch;
+        const int b = c * Q80S_CB + lane;
+        if (b < nb) {
+            const uint8_t* q = wbuf + (i & 1) * Q80S_BUF + lane * Q80_BYTES;
+            uint16_t h;
+            uint4 lo, hi;
+            __builtin_memcpy(&h, q, 2);
+            __builtin_memcpy(&lo, q + 2, 16);
+            __builtin_memcpy(&hi, q + 18, 16);
+            const float dw = half_bits_to_float(h);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const int4* a = reinterpret_cast<const int4*>(aq + t * K + (int64_t)b * QK80);
+                const int4 a0 = a[0], a1 = a[1];
+                int sm = dot4((int)lo.x, a0.x, 0);
+                sm = dot4((int)lo.y, a0.y, sm);
+                sm = dot4((int)lo.z, a0.z, sm);
+                sm = dot4((int)lo.w, a0.w, sm);
+                sm = dot4((int)hi.x, a1.x, sm);
+                sm = dot4((int)hi.y, a1.y, sm);
+                sm = dot4((int)hi.z, a1.z, sm);
+                sm = dot4((int)hi.w, a1.w, sm);
+                acc[t] = fmaf(dw * ad[t * (int64_t)nb + b], (float)sm, acc[t]);
+            }
+        }
+        if (c == nch - 1) {
+            q80_dense_store<64, T>(p, rw0 + ri * S, total, lane, acc);
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = 0.0f;
+        }
+    }
+}
+
 // Dense: the rows of up to four matrices sharing the input (segments), T
 // tokens, activation row t for token t; y[t * y_tstride + r]. GX: the
 // activations are read from the global planes p.Aq / p.Ad (rows too long
@@ -654,6 +748,45 @@ static hipError_t launch_gemv_q80_t(const Q80Params& p, int grid, hipStream_t st
     return hipGetLastError();
     SPQ_Q80_SHAPES(SPQ_GO)
 #undef SPQ_GO
+}
+
+template <int T>
+static hipError_t launch_q80_staged_t(const Q80Params& p, int grid, hipStream_t st) {
+    const size_t lds = ((q80_lds_bytes(p.n_xrows, p.nb) + 1023) & ~(size_t)1023) + q80s_weight_lds();
+    hipLaunchKernelGGL((gemv_q8_0_staged_kernel<T>), dim3(grid), dim3(Q80_WAVES * 64), lds, st, p);
+    return hipGetLastError();
+}
+
+bool q80_staged_fits(int T, int nb) {
+    return nb % 8 == 0 && nb >= Q80S_CB && T >= 1 && T <= 8 &&
+           ((q80_lds_bytes(T, nb) + 1023) & ~(size_t)1023) + q80s_weight_lds() <= (size_t)Q80_LDS_MAX;
+}
+
+int q80_staged_grid(int64_t rows, int T, int nb, int num_cus, size_t lds_max) {
+    const int64_t need = (rows + Q80_WAVES - 1) / Q80_WAVES;   // one row a wave at a time
+    const size_t per = ((q80_lds_bytes(T, nb) + 1023) & ~(size_t)1023) + q80s_weight_lds();
+    const int64_t fit = lds_max / per >= 2 ? 2 : 1;           // workgroups a CU can hold, up to two
+    const int64_t cap = fit * num_cus;
+    return (int)(need < cap ? need : cap);
+}
+
+size_t q80_staged_lds_bytes(int T, int nb) {
+    return ((q80_lds_bytes(T, nb) + 1023) & ~(size_t)1023) + q80s_weight_lds();
+}
+
+hipError_t launch_gemv_q8_0_staged(const Q80Params& p, int T, int grid, hipStream_t st) {
+    if (grid < 1 || p.n_xrows != T || !q80_staged_fits(T, p.nb)) return hipErrorInvalidValue;
+    switch (T) {
+        case 1: return launch_q80_staged_t<1>(p, grid, st);
+        case 2: return launch_q80_staged_t<2>(p, grid, st);
+        case 3: return launch_q80_staged_t<3>(p, grid, st);
+        case 4: return launch_q80_staged_t<4>(p, grid, st);
+        case 5: return launch_q80_staged_t<5>(p, grid, st);
+        case 6: return launch_q80_staged_t<6>(p, grid, st);
+        case 7: return launch_q80_staged_t<7>(p, grid, st);
+        case 8: return launch_q80_staged_t<8>(p, grid, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemv_q8_0(const Q80Params& p, int T, bool global_acts, int grid, hipStream_t st) {

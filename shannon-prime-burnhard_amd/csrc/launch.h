@@ -228,6 +228,12 @@ struct Q80Params {
     int32_t rows_per_wg;         // grouped: rows of the expert a workgroup takes
 };
 size_t q80_lds_bytes(int xrows, int nb);
+// the weight-staging matvec (K a multiple of 256, activations in LDS):
+// whether T tokens of nb blocks fit, its LDS, and its launch
+bool q80_staged_fits(int T, int nb);
+size_t q80_staged_lds_bytes(int T, int nb);
+int q80_staged_grid(int64_t rows, int T, int nb, int num_cus, size_t lds_max);
+hipError_t launch_gemv_q8_0_staged(const Q80Params& p, int T, int grid, hipStream_t st);
 int q80_lanes_per_row(int nb);
 int q80_rows_per_wg(int nb);
 hipError_t launch_quantize_q8_0(const float* x, uint8_t* y, int64_t nblocks, bool ref_encoder, hipStream_t st);

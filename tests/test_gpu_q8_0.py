@@ -9,7 +9,8 @@ reference in test_oracle_q8_0.py):
     them away from zero): bit-exact;
   - integer block sums: bit-exact against the oracle's brute force;
   - vec_dot, the matvec at every lanes-per-row shape (K from 32 to 147456,
-    the last too long for LDS), batches (over 8 tokens and K a multiple of
+    the last too long for LDS) and its weight-staging form (K a multiple of
+    256: contiguous loads into per-wave LDS buffers), batches (over 8 tokens and K a multiple of
     256: the matrix-core ring, every launch shape, K splits, the int8 ends;
     otherwise the matvec over token slices), several matrices in one launch
     and the expert-gathered matvec (one sweep for small batches, grouped by
@@ -210,7 +211,9 @@ def test_gemv_large_m(ctx, oracle):
     _check_bounded(got, exact, mag, K // QK, "q8_0 gemv 151936 x 4096")
 
 
-@pytest.mark.parametrize("env", [{}, {"SPQ4K_Q80_GRID": 1}, {"SPQ4K_Q80_GRID": 7}, {"SPQ4K_Q80_PREQ": 1},
+@pytest.mark.parametrize("env", [{}, {"SPQ4K_Q80_STAGED": 0}, {"SPQ4K_Q80_STAGED": 2}, {"SPQ4K_Q80_GRID": 1},
+                                 {"SPQ4K_Q80_GRID": 7},
+                                 {"SPQ4K_Q80_STAGED": 0, "SPQ4K_Q80_PREQ": 1}, {"SPQ4K_Q80_PREQ": 1},
                                  {"SPQ4K_Q80_PREQ": 2}])
 def test_launch_shapes(oracle, env):
     rng = np.random.default_rng(806)
