@@ -103,10 +103,10 @@ size_t spq4k_weights_nbytes(const spq4k_weights *w);
  * ggml-common.h:241-245, K a multiple of 32), as ggml_backend_tensor_set
  * uploads a tensor of any type (llama_weights.cpp:483-560). The plain forms
  * above are type Q4_K. Every matmul entry point below takes weights of any
- * of these types (Q5_K and Q8_0 batches run on the sdot4 kernels, Q4_K and
- * Q6_K ones on the matrix cores); matrices passed together (the *_multi
- * forms) must share it. Q6_K and Q8_0 data need 2-byte alignment, Q4_K and
- * Q5_K 16. */
+ * of these types (batches run on the matrix cores: Q4_K, Q5_K and Q6_K from
+ * 4 tokens, Q8_0 from 9 tokens when K is a multiple of 256; the others on
+ * the matvec kernels); matrices passed together (the *_multi forms) must
+ * share it. Q6_K and Q8_0 data need 2-byte alignment, Q4_K and Q5_K 16. */
 int spq4k_weights_upload_type(spq4k_ctx *ctx, int type, const void *host, int64_t M, int64_t K, int64_t E,
                               spq4k_weights **out);
 int spq4k_weights_wrap_type(spq4k_ctx *ctx, int type, const void *dev, int64_t M, int64_t K, int64_t E,

@@ -98,7 +98,8 @@ size_t type_block_bytes(int type) {
 int64_t type_block_values(int type) { return type == SPQ4K_TYPE_Q8_0 ? SPQ4K_QK8_0 : SPQ4K_QK_K; }
 // alignment the kernels need of a block pointer of the type
 size_t type_align(int type) { return type == SPQ4K_TYPE_Q4_K || type == SPQ4K_TYPE_Q5_K ? 16 : 2; }
-// formats with a matrix-core kernel (the others run batches on the sdot4 kernels)
+// K-quant formats whose batches run on the matrix-core ring from
+// gemv_mfma_min_t tokens (Q8_0 batches take the ring through q80_dense)
 bool fmt_has_mfma(int fmt) { return fmt == WF_Q4K || fmt == WF_Q6K || fmt == WF_Q5K; }
 // formats of the expert-gathered ring kernel (moe_ring_kernel)
 bool fmt_has_moe_ring(int fmt) { return fmt == WF_Q4K || fmt == WF_Q6K || fmt == WF_Q5K; }
