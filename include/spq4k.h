@@ -219,7 +219,9 @@ int spq4k_moe(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int
  * cur, selected) and ggml_mul_mat_id(ffn_gate_exps, cur, selected)). Banks
  * share type, K and E (M may differ); Y[i] is [T][n_used][M_i], each equal
  * to spq4k_moe(banks[i], ...). Small batches of K-quant banks sweep both
- * banks in one launch; otherwise the banks run one after the other. */
+ * banks in one launch; batches whose experts get two pairs on average share
+ * one routing and one matrix-core launch (banks of equal M, K a multiple of
+ * 256); otherwise the banks run one after the other. */
 int spq4k_moe_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *banks, const int32_t *ids,
                     int64_t n_used, int64_t ne11, int64_t T, const float *X, float *const *Y);
 

@@ -1168,10 +1168,22 @@ namespace {
 // input rows quantised into each workgroup's LDS; larger ones quantise the
 // input rows once into planes, route the pairs by expert and stream each
 // active expert once, its pairs TC at a time.
-int q80_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t n_used, int64_t ne11, int64_t T,
-            const float* X, float* Y) {
+int q80_moe(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, const int32_t* ids, int64_t n_used,
+            int64_t ne11, int64_t T, const float* X, float* const* Ys) {
+    const spq4k_weights* bank = banks[0];
+    float* Y = Ys[0];
     const int E = (int)bank->E, M = (int)bank->M, nb = (int)(bank->K / SPQ4K_QK8_0);
     const int64_t rows = T * ne11, n_pairs = T * n_used;
+    // two banks (gate and up of equal rows) share the planes, the routing and
+    // one launch of the matrix-core expert kernel; anything else is the
+    // caller's, one bank at a time
+    if (nbank > 1) {
+        const int64_t ma = n_pairs < E ? n_pairs : E;
+        if (c->moe_unfused || bank->K % SPQ4K_QK_K != 0 || (n_pairs + ma - 1) / ma < 2 || banks[1]->M != M ||
+            (T <= 4 && n_pairs <= MOE_DEC_MAX_PAIRS && q80_lds_bytes((int)rows, nb) <= 64 * 1024 &&
+             c->moe_mode == 0))
+            return 1;
+    }
     Q80Params p;
     memset(&p, 0, sizeof p);
     p.nb = nb;
@@ -1226,17 +1238,24 @@ int q80_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64_t
         mp.n_used = (int32_t)n_used;
         mp.ne11 = (int32_t)ne11;
         mp.fmt = WF_Q80;
+        mp.nbank = nbank;
+        mp.max_act = (int32_t)max_act;
+        if (nbank > 1) {
+            mp.bank1 = banks[1]->data;
+            mp.Y1 = Ys[1];
+        }
         const int64_t ntiles = (M + 127) / 128;
-        int64_t rtw = ntiles * max_act / (2 * (int64_t)c->num_cus);
+        int64_t rtw = ntiles * max_act * nbank / (2 * (int64_t)c->num_cus);
         if (rtw < 1) rtw = 1;
         if (rtw > ntiles) rtw = ntiles;
         mp.ring_rt = (int32_t)rtw;
         mp.tiles_per_expert = (int32_t)((ntiles + rtw - 1) / rtw);
-        if (max_act * mp.tiles_per_expert > (1ll << 31) - 1) return set_err(c, -EINVAL, "moe: grid too large");
+        if (max_act * mp.tiles_per_expert * nbank > (1ll << 31) - 1) return set_err(c, -EINVAL, "moe: grid too large");
         e = launch_moe_ring_q80(mp, (int)max_act, c->stream);
         if (e != hipSuccess) return hip_fail(c, e, "moe ring (Q8_0) launch");
         return 0;
     }
+    if (nbank > 1) return 1;   // the grouped matvec takes one bank (the caller runs each)
     // pairs a row is dotted with at a time: about twice the mean an active
     // expert receives, at most 8
     int tc = 1;
@@ -1506,6 +1525,10 @@ int spq4k_moe_multi(spq4k_ctx* c, int n, const spq4k_weights* const* banks, cons
         if (banks[i]->type != banks[0]->type || banks[i]->K != banks[0]->K || banks[i]->E != banks[0]->E)
             return set_err(c, -EINVAL, "moe_multi: banks must share type, K and E");
     }
+    if (n == 2 && banks[0]->fmt == WF_Q80) {
+        rc = q80_moe(c, banks, 2, ids, n_used, ne11, T, X, Y);
+        if (rc <= 0) return rc;
+    }
     if (n == 2 && banks[0]->fmt != WF_Q80) {
         rc = moe_decode_try(c, banks, 2, ids, n_used, ne11, T, X, Y);
         if (rc <= 0) return rc;
@@ -1527,7 +1550,11 @@ int spq4k_moe(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
     if (rc) return rc;
     rc = moe_check(c, bank, ids, n_used, ne11, T, X, Y);
     if (rc) return rc;
-    if (bank->fmt == WF_Q80) return q80_moe(c, bank, ids, n_used, ne11, T, X, Y);
+    if (bank->fmt == WF_Q80) {
+        const spq4k_weights* b1[1] = {bank};
+        float* y1[1] = {Y};
+        return q80_moe(c, b1, 1, ids, n_used, ne11, T, X, y1);
+    }
     const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
     const size_t bb = type_block_bytes(bank->type);
     const int64_t rows = T * ne11, n_pairs = T * n_used;

@@ -659,7 +659,7 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
 // (launch_moe_route, the Q8_0 planes quantiser); the ring alone.
 hipError_t launch_moe_ring_q80(const MoeParams& p, int max_act, hipStream_t st) {
     if (p.fmt != WF_Q80) return hipErrorInvalidValue;
-    const int64_t grid = (int64_t)max_act * p.tiles_per_expert;
+    const int64_t grid = (int64_t)max_act * p.tiles_per_expert * (p.nbank > 1 ? 2 : 1);
     hipLaunchKernelGGL((moe_ring_kernel<2, 3>), dim3((unsigned)grid), dim3(512), 0, st, p);
     return hipGetLastError();
 }
