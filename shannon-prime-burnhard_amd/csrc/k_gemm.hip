@@ -789,10 +789,17 @@ GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
             // the largest tile that gives every CU a workgroup without a K
             // split, else 128 x 64 with one. Measured on MI355X at T = 512:
             // 256 x 64 on 32x32 MFMA tiles for 24576 rows (140 us against 155
-            // on 16x16 tiles), 128 x 64 on 16x16 tiles for 4096 and 6144
+            // on 16x16 tiles), 128 x 64 on 16x16 tiles for 4096 rows.
+            // From T = 128 the 32x32 tiles also win on matrices of 6144 rows
+            // or more (24 tiles of 256), measured at T = 128 / 512:
+            //   6144 x 4096: 29.1 / 52.1 us against 32.1 / 64.0;
+            //   24576 x 4096 at T = 128: 54.0 against 62.8.
+            // They lose at 4096 rows: 4096 x 4096 at T = 512 is 50.0 against
+            // 37.1, and 4096 x 12288 is 129 against 91.
             cfg = 1;
-            const int64_t g0 = row_tiles(p, 256) * ((p.T + 63) / 64);
-            if (g0 >= num_cus) cfg = 11;
+            const int64_t rt = row_tiles(p, 256);
+            const int64_t g0 = rt * ((p.T + 63) / 64);
+            if (g0 >= num_cus || (p.T >= 128 && rt >= 24)) cfg = 11;
         }
     }
     const TiledShape& s = kTiled[cfg];
