@@ -781,9 +781,24 @@ GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
         // CU) against 35.3 (3 stages, one); T = 512 227 us on 128 x 64 tiles
         cfg = p.T <= 32 ? 28 : 26;
     } else if (cfg < 0 || cfg >= N_TILED) {
+        // tall (12288 rows or more) or long-K (48 super-blocks or more)
+        const bool big = p.rows >= 12288 || p.nb >= 48;
+        // measured on the 8B shapes (us, the choice against the next best):
+        //   T = 16: 64 x 16 tiles, 4 waves: 24576 x 4096 24.5 / 28.3,
+        //           4096 x 12288 17.4 / 18.7, 4096 x 4096 12.5 / 13.4
+        //           (6144 x 4096 14.7 / 14.3);
+        //   T = 32: the same on big matrices (24576 rows 29.2 / 38.8,
+        //           4096 x 12288 21.4 / 23.6), 128 x 32 otherwise;
+        //   32 < T < 128: 32x32 tiles on big matrices (24576 rows at T = 64
+        //           41.4 / 48.2, 4096 x 12288 26.2 / 30.8), 128 x 32 on 4096
+        //           rows (16.8 / 19.2), else 128 x 64
         if (p.T <= 16) {
-            cfg = 6;
+            cfg = 8;
         } else if (p.T <= 32) {
+            cfg = big ? 8 : 7;
+        } else if (p.T < 128 && big) {
+            cfg = 11;
+        } else if (p.T < 128 && p.rows <= 4096) {
             cfg = 7;
         } else {
             // the largest tile that gives every CU a workgroup without a K
