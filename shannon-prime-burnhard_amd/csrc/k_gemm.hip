@@ -757,6 +757,10 @@ static const TiledShape kTiled[] = {
     {128, 64, true, launch_ring_<1, 4, 8, 2, 16, 3>, WF_Q80},   // 26: 8 waves, 2 stages of 56 KB
     {64, 64, true, launch_ring_<1, 4, 4, 3, 16, 3>, WF_Q80},    // 27: 4 waves, 3 stages
     {128, 16, true, launch_ring_<1, 1, 8, 2, 16, 3>, WF_Q80},   // 28: T <= 16, 2 stages (two workgroups a CU)
+    // 64 x 16 tiles, 4 waves, 3 stages (the Q4_K shape 8 of each format)
+    {64, 16, true, launch_ring_<1, 1, 4, 3, 16, 1>, WF_Q6K},    // 29
+    {64, 16, true, launch_ring_<1, 1, 4, 3, 16, 2>, WF_Q5K},    // 30
+    {64, 16, true, launch_ring_<1, 1, 4, 3, 16, 3>, WF_Q80},    // 31
 };
 constexpr int N_TILED = (int)(sizeof(kTiled) / sizeof(kTiled[0]));
 
@@ -772,14 +776,21 @@ GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
     GemmPlan g;
     int cfg = p.cfg;
     if (cfg >= 0 && cfg < N_TILED && kTiled[cfg].fmt != p.fmt) cfg = -1;   // a shape of the other format
+    // T <= 32 (Q8_0: T <= 16, or <= 32 on 4096 rows or fewer): 64 x 16 tiles
+    // of 4 waves, measured (us, against the 128-row shapes) at T = 16 on
+    // 24576 x 4096 / 4096 x 12288 / 1024 x 4096: Q6_K 34.1 / 22.3 / 13.1
+    // against 47.9 / 28.4 / 16.5, Q5_K 29.7 / 20.3 / 12.2 against
+    // 36.6 / 23.0 / 14.0, Q8_0 44.8 / 26.5 / 15.5 against 49.9 / 28.7 / 19.5;
+    // at T = 32 Q6_K 47.4 against 52.5 and Q5_K 37.9 against 46.2 on 24576
+    // rows, Q8_0 66.7 against 62.3 there
     if ((cfg < 0 || cfg >= N_TILED) && p.fmt == WF_Q6K) {
-        cfg = p.T <= 16 ? 15 : (p.T <= 32 ? 16 : 14);
+        cfg = p.T <= 32 ? 29 : 14;
     } else if ((cfg < 0 || cfg >= N_TILED) && p.fmt == WF_Q5K) {
-        cfg = p.T <= 16 ? 20 : (p.T <= 32 ? 21 : 19);
+        cfg = p.T <= 32 ? 30 : 19;
     } else if ((cfg < 0 || cfg >= N_TILED) && p.fmt == WF_Q80) {
-        // measured on 4096 x 12288: T = 16 28.7 us (2 stages, two workgroups a
-        // CU) against 35.3 (3 stages, one); T = 512 227 us on 128 x 64 tiles
-        cfg = p.T <= 32 ? 28 : 26;
+        // above 32 tokens: 128 x 64 tiles, 2 stages (4096 x 12288 at T = 512:
+        // 227 us); 17..32 tokens on more than 4096 rows: 128 x 16, 2 stages
+        cfg = (p.T <= 16 || (p.T <= 32 && p.rows <= 4096)) ? 31 : (p.T <= 32 ? 28 : 26);
     } else if (cfg < 0 || cfg >= N_TILED) {
         // tall (12288 rows or more) or long-K (48 super-blocks or more)
         const bool big = p.rows >= 12288 || p.nb >= 48;

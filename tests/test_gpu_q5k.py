@@ -214,7 +214,7 @@ def test_mul_mat_batched(ctx, oracle, T):
         _check(got, oracle.mul_mat_type(TYPE_Q5_K, W, M, K, X), f"q5k mul_mat T={T} M={M} K={K}")
 
 
-@pytest.mark.parametrize("cfg", [19, 20, 21, 22, 23])
+@pytest.mark.parametrize("cfg", [19, 20, 21, 22, 23, 30])
 def test_ring_launch_shapes(oracle, cfg):
     """Every Q5_K matrix-core launch shape, on ragged rows and tokens."""
     rng = np.random.default_rng(510 + cfg)

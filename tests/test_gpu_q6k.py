@@ -214,7 +214,7 @@ def test_mul_mat_batched(ctx, oracle, T):
         _check(got, oracle.mul_mat_type(TYPE_Q6_K, W, M, K, X), f"q6k mul_mat T={T} M={M} K={K}")
 
 
-@pytest.mark.parametrize("cfg", [14, 15, 16, 17, 18])
+@pytest.mark.parametrize("cfg", [14, 15, 16, 17, 18, 29])
 def test_ring_launch_shapes(oracle, cfg):
     """Every Q6_K matrix-core launch shape, on ragged rows and tokens and on
     rows of an odd number of blocks (2-byte-aligned block starts)."""

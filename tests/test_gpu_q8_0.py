@@ -239,7 +239,7 @@ def test_mul_mat_batched(ctx, oracle, T):
         _check(got, oracle.mul_mat_q8_0(W, M, K, X), f"q8_0 mul_mat T={T} M={M} K={K}")
 
 
-@pytest.mark.parametrize("cfg", [24, 25, 26, 27, 28])
+@pytest.mark.parametrize("cfg", [24, 25, 26, 27, 28, 31])
 def test_ring_launch_shapes(oracle, cfg):
     """Every Q8_0 matrix-core launch shape (K a multiple of 256), on ragged
     rows and tokens."""
