@@ -36,6 +36,7 @@ struct spq4k_ctx {
     int gemv_mfma_min_t = 4;     // SPQ4K_GEMV_MFMA_MIN_T: batches of at least this many tokens use matrix cores
     int no_decode = 0;           // SPQ4K_GEMV_GENERIC=1: T = 1 also uses the generic kernel
     int moe_unfused = 0;         // SPQ4K_MOE_UNFUSED=1: routing pass + Q8_K planes + matvec (3 launches)
+    int moe_ring_waves = 0;      // SPQ4K_MOE_RING_WAVES: 4 or 8 waves (64- or 128-row tiles) in the expert ring kernel, 0 by format
     int moe_mode = 0;            // SPQ4K_MOE_MODE: 2 skips the small-batch decode mapping, 3 takes the single-launch sdot4 kernel
     int gemm_mode = 0;           // SPQ4K_GEMM_MODE: 0 auto, 1 skinny kernel, 2 tiled kernel
     int gemm_cfg = -1;           // SPQ4K_GEMM_CFG: tiled launch shape, -1 automatic
@@ -103,6 +104,13 @@ size_t type_align(int type) { return type == SPQ4K_TYPE_Q4_K || type == SPQ4K_TY
 bool fmt_has_mfma(int fmt) { return fmt == WF_Q4K || fmt == WF_Q6K || fmt == WF_Q5K; }
 // formats of the expert-gathered ring kernel (moe_ring_kernel)
 bool fmt_has_moe_ring(int fmt) { return fmt == WF_Q4K || fmt == WF_Q6K || fmt == WF_Q5K; }
+// Waves of the expert ring kernel, measured on the 128-expert down bank at
+// T = 32 (us, 4 / 8 waves): Q6_K 54.9 / 59.9, Q5_K 45.0 / 48.0; Q4_K (the
+// MoE layer) 97.0 / 88.7 and Q8_0 70.2 / 67.6 keep 8.
+int moe_ring_waves(const spq4k_ctx* c, int fmt) {
+    if (c->moe_ring_waves) return c->moe_ring_waves;
+    return fmt == WF_Q6K || fmt == WF_Q5K ? 4 : 8;
+}
 
 int use_device(spq4k_ctx* c) {
     if (!c) return -EINVAL;
@@ -624,6 +632,10 @@ int spq4k_init(int device, spq4k_ctx** out) {
     if (const char* f = getenv("SPQ4K_Q80_STAGED")) {
         const int v = atoi(f);
         if (v >= 0 && v <= 2) c->q80_staged = v;
+    }
+    if (const char* f = getenv("SPQ4K_MOE_RING_WAVES")) {
+        const int v = atoi(f);
+        if (v == 4 || v == 8) c->moe_ring_waves = v;
     }
     if (const char* f = getenv("SPQ4K_Q80_PREQ")) {
         const int v = atoi(f);
@@ -1244,14 +1256,15 @@ int q80_moe(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, const in
             mp.bank1 = banks[1]->data;
             mp.Y1 = Ys[1];
         }
-        const int64_t ntiles = (M + 127) / 128;
+        const int nw = moe_ring_waves(c, WF_Q80);
+        const int64_t ntiles = (M + 16 * nw - 1) / (16 * nw);
         int64_t rtw = ntiles * max_act * nbank / (2 * (int64_t)c->num_cus);
         if (rtw < 1) rtw = 1;
         if (rtw > ntiles) rtw = ntiles;
         mp.ring_rt = (int32_t)rtw;
         mp.tiles_per_expert = (int32_t)((ntiles + rtw - 1) / rtw);
         if (max_act * mp.tiles_per_expert * nbank > (1ll << 31) - 1) return set_err(c, -EINVAL, "moe: grid too large");
-        e = launch_moe_ring_q80(mp, (int)max_act, c->stream);
+        e = launch_moe_ring_q80(mp, (int)max_act, nw, c->stream);
         if (e != hipSuccess) return hip_fail(c, e, "moe ring (Q8_0) launch");
         return 0;
     }
@@ -1499,7 +1512,8 @@ int moe_ring_run(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, con
     }
     // row tiles a workgroup streams: as many as still leave two workgroups
     // per CU over the experts (of every bank) that can be active
-    const int64_t ntiles = (M + 127) / 128;
+    const int nw = moe_ring_waves(c, bank->fmt);
+    const int64_t ntiles = (M + 16 * nw - 1) / (16 * nw);
     int64_t rtw = ntiles * max_act * nbank / (2 * (int64_t)c->num_cus);
     if (rtw < 1) rtw = 1;
     if (rtw > ntiles) rtw = ntiles;
@@ -1507,7 +1521,8 @@ int moe_ring_run(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, con
     p.tiles_per_expert = (int32_t)((ntiles + rtw - 1) / rtw);
     if (max_act * p.tiles_per_expert * nbank > (1ll << 31) - 1 || rows * nb / 16 > (1ll << 31) - 2)
         return set_err(c, -EINVAL, "moe: grid too large");
-    const hipError_t e = launch_moe_ring(p, ids, (int)n_pairs, E, X, bank->K, (int)rows, (int)max_act, c->stream);
+    const hipError_t e = launch_moe_ring(p, ids, (int)n_pairs, E, X, bank->K, (int)rows, (int)max_act, nw,
+                                         c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "moe ring launch");
     return 0;
 }

@@ -531,9 +531,9 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(const int32_t* __restrict
 // F = 3: Q8_0 banks with K a multiple of 256 (17 slots: eight 34-byte
 // blocks; Q8_0 planes, the token's eight scales in its min-term slots;
 // ring_block_q80); as in gemm_ring_kernel.
-template <int S, int F = 0>
-__global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
-    constexpr int NW = 8, ROWS = 128, TOK = 16;
+template <int S, int F = 0, int NW = 8>
+__global__ __launch_bounds__(NW * 64) void moe_ring_kernel(MoeParams p) {
+    constexpr int ROWS = 16 * NW, TOK = 16;   // a wave's 16 rows of each row tile
     constexpr int WSL = F == 1 ? 14 : F == 2 ? 11 : F == 3 ? 17 : 9;
     constexpr int BB = F == 1 ? Q6K_BYTES : F == 2 ? Q5K_BYTES : F == 3 ? Q80_RING_ROW : Q4K_BYTES;
     constexpr int ROWB = 16 * WSL;
@@ -657,27 +657,39 @@ __global__ __launch_bounds__(512) void moe_ring_kernel(MoeParams p) {
 
 // Q8_0 banks: the routing tables and Q8_0 planes are already in place
 // (launch_moe_route, the Q8_0 planes quantiser); the ring alone.
-hipError_t launch_moe_ring_q80(const MoeParams& p, int max_act, hipStream_t st) {
-    if (p.fmt != WF_Q80) return hipErrorInvalidValue;
+hipError_t launch_moe_ring_q80(const MoeParams& p, int max_act, int nw, hipStream_t st) {
+    if (p.fmt != WF_Q80 || (nw != 4 && nw != 8)) return hipErrorInvalidValue;
     const int64_t grid = (int64_t)max_act * p.tiles_per_expert * (p.nbank > 1 ? 2 : 1);
-    hipLaunchKernelGGL((moe_ring_kernel<2, 3>), dim3((unsigned)grid), dim3(512), 0, st, p);
+    if (nw == 4)
+        hipLaunchKernelGGL((moe_ring_kernel<2, 3, 4>), dim3((unsigned)grid), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL((moe_ring_kernel<2, 3, 8>), dim3((unsigned)grid), dim3(512), 0, st, p);
     return hipGetLastError();
 }
 
 hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, int E, const float* X,
-                           int64_t x_tstride, int n_xrows, int max_act, hipStream_t st) {
+                           int64_t x_tstride, int n_xrows, int max_act, int nw, hipStream_t st) {
+    if (nw != 4 && nw != 8) return hipErrorInvalidValue;
     const int64_t items = (int64_t)n_xrows * p.nb;
     hipLaunchKernelGGL(moe_prep_kernel, dim3((unsigned)(1 + (items + 15) / 16)), dim3(256), moe_route_lds_bytes(E), st,
                        ids, n_pairs, E, p.route, X, x_tstride, n_xrows, p.nb, p.Q);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t grid = (int64_t)max_act * p.tiles_per_expert * (p.nbank > 1 ? 2 : 1);
-    if (p.fmt == WF_Q6K)
-        hipLaunchKernelGGL((moe_ring_kernel<3, 1>), dim3((unsigned)grid), dim3(512), 0, st, p);
-    else if (p.fmt == WF_Q5K)
-        hipLaunchKernelGGL((moe_ring_kernel<3, 2>), dim3((unsigned)grid), dim3(512), 0, st, p);
-    else
-        hipLaunchKernelGGL((moe_ring_kernel<3, 0>), dim3((unsigned)grid), dim3(512), 0, st, p);
+    if (nw == 4) {
+        if (p.fmt == WF_Q6K)
+            hipLaunchKernelGGL((moe_ring_kernel<3, 1, 4>), dim3((unsigned)grid), dim3(256), 0, st, p);
+        else if (p.fmt == WF_Q5K)
+            hipLaunchKernelGGL((moe_ring_kernel<3, 2, 4>), dim3((unsigned)grid), dim3(256), 0, st, p);
+        else
+            hipLaunchKernelGGL((moe_ring_kernel<3, 0, 4>), dim3((unsigned)grid), dim3(256), 0, st, p);
+    } else if (p.fmt == WF_Q6K) {
+        hipLaunchKernelGGL((moe_ring_kernel<3, 1, 8>), dim3((unsigned)grid), dim3(512), 0, st, p);
+    } else if (p.fmt == WF_Q5K) {
+        hipLaunchKernelGGL((moe_ring_kernel<3, 2, 8>), dim3((unsigned)grid), dim3(512), 0, st, p);
+    } else {
+        hipLaunchKernelGGL((moe_ring_kernel<3, 0, 8>), dim3((unsigned)grid), dim3(512), 0, st, p);
+    }
     return hipGetLastError();
 }
 

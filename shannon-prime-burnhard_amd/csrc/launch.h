@@ -134,11 +134,12 @@ hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStr
 // matrix-core form: moe_prep_kernel (routing in workgroup 0, permuted Q8_K
 // planes of the n_xrows input rows X in the others), then the ring kernel
 // over max_act experts x p.tiles_per_expert groups of p.ring_rt row tiles
+// nw: waves of a workgroup, 4 or 8 (row tiles of 16 * nw rows)
 hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, int E, const float* X,
-                           int64_t x_tstride, int n_xrows, int max_act, hipStream_t st);
+                           int64_t x_tstride, int n_xrows, int max_act, int nw, hipStream_t st);
 // Q8_0 banks (K a multiple of 256; p.Q.qs / p.Q.d the Q8_0 planes, p.route
 // filled): the ring kernel only
-hipError_t launch_moe_ring_q80(const MoeParams& p, int max_act, hipStream_t st);
+hipError_t launch_moe_ring_q80(const MoeParams& p, int max_act, int nw, hipStream_t st);
 
 // prefill matmul on matrix cores (k_gemm.hip)
 constexpr int GEMM_MAX_SEG = 4;

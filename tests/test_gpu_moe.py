@@ -96,14 +96,15 @@ def test_moe_rejects_bad_ids(ctx):
 def test_moe_paths_agree(oracle, T, ne11, M, K):
     """Every MoE path against the oracle: the planner's choice, the matrix-core
     path at any batch (SPQ4K_MOE_MODE=2: routing pass, Q8_K planes, ring
-    kernel), the single-launch sdot4 kernel (=3) and the three-launch sdot4
+    kernel of 8 waves, and of 4 with SPQ4K_MOE_RING_WAVES=4), the single-launch sdot4 kernel (=3) and the three-launch sdot4
     path (SPQ4K_MOE_UNFUSED)."""
     from _envctx import context_with
     E, k = 128, 8
     ids = _topk_ids(np.random.default_rng(T), T, E, k)
     X = np.random.default_rng(T + 1).standard_normal((T, ne11, K)).astype(np.float32)
     outs, host = [], None
-    for env in ({}, {"SPQ4K_MOE_MODE": 2}, {"SPQ4K_MOE_MODE": 3}, {"SPQ4K_MOE_UNFUSED": 1}):
+    for env in ({}, {"SPQ4K_MOE_MODE": 2}, {"SPQ4K_MOE_MODE": 2, "SPQ4K_MOE_RING_WAVES": 4}, {"SPQ4K_MOE_MODE": 3},
+                {"SPQ4K_MOE_UNFUSED": 1}):
         c = context_with(env)
         try:
             bank, host = _gpu_bank(c, E, M, K, 71)

@@ -333,7 +333,7 @@ def test_mul_mat_id_golden(ctx, tag):
     _check(got, GOLD[f"mmid_Y_{tag}"], f"golden mul_mat_id {tag}")
 
 
-@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 3}, {"SPQ4K_MOE_UNFUSED": 1}, {"SPQ4K_MOE_MODE": 2}])
+@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 3}, {"SPQ4K_MOE_UNFUSED": 1}, {"SPQ4K_MOE_MODE": 2}, {"SPQ4K_MOE_RING_WAVES": 8}])
 @pytest.mark.parametrize("T,ne11", [(1, 1), (3, 8), (12, 1), (32, 8)])
 def test_moe(oracle, env, T, ne11):
     """A Q6_K expert bank of the MoE shape (down projection K = 768, and

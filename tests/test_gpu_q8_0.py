@@ -364,7 +364,7 @@ def test_mul_mat_id_golden(ctx, tag):
     _check(got, GOLD[f"mmid_Y_{tag}"], f"golden mul_mat_id {tag}")
 
 
-@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 2}, {"SPQ4K_MOE_UNFUSED": 1}])
+@pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 2}, {"SPQ4K_MOE_UNFUSED": 1}, {"SPQ4K_MOE_RING_WAVES": 4}])
 @pytest.mark.parametrize("T,ne11", [(1, 1), (3, 8), (12, 1), (32, 8), (200, 1)])
 def test_moe(oracle, env, T, ne11):
     """Every MoE path: the one-launch sweep (small batches), the matrix-core
