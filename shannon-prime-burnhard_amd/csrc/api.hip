@@ -36,6 +36,11 @@ struct spq4k_ctx {
     int gemv_mfma_min_t = 4;     // SPQ4K_GEMV_MFMA_MIN_T: batches of at least this many tokens use matrix cores
     int no_decode = 0;           // SPQ4K_GEMV_GENERIC=1: T = 1 also uses the generic kernel
     int moe_unfused = 0;         // SPQ4K_MOE_UNFUSED=1: routing pass + Q8_K planes + matvec (3 launches)
+    // SPQ4K_MOE_DEC_MAX_T: largest batch of the K-quant MoE decode sweep (1..8);
+    // at T = 8 the sweep streams an expert once per pair, about a quarter more
+    // bytes than the ring, but skips its prep launch: the 128-expert Q4_K layer
+    // takes 49.0 us against 56.5 on the ring
+    int moe_dec_max_t = 8;
     int moe_ring_waves = 0;      // SPQ4K_MOE_RING_WAVES: 4 or 8 waves (64- or 128-row tiles) in the expert ring kernel, 0 by format
     int moe_mode = 0;            // SPQ4K_MOE_MODE: 2 skips the small-batch decode mapping, 3 takes the single-launch sdot4 kernel
     int gemm_mode = 0;           // SPQ4K_GEMM_MODE: 0 auto, 1 skinny kernel, 2 tiled kernel
@@ -632,6 +637,10 @@ int spq4k_init(int device, spq4k_ctx** out) {
     if (const char* f = getenv("SPQ4K_Q80_STAGED")) {
         const int v = atoi(f);
         if (v >= 0 && v <= 2) c->q80_staged = v;
+    }
+    if (const char* f = getenv("SPQ4K_MOE_DEC_MAX_T")) {
+        const int v = atoi(f);
+        if (v >= 1 && v <= 8) c->moe_dec_max_t = v;
     }
     if (const char* f = getenv("SPQ4K_MOE_RING_WAVES")) {
         const int v = atoi(f);
@@ -1421,7 +1430,8 @@ int moe_check(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
 // Small batches of a K-quant bank, or of two banks of one type, K and E
 // sharing ids and X (gate and up): the decode mapping, every routed pair's
 // rows (of both banks) in one sweep and one launch. An expert chosen twice
-// is streamed twice, so only for T <= 4. Returns 1 when it does not apply.
+// is streamed twice, so only for small batches (T <= moe_dec_max_t).
+// Returns 1 when it does not apply.
 int moe_decode_try(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, const int32_t* ids,
                    int64_t n_used, int64_t ne11, int64_t T, const float* X, float* const* Y) {
     const spq4k_weights* bank = banks[0];
@@ -1429,7 +1439,7 @@ int moe_decode_try(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, c
     const int M1 = nbank > 1 ? (int)banks[1]->M : 0;
     const size_t bb = type_block_bytes(bank->type);
     const int64_t rows = T * ne11, n_pairs = T * n_used;
-    if (!(T <= 4 && n_pairs <= MOE_DEC_MAX_PAIRS && rows <= MOE_DEC_MAX_XROWS && moe_decode_supported(nb) &&
+    if (!(T <= c->moe_dec_max_t && n_pairs <= MOE_DEC_MAX_PAIRS && rows <= MOE_DEC_MAX_XROWS && moe_decode_supported(nb) &&
           !c->moe_unfused && c->moe_mode == 0 && (size_t)q8lds_bytes((int)rows * nb) <= (size_t)LDS_BUDGET &&
           n_pairs * (M + M1) <= INT32_MAX))
         return 1;

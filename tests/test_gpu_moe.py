@@ -150,7 +150,7 @@ def test_moe_multi(ctx, oracle, qtype, T, ne11, shapes):
     rows; a second bank of 512 rows) in one call, each output bit for bit the
     one spq4k_moe gives that bank alone (both the two-bank sweep and the
     two-bank expert ring run every row with the same arithmetic), and within
-    tolerance of the oracle. K-quant banks: T <= 4 sweeps both banks in one
+    tolerance of the oracle. K-quant banks: T <= 8 sweeps both banks in one
     launch; larger batches of banks of equal rows share one prep and one
     ring launch; the rest run the banks one after the other."""
     from spq4k.hip import DeviceArray

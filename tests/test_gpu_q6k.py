@@ -337,7 +337,7 @@ def test_mul_mat_id_golden(ctx, tag):
 @pytest.mark.parametrize("T,ne11", [(1, 1), (3, 8), (12, 1), (32, 8)])
 def test_moe(oracle, env, T, ne11):
     """A Q6_K expert bank of the MoE shape (down projection K = 768, and
-    K = 2048) through every MoE path: the decode mapping (T <= 4), the
+    K = 2048) through every MoE path: the decode mapping (T <= 8), the
     single-launch kernel, and routing + Q8_K planes + grouped matvec."""
     rng = np.random.default_rng(608 + T)
     E, n_used = 32, 8
