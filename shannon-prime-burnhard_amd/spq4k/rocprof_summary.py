@@ -24,6 +24,7 @@ import csv
 import glob
 import json
 import os
+import shlex
 import statistics
 import sys
 
@@ -114,6 +115,13 @@ def stats_table(d, out, title, commands):
     print(open(out).read())
 
 
+def _own_command(argv):
+    """The summary's own command line, recorded when no --command is given, so
+    that the commands block never comes out empty (the profiler run that made
+    the input is named with --command)."""
+    return "PYTHONPATH=shannon-prime-burnhard_amd python3 -m spq4k.rocprof_summary " + shlex.join(argv)
+
+
 def main(argv=None):
     if argv is None:
         argv = sys.argv[1:]
@@ -124,13 +132,15 @@ def main(argv=None):
         ap.add_argument("--title", required=True)
         ap.add_argument("--command", action="append", default=[])
         a = ap.parse_args(argv)
-        stats_table(a.stats, a.out, a.title, a.command)
+        stats_table(a.stats, a.out, a.title, a.command or [_own_command(argv)])
         return 0
     ap = argparse.ArgumentParser()
     for a in ("trace", "fetch", "write", "fetch_copy", "write_copy", "out", "json"):
         ap.add_argument("--" + a.replace("_", "-"), required=True)
     ap.add_argument("--command", action="append", default=[], help="command line to record (repeatable)")
     args = ap.parse_args(argv)
+    if not args.command:
+        args.command = [_own_command(argv)]
 
     trace = _gemv(_csv(args.trace, "kernel_trace.csv"))
     by_stage = _staged(trace, "Dispatch_Id" if "Dispatch_Id" in trace[0] else "Start_Timestamp")
