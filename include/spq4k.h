@@ -20,8 +20,10 @@
  *     -EINVAL (bad argument: K not a multiple of 256, null or misaligned
  *     pointer, T out of range), -ENOMEM (device allocation failed),
  *     -ENODEV (no such HIP device), -EIO (a HIP runtime call failed;
- *     spq4k_last_error() has the message). This follows the reference's
- *     burnhard_residue_matmul.h:39-56 (0 / -EINVAL / -ENOMEM).
+ *     spq4k_last_error() has the message), -EBUSY (the call would have to
+ *     grow its scratch while its stream is being captured; spq4k_reserve).
+ *     This follows the reference's burnhard_residue_matmul.h:39-56
+ *     (0 / -EINVAL / -ENOMEM).
  *   - Plain pointers are DEVICE pointers and the call only enqueues work on
  *     the context's stream (like a ggml backend's compute); *_host variants
  *     take host pointers, copy in and out, and return when the result is in
@@ -79,6 +81,20 @@ int         spq4k_get_device(const spq4k_ctx *ctx);
 int         spq4k_synchronize(spq4k_ctx *ctx);
 const char *spq4k_last_error(const spq4k_ctx *ctx);
 int         spq4k_device_count(void);
+/* Grow the context's scratch to at least scratch_bytes (activation planes,
+ * K-split partial sums, MoE routing) and its fusion scratch to at least
+ * fusion_bytes (normalised rows and gate / up outputs of the unfused
+ * spq4k_mul_mat_rms_norm / spq4k_mul_mat_swiglu paths), as the CUDA backend's
+ * memory pool grows on demand (ggml_cuda_pool_leg::alloc,
+ * ggml-cuda/ggml-cuda.cu:382). A call that needs more scratch than the
+ * context holds grows it itself, except while its stream is being captured
+ * into a HIP graph: it then returns -EBUSY and enqueues nothing, so reserve
+ * before capturing. Buffers replaced by larger ones stay allocated until
+ * spq4k_free, so graphs captured earlier stay valid. Sizes: activation
+ * planes take 340 bytes per 256 values of each input row (Q8_0: 36 bytes per
+ * 32), a K split up to 8 MiB of partial sums beside them; the fusion scratch
+ * takes 4 bytes per input value (the norm) plus 8 per output (SwiGLU). */
+int         spq4k_reserve(spq4k_ctx *ctx, size_t scratch_bytes, size_t fusion_bytes);
 
 /* ---- weights -----------------------------------------------------------
  * Replaces the backend weight upload (ggml_backend_tensor_set of a Q4_K

@@ -11,6 +11,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <vector>
+
 #include <hip/hip_runtime.h>
 
 #include "launch.h"
@@ -31,6 +33,8 @@ struct spq4k_ctx {
     // intermediates of the fused entry points (normalised rows, gate / up outputs)
     uint8_t* scratch2 = nullptr;
     size_t scratch2_cap = 0;
+    // scratch buffers replaced by larger ones, freed by spq4k_free
+    std::vector<void*> retired;
     int force_bpr = 0;           // tuning override (SPQ4K_GEMV_BPR = 1, 2, 4 or 8)
     int preq_mode = 0;           // SPQ4K_GEMV_PREQ: 0 auto, 1 always, 2 never
     int gemv_mfma_min_t = 4;     // SPQ4K_GEMV_MFMA_MIN_T: batches of at least this many tokens use matrix cores
@@ -125,33 +129,39 @@ int use_device(spq4k_ctx* c) {
     return 0;
 }
 
-int ensure_scratch(spq4k_ctx* c, size_t bytes) {
-    if (bytes <= c->scratch_cap) return 0;
-    SPQ_HIP(c, hipStreamSynchronize(c->stream));
-    if (c->scratch) (void)hipFree(c->scratch);
-    c->scratch = nullptr;
-    c->scratch_cap = 0;
-    size_t cap = bytes < (size_t)(4 << 20) ? (size_t)(4 << 20) : bytes;
-    if (hipMalloc(&c->scratch, cap) != hipSuccess) {
-        c->scratch = nullptr;
-        return set_err(c, -ENOMEM, "scratch of %zu bytes", cap);
-    }
-    c->scratch_cap = cap;
+// Grows one of the context's scratch buffers to at least `bytes`. The buffer
+// it replaces is retired, not freed: work already enqueued, and HIP graphs
+// captured earlier, keep pointing at it, so it stays allocated until
+// spq4k_free. Growth at least doubles the capacity, so the retired buffers
+// of a context add up to less than its current one. A call that would grow
+// a buffer while the stream is being captured fails with -EBUSY (nothing is
+// enqueued): a graph must not depend on an allocation made during its
+// capture; spq4k_reserve grows the buffers ahead of a capture.
+int grow_scratch(spq4k_ctx* c, uint8_t** buf, size_t* cap, size_t bytes, size_t min_cap, const char* what) {
+    if (bytes <= *cap) return 0;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    SPQ_HIP(c, hipStreamIsCapturing(c->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return set_err(c, -EBUSY,
+                       "%s: %zu bytes needed, %zu held, and the stream is capturing a graph (call spq4k_reserve "
+                       "before the capture)", what, bytes, *cap);
+    size_t ncap = 2 * *cap;
+    if (ncap < bytes) ncap = bytes;
+    if (ncap < min_cap) ncap = min_cap;
+    void* p = nullptr;
+    if (hipMalloc(&p, ncap) != hipSuccess) return set_err(c, -ENOMEM, "%s of %zu bytes", what, ncap);
+    if (*buf) c->retired.push_back(*buf);
+    *buf = static_cast<uint8_t*>(p);
+    *cap = ncap;
     return 0;
 }
 
+int ensure_scratch(spq4k_ctx* c, size_t bytes) {
+    return grow_scratch(c, &c->scratch, &c->scratch_cap, bytes, (size_t)4 << 20, "scratch");
+}
+
 int ensure_scratch2(spq4k_ctx* c, size_t bytes) {
-    if (bytes <= c->scratch2_cap) return 0;
-    SPQ_HIP(c, hipStreamSynchronize(c->stream));
-    if (c->scratch2) (void)hipFree(c->scratch2);
-    c->scratch2 = nullptr;
-    c->scratch2_cap = 0;
-    if (hipMalloc(&c->scratch2, bytes) != hipSuccess) {
-        c->scratch2 = nullptr;
-        return set_err(c, -ENOMEM, "scratch of %zu bytes", bytes);
-    }
-    c->scratch2_cap = bytes;
-    return 0;
+    return grow_scratch(c, &c->scratch2, &c->scratch2_cap, bytes, (size_t)1 << 20, "fusion scratch");
 }
 
 int check_shape(spq4k_ctx* c, int64_t M, int64_t K, int64_t E, int64_t qk = SPQ4K_QK_K) {
@@ -652,7 +662,13 @@ int spq4k_init(int device, spq4k_ctx** out) {
     }
     // scratch for Q8_K activation planes: sized for prefill batches up front
     // so that steady-state calls (and graph capture) never allocate
-    if (ensure_scratch(c, (size_t)16 << 20) != 0) { (void)hipStreamDestroy(c->own_stream); delete c; return -ENOMEM; }
+    if (ensure_scratch(c, (size_t)16 << 20) != 0 || ensure_scratch2(c, (size_t)4 << 20) != 0) {
+        if (c->scratch) (void)hipFree(c->scratch);
+        if (c->scratch2) (void)hipFree(c->scratch2);
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return -ENOMEM;
+    }
     *out = c;
     return 0;
 }
@@ -663,6 +679,7 @@ void spq4k_free(spq4k_ctx* c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->scratch) (void)hipFree(c->scratch);
     if (c->scratch2) (void)hipFree(c->scratch2);
+    for (void* p : c->retired) (void)hipFree(p);
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     delete c;
 }
@@ -717,8 +734,9 @@ int spq4k_weights_alloc_type(spq4k_ctx* c, int type, int64_t M, int64_t K, int64
     rc = weights_new(c, type, M, K, E, &w);
     if (rc) return rc;
     if (hipMalloc(&w->data, w->nbytes) != hipSuccess) {
+        const size_t nbytes = w->nbytes;
         delete w;
-        return set_err(c, -ENOMEM, "weights: %zu bytes", (size_t)0);
+        return set_err(c, -ENOMEM, "weights: %zu bytes", nbytes);
     }
     w->owned = true;
     *out = w;
@@ -1180,6 +1198,14 @@ int spq4k_gemm(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, i
 int spq4k_mul_mat(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
     if (T >= 1 && T <= SPQ4K_GEMV_MAX_T) return spq4k_gemv(c, W, X, Y, T);
     return spq4k_gemm(c, W, X, Y, T);
+}
+
+int spq4k_reserve(spq4k_ctx* c, size_t scratch_bytes, size_t fusion_bytes) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    rc = ensure_scratch(c, scratch_bytes);
+    if (rc) return rc;
+    return ensure_scratch2(c, fusion_bytes);
 }
 
 namespace {

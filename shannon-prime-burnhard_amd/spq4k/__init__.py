@@ -155,6 +155,7 @@ def load_library(path: str | None = None):
         "spq4k_quantize_q8_0_host": (I, [V, V, V, I64]),
         "spq4k_vec_dot_q8_0_host": (I, [V, I, V, V, V]),
         "spq4k_synth_fill": (I, [V, V, I64, U64, I, I64, F, F, F, I64]),
+        "spq4k_reserve": (I, [V, S, S]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -397,6 +398,10 @@ class Context:
 
     def synchronize(self):
         self._check("spq4k_synchronize", self.lib.spq4k_synchronize(self.handle))
+
+    def reserve(self, scratch_bytes: int, fusion_bytes: int = 0):
+        """spq4k_reserve: grow the scratch ahead of a graph capture."""
+        self._check("spq4k_reserve", self.lib.spq4k_reserve(self.handle, scratch_bytes, fusion_bytes))
 
     # -- weights
     def upload(self, q: np.ndarray, M: int, K: int, E: int = 1, type: int = TYPE_Q4_K) -> Weights:
