@@ -501,19 +501,43 @@ int or_mul_mat_id(const void *as, int64_t M, int64_t K, int64_t E,
     return or_mul_mat_id_type(OR_TYPE_Q4_K, as, M, K, E, X, ne11, ids, k, T, Y, order);
 }
 
-/* Dequant-then-dot in double (the fp32 weights of the type's to_float times
- * the fp32 activations, accumulated in double); the reference's scalar
- * dequant-then-dot path is desktop/beast_canyon/sp_beast_canyon.c:1122-1134. */
+/* Q8_K -> fp32. Follows ggml-quants.c:2731-2740 (dequantize_row_q8_K):
+ * y = d * q, one fp32 product per value. */
+void or_dequantize_row_q8K(const void *vx, float *y, int64_t k) {
+    const or_block_q8K *x = (const or_block_q8K *)vx;
+    const int64_t nb = k / OR_QK_K;
+    for (int64_t i = 0; i < nb; ++i)
+        for (int j = 0; j < OR_QK_K; ++j) y[i * OR_QK_K + j] = x[i].d * (float)x[i].qs[j];
+}
+
+/* fp32 weights of one row of a weight type (its to_float), 0 or -22 */
+static int dequant_row_type(int type, const void *src, float *w, int64_t K) {
+    if (type == OR_TYPE_Q4_K) or_dequantize_row_q4K(src, w, K);
+    else if (type == OR_TYPE_Q5_K) or_dequantize_row_q5K(src, w, K);
+    else if (type == OR_TYPE_Q6_K) or_dequantize_row_q6K(src, w, K);
+    else if (type == OR_TYPE_Q8_0) or_dequantize_row_q8_0(src, w, K);
+    else return -22;
+    return 0;
+}
+
+static size_t row_bytes_type(int type, int64_t K) {
+    if (type == OR_TYPE_Q8_0) return (size_t)(K / 32) * 34;
+    return (size_t)(K / OR_QK_K) * block_bytes(type);
+}
+
+/* Dequant-then-dot in double with the fp32 activations as given: the exact
+ * value of sum_c dequant(W)[r][c] * x[t][c] for the type's to_float weights.
+ * It is what an fp32-activation dequant-then-dot computes in exact
+ * arithmetic (the reference's scalar path: beast_matvec,
+ * desktop/beast_canyon/sp_beast_canyon.c:1122-1134, which rounds its sum in
+ * fp32); Q8_K-activation kernels differ from it by the quantisation of x. */
 int or_mul_mat_dequant_f64_type(int type, const void *W, int64_t M, int64_t K, const float *X,
                                 int64_t T, double *Y) {
-    const size_t row_bytes = (size_t)(K / OR_QK_K) * block_bytes(type);
-    if (!row_bytes) return -22;
+    const size_t rb = row_bytes_type(type, K);
+    if (!rb) return -22;
     float *wrow = (float *)malloc((size_t)K * sizeof(float));
     for (int64_t r = 0; r < M; ++r) {
-        const uint8_t *src = (const uint8_t *)W + (size_t)r * row_bytes;
-        if (type == OR_TYPE_Q6_K) or_dequantize_row_q6K(src, wrow, K);
-        else if (type == OR_TYPE_Q5_K) or_dequantize_row_q5K(src, wrow, K);
-        else or_dequantize_row_q4K(src, wrow, K);
+        if (dequant_row_type(type, (const uint8_t *)W + (size_t)r * rb, wrow, K)) { free(wrow); return -22; }
         for (int64_t t = 0; t < T; ++t) {
             double acc = 0;
             const float *xt = X + t * K;
@@ -528,6 +552,100 @@ int or_mul_mat_dequant_f64_type(int type, const void *W, int64_t M, int64_t K, c
 void or_mul_mat_dequant_f64(const void *W, int64_t M, int64_t K, const float *X,
                             int64_t T, double *Y) {
     (void)or_mul_mat_dequant_f64_type(OR_TYPE_Q4_K, W, M, K, X, T, Y);
+}
+
+/* The second form of the parity bar for the Q8_K / Q8_0 matmuls: the exact
+ * value of sum_c dequant(W)[r][c] * dequant(Q(x[t]))[c] in double, where Q is
+ * the CPU backend's activation quantiser of the type's vec_dot_type
+ * (quantize_row_q8_K, ggml-quants.c:2692-2729; for Q8_0 weights
+ * quantize_row_q8_0, ggml-cpu/arch/x86/quants.c:302-367) and dequant its
+ * to_float (dequantize_row_q8_K, ggml-quants.c:2731-2740; dequantize_row_q8_0,
+ * :491-505). ggml_vec_dot_q4_K_q8_K computes the same sum with integer
+ * sub-block sums and an fp32 combine, so its outputs sit within fp32
+ * rounding of this one. */
+int or_mul_mat_dq_f64_type(int type, const void *W, int64_t M, int64_t K, const float *X,
+                           int64_t T, double *Y) {
+    const size_t rb = row_bytes_type(type, K);
+    if (!rb) return -22;
+    const int q80 = type == OR_TYPE_Q8_0;
+    float *wrow = (float *)malloc((size_t)K * sizeof(float));
+    float *xq = (float *)malloc((size_t)(T * K) * sizeof(float));
+    void *qb = malloc(q80 ? (size_t)(K / 32) * 34 : (size_t)(K / OR_QK_K) * sizeof(or_block_q8K));
+    for (int64_t t = 0; t < T; ++t) {
+        if (q80) {
+            or_quantize_row_q8_0(X + t * K, qb, K);
+            or_dequantize_row_q8_0(qb, xq + t * K, K);
+        } else {
+            or_quantize_row_q8K(X + t * K, qb, K);
+            or_dequantize_row_q8K(qb, xq + t * K, K);
+        }
+    }
+    int rc = 0;
+    for (int64_t r = 0; r < M && !rc; ++r) {
+        rc = dequant_row_type(type, (const uint8_t *)W + (size_t)r * rb, wrow, K);
+        for (int64_t t = 0; t < T && !rc; ++t) {
+            double acc = 0;
+            const float *xt = xq + t * K;
+            for (int64_t c = 0; c < K; ++c) acc += (double)wrow[c] * (double)xt[c];
+            Y[t * M + r] = acc;
+        }
+    }
+    free(wrow);
+    free(xq);
+    free(qb);
+    return rc;
+}
+
+/* beast_matvec (desktop/beast_canyon/sp_beast_canyon.c:1122-1134) for Q4_K
+ * and Q8_0 rows, as the reference's own build of that file evaluates it
+ * (desktop/beast_canyon/CMakeLists.txt:52-54, GCC -O3 -mfma):
+ *   Q4_K (beast_dequant_q4_K, :1000-1021): w = d*sc * q - dmin*m. The
+ *     compiler fuses the multiply-subtract, but d*sc (an fp16 times a 6-bit
+ *     integer) times a 4-bit q is exact in fp32, so w equals
+ *     dequantize_row_q4_K's value bit for bit;
+ *   Q8_0 (beast_dequant_q8_0, :976-984): w = q * d;
+ *   y = y + w[c]*x[c] over c = 0 .. K-1 in index order, each product and
+ *     each sum rounded to fp32 (the vectorised loop multiplies eight at a
+ *     time and adds them one by one; its fused tail serves only K not a
+ *     multiple of 8, which no K-quant row has).
+ * beast_dequant_q5_K (:1056-1085) and beast_dequant_q6_K (:1025-1053) read
+ * other bits than ggml's dequantize_row_q5_K / _q6_K (the qh bit of a
+ * sub-block, the scale of a 16-value group), so they are not restated: for
+ * those types the format's own dequantiser is the parity target. */
+int or_beast_matvec_type(int type, const void *W, int64_t M, int64_t K, const float *x, float *y) {
+    if (type != OR_TYPE_Q4_K && type != OR_TYPE_Q8_0) return -22;
+    const size_t rb = row_bytes_type(type, K);
+    float *w = (float *)malloc((size_t)K * sizeof(float));
+    for (int64_t r = 0; r < M; ++r) {
+        const uint8_t *src = (const uint8_t *)W + (size_t)r * rb;
+        if (type == OR_TYPE_Q4_K) {
+            const or_block_q4K *b = (const or_block_q4K *)src;
+            for (int64_t i = 0; i < K / OR_QK_K; ++i) {
+                const float d = or_fp16_to_fp32(b[i].d), dmin = or_fp16_to_fp32(b[i].dmin);
+                for (int g = 0; g < 4; ++g) {
+                    uint8_t sc0, m0, sc1, m1;
+                    or_scale_min_k4(2 * g, b[i].scales, &sc0, &m0);
+                    or_scale_min_k4(2 * g + 1, b[i].scales, &sc1, &m1);
+                    const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+                    const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+                    const uint8_t *q = b[i].qs + 32 * g;
+                    float *wo = w + i * OR_QK_K + 64 * g;
+                    for (int l = 0; l < 32; ++l) wo[l] = d1 * (float)(q[l] & 0x0F) - mm1;
+                    for (int l = 0; l < 32; ++l) wo[32 + l] = d2 * (float)(q[l] >> 4) - mm2;
+                }
+            }
+        } else {
+            for (int64_t i = 0; i < K / 32; ++i) {
+                const float d = or_fp16_to_fp32((uint16_t)(src[34 * i] | (src[34 * i + 1] << 8)));
+                for (int j = 0; j < 32; ++j) w[32 * i + j] = (float)(int8_t)src[34 * i + 2 + j] * d;
+            }
+        }
+        float sum = 0.0f;
+        for (int64_t c = 0; c < K; ++c) sum += w[c] * x[c];
+        y[r] = sum;
+    }
+    free(w);
+    return 0;
 }
 
 /* ------------------------------------------------------------------------ */

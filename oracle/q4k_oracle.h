@@ -105,7 +105,8 @@ void or_mul_mat(const void *W, int64_t M, int64_t K, const float *X, int64_t T,
 int  or_mul_mat_id(const void *as, int64_t M, int64_t K, int64_t E,
                    const float *X, int64_t ne11, const int32_t *ids, int64_t k,
                    int64_t T, float *Y, int order);
-/* dequant-then-dot in double: the "dequant-then-dot" branch of the parity bar */
+/* dequant-then-dot in double with the fp32 activations as given (the exact
+ * value of an fp32-activation dequant-then-dot: beast_matvec's semantics) */
 void or_mul_mat_dequant_f64(const void *W, int64_t M, int64_t K, const float *X,
                             int64_t T, double *Y);
 
@@ -154,6 +155,17 @@ int or_mul_mat_id_type(int type, const void *as, int64_t M, int64_t K, int64_t E
                        int64_t T, float *Y, int order);
 int or_mul_mat_dequant_f64_type(int type, const void *W, int64_t M, int64_t K, const float *X,
                                 int64_t T, double *Y);
+/* dequantize_row_q8_K (ggml-quants.c:2731-2740) */
+void or_dequantize_row_q8K(const void *x, float *y, int64_t k);
+/* the parity bar's second form for the matmuls: sum of dequant(W) *
+ * dequant(Q(x)) in double, Q the type's activation quantiser (Q8_K, or
+ * Q8_0 for Q8_0 weights); types Q4_K, Q5_K, Q6_K, Q8_0 */
+int or_mul_mat_dq_f64_type(int type, const void *W, int64_t M, int64_t K, const float *X,
+                           int64_t T, double *Y);
+/* beast_matvec (sp_beast_canyon.c:1122-1134) as the reference's build
+ * evaluates it (fp32 products summed in index order), for one fp32 input x;
+ * Q4_K and Q8_0 */
+int or_beast_matvec_type(int type, const void *W, int64_t M, int64_t K, const float *x, float *y);
 
 /* synthetic data, bit-identical with the device generator */
 void or_synth_fill(float *out, int64_t n, uint64_t seed, int dist, int64_t cols,

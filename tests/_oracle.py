@@ -49,6 +49,13 @@ class Oracle:
         L.or_mul_mat_id.argtypes = [V, I64, I64, I64, V, I64, V, I64, I64, V, I]
         L.or_mul_mat_id.restype = I
         L.or_mul_mat_dequant_f64.argtypes = [V, I64, I64, V, I64, V]
+        L.or_mul_mat_dequant_f64_type.argtypes = [I, V, I64, I64, V, I64, V]
+        L.or_mul_mat_dequant_f64_type.restype = I
+        L.or_dequantize_row_q8K.argtypes = [V, V, I64]
+        L.or_mul_mat_dq_f64_type.argtypes = [I, V, I64, I64, V, I64, V]
+        L.or_mul_mat_dq_f64_type.restype = I
+        L.or_beast_matvec_type.argtypes = [I, V, I64, I64, V, V]
+        L.or_beast_matvec_type.restype = I
         L.or_synth_fill.argtypes = [V, I64, U64, I, I64, F, F, F, I64]
         L.or_rms_norm.argtypes = [V, I64, I64, V, F, V]
         L.or_swiglu.argtypes = [V, V, I64, V]
@@ -277,6 +284,46 @@ class Oracle:
         self.L.or_swiglu(_p(g), _p(u), g.size, _p(y))
         return y
 
+    def dequant_q8K(self, q: np.ndarray, k: int) -> np.ndarray:
+        y = np.empty(k, np.float32)
+        self.L.or_dequantize_row_q8K(_p(np.ascontiguousarray(q)), _p(y), k)
+        return y
+
+    def mul_mat_dq_f64(self, qtype, W, M, K, X) -> np.ndarray:
+        """sum of dequant(W) * dequant(Q(x)) in double (the second form of the parity bar)"""
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+        Y = np.empty((X.shape[0], M), np.float64)
+        assert self.L.or_mul_mat_dq_f64_type(qtype, _p(np.ascontiguousarray(W)), M, K, _p(X), X.shape[0], _p(Y)) == 0
+        return Y
+
+    def mul_mat_dequant_f64(self, qtype, W, M, K, X) -> np.ndarray:
+        """sum of dequant(W) * x in double, x as given (fp32-activation dequant-then-dot)"""
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+        Y = np.empty((X.shape[0], M), np.float64)
+        assert self.L.or_mul_mat_dequant_f64_type(qtype, _p(np.ascontiguousarray(W)), M, K, _p(X), X.shape[0],
+                                                  _p(Y)) == 0
+        return Y
+
+    def mul_mat_id_dq_f64(self, qtype, bank, M, K, E, X, ids) -> np.ndarray:
+        """mul_mat_id of the dequant-then-dot form: Y[t][s] = mul_mat_dq_f64 of
+        expert ids[t][s] on input row X[t][s % ne11]"""
+        ids = np.ascontiguousarray(ids, np.int32)
+        T, k = ids.shape
+        X = np.ascontiguousarray(X, np.float32).reshape(T, -1, K)
+        eb = bank.size // E
+        Y = np.empty((T, k, M), np.float64)
+        for t in range(T):
+            for s_ in range(k):
+                e = int(ids[t, s_])
+                Y[t, s_] = self.mul_mat_dq_f64(qtype, bank[e * eb:(e + 1) * eb], M, K, X[t, s_ % X.shape[1]])[0]
+        return Y
+
+    def beast_matvec(self, qtype, W, M, K, x) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.empty(M, np.float32)
+        assert self.L.or_beast_matvec_type(qtype, _p(np.ascontiguousarray(W)), M, K, _p(x), _p(y)) == 0
+        return y
+
     def synth(self, n, seed, dist=0, cols=0, mean=0.0, std=1.0, mult=1.0, offset=0) -> np.ndarray:
         out = np.empty(n, np.float32)
         self.L.or_synth_fill(_p(out), n, seed, dist, cols, mean, std, mult, offset)
@@ -445,8 +492,39 @@ def _ref_swiglu_ffn(self, qtype, Wg, Wu, M, K, X, w=None, eps=1e-6, nthreads=1):
     return Y
 
 
+def _ref_dequant_q8K(self, q, k):
+    """the reference's dequantize_row_q8_K (ggml-quants.c:2731-2740)"""
+    f = self.L.dequantize_row_q8_K
+    f.argtypes = [V, V, I64]
+    y = np.empty(k, np.float32)
+    f(_p(np.ascontiguousarray(q)), _p(y), k)
+    return y
+
+
 Ref.rms_norm = _ref_rms_norm
 Ref.swiglu_ffn = _ref_swiglu_ffn
+Ref.dequant_q8K = _ref_dequant_q8K
+
+BEAST_SO = os.path.join(REF_DIR, "beast", "libbeast_ref.so")
+
+
+class BeastRef:
+    """The reference's beast_matvec (desktop/beast_canyon/sp_beast_canyon.c:
+    1122-1134) compiled from its source by oracle/Makefile into
+    oracle/_ref/beast (oracle/beast_driver.c)."""
+
+    def __init__(self, path=BEAST_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (make -C oracle ref)")
+        self.L = C.CDLL(path)
+        self.L.ref_beast_matvec.argtypes = [V, C.c_uint, V, V, I, I]
+        self.L.ref_beast_matvec.restype = I
+
+    def matvec(self, qtype, W, M, K, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        y = np.empty(M, np.float32)
+        assert self.L.ref_beast_matvec(_p(np.ascontiguousarray(W)), qtype, _p(x), _p(y), M, K) == 0
+        return y
 
 
 def close_enough(a, b, rel=1e-4, abs_=1e-5):
@@ -459,3 +537,13 @@ def close_enough(a, b, rel=1e-4, abs_=1e-5):
     with np.errstate(divide="ignore", invalid="ignore"):
         rel_ok = d <= rel * scale
     return (a == b) | (d <= abs_) | rel_ok
+
+
+def parity_ok(got, exp, exact):
+    """The parity bar of the matmul outputs: each output
+    within close_enough of ggml_vec_dot's value (exp: the oracle in ggml's x86
+    order) or of the dequant-then-dot value (exact: the sum of dequant(W) *
+    dequant(Q(x)) in double, Oracle.mul_mat_dq_f64). Where a row's products
+    cancel, the two fp32 summation orders can differ by more than 1e-4 of the
+    small result while both stay within it of the exact sum."""
+    return close_enough(got, exp) | close_enough(got, exact)

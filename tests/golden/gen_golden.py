@@ -32,7 +32,12 @@ backend's activation quantiser (quantize_row_q8_0, which rounds half to even
 where the encoder rounds half away from zero: tie cases included),
 ggml_vec_dot_q8_0_q8_0 and its _generic form, MUL_MAT, MUL_MAT_ID.
 
-Usage: gen_golden.py [q4k] [q5k] [q6k] [q8_0]   (default: all)
+dq_golden.npz holds dequantize_row_q8_K outputs (the activation side of the
+dequant-then-dot form of the parity bar) and the reference's BurnHard scalar
+matvec beast_matvec (desktop/beast_canyon/sp_beast_canyon.c:1122-1134, built
+by oracle/Makefile from that file) on Q4_K and Q8_0 rows with fp32 inputs.
+
+Usage: gen_golden.py [q4k] [q5k] [q6k] [q8_0] [dq]   (default: all)
 """
 import os
 import sys
@@ -236,11 +241,39 @@ def gen_q6k(ref, rng):
     return out
 
 
+def gen_dq(ref, rng):
+    """Dequant-then-dot vectors: the reference's dequantize_row_q8_K of Q8_K
+    blocks (the activation side of the parity bar's dequant-then-dot form)
+    and the reference's own beast_matvec (desktop/beast_canyon, built into
+    oracle/_ref/beast) on Q4_K and Q8_0 rows with fp32 inputs."""
+    from _oracle import BeastRef, TYPE_Q4_K
+    beast = BeastRef()
+    out = {}
+    xq = np.concatenate([q8_inputs(rng), rng.standard_normal(QK * 8).astype(np.float32) * 3.0])
+    q8 = ref.quantize_q8K(xq)
+    out["dq8_q"] = q8
+    out["dq8_y"] = ref.dequant_q8K(q8, xq.size)
+    for tag, qtype in (("q4k", TYPE_Q4_K), ("q8_0", TYPE_Q8_0)):
+        for K, M in ((256, 4), (4096, 16), (12288, 8)):
+            w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+            W = ref.quantize_type(qtype, w, M, K)
+            x = rng.standard_normal(K).astype(np.float32)
+            out[f"beast_{tag}_{K}_W"] = W
+            out[f"beast_{tag}_{K}_x"] = x
+            out[f"beast_{tag}_{K}_y"] = beast.matvec(qtype, W, M, K, x)
+    return out
+
+
 def main():
     if ref_library_path() is None:
         sys.exit("oracle/_ref is not built (make -C oracle ref)")
-    which = set(sys.argv[1:]) or {"q4k", "q5k", "q6k", "q8_0"}
+    which = set(sys.argv[1:]) or {"q4k", "q5k", "q6k", "q8_0", "dq"}
     ref = Ref()
+    if "dq" in which:
+        out = gen_dq(ref, np.random.default_rng(0xD0D0))
+        path = os.path.join(HERE, "dq_golden.npz")
+        np.savez_compressed(path, **out)
+        print(f"wrote {path} ({os.path.getsize(path)/1024:.0f} KiB, {len(out)} arrays) using {ref.path}")
     for tag, fn in (("q6k", lambda: gen_q6k(ref, np.random.default_rng(0x6B6B))),
                     ("q5k", lambda: gen_kquant(ref, np.random.default_rng(0x5B5B), TYPE_Q5_K, Q5K)),
                     ("q8_0", lambda: gen_q8_0(ref, np.random.default_rng(0x8080)))):

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from _envctx import context_with as _context_with
-from _oracle import close_enough
+from _oracle import close_enough, parity_ok
 
 pytestmark = pytest.mark.gpu
 
@@ -23,8 +23,10 @@ def _weights(oracle, rng, M, K, scale=0.02):
     return oracle.quantize_q4K((rng.standard_normal((M, K)) * scale).astype(np.float32))
 
 
-def _check(got, exp, what):
-    ok = close_enough(got, exp)
+def _check(got, exp, what, exact=None):
+    """close_enough of the oracle (ggml's x86 order); with `exact`, the parity
+    bar's either-or: of the oracle or of the dequant-then-dot value"""
+    ok = close_enough(got, exp) if exact is None else parity_ok(got, exp, exact)
     if not ok.all():
         i = np.argwhere(~ok)[0]
         raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} outside tolerance; first {tuple(i)} "
@@ -38,7 +40,7 @@ def test_decode_single(ctx, oracle, M, K):
     W = _weights(oracle, rng, M, K)
     x = rng.standard_normal((1, K)).astype(np.float32)
     Wd = ctx.upload(W, M, K)
-    _check(ctx.mul_mat(Wd, x), oracle.mul_mat(W, M, K, x), f"decode M={M} K={K}")
+    _check(ctx.mul_mat(Wd, x), oracle.mul_mat(W, M, K, x), f"decode M={M} K={K}", oracle.mul_mat_dq_f64(12, W, M, K, x))
 
 
 @pytest.mark.parametrize("K,shapes", [(4096, (4096, 1024, 1024)), (4096, (12288, 12288)), (12288, (4096,)),

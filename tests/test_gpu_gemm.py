@@ -9,14 +9,16 @@ import os
 import numpy as np
 import pytest
 
-from _oracle import close_enough
+from _oracle import close_enough, parity_ok
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
-def _check(got, exp, what):
-    ok = close_enough(got, exp)
+def _check(got, exp, what, exact=None):
+    """close_enough of the oracle (ggml's x86 order); with `exact`, the parity
+    bar's either-or: of the oracle or of the dequant-then-dot value"""
+    ok = close_enough(got, exp) if exact is None else parity_ok(got, exp, exact)
     assert ok.all(), (f"{what}: {int((~ok).sum())}/{ok.size} outside tolerance; first {np.argwhere(~ok)[0]} "
                       f"got {got[tuple(np.argwhere(~ok)[0])]} exp {exp[tuple(np.argwhere(~ok)[0])]}")
 
@@ -35,7 +37,8 @@ def test_gemm_vs_oracle(ctx, oracle, M, K, T):
     W = oracle.quantize_q4K((rng.standard_normal((M, K)) * 0.02).astype(np.float32))
     X = rng.standard_normal((T, K)).astype(np.float32)
     Wd = ctx.upload(W, M, K)
-    _check(ctx.mul_mat(Wd, X), oracle.mul_mat(W, M, K, X), f"gemm M={M} K={K} T={T}")
+    _check(ctx.mul_mat(Wd, X), oracle.mul_mat(W, M, K, X), f"gemm M={M} K={K} T={T}",
+           oracle.mul_mat_dq_f64(12, W, M, K, X))
 
 
 @pytest.mark.parametrize("T", [1, 3, 8])

@@ -8,7 +8,7 @@ reference's own ggml_vec_dot_q4_K_q8_K (pinned in test_oracle_golden.py)."""
 import numpy as np
 import pytest
 
-from _oracle import close_enough
+from _oracle import close_enough, parity_ok
 
 pytestmark = pytest.mark.gpu
 
@@ -17,8 +17,10 @@ def _weights(oracle, rng, M, K, scale=0.02):
     return oracle.quantize_q4K((rng.standard_normal((M, K)) * scale).astype(np.float32))
 
 
-def _check(got, exp, what):
-    ok = close_enough(got, exp)
+def _check(got, exp, what, exact=None):
+    """close_enough of the oracle (ggml's x86 order); with `exact`, the parity
+    bar's either-or: of the oracle or of the dequant-then-dot value"""
+    ok = close_enough(got, exp) if exact is None else parity_ok(got, exp, exact)
     if not ok.all():
         i = np.argwhere(~ok)[0]
         raise AssertionError(f"{what}: {int((~ok).sum())} of {ok.size} outside tolerance; first {tuple(i)} "
@@ -52,7 +54,7 @@ def test_gemv_t1(ctx, oracle, M, K):
     Wd = ctx.upload(W, M, K)
     got = ctx.mul_mat(Wd, x)
     exp = oracle.mul_mat(W, M, K, x)
-    _check(got, exp, f"gemv M={M} K={K}")
+    _check(got, exp, f"gemv M={M} K={K}", oracle.mul_mat_dq_f64(12, W, M, K, x))
 
 
 @pytest.mark.parametrize("sdot4", [False, True])

@@ -10,15 +10,17 @@ import os
 import numpy as np
 import pytest
 
-from _oracle import close_enough
+from _oracle import close_enough, parity_ok
 
 pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
-def _check(got, exp, what):
-    ok = close_enough(got, exp)
+def _check(got, exp, what, exact=None):
+    """close_enough of the oracle (ggml's x86 order); with `exact`, the parity
+    bar's either-or: of the oracle or of the dequant-then-dot value"""
+    ok = close_enough(got, exp) if exact is None else parity_ok(got, exp, exact)
     assert ok.all(), f"{what}: {int((~ok).sum())}/{ok.size} outside tolerance, first {np.argwhere(~ok)[0]}"
 
 
@@ -61,7 +63,7 @@ def test_moe_30b_shapes(ctx, oracle, M, K, T, ne11):
     X = rng.standard_normal((T, ne11, K)).astype(np.float32)
     got = ctx.mul_mat_id(bank, X, ids)
     exp = oracle.mul_mat_id(host, M, K, E, X, ids)
-    _check(got, exp, f"moe M={M} K={K} T={T} ne11={ne11}")
+    _check(got, exp, f"moe M={M} K={K} T={T} ne11={ne11}", oracle.mul_mat_id_dq_f64(12, host, M, K, E, X, ids))
 
 
 @pytest.mark.parametrize("env", [{}, {"SPQ4K_MOE_MODE": 3}])
