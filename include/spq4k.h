@@ -227,6 +227,22 @@ int spq4k_gemm(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y,
 int spq4k_gemm_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *W, const float *X, float *const *Y,
                      int64_t T);
 int spq4k_mul_mat(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
+/* spq4k_mul_mat_noalloc: spq4k_mul_mat (same kernels, same results) with
+ * every intermediate (activation planes, K-split partial sums) in a fixed
+ * device array of SPQ4K_NOALLOC_SCRATCH_BYTES that each GPU holds from the
+ * library's first use on it until the process ends, in place of the
+ * context's scratch: the call never allocates (no hipMalloc, hipFree or
+ * allocating library routine). It has no counterpart in the reference; it is
+ * for callers that cannot allocate: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation. Limit: T rows of K inputs
+ * whose activation planes (spq4k_reserve's sizes) exceed
+ * SPQ4K_NOALLOC_PLANES_MAX are rejected with -EINVAL. Every call on one GPU
+ * shares its array, from any context: calls that overlap on one GPU (two
+ * streams, two threads, two contexts) race on it and must be ordered by the
+ * caller. */
+#define SPQ4K_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+#define SPQ4K_NOALLOC_PLANES_MAX ((size_t)24 << 20)
+int spq4k_mul_mat_noalloc(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
 int spq4k_moe(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int64_t n_used,
               int64_t ne11, int64_t T, const float *X, float *Y);
 /* spq4k_moe_multi: the n (1 or 2) GGML_OP_MUL_MAT_ID nodes of one MoE layer

@@ -11,6 +11,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include <hip/hip_runtime.h>
@@ -35,6 +36,9 @@ struct spq4k_ctx {
     size_t scratch2_cap = 0;
     // scratch buffers replaced by larger ones, freed by spq4k_free
     std::vector<void*> retired;
+    // set while a call runs on the no-allocation scratch (spq4k_mul_mat_noalloc):
+    // a call that needs more than it holds fails instead of allocating
+    bool no_alloc = false;
     int force_bpr = 0;           // tuning override (SPQ4K_GEMV_BPR = 1, 2, 4 or 8)
     int preq_mode = 0;           // SPQ4K_GEMV_PREQ: 0 auto, 1 always, 2 never
     int gemv_mfma_min_t = 4;     // SPQ4K_GEMV_MFMA_MIN_T: batches of at least this many tokens use matrix cores
@@ -139,6 +143,9 @@ int use_device(spq4k_ctx* c) {
 // capture; spq4k_reserve grows the buffers ahead of a capture.
 int grow_scratch(spq4k_ctx* c, uint8_t** buf, size_t* cap, size_t bytes, size_t min_cap, const char* what) {
     if (bytes <= *cap) return 0;
+    if (c->no_alloc)
+        return set_err(c, -EINVAL, "%s: %zu bytes needed, beyond the %zu bytes of the no-allocation scratch", what,
+                       bytes, *cap);
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     SPQ_HIP(c, hipStreamIsCapturing(c->stream, &cs));
     if (cs != hipStreamCaptureStatusNone)
@@ -579,6 +586,39 @@ int gemv_chunked(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float
 
 }  // namespace
 
+// ---- the no-allocation scratch ---------------------------------------------
+// Device memory of spq4k_mul_mat_noalloc: a file-scope array, so that the
+// entry point needs no hipMalloc. Every GPU the library runs on holds its own
+// copy (SPQ4K_NOALLOC_SCRATCH_BYTES) from the first use of the library on
+// that GPU until the process ends. In host code `scratch` names a host-side
+// stand-in, never the device memory: its device address is looked up once per
+// device (hipGetSymbolAddress, at spq4k_init with the device current) and only
+// that address is passed to kernels.
+static __device__ __align__(256) uint8_t scratch[SPQ4K_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_noalloc_mu;
+uint8_t* g_noalloc_ptr[NOALLOC_MAX_DEVICES] = {};
+
+// device address of `scratch` on `device`, the current device (0 on error)
+int noalloc_scratch_setup(int device) {
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) return -ENODEV;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (g_noalloc_ptr[device]) return 0;
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return -EIO;
+    g_noalloc_ptr[device] = static_cast<uint8_t*>(p);
+    return 0;
+}
+
+uint8_t* noalloc_scratch_of(int device) {
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    return g_noalloc_ptr[device];
+}
+}  // namespace
+
 // ============================================================================
 extern "C" {
 
@@ -659,6 +699,11 @@ int spq4k_init(int device, spq4k_ctx** out) {
     if (const char* f = getenv("SPQ4K_Q80_PREQ")) {
         const int v = atoi(f);
         if (v == 1 || v == 2) c->q80_preq = v;
+    }
+    if (noalloc_scratch_setup(device) != 0) {
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return -EIO;
     }
     // scratch for Q8_K activation planes: sized for prefill batches up front
     // so that steady-state calls (and graph capture) never allocate
@@ -1198,6 +1243,33 @@ int spq4k_gemm(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, i
 int spq4k_mul_mat(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
     if (T >= 1 && T <= SPQ4K_GEMV_MAX_T) return spq4k_gemv(c, W, X, Y, T);
     return spq4k_gemm(c, W, X, Y, T);
+}
+
+int spq4k_mul_mat_noalloc(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!W || !W->data) return set_err(c, -EINVAL, "mul_mat_noalloc: null weight");
+    uint8_t* base = noalloc_scratch_of(c->device);
+    if (!base) return set_err(c, -EIO, "mul_mat_noalloc: no device address of the no-allocation scratch");
+    if (T < 1 || T > (1 << 20)) return set_err(c, -EINVAL, "mul_mat_noalloc: T=%lld", (long long)T);
+    // the activation planes must leave the partial plane of a K split its 8 MiB
+    const size_t planes = W->fmt == WF_Q80 ? q80_planes_bytes(T, (int)(W->K / SPQ4K_QK8_0))
+                                           : q8_planes_bytes((int)T, (int)(W->K / SPQ4K_QK_K));
+    if (planes > SPQ4K_NOALLOC_PLANES_MAX)
+        return set_err(c, -EINVAL,
+                       "mul_mat_noalloc: T=%lld rows of K=%lld need %zu bytes of activation planes, more than the "
+                       "%zu the no-allocation scratch holds for them", (long long)T, (long long)W->K, planes,
+                       (size_t)SPQ4K_NOALLOC_PLANES_MAX);
+    uint8_t* const own = c->scratch;
+    const size_t own_cap = c->scratch_cap;
+    c->scratch = base;
+    c->scratch_cap = SPQ4K_NOALLOC_SCRATCH_BYTES;
+    c->no_alloc = true;
+    rc = spq4k_mul_mat(c, W, X, Y, T);
+    c->scratch = own;
+    c->scratch_cap = own_cap;
+    c->no_alloc = false;
+    return rc;
 }
 
 int spq4k_reserve(spq4k_ctx* c, size_t scratch_bytes, size_t fusion_bytes) {

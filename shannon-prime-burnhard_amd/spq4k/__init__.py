@@ -156,6 +156,7 @@ def load_library(path: str | None = None):
         "spq4k_vec_dot_q8_0_host": (I, [V, I, V, V, V]),
         "spq4k_synth_fill": (I, [V, V, I64, U64, I, I64, F, F, F, I64]),
         "spq4k_reserve": (I, [V, S, S]),
+        "spq4k_mul_mat_noalloc": (I, [V, V, V, V, I64]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
