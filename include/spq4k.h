@@ -291,6 +291,54 @@ int spq4k_mul_mat_host(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, f
 int spq4k_moe_host(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int64_t n_used,
                    int64_t ne11, int64_t T, const float *X, float *Y);
 
+/* ---- decode chains: dependent T = 1 stages in one launch -----------------
+ * Replaces, for a run of a dense decode graph's nodes, the per-node
+ * execution of the reference's decode layer (build_block_decode,
+ * desktop/engine/src/forward.cpp:2663-2856: rms_norm * attn_norm, the q/k/v
+ * MUL_MATs, the o MUL_MAT, the residual add, rms_norm * ffn_norm, gate / up,
+ * silu * up, down, the residual add; and the output head, :3411-3413) --
+ * everything but the attention core, which stays with the engine. Each
+ * stage is
+ *     x    = in0 (+ in1)                    ggml_add, fp32
+ *     x_out = x                             when x_out is set (the residual)
+ *     x    = rms_norm(x, eps) * norm_w      when norm_w is set
+ *     y[i] = W[i] . Q8_K(x), i < n          n <= 4 matrices sharing x
+ *  or y[0] = silu(W[0] . Q8_K(x)) * (W[1] . Q8_K(x))   with glu (n = 2)
+ * with the arithmetic of spq4k_mul_mat_rms_norm / spq4k_mul_mat_swiglu at
+ * T = 1 (the norm bit-exact but for its double sum's order; Q8_K bit-exact;
+ * the matvec's per-lane sums those of the decode kernel). The stages run
+ * in order, each seeing every earlier stage's outputs, in one cooperative
+ * launch that streams the next stages' weights while a stage waits for the
+ * previous one. Q4_K weights, E = 1, K <= 12288; per stage
+ * (1 + [in1] + [norm_w]) * K <= 12288; all pointers device pointers,
+ * 16-byte aligned; a stage's outputs (y, x_out) must not overlap its inputs
+ * (in0, in1). Stages may read what any earlier stage wrote.
+ *   spq4k_chain_create  validates and uploads the stage table;
+ *   spq4k_chain_run     launches it on the context's stream (asynchronous);
+ *   spq4k_chain_status  synchronises and returns 0, or -ETIMEDOUT if a
+ *                       stage wait gave up (the outputs are then invalid;
+ *                       the chain is reset for the next run);
+ *   spq4k_chain_free    releases it.
+ * A chain runs one launch at a time (its barrier counters are its own).
+ * No reference entry point takes a whole chain; the per-node entry points
+ * above remain the drop-in for single nodes. */
+typedef struct spq4k_chain spq4k_chain;
+typedef struct spq4k_chain_stage {
+    int n;                             /* matrices sharing the input, 1..4 (2 with glu) */
+    int glu;                           /* y[0] = silu(W[0] . x) * (W[1] . x) */
+    const spq4k_weights *W[4];
+    float *y[4];                       /* [M_i] each */
+    const float *in0;                  /* [K] */
+    const float *in1;                  /* [K] or NULL */
+    float *x_out;                      /* [K] or NULL */
+    const float *norm_w;               /* [K] or NULL */
+} spq4k_chain_stage;
+int spq4k_chain_create(spq4k_ctx *ctx, const spq4k_chain_stage *stages, int n_stages, float eps,
+                       spq4k_chain **out);
+int spq4k_chain_run(spq4k_ctx *ctx, spq4k_chain *chain);
+int spq4k_chain_status(spq4k_ctx *ctx, spq4k_chain *chain);
+void spq4k_chain_free(spq4k_chain *chain);
+
 /* ---- diagnostics -------------------------------------------------------
  * Exact integer sub-block sums S[r][b][j] = sum_{l<32} q4 * q8 over
  * sub-block j of block b of row r, against Q8_K(x), formed by the same lane

@@ -1867,3 +1867,165 @@ int spq4k_synth_fill(spq4k_ctx* c, float* out, int64_t n, uint64_t seed, int dis
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// decode chains (k_chain.hip)
+struct spq4k_chain {
+    int device = 0;
+    ChainStage* d_st = nullptr;
+    ChainSync* d_sync = nullptr;
+    int nstages = 0;
+    float eps = 0.0f;
+    int grid = 0;
+    int shape = 0;
+};
+
+namespace {
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+    if (!a || !b) return false;
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + nb && y < x + na;
+}
+}  // namespace
+
+extern "C" {
+
+void spq4k_chain_free(spq4k_chain* ch) {
+    if (!ch) return;
+    int prev = -1;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(ch->device);
+    if (ch->d_st) (void)hipFree(ch->d_st);
+    if (ch->d_sync) (void)hipFree(ch->d_sync);
+    if (prev >= 0) (void)hipSetDevice(prev);
+    delete ch;
+}
+
+int spq4k_chain_create(spq4k_ctx* c, const spq4k_chain_stage* stages, int n, float eps, spq4k_chain** out) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!out) return set_err(c, -EINVAL, "chain_create: null output");
+    *out = nullptr;
+    if (!stages || n <= 0 || n > (1 << 20)) return set_err(c, -EINVAL, "chain_create: bad stage count %d", n);
+    if (!(eps >= 0.0f)) return set_err(c, -EINVAL, "chain_create: bad eps");
+    int shape = 0;
+    if (const char* f = getenv("SPQ4K_CHAIN_SHAPE")) {
+        const int v = atoi(f);
+        if (v >= 0 && v <= 2) shape = v;
+    }
+    const int grid = chain_grid(c->num_cus);
+    if (grid <= 0) return set_err(c, -ENODEV, "chain_create: %d CUs is too few", c->num_cus);
+    const int cw = chain_compute_waves(shape);
+    const int64_t G = (int64_t)grid * cw;
+    std::vector<ChainStage> tab((size_t)n);
+    for (int s = 0; s < n; ++s) {
+        const spq4k_chain_stage& in = stages[s];
+        ChainStage& o = tab[(size_t)s];
+        memset(&o, 0, sizeof o);
+        if (in.n < 1 || in.n > 4 || (in.glu && in.n != 2))
+            return set_err(c, -EINVAL, "chain stage %d: %d matrices%s", s, in.n, in.glu ? " with glu (needs 2)" : "");
+        const int64_t K = in.W[0] ? in.W[0]->K : 0;
+        int64_t rows = 0;
+        for (int j = 0; j < in.n; ++j) {
+            const spq4k_weights* w = in.W[j];
+            const bool need_y = !(in.glu && j == 1);   // with glu the product goes to y[0]
+            if (!w || (need_y && !in.y[j])) return set_err(c, -EINVAL, "chain stage %d: null matrix or output %d", s, j);
+            if (w->device != c->device) return set_err(c, -EINVAL, "chain stage %d: weights on another device", s);
+            if (w->type != SPQ4K_TYPE_Q4_K || w->E != 1)
+                return set_err(c, -EINVAL, "chain stage %d: matrix %d is not a dense Q4_K matrix", s, j);
+            if (w->K != K) return set_err(c, -EINVAL, "chain stage %d: matrices differ in K", s);
+            if (need_y && !aligned(in.y[j], 16))
+                return set_err(c, -EINVAL, "chain stage %d: output %d not 16-byte aligned", s, j);
+            o.W[j] = w->data;
+            o.Y[j] = in.y[j];
+            if (!in.glu) {
+                o.row_begin[j] = (int32_t)rows;
+                rows += w->M;
+            }
+        }
+        if (in.glu) {
+            if (in.W[0]->M != in.W[1]->M) return set_err(c, -EINVAL, "chain stage %d: gate and up rows differ", s);
+            rows = in.W[0]->M;
+            o.row_begin[0] = 0;
+            o.Y[1] = nullptr;
+        }
+        for (int j = in.glu ? 1 : in.n; j < 4; ++j) o.row_begin[j] = INT32_MAX;
+        if (K <= 0 || K % SPQ4K_QK_K || K / SPQ4K_QK_K > CHAIN_MAX_NB)
+            return set_err(c, -EINVAL, "chain stage %d: K = %lld (a multiple of 256 up to %d)", s, (long long)K,
+                           CHAIN_MAX_K);
+        if (rows <= 0 || rows > INT32_MAX / 2 || (rows + G - 1) / G * cw > CHAIN_YCAP)
+            return set_err(c, -EINVAL, "chain stage %d: %lld rows", s, (long long)rows);
+        const int nvec = 1 + (in.in1 ? 1 : 0) + (in.norm_w ? 1 : 0);
+        if (nvec * K > CHAIN_MAX_K)
+            return set_err(c, -EINVAL, "chain stage %d: %d input vectors of %lld exceed %d values", s, nvec,
+                           (long long)K, CHAIN_MAX_K);
+        if (!in.in0 || !aligned(in.in0, 16) || !aligned(in.in1, 16) || !aligned(in.x_out, 16) ||
+            !aligned(in.norm_w, 16))
+            return set_err(c, -EINVAL, "chain stage %d: null or misaligned input", s);
+        const size_t xb = (size_t)K * sizeof(float);
+        for (int j = 0; j < in.n; ++j) {
+            const size_t yb = (size_t)(in.glu ? rows : in.W[j]->M) * sizeof(float);
+            if (in.glu && j == 1) break;
+            if (overlaps(in.y[j], yb, in.in0, xb) || overlaps(in.y[j], yb, in.in1, xb) ||
+                overlaps(in.y[j], yb, in.x_out, xb))
+                return set_err(c, -EINVAL, "chain stage %d: output %d overlaps the stage's inputs", s, j);
+        }
+        if (overlaps(in.x_out, xb, in.in0, xb) || overlaps(in.x_out, xb, in.in1, xb))
+            return set_err(c, -EINVAL, "chain stage %d: x_out overlaps the stage's inputs", s);
+        o.rows = (int32_t)rows;
+        o.nb = (int32_t)(K / SPQ4K_QK_K);
+        o.glu = in.glu ? 1 : 0;
+        o.in0 = in.in0;
+        o.in1 = in.in1;
+        o.xout = in.x_out;
+        o.norm_w = in.norm_w;
+    }
+    spq4k_chain* ch = new (std::nothrow) spq4k_chain();
+    if (!ch) return set_err(c, -ENOMEM, "chain_create: out of host memory");
+    ch->device = c->device;
+    ch->nstages = n;
+    ch->eps = eps;
+    ch->grid = grid;
+    ch->shape = shape;
+    hipError_t e = hipMalloc(&ch->d_st, sizeof(ChainStage) * (size_t)n);
+    if (e == hipSuccess) e = hipMalloc(&ch->d_sync, sizeof(ChainSync));
+    if (e == hipSuccess) e = hipMemcpy(ch->d_st, tab.data(), sizeof(ChainStage) * (size_t)n, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(ch->d_sync, 0, sizeof(ChainSync));
+    if (e != hipSuccess) {
+        spq4k_chain_free(ch);
+        return e == hipErrorOutOfMemory ? set_err(c, -ENOMEM, "chain_create: out of device memory")
+                                        : hip_fail(c, e, "chain_create");
+    }
+    *out = ch;
+    return 0;
+}
+
+int spq4k_chain_run(spq4k_ctx* c, spq4k_chain* ch) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!ch || ch->device != c->device) return set_err(c, -EINVAL, "chain_run: no chain for this device");
+    ChainParams p;
+    p.st = ch->d_st;
+    p.sync = ch->d_sync;
+    p.nstages = ch->nstages;
+    p.eps = ch->eps;
+    hipError_t e = launch_chain(p, ch->grid, ch->shape, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "chain launch");
+    return 0;
+}
+
+int spq4k_chain_status(spq4k_ctx* c, spq4k_chain* ch) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!ch || ch->device != c->device) return set_err(c, -EINVAL, "chain_status: no chain for this device");
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    uint32_t err = 0;
+    SPQ_HIP(c, hipMemcpy(&err, &ch->d_sync->err, sizeof err, hipMemcpyDeviceToHost));
+    if (err) {
+        SPQ_HIP(c, hipMemset(ch->d_sync, 0, sizeof(ChainSync)));
+        return set_err(c, -ETIMEDOUT, "chain: a stage wait gave up; outputs invalid, chain reset");
+    }
+    return 0;
+}
+
+}  // extern "C"

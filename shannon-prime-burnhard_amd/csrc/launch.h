@@ -249,4 +249,48 @@ hipError_t launch_gemv_q8_0(const Q80Params& p, int T, bool global_acts, int gri
 hipError_t launch_moe_q8_0_sweep(const Q80Params& p, int grid, hipStream_t st);
 hipError_t launch_moe_q8_0_grouped(const Q80Params& p, int tc, int grid, hipStream_t st);
 
+// A chain of dependent T = 1 Q4_K matvec stages in one persistent launch
+// (k_chain.hip). Stage s: x = in0 (+ in1); xout = x when set; x = rms_norm(x)
+// * norm_w when set; Q8_K(x); then either the matrices W[j] (rows of segment
+// j at row_begin[j] .. row_begin[j + 1]) or, with glu, y = silu(W[0] . x) *
+// (W[1] . x) into Y[0].
+constexpr int CHAIN_MAX_NB = 48;                 // K <= 12288
+constexpr int CHAIN_MAX_K = CHAIN_MAX_NB * 256;  // fp32 input staging (LDS)
+constexpr int CHAIN_NCTR = 16;                   // grid-barrier counters
+constexpr int CHAIN_YCAP = 1024;                 // row results a workgroup holds per stage
+
+struct ChainStage {
+    const uint8_t* W[4];
+    float* Y[4];
+    int32_t row_begin[4];   // [0] = 0; segments not used start at INT32_MAX
+    int32_t rows;           // total rows (glu: rows of the gate, = up)
+    int32_t nb;             // Q4_K blocks per row
+    int32_t glu;
+    int32_t pad;
+    const float* in0;       // [nb * 256]
+    const float* in1;       // optional, added to in0
+    float* xout;            // optional: in0 (+ in1) written here
+    const float* norm_w;    // optional: RMS norm weights
+};
+
+struct ChainSync {
+    uint32_t ctr[CHAIN_NCTR * 64];   // arrival counters, 256 B apart
+    uint32_t gen;                    // launches completed past their first grid wait
+    uint32_t pad0[63];
+    uint32_t err;                    // set when a wait gave up
+    uint32_t pad1[63];
+};
+
+struct ChainParams {
+    const ChainStage* st;   // device table of nstages stages
+    ChainSync* sync;        // zeroed before the chain's first launch
+    int32_t nstages;
+    float eps;
+};
+// workgroups of a chain launch on a device with num_cus CUs (a multiple of CHAIN_NCTR)
+int chain_grid(int num_cus);
+// launch shapes (compute waves x pieces in flight each): 0 = 8 x 8, 1 = 8 x 6, 2 = 7 x 8
+int chain_compute_waves(int shape);
+hipError_t launch_chain(const ChainParams& p, int grid, int shape, hipStream_t st);
+
 }  // namespace spq4k

@@ -157,6 +157,10 @@ def load_library(path: str | None = None):
         "spq4k_synth_fill": (I, [V, V, I64, U64, I, I64, F, F, F, I64]),
         "spq4k_reserve": (I, [V, S, S]),
         "spq4k_mul_mat_noalloc": (I, [V, V, V, V, I64]),
+        "spq4k_chain_create": (I, [V, C.POINTER(ChainStage), I, F, PV]),
+        "spq4k_chain_run": (I, [V, V]),
+        "spq4k_chain_status": (I, [V, V]),
+        "spq4k_chain_free": (None, [V]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -164,6 +168,39 @@ def load_library(path: str | None = None):
         fn.argtypes = args
     _lib = lib
     return lib
+
+
+class ChainStage(C.Structure):
+    """spq4k_chain_stage (include/spq4k.h): one stage of a decode chain."""
+    _fields_ = [("n", C.c_int), ("glu", C.c_int), ("W", C.c_void_p * 4), ("y", C.c_void_p * 4),
+                ("in0", C.c_void_p), ("in1", C.c_void_p), ("x_out", C.c_void_p), ("norm_w", C.c_void_p)]
+
+
+class Chain:
+    """A prepared decode chain (spq4k_chain): dependent T = 1 stages run by one launch."""
+
+    def __init__(self, ctx: "Context", handle, n_stages: int, refs):
+        self.ctx, self.handle, self.n_stages = ctx, handle, n_stages
+        self._refs = refs   # the Weights the stage table points into
+
+    def run(self):
+        """Launch the chain on the context's stream (asynchronous)."""
+        self.ctx._check("spq4k_chain_run", self.ctx.lib.spq4k_chain_run(self.ctx.handle, self.handle))
+
+    def status(self):
+        """Synchronise; raises (rc -ETIMEDOUT) if a stage wait gave up."""
+        self.ctx._check("spq4k_chain_status", self.ctx.lib.spq4k_chain_status(self.ctx.handle, self.handle))
+
+    def free(self):
+        if self.handle:
+            self.ctx.lib.spq4k_chain_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 def _ptr(a):
@@ -552,6 +589,30 @@ class Context:
     def mul_mat_swiglu_dev(self, Wg, Wu, x_dev: int, norm_w_dev, eps: float, y_dev: int, T: int = 1):
         self._check("spq4k_mul_mat_swiglu",
                     self.lib.spq4k_mul_mat_swiglu(self.handle, Wg.handle, Wu.handle, x_dev, norm_w_dev, eps, y_dev, T))
+
+    def chain_create(self, stages, eps: float) -> Chain:
+        """spq4k_chain_create. `stages` is a list of dicts: W (list of Weights),
+        y (list of device pointers; with glu one), in0, and optionally glu,
+        in1, x_out, norm_w (device pointers)."""
+        n = len(stages)
+        arr = (ChainStage * n)()
+        refs = []
+        for i, st in enumerate(stages):
+            Ws = st["W"]
+            arr[i].n = len(Ws)
+            arr[i].glu = 1 if st.get("glu") else 0
+            for j, w in enumerate(Ws):
+                arr[i].W[j] = w.handle.value if isinstance(w.handle, C.c_void_p) else w.handle
+                refs.append(w)
+            for j, y in enumerate(st["y"]):
+                arr[i].y[j] = y
+            arr[i].in0 = st["in0"]
+            arr[i].in1 = st.get("in1")
+            arr[i].x_out = st.get("x_out")
+            arr[i].norm_w = st.get("norm_w")
+        h = C.c_void_p()
+        self._check("spq4k_chain_create", self.lib.spq4k_chain_create(self.handle, arr, n, eps, C.byref(h)))
+        return Chain(self, h, n, refs)
 
     def quantize_q8_0_dev(self, x: int, vy: int, k: int):
         self._check("spq4k_quantize_q8_0", self.lib.spq4k_quantize_q8_0(self.handle, x, vy, k))
