@@ -14,7 +14,13 @@ Metric: effective HBM GB/s = algorithmic bytes of the step (Q4_K weights +
 fp32 x and y of every matvec: 4,268,590,592 B) / step time; also tok/s-equiv
 and % of the 8 TB/s peak. Every launch of the step is gemv_decode_kernel, so
 the HIP events around the timed replays give that kernel's average launch
-duration directly. Each stage kind (q/k/v, o, gate/up, down, lm_head) is also
+duration directly. Beside it ("chain"), the same weights run as one
+dependent decode chain in one cooperative launch of chain_kernel
+(spq4k_chain_run): per layer rms_norm * attn_norm -> [q,k,v] -> o -> residual
+add, rms_norm * ffn_norm -> silu(gate) * up -> down -> residual add, then the
+output norm and lm_head, each stage reading what the stages before it wrote
+(the q projection stands in for the attention output, which is not on this
+path). Each stage kind (q/k/v, o, gate/up, down, lm_head) is also
 replayed on its own for a per-stage breakdown. CPU baseline: the reference's
 own ggml CPU path (oracle/_ref, built from /root/reference sources) on a
 bounded sample of the same workload (layers 0-9, 1.09 GB, larger than the
@@ -121,6 +127,73 @@ def build_decode8b(ctx):
     return stages
 
 
+CHAIN_EPS = 1e-6
+
+
+def build_chain8b(ctx, stages):
+    """The same weights as one dependent decode step (build_block_decode,
+    desktop/engine/src/forward.cpp:2663-2856, and the output head, :3411-3413):
+    per layer
+        A: x = h + down (the residual), xres = x, rms_norm * attn_norm, q/k/v
+        B: o of the attention output (the attention core is outside this path;
+           the q projection, of the same shape, stands in for its output)
+        C: x = xres + o, h = x, rms_norm * ffn_norm, silu(gate) * up
+        D: down
+    then logits = out . (rms_norm(h + down) * out_norm). Every stage's input is
+    what the stages before it wrote. Norm weights are seeded N(1, 0.2)."""
+    bufs = []
+
+    def buf(n, seed=None):
+        a = DeviceArray(n, np.float32)
+        if seed is None:
+            a.fill_byte(0)
+        else:
+            ctx.synth_fill_dev(a.ptr, n, seed, spq4k.DIST_NORMAL, 0, 1.0, 0.2, 1.0, 0)
+        bufs.append(a)
+        return a.ptr
+
+    x0a = DeviceArray(HID, np.float32)
+    ctx.synth_fill_dev(x0a.ptr, HID, 7, spq4k.DIST_NORMAL, 0, 0.0, 1.0, 1.0, 0)
+    bufs.append(x0a)
+    x0 = x0a.ptr
+    chain = []
+    h = d = None
+    for L in range(LAYERS):
+        (_, (q, k, v), _, _), (_, (o,), _, _), (_, (g, u), _, _), (_, (dn,), _, _) = stages[4 * L:4 * L + 4]
+        yq, yk, yv, yo = buf(HID), buf(KV), buf(KV), buf(HID)
+        yg, yd, xres, hn = buf(FFN), buf(HID), buf(HID), buf(HID)
+        an, fn = buf(HID, 50000 + 2 * L), buf(HID, 50001 + 2 * L)
+        a = {"W": [q, k, v], "y": [yq, yk, yv], "in0": x0 if h is None else h, "x_out": xres, "norm_w": an}
+        if d is not None:
+            a["in1"] = d
+        chain.append(a)
+        chain.append({"W": [o], "y": [yo], "in0": yq})
+        chain.append({"W": [g, u], "y": [yg], "glu": 1, "in0": xres, "in1": yo, "x_out": hn, "norm_w": fn})
+        chain.append({"W": [dn], "y": [yd], "in0": yg})
+        h, d = hn, yd
+    _, (lm,), _, _ = stages[-1]
+    logits = DeviceArray(VOCAB, np.float32)
+    bufs.append(logits)
+    chain.append({"W": [lm], "y": [logits.ptr], "in0": h, "in1": d, "x_out": buf(HID), "norm_w": buf(HID, 59999)})
+    ctx.synchronize()
+    return ctx.chain_create(chain, CHAIN_EPS), bufs, logits
+
+
+def time_chain(ctx, ch, steps, warmup):
+    """HIP events on the context stream around `steps` back-to-back launches"""
+    for _ in range(warmup):
+        ch.run()
+    ch.status()
+    e0, e1 = Event(), Event()
+    e0.record(ctx.stream)
+    for _ in range(steps):
+        ch.run()
+    e1.record(ctx.stream)
+    e1.synchronize()
+    ch.status()
+    return e0.elapsed_ms(e1) / steps
+
+
 def stage_bytes(stage):
     _, ws, _, _ = stage
     # algorithmic: weights + one fp32 x and y per matvec (BASELINE accounting)
@@ -173,6 +246,35 @@ def time_graph(ctx, g, steps, warmup):
 
 
 # ---------------------------------------------------------------------------
+def host_cpu():
+    """CPU model, physical cores of the host and the CPUs this process may use"""
+    model, cores = None, set()
+    try:
+        phys = core = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count()
+    return {"cpu_model": model, "host_physical_cores": len(cores) or None, "cpus_allowed": allowed}
+
+
 def cpu_baseline_decode(stages, budget_s=10.0):
     """Reference ggml CPU path (oracle/_ref) on layers 0-9 of the same step."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
@@ -243,6 +345,7 @@ def cpu_baseline_decode(stages, budget_s=10.0):
         "tok_s_equiv": round(1.0 / (med * 4268590592 / nbytes), 2),
         "parity_outside_tol": worst_bad,
     }
+    res.update(host_cpu())
     return res, None
 
 
@@ -276,6 +379,23 @@ def run_decode8b(args):
     stages_t = time_stage_kinds(ctx, stages)
     for k, v in stages_t.items():
         log(f"[bench]   {k:8s} {v['us_per_launch']:7.2f} us/launch  {v['GBps']:7.1f} GB/s")
+    # The same weights as one dependent chain in one launch (chain_kernel):
+    # each stage's input produced by the stages before it.
+    chain = None
+    if not args.no_chain:
+        ch, chain_bufs, logits = build_chain8b(ctx, stages)
+        ms_ch = time_chain(ctx, ch, args.steps, args.warmup)
+        lg = logits.to_host()
+        if not np.isfinite(lg).all() or not np.any(lg):
+            raise RuntimeError("chain step produced non-finite or all-zero logits")
+        ch.free()
+        for b in chain_bufs:
+            b.free()
+        chain = {"kernel": "chain_kernel", "launches_per_step": 1, "ms_per_step": round(ms_ch, 5),
+                 "GBps": round(step_bytes / (ms_ch * 1e-3) / 1e9, 2),
+                 "what": "the step's 145 stages as one dependent chain (norm, q/k/v, o, residual, norm, "
+                         "gate/up + SwiGLU, down, head; q stands in for the attention output)"}
+        log(f"[bench] chain step {ms_ch*1e3:.1f} us (1 launch), {chain['GBps']:.1f} GB/s")
     traffic = load_traffic("decode8b")
     cpu, why = (None, "skipped")
     if not args.no_cpu:
@@ -322,6 +442,7 @@ def run_decode8b(args):
             "bytes_per_launch": step_bytes // launches,
         },
         "stages": stages_t,
+        "chain": chain,
         "cpu_baseline": cpu,
     }
     if cpu is None:
@@ -708,6 +829,7 @@ def main():
     ap.add_argument("--T", type=int, default=1, help="tokens (--config single)")
     ap.add_argument("--qtype", type=int, default=spq4k.TYPE_Q4_K, help="ggml weight type (--config single)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-chain", action="store_true", help="decode8b: skip the one-launch chain leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested). The Q4_K path "
