@@ -256,6 +256,42 @@ int spq4k_moe(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids, int
  * 256); otherwise the banks run one after the other. */
 int spq4k_moe_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *banks, const int32_t *ids,
                     int64_t n_used, int64_t ne11, int64_t T, const float *X, float *const *Y);
+/* spq4k_dequant_matvec: the reference's scalar BurnHard matvec, beast_matvec
+ * (desktop/beast_canyon/sp_beast_canyon.c:1122-1134, used by its MoE
+ * forward, :455-562): Y[t][r] = sum_j dequant(W[r])[j] * X[t][j] with the fp32
+ * activations as given -- no Q8_K quantisation, so its outputs differ from
+ * spq4k_mul_mat's (the ggml CPU path's arithmetic) by about 0.75% normwise
+ * at N(0, 0.02) weights and N(0, 1) activations. The dequantised weights
+ * are dequantize_row_q4_K's bit for bit; each product is rounded to fp32 and
+ * the products are added in fp32 (per lane, then across the wave in a fixed
+ * order, where beast_matvec adds them serially). Dense Q4_K, any T (tokens
+ * run in groups of up to 8), K <= 32768; X [T][K] 16-byte aligned, Y [T][M],
+ * device pointers; the _host twin copies in and out. */
+int spq4k_dequant_matvec(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
+int spq4k_dequant_matvec_host(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
+/* spq4k_moe_ffn: the routed-expert FFN block of a MoE layer, the unit the
+ * reference's BURN_MOE custom op replaces (sp_build_burn_moe_op,
+ * desktop/engine/src/burn_moe_op.cpp:377-430, computing burn_moe_compute,
+ * :202-372: per token and slot, gate and up, silu(gate) * up, down, weighted
+ * sum) with the arithmetic of the stock ggml graph it stands for
+ * (forward.cpp:1098-1117):
+ *   G, U = ggml_mul_mat_id(gate / up, X, ids)          [T][n_used][n_ff]
+ *   H    = silu(G) * U                                  ggml_silu, ggml_mul
+ *   D    = ggml_mul_mat_id(down, H, ids)   (input row t * n_used + s)
+ *   Y[t] = sum_s D[t][s] * weights[t][s]   fp32 products added in double in
+ *                                          slot order (ggml_mul, ggml_sum_rows)
+ * gate and up banks [n_embd -> n_ff] x E share type and shape; down is
+ * [n_ff -> n_embd] x E of any supported type. ids [T][n_used] int32 and
+ * weights [T][n_used] fp32 (the router's top-k and its weights, the
+ * op's `selected` and `weights` sources), X [T][n_embd] (16-byte aligned),
+ * Y [T][n_embd]; device pointers. Equals spq4k_moe_multi(gate, up),
+ * spq4k_swiglu, spq4k_moe(down, ne11 = n_used) and the weighted sum run one
+ * after the other, bit for bit. The _host twin copies in and out. */
+int spq4k_moe_ffn(spq4k_ctx *ctx, const spq4k_weights *gate, const spq4k_weights *up, const spq4k_weights *down,
+                  const int32_t *ids, const float *weights, int64_t n_used, int64_t T, const float *X, float *Y);
+int spq4k_moe_ffn_host(spq4k_ctx *ctx, const spq4k_weights *gate, const spq4k_weights *up,
+                       const spq4k_weights *down, const int32_t *ids, const float *weights, int64_t n_used,
+                       int64_t T, const float *X, float *Y);
 
 /* ---- the operations either side of the matvec ---------------------------
  * spq4k_rms_norm         : ggml_mul(ggml_rms_norm(x, eps), w) over T rows of K

@@ -13,8 +13,9 @@
  * live in a plain ggml context.
  *
  * Weights are uploaded to the GPU the first time a weight tensor is seen and
- * stay resident (keyed by tensor and data pointer); activations and outputs
- * cross PCIe per call. Built against the host engine's ggml.h.
+ * stay resident (keyed by tensor, data pointer, byte count, type and shape)
+ * until spq4k_ggml_forget or spq4k_ggml_free; activations and outputs cross
+ * PCIe per node. Built against the host engine's ggml.h.
  */
 #ifndef SPQ4K_GGML_H
 #define SPQ4K_GGML_H
@@ -44,6 +45,24 @@ struct ggml_tensor *spq4k_ggml_mul_mat(struct ggml_context *ctx, struct ggml_ten
  * [n_used, T] i32 -> [M, n_used, T] f32. */
 struct ggml_tensor *spq4k_ggml_mul_mat_id(struct ggml_context *ctx, struct ggml_tensor *as, struct ggml_tensor *x,
                                           struct ggml_tensor *ids, spq4k_ggml *b);
+
+/* The routed-expert FFN block of a MoE layer as one node, in place of the
+ * reference's BURN_MOE custom op (sp_build_burn_moe_op,
+ * desktop/engine/src/burn_moe_op.cpp:377-430, same sources in the same
+ * order: cur [n_embd, T] f32, selected [k, T] i32, weights [1, k, T] f32,
+ * gate_exps / up_exps [n_embd, n_ff, E], down_exps [n_ff, n_embd, E]) with the
+ * arithmetic of the stock graph it replaces (forward.cpp:1098-1117): runs
+ * spq4k_moe_ffn on the GPU -> [n_embd, T] f32. All experts resident on the
+ * GPU (the op's CPU-side sub-bank split, pivot > 0, is not taken). Returns
+ * NULL (build the stock graph instead) for other types or shapes. */
+struct ggml_tensor *spq4k_ggml_moe_ffn(struct ggml_context *ctx, struct ggml_tensor *cur, struct ggml_tensor *selected,
+                                       struct ggml_tensor *weights, struct ggml_tensor *gate_exps,
+                                       struct ggml_tensor *up_exps, struct ggml_tensor *down_exps, spq4k_ggml *b);
+
+/* Drop the resident GPU copy of weight tensor W (every copy when W is NULL),
+ * e.g. before its ggml context is freed or its model reloaded; a later node
+ * on W uploads it again. Returns the number of copies freed. */
+int spq4k_ggml_forget(spq4k_ggml *b, const struct ggml_tensor *W);
 
 /* Custom-op callbacks return nothing: the first failure is kept here (0 when
  * every node succeeded) and the failed node's output is filled with NaN. */

@@ -1817,6 +1817,117 @@ int spq4k_moe_host(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, 
     return 0;
 }
 
+// ---- fp32-activation dequant-then-dot (beast_matvec) ----------------------------------
+int spq4k_dequant_matvec(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!W || !W->data || !X || !Y || T < 1) return set_err(c, -EINVAL, "dequant_matvec: bad arguments");
+    if (W->type != SPQ4K_TYPE_Q4_K || W->E != 1)
+        return set_err(c, -EINVAL, "dequant_matvec: a dense Q4_K matrix is required");
+    if (!aligned(X, 16) || !aligned(Y, 4)) return set_err(c, -EINVAL, "dequant_matvec: misaligned pointer");
+    const int nb = (int)(W->K / SPQ4K_QK_K);
+    if (dequant_matvec_lds_bytes(1, nb) > DQ_MATVEC_LDS_MAX)
+        return set_err(c, -EINVAL, "dequant_matvec: K = %lld exceeds %zu staged values", (long long)W->K,
+                       DQ_MATVEC_LDS_MAX / sizeof(float));
+    // tokens in groups whose x fits the staging area
+    int tg = DQ_MATVEC_MAX_T;
+    while (tg > 1 && dequant_matvec_lds_bytes(tg, nb) > DQ_MATVEC_LDS_MAX) --tg;
+    for (int64_t t0 = 0; t0 < T; t0 += tg) {
+        const int n = (int)(T - t0 < tg ? T - t0 : tg);
+        hipError_t e = launch_dequant_matvec(W->data, (int)W->M, nb, X + t0 * W->K, W->K, Y + t0 * W->M, W->M, n,
+                                             c->num_cus, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "dequant_matvec launch");
+    }
+    return 0;
+}
+
+int spq4k_dequant_matvec_host(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!W || !X || !Y || T < 1) return set_err(c, -EINVAL, "dequant_matvec_host: bad arguments");
+    const size_t nx = (size_t)T * W->K * sizeof(float), ny = (size_t)T * W->M * sizeof(float);
+    DevBuf a, b;
+    if (hipMalloc(&a.p, nx + 16) != hipSuccess || hipMalloc(&b.p, ny + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "dequant_matvec_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, X, nx, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_dequant_matvec(c, W, (const float*)a.p, (float*)b.p, T);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(Y, b.p, ny, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+// ---- routed-expert FFN block (BURN_MOE) --------------------------------------------
+int spq4k_moe_ffn(spq4k_ctx* c, const spq4k_weights* gate, const spq4k_weights* up, const spq4k_weights* down,
+                  const int32_t* ids, const float* weights, int64_t n_used, int64_t T, const float* X, float* Y) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!gate || !up || !down || !weights || !Y) return set_err(c, -EINVAL, "moe_ffn: null argument");
+    if (gate->type != up->type || gate->K != up->K || gate->M != up->M || gate->E != up->E)
+        return set_err(c, -EINVAL, "moe_ffn: gate and up banks differ in type or shape");
+    if (down->K != gate->M || down->M != gate->K || down->E != gate->E)
+        return set_err(c, -EINVAL, "moe_ffn: down bank [%lld x %lld x %lld] does not match gate [%lld x %lld x %lld]",
+                       (long long)down->K, (long long)down->M, (long long)down->E, (long long)gate->K,
+                       (long long)gate->M, (long long)gate->E);
+    rc = moe_check(c, gate, ids, n_used, 1, T, X, Y);
+    if (rc) return rc;
+    if (!aligned(weights, 4) || !aligned(Y, 4)) return set_err(c, -EINVAL, "moe_ffn: misaligned pointer");
+    const int64_t n_embd = gate->K, n_ff = gate->M, pairs = T * n_used;
+    // fusion scratch: gate and up outputs, their SwiGLU (down's input rows, 16-byte
+    // aligned for the matvec), down outputs
+    const size_t fb = (((size_t)pairs * n_ff * sizeof(float)) + 255) & ~(size_t)255;
+    const size_t db = (((size_t)pairs * n_embd * sizeof(float)) + 255) & ~(size_t)255;
+    rc = ensure_scratch2(c, 3 * fb + db);
+    if (rc) return rc;
+    float* G = reinterpret_cast<float*>(c->scratch2);
+    float* U = reinterpret_cast<float*>(c->scratch2 + fb);
+    float* H = reinterpret_cast<float*>(c->scratch2 + 2 * fb);
+    float* D = reinterpret_cast<float*>(c->scratch2 + 3 * fb);
+    // up and gate of every routed pair (forward.cpp:1100-1101), one call
+    const spq4k_weights* gu[2] = {gate, up};
+    float* gy[2] = {G, U};
+    rc = spq4k_moe_multi(c, 2, gu, ids, n_used, 1, T, X, gy);
+    if (rc) return rc;
+    // silu(gate) * up (forward.cpp:1102-1103)
+    hipError_t e = launch_swiglu(G, U, H, pairs * n_ff, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "swiglu launch");
+    // down of each pair's own hidden row (forward.cpp:1104: b = par [n_ff, n_used, T], ne11 = n_used)
+    rc = spq4k_moe(c, down, ids, n_used, n_used, T, H, D);
+    if (rc) return rc;
+    // weights and the sum over the slots (forward.cpp:1107-1116)
+    e = launch_moe_combine(D, weights, Y, (int)T, (int)n_used, (int)n_embd, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe_combine launch");
+    return 0;
+}
+
+int spq4k_moe_ffn_host(spq4k_ctx* c, const spq4k_weights* gate, const spq4k_weights* up, const spq4k_weights* down,
+                       const int32_t* ids, const float* weights, int64_t n_used, int64_t T, const float* X,
+                       float* Y) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!gate || !up || !down || !ids || !weights || !X || !Y || T < 1 || n_used < 1 || n_used > gate->E)
+        return set_err(c, -EINVAL, "moe_ffn_host: bad arguments");
+    for (int64_t i = 0; i < T * n_used; ++i)
+        if (ids[i] < 0 || ids[i] >= gate->E)
+            return set_err(c, -EINVAL, "moe_ffn_host: expert id %d out of range", ids[i]);
+    const size_t ni = (size_t)T * n_used * sizeof(int32_t);
+    const size_t nw = (size_t)T * n_used * sizeof(float);
+    const size_t nx = (size_t)T * gate->K * sizeof(float);
+    DevBuf a, w, b, d;
+    if (hipMalloc(&a.p, ni + 16) != hipSuccess || hipMalloc(&w.p, nw + 16) != hipSuccess ||
+        hipMalloc(&b.p, nx + 16) != hipSuccess || hipMalloc(&d.p, nx + 16) != hipSuccess)
+        return set_err(c, -ENOMEM, "moe_ffn_host");
+    SPQ_HIP(c, hipMemcpyAsync(a.p, ids, ni, hipMemcpyHostToDevice, c->stream));
+    SPQ_HIP(c, hipMemcpyAsync(w.p, weights, nw, hipMemcpyHostToDevice, c->stream));
+    SPQ_HIP(c, hipMemcpyAsync(b.p, X, nx, hipMemcpyHostToDevice, c->stream));
+    rc = spq4k_moe_ffn(c, gate, up, down, (const int32_t*)a.p, (const float*)w.p, n_used, T, (const float*)b.p,
+                       (float*)d.p);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(Y, d.p, nx, hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
 // ---- diagnostics / synth -------------------------------------------------------------
 int spq4k_subblock_sums(spq4k_ctx* c, const void* W, int64_t M, int64_t K, const float* x, int32_t* S) {
     int rc = use_device(c);

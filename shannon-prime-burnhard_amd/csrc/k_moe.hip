@@ -693,4 +693,35 @@ hipError_t launch_moe_ring(const MoeParams& p, const int32_t* ids, int n_pairs, 
     return hipGetLastError();
 }
 
+// The weighted sum over the routed experts that ends a MoE FFN block
+// (desktop/engine/src/forward.cpp:1107-1116): ggml_mul of the down outputs
+// [n, n_used, T] by the router weights [1, n_used, T] (one fp32 product an
+// element), then ggml_sum_rows over the slot axis, whose ggml_vec_sum_f32
+// (ggml-cpu/vec.h:1513-1519) adds the products in double in slot order and
+// rounds once. One thread per output element; a wave reads 64 consecutive
+// elements of one slot row at a time.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ D, const float* __restrict__ w,
+                                                          float* __restrict__ Y, int T, int n_used, int n) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)T * n) return;
+    const int t = (int)(idx / n);
+    const int i = (int)(idx - (int64_t)t * n);
+    const float* row = D + (int64_t)t * n_used * n + i;
+    const float* wt = w + (int64_t)t * n_used;
+    double acc = 0.0;
+    for (int s = 0; s < n_used; ++s) {
+        const float prod = row[(int64_t)s * n] * wt[s];
+        acc += (double)prod;
+    }
+    Y[idx] = (float)acc;
+}
+
+hipError_t launch_moe_combine(const float* D, const float* w, float* Y, int T, int n_used, int n, hipStream_t st) {
+    const int64_t total = (int64_t)T * n;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, D, w, Y, T,
+                       n_used, n);
+    return hipGetLastError();
+}
+
 }  // namespace spq4k

@@ -97,6 +97,9 @@ struct MoeParams {
 };
 
 hipError_t launch_moe_route(const int32_t* ids, int n_pairs, int E, const MoeRoute& r, hipStream_t st);
+// Y[t][i] = sum over s < n_used of D[t][s][i] * w[t][s]: fp32 products added
+// in double in slot order, rounded once (ggml_mul then ggml_sum_rows)
+hipError_t launch_moe_combine(const float* D, const float* w, float* Y, int T, int n_used, int n, hipStream_t st);
 
 // single-launch MoE (routing and Q8_K quantisation inside the matvec kernel)
 constexpr int MOE_FUSED_MAX_PAIRS = 2048;
@@ -248,6 +251,15 @@ hipError_t launch_vec_dot_q8_0(const uint8_t* wx, const uint8_t* a, int nb, floa
 hipError_t launch_gemv_q8_0(const Q80Params& p, int T, bool global_acts, int grid, hipStream_t st);
 hipError_t launch_moe_q8_0_sweep(const Q80Params& p, int grid, hipStream_t st);
 hipError_t launch_moe_q8_0_grouped(const Q80Params& p, int tc, int grid, hipStream_t st);
+
+// Q4_K dequant-then-dot with fp32 activations (k_dqdot.hip, beast_matvec's
+// arithmetic): Y[t * y_tstride + r] = sum_j dequant(W[r])[j] * X[t * x_tstride + j],
+// T <= DQ_MATVEC_MAX_T tokens whose x (staged in LDS) fits DQ_MATVEC_LDS_MAX
+constexpr int DQ_MATVEC_MAX_T = 8;
+constexpr size_t DQ_MATVEC_LDS_MAX = 128 * 1024;
+size_t dequant_matvec_lds_bytes(int T, int nb);
+hipError_t launch_dequant_matvec(const uint8_t* W, int M, int nb, const float* X, int64_t x_tstride, float* Y,
+                                 int64_t y_tstride, int T, int num_cus, hipStream_t st);
 
 // A chain of dependent T = 1 Q4_K matvec stages in one persistent launch
 // (k_chain.hip). Stage s: x = in0 (+ in1); xout = x when set; x = rms_norm(x)

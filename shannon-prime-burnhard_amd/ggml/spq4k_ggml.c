@@ -8,14 +8,18 @@
  *     (desktop/engine/src/forward.cpp:1248, burn_moe_op.cpp:203);
  *   - finds the weight in the resident table, uploading it on first use
  *     (spq4k_weights_upload_type with the tensor's ggml type), keyed by
- *     tensor and data pointer so that a buffer reused for other bytes is
- *     uploaded again;
+ *     tensor, data pointer, byte count, type and shape so that a buffer
+ *     reused for another tensor is uploaded again (spq4k_ggml_forget drops
+ *     entries);
  *   - reads activations and ids, and writes the output, through
  *     ggml_backend_tensor_get / _set when the tensor has a backend buffer and
  *     through tensor->data otherwise;
  *   - runs spq4k_mul_mat_host / spq4k_moe_host (GGML_OP_MUL_MAT: y[t][m] =
  *     W[m] . x[t]; GGML_OP_MUL_MAT_ID with the CPU driver's semantics,
- *     ggml-cpu.c:1521-1690).
+ *     ggml-cpu.c:1521-1690), or spq4k_moe_ffn_host for the routed-expert FFN
+ *     block node (the BURN_MOE op's unit, burn_moe_op.cpp:202-372): one copy
+ *     of the activations in and of the block's output out, where the stock
+ *     graph's three MUL_MAT_ID nodes would each cross PCIe.
  * A failure is recorded in the binding and the node's output is NaN.
  */
 #include "spq4k_ggml.h"
@@ -32,6 +36,8 @@ struct resident {
     const struct ggml_tensor *t;
     const void *data;
     size_t nbytes;
+    enum ggml_type type;
+    int64_t ne[3];
     spq4k_weights *w;
 };
 
@@ -67,6 +73,21 @@ void spq4k_ggml_free(spq4k_ggml *b) {
 
 int spq4k_ggml_status(const spq4k_ggml *b) { return b ? b->status : -EINVAL; }
 
+int spq4k_ggml_forget(spq4k_ggml *b, const struct ggml_tensor *W) {
+    if (!b) return 0;
+    int n = 0;
+    for (int i = 0; i < b->nres;) {
+        if (!W || b->res[i].t == W) {
+            spq4k_weights_free(b->res[i].w);
+            b->res[i] = b->res[--b->nres];
+            ++n;
+        } else {
+            ++i;
+        }
+    }
+    return n;
+}
+
 const char *spq4k_ggml_last_error(const spq4k_ggml *b) { return b ? b->err : "null binding"; }
 
 static void fail(spq4k_ggml *b, struct ggml_tensor *dst, int code, const char *what) {
@@ -99,12 +120,17 @@ static void *host_bytes(const struct ggml_tensor *t, int *owned) {
     return p;
 }
 
+/* the resident copy of W: found by tensor, data pointer, byte count, type
+ * and shape (a recycled context can put a tensor of another type or shape at
+ * the same addresses), else uploaded */
 static int resident_weight(spq4k_ggml *b, const struct ggml_tensor *W, int64_t M, int64_t K, int64_t E,
                            spq4k_weights **out) {
     const size_t nbytes = ggml_nbytes(W);
     for (int i = 0; i < b->nres; ++i) {
-        if (b->res[i].t == W && b->res[i].data == W->data && b->res[i].nbytes == nbytes) {
-            *out = b->res[i].w;
+        const struct resident *r = &b->res[i];
+        if (r->t == W && r->data == W->data && r->nbytes == nbytes && r->type == W->type && r->ne[0] == W->ne[0] &&
+            r->ne[1] == W->ne[1] && r->ne[2] == W->ne[2]) {
+            *out = r->w;
             return 0;
         }
     }
@@ -122,7 +148,7 @@ static int resident_weight(spq4k_ggml *b, const struct ggml_tensor *W, int64_t M
     const int rc = spq4k_weights_upload_type(b->ctx, (int)W->type, bytes, M, K, E, &w);
     if (owned) free(bytes);
     if (rc) return rc;
-    b->res[b->nres++] = (struct resident){W, W->data, nbytes, w};
+    b->res[b->nres++] = (struct resident){W, W->data, nbytes, W->type, {W->ne[0], W->ne[1], W->ne[2]}, w};
     *out = w;
     return 0;
 }
@@ -183,6 +209,37 @@ static void run_mul_mat_id(struct ggml_tensor *dst, int ith, int nth, void *user
     if (rc) fail(b, dst, rc, "spq4k_ggml_mul_mat_id");
 }
 
+static void run_moe_ffn(struct ggml_tensor *dst, int ith, int nth, void *userdata) {
+    (void)nth;
+    if (ith != 0) return;
+    spq4k_ggml *b = (spq4k_ggml *)userdata;
+    const struct ggml_tensor *cur = dst->src[0], *sel = dst->src[1], *wts = dst->src[2];
+    const struct ggml_tensor *gate = dst->src[3], *up = dst->src[4], *down = dst->src[5];
+    const int64_t n_embd = cur->ne[0], T = cur->ne[1], n_used = sel->ne[0];
+    spq4k_weights *wg, *wu, *wd;
+    int rc = resident_weight(b, gate, gate->ne[1], gate->ne[0], gate->ne[2], &wg);
+    if (!rc) rc = resident_weight(b, up, up->ne[1], up->ne[0], up->ne[2], &wu);
+    if (!rc) rc = resident_weight(b, down, down->ne[1], down->ne[0], down->ne[2], &wd);
+    if (rc) {
+        fail(b, dst, rc, "spq4k_ggml_moe_ffn: weight upload");
+        return;
+    }
+    int ox, oi, ow, oy = 0;
+    const float *X = (const float *)host_bytes(cur, &ox);
+    const int32_t *I = (const int32_t *)host_bytes(sel, &oi);
+    const float *Wt = (const float *)host_bytes(wts, &ow);
+    float *Y = dst->buffer ? (float *)malloc((size_t)n_embd * T * sizeof(float)) : (float *)dst->data;
+    if (dst->buffer) oy = 1;
+    if (X && I && Wt && Y) rc = spq4k_moe_ffn_host(b->ctx, wg, wu, wd, I, Wt, n_used, T, X, Y);
+    else rc = -ENOMEM;
+    if (rc == 0 && oy) ggml_backend_tensor_set(dst, Y, 0, (size_t)n_embd * T * sizeof(float));
+    if (ox) free((void *)X);
+    if (oi) free((void *)I);
+    if (ow) free((void *)Wt);
+    if (oy) free(Y);
+    if (rc) fail(b, dst, rc, "spq4k_ggml_moe_ffn");
+}
+
 /* weight types the library runs (spq4k.h: SPQ4K_TYPE_Q4_K, _Q5_K, _Q6_K, _Q8_0) */
 static int supported(enum ggml_type t) {
     return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K || t == GGML_TYPE_Q8_0;
@@ -207,4 +264,24 @@ struct ggml_tensor *spq4k_ggml_mul_mat_id(struct ggml_context *ctx, struct ggml_
         return NULL;
     struct ggml_tensor *args[3] = {as, x, ids};
     return ggml_custom_4d(ctx, GGML_TYPE_F32, as->ne[1], ids->ne[0], ids->ne[1], 1, args, 3, run_mul_mat_id, 1, b);
+}
+
+struct ggml_tensor *spq4k_ggml_moe_ffn(struct ggml_context *ctx, struct ggml_tensor *cur, struct ggml_tensor *selected,
+                                       struct ggml_tensor *weights, struct ggml_tensor *gate_exps,
+                                       struct ggml_tensor *up_exps, struct ggml_tensor *down_exps, spq4k_ggml *b) {
+    if (!ctx || !cur || !selected || !weights || !gate_exps || !up_exps || !down_exps || !b) return NULL;
+    const int64_t n_embd = cur->ne[0], T = cur->ne[1], k = selected->ne[0];
+    const struct ggml_tensor *banks[3] = {gate_exps, up_exps, down_exps};
+    for (int i = 0; i < 3; ++i)
+        if (!supported(banks[i]->type) || banks[i]->ne[3] != 1 || !ggml_is_contiguous(banks[i])) return NULL;
+    if (cur->type != GGML_TYPE_F32 || cur->ne[2] != 1 || cur->ne[3] != 1 || !ggml_is_contiguous(cur) ||
+        selected->type != GGML_TYPE_I32 || selected->ne[1] != T || selected->ne[2] != 1 ||
+        !ggml_is_contiguous(selected) || weights->type != GGML_TYPE_F32 || ggml_nelements(weights) != k * T ||
+        !ggml_is_contiguous(weights) || gate_exps->type != up_exps->type || gate_exps->ne[0] != n_embd ||
+        up_exps->ne[0] != n_embd || up_exps->ne[1] != gate_exps->ne[1] || up_exps->ne[2] != gate_exps->ne[2] ||
+        down_exps->ne[0] != gate_exps->ne[1] || down_exps->ne[1] != n_embd || down_exps->ne[2] != gate_exps->ne[2] ||
+        k > gate_exps->ne[2])
+        return NULL;
+    struct ggml_tensor *args[6] = {cur, selected, weights, gate_exps, up_exps, down_exps};
+    return ggml_custom_4d(ctx, GGML_TYPE_F32, n_embd, T, 1, 1, args, 6, run_moe_ffn, 1, b);
 }

@@ -99,6 +99,10 @@ def load_library(path: str | None = None):
         "spq4k_mul_mat": (I, [V, V, V, V, I64]),
         "spq4k_moe": (I, [V, V, V, I64, I64, I64, V, V]),
         "spq4k_moe_multi": (I, [V, I, PV, V, I64, I64, I64, V, PV]),
+        "spq4k_moe_ffn": (I, [V, V, V, V, V, V, I64, I64, V, V]),
+        "spq4k_dequant_matvec": (I, [V, V, V, V, I64]),
+        "spq4k_dequant_matvec_host": (I, [V, V, V, V, I64]),
+        "spq4k_moe_ffn_host": (I, [V, V, V, V, V, V, I64, I64, V, V]),
         "spq4k_mul_mat_host": (I, [V, V, V, V, I64]),
         "spq4k_moe_host": (I, [V, V, V, I64, I64, I64, V, V]),
         "spq4k_subblock_sums": (I, [V, V, I64, I64, V, V]),
@@ -554,6 +558,37 @@ class Context:
         yb = (C.c_void_p * n)(*Y_devs)
         self._check("spq4k_moe_multi", self.lib.spq4k_moe_multi(self.handle, n, hb, ids_dev, n_used, ne11, T,
                                                                X_dev, yb))
+
+    def dequant_matvec_dev(self, W: Weights, X_dev: int, Y_dev: int, T: int = 1):
+        """spq4k_dequant_matvec: beast_matvec's fp32-activation dequant-then-dot."""
+        self._check("spq4k_dequant_matvec", self.lib.spq4k_dequant_matvec(self.handle, W.handle, X_dev, Y_dev, T))
+
+    def dequant_matvec(self, W: Weights, X: np.ndarray) -> np.ndarray:
+        """spq4k_dequant_matvec_host: X [T, K] -> Y [T, M]."""
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, W.K)
+        Y = np.empty((X.shape[0], W.M), np.float32)
+        self._check("spq4k_dequant_matvec_host", self.lib.spq4k_dequant_matvec_host(
+            self.handle, W.handle, X.ctypes.data, Y.ctypes.data, X.shape[0]))
+        return Y
+
+    def moe_ffn_dev(self, gate: Weights, up: Weights, down: Weights, ids_dev: int, w_dev: int, n_used: int, T: int,
+                    X_dev: int, Y_dev: int):
+        """spq4k_moe_ffn: the routed-expert FFN block (gate/up, SwiGLU, down, weighted sum)."""
+        self._check("spq4k_moe_ffn", self.lib.spq4k_moe_ffn(self.handle, gate.handle, up.handle, down.handle, ids_dev,
+                                                           w_dev, n_used, T, X_dev, Y_dev))
+
+    def moe_ffn(self, gate: Weights, up: Weights, down: Weights, ids: np.ndarray, weights: np.ndarray,
+                X: np.ndarray) -> np.ndarray:
+        """spq4k_moe_ffn_host: ids / weights [T, n_used], X [T, n_embd] -> [T, n_embd]."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        weights = np.ascontiguousarray(weights, np.float32)
+        X = np.ascontiguousarray(X, np.float32)
+        T, n_used = ids.shape
+        Y = np.empty((T, gate.K), np.float32)
+        self._check("spq4k_moe_ffn_host", self.lib.spq4k_moe_ffn_host(
+            self.handle, gate.handle, up.handle, down.handle, ids.ctypes.data, weights.ctypes.data, n_used, T,
+            X.ctypes.data, Y.ctypes.data))
+        return Y
 
     def dequant_dev(self, vx: int, y: int, k: int):
         self._check("spq4k_dequant", self.lib.spq4k_dequant(self.handle, vx, y, k))

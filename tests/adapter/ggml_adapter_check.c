@@ -162,3 +162,97 @@ int check_mul_mat_id(int type, int64_t M, int64_t K, int64_t E, int64_t n_used, 
     return finish(ctx, b, ggml_mul_mat_id(ctx, as, x, ids), spq4k_ggml_mul_mat_id(ctx, as, x, ids, b), nthreads,
                   y_ref, y_ada, err, errlen);
 }
+
+/* The routed-expert FFN block of a MoE layer: y_ref is the stock ggml graph
+ * (desktop/engine/src/forward.cpp:1098-1117: up and gate MUL_MAT_ID, silu,
+ * mul, down MUL_MAT_ID, mul by the router weights, permute, cont, sum_rows,
+ * reshape), y_ada the adapter's single node (spq4k_ggml_moe_ffn, in place of
+ * the reference's BURN_MOE op); gate and up Q4_K [D, F, E], down of
+ * down_type [F, D, E]; ids_in / w_in [T][n_used]; cur [D, T] seeded N(0, 1). */
+int check_moe_ffn(int down_type, int64_t D, int64_t F, int64_t E, int64_t n_used, int64_t T, const int32_t *ids_in,
+                  const float *w_in, uint64_t seed, int nthreads, float *y_ref, float *y_ada, char *err, int errlen) {
+    spq4k_ggml *b;
+    int rc = spq4k_ggml_init(0, &b);
+    if (rc) {
+        snprintf(err, errlen, "spq4k_ggml_init: %d", rc);
+        return rc;
+    }
+    struct ggml_context *ctx =
+        new_ctx((size_t)3 * D * F * E * 2 + (size_t)(D + F) * n_used * T * 64 + (64 << 20));
+    float *tmp = (float *)malloc((size_t)D * F * E * sizeof(float));
+    struct ggml_tensor *gate = q_weight(ctx, GGML_TYPE_Q4_K, D, F, E, seed, tmp);
+    struct ggml_tensor *up = q_weight(ctx, GGML_TYPE_Q4_K, D, F, E, seed + 1, tmp);
+    struct ggml_tensor *down = q_weight(ctx, down_type, F, D, E, seed + 2, tmp);
+    free(tmp);
+    struct ggml_tensor *cur = f32_input(ctx, D, T, 1, seed + 3);
+    cur = ggml_reshape_2d(ctx, cur, D, T);
+    struct ggml_tensor *sel = ggml_new_tensor_2d(ctx, GGML_TYPE_I32, n_used, T);
+    memcpy(sel->data, ids_in, (size_t)n_used * T * sizeof(int32_t));
+    struct ggml_tensor *wts = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, 1, n_used, T);
+    memcpy(wts->data, w_in, (size_t)n_used * T * sizeof(float));
+    /* the stock routed-expert graph */
+    struct ggml_tensor *cur3 = ggml_reshape_3d(ctx, cur, D, 1, T);
+    struct ggml_tensor *up_e = ggml_mul_mat_id(ctx, up, cur3, sel);
+    struct ggml_tensor *gate_e = ggml_silu(ctx, ggml_mul_mat_id(ctx, gate, cur3, sel));
+    struct ggml_tensor *par = ggml_mul(ctx, gate_e, up_e);
+    struct ggml_tensor *down_e = ggml_mul_mat_id(ctx, down, par, sel);
+    struct ggml_tensor *weighted = ggml_mul(ctx, down_e, wts);
+    struct ggml_tensor *kfirst = ggml_cont(ctx, ggml_permute(ctx, weighted, 1, 0, 2, 3));
+    struct ggml_tensor *yr = ggml_reshape_2d(ctx, ggml_sum_rows(ctx, kfirst), D, T);
+    struct ggml_tensor *ya = spq4k_ggml_moe_ffn(ctx, cur, sel, wts, gate, up, down, b);
+    return finish(ctx, b, yr, ya, nthreads, y_ref, y_ada, err, errlen);
+}
+
+/* The resident-weight table: a node on a weight keeps one GPU copy across
+ * graphs; a tensor whose type or shape changed at the same addresses is
+ * uploaded again; spq4k_ggml_forget drops copies. Returns 0 when every step
+ * behaves, else the failing step's number. */
+int check_resident(char *err, int errlen) {
+    spq4k_ggml *b;
+    int rc = spq4k_ggml_init(0, &b);
+    if (rc) {
+        snprintf(err, errlen, "spq4k_ggml_init: %d", rc);
+        return rc;
+    }
+    struct ggml_context *ctx = new_ctx((size_t)64 << 20);
+    const int64_t K = 512, M = 64;
+    float *tmp = (float *)malloc((size_t)M * K * sizeof(float));
+    struct ggml_tensor *W = q_weight(ctx, GGML_TYPE_Q4_K, K, M, 1, 5, tmp);
+    struct ggml_tensor *x = f32_input(ctx, K, 1, 1, 6);
+    int step = 0;
+    for (int it = 0; it < 2 && !step; ++it) {
+        struct ggml_tensor *y = spq4k_ggml_mul_mat(ctx, W, x, b);
+        struct ggml_cgraph *gf = ggml_new_graph(ctx);
+        ggml_build_forward_expand(gf, y);
+        if (ggml_graph_compute_with_ctx(ctx, gf, 1) != GGML_STATUS_SUCCESS || spq4k_ggml_status(b)) step = 1 + it;
+    }
+    /* same tensor, same data pointer, same byte count, another shape: K = 256, M = 128 */
+    if (!step) {
+        W->ne[0] = K / 2;
+        W->ne[1] = 2 * M;
+        W->nb[1] = 144;
+        W->nb[2] = W->nb[3] = W->nb[1] * (size_t)(2 * M);
+        normal_fill(tmp, M * K, 9, 0.02f);
+        ggml_quantize_chunk(GGML_TYPE_Q4_K, tmp, W->data, 0, 2 * M, K / 2, NULL);
+        struct ggml_tensor *x2 = f32_input(ctx, K / 2, 1, 1, 7);
+        struct ggml_tensor *y = spq4k_ggml_mul_mat(ctx, W, x2, b);
+        struct ggml_tensor *yr = ggml_mul_mat(ctx, W, x2);
+        struct ggml_cgraph *gf = ggml_new_graph(ctx);
+        ggml_build_forward_expand(gf, y);
+        ggml_build_forward_expand(gf, yr);
+        if (!y || ggml_graph_compute_with_ctx(ctx, gf, 1) != GGML_STATUS_SUCCESS || spq4k_ggml_status(b)) {
+            step = 3;
+        } else {
+            const float *a = (const float *)y->data, *r = (const float *)yr->data;
+            for (int64_t i = 0; i < 2 * M && !step; ++i)
+                if (!(fabsf(a[i] - r[i]) <= 1e-5f || fabsf(a[i] - r[i]) <= 1e-4f * fabsf(r[i]))) step = 4;
+        }
+    }
+    if (!step && spq4k_ggml_forget(b, W) != 2) step = 5;   /* the copies of both shapes */
+    if (!step && spq4k_ggml_forget(b, NULL) != 0) step = 6;
+    free(tmp);
+    if (step) snprintf(err, errlen, "resident-table step %d failed: %s", step, spq4k_ggml_last_error(b));
+    spq4k_ggml_free(b);
+    ggml_free(ctx);
+    return step;
+}

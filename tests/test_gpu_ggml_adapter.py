@@ -96,3 +96,44 @@ def test_adapter_mul_mat_id(drv, qtype, T, ne11):
     yr, ya = _run(drv.check_mul_mat_id, M * k * T, qtype, M, K, E, k, ne11 if ne11 != 4 else k, T,
                   ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), 21 + T)
     _check(yr, ya, f"mul_mat_id type={qtype} T={T} ne11={ne11}")
+
+
+@pytest.mark.parametrize("down_type", [TYPE_Q4_K, TYPE_Q6_K])
+@pytest.mark.parametrize("T", [1, 4, 32])
+def test_adapter_moe_ffn(drv, down_type, T):
+    """The routed-expert FFN block node (spq4k_ggml_moe_ffn, the BURN_MOE op's
+    unit) against ggml's stock routed-expert graph (forward.cpp:1098-1117) at
+    the 30B-A3B-like expert shapes (top-8, gate/up 2048 -> 768, down 768 ->
+    2048; 32 experts, so the CPU encodes the banks quickly): normwise, for the
+    reason given for the feed-forward block; the block's stages are compared
+    element-wise at 128 experts in tests/test_gpu_moe_ffn.py."""
+    E, D, F, k = 32, 2048, 768, 8
+    rng = np.random.default_rng(40 + T)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    ids = np.ascontiguousarray(np.argsort(-logits, axis=1, kind="stable")[:, :k].astype(np.int32))
+    top = np.take_along_axis(logits, ids, axis=1).astype(np.float64)
+    w = np.exp(top - top.max(axis=1, keepdims=True))
+    w = np.ascontiguousarray((w / w.sum(axis=1, keepdims=True)).astype(np.float32))
+    yr = np.full(D * T, np.nan, np.float32)
+    ya = np.full(D * T, np.nan, np.float32)
+    err = ctypes.create_string_buffer(256)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    drv.check_moe_ffn.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                  ctypes.c_int64, ctypes.POINTER(ctypes.c_int32), f32p, ctypes.c_uint64, ctypes.c_int,
+                                  f32p, f32p, ctypes.c_char_p, ctypes.c_int]
+    rc = drv.check_moe_ffn(down_type, D, F, E, k, T, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                           w.ctypes.data_as(f32p), 50 + T, 8, yr.ctypes.data_as(f32p), ya.ctypes.data_as(f32p), err,
+                           256)
+    assert rc == 0, err.value.decode()
+    assert np.isfinite(yr).all() and np.isfinite(ya).all()
+    rel = float(np.linalg.norm(ya.astype(np.float64) - yr) / np.linalg.norm(yr.astype(np.float64)))
+    assert rel <= FF_NORMWISE, f"moe ffn block down={down_type} T={T}: normwise {rel:.3e} > {FF_NORMWISE}"
+
+
+def test_adapter_resident_table(drv):
+    """a weight re-used at the same addresses with another shape is uploaded
+    again (the key holds type and shape); spq4k_ggml_forget drops copies"""
+    err = ctypes.create_string_buffer(256)
+    drv.check_resident.argtypes = [ctypes.c_char_p, ctypes.c_int]
+    rc = drv.check_resident(err, 256)
+    assert rc == 0, err.value.decode()
