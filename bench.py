@@ -462,9 +462,12 @@ def run_single(args, M, K, T, dist, outlier, name, qtype=spq4k.TYPE_Q4_K):
     y = DeviceArray(T * M)
     ctx.synchronize()
     n = max(args.steps, copies)
+    # spq4k_mul_mat (Q8_K activations, ggml's CPU arithmetic), or with
+    # --op dequant_matvec spq4k_dequant_matvec (fp32 activations, beast_matvec's)
+    call = ctx.dequant_matvec_dev if getattr(args, "op", "mul_mat") == "dequant_matvec" else ctx.mul_mat_dev
     with Graph.capture(ctx.stream) as g:
         for i in range(n):
-            ctx.mul_mat_dev(ws[i % copies], x.ptr, y.ptr, T)
+            call(ws[i % copies], x.ptr, y.ptr, T)
     ms = time_graph(ctx, g, 1, max(1, args.warmup // 10)) / n
     alg = nb + 4 * K * T + 4 * M * T
     gbs = alg / (ms * 1e-3) / 1e9
@@ -472,7 +475,7 @@ def run_single(args, M, K, T, dist, outlier, name, qtype=spq4k.TYPE_Q4_K):
     # resident in the 256 MB Infinity Cache when they fit
     with Graph.capture(ctx.stream) as gh:
         for i in range(n):
-            ctx.mul_mat_dev(ws[0], x.ptr, y.ptr, T)
+            call(ws[0], x.ptr, y.ptr, T)
     ms_hot = time_graph(ctx, gh, 1, 1) / n
     print(json.dumps({"metric": f"{name} effective HBM GB/s", "value": round(gbs, 2), "unit": "GB/s",
                       "us_per_call": round(ms * 1e3, 3), "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2),
@@ -480,7 +483,8 @@ def run_single(args, M, K, T, dist, outlier, name, qtype=spq4k.TYPE_Q4_K):
                       "hot_cache": {"us_per_call": round(ms_hot * 1e3, 3),
                                     "GBps": round(alg / (ms_hot * 1e-3) / 1e9, 1),
                                     "note": "same weights every call (Infinity Cache resident when under 256 MB)"},
-                      "config": {"workload": name, "M": M, "K": K, "T": T, "weight_copies": copies}}), flush=True)
+                      "config": {"workload": name, "M": M, "K": K, "T": T, "weight_copies": copies,
+                                 "op": getattr(args, "op", "mul_mat")}}), flush=True)
     for w in ws:
         w.free()
     syn.tmp.free()
@@ -577,16 +581,47 @@ def run_moe(args):
         wbytes = uniq * sum(q4k_bytes(M, K) for (_, M, K) in shapes)
         abytes = wbytes + 4 * T * (2 * 2048 + 2 * k * 768) + 4 * T * k * (768 + 2048)
         gbs = abytes / (ms * 1e-3) / 1e9
+        # the whole routed-expert FFN block per layer (spq4k_moe_ffn: gate/up,
+        # SwiGLU, down on the pairs' own hidden rows, weighted sum), cold
+        wts = [DeviceArray.from_host(np.full((T, k), 1.0 / k, np.float32)) for _ in range(NL)]
+        Yb = DeviceArray(T * 2048)
+        (wg, _, _), (wu, _, _), (wd, _, _) = layers[0]
+        ctx.moe_ffn_dev(wg, wu, wd, idd[0].ptr, wts[0].ptr, k, T, xg.ptr, Yb.ptr)   # sizes the scratch
+        ctx.synchronize()
+        with Graph.capture(ctx.stream) as gb:
+            for L in range(NL):
+                (wg, _, _), (wu, _, _), (wd, _, _) = layers[L]
+                ctx.moe_ffn_dev(wg, wu, wd, idd[L].ptr, wts[L].ptr, k, T, xg.ptr, Yb.ptr)
+        ms_blk = time_graph(ctx, gb, max(5, args.steps // 5), 2) / NL
+        # the adapter's path for one block node: host activations, ids and
+        # weights copied in, the output copied out, synchronised (wall clock)
+        xh = np.random.default_rng(T).standard_normal((T, 2048)).astype(np.float32)
+        wh = np.full((T, k), 1.0 / k, np.float32)
+        (wg, _, _), (wu, _, _), (wd, _, _) = layers[0]
+        ctx.moe_ffn(wg, wu, wd, ids_l[0], wh, xh)
+        host_t = []
+        for _ in range(20):
+            t0 = time.perf_counter()
+            ctx.moe_ffn(wg, wu, wd, ids_l[0], wh, xh)
+            host_t.append(time.perf_counter() - t0)
+        blk_bytes = abytes + 4 * T * 2048
         print(json.dumps({"metric": f"Q4_K MoE expert matvec (gate+up+down), T={T}", "value": round(gbs, 1),
                           "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
                           "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2), "unique_experts": uniq,
                           "hot_cache": {"us_per_layer": round(ms_hot * 1e3, 2),
                                         "note": "one layer's banks and routing every time (Infinity Cache resident)"},
+                          "ffn_block": {"us_per_layer": round(ms_blk * 1e3, 2),
+                                        "GBps": round(blk_bytes / (ms_blk * 1e-3) / 1e9, 1),
+                                        "what": "spq4k_moe_ffn: gate/up, SwiGLU, down, router-weighted sum (cold)",
+                                        "host_path_us": round(float(np.median(host_t)) * 1e6, 1),
+                                        "host_path_what": "spq4k_moe_ffn_host, the ggml node's path: copies in, "
+                                                          "block, copy out, synchronise (wall clock, median of 20, "
+                                                          "layer 0 hot)"},
                           "config": {"workload": "30B-A3B-like MoE layer, 128 experts, top-8, 8 layers of banks (cold)",
                                      "T": T}}), flush=True)
-        for a in idd:
+        for a in idd + wts:
             a.free()
-        xg.free(); xd.free(); Y.free(); Y2.free()
+        xg.free(); xd.free(); Y.free(); Y2.free(); Yb.free()
     ctx.close()
 
 
@@ -830,6 +865,8 @@ def main():
     ap.add_argument("--qtype", type=int, default=spq4k.TYPE_Q4_K, help="ggml weight type (--config single)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-chain", action="store_true", help="decode8b: skip the one-launch chain leg")
+    ap.add_argument("--op", default="mul_mat", choices=["mul_mat", "dequant_matvec"],
+                    help="--config single: the entry point timed (dequant_matvec: Q4_K, fp32 activations)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested). The Q4_K path "

@@ -231,8 +231,10 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
 //   K = 12288              : 16 waves, x-first: 48 KB of x per CU would
 //                            otherwise queue behind the CU's weight loads
 //   K = 27648              : 8 waves (the registers of 7 Q8_K blocks a lane), x-first
-DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb, int64_t rows) {
+DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb_rows, int64_t rows) {
     DecodeCfg d{};
+    // register limits follow the row length the kernel instance is compiled for
+    const int nb = decode_bucket(fmt, nb_rows) > 0 ? decode_bucket(fmt, nb_rows) : nb_rows;
     if (nb > 48) {
         d.waves = 8; d.depth = 1; d.xfirst = true;
     } else if (nb >= 48) {

@@ -128,14 +128,20 @@ __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)
 // g takes rows g, g + G, ... of both (the two rows in flight are gate r and
 // up r) and stores silu(gate r . x) * (up r . x) to segment 0's output
 // (ggml_silu + ggml_mul, forward.cpp:1703-1706).
-template <typename Fmt, int NB, int WAVES, int D, bool XFW, bool NORM, bool GLU>
+// RT: the row length is p.nb, any value up to NB (NB a multiple of 16, the
+// registers and LDS sized for NB); otherwise exactly NB blocks, known at
+// compile time.
+template <typename Fmt, int NB, int WAVES, int D, bool XFW, bool NORM, bool GLU, bool RT>
 __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     static_assert(!GLU || D == 2, "the fused gate/up pair is the two rows in flight");
+    static_assert(!RT || NB % 16 == 0, "a runtime row length is bounded by whole 16-block passes");
     using W = typename Fmt::W;
     constexpr int NIT = (NB + 15) / 16;           // blocks per lane per row
-    constexpr int QW = (NB + 3) / 4;              // quantising waves
-    constexpr int PASSES = (QW + WAVES - 1) / WAVES;
-    constexpr size_t ROWB = (size_t)NB * Fmt::BYTES;
+    constexpr int QWMAX = (NB + 3) / 4;           // quantising waves at most
+    constexpr int PASSES = (QWMAX + WAVES - 1) / WAVES;
+    const int nb = RT ? p.nb : NB;                // blocks per row
+    const int QW = (nb + 3) / 4;                  // quantising waves
+    const size_t ROWB = (size_t)nb * Fmt::BYTES;
     __shared__ __align__(16) char q8s[q8lds_bytes(NB)];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -183,7 +189,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int bb = bsub + 16 * it;
-            b[it] = Fmt::load(wr + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
+            b[it] = Fmt::load(wr + (size_t)(bb < nb ? bb : nb - 1) * Fmt::BYTES, l4);
         }
     };
     // GLU: row r of gate (which = 0) or up (which = 1)
@@ -194,7 +200,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int bb = bsub + 16 * it;
-            b[it] = Fmt::load(wr + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
+            b[it] = Fmt::load(wr + (size_t)(bb < nb ? bb : nb - 1) * Fmt::BYTES, l4);
         }
     };
 
@@ -207,8 +213,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     for (int ps = 0; ps < PASSES; ++ps) {
         const int qw = ps * WAVES + wave;
         const int item = qw * 4 + (lane >> 4);
-        xv[ps] = qw < QW && item < NB;
-        xb[ps] = item < NB ? item : NB - 1;
+        xv[ps] = qw < QW && item < nb;
+        xb[ps] = item < nb ? item : nb - 1;
         if (qw < QW) xr[ps] = load_x16(p.X, 0, 0, xb[ps]);
         if (NORM && qw < QW) nw[NORM ? ps : 0] = load_x16(p.norm_w, 0, 0, xb[ps]);
     }
@@ -228,7 +234,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
         double S = 0.0;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) S += ssq[w];
-        const float mean = (float)(S / (double)(NB * QK));
+        const float mean = (float)(S / (double)(nb * QK));
         const float scale = 1.0f / sqrtf(mean + p.eps);
 #pragma unroll
         for (int ps = 0; ps < PASSES; ++ps)
@@ -261,7 +267,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int bb = bsub + 16 * it;
-        Fmt::load_reg(L, bb < NB ? bb : NB - 1, l4, qr[it]);
+        Fmt::load_reg(L, bb < nb ? bb : nb - 1, l4, qr[it]);
     }
     if (GLU) {
         for (int i = 0; i < nrows; ++i) {
@@ -272,7 +278,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
 #pragma unroll
                 for (int it = 0; it < NIT; ++it) {
                     const float a = Fmt::dot_reg(buf[u * (D - 1)][it], l4, qr[it], acc);
-                    acc = (bsub + 16 * it < NB) ? a : acc;
+                    acc = (bsub + 16 * it < nb) ? a : acc;
                 }
                 a2[u] = group_sum_last<64>(acc);
             }
@@ -293,7 +299,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
 #pragma unroll
                 for (int it = 0; it < NIT; ++it) {
                     const float a = Fmt::dot_reg(buf[u][it], l4, qr[it], acc);
-                    acc = (bsub + 16 * it < NB) ? a : acc;
+                    acc = (bsub + 16 * it < nb) ? a : acc;
                 }
                 acc = group_sum_last<64>(acc);
                 if (lane == 63) {
@@ -404,10 +410,10 @@ static hipError_t launch_t(const GemvParams& p, int bpr, int ntiles, hipStream_t
 
 int gemv_rows_per_tile(int bpr) { return 4 * (64 / (4 * bpr)); }
 
-template <typename Fmt, int NB, int WAVES, int D, bool XFW, bool NORM = false, bool GLU = false>
+template <typename Fmt, int NB, bool RT, int WAVES, int D, bool XFW, bool NORM = false, bool GLU = false>
 static hipError_t launch_dec(const GemvParams& p, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_decode_kernel<Fmt, NB, WAVES, D, XFW, NORM, GLU>), dim3(grid), dim3(WAVES * 64), 0, st,
-                       p);
+    hipLaunchKernelGGL((gemv_decode_kernel<Fmt, NB, WAVES, D, XFW, NORM, GLU, RT>), dim3(grid), dim3(WAVES * 64), 0,
+                       st, p);
     return hipGetLastError();
 }
 
@@ -419,14 +425,16 @@ constexpr bool dec_shape_ok(int nb, int waves, int depth) {
 }
 // Q6_K holds 15 + 21 registers a block, Q5_K 20 + 19 (Q4_K 12 + 19): at
 // K = 12288 a 16-wave workgroup (128 registers) or two rows in flight at 12
-// waves would spill
+// waves would spill, and at K = 8192 two rows in flight at 16 waves
 template <typename Fmt>
 constexpr bool dec_shape_ok_fmt(int nb, int waves, int depth) {
     if (Fmt::BYTES != Q4K_BYTES && nb >= 48 && (waves == 16 || (waves == 12 && depth == 2))) return false;
+    // and from 32 blocks a 16-wave workgroup holds one row in flight
+    if (Fmt::BYTES != Q4K_BYTES && nb >= 32 && waves == 16 && depth == 2) return false;
     return dec_shape_ok(nb, waves, depth);
 }
 
-template <typename Fmt, int NB>
+template <typename Fmt, int NB, bool RT = false>
 static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
     if (c.glu || c.norm) {
         // the fused forms run x first; the gate/up pair is the two rows in flight
@@ -434,9 +442,9 @@ static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStre
 #define SPQ_DECF(W, DD)                                                                             \
         if constexpr (dec_shape_ok_fmt<Fmt>(NB, W, DD))                                             \
             if (c.waves == W && c.depth == DD) {                                                     \
-                if (c.glu && c.norm) return launch_dec<Fmt, NB, W, DD, true, true, DD == 2>(p, c.grid, st); \
-                if (c.glu) return launch_dec<Fmt, NB, W, DD, true, false, DD == 2>(p, c.grid, st);  \
-                return launch_dec<Fmt, NB, W, DD, true, true, false>(p, c.grid, st);                \
+                if (c.glu && c.norm) return launch_dec<Fmt, NB, RT, W, DD, true, true, DD == 2>(p, c.grid, st); \
+                if (c.glu) return launch_dec<Fmt, NB, RT, W, DD, true, false, DD == 2>(p, c.grid, st);  \
+                return launch_dec<Fmt, NB, RT, W, DD, true, true, false>(p, c.grid, st);                \
             }
         SPQ_DECF(16, 1) SPQ_DECF(16, 2) SPQ_DECF(12, 1) SPQ_DECF(12, 2) SPQ_DECF(8, 1) SPQ_DECF(8, 2)
 #undef SPQ_DECF
@@ -444,7 +452,7 @@ static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStre
     }
 #define SPQ_DEC(W, DD, X)                                                                  \
     if constexpr (dec_shape_ok_fmt<Fmt>(NB, W, DD))                                        \
-        if (c.waves == W && c.depth == DD && c.xfirst == X) return launch_dec<Fmt, NB, W, DD, X>(p, c.grid, st);
+        if (c.waves == W && c.depth == DD && c.xfirst == X) return launch_dec<Fmt, NB, RT, W, DD, X>(p, c.grid, st);
     SPQ_DEC(16, 1, false) SPQ_DEC(16, 1, true) SPQ_DEC(16, 2, false) SPQ_DEC(16, 2, true)
     SPQ_DEC(12, 1, false) SPQ_DEC(12, 1, true) SPQ_DEC(12, 2, false) SPQ_DEC(12, 2, true)
     SPQ_DEC(8, 1, false) SPQ_DEC(8, 1, true) SPQ_DEC(8, 2, false) SPQ_DEC(8, 2, true)
@@ -466,37 +474,73 @@ static bool dec_fused_ok(int nb, const DecodeCfg& c) {
 
 bool decode_fused_supported(int fmt, int nb, const DecodeCfg& c) {
     if (!decode_supported(fmt, nb)) return false;
-    if (fmt == WF_Q6K) return dec_fused_ok<FmtQ6K>(nb, c);
-    if (fmt == WF_Q5K) return dec_fused_ok<FmtQ5K>(nb, c);
-    if (fmt == WF_Q4K) return dec_fused_ok<FmtQ4K>(nb, c);
+    const int nbk = decode_bucket(fmt, nb);
+    if (fmt == WF_Q6K) return dec_fused_ok<FmtQ6K>(nbk, c);
+    if (fmt == WF_Q5K) return dec_fused_ok<FmtQ5K>(nbk, c);
+    if (fmt == WF_Q4K) return dec_fused_ok<FmtQ4K>(nbk, c);
     return false;
 }
 
-// Q4_K: K = 4096, 5120, 12288, 27648, the dense shapes of the 8B model and of
-// the large-K configuration. Q6_K (15 weight and 21 activation registers a
-// block a lane): K = 4096 and 12288; at K = 27648 its seven blocks a lane
-// would not fit the register file, and the generic kernel runs.
-bool decode_supported(int fmt, int nb) {
+// Q4_K: K = 4096, 5120, 12288 and 27648 (the dense shapes of the 8B model and
+// of the large-K configuration) compiled for their exact length; any other
+// K up to 28672 runs the instance of the next multiple of 16 blocks with the
+// length read at run time (decode_bucket). Q6_K / Q5_K (15 + 21 and 20 + 19
+// registers a block a lane): K = 4096 and 12288 exactly, and K up to 8192 in
+// the runtime-length instances of 16 and 32 blocks; longer rows would not
+// fit the register file, and the generic kernel runs.
+static bool decode_exact(int fmt, int nb) {
     if (fmt == WF_Q6K || fmt == WF_Q5K) return nb == 16 || nb == 48;
     return nb == 16 || nb == 20 || nb == 48 || nb == 108;
+}
+
+int decode_bucket(int fmt, int nb) {
+    if (nb <= 0 || decode_exact(fmt, nb)) return nb;
+    const int b = (nb + 15) / 16 * 16;
+    if (fmt == WF_Q6K || fmt == WF_Q5K) return b <= 32 ? b : 0;
+    return b <= DEC_MAX_NB ? b : 0;
+}
+
+bool decode_supported(int fmt, int nb) {
+    if (fmt != WF_Q4K && fmt != WF_Q6K && fmt != WF_Q5K) return false;
+    return decode_bucket(fmt, nb) > 0;
+}
+
+template <typename Fmt, int FMT>
+static hipError_t launch_dec_bucket(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
+    switch (decode_bucket(FMT, p.nb)) {
+        case 16: return launch_dec_nb<Fmt, 16, true>(p, c, st);
+        case 32: return launch_dec_nb<Fmt, 32, true>(p, c, st);
+        default: break;
+    }
+    if constexpr (FMT == WF_Q4K) {
+        switch (decode_bucket(WF_Q4K, p.nb)) {
+            case 48: return launch_dec_nb<Fmt, 48, true>(p, c, st);
+            case 64: return launch_dec_nb<Fmt, 64, true>(p, c, st);
+            case 80: return launch_dec_nb<Fmt, 80, true>(p, c, st);
+            case 96: return launch_dec_nb<Fmt, 96, true>(p, c, st);
+            case 112: return launch_dec_nb<Fmt, 112, true>(p, c, st);
+            default: break;
+        }
+    }
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
     if (p.fmt == WF_Q6K) {
         if (p.nb == 16) return launch_dec_nb<FmtQ6K, 16>(p, c, st);
         if (p.nb == 48) return launch_dec_nb<FmtQ6K, 48>(p, c, st);
-        return hipErrorInvalidValue;
+        return launch_dec_bucket<FmtQ6K, WF_Q6K>(p, c, st);
     }
     if (p.fmt == WF_Q5K) {
         if (p.nb == 16) return launch_dec_nb<FmtQ5K, 16>(p, c, st);
         if (p.nb == 48) return launch_dec_nb<FmtQ5K, 48>(p, c, st);
-        return hipErrorInvalidValue;
+        return launch_dec_bucket<FmtQ5K, WF_Q5K>(p, c, st);
     }
     if (p.nb == 16) return launch_dec_nb<FmtQ4K, 16>(p, c, st);
     if (p.nb == 20) return launch_dec_nb<FmtQ4K, 20>(p, c, st);
     if (p.nb == 48) return launch_dec_nb<FmtQ4K, 48>(p, c, st);
     if (p.nb == 108) return launch_dec_nb<FmtQ4K, 108>(p, c, st);
-    return hipErrorInvalidValue;
+    return launch_dec_bucket<FmtQ4K, WF_Q4K>(p, c, st);
 }
 
 template <typename Fmt>

@@ -57,6 +57,11 @@ struct DecodeCfg {
 int gemv_rows_per_tile(int bpr);
 hipError_t launch_gemv(const GemvParams& p, int T, int bpr, int ntiles, hipStream_t st);
 bool decode_supported(int fmt, int nb);
+// the row length (in blocks) the decode kernel instance for nb is compiled for:
+// nb itself for the exact instances, else the next multiple of 16 (the
+// runtime-length instances, up to DEC_MAX_NB for Q4_K, 32 for Q6_K / Q5_K); 0 if none
+constexpr int DEC_MAX_NB = 112;
+int decode_bucket(int fmt, int nb);
 hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st);
 // whether the decode kernel has the fused form c (norm / glu) for this format and row length
 bool decode_fused_supported(int fmt, int nb, const DecodeCfg& c);

@@ -2,7 +2,10 @@
 shape the planner can pick, against the CPU oracle.
 
 The decode kernel serves K = 4096, 5120, 12288 and 27648 (the 8B and large-K
-shapes); the generic kernel serves every other K at T = 1, and T = 2, 3. Launch shapes are forced through the
+shapes) from instances compiled for that row length, and every other K up to
+28672 (Q6_K and Q5_K: up to 8192) from instances that read the row length at
+run time, one per multiple of 16 blocks; the generic kernel serves longer
+rows at T = 1, and T = 2, 3. Launch shapes are forced through the
 context's environment overrides (read when a context is created), so each
 (waves, depth, x-first) instantiation and each lanes-per-row choice of the
 generic kernel is checked, not only the ones the planner picks for the sizes
@@ -69,7 +72,8 @@ def test_decode_launch_shapes(oracle, waves, depth, xfirst):
     several rows (the depth pipeline and its ragged tail) and a full grid
     (K = 27648 runs 8 waves and one row in flight whatever is asked)."""
     rng = np.random.default_rng(1000 + waves * 10 + depth * 2 + xfirst)
-    cases = [(1000, 4096), (333, 12288), (210, 5120), (77, 27648)]
+    cases = [(1000, 4096), (333, 12288), (210, 5120), (77, 27648), (130, 2048), (90, 8192), (61, 14336),
+             (40, 20480), (33, 24576), (29, 28416)]
     data = [(M, K, _weights(oracle, rng, M, K), rng.standard_normal((1, K)).astype(np.float32)) for M, K in cases]
     for grid in (3, 0):
         env = {"SPQ4K_DEC_WAVES": waves, "SPQ4K_DEC_DEPTH": depth, "SPQ4K_DEC_XFIRST": xfirst}
@@ -130,3 +134,37 @@ def test_decode_repeatable(ctx, oracle):
     a = ctx.mul_mat(Wd, x)
     for _ in range(3):
         np.testing.assert_array_equal(ctx.mul_mat(Wd, x), a)
+
+
+@pytest.mark.parametrize("K", [256, 512, 2048, 3072, 4352, 6144, 8192, 11264, 14336, 16384, 18432, 20480, 24576,
+                               28672])
+def test_decode_any_k(ctx, oracle, K):
+    """Row lengths without an exact instance: the runtime-length instance of
+    the next multiple of 16 blocks (a partial last pass of 16 blocks where K
+    is not a multiple of 4096), against the oracle and the generic kernel."""
+    rng = np.random.default_rng(K)
+    M = 2048 if K <= 8192 else 384
+    W = _weights(oracle, rng, M, K)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    a = ctx.mul_mat(ctx.upload(W, M, K), x)
+    exp = oracle.mul_mat(W, M, K, x)
+    _check(a, exp, f"decode any-K M={M} K={K}", oracle.mul_mat_dq_f64(12, W, M, K, x))
+    g = _context_with({"SPQ4K_GEMV_GENERIC": 1})
+    try:
+        b = g.mul_mat(g.upload(W, M, K), x)
+    finally:
+        g.close()
+    _check(a, b, f"decode vs generic K={K}")
+
+
+@pytest.mark.parametrize("qtype", [13, 14])
+@pytest.mark.parametrize("K", [512, 2048, 5120, 8192])
+def test_decode_any_k_q5k_q6k(ctx, oracle, qtype, K):
+    """Q5_K / Q6_K rows of up to 32 blocks in the runtime-length instances"""
+    rng = np.random.default_rng(K + qtype)
+    M = 1024
+    W = oracle.quantize(qtype, (rng.standard_normal((M, K)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    got = ctx.mul_mat(ctx.upload(W, M, K, type=qtype), x)
+    _check(got, oracle.mul_mat_type(qtype, W, M, K, x), f"decode type={qtype} K={K}",
+           oracle.mul_mat_dq_f64(qtype, W, M, K, x))

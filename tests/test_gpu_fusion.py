@@ -140,3 +140,42 @@ def test_fusion_errors(ctx, oracle):
         ctx.mul_mat_rms_norm_dev([a], x.ptr, None, EPS, [y.ptr], 1)
     with pytest.raises(Spq4kError):   # eps < 0
         ctx.rms_norm_dev(x.ptr, x.ptr, -1.0, y.ptr, 64, 1)
+
+
+@pytest.mark.parametrize("K", [2048, 3072, 8192, 14336])
+def test_fused_any_k(ctx, oracle, K):
+    """The fused decode forms at row lengths served by the runtime-length
+    decode instances (norm prologue; SwiGLU epilogue where two rows in flight
+    fit the register file, the unfused steps beyond): bit for bit against the
+    unfused steps, and the parity bar against the oracle."""
+    from spq4k.hip import DeviceArray
+    rng = np.random.default_rng(K)
+    shapes = (512, 128, 128)
+    Ws = [_enc(oracle, TYPE_Q4_K, M, K, rng) for M in shapes]
+    X, w = _inputs(rng, 1, K)
+    wd = [ctx.upload(W, M, K) for W, M in zip(Ws, shapes)]
+    xd, nd = DeviceArray.from_host(X), DeviceArray.from_host(w)
+    yd = [DeviceArray((1, M)) for M in shapes]
+    ctx.mul_mat_rms_norm_dev(wd, xd.ptr, nd.ptr, EPS, [y.ptr for y in yd], 1)
+    xn = DeviceArray((1, K))
+    ctx.rms_norm_dev(xd.ptr, nd.ptr, EPS, xn.ptr, K, 1)
+    y2 = [DeviceArray((1, M)) for M in shapes]
+    ctx.gemv_multi_dev(wd, xn.ptr, [y.ptr for y in y2], 1)
+    ctx.synchronize()
+    xb = oracle.rms_norm(X, w, EPS)
+    for W, M, a, b in zip(Ws, shapes, yd, y2):
+        np.testing.assert_array_equal(a.to_host().view(np.uint32), b.to_host().view(np.uint32))
+        _check(a.to_host(), _mm(oracle, TYPE_Q4_K, W, M, K, xb), f"norm K={K} M={M}")
+    # gate / up with the SwiGLU epilogue
+    M = 640
+    Wg, Wu = _enc(oracle, TYPE_Q4_K, M, K, rng), _enc(oracle, TYPE_Q4_K, M, K, rng)
+    gd, ud = ctx.upload(Wg, M, K), ctx.upload(Wu, M, K)
+    yg = DeviceArray((1, M))
+    ctx.mul_mat_swiglu_dev(gd, ud, xd.ptr, nd.ptr, EPS, yg.ptr, 1)
+    g2, u2 = DeviceArray((1, M)), DeviceArray((1, M))
+    ctx.gemv_multi_dev([gd, ud], xn.ptr, [g2.ptr, u2.ptr], 1)
+    ctx.synchronize()
+    g, u = g2.to_host(), u2.to_host()
+    _check(g, _mm(oracle, TYPE_Q4_K, Wg, M, K, xb), f"gate K={K}")
+    _check(u, _mm(oracle, TYPE_Q4_K, Wu, M, K, xb), f"up K={K}")
+    np.testing.assert_allclose(yg.to_host(), oracle.swiglu(g, u), rtol=4e-7, atol=1e-30, err_msg=f"swiglu K={K}")
