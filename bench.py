@@ -28,7 +28,7 @@ host's last-level cache), timed on this host with 16 and with 4 threads;
 its outputs are checked against the GPU's on identical inputs.
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
-                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|q5k|q8_0|single|gguf|fusion|copy]
+                  [--config decode8b|gemv4096|largek|prefill|moe|q6k|q5k|q8_0|single|gguf|fusion|copy|floor]
                   [--M M --K K --T T --qtype TYPE]   (--config single)
 
 --config q6k / q5k / q8_0 measure the Q6_K / Q5_K / Q8_0 tensors a Q4_K model
@@ -829,6 +829,52 @@ def run_fusion(args):
     ctx.close()
 
 
+def run_floor(args):
+    """The streaming floor of the 8B decode sweep: the same 145 dependent
+    launches as decode8b, each a kernel that only reads its stage's bytes
+    (spq4k_stream_read: 16-byte loads, four in flight a lane, no compute, no
+    activations), over distinct buffers of the stage sizes (4.257 GB in all),
+    replayed as one HIP graph; and 145 launches that read nothing (the launch
+    floor). A per-op drop-in of the sweep cannot run faster than this."""
+    ctx = spq4k.Context(0)
+    sizes = {"qkv": q4k_bytes(HID, HID) + 2 * q4k_bytes(KV, HID), "o": q4k_bytes(HID, HID),
+             "gate_up": 2 * q4k_bytes(FFN, HID), "down": q4k_bytes(HID, FFN), "lm_head": q4k_bytes(VOCAB, HID)}
+    order = [k for _ in range(LAYERS) for k in ("qkv", "o", "gate_up", "down")] + ["lm_head"]
+    bufs = [(k, DeviceArray(sizes[k], np.uint8)) for k in order]
+    total = sum(sizes[k] for k in order)
+    with Graph.capture(ctx.stream) as g:
+        for _, b in bufs:
+            ctx.stream_read_dev(b.ptr, sizes_of(b))
+    ms = time_graph(ctx, g, args.steps, args.warmup)
+    with Graph.capture(ctx.stream) as ge:
+        for _, b in bufs:
+            ctx.stream_read_dev(b.ptr, 0)
+    ms_empty = time_graph(ctx, ge, args.steps, args.warmup)
+    per = {}
+    for kind in ("o", "qkv", "down", "gate_up", "lm_head"):
+        sel = [b for k, b in bufs if k == kind]
+        with Graph.capture(ctx.stream) as gk:
+            for b in sel:
+                ctx.stream_read_dev(b.ptr, sizes_of(b))
+        mk = time_graph(ctx, gk, max(5, args.steps // 5), 2) / len(sel)
+        per[kind] = {"MB": round(sizes[kind] / 1e6, 2), "us_per_launch": round(mk * 1e3, 3),
+                     "GBps": round(sizes[kind] / (mk * 1e-3) / 1e9, 1)}
+    out = {"metric": "streaming floor of the 8B decode sweep (145 dependent read-only launches)",
+           "value": round(total / (ms * 1e-3) / 1e9, 1), "unit": "GB/s", "us_per_step": round(ms * 1e3, 1),
+           "pct_of_peak_hbm": round(total / (ms * 1e-3) / PEAK_HBM * 100, 2),
+           "empty_launch_us": round(ms_empty * 1e3 / len(bufs), 3), "per_launch": per,
+           "config": {"workload": "stream reads of the decode8b stage sizes, distinct buffers", "bytes": total,
+                      "launches": len(bufs)}}
+    print(json.dumps(out), flush=True)
+    for _, b in bufs:
+        b.free()
+    ctx.close()
+
+
+def sizes_of(b):
+    return b.nbytes
+
+
 def run_copy(args):
     """A plain device-to-device copy of 1 GiB (the runtime's blit kernel): the
     known-size reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE."""
@@ -858,7 +904,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "q8_0",
-                                                          "single", "gguf", "fusion", "copy"])
+                                                          "single", "gguf", "fusion", "copy", "floor"])
     ap.add_argument("--M", type=int, default=4096, help="rows (--config single)")
     ap.add_argument("--K", type=int, default=4096, help="inputs (--config single)")
     ap.add_argument("--T", type=int, default=1, help="tokens (--config single)")
@@ -894,6 +940,8 @@ def main():
         tag = {spq4k.TYPE_Q4_K: "Q4_K", spq4k.TYPE_Q5_K: "Q5_K", spq4k.TYPE_Q6_K: "Q6_K", spq4k.TYPE_Q8_0: "Q8_0"}
         run_single(args, args.M, args.K, args.T, spq4k.DIST_NORMAL, 1.0,
                    f"{tag[args.qtype]} {args.M}x{args.K} T={args.T}", args.qtype)
+    elif args.config == "floor":
+        run_floor(args)
     elif args.config == "copy":
         run_copy(args)
     elif args.config == "largek":

@@ -390,6 +390,14 @@ int spq4k_subblock_sums(spq4k_ctx *ctx, const void *W, int64_t M, int64_t K, con
  * ggml_vec_dot_q8_0_q8_0 (ggml-cpu/quants.c:400-428). */
 int spq4k_subblock_sums_type(spq4k_ctx *ctx, int type, const void *W, int64_t M, int64_t K, const float *x,
                              int32_t *S);
+/* A read of `bytes` of device memory at p (16-byte aligned, a multiple of
+ * 16 bytes; 0 launches a kernel that reads nothing) by one launch on the
+ * context stream: each wave reads 4 KB of consecutive bytes per step as four
+ * coalesced 16-byte-a-lane loads, four workgroups a CU (SPQ4K_STREAM_GRID
+ * sets another largest grid), no other work -- the HBM floor of a launch of
+ * the same bytes. No reference counterpart; for measurement (bench.py
+ * --config floor). */
+int spq4k_stream_read(spq4k_ctx *ctx, const void *p, size_t bytes);
 
 #ifdef __cplusplus
 }

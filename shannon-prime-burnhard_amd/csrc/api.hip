@@ -1931,6 +1931,23 @@ int spq4k_moe_ffn_host(spq4k_ctx* c, const spq4k_weights* gate, const spq4k_weig
 }
 
 // ---- diagnostics / synth -------------------------------------------------------------
+int spq4k_stream_read(spq4k_ctx* c, const void* p, size_t bytes) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if ((bytes && !p) || !aligned(p, 16) || bytes % 16) return set_err(c, -EINVAL, "stream_read: bad arguments");
+    // four workgroups a CU unless SPQ4K_STREAM_GRID sets the largest grid
+    int max_grid = 4 * c->num_cus;
+    if (const char* g = getenv("SPQ4K_STREAM_GRID")) {
+        const int v = atoi(g);
+        if (v > 0 && v <= (1 << 16)) max_grid = v;
+    }
+    rc = ensure_scratch(c, (size_t)max_grid * sizeof(uint32_t));
+    if (rc) return rc;
+    hipError_t e = launch_stream_read(p, bytes, max_grid, reinterpret_cast<uint32_t*>(c->scratch), c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "stream_read launch");
+    return 0;
+}
+
 int spq4k_subblock_sums(spq4k_ctx* c, const void* W, int64_t M, int64_t K, const float* x, int32_t* S) {
     int rc = use_device(c);
     if (rc) return rc;

@@ -604,4 +604,35 @@ hipError_t launch_vec_dot_q8(const uint8_t* wx, const uint8_t* q8, int nb, float
     return hipGetLastError();
 }
 
+// The streaming floor: every wave reads 4 KB of consecutive bytes per step
+// as four fully coalesced 1 KB loads (16 bytes a lane, four in flight) and
+// folds them into a value that is stored only if it matches a constant no
+// data makes likely (so the loads are not dead code and nothing is written).
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, int64_t n16,
+                                                          uint32_t* __restrict__ sink) {
+    uint32_t acc = 0;
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t step = (int64_t)gridDim.x * 4 * 256;   // uint4 per step of the grid
+    int64_t i = wave * 256 + lane;
+    for (; i + 192 < n16; i += step) {
+        const uint4 a = p[i], b = p[i + 64], c = p[i + 128], d = p[i + 192];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+    }
+    for (int k = 0; k < 4; ++k, i += 64)
+        if (i < n16) {
+            const uint4 a = p[i];
+            acc ^= a.x ^ a.y ^ a.z ^ a.w;
+        }
+    if (acc == 0x5EEDF00Du && threadIdx.x == 0) sink[blockIdx.x] = acc;
+}
+
+hipError_t launch_stream_read(const void* p, size_t bytes, int max_grid, uint32_t* sink, hipStream_t st) {
+    const int64_t n16 = (int64_t)(bytes / 16);
+    int64_t grid = (n16 + 4 * 256 - 1) / (4 * 256);
+    grid = grid < 1 ? 1 : (grid > max_grid ? max_grid : grid);
+    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)grid), dim3(256), 0, st, (const uint4*)p, n16, sink);
+    return hipGetLastError();
+}
+
 }  // namespace spq4k

@@ -198,6 +198,9 @@ hipError_t launch_quantize_q4k(const float* x, uint8_t* y, int64_t nblocks, hipS
 hipError_t launch_synth(float* out, int64_t n, uint64_t seed, int dist, int64_t cols, float mean, float std,
                         float outlier_mult, int64_t offset, hipStream_t st);
 hipError_t launch_vec_dot_q8(const uint8_t* wx, const uint8_t* q8, int nb, float* out, hipStream_t st);
+// one streaming read of `bytes` (a multiple of 16) at p by at most max_grid
+// workgroups; sink: max_grid words of scratch
+hipError_t launch_stream_read(const void* p, size_t bytes, int max_grid, uint32_t* sink, hipStream_t st);
 
 // Q6_K conversions (k_q6k.hip); the Q6_K matvecs are the FmtQ6K instances of
 // launch_gemv / launch_gemv_decode / launch_moe_* (fmt = WF_Q6K)

@@ -101,6 +101,7 @@ def load_library(path: str | None = None):
         "spq4k_moe_multi": (I, [V, I, PV, V, I64, I64, I64, V, PV]),
         "spq4k_moe_ffn": (I, [V, V, V, V, V, V, I64, I64, V, V]),
         "spq4k_dequant_matvec": (I, [V, V, V, V, I64]),
+        "spq4k_stream_read": (I, [V, V, S]),
         "spq4k_dequant_matvec_host": (I, [V, V, V, V, I64]),
         "spq4k_moe_ffn_host": (I, [V, V, V, V, V, V, I64, I64, V, V]),
         "spq4k_mul_mat_host": (I, [V, V, V, V, I64]),
@@ -558,6 +559,10 @@ class Context:
         yb = (C.c_void_p * n)(*Y_devs)
         self._check("spq4k_moe_multi", self.lib.spq4k_moe_multi(self.handle, n, hb, ids_dev, n_used, ne11, T,
                                                                X_dev, yb))
+
+    def stream_read_dev(self, p: int, nbytes: int):
+        """spq4k_stream_read: one launch that only reads nbytes at p (the streaming floor)."""
+        self._check("spq4k_stream_read", self.lib.spq4k_stream_read(self.handle, p, nbytes))
 
     def dequant_matvec_dev(self, W: Weights, X_dev: int, Y_dev: int, T: int = 1):
         """spq4k_dequant_matvec: beast_matvec's fp32-activation dequant-then-dot."""
