@@ -1532,16 +1532,20 @@ int moe_check(spq4k_ctx* c, const spq4k_weights* bank, const int32_t* ids, int64
 // rows (of both banks) in one sweep and one launch. An expert chosen twice
 // is streamed twice, so only for small batches (T <= moe_dec_max_t).
 // Returns 1 when it does not apply.
+// glu (nbank 2, banks of equal M: gate then up): Y[0] = silu(gate . x) * (up . x)
+// in the same launch, the SwiGLU epilogue of the pair
 int moe_decode_try(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, const int32_t* ids,
-                   int64_t n_used, int64_t ne11, int64_t T, const float* X, float* const* Y) {
+                   int64_t n_used, int64_t ne11, int64_t T, const float* X, float* const* Y, bool glu = false) {
     const spq4k_weights* bank = banks[0];
     const int E = (int)bank->E, nb = (int)(bank->K / SPQ4K_QK_K), M = (int)bank->M;
     const int M1 = nbank > 1 ? (int)banks[1]->M : 0;
+    if (glu && (nbank != 2 || M1 != M)) return 1;
+    const int64_t MV = glu ? M : (int64_t)M + M1;   // sweep rows a pair
     const size_t bb = type_block_bytes(bank->type);
     const int64_t rows = T * ne11, n_pairs = T * n_used;
     if (!(T <= c->moe_dec_max_t && n_pairs <= MOE_DEC_MAX_PAIRS && rows <= MOE_DEC_MAX_XROWS && moe_decode_supported(nb) &&
           !c->moe_unfused && c->moe_mode == 0 && (size_t)q8lds_bytes((int)rows * nb) <= (size_t)LDS_BUDGET &&
-          n_pairs * (M + M1) <= INT32_MAX))
+          n_pairs * MV <= INT32_MAX))
         return 1;
     MoeFusedParams f;
     memset(&f, 0, sizeof f);
@@ -1562,11 +1566,12 @@ int moe_decode_try(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, c
     if (nbank > 1) {
         f.bank1 = banks[1]->data;
         f.expert_bytes1 = (size_t)M1 * nb * bb;
-        f.Y1 = Y[1];
-        f.M1 = M1;
+        f.Y1 = glu ? nullptr : Y[1];
+        f.M1 = glu ? 0 : M1;
+        f.glu = glu ? 1 : 0;
     }
     const int64_t per_wg = moe_decode_rows_per_wg(nb);
-    const int64_t need = (n_pairs * (M + M1) + per_wg - 1) / per_wg;
+    const int64_t need = (n_pairs * MV + per_wg - 1) / per_wg;
     const int grid = (int)(need < 2 * c->num_cus ? need : 2 * c->num_cus);
     moe_decode_plan(f, grid, &f.rows_per_wg, &f.xwin_rows);
     hipError_t e = launch_moe_decode(f, grid, c->stream);
@@ -1885,14 +1890,21 @@ int spq4k_moe_ffn(spq4k_ctx* c, const spq4k_weights* gate, const spq4k_weights* 
     float* U = reinterpret_cast<float*>(c->scratch2 + fb);
     float* H = reinterpret_cast<float*>(c->scratch2 + 2 * fb);
     float* D = reinterpret_cast<float*>(c->scratch2 + 3 * fb);
-    // up and gate of every routed pair (forward.cpp:1100-1101), one call
+    // up and gate of every routed pair (forward.cpp:1100-1101) and silu(gate)
+    // * up (:1102-1103): small batches of K-quant banks in one sweep with the
+    // SwiGLU epilogue, otherwise one spq4k_moe_multi call and swiglu_kernel
     const spq4k_weights* gu[2] = {gate, up};
-    float* gy[2] = {G, U};
-    rc = spq4k_moe_multi(c, 2, gu, ids, n_used, 1, T, X, gy);
-    if (rc) return rc;
-    // silu(gate) * up (forward.cpp:1102-1103)
-    hipError_t e = launch_swiglu(G, U, H, pairs * n_ff, c->stream);
-    if (e != hipSuccess) return hip_fail(c, e, "swiglu launch");
+    float* hy[1] = {H};
+    hipError_t e;
+    rc = gate->fmt == WF_Q80 ? 1 : moe_decode_try(c, gu, 2, ids, n_used, 1, T, X, hy, true);
+    if (rc < 0) return rc;
+    if (rc > 0) {
+        float* gy[2] = {G, U};
+        rc = spq4k_moe_multi(c, 2, gu, ids, n_used, 1, T, X, gy);
+        if (rc) return rc;
+        e = launch_swiglu(G, U, H, pairs * n_ff, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "swiglu launch");
+    }
     // down of each pair's own hidden row (forward.cpp:1104: b = par [n_ff, n_used, T], ne11 = n_used)
     rc = spq4k_moe(c, down, ids, n_used, n_used, T, H, D);
     if (rc) return rc;

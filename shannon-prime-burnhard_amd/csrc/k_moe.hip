@@ -288,7 +288,14 @@ __global__ __launch_bounds__(WAVES * 64) void moe_fused_kernel(MoeFusedParams p)
 // bank (p.M1 > 0: the up projection beside the gate, the same ids and input)
 // pair p owns rows [p (M + M1), (p + 1)(M + M1)): M rows of the first bank,
 // then M1 of the second, so both go in one launch and one quantisation.
-template <typename Fmt, int NB, int BSL, int WAVES>
+// silu(x) = x / (1 + e^-x) (ggml_silu_f32, ggml-cpu/vec.h:1064-1066), as the
+// dense kernels' SwiGLU epilogue and swiglu_kernel compute it
+__device__ __forceinline__ float moe_silu(float x) { return x / (1.0f + expf(-x)); }
+
+// GLU: the gate / up pair of a MoE layer (bank, bank1 of equal M): sweep row
+// (pair, r) streams gate row r and up row r of the pair's expert and stores
+// silu(gate . x) * (up . x) (ggml_silu then ggml_mul, forward.cpp:1102-1103).
+template <typename Fmt, int NB, int BSL, int WAVES, bool GLU>
 __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p) {
     using W = typename Fmt::W;
     extern __shared__ __align__(16) char smem[];
@@ -302,7 +309,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     const int bsub = (lane & (LPR - 1)) >> 2;
     // a pair's sweep rows: the M rows of the bank, then the M1 rows of the
     // second bank when there is one (same expert, same input row)
-    const int M = p.M, MV = p.M + p.M1;
+    const int M = p.M, MV = GLU ? p.M : p.M + p.M1;
     const int total = p.n_pairs * MV;
     // this workgroup's rows of the sweep: one contiguous run (one or two
     // pairs), so it quantises only the input rows those pairs read
@@ -323,6 +330,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     // its input window slot
     struct Loc {
         const uint8_t* w;
+        const uint8_t* w1;   // GLU: the up row beside the gate row
         float* y;
         int e, xs;
     };
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
         const int rc = r < r1 ? r : r1 - 1;
         const int pr = rc / MV;
         const int v = rc - pr * MV;
-        const bool second = v >= M;
+        const bool second = !GLU && v >= M;
         const int lr = second ? v - M : v;
         const int e = p.ids[pr];
         l.e = (r < r1 && e >= 0 && e < p.E) ? e : -1;
@@ -339,14 +347,22 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
         const size_t eo = (size_t)(l.e >= 0 ? l.e : 0);
         l.w = (second ? p.bank1 + eo * p.expert_bytes1 : p.bank + eo * p.expert_bytes) +
               (size_t)lr * ((size_t)NB * Fmt::BYTES);
+        l.w1 = GLU ? p.bank1 + eo * p.expert_bytes1 + (size_t)lr * ((size_t)NB * Fmt::BYTES) : l.w;
         l.y = second ? p.Y1 + (int64_t)pr * p.M1 + lr : p.Y + (int64_t)pr * M + lr;
         return l;
     };
-    auto load = [&](const Loc& l, W (&w)[NIT]) {
+    auto load = [&](const Loc& l, W (&w)[NIT], W (&w1)[GLU ? NIT : 1]) {
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int bb = bsub + BSL * it;
             w[it] = Fmt::load(l.w + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
+        }
+        if constexpr (GLU) {
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int bb = bsub + BSL * it;
+                w1[it] = Fmt::load(l.w1 + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
+            }
         }
     };
     // order of the loads (they complete in order): the expert id of the first
@@ -357,7 +373,8 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     Loc cur = locate(g0);
     const XRegs xa = load_x16(p.X, p.K, xlo + ci_a / NB, ci_a % NB);
     W w[NIT];
-    load(cur, w);
+    W w1[GLU ? NIT : 1];
+    load(cur, w, w1);
     store_q8_item(xa, item_a < nitems, ci_a, L);
     for (int base = 4 * WAVES; base < nitems; base += 4 * WAVES) {
         const int item0 = base + item_a;
@@ -374,11 +391,20 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
             const int bb = bsub + BSL * it;
             Fmt::template dot<1>(w[it], l4, L, cur.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && cur.e >= 0, acc);
         }
-        const float sum = group_sum_last<LPR>(acc[0]);
+        float sum = group_sum_last<LPR>(acc[0]);
+        if constexpr (GLU) {
+            float acc1[1] = {0.0f};
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int bb = bsub + BSL * it;
+                Fmt::template dot<1>(w1[it], l4, L, cur.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && cur.e >= 0, acc1);
+            }
+            sum = moe_silu(sum) * group_sum_last<LPR>(acc1[0]);
+        }
         if (cur.e >= 0 && (lane & (LPR - 1)) == LPR - 1) *cur.y = sum;
         if (r + RPG < r1) {
             cur = locate(r + RPG);
-            load(cur, w);
+            load(cur, w, w1);
         }
     }
 }
@@ -387,7 +413,10 @@ template <typename Fmt, int NB, int BSL>
 static hipError_t launch_mdec(const MoeFusedParams& p, int grid, hipStream_t st) {
     constexpr int WAVES = 8;
     const size_t lds = (size_t)q8lds_bytes(p.xwin_rows * NB);
-    hipLaunchKernelGGL((moe_decode_kernel<Fmt, NB, BSL, WAVES>), dim3(grid), dim3(WAVES * 64), lds, st, p);
+    if (p.glu)
+        hipLaunchKernelGGL((moe_decode_kernel<Fmt, NB, BSL, WAVES, true>), dim3(grid), dim3(WAVES * 64), lds, st, p);
+    else
+        hipLaunchKernelGGL((moe_decode_kernel<Fmt, NB, BSL, WAVES, false>), dim3(grid), dim3(WAVES * 64), lds, st, p);
     return hipGetLastError();
 }
 
@@ -399,7 +428,7 @@ int moe_decode_rows_per_wg(int nb) { return nb == 3 ? 32 : (nb == 8 ? 16 : 8); }
 // rows per workgroup (a whole number of passes) and the input rows the
 // largest run of that many sweep rows can read
 void moe_decode_plan(const MoeFusedParams& p, int grid, int32_t* rows_per_wg, int32_t* xwin_rows) {
-    const int64_t MV = (int64_t)p.M + p.M1;
+    const int64_t MV = p.glu ? (int64_t)p.M : (int64_t)p.M + p.M1;
     const int64_t total = (int64_t)p.n_pairs * MV;
     const int64_t pass = moe_decode_rows_per_wg(p.nb);
     int64_t rw = (total + grid - 1) / grid;

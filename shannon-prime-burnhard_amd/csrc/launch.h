@@ -128,6 +128,9 @@ struct MoeFusedParams {
     size_t expert_bytes1;
     float* Y1;               // [T][n_used][M1]
     int32_t M1;
+    // moe_decode_kernel only: bank1 is the up bank beside the gate bank (same
+    // M); Y[pair][r] = silu(gate row r . x) * (up row r . x), Y1 unused
+    int32_t glu;
 };
 hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st);
 
