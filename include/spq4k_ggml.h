@@ -15,7 +15,11 @@
  * Weights are uploaded to the GPU the first time a weight tensor is seen and
  * stay resident (keyed by tensor, data pointer, byte count, type and shape)
  * until spq4k_ggml_forget or spq4k_ggml_free; activations and outputs cross
- * PCIe per node. Built against the host engine's ggml.h.
+ * PCIe per node. Tensors that live in a device (non-host) backend buffer --
+ * a HIP build of ggml on the same GPU -- are used in place instead: the
+ * weight is adopted without a copy and a node whose activations, ids and
+ * output are all device-resident moves nothing over PCIe. Built against the
+ * host engine's ggml.h.
  */
 #ifndef SPQ4K_GGML_H
 #define SPQ4K_GGML_H
@@ -63,6 +67,11 @@ struct ggml_tensor *spq4k_ggml_moe_ffn(struct ggml_context *ctx, struct ggml_ten
  * e.g. before its ggml context is freed or its model reloaded; a later node
  * on W uploads it again. Returns the number of copies freed. */
 int spq4k_ggml_forget(spq4k_ggml *b, const struct ggml_tensor *W);
+
+/* The device address of the binding's resident copy of W (NULL when W has
+ * none yet). For a W that lives in a device buffer it is W->data itself: the
+ * binding adopted it in place. */
+const void *spq4k_ggml_resident_data(const spq4k_ggml *b, const struct ggml_tensor *W);
 
 /* Custom-op callbacks return nothing: the first failure is kept here (0 when
  * every node succeeded) and the failed node's output is filled with NaN. */

@@ -11,7 +11,12 @@
  *     tensor, data pointer, byte count, type and shape so that a buffer
  *     reused for another tensor is uploaded again (spq4k_ggml_forget drops
  *     entries);
- *   - reads activations and ids, and writes the output, through
+ *   - when every tensor of the node lives in a device (non-host) backend
+ *     buffer -- a HIP build of ggml on this GPU -- runs on those device
+ *     pointers in place: the weight is wrapped (spq4k_weights_wrap_type, no
+ *     copy) and the activations and output never cross PCIe; the call
+ *     synchronises before returning, as the next node may read the output;
+ *   - otherwise reads activations and ids, and writes the output, through
  *     ggml_backend_tensor_get / _set when the tensor has a backend buffer and
  *     through tensor->data otherwise;
  *   - runs spq4k_mul_mat_host / spq4k_moe_host (GGML_OP_MUL_MAT: y[t][m] =
@@ -90,6 +95,13 @@ int spq4k_ggml_forget(spq4k_ggml *b, const struct ggml_tensor *W) {
 
 const char *spq4k_ggml_last_error(const spq4k_ggml *b) { return b ? b->err : "null binding"; }
 
+const void *spq4k_ggml_resident_data(const spq4k_ggml *b, const struct ggml_tensor *W) {
+    if (!b || !W) return NULL;
+    for (int i = 0; i < b->nres; ++i)
+        if (b->res[i].t == W && b->res[i].data == W->data) return spq4k_weights_data(b->res[i].w);
+    return NULL;
+}
+
 static void fail(spq4k_ggml *b, struct ggml_tensor *dst, int code, const char *what) {
     if (b->status == 0) {
         b->status = code;
@@ -104,6 +116,13 @@ static void fail(spq4k_ggml *b, struct ggml_tensor *dst, int code, const char *w
     else
         memcpy(dst->data, nan, n * sizeof(float));
     free(nan);
+}
+
+/* whether t lives in a device (non-host) backend buffer -- on a HIP build of
+ * ggml, device memory of this GPU that spq4k can use in place */
+static int on_device(const struct ggml_tensor *t) {
+    const struct ggml_tensor *s = t->view_src ? t->view_src : t;
+    return s->buffer && !ggml_backend_buffer_is_host(s->buffer);
 }
 
 /* tensor bytes in host memory: the tensor's own when it has no backend
@@ -141,12 +160,18 @@ static int resident_weight(spq4k_ggml *b, const struct ggml_tensor *W, int64_t M
         b->res = r;
         b->cap = cap;
     }
-    int owned;
-    void *bytes = host_bytes(W, &owned);
-    if (!bytes) return -ENOMEM;
     spq4k_weights *w = NULL;
-    const int rc = spq4k_weights_upload_type(b->ctx, (int)W->type, bytes, M, K, E, &w);
-    if (owned) free(bytes);
+    int rc;
+    if (on_device(W)) {
+        /* already in device memory: adopt it in place, no copy */
+        rc = spq4k_weights_wrap_type(b->ctx, (int)W->type, W->data, M, K, E, &w);
+    } else {
+        int owned;
+        void *bytes = host_bytes(W, &owned);
+        if (!bytes) return -ENOMEM;
+        rc = spq4k_weights_upload_type(b->ctx, (int)W->type, bytes, M, K, E, &w);
+        if (owned) free(bytes);
+    }
     if (rc) return rc;
     b->res[b->nres++] = (struct resident){W, W->data, nbytes, W->type, {W->ne[0], W->ne[1], W->ne[2]}, w};
     *out = w;
@@ -163,6 +188,13 @@ static void run_mul_mat(struct ggml_tensor *dst, int ith, int nth, void *userdat
     int rc = resident_weight(b, W, M, K, 1, &w);
     if (rc) {
         fail(b, dst, rc, "spq4k_ggml_mul_mat: weight upload");
+        return;
+    }
+    if (on_device(x) && on_device(dst)) {
+        /* device-resident node: the activations and the output stay on the GPU */
+        rc = spq4k_mul_mat(b->ctx, w, (const float *)x->data, (float *)dst->data, T);
+        if (!rc) rc = spq4k_synchronize(b->ctx);
+        if (rc) fail(b, dst, rc, "spq4k_ggml_mul_mat");
         return;
     }
     int ox, oy = 0;
@@ -195,6 +227,13 @@ static void run_mul_mat_id(struct ggml_tensor *dst, int ith, int nth, void *user
         fail(b, dst, rc, "spq4k_ggml_mul_mat_id: weight upload");
         return;
     }
+    if (on_device(x) && on_device(ids) && on_device(dst)) {
+        rc = spq4k_moe(b->ctx, w, (const int32_t *)ids->data, n_used, ne11, T, (const float *)x->data,
+                       (float *)dst->data);
+        if (!rc) rc = spq4k_synchronize(b->ctx);
+        if (rc) fail(b, dst, rc, "spq4k_ggml_mul_mat_id");
+        return;
+    }
     int ox, oi, oy = 0;
     const float *X = (const float *)host_bytes(x, &ox);
     const int32_t *I = (const int32_t *)host_bytes(ids, &oi);
@@ -222,6 +261,13 @@ static void run_moe_ffn(struct ggml_tensor *dst, int ith, int nth, void *userdat
     if (!rc) rc = resident_weight(b, down, down->ne[1], down->ne[0], down->ne[2], &wd);
     if (rc) {
         fail(b, dst, rc, "spq4k_ggml_moe_ffn: weight upload");
+        return;
+    }
+    if (on_device(cur) && on_device(sel) && on_device(wts) && on_device(dst)) {
+        rc = spq4k_moe_ffn(b->ctx, wg, wu, wd, (const int32_t *)sel->data, (const float *)wts->data, n_used, T,
+                           (const float *)cur->data, (float *)dst->data);
+        if (!rc) rc = spq4k_synchronize(b->ctx);
+        if (rc) fail(b, dst, rc, "spq4k_ggml_moe_ffn");
         return;
     }
     int ox, oi, ow, oy = 0;

@@ -14,6 +14,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <hip/hip_runtime_api.h>
+
+#include "ggml-alloc.h"
+#include "ggml-backend-impl.h"   /* the reference's buffer interface: a device buffer type for the tests */
 #include "ggml-cpu.h"
 #include "ggml.h"
 #include "spq4k_ggml.h"
@@ -254,5 +258,140 @@ int check_resident(char *err, int errlen) {
     if (step) snprintf(err, errlen, "resident-table step %d failed: %s", step, spq4k_ggml_last_error(b));
     spq4k_ggml_free(b);
     ggml_free(ctx);
+    return step;
+}
+
+/* ---- device-resident graphs -------------------------------------------------
+ * A minimal ggml buffer type in GPU memory (hipMalloc, is_host false), the
+ * stand-in for a HIP build of ggml's device buffers: tensors allocated in it
+ * have device addresses in tensor->data, as on the engine's GPU backend. */
+static void dv_free(ggml_backend_buffer_t buf) { (void)hipFree(buf->context); }
+static void *dv_base(ggml_backend_buffer_t buf) { return buf->context; }
+static void dv_memset(ggml_backend_buffer_t buf, struct ggml_tensor *t, uint8_t v, size_t off, size_t size) {
+    (void)buf;
+    (void)hipMemset((char *)t->data + off, v, size);
+}
+static void dv_set(ggml_backend_buffer_t buf, struct ggml_tensor *t, const void *d, size_t off, size_t size) {
+    (void)buf;
+    (void)hipMemcpy((char *)t->data + off, d, size, hipMemcpyHostToDevice);
+}
+static void dv_get(ggml_backend_buffer_t buf, const struct ggml_tensor *t, void *d, size_t off, size_t size) {
+    (void)buf;
+    (void)hipMemcpy(d, (const char *)t->data + off, size, hipMemcpyDeviceToHost);
+}
+static void dv_clear(ggml_backend_buffer_t buf, uint8_t v) { (void)hipMemset(buf->context, v, buf->size); }
+static const struct ggml_backend_buffer_i dv_iface = {
+    .free_buffer = dv_free, .get_base = dv_base, .memset_tensor = dv_memset, .set_tensor = dv_set,
+    .get_tensor = dv_get, .clear = dv_clear,
+};
+static const char *dvt_name(ggml_backend_buffer_type_t t) {
+    (void)t;
+    return "spq4k-test-device";
+}
+static ggml_backend_buffer_t dvt_alloc(ggml_backend_buffer_type_t t, size_t size) {
+    void *p = NULL;
+    if (hipMalloc(&p, size ? size : 256) != hipSuccess) return NULL;
+    return ggml_backend_buffer_init(t, dv_iface, p, size);
+}
+static size_t dvt_align(ggml_backend_buffer_type_t t) {
+    (void)t;
+    return 256;
+}
+static bool dvt_is_host(ggml_backend_buffer_type_t t) {
+    (void)t;
+    return false;
+}
+static struct ggml_backend_buffer_type dv_buft = {
+    .iface = {.get_name = dvt_name, .alloc_buffer = dvt_alloc, .get_alignment = dvt_align, .is_host = dvt_is_host},
+};
+
+static int compute_graph(struct ggml_tensor *out, int nthreads) {
+    struct ggml_init_params ip = {(size_t)16 << 20, NULL, false};
+    struct ggml_context *gctx = ggml_init(ip);
+    struct ggml_cgraph *gf = ggml_new_graph(gctx);
+    ggml_build_forward_expand(gf, out);
+    struct ggml_cplan plan = ggml_graph_plan(gf, nthreads, NULL);
+    void *work = plan.work_size ? malloc(plan.work_size) : NULL;
+    plan.work_data = work;
+    const int rc = ggml_graph_compute(gf, &plan) == GGML_STATUS_SUCCESS ? 0 : -1;
+    free(work);
+    ggml_free(gctx);
+    return rc;
+}
+
+/* The same node on host tensors (ggml's own MUL_MAT / the stock routed-expert
+ * graph, y_ref) and on device-resident tensors through the adapter (y_ada).
+ * mode 0: y [M, T] = W [K, M] x x [K, T] of ggml type `type`; mode 1: the
+ * routed-expert FFN block (gate / up Q4_K [K, M, E], down of `type`
+ * [M, K, E], n_used of E experts, ids_in / w_in [T][n_used]). Returns 0, or
+ * the step that failed; *wrapped is set when the binding adopted the device
+ * weight in place (its resident copy is W->data). */
+int check_device(int mode, int type, int64_t M, int64_t K, int64_t E, int64_t n_used, int64_t T,
+                 const int32_t *ids_in, const float *w_in, uint64_t seed, int nthreads, float *y_ref, float *y_ada,
+                 int *wrapped, char *err, int errlen) {
+    spq4k_ggml *b;
+    int rc = spq4k_ggml_init(0, &b);
+    if (rc) {
+        snprintf(err, errlen, "spq4k_ggml_init: %d", rc);
+        return rc;
+    }
+    const int64_t Eh = mode ? E : 1;
+    struct ggml_context *hctx = new_ctx((size_t)3 * M * K * Eh * 2 + (size_t)(M + K) * T * n_used * 32 + (64 << 20));
+    struct ggml_init_params dp = {(size_t)64 << 10, NULL, true};
+    struct ggml_context *dctx = ggml_init(dp);
+    float *tmp = (float *)malloc((size_t)M * K * Eh * sizeof(float));
+    struct ggml_tensor *yr, *ya;
+    struct ggml_tensor *hsrc[6], *dsrc[6];
+    int nsrc;
+    if (mode == 0) {
+        hsrc[0] = q_weight(hctx, type, K, M, 1, seed, tmp);
+        hsrc[1] = f32_input(hctx, K, T, 1, seed + 1);
+        nsrc = 2;
+        dsrc[0] = ggml_new_tensor_2d(dctx, hsrc[0]->type, K, M);
+        dsrc[1] = ggml_new_tensor_2d(dctx, GGML_TYPE_F32, K, T);
+        yr = ggml_mul_mat(hctx, hsrc[0], hsrc[1]);
+        ya = spq4k_ggml_mul_mat(dctx, dsrc[0], dsrc[1], b);
+    } else {
+        struct ggml_tensor *gate = q_weight(hctx, GGML_TYPE_Q4_K, K, M, E, seed, tmp);
+        struct ggml_tensor *up = q_weight(hctx, GGML_TYPE_Q4_K, K, M, E, seed + 1, tmp);
+        struct ggml_tensor *down = q_weight(hctx, type, M, K, E, seed + 2, tmp);
+        struct ggml_tensor *cur = ggml_reshape_2d(hctx, f32_input(hctx, K, T, 1, seed + 3), K, T);
+        struct ggml_tensor *sel = ggml_new_tensor_2d(hctx, GGML_TYPE_I32, n_used, T);
+        memcpy(sel->data, ids_in, (size_t)n_used * T * sizeof(int32_t));
+        struct ggml_tensor *wts = ggml_new_tensor_3d(hctx, GGML_TYPE_F32, 1, n_used, T);
+        memcpy(wts->data, w_in, (size_t)n_used * T * sizeof(float));
+        struct ggml_tensor *cur3 = ggml_reshape_3d(hctx, cur, K, 1, T);
+        struct ggml_tensor *par = ggml_mul(hctx, ggml_silu(hctx, ggml_mul_mat_id(hctx, gate, cur3, sel)),
+                                           ggml_mul_mat_id(hctx, up, cur3, sel));
+        struct ggml_tensor *weighted = ggml_mul(hctx, ggml_mul_mat_id(hctx, down, par, sel), wts);
+        yr = ggml_reshape_2d(hctx, ggml_sum_rows(hctx, ggml_cont(hctx, ggml_permute(hctx, weighted, 1, 0, 2, 3))), K, T);
+        hsrc[0] = cur; hsrc[1] = sel; hsrc[2] = wts; hsrc[3] = gate; hsrc[4] = up; hsrc[5] = down;
+        nsrc = 6;
+        for (int i = 0; i < 6; ++i) {
+            dsrc[i] = ggml_new_tensor(dctx, hsrc[i]->type, GGML_MAX_DIMS, hsrc[i]->ne);
+        }
+        ya = spq4k_ggml_moe_ffn(dctx, dsrc[0], dsrc[1], dsrc[2], dsrc[3], dsrc[4], dsrc[5], b);
+    }
+    free(tmp);
+    int step = 0;
+    ggml_backend_buffer_t dbuf = NULL;
+    if (!ya) step = 1;
+    if (!step && !(dbuf = ggml_backend_alloc_ctx_tensors_from_buft(dctx, &dv_buft))) step = 2;
+    if (!step) {
+        for (int i = 0; i < nsrc; ++i) ggml_backend_tensor_set(dsrc[i], hsrc[i]->data, 0, ggml_nbytes(hsrc[i]));
+        if (compute_graph(yr, nthreads) || compute_graph(ya, 1)) step = 3;
+        else if (spq4k_ggml_status(b)) step = 4;
+    }
+    if (!step) {
+        memcpy(y_ref, yr->data, ggml_nbytes(yr));
+        ggml_backend_tensor_get(ya, y_ada, 0, ggml_nbytes(ya));
+        const struct ggml_tensor *W = mode ? dsrc[3] : dsrc[0];
+        *wrapped = spq4k_ggml_resident_data(b, W) == W->data;
+    }
+    if (step) snprintf(err, errlen, "device-resident check step %d: %s", step, spq4k_ggml_last_error(b));
+    spq4k_ggml_free(b);
+    if (dbuf) ggml_backend_buffer_free(dbuf);
+    ggml_free(dctx);
+    ggml_free(hctx);
     return step;
 }

@@ -137,3 +137,48 @@ def test_adapter_resident_table(drv):
     drv.check_resident.argtypes = [ctypes.c_char_p, ctypes.c_int]
     rc = drv.check_resident(err, 256)
     assert rc == 0, err.value.decode()
+
+
+def _device_check(drv, mode, qtype, M, K, E, k, T, ids, w, seed):
+    f32p = ctypes.POINTER(ctypes.c_float)
+    i64 = ctypes.c_int64
+    drv.check_device.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64, i64, i64, i64, ctypes.POINTER(ctypes.c_int32),
+                                 f32p, ctypes.c_uint64, ctypes.c_int, f32p, f32p, ctypes.POINTER(ctypes.c_int),
+                                 ctypes.c_char_p, ctypes.c_int]
+    n = (M if mode == 0 else K) * T
+    yr, ya = np.full(n, np.nan, np.float32), np.full(n, np.nan, np.float32)
+    wrapped = ctypes.c_int(0)
+    err = ctypes.create_string_buffer(256)
+    rc = drv.check_device(mode, qtype, M, K, E, k, T, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                          w.ctypes.data_as(f32p), seed, 8, yr.ctypes.data_as(f32p), ya.ctypes.data_as(f32p),
+                          ctypes.byref(wrapped), err, 256)
+    assert rc == 0, err.value.decode()
+    assert wrapped.value == 1, "the device-resident weight was copied instead of adopted in place"
+    return yr, ya
+
+
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0])
+@pytest.mark.parametrize("M,K,T", [(4096, 4096, 1), (512, 4096, 16), (300, 2048, 3)])
+def test_adapter_device_resident_mul_mat(drv, qtype, M, K, T):
+    """Tensors in a device (non-host) ggml buffer -- as on a HIP build of the
+    engine's ggml -- run in place: the weight adopted without a copy, the
+    activations and output never copied through the host; the output within
+    close_enough of ggml's own MUL_MAT on the same values."""
+    none_i, none_f = np.zeros(1, np.int32), np.zeros(1, np.float32)
+    yr, ya = _device_check(drv, 0, qtype, M, K, 1, 1, T, none_i, none_f, 61 + T)
+    _check(yr, ya, f"device-resident mul_mat type={qtype} M={M} K={K} T={T}")
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_adapter_device_resident_moe_ffn(drv, T):
+    """The routed-expert FFN block node on device-resident tensors against
+    ggml's stock routed-expert graph on the host (normwise, as above)."""
+    E, D, F, k = 32, 2048, 768, 8
+    rng = np.random.default_rng(70 + T)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    ids = np.ascontiguousarray(np.argsort(-logits, axis=1, kind="stable")[:, :k].astype(np.int32))
+    w = np.ascontiguousarray(rng.random((T, k)).astype(np.float32))
+    yr, ya = _device_check(drv, 1, TYPE_Q4_K, F, D, E, k, T, ids, w, 80 + T)
+    assert np.isfinite(ya).all()
+    rel = float(np.linalg.norm(ya.astype(np.float64) - yr) / np.linalg.norm(yr.astype(np.float64)))
+    assert rel <= FF_NORMWISE, f"device-resident moe ffn T={T}: normwise {rel:.3e} > {FF_NORMWISE}"
