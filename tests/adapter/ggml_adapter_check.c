@@ -395,3 +395,68 @@ int check_device(int mode, int type, int64_t M, int64_t K, int64_t E, int64_t n_
     ggml_free(hctx);
     return step;
 }
+
+/* A small dense decoder built twice in one graph of the reference's ggml --
+ * the CPU's MUL_MAT nodes (y_ref) and the adapter's (y_ada) -- the node
+ * sequence of the engine's dense layer around attention (build_block_decode,
+ * desktop/engine/src/forward.cpp:2663-2856) and its output head (:3411-3413):
+ * per layer x = x + o(q(xa)) with xa = rms_norm(x) * attn_norm (the
+ * attention core, not on this path, is stood in for by q; k and v feed only
+ * attention and are left out), then x = x + down(silu(gate(xb)) * up(xb)) with
+ * xb = rms_norm(x) * ffn_norm; logits = out(rms_norm(x) * out_norm). All
+ * matrices Q4_K; norms, residual adds, SiLU and the product are ggml CPU ops
+ * in both graphs. y_* are the logits [n_vocab, T]. */
+int check_decoder(int n_layers, int64_t n_embd, int64_t n_q, int64_t n_ff, int64_t n_vocab, int64_t T,
+                  uint64_t seed, int nthreads, float *y_ref, float *y_ada, char *err, int errlen) {
+    spq4k_ggml *b;
+    int rc = spq4k_ggml_init(0, &b);
+    if (rc) {
+        snprintf(err, errlen, "spq4k_ggml_init: %d", rc);
+        return rc;
+    }
+    const size_t wvals = (size_t)n_layers * (n_embd * n_q * 2 + n_embd * n_ff * 3) + n_embd * n_vocab;
+    struct ggml_context *ctx = new_ctx(wvals + (size_t)(n_embd + n_ff + n_vocab) * T * 400 + (256 << 20));
+    const int64_t mx = n_ff * n_embd > n_vocab * n_embd ? n_ff * n_embd : n_vocab * n_embd;
+    float *tmp = (float *)malloc((size_t)mx * sizeof(float));
+    struct ggml_tensor *x0 = f32_input(ctx, n_embd, T, 1, seed);
+    x0 = ggml_reshape_2d(ctx, x0, n_embd, T);
+    struct ggml_tensor *xr = x0, *xa = x0;
+    uint64_t s = seed + 1;
+    const float eps = 1e-6f;
+    for (int l = 0; l < n_layers; ++l) {
+        struct ggml_tensor *wq = q_weight(ctx, GGML_TYPE_Q4_K, n_embd, n_q, 1, s++, tmp);
+        struct ggml_tensor *wo = q_weight(ctx, GGML_TYPE_Q4_K, n_q, n_embd, 1, s++, tmp);
+        struct ggml_tensor *wg = q_weight(ctx, GGML_TYPE_Q4_K, n_embd, n_ff, 1, s++, tmp);
+        struct ggml_tensor *wu = q_weight(ctx, GGML_TYPE_Q4_K, n_embd, n_ff, 1, s++, tmp);
+        struct ggml_tensor *wd = q_weight(ctx, GGML_TYPE_Q4_K, n_ff, n_embd, 1, s++, tmp);
+        struct ggml_tensor *an = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, n_embd);
+        struct ggml_tensor *fn = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, n_embd);
+        normal_fill((float *)an->data, n_embd, s++, 0.2f);
+        normal_fill((float *)fn->data, n_embd, s++, 0.2f);
+        for (int64_t i = 0; i < n_embd; ++i) {
+            ((float *)an->data)[i] += 1.0f;
+            ((float *)fn->data)[i] += 1.0f;
+        }
+        for (int g = 0; g < 2; ++g) {
+            struct ggml_tensor **x = g ? &xa : &xr;
+            struct ggml_tensor *h = ggml_mul(ctx, ggml_rms_norm(ctx, *x, eps), an);
+            struct ggml_tensor *q = g ? spq4k_ggml_mul_mat(ctx, wq, h, b) : ggml_mul_mat(ctx, wq, h);
+            struct ggml_tensor *o = g ? spq4k_ggml_mul_mat(ctx, wo, q, b) : ggml_mul_mat(ctx, wo, q);
+            struct ggml_tensor *x1 = ggml_add(ctx, *x, o);
+            struct ggml_tensor *hb = ggml_mul(ctx, ggml_rms_norm(ctx, x1, eps), fn);
+            struct ggml_tensor *gt = g ? spq4k_ggml_mul_mat(ctx, wg, hb, b) : ggml_mul_mat(ctx, wg, hb);
+            struct ggml_tensor *ut = g ? spq4k_ggml_mul_mat(ctx, wu, hb, b) : ggml_mul_mat(ctx, wu, hb);
+            struct ggml_tensor *par = ggml_mul(ctx, ggml_silu(ctx, gt), ut);
+            struct ggml_tensor *dn = g ? spq4k_ggml_mul_mat(ctx, wd, par, b) : ggml_mul_mat(ctx, wd, par);
+            *x = ggml_add(ctx, x1, dn);
+        }
+    }
+    struct ggml_tensor *wout = q_weight(ctx, GGML_TYPE_Q4_K, n_embd, n_vocab, 1, s++, tmp);
+    struct ggml_tensor *on = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, n_embd);
+    normal_fill((float *)on->data, n_embd, s++, 0.2f);
+    for (int64_t i = 0; i < n_embd; ++i) ((float *)on->data)[i] += 1.0f;
+    free(tmp);
+    struct ggml_tensor *yr = ggml_mul_mat(ctx, wout, ggml_mul(ctx, ggml_rms_norm(ctx, xr, eps), on));
+    struct ggml_tensor *ya = spq4k_ggml_mul_mat(ctx, wout, ggml_mul(ctx, ggml_rms_norm(ctx, xa, eps), on), b);
+    return finish(ctx, b, yr, ya, nthreads, y_ref, y_ada, err, errlen);
+}
