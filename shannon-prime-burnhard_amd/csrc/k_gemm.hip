@@ -761,6 +761,7 @@ static const TiledShape kTiled[] = {
     {64, 16, true, launch_ring_<1, 1, 4, 3, 16, 1>, WF_Q6K},    // 29
     {64, 16, true, launch_ring_<1, 1, 4, 3, 16, 2>, WF_Q5K},    // 30
     {64, 16, true, launch_ring_<1, 1, 4, 3, 16, 3>, WF_Q80},    // 31
+    {128, 64, true, launch_ring_<1, 2, 4, 2, 32>},   // 32: ring 32x32, 4 waves, 2 stages (two workgroups a CU)
 };
 constexpr int N_TILED = (int)(sizeof(kTiled) / sizeof(kTiled[0]));
 
@@ -826,6 +827,12 @@ GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
             const int64_t rt = row_tiles(p, 256);
             const int64_t g0 = rt * ((p.T + 63) / 64);
             if (g0 >= num_cus || (p.T >= 128 && rt >= 24)) cfg = 11;
+            // From T = 256 on 12288 rows or more: the same 32x32 tiles in
+            // 4-wave workgroups of 128 rows, two a CU, whose barriers do not
+            // hold all eight waves of a CU in step (24576 x 4096 at T = 512:
+            // 166 against 178 us; 6144 rows: 54.3 against 52.2; T = 128 on
+            // 24576 rows: 55.0 against 53.9)
+            if (cfg == 11 && p.T >= 256 && p.rows >= 12288) cfg = 32;
         }
     }
     const TiledShape& s = kTiled[cfg];

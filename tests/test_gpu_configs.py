@@ -100,19 +100,22 @@ def test_prefill_t512_planner(ctx, oracle, shapes):
         w.free()
 
 
+@pytest.mark.parametrize("cfg", [11, 32])
 @pytest.mark.parametrize("M,K,T", [(512, 4096, 512), (256, 12288, 512), (300, 4096, 500)])
-def test_prefill_t512_forced_32x32(oracle, M, K, T):
-    """Launch shape 11 (32 x 32 tiles, 256 rows x 64 tokens) on matrices the
-    oracle covers whole, with a ragged token tile at T = 500."""
+def test_prefill_t512_forced_32x32(oracle, M, K, T, cfg):
+    """The 32 x 32-tile launch shapes -- 11 (256 rows x 64 tokens, 8 waves)
+    and 32 (128 rows x 64 tokens, 4 waves, two workgroups a CU: the planner's
+    choice from T = 256 on 12288 rows or more) -- on matrices the oracle
+    covers whole, with a ragged token tile at T = 500."""
     from _envctx import context_with
-    c = context_with({"SPQ4K_GEMM_CFG": 11})
+    c = context_with({"SPQ4K_GEMM_CFG": cfg})
     try:
         rng = np.random.default_rng(M + T)
         W = oracle.quantize_q4K((rng.standard_normal((M, K)) * 0.02).astype(np.float32))
         X = rng.standard_normal((T, K)).astype(np.float32)
         Wd = c.upload(W, M, K)
         _check(c.mul_mat(Wd, X), oracle.mul_mat(W, M, K, X), oracle.mul_mat_dq_f64(12, W, M, K, X),
-               f"cfg 11 {M}x{K} T={T}")
+               f"cfg {cfg} {M}x{K} T={T}")
         Wd.free()
     finally:
         c.close()

@@ -130,7 +130,7 @@ def _one_sign_tokens(rng, T, K):
     return X.astype(np.float32)
 
 
-@pytest.mark.parametrize("cfg", list(range(14)))
+@pytest.mark.parametrize("cfg", list(range(14)) + [32])
 def test_gemm_tiled_shapes(oracle, cfg):
     """Every launch shape of the tiled kernel (SPQ4K_GEMM_CFG) with ragged row,
     token and super-block tails (K = 768 leaves a K-split wave idle), the
