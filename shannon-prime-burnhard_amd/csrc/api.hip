@@ -228,8 +228,10 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
 //   K = 4096,  M <= 8192   : 12 waves = 2 rows a wave   (q/k/v, 6144 rows)
 //   K = 4096,  M <= 32768  : 16 waves                   (gate/up, 24576 rows)
 //   K = 4096,  larger M    : 12 waves, 2 rows in flight, x-first (lm_head)
-//   K = 12288              : 16 waves, x-first: 48 KB of x per CU would
-//                            otherwise queue behind the CU's weight loads
+//   K = 12288, Q4_K        : 8 waves, weights first (4096 x 12288: 8.21 against
+//                            8.52 us with 16 waves x-first; 1024 rows 5.25 against
+//                            6.53, 28672 rows 35.7 against 36.8, 12288 rows 16.8
+//                            against 16.7); other formats 12 waves, x-first
 //   K = 27648              : 8 waves (the registers of 7 Q8_K blocks a lane), x-first
 DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb_rows, int64_t rows) {
     DecodeCfg d{};
@@ -237,6 +239,8 @@ DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb_rows, int64_t rows) {
     const int nb = decode_bucket(fmt, nb_rows) > 0 ? decode_bucket(fmt, nb_rows) : nb_rows;
     if (nb > 48) {
         d.waves = 8; d.depth = 1; d.xfirst = true;
+    } else if (nb >= 48 && fmt == WF_Q4K) {
+        d.waves = 8; d.depth = 1; d.xfirst = false;
     } else if (nb >= 48) {
         d.waves = 16; d.depth = 1; d.xfirst = true;
     } else if (rows <= 4096) {
