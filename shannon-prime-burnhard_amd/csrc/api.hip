@@ -1548,8 +1548,7 @@ int moe_decode_try(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, c
     const size_t bb = type_block_bytes(bank->type);
     const int64_t rows = T * ne11, n_pairs = T * n_used;
     if (!(T <= c->moe_dec_max_t && n_pairs <= MOE_DEC_MAX_PAIRS && rows <= MOE_DEC_MAX_XROWS && moe_decode_supported(nb) &&
-          !c->moe_unfused && c->moe_mode == 0 && (size_t)q8lds_bytes((int)rows * nb) <= (size_t)LDS_BUDGET &&
-          n_pairs * MV <= INT32_MAX))
+          !c->moe_unfused && c->moe_mode == 0 && n_pairs * MV <= INT32_MAX))
         return 1;
     MoeFusedParams f;
     memset(&f, 0, sizeof f);
@@ -1578,8 +1577,67 @@ int moe_decode_try(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, c
     const int64_t need = (n_pairs * MV + per_wg - 1) / per_wg;
     const int grid = (int)(need < 2 * c->num_cus ? need : 2 * c->num_cus);
     moe_decode_plan(f, grid, &f.rows_per_wg, &f.xwin_rows);
+    // the input rows a workgroup quantises must fit its LDS
+    if ((size_t)q8lds_bytes(f.xwin_rows * nb) > (size_t)LDS_BUDGET) return 1;
     hipError_t e = launch_moe_decode(f, grid, c->stream);
     if (e != hipSuccess) return hip_fail(c, e, "moe decode launch");
+    return 0;
+}
+
+// The routed-expert block's down projection and weighted slot sum in one
+// launch (moe_down_sum_kernel), for n_used <= MOE_SUM_MAX_USED and exactly
+// when spq4k_moe(down, ne11 = n_used) takes the decode mapping
+// (moe_decode_try's conditions), whose per-row arithmetic it shares: the
+// result is then that of the down launch and the combine launch bit for bit.
+// H holds the T * n_used hidden rows. Returns 1 when it does not apply.
+int moe_down_sum_try(spq4k_ctx* c, const spq4k_weights* down, const int32_t* ids, int64_t n_used, int64_t T,
+                     const float* H, const float* w, float* Y) {
+    const int nb = (int)(down->K / SPQ4K_QK_K), M = (int)down->M;
+    const int64_t n_pairs = T * n_used, total = T * down->M;
+    if (!(T <= c->moe_dec_max_t && n_pairs <= MOE_DEC_MAX_PAIRS && n_pairs <= MOE_DEC_MAX_XROWS &&
+          n_used <= MOE_SUM_MAX_USED && moe_decode_supported(nb) && !c->moe_unfused && c->moe_mode == 0 &&
+          down->fmt != WF_Q80 && total <= INT32_MAX))
+        return 1;
+    {
+        // moe_decode_try's window rule for the same call
+        MoeFusedParams d;
+        memset(&d, 0, sizeof d);
+        d.M = M;
+        d.n_pairs = (int32_t)n_pairs;
+        d.nb = nb;
+        d.n_xrows = (int32_t)n_pairs;
+        const int64_t pw = moe_decode_rows_per_wg(nb), need = (n_pairs * M + pw - 1) / pw;
+        int32_t rw, xw;
+        moe_decode_plan(d, (int)(need < 2 * c->num_cus ? need : 2 * c->num_cus), &rw, &xw);
+        if ((size_t)q8lds_bytes(xw * nb) > (size_t)LDS_BUDGET) return 1;
+    }
+    MoeFusedParams f;
+    memset(&f, 0, sizeof f);
+    f.ids = ids;
+    f.X = H;
+    f.bank = down->data;
+    f.expert_bytes = (size_t)M * nb * type_block_bytes(down->type);
+    f.fmt = down->fmt;
+    f.n_pairs = (int32_t)n_pairs;
+    f.n_used = (int32_t)n_used;
+    f.ne11 = (int32_t)n_used;
+    f.K = (int32_t)down->K;
+    f.M = M;
+    f.nb = nb;
+    f.E = (int32_t)down->E;
+    f.n_xrows = (int32_t)n_pairs;
+    // one output element a wave at a time, about two workgroups of 8 waves a CU
+    const int64_t waves = 2 * (int64_t)c->num_cus * 8;
+    int64_t per_wg = 8 * ((total + waves - 1) / waves);
+    const int grid = (int)((total + per_wg - 1) / per_wg);
+    // a run of per_wg elements spans at most per_wg / M + 2 tokens
+    int64_t toks = per_wg / M + 2;
+    if (toks > T) toks = T;
+    f.rows_per_wg = (int32_t)per_wg;
+    f.xwin_rows = (int32_t)(toks * n_used);
+    if ((size_t)q8lds_bytes(f.xwin_rows * nb) > (size_t)LDS_BUDGET) return 1;
+    hipError_t e = launch_moe_down_sum(f, w, Y, grid, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "moe down-sum launch");
     return 0;
 }
 
@@ -1910,6 +1968,10 @@ int spq4k_moe_ffn(spq4k_ctx* c, const spq4k_weights* gate, const spq4k_weights* 
         if (e != hipSuccess) return hip_fail(c, e, "swiglu launch");
     }
     // down of each pair's own hidden row (forward.cpp:1104: b = par [n_ff, n_used, T], ne11 = n_used)
+    // with the weights and the sum over the slots (:1107-1116) as its epilogue
+    // for small batches; otherwise down, then the combine launch
+    rc = moe_down_sum_try(c, down, ids, n_used, T, H, weights, Y);
+    if (rc <= 0) return rc;
     rc = spq4k_moe(c, down, ids, n_used, n_used, T, H, D);
     if (rc) return rc;
     // weights and the sum over the slots (forward.cpp:1107-1116)

@@ -409,6 +409,122 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     }
 }
 
+// The routed-expert block's down projection with the weighted sum over the
+// slots as its epilogue (small batches, n_used <= 8): one wave per output
+// element (t, r). Lane group grp (LPR = 4 * BSL lanes, the decode mapping of
+// moe_decode_kernel) computes the dots of slots grp, grp + GPW, ...: row r of
+// expert ids[t][s] against the Q8_K-quantised hidden row t * n_used + s. The
+// wave then adds the fp32 products D_s * w[t][s] in double over s in slot
+// order and stores their sum rounded to fp32 -- moe_combine_kernel's
+// arithmetic (ggml_mul, then ggml_sum_rows' double sum, forward.cpp:1107-1116),
+// so Y equals that of the separate down and combine launches bit for bit. A
+// workgroup owns p.rows_per_wg consecutive elements of Y [T][M] and quantises
+// the hidden rows of the tokens they belong to. An id outside [0, E)
+// contributes nothing.
+template <typename Fmt, int NB, int BSL, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void moe_down_sum_kernel(MoeFusedParams p, const float* __restrict__ cw,
+                                                                  float* __restrict__ Yc) {
+    using W = typename Fmt::W;
+    extern __shared__ __align__(16) char smem[];
+    constexpr int LPR = 4 * BSL, GPW = 64 / LPR, SPG = (MOE_SUM_MAX_USED + GPW - 1) / GPW;
+    constexpr int NIT = (NB + BSL - 1) / BSL;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int l4 = lane & 3;
+    const int bsub = (lane & (LPR - 1)) >> 2;
+    const int grp = lane / LPR;
+    const int M = p.M, nu = p.n_used;
+    const int total = (p.n_pairs / nu) * M;
+    const int u0 = blockIdx.x * p.rows_per_wg;
+    if (u0 >= total) return;                     // uniform over the workgroup
+    const int u1 = min(total, u0 + p.rows_per_wg);
+    const int tlo = u0 / M;
+    const int nitems = ((u1 - 1) / M - tlo + 1) * nu * NB;
+    const Q8Lds L = q8lds_carve(smem, p.xwin_rows * NB);
+    const float* __restrict__ X = p.X + (int64_t)tlo * nu * p.K;
+    for (int base = 0; base < nitems; base += 4 * WAVES) {
+        const int item0 = base + wave * 4 + (lane >> 4);
+        const bool valid = item0 < nitems;
+        const int item = valid ? item0 : nitems - 1;
+        const XRegs r = load_x16(X, p.K, item / NB, item % NB);
+        store_q8_item(r, valid, item, L);
+    }
+    __syncthreads();
+    const size_t row_bytes = (size_t)NB * Fmt::BYTES;
+    for (int u = u0 + wave; u < u1; u += WAVES) {
+        const int t = u / M;
+        const int r = u - t * M;
+        W w[SPG][NIT];
+        bool live[SPG];
+#pragma unroll
+        for (int k = 0; k < SPG; ++k) {
+            const int s = grp + GPW * k;
+            const int e = s < nu ? p.ids[t * nu + s] : -1;
+            live[k] = e >= 0 && e < p.E;
+            const uint8_t* wr = p.bank + (size_t)(live[k] ? e : 0) * p.expert_bytes + (size_t)r * row_bytes;
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int bb = bsub + BSL * it;
+                w[k][it] = Fmt::load(wr + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
+            }
+        }
+        float d[SPG];
+#pragma unroll
+        for (int k = 0; k < SPG; ++k) {
+            const int s = grp + GPW * k;
+            const int xs = ((t - tlo) * nu + (s < nu ? s : 0)) * NB;
+            float acc[1] = {0.0f};
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int bb = bsub + BSL * it;
+                Fmt::template dot<1>(w[k][it], l4, L, xs + (bb < NB ? bb : NB - 1), 0, bb < NB && live[k], acc);
+            }
+            d[k] = group_sum_last<LPR>(acc[0]);
+        }
+        // slot s = k * GPW + g sits in lane g * LPR + LPR - 1 of dot k
+        double sum = 0.0;
+#pragma unroll
+        for (int k = 0; k < SPG; ++k)
+#pragma unroll
+            for (int g = 0; g < GPW; ++g) {
+                const int s = k * GPW + g;
+                const float ds = __shfl(d[k], g * LPR + LPR - 1, 64);
+                if (s < nu) {
+                    const float prod = ds * cw[t * nu + s];
+                    sum += (double)prod;
+                }
+            }
+        if (lane == 63) Yc[(int64_t)t * M + r] = (float)sum;
+    }
+}
+
+template <typename Fmt, int NB, int BSL>
+static hipError_t launch_mdsum(const MoeFusedParams& p, const float* cw, float* Yc, int grid, hipStream_t st) {
+    constexpr int WAVES = 8;
+    const size_t lds = (size_t)q8lds_bytes(p.xwin_rows * NB);
+    hipLaunchKernelGGL((moe_down_sum_kernel<Fmt, NB, BSL, WAVES>), dim3(grid), dim3(WAVES * 64), lds, st, p, cw, Yc);
+    return hipGetLastError();
+}
+
+template <typename Fmt>
+static hipError_t launch_moe_down_sum_fmt(const MoeFusedParams& p, const float* cw, float* Yc, int grid,
+                                          hipStream_t st) {
+    switch (p.nb) {
+        case 3: return launch_mdsum<Fmt, 3, 4>(p, cw, Yc, grid, st);
+        case 8: return launch_mdsum<Fmt, 8, 8>(p, cw, Yc, grid, st);
+        case 16: return launch_mdsum<Fmt, 16, 16>(p, cw, Yc, grid, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_moe_down_sum(const MoeFusedParams& p, const float* cw, float* Yc, int grid, hipStream_t st) {
+    if (p.n_used < 1 || p.n_used > MOE_SUM_MAX_USED || p.n_pairs % p.n_used) return hipErrorInvalidValue;
+    if (p.fmt == WF_Q6K) return launch_moe_down_sum_fmt<FmtQ6K>(p, cw, Yc, grid, st);
+    if (p.fmt == WF_Q5K) return launch_moe_down_sum_fmt<FmtQ5K>(p, cw, Yc, grid, st);
+    if (p.fmt == WF_Q4K) return launch_moe_down_sum_fmt<FmtQ4K>(p, cw, Yc, grid, st);
+    return hipErrorInvalidValue;
+}
+
 template <typename Fmt, int NB, int BSL>
 static hipError_t launch_mdec(const MoeFusedParams& p, int grid, hipStream_t st) {
     constexpr int WAVES = 8;

@@ -141,6 +141,12 @@ bool moe_decode_supported(int nb);
 int moe_decode_rows_per_wg(int nb);
 void moe_decode_plan(const MoeFusedParams& p, int grid, int32_t* rows_per_wg, int32_t* xwin_rows);
 hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st);
+// the routed-expert block's down projection with the weighted slot sum as its
+// epilogue (moe_down_sum_kernel): Yc [T][M] = sum over s of (bank row of ids[t][s]
+// . X[t * n_used + s]) * cw[t][s]; p.rows_per_wg elements of Yc a workgroup,
+// p.xwin_rows the hidden rows one quantises at most; n_used <= MOE_SUM_MAX_USED
+constexpr int MOE_SUM_MAX_USED = 8;
+hipError_t launch_moe_down_sum(const MoeFusedParams& p, const float* cw, float* Yc, int grid, hipStream_t st);
 hipError_t launch_moe_gemv(const MoeParams& p, int tc, int bpr, int grid, hipStream_t st);
 // matrix-core form: moe_prep_kernel (routing in workgroup 0, permuted Q8_K
 // planes of the n_xrows input rows X in the others), then the ring kernel

@@ -23,7 +23,7 @@ gate/up 768x2048, down 2048x768) and ragged ones:
 import numpy as np
 import pytest
 
-from _oracle import TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, close_enough, parity_ok
+from _oracle import TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, close_enough, parity_ok
 
 pytestmark = pytest.mark.gpu
 CHAIN_NORMWISE = 2e-3
@@ -119,6 +119,49 @@ def test_moe_ffn_30b(ctx, oracle, down_type, T):
     assert err < CHAIN_NORMWISE, f"block T={T} normwise {err:.3e}"
     for a in (gate, up, down):
         a.free()
+
+
+@pytest.mark.parametrize("n_ff,n_used,T,down_type", [
+    (768, 8, 8, TYPE_Q4_K),      # 64 pairs, the largest small batch
+    (768, 8, 9, TYPE_Q4_K),      # 72 pairs: down on the matrix cores, then the combine
+    (768, 1, 5, TYPE_Q4_K),
+    (768, 3, 2, TYPE_Q6_K),
+    (2048, 6, 3, TYPE_Q4_K),     # 8 super-blocks a down row, two lane groups a wave
+    (2048, 8, 1, TYPE_Q5_K),
+    (4096, 8, 2, TYPE_Q4_K),     # 16 super-blocks a down row, one lane group a wave
+    (4096, 5, 1, TYPE_Q6_K),
+])
+def test_moe_ffn_down_sum_shapes(ctx, oracle, n_ff, n_used, T, down_type):
+    """the down projection with the slot sum in its epilogue (small batches)
+    equals the down launch followed by the combine, bit for bit, for every
+    down row length the small-batch sweep serves and n_used up to 8; and the
+    batch past it still runs the two launches"""
+    from spq4k.hip import DeviceArray
+    E, D_ = 16, 512
+    rng = np.random.default_rng(7 * n_ff + n_used + T)
+    gate, _ = _bank(ctx, TYPE_Q4_K, E, n_ff, D_, 31)
+    up, _ = _bank(ctx, TYPE_Q4_K, E, n_ff, D_, 32)
+    down, dh = _bank(ctx, down_type, E, D_, n_ff, 33)
+    ids, w = _routing(rng, T, E, n_used)
+    X = rng.standard_normal((T, D_)).astype(np.float32)
+    Y = ctx.moe_ffn(gate, up, down, ids, w, X)
+    ids_d, X_d = DeviceArray.from_host(ids), DeviceArray.from_host(X)
+    G_d, U_d, H_d = (DeviceArray(T * n_used * n_ff, np.float32) for _ in range(3))
+    Dn_d = DeviceArray(T * n_used * D_, np.float32)
+    ctx.moe_multi_dev([gate, up], ids_d.ptr, n_used, 1, T, X_d.ptr, [G_d.ptr, U_d.ptr])
+    ctx.swiglu_dev(G_d.ptr, U_d.ptr, H_d.ptr, T * n_used * n_ff)
+    ctx.moe_dev(down, ids_d.ptr, n_used, n_used, T, H_d.ptr, Dn_d.ptr)
+    ctx.synchronize()
+    H = H_d.to_host().reshape(T, n_used, n_ff)
+    Dn = Dn_d.to_host().reshape(T, n_used, D_)
+    _bits_equal(Y, _weighted_sum(Dn, w), f"n_ff={n_ff} n_used={n_used} T={T} fused vs composed")
+    exp = _mmid(oracle, down_type, dh, D_, n_ff, E, H, ids)
+    ok = parity_ok(Dn, exp, oracle.mul_mat_id_dq_f64(down_type, dh, D_, n_ff, E, H, ids))
+    assert ok.all(), f"down: {int((~ok).sum())}/{ok.size} outside tolerance"
+    for a in (gate, up, down):
+        a.free()
+    for d in (ids_d, X_d, G_d, U_d, H_d, Dn_d):
+        d.free()
 
 
 def test_moe_ffn_ragged(ctx, oracle):
