@@ -162,3 +162,49 @@ def test_gemm_tiled_shapes(oracle, cfg):
             _check(y.to_host(), oracle.mul_mat(w, M, K, X), f"cfg={cfg} multi M={M}")
     finally:
         c.close()
+
+
+@pytest.mark.parametrize("M,K,T,qtype", [(4096, 12288, 16, 12), (1000, 4096, 24, 12), (4096, 12288, 16, 14),
+                                         (700, 8192, 40, 13), (2048, 4096, 16, 8)])
+def test_gemm_k_split_fixup(ctx, oracle, M, K, T, qtype):
+    """Matmuls the planner splits over K ranges (few output tiles: the ring
+    kernel's partial planes, then gemm_reduce_kernel's sum in range order),
+    Q4_K, Q6_K, Q5_K and Q8_0. The result matches the oracle; a graph of the
+    call replayed three times, with eager calls of another split shape between
+    the replays, gives the eager result bit for bit every time."""
+    from spq4k.hip import DeviceArray, Graph
+    rng = np.random.default_rng(M + K + T + qtype)
+    Wf = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    W = oracle.quantize_q8_0(Wf, ref_encoder=True) if qtype == 8 else oracle.quantize(qtype, Wf)
+    Wd = ctx.upload(W, M, K, type=qtype)
+    xd = DeviceArray.from_host(X)
+    yd = DeviceArray((T, M), np.float32)
+    ctx.mul_mat_dev(Wd, xd.ptr, yd.ptr, T)
+    ctx.synchronize()
+    eager = yd.to_host()
+    if qtype == 8:
+        exp = oracle.mul_mat_q8_0(W, M, K, X)
+        _check(eager, exp, f"Q8_0 M={M} K={K} T={T}")
+    else:
+        _check(eager, oracle.mul_mat_type(qtype, W, M, K, X), f"type {qtype} M={M} K={K} T={T}",
+               oracle.mul_mat_dq_f64(qtype, W, M, K, X))
+    # another split shape between the replays
+    M2, K2, T2 = 512, 12288, 20
+    W2 = oracle.quantize_q4K((rng.standard_normal((M2, K2)) * 0.02).astype(np.float32))
+    W2d = ctx.upload(W2, M2, K2)
+    X2 = rng.standard_normal((T2, K2)).astype(np.float32)
+    exp2 = ctx.mul_mat(W2d, X2)
+    yd.fill_byte(0)
+    with Graph.capture(ctx.stream) as g:
+        ctx.mul_mat_dev(Wd, xd.ptr, yd.ptr, T)
+    for rep in range(3):
+        yd.fill_byte(0)
+        g.launch()
+        ctx.synchronize()
+        got = yd.to_host()
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {rep} differs from the eager call"
+        assert np.array_equal(ctx.mul_mat(W2d, X2).view(np.uint32), exp2.view(np.uint32)), f"eager call after replay {rep}"
+    del g
+    for a in (Wd, W2d, xd, yd):
+        a.free()
