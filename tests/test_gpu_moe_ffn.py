@@ -164,6 +164,50 @@ def test_moe_ffn_down_sum_shapes(ctx, oracle, n_ff, n_used, T, down_type):
         d.free()
 
 
+def test_moe_ffn_device_ids_out_of_range(ctx):
+    """Device ids are not validated on the host: through the small-batch down
+    projection an id outside [0, E) contributes nothing to the slot sum (the
+    weighted sum over the valid slots, in slot order), and the other tokens'
+    outputs are untouched by it."""
+    from spq4k.hip import DeviceArray
+    E, k, D_, F, T = 8, 4, 512, 768, 2
+    rng = np.random.default_rng(91)
+    gate, _ = _bank(ctx, TYPE_Q4_K, E, F, D_, 41)
+    up, _ = _bank(ctx, TYPE_Q4_K, E, F, D_, 42)
+    down, _ = _bank(ctx, TYPE_Q4_K, E, D_, F, 43)
+    ids = np.array([[1, 5, 2, 7], [3, 0, 6, 4]], np.int32)
+    w = rng.random((T, k)).astype(np.float32)
+    X = rng.standard_normal((T, D_)).astype(np.float32)
+    ids_d, w_d, X_d = DeviceArray.from_host(ids), DeviceArray.from_host(w), DeviceArray.from_host(X)
+    Y_d = DeviceArray(T * D_, np.float32)
+    ctx.moe_ffn_dev(gate, up, down, ids_d.ptr, w_d.ptr, k, T, X_d.ptr, Y_d.ptr)
+    ctx.synchronize()
+    Y = Y_d.to_host().reshape(T, D_)
+    bad = ids.copy()
+    bad[0, 2] = E          # token 0, slot 2 out of range
+    bad_d = DeviceArray.from_host(bad)
+    ctx.moe_ffn_dev(gate, up, down, bad_d.ptr, w_d.ptr, k, T, X_d.ptr, Y_d.ptr)
+    ctx.synchronize()
+    Yb = Y_d.to_host().reshape(T, D_)
+    _bits_equal(Yb[1], Y[1], "the other token")
+    # token 0 without slot 2: the composed down rows of the valid slots
+    H_d = DeviceArray(T * k * F, np.float32)
+    G_d, U_d = DeviceArray(T * k * F, np.float32), DeviceArray(T * k * F, np.float32)
+    Dn_d = DeviceArray(T * k * D_, np.float32)
+    ctx.moe_multi_dev([gate, up], ids_d.ptr, k, 1, T, X_d.ptr, [G_d.ptr, U_d.ptr])
+    ctx.swiglu_dev(G_d.ptr, U_d.ptr, H_d.ptr, T * k * F)
+    ctx.moe_dev(down, ids_d.ptr, k, k, T, H_d.ptr, Dn_d.ptr)
+    ctx.synchronize()
+    Dn = Dn_d.to_host().reshape(T, k, D_)
+    keep = [0, 1, 3]
+    exp = _weighted_sum(Dn[:1, keep, :], w[:1, keep])[0]
+    _bits_equal(Yb[0], exp, "token 0 with slot 2 out of range")
+    for a in (gate, up, down):
+        a.free()
+    for d in (ids_d, w_d, X_d, Y_d, bad_d, H_d, G_d, U_d, Dn_d):
+        d.free()
+
+
 def test_moe_ffn_ragged(ctx, oracle):
     """n_used 2 of 16 experts, an expert picked by several tokens, n_ff 256"""
     E, k, D_, F, T = 16, 2, 512, 256, 5
