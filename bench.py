@@ -605,6 +605,27 @@ def run_moe(args):
             ctx.moe_ffn(wg, wu, wd, ids_l[0], wh, xh)
             host_t.append(time.perf_counter() - t0)
         blk_bytes = abytes + 4 * T * 2048
+        beast = None
+        if T == 1:
+            # the reference's BurnHard MoE forward for one token (routing of
+            # 128 logits to the top 8, gate / up / down in beast_matvec's fp32
+            # arithmetic, score-weighted sum), per layer, cold
+            lg = [DeviceArray.from_host(np.random.default_rng(50 + L).standard_normal(E).astype(np.float32))
+                  for L in range(NL)]
+            (wg, _, _), (wu, _, _), (wd, _, _) = layers[0]
+            ctx.beast_moe_forward_dev(wg, wu, wd, lg[0].ptr, k, xg.ptr, Yb.ptr)   # sizes the scratch
+            ctx.synchronize()
+            with Graph.capture(ctx.stream) as gf:
+                for L in range(NL):
+                    (wg, _, _), (wu, _, _), (wd, _, _) = layers[L]
+                    ctx.beast_moe_forward_dev(wg, wu, wd, lg[L].ptr, k, xg.ptr, Yb.ptr)
+            ms_bf = time_graph(ctx, gf, max(5, args.steps // 5), 2) / NL
+            bf_bytes = k * sum(q4k_bytes(M, K) for (_, M, K) in shapes) + 4 * (E + 2 * 2048)
+            beast = {"us_per_layer": round(ms_bf * 1e3, 2), "GBps": round(bf_bytes / (ms_bf * 1e-3) / 1e9, 1),
+                     "what": "spq4k_beast_moe_forward: routing (softmax, top-8 of 128) and the 8 experts' "
+                             "gate / up / down in beast_matvec's fp32 dequant-then-dot, score-weighted sum (cold)"}
+            for a in lg:
+                a.free()
         print(json.dumps({"metric": f"Q4_K MoE expert matvec (gate+up+down), T={T}", "value": round(gbs, 1),
                           "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
                           "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2), "unique_experts": uniq,
@@ -617,6 +638,7 @@ def run_moe(args):
                                         "host_path_what": "spq4k_moe_ffn_host, the ggml node's path: copies in, "
                                                           "block, copy out, synchronise (wall clock, median of 20, "
                                                           "layer 0 hot)"},
+                          **({"beast_forward": beast} if beast else {}),
                           "config": {"workload": "30B-A3B-like MoE layer, 128 experts, top-8, 8 layers of banks (cold)",
                                      "T": T}}), flush=True)
         for a in idd + wts:

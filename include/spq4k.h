@@ -269,6 +269,33 @@ int spq4k_moe_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *banks, co
  * device pointers; the _host twin copies in and out. */
 int spq4k_dequant_matvec(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
 int spq4k_dequant_matvec_host(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
+/* spq4k_beast_moe_forward: the reference's BurnHard MoE forward for one
+ * token (sp_beast_moe_forward, desktop/beast_canyon/sp_beast_canyon.c:455-562)
+ * with its routing (sp_beast_route_experts, :385-443), on the GPU:
+ *   score_e = softmax(router_logits)_e (fp32: the largest logit, expf of the
+ *             differences, their sum in expert order);
+ *   the top_k experts by score, the lowest index first among equal scores,
+ *             their scores divided by the sum of the chosen ones;
+ *   per chosen expert, in rank order: g = beast_matvec(gate_e, hidden),
+ *             u = beast_matvec(up_e, hidden), h = (g / (1 + expf(-g))) * u
+ *             (beast_silu_mul, :1168-1173), d = beast_matvec(down_e, h),
+ *             output += score * d (fused multiply-add, as the reference's
+ *             GCC build compiles it).
+ * beast_matvec's arithmetic as in spq4k_dequant_matvec (fp32 activations,
+ * no Q8_K; the dequantised weights bit for bit, the products summed per lane
+ * and across the wave where the reference adds serially). top_k <= 0 means 2
+ * (the reference's default) and is capped at E; at most 16. Q4_K banks: gate
+ * and up [n_ff x n_embd] x E, down [n_embd x n_ff] x E, E <= 4096, rows of at
+ * most 32768 values. router_logits [E], hidden [n_embd] (16-byte aligned),
+ * output [n_embd]; ids / scores [top_k] receive the routing when not NULL
+ * (engine->routing's expert_ids / expert_scores). Device pointers; the _host
+ * twin copies in and out. */
+int spq4k_beast_moe_forward(spq4k_ctx *ctx, const spq4k_weights *gate, const spq4k_weights *up,
+                            const spq4k_weights *down, const float *router_logits, int64_t top_k,
+                            const float *hidden, float *output, int32_t *ids, float *scores);
+int spq4k_beast_moe_forward_host(spq4k_ctx *ctx, const spq4k_weights *gate, const spq4k_weights *up,
+                                 const spq4k_weights *down, const float *router_logits, int64_t top_k,
+                                 const float *hidden, float *output, int32_t *ids, float *scores);
 /* spq4k_moe_ffn: the routed-expert FFN block of a MoE layer, the unit the
  * reference's BURN_MOE custom op replaces (sp_build_burn_moe_op,
  * desktop/engine/src/burn_moe_op.cpp:377-430, computing burn_moe_compute,

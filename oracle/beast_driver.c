@@ -3,8 +3,10 @@
  *
  * Exposes the reference's own beast_matvec (a static function of
  * desktop/beast_canyon/sp_beast_canyon.c:1122-1134, the BurnHard scalar
- * dequant-then-dot matvec) to the tests: this file includes that source file
- * where it lies under /root/reference and adds one exported wrapper. `make -C
+ * dequant-then-dot matvec), its expert routing (sp_beast_route_experts,
+ * :385-443) and the MoE forward built on them (:455-562) to the tests: this
+ * file includes that source file where it lies under /root/reference and adds
+ * exported wrappers. `make -C
  * oracle ref` compiles it with the flags the reference's CMake gives that file
  * under GCC (desktop/beast_canyon/CMakeLists.txt:52-54: -O3 -mfma -mf16c and
  * GCC's default fp contraction), with -march=native narrowed to x86-64-v3 so
@@ -26,4 +28,70 @@ int ref_beast_matvec(const void *W, unsigned type, const float *x, float *y, int
     beast_matvec(&t, x, y, scratch, n_out, n_in);
     free(scratch);
     return 0;
+}
+
+/* sp_beast_route_experts (sp_beast_canyon.c:385-443) on a zeroed engine whose
+ * only settings are the top-k (config.n_experts_per_token) and no GPUs: the
+ * reference's own softmax, top-k and renormalisation. */
+__attribute__((visibility("default")))
+int ref_beast_route(const float *logits, int n_experts, int top_k, int *ids, float *scores) {
+    sp_beast_engine_t *engine = (sp_beast_engine_t *)calloc(1, sizeof *engine);
+    if (!engine) return -1;
+    engine->config.n_experts_per_token = top_k;
+    sp_beast_route_experts(engine, logits, n_experts);
+    const sp_expert_routing_t *r = &engine->routing;
+    for (int k = 0; k < r->n_selected; ++k) {
+        ids[k] = r->expert_ids[k];
+        scores[k] = r->expert_scores[k];
+    }
+    const int n = r->n_selected;
+    free(engine);
+    return n;
+}
+
+/* sp_beast_moe_forward (sp_beast_canyon.c:455-562) for one token over expert
+ * banks held contiguously in memory (E experts of gate / up [n_ff x n_embd]
+ * and down [n_embd x n_ff]): the reference's routing, beast_matvec and
+ * beast_silu_mul, and its per-expert loop restated (:486-545: gate, up,
+ * silu(gate) * up, down, output += score * down_out, output zeroed first);
+ * the engine's reservoir lookup, prefetch, CRT telemetry and barrier, which
+ * do not touch the numbers, are left out. Returns the number of experts. */
+__attribute__((visibility("default")))
+int ref_beast_moe(const void *gate, const void *up, const void *down, unsigned type, int n_experts, int n_embd,
+                  int n_ff, const float *logits, int top_k, const float *hidden, float *output, int *ids,
+                  float *scores) {
+    int k_sel = ref_beast_route(logits, n_experts, top_k, ids, scores);
+    if (k_sel < 0) return -1;
+    const size_t gb = beast_row_bytes(type, n_embd) * (size_t)n_ff;    /* one expert of gate / up */
+    const size_t db = beast_row_bytes(type, n_ff) * (size_t)n_embd;    /* one expert of down */
+    float *gate_buf = (float *)malloc((size_t)n_ff * sizeof(float));
+    float *up_buf = (float *)malloc((size_t)n_ff * sizeof(float));
+    float *down_out = (float *)malloc((size_t)n_embd * sizeof(float));
+    float *scratch = (float *)malloc((size_t)(n_embd > n_ff ? n_embd : n_ff) * sizeof(float));
+    if (!gate_buf || !up_buf || !down_out || !scratch) return -1;
+    memset(output, 0, (size_t)n_embd * sizeof(float));
+    sp_optane_tensor_t tg, tu, td;
+    memset(&tg, 0, sizeof tg);
+    memset(&tu, 0, sizeof tu);
+    memset(&td, 0, sizeof td);
+    tg.type = tu.type = td.type = type;
+    for (int k = 0; k < k_sel; ++k) {
+        const int eid = ids[k];
+        const float score = scores[k];
+        tg.ptr = (void *)((const uint8_t *)gate + (size_t)eid * gb);
+        tu.ptr = (void *)((const uint8_t *)up + (size_t)eid * gb);
+        td.ptr = (void *)((const uint8_t *)down + (size_t)eid * db);
+        beast_matvec(&tg, hidden, gate_buf, scratch, n_ff, n_embd);
+        beast_matvec(&tu, hidden, up_buf, scratch, n_ff, n_embd);
+        beast_silu_mul(gate_buf, up_buf, n_ff);
+        beast_matvec(&td, gate_buf, down_out, scratch, n_embd, n_ff);
+        for (int i = 0; i < n_embd; i++) {
+            output[i] += score * down_out[i];
+        }
+    }
+    free(gate_buf);
+    free(up_buf);
+    free(down_out);
+    free(scratch);
+    return k_sel;
 }

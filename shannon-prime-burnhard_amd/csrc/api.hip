@@ -1926,6 +1926,77 @@ int spq4k_dequant_matvec_host(spq4k_ctx* c, const spq4k_weights* W, const float*
     return 0;
 }
 
+// ---- BurnHard MoE forward (sp_beast_moe_forward) ------------------------------------
+int spq4k_beast_moe_forward(spq4k_ctx* c, const spq4k_weights* gate, const spq4k_weights* up,
+                            const spq4k_weights* down, const float* router_logits, int64_t top_k,
+                            const float* hidden, float* output, int32_t* ids, float* scores) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!gate || !up || !down || !gate->data || !up->data || !down->data || !router_logits || !hidden || !output)
+        return set_err(c, -EINVAL, "beast_moe_forward: null argument");
+    if (gate->type != SPQ4K_TYPE_Q4_K || up->type != SPQ4K_TYPE_Q4_K || down->type != SPQ4K_TYPE_Q4_K)
+        return set_err(c, -EINVAL, "beast_moe_forward: Q4_K expert banks are required");
+    const int64_t E = gate->E, n_embd = gate->K, n_ff = gate->M;
+    if (up->E != E || up->K != n_embd || up->M != n_ff || down->E != E || down->K != n_ff || down->M != n_embd)
+        return set_err(c, -EINVAL, "beast_moe_forward: gate [%lld x %lld x %lld], up and down banks do not match",
+                       (long long)n_ff, (long long)n_embd, (long long)E);
+    if (E > BEAST_MAX_EXPERTS) return set_err(c, -EINVAL, "beast_moe_forward: E = %lld experts", (long long)E);
+    // sp_beast_route_experts (sp_beast_canyon.c:389-392): 2 by default, at most E
+    if (top_k <= 0) top_k = 2;
+    if (top_k > E) top_k = E;
+    if (top_k > BEAST_MAX_TOPK) return set_err(c, -EINVAL, "beast_moe_forward: top_k = %lld", (long long)top_k);
+    if (dequant_matvec_lds_bytes(1, (int)(n_embd / SPQ4K_QK_K)) > DQ_MATVEC_LDS_MAX ||
+        dequant_matvec_lds_bytes(1, (int)(n_ff / SPQ4K_QK_K)) > DQ_MATVEC_LDS_MAX)
+        return set_err(c, -EINVAL, "beast_moe_forward: rows longer than %zu values", DQ_MATVEC_LDS_MAX / sizeof(float));
+    if (!aligned(hidden, 16) || !aligned(router_logits, 4) || !aligned(output, 4) || !aligned(ids, 4) ||
+        !aligned(scores, 4))
+        return set_err(c, -EINVAL, "beast_moe_forward: misaligned pointer");
+    // routing, then the hidden rows, in the fusion scratch
+    const size_t rb = 256;
+    rc = ensure_scratch2(c, rb + (size_t)top_k * n_ff * sizeof(float));
+    if (rc) return rc;
+    int32_t* rid = reinterpret_cast<int32_t*>(c->scratch2);
+    float* rsc = reinterpret_cast<float*>(c->scratch2 + 128);
+    float* H = reinterpret_cast<float*>(c->scratch2 + rb);
+    hipError_t e = launch_beast_moe(gate->data, up->data, down->data, (int)E, (int)n_embd, (int)n_ff, router_logits,
+                                    (int)top_k, hidden, output, rid, rsc, H, c->num_cus, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "beast moe launch");
+    if (ids) SPQ_HIP(c, hipMemcpyAsync(ids, rid, (size_t)top_k * sizeof(int32_t), hipMemcpyDeviceToDevice, c->stream));
+    if (scores)
+        SPQ_HIP(c, hipMemcpyAsync(scores, rsc, (size_t)top_k * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+    return 0;
+}
+
+int spq4k_beast_moe_forward_host(spq4k_ctx* c, const spq4k_weights* gate, const spq4k_weights* up,
+                                 const spq4k_weights* down, const float* router_logits, int64_t top_k,
+                                 const float* hidden, float* output, int32_t* ids, float* scores) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!gate || !up || !down || !router_logits || !hidden || !output)
+        return set_err(c, -EINVAL, "beast_moe_forward_host: null argument");
+    const int64_t E = gate->E, n_embd = gate->K;
+    int64_t k = top_k <= 0 ? 2 : top_k;
+    if (k > E) k = E;
+    if (k > BEAST_MAX_TOPK) return set_err(c, -EINVAL, "beast_moe_forward_host: top_k = %lld", (long long)top_k);
+    DevBuf l, h, o, r;
+    if (hipMalloc(&l.p, (size_t)E * sizeof(float) + 16) != hipSuccess ||
+        hipMalloc(&h.p, (size_t)n_embd * sizeof(float) + 16) != hipSuccess ||
+        hipMalloc(&o.p, (size_t)n_embd * sizeof(float) + 16) != hipSuccess ||
+        hipMalloc(&r.p, 2 * BEAST_MAX_TOPK * sizeof(float)) != hipSuccess)
+        return set_err(c, -ENOMEM, "beast_moe_forward_host");
+    SPQ_HIP(c, hipMemcpyAsync(l.p, router_logits, (size_t)E * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    SPQ_HIP(c, hipMemcpyAsync(h.p, hidden, (size_t)n_embd * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    int32_t* di = reinterpret_cast<int32_t*>(r.p);
+    float* ds = reinterpret_cast<float*>(r.p) + BEAST_MAX_TOPK;
+    rc = spq4k_beast_moe_forward(c, gate, up, down, (const float*)l.p, top_k, (const float*)h.p, (float*)o.p, di, ds);
+    if (rc) return rc;
+    SPQ_HIP(c, hipMemcpyAsync(output, o.p, (size_t)n_embd * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    if (ids) SPQ_HIP(c, hipMemcpyAsync(ids, di, (size_t)k * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+    if (scores) SPQ_HIP(c, hipMemcpyAsync(scores, ds, (size_t)k * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    SPQ_HIP(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+
 // ---- routed-expert FFN block (BURN_MOE) --------------------------------------------
 int spq4k_moe_ffn(spq4k_ctx* c, const spq4k_weights* gate, const spq4k_weights* up, const spq4k_weights* down,
                   const int32_t* ids, const float* weights, int64_t n_used, int64_t T, const float* X, float* Y) {

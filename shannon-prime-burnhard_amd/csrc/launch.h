@@ -274,6 +274,16 @@ hipError_t launch_moe_q8_0_grouped(const Q80Params& p, int tc, int grid, hipStre
 // T <= DQ_MATVEC_MAX_T tokens whose x (staged in LDS) fits DQ_MATVEC_LDS_MAX
 constexpr int DQ_MATVEC_MAX_T = 8;
 constexpr size_t DQ_MATVEC_LDS_MAX = 128 * 1024;
+// the BurnHard MoE forward (k_dqdot.hip): routing of E <= BEAST_MAX_EXPERTS
+// logits to top_k <= BEAST_MAX_TOPK experts (ids, scores), H [top_k][n_ff]
+// the silu(gate) * up rows, out [n_embd]; Q4_K banks, n_embd and n_ff
+// multiples of 256 whose rows fit the x staging
+constexpr int BEAST_MAX_EXPERTS = 4096;
+constexpr int BEAST_MAX_TOPK = 16;
+constexpr int BEAST_DOWN_RPW = 8;
+hipError_t launch_beast_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* down, int E, int n_embd, int n_ff,
+                            const float* logits, int top_k, const float* hidden, float* out, int32_t* ids,
+                            float* scores, float* H, int num_cus, hipStream_t st);
 size_t dequant_matvec_lds_bytes(int T, int nb);
 hipError_t launch_dequant_matvec(const uint8_t* W, int M, int nb, const float* X, int64_t x_tstride, float* Y,
                                  int64_t y_tstride, int T, int num_cus, hipStream_t st);

@@ -103,6 +103,8 @@ def load_library(path: str | None = None):
         "spq4k_dequant_matvec": (I, [V, V, V, V, I64]),
         "spq4k_stream_read": (I, [V, V, S]),
         "spq4k_dequant_matvec_host": (I, [V, V, V, V, I64]),
+        "spq4k_beast_moe_forward": (I, [V, V, V, V, V, I64, V, V, V, V]),
+        "spq4k_beast_moe_forward_host": (I, [V, V, V, V, V, I64, V, V, V, V]),
         "spq4k_moe_ffn_host": (I, [V, V, V, V, V, V, I64, I64, V, V]),
         "spq4k_mul_mat_host": (I, [V, V, V, V, I64]),
         "spq4k_moe_host": (I, [V, V, V, I64, I64, I64, V, V]),
@@ -575,6 +577,28 @@ class Context:
         self._check("spq4k_dequant_matvec_host", self.lib.spq4k_dequant_matvec_host(
             self.handle, W.handle, X.ctypes.data, Y.ctypes.data, X.shape[0]))
         return Y
+
+    def beast_moe_forward(self, gate: Weights, up: Weights, down: Weights, logits: np.ndarray, top_k: int,
+                          hidden: np.ndarray):
+        """spq4k_beast_moe_forward_host: router logits [E], hidden [n_embd] ->
+        (output [n_embd], expert ids [k], scores [k]), k = top_k (2 when <= 0, at most E)."""
+        logits = np.ascontiguousarray(logits, np.float32).ravel()
+        hidden = np.ascontiguousarray(hidden, np.float32).ravel()
+        k = 2 if top_k <= 0 else min(top_k, gate.E)
+        out = np.empty(gate.K, np.float32)
+        ids = np.empty(k, np.int32)
+        scores = np.empty(k, np.float32)
+        self._check("spq4k_beast_moe_forward_host", self.lib.spq4k_beast_moe_forward_host(
+            self.handle, gate.handle, up.handle, down.handle, logits.ctypes.data, top_k, hidden.ctypes.data,
+            out.ctypes.data, ids.ctypes.data, scores.ctypes.data))
+        return out, ids, scores
+
+    def beast_moe_forward_dev(self, gate: Weights, up: Weights, down: Weights, logits_dev: int, top_k: int,
+                              hidden_dev: int, out_dev: int, ids_dev: int = 0, scores_dev: int = 0):
+        """spq4k_beast_moe_forward on device pointers (ids / scores optional)."""
+        self._check("spq4k_beast_moe_forward", self.lib.spq4k_beast_moe_forward(
+            self.handle, gate.handle, up.handle, down.handle, logits_dev, top_k, hidden_dev, out_dev,
+            ids_dev or None, scores_dev or None))
 
     def moe_ffn_dev(self, gate: Weights, up: Weights, down: Weights, ids_dev: int, w_dev: int, n_used: int, T: int,
                     X_dev: int, Y_dev: int):

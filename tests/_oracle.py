@@ -519,12 +519,38 @@ class BeastRef:
         self.L = C.CDLL(path)
         self.L.ref_beast_matvec.argtypes = [V, C.c_uint, V, V, I, I]
         self.L.ref_beast_matvec.restype = I
+        self.L.ref_beast_route.argtypes = [V, I, I, V, V]
+        self.L.ref_beast_route.restype = I
+        self.L.ref_beast_moe.argtypes = [V, V, V, C.c_uint, I, I, I, V, I, V, V, V, V]
+        self.L.ref_beast_moe.restype = I
 
     def matvec(self, qtype, W, M, K, x):
         x = np.ascontiguousarray(x, np.float32).ravel()
         y = np.empty(M, np.float32)
         assert self.L.ref_beast_matvec(_p(np.ascontiguousarray(W)), qtype, _p(x), _p(y), M, K) == 0
         return y
+
+    def route(self, logits, top_k):
+        """sp_beast_route_experts (:385-443): expert ids and renormalised scores"""
+        logits = np.ascontiguousarray(logits, np.float32).ravel()
+        ids = np.empty(logits.size, np.int32)          # the routing selects at most every expert
+        scores = np.empty(logits.size, np.float32)
+        n = self.L.ref_beast_route(_p(logits), logits.size, top_k, _p(ids), _p(scores))
+        assert n > 0
+        return ids[:n].copy(), scores[:n].copy()
+
+    def moe(self, qtype, gate, up, down, E, n_embd, n_ff, logits, top_k, hidden):
+        """sp_beast_moe_forward (:455-562) on contiguous expert banks: output, ids, scores"""
+        logits = np.ascontiguousarray(logits, np.float32).ravel()
+        hidden = np.ascontiguousarray(hidden, np.float32).ravel()
+        out = np.empty(n_embd, np.float32)
+        ids = np.empty(E, np.int32)
+        scores = np.empty(E, np.float32)
+        n = self.L.ref_beast_moe(_p(np.ascontiguousarray(gate)), _p(np.ascontiguousarray(up)),
+                                 _p(np.ascontiguousarray(down)), qtype, E, n_embd, n_ff, _p(logits), top_k,
+                                 _p(hidden), _p(out), _p(ids), _p(scores))
+        assert n > 0
+        return out, ids[:n].copy(), scores[:n].copy()
 
 
 def close_enough(a, b, rel=1e-4, abs_=1e-5):

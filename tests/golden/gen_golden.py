@@ -264,11 +264,49 @@ def gen_dq(ref, rng):
     return out
 
 
+def gen_beast_moe(ref, rng):
+    """The reference's BurnHard routing (sp_beast_route_experts) and MoE forward
+    (sp_beast_moe_forward's loop over beast_matvec and beast_silu_mul), built
+    into oracle/_ref/beast: routing of logits with distinct values, ties and
+    -inf, and one small forward over Q4_K banks. (A NaN logit makes the
+    reference select index -1, outside its arrays: not a case to match.)"""
+    from _oracle import BeastRef, TYPE_Q4_K
+    beast = BeastRef()
+    out = {}
+    cases = [rng.standard_normal(16).astype(np.float32),
+             np.array([0.5, 2.0, 2.0, -1.0, 2.0, 0.0, 1.5, 2.0], np.float32),
+             np.array([1.0, -np.inf, 3.0, 2.0, 3.0, -np.inf], np.float32),
+             (rng.standard_normal(128) * 3.0).astype(np.float32)]
+    for i, (l, k) in enumerate(zip(cases, (4, 3, 2, 8))):
+        ids, sc = beast.route(l, k)
+        out[f"route{i}_logits"], out[f"route{i}_k"] = l, np.int32(k)
+        out[f"route{i}_ids"], out[f"route{i}_scores"] = ids, sc
+    E, k, n_embd, n_ff = 4, 2, 256, 256
+    banks = {}
+    for name, M, K in (("gate", n_ff, n_embd), ("up", n_ff, n_embd), ("down", n_embd, n_ff)):
+        w = (rng.standard_normal((E * M, K)) * 0.05).astype(np.float32)
+        banks[name] = ref.quantize_type(TYPE_Q4_K, w, E * M, K)
+    logits = rng.standard_normal(E).astype(np.float32)
+    hidden = rng.standard_normal(n_embd).astype(np.float32)
+    y, ids, sc = beast.moe(TYPE_Q4_K, banks["gate"], banks["up"], banks["down"], E, n_embd, n_ff, logits, k, hidden)
+    for name, b in banks.items():
+        out[f"moe_{name}"] = b
+    out["moe_shape"] = np.array([E, k, n_embd, n_ff], np.int32)
+    out["moe_logits"], out["moe_hidden"] = logits, hidden
+    out["moe_y"], out["moe_ids"], out["moe_scores"] = y, ids, sc
+    return out
+
+
 def main():
     if ref_library_path() is None:
         sys.exit("oracle/_ref is not built (make -C oracle ref)")
-    which = set(sys.argv[1:]) or {"q4k", "q5k", "q6k", "q8_0", "dq"}
+    which = set(sys.argv[1:]) or {"q4k", "q5k", "q6k", "q8_0", "dq", "beast_moe"}
     ref = Ref()
+    if "beast_moe" in which:
+        out = gen_beast_moe(ref, np.random.default_rng(0xBEA5))
+        path = os.path.join(HERE, "beast_moe_golden.npz")
+        np.savez_compressed(path, **out)
+        print(f"wrote {path} ({os.path.getsize(path)/1024:.0f} KiB, {len(out)} arrays) using {ref.path}")
     if "dq" in which:
         out = gen_dq(ref, np.random.default_rng(0xD0D0))
         path = os.path.join(HERE, "dq_golden.npz")

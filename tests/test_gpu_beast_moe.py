@@ -1,0 +1,116 @@
+"""GPU parity of the BurnHard MoE forward (spq4k_beast_moe_forward,
+include/spq4k.h) with the reference's own sp_beast_route_experts and
+sp_beast_moe_forward loop (desktop/beast_canyon/sp_beast_canyon.c:385-443,
+:455-562), built from its source into oracle/_ref/beast, and with the golden
+vectors that build wrote (tests/golden/beast_moe_golden.npz).
+
+The routing is the reference's: the same experts in the same order; scores
+within 2e-6 (expf on the GPU and in libm may differ in the last place). The
+output is the score-weighted sum of beast_matvec's dequant-then-dot (fp32
+activations, no Q8_K), whose fp32 sums the GPU takes per lane and across the
+wave where the reference adds serially: element-wise within close_enough
+(1e-4 relative or 1e-5 absolute, tests/desktop/test_sp_kernels.cpp:34-48)."""
+import os
+
+import numpy as np
+import pytest
+
+from _oracle import BEAST_SO, TYPE_Q4_K, BeastRef, close_enough
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+G = np.load(os.path.join(HERE, "golden", "beast_moe_golden.npz"))
+
+
+def _check(got, exp, what):
+    ok = close_enough(got, exp)
+    assert ok.all(), f"{what}: {int((~ok).sum())}/{ok.size} outside tolerance, first {np.argwhere(~ok)[0]}"
+
+
+def test_beast_moe_golden(ctx):
+    E, k, n_embd, n_ff = (int(v) for v in G["moe_shape"])
+    gate = ctx.upload(G["moe_gate"], n_ff, n_embd, E=E)
+    up = ctx.upload(G["moe_up"], n_ff, n_embd, E=E)
+    down = ctx.upload(G["moe_down"], n_embd, n_ff, E=E)
+    y, ids, sc = ctx.beast_moe_forward(gate, up, down, G["moe_logits"], k, G["moe_hidden"])
+    assert np.array_equal(ids, G["moe_ids"])
+    np.testing.assert_allclose(sc, G["moe_scores"], rtol=2e-6)
+    _check(y, G["moe_y"], "golden forward")
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_beast_route_golden(ctx, case):
+    """the routing of the golden logits (ties, -inf, 128 experts) through a
+    forward over small banks of as many experts"""
+    l, k = G[f"route{case}_logits"], int(G[f"route{case}_k"])
+    E, n = l.size, 256
+    rng = np.random.default_rng(case)
+    from _oracle import Oracle
+    o = Oracle()
+    banks = [ctx.upload(o.quantize_q4K((rng.standard_normal((E * n, n)) * 0.05).astype(np.float32)), n, n, E=E)
+             for _ in range(3)]
+    _, ids, sc = ctx.beast_moe_forward(*banks, l, k, rng.standard_normal(n).astype(np.float32))
+    assert np.array_equal(ids, G[f"route{case}_ids"])
+    np.testing.assert_allclose(sc, G[f"route{case}_scores"], rtol=2e-6)
+    for b in banks:
+        b.free()
+
+
+@pytest.mark.skipif(not os.path.exists(BEAST_SO), reason="oracle/_ref/beast (the reference) not built")
+@pytest.mark.parametrize("E,k,n_embd,n_ff", [(32, 8, 2048, 768), (16, 2, 1024, 512), (8, 0, 512, 256),
+                                             (6, 9, 256, 1024), (8, 4, 4096, 1536)])
+def test_beast_moe_vs_reference(ctx, oracle, E, k, n_embd, n_ff):
+    """the forward against the reference's own build: the 30B-A3B widths
+    (top-8, 2048 -> 768 -> 2048) over 32 experts, the default top-2 (k = 0),
+    k above E (every expert), and 4096-wide rows"""
+    b = BeastRef()
+    rng = np.random.default_rng(E * 7 + k + n_embd)
+
+    def bank(rows, cols):
+        return oracle.quantize_q4K(rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.03))
+
+    Wg, Wu, Wd = bank(E * n_ff, n_embd), bank(E * n_ff, n_embd), bank(E * n_embd, n_ff)
+    logits = (rng.standard_normal(E) * 2.0).astype(np.float32)
+    hidden = rng.standard_normal(n_embd).astype(np.float32)
+    y_ref, ids_ref, sc_ref = b.moe(TYPE_Q4_K, Wg, Wu, Wd, E, n_embd, n_ff, logits, k, hidden)
+    gate, up = ctx.upload(Wg, n_ff, n_embd, E=E), ctx.upload(Wu, n_ff, n_embd, E=E)
+    down = ctx.upload(Wd, n_embd, n_ff, E=E)
+    y, ids, sc = ctx.beast_moe_forward(gate, up, down, logits, k, hidden)
+    assert np.array_equal(ids, ids_ref), f"experts {ids} against {ids_ref}"
+    np.testing.assert_allclose(sc, sc_ref, rtol=2e-6)
+    _check(y, y_ref, f"E={E} k={k} {n_embd}->{n_ff}")
+    for w in (gate, up, down):
+        w.free()
+
+
+def test_beast_moe_device_pointers_and_rejects(ctx):
+    """the device entry point leaves ids / scores alone when not asked, and
+    refuses banks of another type or shape"""
+    import spq4k
+    from spq4k.hip import DeviceArray
+    E, n = 4, 256
+    rng = np.random.default_rng(5)
+    from _oracle import Oracle
+    o = Oracle()
+    W = [o.quantize_q4K((rng.standard_normal((E * n, n)) * 0.05).astype(np.float32)) for _ in range(3)]
+    banks = [ctx.upload(w, n, n, E=E) for w in W]
+    logits = np.array([0.1, 2.0, -1.0, 1.5], np.float32)
+    hidden = rng.standard_normal(n).astype(np.float32)
+    y_host, ids_host, _ = ctx.beast_moe_forward(*banks, logits, 2, hidden)
+    ld, hd, od = DeviceArray.from_host(logits), DeviceArray.from_host(hidden), DeviceArray(n, np.float32)
+    ctx.beast_moe_forward_dev(*banks, ld.ptr, 2, hd.ptr, od.ptr)
+    ctx.synchronize()
+    assert np.array_equal(od.to_host().view(np.uint32), y_host.view(np.uint32))
+    assert ids_host.tolist() == [1, 3]
+    q6 = ctx.upload(o.quantize_q6K((rng.standard_normal((E * n, n)) * 0.05).astype(np.float32)), n, n, E=E,
+                    type=14)
+    with pytest.raises(spq4k.Spq4kError):
+        ctx.beast_moe_forward(q6, banks[1], banks[2], logits, 2, hidden)
+    wide = ctx.upload(o.quantize_q4K((rng.standard_normal((E * n, 2 * n)) * 0.05).astype(np.float32)), n, 2 * n,
+                      E=E)
+    with pytest.raises(spq4k.Spq4kError):
+        ctx.beast_moe_forward(banks[0], banks[1], wide, logits, 2, hidden)
+    for w in banks + [q6, wide]:
+        w.free()
+    for d in (ld, hd, od):
+        d.free()
