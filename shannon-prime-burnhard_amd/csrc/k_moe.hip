@@ -384,7 +384,19 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
         store_q8_item(r, valid, item, L);
     }
     __syncthreads();
-    for (int r = g0; r < r1; r += RPG) {
+    // passes of the workgroup's rows (uniform: every lane's next pass is
+    // loaded while this one is computed; a lane whose next row lies past r1
+    // loads row r1 - 1 again and drops it)
+    const int npass = (r1 - r0 + RPG - 1) / RPG;
+    for (int pass = 0, r = g0; pass < npass; ++pass, r += RPG) {
+        Loc nxt = cur;
+        W wn[NIT];
+        W wn1[GLU ? NIT : 1];
+        const bool more = pass + 1 < npass;
+        if (more) {
+            nxt = locate(r + RPG);
+            load(nxt, wn, wn1);
+        }
         float acc[1] = {0.0f};
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
@@ -401,10 +413,15 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
             }
             sum = moe_silu(sum) * group_sum_last<LPR>(acc1[0]);
         }
-        if (cur.e >= 0 && (lane & (LPR - 1)) == LPR - 1) *cur.y = sum;
-        if (r + RPG < r1) {
-            cur = locate(r + RPG);
-            load(cur, w, w1);
+        if (r < r1 && cur.e >= 0 && (lane & (LPR - 1)) == LPR - 1) *cur.y = sum;
+        if (more) {
+            cur = nxt;
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) w[it] = wn[it];
+            if constexpr (GLU) {
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) w1[it] = wn1[it];
+            }
         }
     }
 }
@@ -442,24 +459,27 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_sum_kernel(MoeFusedParams
     const int nitems = ((u1 - 1) / M - tlo + 1) * nu * NB;
     const Q8Lds L = q8lds_carve(smem, p.xwin_rows * NB);
     const float* __restrict__ X = p.X + (int64_t)tlo * nu * p.K;
-    for (int base = 0; base < nitems; base += 4 * WAVES) {
-        const int item0 = base + wave * 4 + (lane >> 4);
-        const bool valid = item0 < nitems;
-        const int item = valid ? item0 : nitems - 1;
-        const XRegs r = load_x16(X, p.K, item / NB, item % NB);
-        store_q8_item(r, valid, item, L);
-    }
-    __syncthreads();
     const size_t row_bytes = (size_t)NB * Fmt::BYTES;
-    for (int u = u0 + wave; u < u1; u += WAVES) {
-        const int t = u / M;
-        const int r = u - t * M;
-        W w[SPG][NIT];
-        bool live[SPG];
+    // a unit's expert ids and router weights, every load unconditional (a
+    // slot past n_used reads the last one and is dropped, a unit past u1 the
+    // last unit), so that no load waits behind another's branch
+    auto fetch_ids = [&](int u, int (&ev)[SPG], float (&cws)[SPG * GPW]) {
+        const int tu = __builtin_amdgcn_readfirstlane((u < u1 ? u : u1 - 1) / M);
 #pragma unroll
         for (int k = 0; k < SPG; ++k) {
             const int s = grp + GPW * k;
-            const int e = s < nu ? p.ids[t * nu + s] : -1;
+            ev[k] = p.ids[tu * nu + (s < nu ? s : nu - 1)];
+        }
+#pragma unroll
+        for (int s = 0; s < SPG * GPW; ++s) cws[s] = cw[tu * nu + (s < nu ? s : nu - 1)];
+    };
+    auto fetch_w = [&](int u, const int (&ev)[SPG], W (&w)[SPG][NIT], bool (&live)[SPG]) {
+        const int uc = u < u1 ? u : u1 - 1;
+        const int r = uc - (uc / M) * M;
+#pragma unroll
+        for (int k = 0; k < SPG; ++k) {
+            const int s = grp + GPW * k;
+            const int e = s < nu ? ev[k] : -1;
             live[k] = e >= 0 && e < p.E;
             const uint8_t* wr = p.bank + (size_t)(live[k] ? e : 0) * p.expert_bytes + (size_t)r * row_bytes;
 #pragma unroll
@@ -468,6 +488,46 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_sum_kernel(MoeFusedParams
                 w[k][it] = Fmt::load(wr + (size_t)(bb < NB ? bb : NB - 1) * Fmt::BYTES, l4);
             }
         }
+    };
+    // order of the loads (they complete in order): the first unit's ids, the
+    // first pass of hidden rows, then the unit's weights, so that the
+    // quantisation waits only for x while the weights are in flight
+    int u = u0 + wave;
+    int ev[SPG];
+    float cws[SPG * GPW];
+    W w[SPG][NIT];
+    bool live[SPG];
+    fetch_ids(u, ev, cws);
+    {
+        const int item0 = wave * 4 + (lane >> 4);
+        const int item = item0 < nitems ? item0 : nitems - 1;
+        const XRegs xr = load_x16(X, p.K, item / NB, item % NB);
+        fetch_w(u, ev, w, live);
+        store_q8_item(xr, item0 < nitems, item, L);
+    }
+    for (int base = 4 * WAVES; base < nitems; base += 4 * WAVES) {
+        const int item0 = base + wave * 4 + (lane >> 4);
+        const bool valid = item0 < nitems;
+        const int item = valid ? item0 : nitems - 1;
+        const XRegs r = load_x16(X, p.K, item / NB, item % NB);
+        store_q8_item(r, valid, item, L);
+    }
+    __syncthreads();
+    for (; u < u1; u += WAVES) {
+        const int t = u / M;
+        const int r = u - t * M;
+        // the wave's next unit (u is uniform over the wave) in flight while
+        // this one is computed
+        int evn[SPG];
+        float cwn[SPG * GPW];
+        W wn[SPG][NIT];
+        bool liven[SPG];
+        const bool more = u + WAVES < u1;
+        if (more) {
+            fetch_ids(u + WAVES, evn, cwn);
+            fetch_w(u + WAVES, evn, wn, liven);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         float d[SPG];
 #pragma unroll
         for (int k = 0; k < SPG; ++k) {
@@ -490,11 +550,22 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_sum_kernel(MoeFusedParams
                 const int s = k * GPW + g;
                 const float ds = __shfl(d[k], g * LPR + LPR - 1, 64);
                 if (s < nu) {
-                    const float prod = ds * cw[t * nu + s];
+                    const float prod = ds * cws[s];
                     sum += (double)prod;
                 }
             }
         if (lane == 63) Yc[(int64_t)t * M + r] = (float)sum;
+        if (more) {
+#pragma unroll
+            for (int k = 0; k < SPG; ++k) {
+                ev[k] = evn[k];
+                live[k] = liven[k];
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) w[k][it] = wn[k][it];
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < SPG * GPW; ++s2) cws[s2] = cwn[s2];
+        }
     }
 }
 
