@@ -49,7 +49,8 @@ def _csv(d, suffix):
                                                                  recursive=True)
     if not files:
         raise FileNotFoundError(f"no *{suffix} in {d}")
-    with open(files[0]) as f:
+    files.sort(key=os.path.getmtime)          # a directory reused across runs: the latest run's file
+    with open(files[-1]) as f:
         return list(csv.DictReader(f))
 
 
@@ -108,6 +109,7 @@ def stats_table(d, out, title, commands):
         for (name, grid, wg), v in groups.items():
             name = name.replace("spq4k::", "").replace("(spq4k::GemmParams)", "").replace(
                 "(spq4k::MoeParams)", "").replace("(spq4k::MoeFusedParams)", "").replace("(spq4k::GemvParams)", "")
+            name = name.replace("(anonymous namespace)::", "")
             if "(" in name:
                 name = name[:name.index("(")]
             f.write(f"| `{name}` | {grid} | {wg} | {len(v)} | {statistics.mean(v):.2f} | {min(v):.2f} | "
