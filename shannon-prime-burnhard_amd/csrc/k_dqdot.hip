@@ -143,6 +143,147 @@ __global__ __launch_bounds__(256) void dequant_matvec_kernel(const uint8_t* __re
     }
 }
 
+// Rows of at most 16 blocks (K, n_embd or n_ff up to 4096): LPR lanes a
+// weight row (4 a block, rounded up to a power of two), 64 / LPR rows side by
+// side in a wave. The activations are staged in LDS, float4 j of lane ll of a row at
+// j * LPR + ll (a row's lanes read consecutive 16-byte words, the rows of a
+// wave the same ones), with their loads issued ahead of the weights' and each
+// wave's weight loads all in flight before its first product. Products and
+// sums per lane are dq_block's.
+
+// x of nb blocks into the staging layout, from values a thread loaded:
+// float4 e4 of x (value 4 e4) is float4 (e4 & 15) of lane 4 (e4 >> 6) + ((e4 >> 4) & 3)
+template <int LPR>
+__device__ __forceinline__ void dq_stage_put(f32x4* xs, int e4, const f32x4& v) {
+    xs[(e4 & 15) * LPR + 4 * (e4 >> 6) + ((e4 >> 4) & 3)] = v;
+}
+
+// N rows' products at once, each against its own staged x (xl[n]), their
+// sums interleaved so that a lone wave on its SIMD has N independent chains;
+// each row's products and sum are dq_block's. Returns each row's sum in the
+// last lane of its group.
+template <int LPR, int N>
+__device__ __forceinline__ void dq_dots_lds(const DqRow (&w)[N], int l4, int bsub, int nb, const lf32x4* const (&xl)[N],
+                                            int ll, float (&out)[N]) {
+    float acc[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) acc[n] = 0.0f;
+    if (bsub < nb) {
+        float dd[N][2], mm[N][2];
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+            const float d = half_bits_to_float(w[n].h.x & 0xFFFFu);
+            const float dmin = half_bits_to_float(w[n].h.x >> 16);
+            const ScaleMin sm = unpack_scale_min(w[n].h.y, w[n].h.z, w[n].h.w);
+            const uint32_t scw = l4 < 2 ? sm.sc_lo : sm.sc_hi;
+            const uint32_t mw = l4 < 2 ? sm.m_lo : sm.m_hi;
+            const int sh = 16 * (l4 & 1);
+            dd[n][0] = d * (float)((scw >> sh) & 0xFFu);
+            mm[n][0] = dmin * (float)((mw >> sh) & 0xFFu);
+            dd[n][1] = d * (float)((scw >> (sh + 8)) & 0xFFu);
+            mm[n][1] = dmin * (float)((mw >> (sh + 8)) & 0xFFu);
+        }
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+#pragma unroll
+            for (int i4 = 0; i4 < 8; ++i4) {
+#pragma unroll
+                for (int n = 0; n < N; ++n) {
+                    const uint32_t qw = i4 < 4 ? (&w[n].qa.x)[i4] : (&w[n].qb.x)[i4 - 4];
+                    uint32_t qn = (half ? qw_hi(qw) : qw) & 0x0F0F0F0Fu;
+                    asm volatile("" : "+v"(qn));
+                    const f32x4 x = xl[n][(8 * half + i4) * LPR + ll];
+                    float wv[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        wv[k] = __builtin_fmaf(dd[n][half], (float)((qn >> (8 * k)) & 0xFFu), -mm[n][half]);
+                    float a = acc[n];
+                    a = a + wv[0] * x.x;
+                    a = a + wv[1] * x.y;
+                    a = a + wv[2] * x.z;
+                    a = a + wv[3] * x.w;
+                    acc[n] = a;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) out[n] = group_sum_last<LPR>(acc[n]);
+}
+
+// One token, rows of at most 16 blocks (K <= 4096): LPR = 4 nb rounded up to
+// a power of two lanes a row, 64 / LPR rows side by side in a wave, R steps a
+// wave; x staged once a workgroup (float4 j of lane ll at j * LPR + ll), every
+// weight load of a wave issued before its first product and the R rows' sums
+// interleaved. The lane arithmetic and the reduction are
+// dequant_matvec_kernel's, so the outputs are the same bit for bit.
+template <int LPR, int R>
+__global__ __launch_bounds__(256) void dequant_matvec_short_kernel(const uint8_t* __restrict__ W, int M, int nb,
+                                                                   const float* __restrict__ X,
+                                                                   float* __restrict__ Y) {
+    constexpr int RW = 64 / LPR;
+    __shared__ f32x4 xs[16 * LPR];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane / LPR, ll = lane % LPR;
+    const int l4 = ll & 3, bsub = ll >> 2;
+    const int row0 = (blockIdx.x * 4 + wave) * RW * R + grp;   // this lane group's first row; then + RW each step
+    const size_t row_bytes = (size_t)nb * Q4K_BYTES;
+    // x loads first (unconditional: past the row's end they read its last float4)
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(X);
+    f32x4 xr[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int e4 = threadIdx.x + 256 * k;
+        xr[k] = x4[e4 < nb * 64 ? e4 : nb * 64 - 1];
+    }
+    DqRow w[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int r = row0 + u * RW;
+        w[u] = dq_load(W + (size_t)(r < M ? r : M - 1) * row_bytes, nb, bsub, l4, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int e4 = threadIdx.x + 256 * k;
+        if (e4 < nb * 64) dq_stage_put<LPR>(xs, e4, xr[k]);
+    }
+    __syncthreads();
+    const lf32x4* xl[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) xl[u] = (const lf32x4*)xs;
+    float d[R];
+    dq_dots_lds<LPR, R>(w, l4, bsub, nb, xl, ll, d);
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int r = row0 + u * RW;
+        if (ll == LPR - 1 && r < M) Y[r] = d[u];
+    }
+}
+
+template <int LPR, int R>
+hipError_t launch_dq_short(const uint8_t* W, int M, int nb, const float* X, float* Y, hipStream_t st) {
+    constexpr int per_wg = 4 * (64 / LPR) * R;
+    hipLaunchKernelGGL((dequant_matvec_short_kernel<LPR, R>), dim3((unsigned)((M + per_wg - 1) / per_wg)), dim3(256), 0,
+                       st, W, M, nb, X, Y);
+    return hipGetLastError();
+}
+
+// R (rows a lane group takes) in {1, 2, 4}: the largest that still leaves at
+// least two workgroups a CU (the launch is a latency chain: a lone wave on its
+// SIMD waits out its loads however many rows it interleaves; measured on
+// 4096 x 4096: 5.9 us with R = 1 or 2, 7.5 us with R = 4)
+template <int LPR>
+hipError_t launch_dq_short_r(const uint8_t* W, int M, int nb, const float* X, float* Y, int num_cus,
+                             hipStream_t st) {
+    int best = 1;
+    for (int r = 2; r <= 4; r *= 2) {
+        const int64_t per = 4LL * (64 / LPR) * r;
+        if ((M + per - 1) / per >= 2LL * num_cus) best = r;
+    }
+    if (best == 4) return launch_dq_short<LPR, 4>(W, M, nb, X, Y, st);
+    if (best == 2) return launch_dq_short<LPR, 2>(W, M, nb, X, Y, st);
+    return launch_dq_short<LPR, 1>(W, M, nb, X, Y, st);
+}
+
 template <int T>
 hipError_t launch_dq_t(const uint8_t* W, int M, int nb, const float* X, int64_t x_tstride, float* Y,
                        int64_t y_tstride, int grid, int rows_per_wg, size_t lds, hipStream_t st) {
@@ -185,12 +326,6 @@ __device__ __forceinline__ float dq_row_dot(const uint8_t* __restrict__ row, int
     return __shfl(s, 63, 64);
 }
 
-// sp_beast_route_experts (:385-443) in one wave: the largest logit (NaNs
-// skipped, -1e30 when none), exp_i = expf(l_i - max), their fp32 sum in index
-// order, score_i = exp_i / sum; top_k rounds, each taking the unselected
-// expert of the largest score (the lowest index among equal ones, as the
-// reference's strictly-greater scan); the chosen scores renormalised by
-// 1 / (their fp32 sum in rank order) when that sum is positive.
 // A candidate (score, index) as one 64-bit key that orders as the selection
 // does: a score is >= +0 (an exp over a positive sum), whose bits order as
 // its value, in the high word; 0xFFFFFFFF - index in the low word, so that of
@@ -209,6 +344,12 @@ __device__ __forceinline__ uint64_t route_max_dpp(uint64_t k) {
     return o > k ? o : k;
 }
 
+// sp_beast_route_experts (:385-443) in one wave: the largest logit (NaNs
+// skipped, -1e30 when none), exp_i = expf(l_i - max), their fp32 sum in index
+// order, score_i = exp_i / sum; top_k rounds, each taking the unselected
+// expert of the largest score (the lowest index among equal ones, as the
+// reference's strictly-greater scan); the chosen scores renormalised by
+// 1 / (their fp32 sum in rank order) when that sum is positive.
 __global__ __launch_bounds__(64) void beast_route_kernel(const float* __restrict__ logits, int E, int top_k,
                                                          int32_t* __restrict__ ids, float* __restrict__ scores) {
     // E exps for lane 0's sum in index order, then (E > 256) the keys of
@@ -386,74 +527,6 @@ __global__ __launch_bounds__(256) void beast_down_sum_kernel(const uint8_t* __re
         const int i = r0 + wave + 4 * j;
         if (i < r1 && lane == 0) out[i] = acc[j];
     }
-}
-
-// Rows of at most 16 blocks (n_embd or n_ff up to 4096): LPR lanes a weight
-// row (4 a block, rounded up to a power of two), 64 / LPR rows side by side in
-// a wave. The activations are staged in LDS, float4 j of lane ll of a row at
-// j * LPR + ll (a row's lanes read consecutive 16-byte words, the rows of a
-// wave the same ones), with their loads issued ahead of the weights' and each
-// wave's weight loads all in flight before its first product. Products and
-// sums per lane are dq_block's.
-
-// x of nb blocks into the staging layout, from values a thread loaded:
-// float4 e4 of x (value 4 e4) is float4 (e4 & 15) of lane 4 (e4 >> 6) + ((e4 >> 4) & 3)
-template <int LPR>
-__device__ __forceinline__ void dq_stage_put(f32x4* xs, int e4, const f32x4& v) {
-    xs[(e4 & 15) * LPR + 4 * (e4 >> 6) + ((e4 >> 4) & 3)] = v;
-}
-
-// N rows' products at once, each against its own staged x (xl[n]), their
-// sums interleaved so that a lone wave on its SIMD has N independent chains;
-// each row's products and sum are dq_block's. Returns each row's sum in the
-// last lane of its group.
-template <int LPR, int N>
-__device__ __forceinline__ void dq_dots_lds(const DqRow (&w)[N], int l4, int bsub, int nb, const lf32x4* const (&xl)[N],
-                                            int ll, float (&out)[N]) {
-    float acc[N];
-#pragma unroll
-    for (int n = 0; n < N; ++n) acc[n] = 0.0f;
-    if (bsub < nb) {
-        float dd[N][2], mm[N][2];
-#pragma unroll
-        for (int n = 0; n < N; ++n) {
-            const float d = half_bits_to_float(w[n].h.x & 0xFFFFu);
-            const float dmin = half_bits_to_float(w[n].h.x >> 16);
-            const ScaleMin sm = unpack_scale_min(w[n].h.y, w[n].h.z, w[n].h.w);
-            const uint32_t scw = l4 < 2 ? sm.sc_lo : sm.sc_hi;
-            const uint32_t mw = l4 < 2 ? sm.m_lo : sm.m_hi;
-            const int sh = 16 * (l4 & 1);
-            dd[n][0] = d * (float)((scw >> sh) & 0xFFu);
-            mm[n][0] = dmin * (float)((mw >> sh) & 0xFFu);
-            dd[n][1] = d * (float)((scw >> (sh + 8)) & 0xFFu);
-            mm[n][1] = dmin * (float)((mw >> (sh + 8)) & 0xFFu);
-        }
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-#pragma unroll
-            for (int i4 = 0; i4 < 8; ++i4) {
-#pragma unroll
-                for (int n = 0; n < N; ++n) {
-                    const uint32_t qw = i4 < 4 ? (&w[n].qa.x)[i4] : (&w[n].qb.x)[i4 - 4];
-                    uint32_t qn = (half ? qw_hi(qw) : qw) & 0x0F0F0F0Fu;
-                    asm volatile("" : "+v"(qn));
-                    const f32x4 x = xl[n][(8 * half + i4) * LPR + ll];
-                    float wv[4];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        wv[k] = __builtin_fmaf(dd[n][half], (float)((qn >> (8 * k)) & 0xFFu), -mm[n][half]);
-                    float a = acc[n];
-                    a = a + wv[0] * x.x;
-                    a = a + wv[1] * x.y;
-                    a = a + wv[2] * x.z;
-                    a = a + wv[3] * x.w;
-                    acc[n] = a;
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int n = 0; n < N; ++n) out[n] = group_sum_last<LPR>(acc[n]);
 }
 
 // The routing of sp_beast_route_experts (:385-443) by a workgroup of 256
@@ -905,6 +978,13 @@ hipError_t launch_dequant_matvec(const uint8_t* W, int M, int nb, const float* X
     if (M <= 0 || nb <= 0 || T < 1 || T > DQ_MATVEC_MAX_T) return hipErrorInvalidValue;
     const size_t lds = dequant_matvec_lds_bytes(T, nb);
     if (lds > DQ_MATVEC_LDS_MAX) return hipErrorInvalidValue;
+    if (T == 1 && nb <= 16) {
+        if (nb <= 1) return launch_dq_short_r<4>(W, M, nb, X, Y, num_cus, st);
+        if (nb <= 2) return launch_dq_short_r<8>(W, M, nb, X, Y, num_cus, st);
+        if (nb <= 4) return launch_dq_short_r<16>(W, M, nb, X, Y, num_cus, st);
+        if (nb <= 8) return launch_dq_short_r<32>(W, M, nb, X, Y, num_cus, st);
+        return launch_dq_short_r<64>(W, M, nb, X, Y, num_cus, st);
+    }
     // about four workgroups a CU, each a contiguous range of rows (a multiple of its four waves)
     int64_t want = (int64_t)num_cus * 4;
     int64_t rows_per_wg = ((int64_t)M + want - 1) / want;

@@ -53,8 +53,25 @@ def test_dequant_matvec_one_hot_is_dequant(ctx, oracle):
     w.free()
 
 
+@pytest.mark.parametrize("K", [256, 512, 1024, 3072, 4096])
+def test_dequant_matvec_one_hot_one_token(ctx, oracle, K):
+    """one token with rows of at most 16 blocks (the one-token kernel, every
+    lane count): one-hot activations give the dequantised weights bit for bit"""
+    M = 333
+    w, wb = _weights(ctx, M, K, 11 + K)
+    deq = oracle.dequant(wb, M * K).reshape(M, K)
+    for c in (0, 33, K // 2 + 5, K - 1):
+        x = np.zeros((1, K), np.float32)
+        x[0, c] = 1.0
+        got = ctx.dequant_matvec(w, x)
+        assert np.array_equal(got[0].view(np.uint32), np.ascontiguousarray(deq[:, c]).view(np.uint32)), f"K={K} col {c}"
+    w.free()
+
+
 @pytest.mark.parametrize("M,K,T,dist", [(4096, 4096, 1, 0), (256, 12288, 1, 0), (300, 2048, 3, 0), (768, 2048, 1, 0),
-                                        (2048, 768, 8, 0), (96, 27648, 1, 1), (512, 5120, 4, 1), (40, 4352, 11, 0)])
+                                        (2048, 768, 8, 0), (96, 27648, 1, 1), (512, 5120, 4, 1), (40, 4352, 11, 0),
+                                        (12288, 4096, 1, 1), (1001, 256, 1, 0), (37, 1024, 1, 0), (5000, 3072, 1, 0),
+                                        (130, 512, 1, 1)])
 def test_dequant_matvec_vs_beast(ctx, oracle, M, K, T, dist):
     rng = np.random.default_rng(M + K + T)
     w, wb = _weights(ctx, M, K, 7 + T, dist, 8.0 if dist else 1.0)
