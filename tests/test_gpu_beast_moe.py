@@ -75,11 +75,13 @@ def test_beast_route_golden(ctx, case):
 
 
 @pytest.mark.skipif(not os.path.exists(BEAST_SO), reason="oracle/_ref/beast (the reference) not built")
-@pytest.mark.parametrize("E,k", [(300, 16), (1000, 9), (4096, 16), (257, 3)])
-def test_beast_route_many_experts(ctx, E, k):
-    """routings of more than 256 experts (the candidates past the fourth a
-    lane kept in LDS) against the reference's own sp_beast_route_experts:
-    runs of equal logits, -inf logits, the largest logit at the last index"""
+@pytest.mark.parametrize("E,k,n_embd", [(300, 16, 256), (1000, 9, 256), (4096, 16, 256), (257, 3, 256),
+                                        (4096, 16, 2304)])
+def test_beast_route_many_experts(ctx, E, k, n_embd):
+    """routings of more than 256 experts against the reference's own
+    sp_beast_route_experts: runs of equal logits, -inf logits, the largest
+    logit at the last index; 4096 experts beside 2304-wide rows take more than
+    64 KB of LDS in the routing launch"""
     rng = np.random.default_rng(E + k)
     logits = (rng.standard_normal(E) * 3.0).astype(np.float32)
     logits[rng.choice(E, E // 10, replace=False)] = -np.inf
@@ -87,9 +89,10 @@ def test_beast_route_many_experts(ctx, E, k):
     logits[tie] = np.float32(logits.max() + 0.5)     # twenty equal top scores, the rank order by index
     logits[-1] = np.float32(logits.max() + 1.0)
     ids_ref, sc_ref = BeastRef().route(logits, k)
-    zero = np.zeros(E * 256 * 144, np.uint8)           # all-zero blocks: the outputs are not checked here
-    banks = [ctx.upload(zero, 256, 256, E=E) for _ in range(3)]
-    _, ids, sc = ctx.beast_moe_forward(*banks, logits, k, np.ones(256, np.float32))
+    zero = np.zeros(E * n_embd * 144, np.uint8)        # all-zero blocks: the outputs are not checked here
+    banks = [ctx.upload(zero, 256, n_embd, E=E), ctx.upload(zero, 256, n_embd, E=E),
+             ctx.upload(zero, n_embd, 256, E=E)]
+    _, ids, sc = ctx.beast_moe_forward(*banks, logits, k, np.ones(n_embd, np.float32))
     assert np.array_equal(ids, ids_ref), f"experts {ids} against {ids_ref}"
     np.testing.assert_allclose(sc, sc_ref, rtol=2e-6)
     for b in banks:
