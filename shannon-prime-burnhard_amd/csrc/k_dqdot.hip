@@ -697,7 +697,7 @@ __global__ __launch_bounds__(256) void beast_route_gate_up_kernel(const uint8_t*
         xr[k] = x4[e4 < nb * 64 ? e4 : nb * 64 - 1];
     }
     beast_route_wg(logits, lg0, E, top_k, L);
-    if (blockIdx.x == 0 && threadIdx.x < top_k) {
+    if (blockIdx.x == 0 && (int)threadIdx.x < top_k) {
         ids[threadIdx.x] = L.sel_id[threadIdx.x];
         scores[threadIdx.x] = L.sel_sc[threadIdx.x];
     }
@@ -777,7 +777,8 @@ __global__ __launch_bounds__(256) void beast_down_short_kernel(const uint8_t* __
         f32x4 hr[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            const int e4 = threadIdx.x + 256 * m < nv ? threadIdx.x + 256 * m : nv - 1;   // unconditional
+            const int e4r = (int)threadIdx.x + 256 * m;
+            const int e4 = e4r < nv ? e4r : nv - 1;   // unconditional
             const int sl = e4 / nb64;
             hr[m] = reinterpret_cast<const f32x4*>(H + (size_t)(s0 + sl) * n_ff)[e4 - sl * nb64];
         }
