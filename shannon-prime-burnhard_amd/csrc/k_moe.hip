@@ -370,11 +370,29 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
     // quantisation waits only for x while the weights are in flight
     const int item_a = wave * 4 + (lane >> 4);
     const int ci_a = item_a < nitems ? item_a : nitems - 1;
-    Loc cur = locate(g0);
+    // passes of the workgroup's rows, DP at a time: the next DP passes are
+    // loaded while these are computed (uniform over the workgroup; a lane
+    // whose row lies past r1 loads row r1 - 1 again and drops it). Two for
+    // the plain sweep of rows of 8 or more blocks; one for the GLU sweep,
+    // whose gate and up rows already double the loads of a pass and whose
+    // registers would allow only one workgroup a CU with two, and for short
+    // rows (the down bank's 3 blocks: measured no faster, one token slower)
+    constexpr int DP = (GLU || NB < 8) ? 1 : 2;
+    const int npass = (r1 - r0 + RPG - 1) / RPG;
+    Loc cur[DP];
+    W w[DP][NIT];
+    W w1[DP][GLU ? NIT : 1];
+    cur[0] = locate(g0);
     const XRegs xa = load_x16(p.X, p.K, xlo + ci_a / NB, ci_a % NB);
-    W w[NIT];
-    W w1[GLU ? NIT : 1];
-    load(cur, w, w1);
+#pragma unroll
+    for (int d = 0; d < DP; ++d) {
+        if (d > 0) {
+            cur[d] = locate(g0 + d * RPG);
+            if (d < npass) load(cur[d], w[d], w1[d]);   // uniform
+        } else {
+            load(cur[d], w[d], w1[d]);
+        }
+    }
     store_q8_item(xa, item_a < nitems, ci_a, L);
     for (int base = 4 * WAVES; base < nitems; base += 4 * WAVES) {
         const int item0 = base + item_a;
@@ -384,43 +402,52 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
         store_q8_item(r, valid, item, L);
     }
     __syncthreads();
-    // passes of the workgroup's rows (uniform: every lane's next pass is
-    // loaded while this one is computed; a lane whose next row lies past r1
-    // loads row r1 - 1 again and drops it)
-    const int npass = (r1 - r0 + RPG - 1) / RPG;
-    for (int pass = 0, r = g0; pass < npass; ++pass, r += RPG) {
-        Loc nxt = cur;
-        W wn[NIT];
-        W wn1[GLU ? NIT : 1];
-        const bool more = pass + 1 < npass;
+    for (int pass = 0; pass < npass; pass += DP) {
+        Loc nxt[DP];
+        W wn[DP][NIT];
+        W wn1[DP][GLU ? NIT : 1];
+        const bool more = pass + DP < npass;
         if (more) {
-            nxt = locate(r + RPG);
-            load(nxt, wn, wn1);
-        }
-        float acc[1] = {0.0f};
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const int bb = bsub + BSL * it;
-            Fmt::template dot<1>(w[it], l4, L, cur.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && cur.e >= 0, acc);
+            for (int d = 0; d < DP; ++d) {
+                nxt[d] = locate(g0 + (pass + DP + d) * RPG);
+                if (pass + DP + d < npass) load(nxt[d], wn[d], wn1[d]);   // uniform
+            }
         }
-        float sum = group_sum_last<LPR>(acc[0]);
-        if constexpr (GLU) {
-            float acc1[1] = {0.0f};
+#pragma unroll
+        for (int d = 0; d < DP; ++d) {
+            if (pass + d >= npass) break;        // uniform
+            const int r = g0 + (pass + d) * RPG;
+            float acc[1] = {0.0f};
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 const int bb = bsub + BSL * it;
-                Fmt::template dot<1>(w1[it], l4, L, cur.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && cur.e >= 0, acc1);
+                Fmt::template dot<1>(w[d][it], l4, L, cur[d].xs + (bb < NB ? bb : NB - 1), 0,
+                                     bb < NB && cur[d].e >= 0, acc);
             }
-            sum = moe_silu(sum) * group_sum_last<LPR>(acc1[0]);
-        }
-        if (r < r1 && cur.e >= 0 && (lane & (LPR - 1)) == LPR - 1) *cur.y = sum;
-        if (more) {
-            cur = nxt;
-#pragma unroll
-            for (int it = 0; it < NIT; ++it) w[it] = wn[it];
+            float sum = group_sum_last<LPR>(acc[0]);
             if constexpr (GLU) {
+                float acc1[1] = {0.0f};
 #pragma unroll
-                for (int it = 0; it < NIT; ++it) w1[it] = wn1[it];
+                for (int it = 0; it < NIT; ++it) {
+                    const int bb = bsub + BSL * it;
+                    Fmt::template dot<1>(w1[d][it], l4, L, cur[d].xs + (bb < NB ? bb : NB - 1), 0,
+                                         bb < NB && cur[d].e >= 0, acc1);
+                }
+                sum = moe_silu(sum) * group_sum_last<LPR>(acc1[0]);
+            }
+            if (r < r1 && cur[d].e >= 0 && (lane & (LPR - 1)) == LPR - 1) *cur[d].y = sum;
+        }
+        if (more) {
+#pragma unroll
+            for (int d = 0; d < DP; ++d) {
+                cur[d] = nxt[d];
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) w[d][it] = wn[d][it];
+                if constexpr (GLU) {
+#pragma unroll
+                    for (int it = 0; it < NIT; ++it) w1[d][it] = wn1[d][it];
+                }
             }
         }
     }
