@@ -103,7 +103,7 @@ def test_beast_route_many_experts(ctx, E, k, n_embd):
 @pytest.mark.parametrize("E,k,n_embd,n_ff", [(32, 8, 2048, 768), (16, 2, 1024, 512), (8, 0, 512, 256),
                                              (6, 9, 256, 1024), (8, 4, 4096, 1536), (20, 16, 512, 768),
                                              (4, 2, 768, 4096), (4, 3, 4608, 512), (2, 2, 4352, 4352),
-                                             (4, 2, 1024, 4352)])
+                                             (4, 2, 1024, 4352), (1, 1, 256, 256), (3, 1, 2048, 768)])
 def test_beast_moe_vs_reference(ctx, oracle, E, k, n_embd, n_ff):
     """the forward against the reference's own build: the 30B-A3B widths
     (top-8, 2048 -> 768 -> 2048) over 32 experts, the default top-2 (k = 0),

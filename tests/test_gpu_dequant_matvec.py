@@ -71,7 +71,7 @@ def test_dequant_matvec_one_hot_one_token(ctx, oracle, K):
 @pytest.mark.parametrize("M,K,T,dist", [(4096, 4096, 1, 0), (256, 12288, 1, 0), (300, 2048, 3, 0), (768, 2048, 1, 0),
                                         (2048, 768, 8, 0), (96, 27648, 1, 1), (512, 5120, 4, 1), (40, 4352, 11, 0),
                                         (12288, 4096, 1, 1), (1001, 256, 1, 0), (37, 1024, 1, 0), (5000, 3072, 1, 0),
-                                        (130, 512, 1, 1)])
+                                        (130, 512, 1, 1), (1, 4096, 1, 0), (3, 256, 1, 0)])
 def test_dequant_matvec_vs_beast(ctx, oracle, M, K, T, dist):
     rng = np.random.default_rng(M + K + T)
     w, wb = _weights(ctx, M, K, 7 + T, dist, 8.0 if dist else 1.0)
