@@ -303,27 +303,28 @@ hipError_t launch_dq_t(const uint8_t* W, int M, int nb, const float* X, int64_t 
 // expert gate / up / down matvecs of beast_matvec's arithmetic and the
 // score-weighted sum.
 
-// x (one row of nb blocks) into the lane-major staging of dequant_matvec_kernel
+// x (one row of nb blocks) into the lane-major staging of dequant_matvec_kernel,
+// eight loads a thread in flight at a time (unconditional: past the row's end
+// they read its last float4, which is not stored)
 __device__ __forceinline__ void dq_stage_row(const float* __restrict__ x, int nb, f32x4* dq_x) {
     const f32x4* xr = reinterpret_cast<const f32x4*>(x);
-    for (int e4 = threadIdx.x; e4 < nb * 64; e4 += blockDim.x) {
-        const int b = e4 >> 6, g = (e4 >> 4) & 3, i4 = e4 & 15;
-        dq_x[((size_t)(b >> 4) * 16 + i4) * 64 + 4 * (b & 15) + g] = xr[e4];
+    const int n4 = nb * 64;
+    for (int base = threadIdx.x; base < n4; base += 8 * blockDim.x) {
+        f32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e4 = base + u * (int)blockDim.x;
+            v[u] = xr[e4 < n4 ? e4 : n4 - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e4 = base + u * (int)blockDim.x;
+            if (e4 < n4) {
+                const int b = e4 >> 6, g = (e4 >> 4) & 3, i4 = e4 & 15;
+                dq_x[((size_t)(b >> 4) * 16 + i4) * 64 + 4 * (b & 15) + g] = v[u];
+            }
+        }
     }
-}
-
-// one row's dequant-then-dot against the staged x, summed over the wave
-// (every lane gets the sum)
-__device__ __forceinline__ float dq_row_dot(const uint8_t* __restrict__ row, int nb, const lf32x4* xl, int lane) {
-    const int l4 = lane & 3, bsub = lane >> 2;
-    const int npass = (nb + 15) >> 4;
-    float acc[1] = {0.0f};
-    for (int it = 0; it < npass; ++it) {
-        const DqRow w = dq_load(row, nb, bsub, l4, it);
-        if (bsub + 16 * it < nb) dq_block<1>(w, l4, xl, npass, it, lane, acc);
-    }
-    const float s = group_sum_last<64>(acc[0]);
-    return __shfl(s, 63, 64);
 }
 
 // A candidate (score, index) as one 64-bit key that orders as the selection
@@ -454,10 +455,32 @@ __global__ __launch_bounds__(64) void beast_route_kernel(const float* __restrict
     }
 }
 
+// Rows of more than 16 blocks: every pass of a row's loads issued at once (NP
+// passes, the row's count rounded up to 2, 4 or 8; a pass past the row's end
+// loads its last block and its products are dropped), then its passes'
+// products as dq_block's and the fixed wave reduction.
+template <int NP>
+__device__ __forceinline__ void dq_load_passes(const uint8_t* __restrict__ row, int nb, int bsub, int l4,
+                                               DqRow (&w)[NP]) {
+#pragma unroll
+    for (int it = 0; it < NP; ++it) w[it] = dq_load(row, nb, bsub, l4, it);
+}
+
+template <int NP>
+__device__ __forceinline__ float dq_dot_passes(const DqRow (&w)[NP], int nb, const lf32x4* xl, int lane) {
+    const int l4 = lane & 3, bsub = lane >> 2;
+    float acc[1] = {0.0f};
+#pragma unroll
+    for (int it = 0; it < NP; ++it)
+        if (bsub + 16 * it < nb) dq_block<1>(w[it], l4, xl, 1, it, lane, acc);
+    return __shfl(group_sum_last<64>(acc[0]), 63, 64);
+}
+
 // gate and up rows of every selected expert against the hidden state, and
 // silu(gate) * up (beast_silu_mul, :1168-1173): H[s][r], s < top_k, r < n_ff;
-// a wave per sweep row (s, r) at a time, rows_per_wg consecutive sweep rows a
-// workgroup of 4 waves.
+// a wave per sweep row (s, r) at a time, its gate and up rows' loads issued
+// together; rows_per_wg consecutive sweep rows a workgroup of 4 waves.
+template <int NP>
 __global__ __launch_bounds__(256) void beast_gate_up_kernel(const uint8_t* __restrict__ gate,
                                                             const uint8_t* __restrict__ up, size_t expert_bytes,
                                                             int n_ff, int nb, const int32_t* __restrict__ ids,
@@ -468,6 +491,7 @@ __global__ __launch_bounds__(256) void beast_gate_up_kernel(const uint8_t* __res
     __syncthreads();
     const lf32x4* xl = (const lf32x4*)dq_x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int l4 = lane & 3, bsub = lane >> 2;
     const int total = top_k * n_ff;
     const int q0 = blockIdx.x * rows_per_wg;
     const int q1 = q0 + rows_per_wg < total ? q0 + rows_per_wg : total;
@@ -475,22 +499,24 @@ __global__ __launch_bounds__(256) void beast_gate_up_kernel(const uint8_t* __res
     for (int q = q0 + wave; q < q1; q += 4) {
         const int s = q / n_ff, r = q - s * n_ff;
         const int e = ids[s];
-        float h = 0.0f;                        // no expert (a routing with no candidate): nothing
-        if (e >= 0 && e < E) {
-            const size_t off = (size_t)e * expert_bytes + (size_t)r * row_bytes;
-            const float g = dq_row_dot(gate + off, nb, xl, lane);
-            const float u = dq_row_dot(up + off, nb, xl, lane);
-            h = (g / (1.0f + expf(-g))) * u;
-        }
-        if (lane == 0) H[q] = h;
+        const bool live = e >= 0 && e < E;    // no expert (a routing with no candidate): nothing
+        const size_t off = (size_t)(live ? e : 0) * expert_bytes + (size_t)r * row_bytes;
+        DqRow wg[NP], wu[NP];
+        dq_load_passes<NP>(gate + off, nb, bsub, l4, wg);
+        dq_load_passes<NP>(up + off, nb, bsub, l4, wu);
+        const float g = dq_dot_passes<NP>(wg, nb, xl, lane);
+        const float u = dq_dot_passes<NP>(wu, nb, xl, lane);
+        if (lane == 0) H[q] = live ? (g / (1.0f + expf(-g))) * u : 0.0f;
     }
 }
 
 // down rows of every selected expert against that expert's H row, summed in
 // rank order as output += score * down (:541-543, fused multiply-add as the
 // reference's GCC build contracts it): out[i], rows_per_wg consecutive rows
-// a workgroup of 4 waves, at most BEAST_DOWN_RPW a wave; the H rows are
-// staged one expert at a time.
+// a workgroup of 4 waves, at most BEAST_DOWN_RPW a wave, each row's loads
+// issued while the previous row is computed; the H rows are staged one expert
+// at a time.
+template <int NP>
 __global__ __launch_bounds__(256) void beast_down_sum_kernel(const uint8_t* __restrict__ down, size_t expert_bytes,
                                                              int n_embd, int nb, const int32_t* __restrict__ ids,
                                                              int E, const float* __restrict__ scores, int top_k,
@@ -499,26 +525,41 @@ __global__ __launch_bounds__(256) void beast_down_sum_kernel(const uint8_t* __re
     extern __shared__ __align__(16) f32x4 dq_x[];
     const lf32x4* xl = (const lf32x4*)dq_x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int l4 = lane & 3, bsub = lane >> 2;
     const int r0 = blockIdx.x * rows_per_wg;
     const int r1 = r0 + rows_per_wg < n_embd ? r0 + rows_per_wg : n_embd;
     const size_t row_bytes = (size_t)nb * Q4K_BYTES;
+    static_assert(BEAST_DOWN_RPW % 2 == 0, "rows are taken in pairs");
     float acc[BEAST_DOWN_RPW];
 #pragma unroll
     for (int j = 0; j < BEAST_DOWN_RPW; ++j) acc[j] = 0.0f;
+    // the wave's rows: nrow of them (uniform over the wave; the second of a
+    // pair past r1 reads row r1 - 1 and is dropped)
+    const int nrow = r0 + wave < r1 ? (r1 - r0 - wave + 3) / 4 : 0;
+    auto row_of = [&](int j) {
+        const int i = r0 + wave + 4 * j;
+        return i < r1 ? i : r1 - 1;
+    };
     for (int s = 0; s < top_k; ++s) {
         const int e = ids[s];
         if (e < 0 || e >= E) continue;         // uniform over the workgroup
+        const uint8_t* base = down + (size_t)e * expert_bytes;
+        DqRow wa[NP], wb[NP];
+        if (nrow > 0) dq_load_passes<NP>(base + (size_t)row_of(0) * row_bytes, nb, bsub, l4, wa);
         __syncthreads();                       // the previous expert's readers are done
         dq_stage_row(H + (size_t)s * n_ff, nb, dq_x);
         __syncthreads();
-        const uint8_t* base = down + (size_t)e * expert_bytes;
         const float sc = scores[s];
 #pragma unroll
-        for (int j = 0; j < BEAST_DOWN_RPW; ++j) {
-            const int i = r0 + wave + 4 * j;
-            if (i < r1) {
-                const float d = dq_row_dot(base + (size_t)i * row_bytes, nb, xl, lane);
-                acc[j] = fmaf(sc, d, acc[j]);
+        for (int j = 0; j < BEAST_DOWN_RPW; j += 2) {
+            if (j >= nrow) break;              // uniform over the wave
+            if (j + 1 < nrow) dq_load_passes<NP>(base + (size_t)row_of(j + 1) * row_bytes, nb, bsub, l4, wb);
+            const float da = dq_dot_passes<NP>(wa, nb, xl, lane);
+            acc[j] = fmaf(sc, da, acc[j]);
+            if (j + 2 < nrow) dq_load_passes<NP>(base + (size_t)row_of(j + 2) * row_bytes, nb, bsub, l4, wa);
+            if (j + 1 < nrow) {
+                const float db = dq_dot_passes<NP>(wb, nb, xl, lane);
+                acc[j + 1] = fmaf(sc, db, acc[j + 1]);
             }
         }
     }
@@ -920,6 +961,34 @@ hipError_t launch_beast_short_nb(int nb, const uint8_t* gate, const uint8_t* up,
 
 size_t dequant_matvec_lds_bytes(int T, int nb) { return (size_t)T * ((nb + 15) / 16) * 16 * 64 * 16; }
 
+template <int NP>
+hipError_t launch_beast_gate_up_np(const uint8_t* gate, const uint8_t* up, size_t gu_bytes, int n_ff, int nb,
+                                   const int32_t* ids, int E, int top_k, const float* hidden, float* H, int rpw,
+                                   int grid, size_t lds, hipStream_t st) {
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void*)beast_gate_up_kernel<NP>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(beast_gate_up_kernel<NP>, dim3((unsigned)grid), dim3(256), lds, st, gate, up, gu_bytes, n_ff,
+                       nb, ids, E, top_k, hidden, H, rpw);
+    return hipGetLastError();
+}
+
+template <int NP>
+hipError_t launch_beast_down_np(const uint8_t* down, size_t dn_bytes, int n_embd, int nb, const int32_t* ids, int E,
+                                const float* scores, int top_k, const float* H, int n_ff, float* out, int drw,
+                                int grid, size_t lds, hipStream_t st) {
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void*)beast_down_sum_kernel<NP>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(beast_down_sum_kernel<NP>, dim3((unsigned)grid), dim3(256), lds, st, down, dn_bytes, n_embd,
+                       nb, ids, E, scores, top_k, H, n_ff, out, drw);
+    return hipGetLastError();
+}
+
 hipError_t launch_beast_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* down, int E, int n_embd, int n_ff,
                             const float* logits, int top_k, const float* hidden, float* out, int32_t* ids,
                             float* scores, float* H, int num_cus, hipStream_t st) {
@@ -946,14 +1015,13 @@ hipError_t launch_beast_moe(const uint8_t* gate, const uint8_t* up, const uint8_
         const int64_t total = (int64_t)top_k * n_ff;
         int64_t rpw = (total + want - 1) / want;
         rpw = (rpw + 3) & ~(int64_t)3;
-        if (lds_e > 64 * 1024) {
-            e = hipFuncSetAttribute((const void*)beast_gate_up_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)lds_e);
-            if (e != hipSuccess) return e;
-        }
-        hipLaunchKernelGGL(beast_gate_up_kernel, dim3((unsigned)((total + rpw - 1) / rpw)), dim3(256), lds_e, st,
-                           gate, up, gu_bytes, n_ff, nb_e, ids, E, top_k, hidden, H, (int)rpw);
-        e = hipGetLastError();
+        const int np = (nb_e + 15) / 16;
+        e = np <= 2 ? launch_beast_gate_up_np<2>(gate, up, gu_bytes, n_ff, nb_e, ids, E, top_k, hidden, H, (int)rpw,
+                                                 (int)((total + rpw - 1) / rpw), lds_e, st)
+            : np <= 4 ? launch_beast_gate_up_np<4>(gate, up, gu_bytes, n_ff, nb_e, ids, E, top_k, hidden, H, (int)rpw,
+                                                   (int)((total + rpw - 1) / rpw), lds_e, st)
+                      : launch_beast_gate_up_np<8>(gate, up, gu_bytes, n_ff, nb_e, ids, E, top_k, hidden, H, (int)rpw,
+                                                   (int)((total + rpw - 1) / rpw), lds_e, st);
     }
     if (e != hipSuccess) return e;
     // down and the weighted sum
@@ -964,14 +1032,16 @@ hipError_t launch_beast_moe(const uint8_t* gate, const uint8_t* up, const uint8_
     int64_t drw = ((int64_t)n_embd + want - 1) / want;
     drw = (drw + 3) & ~(int64_t)3;
     if (drw > 4 * BEAST_DOWN_RPW) drw = 4 * BEAST_DOWN_RPW;
-    if (lds_f > 64 * 1024) {
-        e = hipFuncSetAttribute((const void*)beast_down_sum_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds_f);
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(beast_down_sum_kernel, dim3((unsigned)((n_embd + drw - 1) / drw)), dim3(256), lds_f, st, down,
-                       dn_bytes, n_embd, nb_f, ids, E, scores, top_k, H, n_ff, out, (int)drw);
-    return hipGetLastError();
+    const int np = (nb_f + 15) / 16;
+    const int grid = (int)((n_embd + drw - 1) / drw);
+    if (np <= 2)
+        return launch_beast_down_np<2>(down, dn_bytes, n_embd, nb_f, ids, E, scores, top_k, H, n_ff, out, (int)drw,
+                                       grid, lds_f, st);
+    if (np <= 4)
+        return launch_beast_down_np<4>(down, dn_bytes, n_embd, nb_f, ids, E, scores, top_k, H, n_ff, out, (int)drw,
+                                       grid, lds_f, st);
+    return launch_beast_down_np<8>(down, dn_bytes, n_embd, nb_f, ids, E, scores, top_k, H, n_ff, out, (int)drw, grid,
+                                   lds_f, st);
 }
 
 hipError_t launch_dequant_matvec(const uint8_t* W, int M, int nb, const float* X, int64_t x_tstride, float* Y,

@@ -103,13 +103,16 @@ def test_beast_route_many_experts(ctx, E, k, n_embd):
 @pytest.mark.parametrize("E,k,n_embd,n_ff", [(32, 8, 2048, 768), (16, 2, 1024, 512), (8, 0, 512, 256),
                                              (6, 9, 256, 1024), (8, 4, 4096, 1536), (20, 16, 512, 768),
                                              (4, 2, 768, 4096), (4, 3, 4608, 512), (2, 2, 4352, 4352),
-                                             (4, 2, 1024, 4352), (1, 1, 256, 256), (3, 1, 2048, 768)])
+                                             (4, 2, 1024, 4352), (1, 1, 256, 256), (3, 1, 2048, 768),
+                                             (2, 2, 256, 8448), (2, 2, 8448, 256), (2, 1, 256, 16640),
+                                             (2, 1, 16640, 256)])
 def test_beast_moe_vs_reference(ctx, oracle, E, k, n_embd, n_ff):
     """the forward against the reference's own build: the 30B-A3B widths
     (top-8, 2048 -> 768 -> 2048) over 32 experts, the default top-2 (k = 0),
     k above E (every expert), top-16, rows of 1 to 16 blocks (the one-wave
-    kernels at every lane count) and of more than 16 (the row-a-wave kernels),
-    each side of the forward on either"""
+    kernels at every lane count) and of more than 16 (the row-a-wave kernels,
+    rows of 2, 4 and 8 passes of 16 blocks), each side of the forward on
+    either"""
     b = BeastRef()
     rng = np.random.default_rng(E * 7 + k + n_embd)
 
