@@ -532,6 +532,38 @@ def run_prefill(args):
     ctx.close()
 
 
+def run_beastwide(args):
+    """The BurnHard MoE forward (spq4k_beast_moe_forward) at Mixtral-like
+    widths: 8 experts of 4096 -> 14336 -> 4096, top-2 of seeded N(0,1)
+    logits, one token; 4 layers of banks (3.2 GB, larger than the Infinity
+    Cache) replayed as one graph, timed cold. The hidden rows here are longer
+    than 16 blocks, so down runs the row-a-wave kernel."""
+    ctx = spq4k.Context(0)
+    E, k, NL, n_embd, n_ff = 8, 2, 4, 4096, 14336
+    syn = Synth(ctx, E * n_ff * n_embd)
+    layers = [[syn.weights(M, K, 700 + 10 * L + i, E=E) for i, (M, K) in
+               enumerate(((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff)))] for L in range(NL)]
+    ctx.synchronize()
+    syn.tmp.free()
+    xg = syn.activations(n_embd, 21)
+    Yb = DeviceArray(n_embd)
+    lg = [DeviceArray.from_host(np.random.default_rng(60 + L).standard_normal(E).astype(np.float32))
+          for L in range(NL)]
+    ctx.beast_moe_forward_dev(*layers[0], lg[0].ptr, k, xg.ptr, Yb.ptr)   # sizes the scratch
+    ctx.synchronize()
+    with Graph.capture(ctx.stream) as g:
+        for L in range(NL):
+            ctx.beast_moe_forward_dev(*layers[L], lg[L].ptr, k, xg.ptr, Yb.ptr)
+    ms = time_graph(ctx, g, max(5, args.steps // 5), 2) / NL
+    wbytes = k * 3 * q4k_bytes(n_ff, n_embd)
+    gbs = wbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({"metric": "BurnHard MoE forward (routing, fp32 dequant-then-dot), T=1, wide rows",
+                      "value": round(gbs, 1), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
+                      "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2),
+                      "config": {"workload": "8 experts of 4096 -> 14336 -> 4096, top-2, 4 layers of banks (cold)",
+                                 "T": 1}}), flush=True)
+
+
 def run_moe(args):
     """128 experts (gate/up 768x2048, down 2048x768), top-8,
     T = 1..32. Timed cold: 8 layers, each with its own three expert banks
@@ -926,7 +958,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "q8_0",
-                                                          "single", "gguf", "fusion", "copy", "floor"])
+                                                          "single", "gguf", "fusion", "copy", "floor", "beastwide"])
     ap.add_argument("--M", type=int, default=4096, help="rows (--config single)")
     ap.add_argument("--K", type=int, default=4096, help="inputs (--config single)")
     ap.add_argument("--T", type=int, default=1, help="tokens (--config single)")
@@ -948,6 +980,8 @@ def main():
         run_prefill(args)
     elif args.config == "moe":
         run_moe(args)
+    elif args.config == "beastwide":
+        run_beastwide(args)
     elif args.config == "q6k":
         run_kquant(args, spq4k.TYPE_Q6_K)
     elif args.config == "q5k":
