@@ -1028,8 +1028,12 @@ hipError_t launch_beast_moe(const uint8_t* gate, const uint8_t* up, const uint8_
     if (nb_f <= 16)
         return launch_beast_short_nb(nb_f, gate, up, down, gu_bytes, dn_bytes, n_embd, n_ff, nb_e, nb_f, logits, E,
                                      top_k, ids, scores, hidden, H, out, false, num_cus, st);
-    // rows in runs of a multiple of 4, at most BEAST_DOWN_RPW a wave
-    int64_t drw = ((int64_t)n_embd + want - 1) / want;
+    // rows in runs of a multiple of 4, at most BEAST_DOWN_RPW a wave, about two
+    // workgroups a CU: each workgroup stages every selected expert's whole
+    // hidden row, so longer runs read less of it again (4096 x 14336, top-2:
+    // 79.5 us a forward with two workgroups a CU, 88.1 with four, 88.4 with one)
+    const int64_t want_d = 2 * (int64_t)num_cus;
+    int64_t drw = ((int64_t)n_embd + want_d - 1) / want_d;
     drw = (drw + 3) & ~(int64_t)3;
     if (drw > 4 * BEAST_DOWN_RPW) drw = 4 * BEAST_DOWN_RPW;
     const int np = (nb_f + 15) / 16;
