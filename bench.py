@@ -194,6 +194,45 @@ def time_chain(ctx, ch, steps, warmup):
     return e0.elapsed_ms(e1) / steps
 
 
+def chain_breakdown(ctx, ch, kinds):
+    """Stage timestamps of a form-2 chain (spq4k_chain_set_stamps,
+    include/spq4k_diag.h): per stage kind, the medians over layers of
+      exchange  the last workgroup's rows of the previous stage done -> the
+                first exchange wave's inputs gathered (median over workgroups),
+      staged    the same -> every exchange wave's inputs gathered and x formed,
+      quant     x formed -> Q8_K activations ready (norm and quantisation),
+      rows      activations ready -> the workgroup's rows done,
+      spread    the last workgroup's rows done - the median workgroup's,
+      stage     the last workgroup's rows done, from the previous stage's."""
+    from spq4k.hip import DeviceArray
+    v, grid, n = ch.info()
+    if v != 2:
+        return None
+    buf = DeviceArray(grid * n * 4, np.uint64)
+    buf.fill_byte(0)
+    ch.set_stamps(buf.ptr)
+    for _ in range(3):
+        ch.run()
+    ch.status()
+    s = buf.to_host().reshape(grid, n, 4).astype(np.int64) * 10   # ns (100 MHz clock)
+    ch.set_stamps(None)
+    buf.free()
+    last = s[:, :, 2].max(axis=0)
+    rows = {}
+    for t in range(1, n):
+        k = kinds[t]
+        d = rows.setdefault(k, {"exchange": [], "staged": [], "quant": [], "rows": [], "spread": [], "stage": []})
+        d["exchange"].append(np.median(s[:, t, 0] - last[t - 1]))
+        d["staged"].append(np.median(s[:, t, 3] - last[t - 1]))
+        d["quant"].append(np.median(s[:, t, 1] - s[:, t, 3]))
+        d["rows"].append(np.median(s[:, t, 2] - s[:, t, 1]))
+        d["spread"].append(last[t] - np.median(s[:, t, 2]))
+        d["stage"].append(last[t] - last[t - 1])
+    out = {k: {m: round(float(np.median(v)) / 1e3, 3) for m, v in d.items()} for k, d in rows.items()}
+    out["_step_us"] = round(float(last[-1] - s[:, 0, 0].min()) / 1e3, 1)
+    return out
+
+
 def stage_bytes(stage):
     _, ws, _, _ = stage
     # algorithmic: weights + one fp32 x and y per matvec (BASELINE accounting)
@@ -384,6 +423,7 @@ def run_decode8b(args):
     chain = None
     if not args.no_chain:
         ch, chain_bufs, logits = build_chain8b(ctx, stages)
+        form = ch.version
         ms_ch = time_chain(ctx, ch, args.steps, args.warmup)
         lg = logits.to_host()
         if not np.isfinite(lg).all() or not np.any(lg):
@@ -391,7 +431,8 @@ def run_decode8b(args):
         ch.free()
         for b in chain_bufs:
             b.free()
-        chain = {"kernel": "chain_kernel", "launches_per_step": 1, "ms_per_step": round(ms_ch, 5),
+        chain = {"kernel": "chain2_kernel" if form == 2 else "chain_kernel", "form": form,
+                 "launches_per_step": 1, "ms_per_step": round(ms_ch, 5),
                  "GBps": round(step_bytes / (ms_ch * 1e-3) / 1e9, 2),
                  "what": "the step's 145 stages as one dependent chain (norm, q/k/v, o, residual, norm, "
                          "gate/up + SwiGLU, down, head; q stands in for the attention output)"}
@@ -448,6 +489,39 @@ def run_decode8b(args):
     if cpu is None:
         out["cpu_baseline_note"] = why
     print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+def run_chain(args):
+    """--config chain: the 8B decode step as one dependent chain launch, in
+    each form (1: a grid barrier at every stage, k_chain.hip; 2: the one-hop
+    exchange, k_chain2.hip), and form 2's per-stage breakdown from its
+    timestamps (chain_breakdown)."""
+    ctx = spq4k.Context(0)
+    stages = build_decode8b(ctx)
+    step_bytes = sum(stage_bytes(s) for s in stages)
+    kinds = ["qkv", "o", "gate_up", "down"] * LAYERS + ["lm_head"]
+    res = {}
+    for form in (2, 1):
+        os.environ["SPQ4K_CHAIN_V"] = str(form)
+        ch, bufs, logits = build_chain8b(ctx, stages)
+        os.environ.pop("SPQ4K_CHAIN_V", None)
+        ms = time_chain(ctx, ch, args.steps, args.warmup)
+        lg = logits.to_host()
+        if not np.isfinite(lg).all() or not np.any(lg):
+            raise RuntimeError(f"chain form {form}: non-finite or all-zero logits")
+        r = {"form": ch.version, "ms_per_step": round(ms, 5), "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 2),
+             "pct_of_peak_hbm": round(step_bytes / (ms * 1e-3) / PEAK_HBM * 100, 2)}
+        log(f"[bench] chain form {ch.version}: {ms*1e3:.1f} us/step, {r['GBps']:.1f} GB/s")
+        if ch.version == 2:
+            r["breakdown_us"] = chain_breakdown(ctx, ch, kinds)
+            for k, v in r["breakdown_us"].items():
+                log(f"[bench]   {k:8s} {v}")
+        res[f"form{ch.version}"] = r
+        ch.free()
+        for b in bufs:
+            b.free()
+    print(json.dumps({"config": "chain", "algorithmic_bytes_per_step": step_bytes, **res}), flush=True)
     ctx.close()
 
 
@@ -958,7 +1032,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "q8_0",
-                                                          "single", "gguf", "fusion", "copy", "floor", "beastwide"])
+                                                          "single", "gguf", "fusion", "copy", "floor", "beastwide", "chain"])
     ap.add_argument("--M", type=int, default=4096, help="rows (--config single)")
     ap.add_argument("--K", type=int, default=4096, help="inputs (--config single)")
     ap.add_argument("--T", type=int, default=1, help="tokens (--config single)")
@@ -998,6 +1072,8 @@ def main():
                    f"{tag[args.qtype]} {args.M}x{args.K} T={args.T}", args.qtype)
     elif args.config == "floor":
         run_floor(args)
+    elif args.config == "chain":
+        run_chain(args)
     elif args.config == "copy":
         run_copy(args)
     elif args.config == "largek":

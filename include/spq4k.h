@@ -402,30 +402,6 @@ int spq4k_chain_run(spq4k_ctx *ctx, spq4k_chain *chain);
 int spq4k_chain_status(spq4k_ctx *ctx, spq4k_chain *chain);
 void spq4k_chain_free(spq4k_chain *chain);
 
-/* ---- diagnostics -------------------------------------------------------
- * Exact integer sub-block sums S[r][b][j] = sum_{l<32} q4 * q8 over
- * sub-block j of block b of row r, against Q8_K(x), formed by the same lane
- * code as the GEMV. No reference function returns them; they are the integer
- * core of ggml_vec_dot_q4_K_q8_K (ggml-cpu/quants.c:645-718). */
-int spq4k_subblock_sums(spq4k_ctx *ctx, const void *W, int64_t M, int64_t K, const float *x, int32_t *S);
-/* The same for a weight type: Q4_K as above; Q5_K gives S[r][b][j], j < 8,
- * the sum of q5 * q8 over sub-block j (ggml-cpu/quants.c:720-798); Q6_K gives
- * S[r][b][j], j < 16, the sum over the 16 weights of sub-block j of
- * (q - 32) * q8, the integer core of ggml_vec_dot_q6_K_q8_K
- * (ggml-cpu/quants.c:800-852); Q8_0 gives S[r][b], b < K/32, the sum of
- * qw * qx over block b against spq4k_quantize_q8_0(x), the integer core of
- * ggml_vec_dot_q8_0_q8_0 (ggml-cpu/quants.c:400-428). */
-int spq4k_subblock_sums_type(spq4k_ctx *ctx, int type, const void *W, int64_t M, int64_t K, const float *x,
-                             int32_t *S);
-/* A read of `bytes` of device memory at p (16-byte aligned, a multiple of
- * 16 bytes; 0 launches a kernel that reads nothing) by one launch on the
- * context stream: each wave reads 4 KB of consecutive bytes per step as four
- * coalesced 16-byte-a-lane loads, four workgroups a CU (SPQ4K_STREAM_GRID
- * sets another largest grid), no other work -- the HBM floor of a launch of
- * the same bytes. No reference counterpart; for measurement (bench.py
- * --config floor). */
-int spq4k_stream_read(spq4k_ctx *ctx, const void *p, size_t bytes);
-
 #ifdef __cplusplus
 }
 #endif

@@ -13,14 +13,26 @@
 
 #include <mutex>
 #include <vector>
+#include <algorithm>
 
 #include <hip/hip_runtime.h>
 
 #include "launch.h"
 #include "spq4k.h"
+#include "spq4k_diag.h"
 #include "spq4k_synth.h"
 
 using namespace spq4k;
+
+// The partial-sum plane of a K-split matmul is held to a fixed budget, so the
+// split (and with it the order of the fp32 sums) depends on the shape alone:
+// not on how much scratch a context happens to hold, and not on whether the
+// call runs on the no-allocation scratch (whose activation planes leave it
+// exactly this much, SPQ4K_NOALLOC_SCRATCH_BYTES - SPQ4K_NOALLOC_PLANES_MAX).
+constexpr size_t KSPLIT_PARTIAL_BYTES = (size_t)8 << 20;
+static_assert(SPQ4K_NOALLOC_SCRATCH_BYTES - SPQ4K_NOALLOC_PLANES_MAX == KSPLIT_PARTIAL_BYTES,
+              "the no-allocation scratch leaves a K split its whole budget");
+
 
 struct spq4k_ctx {
     int device = 0;
@@ -348,9 +360,7 @@ int q80_gemm(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float* X,
     if ((rows + 15) / 16 * ((T + 15) / 16) > (1ll << 31) - 1 || rows > (1ll << 31) - 1)
         return set_err(c, -EINVAL, "gemm: grid too large");
     const size_t planes = q80_planes_bytes(T, nb);
-    size_t room = c->scratch_cap > planes ? c->scratch_cap - planes : 0;
-    if (room < ((size_t)8 << 20)) room = (size_t)8 << 20;
-    const GemmPlan g = gemm_plan(p, c->num_cus, room);
+    const GemmPlan g = gemm_plan(p, c->num_cus, KSPLIT_PARTIAL_BYTES);
     p.cfg = g.cfg;
     p.ksplit = g.ksplit;
     p.kchunk = g.kchunk;
@@ -612,6 +622,10 @@ int noalloc_scratch_setup(int device) {
     if (device < 0 || device >= NOALLOC_MAX_DEVICES) return -ENODEV;
     std::lock_guard<std::mutex> lk(g_noalloc_mu);
     if (g_noalloc_ptr[device]) return 0;
+    // SPQ4K_TEST_NOALLOC_LOOKUP_FAIL=1 makes the lookup fail (for the test
+    // that a context still comes up and the entry point reports -EIO)
+    if (const char* f = getenv("SPQ4K_TEST_NOALLOC_LOOKUP_FAIL"))
+        if (atoi(f) == 1) return -EIO;
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return -EIO;
     g_noalloc_ptr[device] = static_cast<uint8_t*>(p);
@@ -706,11 +720,10 @@ int spq4k_init(int device, spq4k_ctx** out) {
         const int v = atoi(f);
         if (v == 1 || v == 2) c->q80_preq = v;
     }
-    if (noalloc_scratch_setup(device) != 0) {
-        (void)hipStreamDestroy(c->own_stream);
-        delete c;
-        return -EIO;
-    }
+    // The no-allocation scratch's address is looked up here, with the device
+    // current; a failure does not fail the context (only the no-allocation
+    // entry point needs it, and it tries again on its first call).
+    (void)noalloc_scratch_setup(device);
     // scratch for Q8_K activation planes: sized for prefill batches up front
     // so that steady-state calls (and graph capture) never allocate
     if (ensure_scratch(c, (size_t)16 << 20) != 0 || ensure_scratch2(c, (size_t)4 << 20) != 0) {
@@ -1202,12 +1215,8 @@ int gemm_segments(spq4k_ctx* c, int n, const spq4k_weights* const* W, const floa
         if (e != hipSuccess) return hip_fail(c, e, "gemm skinny launch");
         return 0;
     }
-    // a K split's partial plane uses the scratch the context already holds,
-    // and at least 8 MB
     const size_t planes = q8_planes_bytes((int)T, p.nb);
-    size_t room = c->scratch_cap > planes ? c->scratch_cap - planes : 0;
-    if (room < ((size_t)8 << 20)) room = (size_t)8 << 20;
-    const GemmPlan g = gemm_plan(p, c->num_cus, room);
+    const GemmPlan g = gemm_plan(p, c->num_cus, KSPLIT_PARTIAL_BYTES);
     p.cfg = g.cfg;
     p.ksplit = g.ksplit;
     p.kchunk = g.kchunk;
@@ -1256,6 +1265,7 @@ int spq4k_mul_mat_noalloc(spq4k_ctx* c, const spq4k_weights* W, const float* X, 
     if (rc) return rc;
     if (!W || !W->data) return set_err(c, -EINVAL, "mul_mat_noalloc: null weight");
     uint8_t* base = noalloc_scratch_of(c->device);
+    if (!base && noalloc_scratch_setup(c->device) == 0) base = noalloc_scratch_of(c->device);
     if (!base) return set_err(c, -EIO, "mul_mat_noalloc: no device address of the no-allocation scratch");
     if (T < 1 || T > (1 << 20)) return set_err(c, -EINVAL, "mul_mat_noalloc: T=%lld", (long long)T);
     // the activation planes must leave the partial plane of a K split its 8 MiB
@@ -2151,8 +2161,14 @@ int spq4k_synth_fill(spq4k_ctx* c, float* out, int64_t n, uint64_t seed, int dis
 // decode chains (k_chain.hip)
 struct spq4k_chain {
     int device = 0;
+    int version = 1;                   // 1: grid barrier a stage (k_chain.hip); 2: one-hop exchange (k_chain2.hip)
     ChainStage* d_st = nullptr;
     ChainSync* d_sync = nullptr;
+    Chain2Stage* d_st2 = nullptr;
+    Chain2Sync* d_sync2 = nullptr;
+    float* d_sh = nullptr;             // v2 shadow arena, two sets of sh_half floats
+    int64_t sh_half = 0;
+    uint64_t* stamps = nullptr;        // v2 diagnostics (caller's buffer) or null
     int nstages = 0;
     float eps = 0.0f;
     int grid = 0;
@@ -2165,6 +2181,123 @@ bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
     const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
     return x < y + nb && y < x + na;
 }
+
+// The v2 form of a chain (k_chain2.hip) when its data flow allows it: every
+// vector a stage writes (y[j], x_out) lies apart from every other one, and an
+// input is either one of them or a part of one written by an earlier stage
+// (read through its shadow, or from LDS when it is the x_out of the latest
+// stage with one) or touches none of them (read as it is). Then no stage
+// writes memory an earlier stage reads or writes, which the loosely ordered
+// stages of v2 need. Returns false (use v1) otherwise.
+bool chain2_plan(const std::vector<ChainStage>& tab, int grid, std::vector<Chain2Stage>& out, int64_t& sh_half) {
+    struct Prod {
+        uintptr_t p;
+        size_t bytes;
+        int stage, which;   // which: 0..3 = y[j], 4 = x_out
+        int64_t sh;
+    };
+    const int n = (int)tab.size();
+    const int64_t G = (int64_t)grid * chain2_compute_waves();
+    std::vector<Prod> prods;
+    for (int s = 0; s < n; ++s) {
+        const ChainStage& t = tab[(size_t)s];
+        if ((t.rows + G - 1) / G * chain2_compute_waves() > CHAIN_YCAP) return false;
+        const int nout = t.glu ? 1 : 4;
+        for (int j = 0; j < nout; ++j) {
+            if (!t.Y[j]) continue;
+            const int64_t end = j + 1 < 4 && t.row_begin[j + 1] != INT32_MAX ? t.row_begin[j + 1] : t.rows;
+            prods.push_back({(uintptr_t)t.Y[j], (size_t)(end - t.row_begin[j]) * sizeof(float), s, j, -1});
+        }
+        if (t.xout) prods.push_back({(uintptr_t)t.xout, (size_t)t.nb * QK * sizeof(float), s, 4, -1});
+    }
+    std::vector<size_t> ord(prods.size());
+    for (size_t i = 0; i < ord.size(); ++i) ord[i] = i;
+    std::sort(ord.begin(), ord.end(), [&](size_t a, size_t b) { return prods[a].p < prods[b].p; });
+    for (size_t i = 1; i < ord.size(); ++i)
+        if (prods[ord[i - 1]].p + prods[ord[i - 1]].bytes > prods[ord[i]].p) return false;
+    // the produced vector holding [p, p + bytes), -1 if none touches it, -2 on a partial overlap
+    auto find = [&](const void* pp, size_t bytes) -> int {
+        const uintptr_t p = (uintptr_t)pp;
+        size_t lo = 0, hi = ord.size();
+        while (lo < hi) {   // first produced range starting past p
+            const size_t mid = (lo + hi) / 2;
+            if (prods[ord[mid]].p <= p) lo = mid + 1; else hi = mid;
+        }
+        if (lo > 0) {
+            const Prod& q = prods[ord[lo - 1]];
+            if (p < q.p + q.bytes) return p + bytes <= q.p + q.bytes ? (int)ord[lo - 1] : -2;
+        }
+        if (lo < ord.size() && prods[ord[lo]].p < p + bytes) return -2;
+        return -1;
+    };
+    out.assign((size_t)n, Chain2Stage{});
+    std::vector<int> in_prod((size_t)n * 2, -1);
+    int last_xout = -1;
+    for (int s = 0; s < n; ++s) {
+        const ChainStage& t = tab[(size_t)s];
+        Chain2Stage& o = out[(size_t)s];
+        for (int j = 0; j < 4; ++j) {
+            o.W[j] = t.W[j];
+            o.Y[j] = t.Y[j];
+            o.ysh[j] = -1;
+            o.row_begin[j] = t.row_begin[j];
+        }
+        o.rows = t.rows;
+        o.nb = t.nb;
+        o.glu = t.glu;
+        o.xout = t.xout;
+        o.xosh = -1;
+        o.norm_w = t.norm_w;
+        const size_t xb = (size_t)t.nb * QK * sizeof(float);
+        if (t.norm_w && find(t.norm_w, xb) != -1) return false;
+        const float* in[2] = {t.in0, t.in1};
+        for (int i = 0; i < 2; ++i) {
+            o.kind[i] = CH2_NONE;
+            if (!in[i]) continue;
+            const int f = find(in[i], xb);
+            if (f == -2) return false;
+            if (f == -1) {
+                o.kind[i] = CH2_EXT;
+                o.ext[i] = in[i];
+                continue;
+            }
+            const Prod& q = prods[(size_t)f];
+            if (q.stage >= s) return false;
+            if (q.which == 4 && q.stage == last_xout && q.p == (uintptr_t)in[i] && q.bytes == xb) {
+                o.kind[i] = CH2_LOCAL;
+                out[(size_t)q.stage].keep = 1;
+            } else {
+                o.kind[i] = CH2_SHADOW;
+                in_prod[(size_t)s * 2 + i] = f;
+            }
+        }
+        if (t.xout) last_xout = s;
+    }
+    // shadows for the vectors read through one, 256-byte aligned
+    int64_t off = 0;
+    for (int s = 0; s < n; ++s)
+        for (int i = 0; i < 2; ++i) {
+            const int f = in_prod[(size_t)s * 2 + i];
+            if (f < 0 || prods[(size_t)f].sh >= 0) continue;
+            prods[(size_t)f].sh = off;
+            off += ((int64_t)(prods[(size_t)f].bytes / sizeof(float)) + 63) / 64 * 64;
+        }
+    for (const Prod& q : prods) {
+        if (q.sh < 0) continue;
+        if (q.which == 4) out[(size_t)q.stage].xosh = q.sh;
+        else out[(size_t)q.stage].ysh[q.which] = q.sh;
+    }
+    for (int s = 0; s < n; ++s)
+        for (int i = 0; i < 2; ++i) {
+            const int f = in_prod[(size_t)s * 2 + i];
+            if (f < 0) continue;
+            const Prod& q = prods[(size_t)f];
+            const float* in = i ? tab[(size_t)s].in1 : tab[(size_t)s].in0;
+            out[(size_t)s].insh[i] = q.sh + (int64_t)(((uintptr_t)in - q.p) / sizeof(float));
+        }
+    sh_half = off;
+    return true;
+}
 }  // namespace
 
 extern "C" {
@@ -2176,6 +2309,9 @@ void spq4k_chain_free(spq4k_chain* ch) {
     (void)hipSetDevice(ch->device);
     if (ch->d_st) (void)hipFree(ch->d_st);
     if (ch->d_sync) (void)hipFree(ch->d_sync);
+    if (ch->d_st2) (void)hipFree(ch->d_st2);
+    if (ch->d_sync2) (void)hipFree(ch->d_sync2);
+    if (ch->d_sh) (void)hipFree(ch->d_sh);
     if (prev >= 0) (void)hipSetDevice(prev);
     delete ch;
 }
@@ -2266,10 +2402,32 @@ int spq4k_chain_create(spq4k_ctx* c, const spq4k_chain_stage* stages, int n, flo
     ch->eps = eps;
     ch->grid = grid;
     ch->shape = shape;
-    hipError_t e = hipMalloc(&ch->d_st, sizeof(ChainStage) * (size_t)n);
-    if (e == hipSuccess) e = hipMalloc(&ch->d_sync, sizeof(ChainSync));
-    if (e == hipSuccess) e = hipMemcpy(ch->d_st, tab.data(), sizeof(ChainStage) * (size_t)n, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemset(ch->d_sync, 0, sizeof(ChainSync));
+    // Form 1 (a grid barrier every stage) unless SPQ4K_CHAIN_V=2 asks for
+    // form 2 (the one-hop exchange) and the chain's data flow allows it. On
+    // the 8B decode step form 1 measures faster (1.56 against 1.69 ms): both
+    // are bound by their compute waves' instruction issue, and form 2 gives
+    // four waves of each workgroup to the exchange.
+    std::vector<Chain2Stage> tab2;
+    int64_t sh_half = 0;
+    const char* fv = getenv("SPQ4K_CHAIN_V");
+    const bool want2 = fv && atoi(fv) == 2;
+    if (want2 && chain2_plan(tab, grid, tab2, sh_half)) ch->version = 2;
+    hipError_t e = hipSuccess;
+    if (ch->version == 2) {
+        ch->sh_half = sh_half;
+        e = hipMalloc(&ch->d_st2, sizeof(Chain2Stage) * (size_t)n);
+        if (e == hipSuccess) e = hipMalloc(&ch->d_sync2, sizeof(Chain2Sync));
+        if (e == hipSuccess) e = hipMalloc(&ch->d_sh, sizeof(float) * (size_t)(2 * sh_half + 64));
+        if (e == hipSuccess)
+            e = hipMemcpy(ch->d_st2, tab2.data(), sizeof(Chain2Stage) * (size_t)n, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemset(ch->d_sync2, 0, sizeof(Chain2Sync));
+        if (e == hipSuccess) e = hipMemset(ch->d_sh, 0xFF, sizeof(float) * (size_t)(2 * sh_half + 64));
+    } else {
+        e = hipMalloc(&ch->d_st, sizeof(ChainStage) * (size_t)n);
+        if (e == hipSuccess) e = hipMalloc(&ch->d_sync, sizeof(ChainSync));
+        if (e == hipSuccess) e = hipMemcpy(ch->d_st, tab.data(), sizeof(ChainStage) * (size_t)n, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemset(ch->d_sync, 0, sizeof(ChainSync));
+    }
     if (e != hipSuccess) {
         spq4k_chain_free(ch);
         return e == hipErrorOutOfMemory ? set_err(c, -ENOMEM, "chain_create: out of device memory")
@@ -2283,6 +2441,21 @@ int spq4k_chain_run(spq4k_ctx* c, spq4k_chain* ch) {
     int rc = use_device(c);
     if (rc) return rc;
     if (!ch || ch->device != c->device) return set_err(c, -EINVAL, "chain_run: no chain for this device");
+    if (ch->version == 2) {
+        Chain2Params p;
+        p.sync = ch->d_sync2;
+        p.sh = ch->d_sh;
+        p.sh_half = ch->sh_half;
+        p.stamps = ch->stamps;
+        p.nstages = ch->nstages;
+        p.eps = ch->eps;
+        int depth = 4;
+        if (const char* f = getenv("SPQ4K_CHAIN2_D")) depth = atoi(f);
+        if (depth != 2 && depth != 3 && depth != 6) depth = 4;
+        hipError_t e = launch_chain2(ch->d_st2, p, ch->grid, depth, c->stream);
+        if (e != hipSuccess) return hip_fail(c, e, "chain launch");
+        return 0;
+    }
     ChainParams p;
     p.st = ch->d_st;
     p.sync = ch->d_sync;
@@ -2293,12 +2466,39 @@ int spq4k_chain_run(spq4k_ctx* c, spq4k_chain* ch) {
     return 0;
 }
 
+int spq4k_chain_info(const spq4k_chain* ch, int* version, int* grid, int* n_stages) {
+    if (!ch) return -EINVAL;
+    if (version) *version = ch->version;
+    if (grid) *grid = ch->grid;
+    if (n_stages) *n_stages = ch->nstages;
+    return 0;
+}
+
+int spq4k_chain_set_stamps(spq4k_ctx* c, spq4k_chain* ch, uint64_t* stamps) {
+    int rc = use_device(c);
+    if (rc) return rc;
+    if (!ch || ch->device != c->device) return set_err(c, -EINVAL, "chain_set_stamps: no chain for this device");
+    if (ch->version != 2) return set_err(c, -EINVAL, "chain_set_stamps: the chain runs in form 1");
+    if (!aligned(stamps, 8)) return set_err(c, -EINVAL, "chain_set_stamps: misaligned buffer");
+    ch->stamps = stamps;
+    return 0;
+}
+
 int spq4k_chain_status(spq4k_ctx* c, spq4k_chain* ch) {
     int rc = use_device(c);
     if (rc) return rc;
     if (!ch || ch->device != c->device) return set_err(c, -EINVAL, "chain_status: no chain for this device");
     SPQ_HIP(c, hipStreamSynchronize(c->stream));
     uint32_t err = 0;
+    if (ch->version == 2) {
+        SPQ_HIP(c, hipMemcpy(&err, &ch->d_sync2->err, sizeof err, hipMemcpyDeviceToHost));
+        if (err) {
+            SPQ_HIP(c, hipMemset(ch->d_sync2, 0, sizeof(Chain2Sync)));
+            SPQ_HIP(c, hipMemset(ch->d_sh, 0xFF, sizeof(float) * (size_t)(2 * ch->sh_half + 64)));
+            return set_err(c, -ETIMEDOUT, "chain: a stage wait gave up; outputs invalid, chain reset");
+        }
+        return 0;
+    }
     SPQ_HIP(c, hipMemcpy(&err, &ch->d_sync->err, sizeof err, hipMemcpyDeviceToHost));
     if (err) {
         SPQ_HIP(c, hipMemset(ch->d_sync, 0, sizeof(ChainSync)));

@@ -290,22 +290,41 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
         }
         return;
     }
-    for (int i0 = 0; i0 < nrows; i0 += D) {
+    auto consume = [&](int i, const W (&b)[NIT]) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const float a = Fmt::dot_reg(b[it], l4, qr[it], acc);
+            acc = (bsub + 16 * it < nb) ? a : acc;
+        }
+        acc = group_sum_last<64>(acc);
+        if (lane == 63) {
+            const Loc l = locate(g + i * G);
+            l.y[l.row] = acc;
+        }
+    };
+    int i0 = 0;
+    if (D > 1) {
+        // Whole passes whose reloads are all real rows: every pass reloads
+        // every buffer, so at the loop header the oldest loads are always
+        // buf[0]'s and the compiler waits for them alone. (A reload under a
+        // condition inside the loop gives the header a path on which buf[0]
+        // was loaded last, and the wait there becomes vmcnt(0): the rows in
+        // flight would drain at every pass.)
+        for (; i0 + 2 * D <= nrows; i0 += D) {
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                consume(i0 + u, buf[u]);
+                load_row(i0 + u + D, buf[u]);
+            }
+        }
+    }
+    for (; i0 < nrows; i0 += D) {
 #pragma unroll
         for (int u = 0; u < D; ++u) {
             const int i = i0 + u;
             if (i < nrows) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int it = 0; it < NIT; ++it) {
-                    const float a = Fmt::dot_reg(buf[u][it], l4, qr[it], acc);
-                    acc = (bsub + 16 * it < nb) ? a : acc;
-                }
-                acc = group_sum_last<64>(acc);
-                if (lane == 63) {
-                    const Loc l = locate(g + i * G);
-                    l.y[l.row] = acc;
-                }
+                consume(i, buf[u]);
                 if (i + D < nrows) load_row(i + D, buf[u]);
             }
         }

@@ -326,6 +326,55 @@ struct ChainParams {
     int32_t nstages;
     float eps;
 };
+// The same chain with a one-hop exchange between stages (k_chain2.hip).
+// Every vector a stage produces and a later stage reads (y[j], x_out) is
+// also written to a shadow in a chain-owned arena whose words hold
+// CHAIN2_SENTINEL until written in the current launch: a reader polls the
+// words themselves, so no barrier, counter or fence sits between a row's
+// store and its consumers. The arena has two sets: launch n uses set
+// parity(n) and refills the other with the sentinel for launch n + 1.
+constexpr uint32_t CHAIN2_SENTINEL = 0xFFFFFFFFu;   // a NaN; a result with these bits
+constexpr uint32_t CHAIN2_SUBST = 0xFFFFFFFEu;      // is passed on as this NaN
+enum : int32_t { CH2_NONE = 0, CH2_EXT = 1, CH2_SHADOW = 2, CH2_LOCAL = 3 };
+struct Chain2Stage {
+    const uint8_t* W[4];
+    float* Y[4];
+    int64_t ysh[4];          // shadow offset (floats) of output j, or -1 (no later reader)
+    int32_t row_begin[4];    // as ChainStage
+    int32_t rows;
+    int32_t nb;
+    int32_t glu;
+    int32_t keep;            // keep x = in0 (+ in1) in the workgroup's LDS (a later CH2_LOCAL input)
+    int32_t kind[2];         // in0, in1: CH2_*
+    const float* ext[2];     // CH2_EXT input
+    int64_t insh[2];         // CH2_SHADOW input: shadow offset of its first value
+    float* xout;             // optional
+    int64_t xosh;            // shadow offset of x_out, or -1
+    const float* norm_w;     // optional
+};
+struct Chain2Sync {
+    uint32_t cnt;            // workgroups of the current launch that have finished
+    uint32_t pad0[63];
+    uint32_t parity;         // shadow set of the next launch
+    uint32_t pad1[63];
+    uint32_t err;            // set when a wait gave up
+    uint32_t pad2[63];
+};
+struct Chain2Params {
+    Chain2Sync* sync;        // zeroed, arena filled with the sentinel, before the first launch
+    float* sh;               // shadow arena: set 0, then set 1 at sh + sh_half
+    int64_t sh_half;         // floats per set (a multiple of 4)
+    uint64_t* stamps;        // optional: s_memrealtime per workgroup and stage (CHAIN2_NSTAMP each)
+    int32_t nstages;
+    float eps;
+};
+constexpr int CHAIN2_XW = 4;         // exchange waves a workgroup
+constexpr int CHAIN2_NSTAMP = 4;     // stamps per workgroup and stage
+// compute waves of the v2 kernel
+int chain2_compute_waves();
+// depth: pieces in flight a compute wave (2, 3, 4 or 6)
+hipError_t launch_chain2(const Chain2Stage* st, const Chain2Params& p, int grid, int depth, hipStream_t stream);
+
 // workgroups of a chain launch on a device with num_cus CUs (a multiple of CHAIN_NCTR)
 int chain_grid(int num_cus);
 // launch shapes (compute waves x pieces in flight each): 0 = 8 x 8, 1 = 8 x 6, 2 = 7 x 8

@@ -168,6 +168,8 @@ def load_library(path: str | None = None):
         "spq4k_chain_run": (I, [V, V]),
         "spq4k_chain_status": (I, [V, V]),
         "spq4k_chain_free": (None, [V]),
+        "spq4k_chain_info": (I, [V, C.POINTER(I), C.POINTER(I), C.POINTER(I)]),
+        "spq4k_chain_set_stamps": (I, [V, V, V]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -197,6 +199,23 @@ class Chain:
     def status(self):
         """Synchronise; raises (rc -ETIMEDOUT) if a stage wait gave up."""
         self.ctx._check("spq4k_chain_status", self.ctx.lib.spq4k_chain_status(self.ctx.handle, self.handle))
+
+    def info(self):
+        """spq4k_chain_info (include/spq4k_diag.h): (form, workgroups, stages)."""
+        v, g, n = C.c_int(), C.c_int(), C.c_int()
+        rc = self.ctx.lib.spq4k_chain_info(self.handle, C.byref(v), C.byref(g), C.byref(n))
+        if rc:
+            raise Spq4kError("spq4k_chain_info", rc, "no chain")
+        return v.value, g.value, n.value
+
+    @property
+    def version(self) -> int:
+        return self.info()[0]
+
+    def set_stamps(self, ptr: int | None):
+        """spq4k_chain_set_stamps: a device buffer of grid * n_stages * 4 uint64, or None."""
+        self.ctx._check("spq4k_chain_set_stamps",
+                        self.ctx.lib.spq4k_chain_set_stamps(self.ctx.handle, self.handle, ptr or None))
 
     def free(self):
         if self.handle:

@@ -66,10 +66,22 @@ def test_no_device_is_an_error_not_a_fallback():
     assert not h.value
 
 
+def test_dropin_header_declares_no_diagnostics():
+    """include/spq4k.h holds the drop-in entry points only; the measurement
+    probe, the integer-sum views and the chain timestamps live in
+    include/spq4k_diag.h"""
+    diag = {"spq4k_stream_read", "spq4k_subblock_sums", "spq4k_subblock_sums_type", "spq4k_chain_info",
+            "spq4k_chain_set_stamps"}
+    dropin = set(declared_functions([os.path.join(REPO, "include", "spq4k.h")]))
+    assert not (dropin & diag), f"diagnostics in the drop-in header: {sorted(dropin & diag)}"
+    assert diag <= set(declared_functions([os.path.join(REPO, "include", "spq4k_diag.h")]))
+
+
 def test_header_compiles_as_c():
     import subprocess
     import tempfile
-    src = "#include <spq4k.h>\n#include <spq4k_synth.h>\nint main(void){return SPQ4K_QK_K == 256 ? 0 : 1;}\n"
+    src = ("#include <spq4k.h>\n#include <spq4k_synth.h>\n#include <spq4k_diag.h>\n"
+           "int main(void){return SPQ4K_QK_K == 256 ? 0 : 1;}\n")
     with tempfile.TemporaryDirectory() as d:
         f = os.path.join(d, "t.c")
         open(f, "w").write(src)

@@ -187,10 +187,20 @@ def _outputs(net, meta):
     return {n: net.host(n) for n in names}
 
 
-def test_chain_8b_layers(ctx, oracle):
+@pytest.fixture(params=[1, 2], ids=["form1", "form2"])
+def form(request, monkeypatch):
+    """the chain's form: 1 a grid barrier every stage (k_chain.hip, the
+    default), 2 the one-hop exchange (k_chain2.hip, SPQ4K_CHAIN_V=2 when the
+    data flow allows it)"""
+    monkeypatch.setenv("SPQ4K_CHAIN_V", str(request.param))
+    return request.param
+
+
+def test_chain_8b_layers(ctx, oracle, form):
     """two 8B decode layers and a 4096-row output head in one launch"""
     net, stages, meta = _layer_net(ctx, 2, 4096, 4096, 1024, 12288, 4096)
     ch = ctx.chain_create(stages, EPS)
+    assert ch.version == form
     ch.run()
     ch.status()
     first = _outputs(net, meta)
@@ -206,7 +216,7 @@ def test_chain_8b_layers(ctx, oracle):
     ch.free()
 
 
-def test_chain_ragged(ctx, oracle):
+def test_chain_ragged(ctx, oracle, form):
     """rows fewer than the grid's waves, partial 16-block passes, four matrices
     in a stage, K from 256 to 12288"""
     net = _Net(ctx)
@@ -248,6 +258,7 @@ def test_chain_ragged(ctx, oracle):
     meta.append({"w_names": ["k6"], "y_names": ["yk6"], "in0_name": "x6", "norm_name": "nw6", "bitwise": False})
     stages = [_to_stage(net, m) for m in meta]
     ch = ctx.chain_create(stages, EPS)
+    assert ch.version == form
     ch.run()
     ch.status()
     for i, m in enumerate(meta):
@@ -291,4 +302,58 @@ def test_chain_rejects_bad_stages(ctx):
     ch = ctx.chain_create([good], EPS)
     ch.run()
     ch.status()
+    ch.free()
+
+
+def test_chain_form1_when_a_stage_overwrites_an_input(ctx, oracle, monkeypatch):
+    """a stage that writes memory an earlier stage read keeps the grid barrier
+    (form 1) even when form 2 is asked for: form 2 lets stages overlap, which
+    only holds when no stage writes what an earlier one reads; the outputs
+    still match the per-op path"""
+    net = _Net(ctx)
+    rng = np.random.default_rng(11)
+    net.buf("x", 4096, rng.standard_normal(4096).astype(np.float32))
+    net.weight("a", 4096, 4096, 61)
+    net.weight("b", 4096, 4096, 62)
+    net.buf("y1", 4096)
+    # stage 0 reads x; stage 1 reads stage 0's output and overwrites x
+    m0 = {"w_names": ["a"], "y_names": ["y1"], "in0_name": "x"}
+    m1 = {"w_names": ["b"], "y_names": ["x"], "in0_name": "y1"}
+    x0 = net.host("x")
+    monkeypatch.setenv("SPQ4K_CHAIN_V", "2")
+    ch = ctx.chain_create([_to_stage(net, m0), _to_stage(net, m1)], EPS)
+    assert ch.version == 1
+    ch.run()
+    ch.status()
+    y1 = net.host("y1")
+    W, wb = net.w["a"]
+    rows = _sample_rows(4096)
+    ok = parity_ok(y1[rows], oracle.mul_mat(_rows_of(wb, 4096, rows), rows.size, 4096, x0[None, :])[0],
+                   oracle.mul_mat_dq_f64(12, _rows_of(wb, 4096, rows), rows.size, 4096, x0[None, :])[0])
+    assert ok.all()
+    _check_stage(ctx, oracle, net, m1, 1)
+    ch.free()
+
+
+def test_chain_stamps(ctx, monkeypatch):
+    """form 2's stage timestamps (include/spq4k_diag.h) are written for every
+    workgroup and stage, in order: inputs gathered <= x formed <= activations
+    ready <= rows done <= the next stage's inputs gathered"""
+    from spq4k.hip import DeviceArray
+    net, stages, meta = _layer_net(ctx, 1, 4096, 4096, 1024, 12288, 4096)
+    monkeypatch.setenv("SPQ4K_CHAIN_V", "2")
+    ch = ctx.chain_create(stages, EPS)
+    v, grid, n = ch.info()
+    assert v == 2 and n == len(stages) and grid > 0
+    st = DeviceArray(grid * n * 4, np.uint64)
+    st.fill_byte(0)
+    ch.set_stamps(st.ptr)
+    ch.run()
+    ch.status()
+    s = st.to_host().reshape(grid, n, 4).astype(np.int64)
+    assert (s > 0).all()
+    assert (s[:, :, 0] <= s[:, :, 3]).all() and (s[:, :, 3] <= s[:, :, 1]).all()
+    assert (s[:, :, 1] <= s[:, :, 2]).all()
+    assert (s[:, :-1, 2] <= s[:, 1:, 0]).all()
+    ch.set_stamps(None)
     ch.free()
