@@ -127,6 +127,13 @@ int spq4k_weights_upload_type(spq4k_ctx *ctx, int type, const void *host, int64_
                               spq4k_weights **out);
 int spq4k_weights_wrap_type(spq4k_ctx *ctx, int type, const void *dev, int64_t M, int64_t K, int64_t E,
                             spq4k_weights **out);
+/* Whether [p, p + bytes) lies in device memory of the context's GPU
+ * (hipPointerGetAttributes): 1 yes, 0 no (host memory, another GPU's, or
+ * memory the runtime does not know). An engine adapter uses it before
+ * passing a tensor's address to the entry points above, which read device
+ * pointers in place -- the decision the reference makes from a buffer's
+ * device type before dereferencing tensor->data (burn_moe_op.cpp:67-80). */
+int spq4k_ptr_on_device(spq4k_ctx *ctx, const void *p, size_t bytes);
 int spq4k_weights_alloc_type(spq4k_ctx *ctx, int type, int64_t M, int64_t K, int64_t E, spq4k_weights **out);
 /* the ggml type id of w, or -EINVAL for NULL */
 int spq4k_weights_type(const spq4k_weights *w);
@@ -262,11 +269,14 @@ int spq4k_moe_multi(spq4k_ctx *ctx, int n, const spq4k_weights *const *banks, co
  * activations as given -- no Q8_K quantisation, so its outputs differ from
  * spq4k_mul_mat's (the ggml CPU path's arithmetic) by about 0.75% normwise
  * at N(0, 0.02) weights and N(0, 1) activations. The dequantised weights
- * are dequantize_row_q4_K's bit for bit; each product is rounded to fp32 and
- * the products are added in fp32 (per lane, then across the wave in a fixed
- * order, where beast_matvec adds them serially). Dense Q4_K, any T (tokens
- * run in groups of up to 8), K <= 32768; X [T][K] 16-byte aligned, Y [T][M],
- * device pointers; the _host twin copies in and out. */
+ * are the format's own dequantiser's bit for bit (dequantize_row_q4_K, _q5_K,
+ * _q6_K, _q8_0; the reference's beast_dequant_q5_K / _q6_K, :1025-1085, read
+ * other bits than those formats and are not followed); each product is
+ * rounded to fp32 and the products are added in fp32 (per lane, then across
+ * the lane group in a fixed order, where beast_matvec adds them serially).
+ * Dense Q4_K, Q5_K, Q6_K or Q8_0 matrices, any T (tokens run in groups of up
+ * to 8), K <= 32768; X [T][K] 16-byte aligned, Y [T][M], device pointers; the
+ * _host twin copies in and out. */
 int spq4k_dequant_matvec(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
 int spq4k_dequant_matvec_host(spq4k_ctx *ctx, const spq4k_weights *W, const float *X, float *Y, int64_t T);
 /* spq4k_beast_moe_forward: the reference's BurnHard MoE forward for one
@@ -284,9 +294,10 @@ int spq4k_dequant_matvec_host(spq4k_ctx *ctx, const spq4k_weights *W, const floa
  * beast_matvec's arithmetic as in spq4k_dequant_matvec (fp32 activations,
  * no Q8_K; the dequantised weights bit for bit, the products summed per lane
  * and across the wave where the reference adds serially). top_k <= 0 means 2
- * (the reference's default) and is capped at E; at most 16. Q4_K banks: gate
- * and up [n_ff x n_embd] x E, down [n_embd x n_ff] x E, E <= 4096, rows of at
- * most 32768 values. router_logits [E], hidden [n_embd] (16-byte aligned),
+ * (the reference's default) and is capped at E; at most 16. Banks of Q4_K,
+ * Q5_K, Q6_K or Q8_0, each of its own type (a Q4_K_M file's Q6_K down bank
+ * beside Q4_K gate / up ones): gate and up [n_ff x n_embd] x E, down
+ * [n_embd x n_ff] x E, E <= 4096, rows of at most 32768 values. router_logits [E], hidden [n_embd] (16-byte aligned),
  * output [n_embd]; ids / scores [top_k] receive the routing when not NULL
  * (engine->routing's expert_ids / expert_scores). Device pointers; the _host
  * twin copies in and out. */
@@ -374,8 +385,9 @@ int spq4k_moe_host(spq4k_ctx *ctx, const spq4k_weights *bank, const int32_t *ids
  * launch that streams the next stages' weights while a stage waits for the
  * previous one. Q4_K weights, E = 1, K <= 12288; per stage
  * (1 + [in1] + [norm_w]) * K <= 12288; all pointers device pointers,
- * 16-byte aligned; a stage's outputs (y, x_out) must not overlap its inputs
- * (in0, in1). Stages may read what any earlier stage wrote.
+ * 16-byte aligned; a stage's outputs (y[i], x_out) must overlap neither its
+ * inputs (in0, in1, norm_w) nor each other (-EINVAL). Stages may read what
+ * any earlier stage wrote.
  *   spq4k_chain_create  validates and uploads the stage table;
  *   spq4k_chain_run     launches it on the context's stream (asynchronous);
  *   spq4k_chain_status  synchronises and returns 0, or -ETIMEDOUT if a

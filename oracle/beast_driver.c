@@ -51,40 +51,44 @@ int ref_beast_route(const float *logits, int n_experts, int top_k, int *ids, flo
 
 /* sp_beast_moe_forward (sp_beast_canyon.c:455-562) for one token over expert
  * banks held contiguously in memory (E experts of gate / up [n_ff x n_embd]
- * and down [n_embd x n_ff]): the reference's routing, beast_matvec and
- * beast_silu_mul, and its per-expert loop restated (:486-545: gate, up,
- * silu(gate) * up, down, output += score * down_out, output zeroed first);
- * the engine's reservoir lookup, prefetch, CRT telemetry and barrier, which
- * do not touch the numbers, are left out. Returns the number of experts. */
+ * and down [n_embd x n_ff]), each bank of its own type as the reference's
+ * tensors are: the reference's routing, beast_matvec and beast_silu_mul, and
+ * its per-expert loop restated (:486-545: gate, up, silu(gate) * up, down,
+ * output += score * down_out, output zeroed first); the engine's reservoir
+ * lookup, prefetch, CRT telemetry and barrier, which do not touch the
+ * numbers, are left out. Returns the number of experts. */
 __attribute__((visibility("default")))
-int ref_beast_moe(const void *gate, const void *up, const void *down, unsigned type, int n_experts, int n_embd,
-                  int n_ff, const float *logits, int top_k, const float *hidden, float *output, int *ids,
-                  float *scores) {
+int ref_beast_moe_types(const void *gate, unsigned tg, const void *up, unsigned tu, const void *down, unsigned td,
+                        int n_experts, int n_embd, int n_ff, const float *logits, int top_k, const float *hidden,
+                        float *output, int *ids, float *scores) {
     int k_sel = ref_beast_route(logits, n_experts, top_k, ids, scores);
     if (k_sel < 0) return -1;
-    const size_t gb = beast_row_bytes(type, n_embd) * (size_t)n_ff;    /* one expert of gate / up */
-    const size_t db = beast_row_bytes(type, n_ff) * (size_t)n_embd;    /* one expert of down */
+    const size_t gb = beast_row_bytes(tg, n_embd) * (size_t)n_ff;      /* one expert of gate */
+    const size_t ub = beast_row_bytes(tu, n_embd) * (size_t)n_ff;      /* one expert of up */
+    const size_t db = beast_row_bytes(td, n_ff) * (size_t)n_embd;      /* one expert of down */
     float *gate_buf = (float *)malloc((size_t)n_ff * sizeof(float));
     float *up_buf = (float *)malloc((size_t)n_ff * sizeof(float));
     float *down_out = (float *)malloc((size_t)n_embd * sizeof(float));
     float *scratch = (float *)malloc((size_t)(n_embd > n_ff ? n_embd : n_ff) * sizeof(float));
     if (!gate_buf || !up_buf || !down_out || !scratch) return -1;
     memset(output, 0, (size_t)n_embd * sizeof(float));
-    sp_optane_tensor_t tg, tu, td;
-    memset(&tg, 0, sizeof tg);
-    memset(&tu, 0, sizeof tu);
-    memset(&td, 0, sizeof td);
-    tg.type = tu.type = td.type = type;
+    sp_optane_tensor_t t_g, t_u, t_d;
+    memset(&t_g, 0, sizeof t_g);
+    memset(&t_u, 0, sizeof t_u);
+    memset(&t_d, 0, sizeof t_d);
+    t_g.type = tg;
+    t_u.type = tu;
+    t_d.type = td;
     for (int k = 0; k < k_sel; ++k) {
         const int eid = ids[k];
         const float score = scores[k];
-        tg.ptr = (void *)((const uint8_t *)gate + (size_t)eid * gb);
-        tu.ptr = (void *)((const uint8_t *)up + (size_t)eid * gb);
-        td.ptr = (void *)((const uint8_t *)down + (size_t)eid * db);
-        beast_matvec(&tg, hidden, gate_buf, scratch, n_ff, n_embd);
-        beast_matvec(&tu, hidden, up_buf, scratch, n_ff, n_embd);
+        t_g.ptr = (void *)((const uint8_t *)gate + (size_t)eid * gb);
+        t_u.ptr = (void *)((const uint8_t *)up + (size_t)eid * ub);
+        t_d.ptr = (void *)((const uint8_t *)down + (size_t)eid * db);
+        beast_matvec(&t_g, hidden, gate_buf, scratch, n_ff, n_embd);
+        beast_matvec(&t_u, hidden, up_buf, scratch, n_ff, n_embd);
         beast_silu_mul(gate_buf, up_buf, n_ff);
-        beast_matvec(&td, gate_buf, down_out, scratch, n_embd, n_ff);
+        beast_matvec(&t_d, gate_buf, down_out, scratch, n_embd, n_ff);
         for (int i = 0; i < n_embd; i++) {
             output[i] += score * down_out[i];
         }
@@ -94,4 +98,13 @@ int ref_beast_moe(const void *gate, const void *up, const void *down, unsigned t
     free(down_out);
     free(scratch);
     return k_sel;
+}
+
+/* the forward with one type for all three banks */
+__attribute__((visibility("default")))
+int ref_beast_moe(const void *gate, const void *up, const void *down, unsigned type, int n_experts, int n_embd,
+                  int n_ff, const float *logits, int top_k, const float *hidden, float *output, int *ids,
+                  float *scores) {
+    return ref_beast_moe_types(gate, type, up, type, down, type, n_experts, n_embd, n_ff, logits, top_k, hidden,
+                               output, ids, scores);
 }

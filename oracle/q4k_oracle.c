@@ -609,16 +609,23 @@ int or_mul_mat_dq_f64_type(int type, const void *W, int64_t M, int64_t K, const 
  *     time and adds them one by one; its fused tail serves only K not a
  *     multiple of 8, which no K-quant row has).
  * beast_dequant_q5_K (:1056-1085) and beast_dequant_q6_K (:1025-1053) read
- * other bits than ggml's dequantize_row_q5_K / _q6_K (the qh bit of a
- * sub-block, the scale of a 16-value group), so they are not restated: for
- * those types the format's own dequantiser is the parity target. */
+ * other bits than ggml's dequantize_row_q5_K / _q6_K (Q5_K: the qh bit of
+ * the 64-value group where the format has one per 32-value sub-block; Q6_K:
+ * one scale per 32 values where the format has one per 16, and the high
+ * nibbles of ql[l] and the low ones of ql[l + 32] in each other's place), so
+ * they are not restated: for Q5_K and Q6_K rows the loop above runs over the
+ * format's own dequantiser (dequantize_row_q5_K / _q6_K, ggml-quants.c:
+ * 1669-1696 / 1877-1905, restated here as or_dequantize_row_q5K / _q6K). */
 int or_beast_matvec_type(int type, const void *W, int64_t M, int64_t K, const float *x, float *y) {
-    if (type != OR_TYPE_Q4_K && type != OR_TYPE_Q8_0) return -22;
+    if (type != OR_TYPE_Q4_K && type != OR_TYPE_Q8_0 && type != OR_TYPE_Q5_K && type != OR_TYPE_Q6_K) return -22;
     const size_t rb = row_bytes_type(type, K);
+    if (!rb) return -22;
     float *w = (float *)malloc((size_t)K * sizeof(float));
     for (int64_t r = 0; r < M; ++r) {
         const uint8_t *src = (const uint8_t *)W + (size_t)r * rb;
-        if (type == OR_TYPE_Q4_K) {
+        if (type == OR_TYPE_Q5_K || type == OR_TYPE_Q6_K) {
+            (void)dequant_row_type(type, src, w, K);
+        } else if (type == OR_TYPE_Q4_K) {
             const or_block_q4K *b = (const or_block_q4K *)src;
             for (int64_t i = 0; i < K / OR_QK_K; ++i) {
                 const float d = or_fp16_to_fp32(b[i].d), dmin = or_fp16_to_fp32(b[i].dmin);
@@ -646,6 +653,43 @@ int or_beast_matvec_type(int type, const void *W, int64_t M, int64_t K, const fl
     }
     free(w);
     return 0;
+}
+
+/* sp_beast_moe_forward's per-expert loop (desktop/beast_canyon/
+ * sp_beast_canyon.c:486-545) over a given routing: output zeroed, then for
+ * each selected expert in rank order g = beast_matvec(gate_e, hidden),
+ * u = beast_matvec(up_e, hidden), h = (g / (1 + expf(-g))) * u
+ * (beast_silu_mul, :1168-1173), d = beast_matvec(down_e, h),
+ * output = fmaf(score, d, output) (:541-543 as the reference's GCC build
+ * contracts it). Each bank has its own type (the reference's tensors carry
+ * theirs; beast_matvec dispatches per tensor): gate / up [n_ff x n_embd] x E,
+ * down [n_embd x n_ff] x E, contiguous experts. An id outside 0 .. E-1 is
+ * skipped. */
+int or_beast_moe_routed(int tg, const void *gate, int tu, const void *up, int td, const void *down, int64_t E,
+                        int64_t n_embd, int64_t n_ff, const int32_t *ids, const float *scores, int64_t k,
+                        const float *hidden, float *out) {
+    const size_t rg = row_bytes_type(tg, n_embd), ru = row_bytes_type(tu, n_embd), rd = row_bytes_type(td, n_ff);
+    if (!rg || !ru || !rd) return -22;
+    float *g = (float *)malloc((size_t)n_ff * sizeof(float));
+    float *u = (float *)malloc((size_t)n_ff * sizeof(float));
+    float *d = (float *)malloc((size_t)n_embd * sizeof(float));
+    int rc = (g && u && d) ? 0 : -12;
+    for (int64_t i = 0; i < n_embd; ++i) out[i] = 0.0f;
+    for (int64_t s = 0; s < k && !rc; ++s) {
+        const int64_t e = ids[s];
+        if (e < 0 || e >= E) continue;
+        rc = or_beast_matvec_type(tg, (const uint8_t *)gate + (size_t)e * n_ff * rg, n_ff, n_embd, hidden, g);
+        if (!rc) rc = or_beast_matvec_type(tu, (const uint8_t *)up + (size_t)e * n_ff * ru, n_ff, n_embd, hidden, u);
+        if (rc) break;
+        for (int64_t i = 0; i < n_ff; ++i) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+        rc = or_beast_matvec_type(td, (const uint8_t *)down + (size_t)e * n_embd * rd, n_embd, n_ff, g, d);
+        if (rc) break;
+        for (int64_t i = 0; i < n_embd; ++i) out[i] = fmaf(scores[s], d[i], out[i]);
+    }
+    free(g);
+    free(u);
+    free(d);
+    return rc;
 }
 
 /* ------------------------------------------------------------------------ */

@@ -164,8 +164,13 @@ int or_mul_mat_dq_f64_type(int type, const void *W, int64_t M, int64_t K, const 
                            int64_t T, double *Y);
 /* beast_matvec (sp_beast_canyon.c:1122-1134) as the reference's build
  * evaluates it (fp32 products summed in index order), for one fp32 input x;
- * Q4_K and Q8_0 */
+ * Q4_K and Q8_0 with the reference's dequantisers, Q5_K and Q6_K with the
+ * format's (the reference's read other bits). or_beast_moe_routed: the MoE
+ * forward's per-expert loop (:486-545) over a given routing, a type per bank */
 int or_beast_matvec_type(int type, const void *W, int64_t M, int64_t K, const float *x, float *y);
+int or_beast_moe_routed(int tg, const void *gate, int tu, const void *up, int td, const void *down, int64_t E,
+                        int64_t n_embd, int64_t n_ff, const int32_t *ids, const float *scores, int64_t k,
+                        const float *hidden, float *out);
 
 /* synthetic data, bit-identical with the device generator */
 void or_synth_fill(float *out, int64_t n, uint64_t seed, int dist, int64_t cols,

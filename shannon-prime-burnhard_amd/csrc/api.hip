@@ -1260,6 +1260,19 @@ int spq4k_mul_mat(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y
     return spq4k_gemm(c, W, X, Y, T);
 }
 
+int spq4k_ptr_on_device(spq4k_ctx* c, const void* p, size_t bytes) {
+    if (!c || !p) return 0;
+    hipPointerAttribute_t a;
+    for (const char* q : {(const char*)p, (const char*)p + (bytes ? bytes - 1 : 0)}) {
+        if (hipPointerGetAttributes(&a, q) != hipSuccess) {
+            (void)hipGetLastError();   // an unknown pointer is an answer, not a sticky error
+            return 0;
+        }
+        if (a.type != hipMemoryTypeDevice || a.device != c->device) return 0;
+    }
+    return 1;
+}
+
 int spq4k_mul_mat_noalloc(spq4k_ctx* c, const spq4k_weights* W, const float* X, float* Y, int64_t T) {
     int rc = use_device(c);
     if (rc) return rc;
@@ -1901,9 +1914,24 @@ int spq4k_dequant_matvec(spq4k_ctx* c, const spq4k_weights* W, const float* X, f
     int rc = use_device(c);
     if (rc) return rc;
     if (!W || !W->data || !X || !Y || T < 1) return set_err(c, -EINVAL, "dequant_matvec: bad arguments");
-    if (W->type != SPQ4K_TYPE_Q4_K || W->E != 1)
-        return set_err(c, -EINVAL, "dequant_matvec: a dense Q4_K matrix is required");
+    if (W->E != 1) return set_err(c, -EINVAL, "dequant_matvec: a dense matrix is required");
     if (!aligned(X, 16) || !aligned(Y, 4)) return set_err(c, -EINVAL, "dequant_matvec: misaligned pointer");
+    if (W->type != SPQ4K_TYPE_Q4_K) {
+        // Q5_K / Q6_K / Q8_0 rows: the type-generic kernels, tokens in groups
+        // whose x fits the staging area
+        if (dqx_lds_bytes(W->type, W->K, 1) > DQ_MATVEC_LDS_MAX)
+            return set_err(c, -EINVAL, "dequant_matvec: K = %lld exceeds %zu staged values", (long long)W->K,
+                           DQ_MATVEC_LDS_MAX / sizeof(float));
+        int tg = DQ_MATVEC_MAX_T;
+        while (tg > 1 && dqx_lds_bytes(W->type, W->K, tg) > DQ_MATVEC_LDS_MAX) --tg;
+        for (int64_t t0 = 0; t0 < T; t0 += tg) {
+            const int n = (int)(T - t0 < tg ? T - t0 : tg);
+            hipError_t e = launch_dqx_matvec(W->type, W->data, (int)W->M, W->K, X + t0 * W->K, W->K, Y + t0 * W->M,
+                                             W->M, n, c->num_cus, c->stream);
+            if (e != hipSuccess) return hip_fail(c, e, "dequant_matvec launch");
+        }
+        return 0;
+    }
     const int nb = (int)(W->K / SPQ4K_QK_K);
     if (dequant_matvec_lds_bytes(1, nb) > DQ_MATVEC_LDS_MAX)
         return set_err(c, -EINVAL, "dequant_matvec: K = %lld exceeds %zu staged values", (long long)W->K,
@@ -1944,8 +1972,6 @@ int spq4k_beast_moe_forward(spq4k_ctx* c, const spq4k_weights* gate, const spq4k
     if (rc) return rc;
     if (!gate || !up || !down || !gate->data || !up->data || !down->data || !router_logits || !hidden || !output)
         return set_err(c, -EINVAL, "beast_moe_forward: null argument");
-    if (gate->type != SPQ4K_TYPE_Q4_K || up->type != SPQ4K_TYPE_Q4_K || down->type != SPQ4K_TYPE_Q4_K)
-        return set_err(c, -EINVAL, "beast_moe_forward: Q4_K expert banks are required");
     const int64_t E = gate->E, n_embd = gate->K, n_ff = gate->M;
     if (up->E != E || up->K != n_embd || up->M != n_ff || down->E != E || down->K != n_ff || down->M != n_embd)
         return set_err(c, -EINVAL, "beast_moe_forward: gate [%lld x %lld x %lld], up and down banks do not match",
@@ -1955,8 +1981,15 @@ int spq4k_beast_moe_forward(spq4k_ctx* c, const spq4k_weights* gate, const spq4k
     if (top_k <= 0) top_k = 2;
     if (top_k > E) top_k = E;
     if (top_k > BEAST_MAX_TOPK) return set_err(c, -EINVAL, "beast_moe_forward: top_k = %lld", (long long)top_k);
-    if (dequant_matvec_lds_bytes(1, (int)(n_embd / SPQ4K_QK_K)) > DQ_MATVEC_LDS_MAX ||
-        dequant_matvec_lds_bytes(1, (int)(n_ff / SPQ4K_QK_K)) > DQ_MATVEC_LDS_MAX)
+    const bool q4_gu = gate->type == SPQ4K_TYPE_Q4_K && up->type == SPQ4K_TYPE_Q4_K;
+    const bool q4_dn = down->type == SPQ4K_TYPE_Q4_K;
+    // every bank's rows staged whole: the Q4_K kernels' layout for Q4_K
+    // gate / up pairs and Q4_K down banks, the type-generic one otherwise
+    const size_t lds_e = q4_gu ? dequant_matvec_lds_bytes(1, (int)(n_embd / SPQ4K_QK_K))
+                               : std::max(dqx_lds_bytes(gate->type, n_embd, 1), dqx_lds_bytes(up->type, n_embd, 1));
+    const size_t lds_f = q4_dn ? dequant_matvec_lds_bytes(1, (int)(n_ff / SPQ4K_QK_K))
+                               : dqx_lds_bytes(down->type, n_ff, 1);
+    if (lds_e > DQ_MATVEC_LDS_MAX || lds_f > DQ_MATVEC_LDS_MAX)
         return set_err(c, -EINVAL, "beast_moe_forward: rows longer than %zu values", DQ_MATVEC_LDS_MAX / sizeof(float));
     if (!aligned(hidden, 16) || !aligned(router_logits, 4) || !aligned(output, 4) || !aligned(ids, 4) ||
         !aligned(scores, 4))
@@ -1968,9 +2001,27 @@ int spq4k_beast_moe_forward(spq4k_ctx* c, const spq4k_weights* gate, const spq4k
     int32_t* rid = reinterpret_cast<int32_t*>(c->scratch2);
     float* rsc = reinterpret_cast<float*>(c->scratch2 + 128);
     float* H = reinterpret_cast<float*>(c->scratch2 + rb);
-    hipError_t e = launch_beast_moe(gate->data, up->data, down->data, (int)E, (int)n_embd, (int)n_ff, router_logits,
-                                    (int)top_k, hidden, output, rid, rsc, H, c->num_cus, c->stream);
-    if (e != hipSuccess) return hip_fail(c, e, "beast moe launch");
+    // routing and H = silu(gate . x) * (up . x): the fused Q4_K launch, or
+    // the routing alone, then the gate rows into H and the up rows finishing it
+    hipError_t e;
+    if (q4_gu) {
+        e = launch_beast_route_gate_up(gate->data, up->data, (int)E, (int)n_embd, (int)n_ff, router_logits, (int)top_k,
+                                       hidden, rid, rsc, H, c->num_cus, c->stream);
+    } else {
+        e = launch_beast_route(router_logits, (int)E, (int)top_k, rid, rsc, c->stream);
+        if (e == hipSuccess)
+            e = launch_dqx_experts(gate->type, false, gate->data, (int)E, (int)n_ff, n_embd, rid, (int)top_k, hidden, H,
+                                   c->num_cus, c->stream);
+        if (e == hipSuccess)
+            e = launch_dqx_experts(up->type, true, up->data, (int)E, (int)n_ff, n_embd, rid, (int)top_k, hidden, H,
+                                   c->num_cus, c->stream);
+    }
+    if (e != hipSuccess) return hip_fail(c, e, "beast moe gate / up launch");
+    e = q4_dn ? launch_beast_down(down->data, (int)E, (int)n_embd, (int)n_ff, rid, rsc, (int)top_k, H, output,
+                                  c->num_cus, c->stream)
+              : launch_dqx_down(down->type, down->data, (int)E, (int)n_embd, n_ff, rid, rsc, (int)top_k, H, output,
+                                c->num_cus, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "beast moe down launch");
     if (ids) SPQ_HIP(c, hipMemcpyAsync(ids, rid, (size_t)top_k * sizeof(int32_t), hipMemcpyDeviceToDevice, c->stream));
     if (scores)
         SPQ_HIP(c, hipMemcpyAsync(scores, rsc, (size_t)top_k * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
@@ -2377,15 +2428,24 @@ int spq4k_chain_create(spq4k_ctx* c, const spq4k_chain_stage* stages, int n, flo
         if (!in.in0 || !aligned(in.in0, 16) || !aligned(in.in1, 16) || !aligned(in.x_out, 16) ||
             !aligned(in.norm_w, 16))
             return set_err(c, -EINVAL, "chain stage %d: null or misaligned input", s);
+        // A stage's outputs (y[j], x_out) overlap none of its inputs (in0,
+        // in1, norm_w) nor each other: the stage's rows and its residual
+        // store run concurrently with the reads of every input.
         const size_t xb = (size_t)K * sizeof(float);
-        for (int j = 0; j < in.n; ++j) {
+        const int ny = in.glu ? 1 : in.n;
+        for (int j = 0; j < ny; ++j) {
             const size_t yb = (size_t)(in.glu ? rows : in.W[j]->M) * sizeof(float);
-            if (in.glu && j == 1) break;
             if (overlaps(in.y[j], yb, in.in0, xb) || overlaps(in.y[j], yb, in.in1, xb) ||
-                overlaps(in.y[j], yb, in.x_out, xb))
+                overlaps(in.y[j], yb, in.norm_w, xb))
                 return set_err(c, -EINVAL, "chain stage %d: output %d overlaps the stage's inputs", s, j);
+            if (overlaps(in.y[j], yb, in.x_out, xb))
+                return set_err(c, -EINVAL, "chain stage %d: output %d overlaps x_out", s, j);
+            for (int k = 0; k < j; ++k)
+                if (overlaps(in.y[j], yb, in.y[k], (size_t)in.W[k]->M * sizeof(float)))
+                    return set_err(c, -EINVAL, "chain stage %d: outputs %d and %d overlap", s, k, j);
         }
-        if (overlaps(in.x_out, xb, in.in0, xb) || overlaps(in.x_out, xb, in.in1, xb))
+        if (overlaps(in.x_out, xb, in.in0, xb) || overlaps(in.x_out, xb, in.in1, xb) ||
+            overlaps(in.x_out, xb, in.norm_w, xb))
             return set_err(c, -EINVAL, "chain stage %d: x_out overlaps the stage's inputs", s);
         o.rows = (int32_t)rows;
         o.nb = (int32_t)(K / SPQ4K_QK_K);

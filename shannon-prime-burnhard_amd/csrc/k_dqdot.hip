@@ -989,27 +989,30 @@ hipError_t launch_beast_down_np(const uint8_t* down, size_t dn_bytes, int n_embd
     return hipGetLastError();
 }
 
-hipError_t launch_beast_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* down, int E, int n_embd, int n_ff,
-                            const float* logits, int top_k, const float* hidden, float* out, int32_t* ids,
-                            float* scores, float* H, int num_cus, hipStream_t st) {
+hipError_t launch_beast_route(const float* logits, int E, int top_k, int32_t* ids, float* scores, hipStream_t st) {
+    if (E < 1 || E > BEAST_MAX_EXPERTS || top_k < 1 || top_k > BEAST_MAX_TOPK) return hipErrorInvalidValue;
+    const size_t lds_rt = (size_t)((E + 3) & ~3) * sizeof(float) + (E > 256 ? (size_t)(E - 256 + 63) / 64 * 64 * 8 : 0);
+    hipLaunchKernelGGL(beast_route_kernel, dim3(1), dim3(64), lds_rt, st, logits, E, top_k, ids, scores);
+    return hipGetLastError();
+}
+
+hipError_t launch_beast_route_gate_up(const uint8_t* gate, const uint8_t* up, int E, int n_embd, int n_ff,
+                                      const float* logits, int top_k, const float* hidden, int32_t* ids,
+                                      float* scores, float* H, int num_cus, hipStream_t st) {
     if (E < 1 || E > BEAST_MAX_EXPERTS || top_k < 1 || top_k > BEAST_MAX_TOPK || n_embd % 256 || n_ff % 256)
         return hipErrorInvalidValue;
-    const int nb_e = n_embd / 256, nb_f = n_ff / 256;
-    const size_t lds_e = dequant_matvec_lds_bytes(1, nb_e), lds_f = dequant_matvec_lds_bytes(1, nb_f);
-    if (lds_e > DQ_MATVEC_LDS_MAX || lds_f > DQ_MATVEC_LDS_MAX) return hipErrorInvalidValue;
+    const int nb_e = n_embd / 256;
+    const size_t lds_e = dequant_matvec_lds_bytes(1, nb_e);
+    if (lds_e > DQ_MATVEC_LDS_MAX) return hipErrorInvalidValue;
     const size_t gu_bytes = (size_t)n_ff * nb_e * Q4K_BYTES;
-    const size_t dn_bytes = (size_t)n_embd * nb_f * Q4K_BYTES;
     const int64_t want = (int64_t)num_cus * 4;
     hipError_t e;
     if (nb_e <= 16) {
         // the routing inside the gate / up launch
-        e = launch_beast_short_nb(nb_e, gate, up, down, gu_bytes, dn_bytes, n_embd, n_ff, nb_e, nb_f, logits, E, top_k,
-                                  ids, scores, hidden, H, out, true, num_cus, st);
+        e = launch_beast_short_nb(nb_e, gate, up, nullptr, gu_bytes, 0, n_embd, n_ff, nb_e, 0, logits, E, top_k, ids,
+                                  scores, hidden, H, nullptr, true, num_cus, st);
     } else {
-        const size_t lds_rt =
-            (size_t)((E + 3) & ~3) * sizeof(float) + (E > 256 ? (size_t)(E - 256 + 63) / 64 * 64 * 8 : 0);
-        hipLaunchKernelGGL(beast_route_kernel, dim3(1), dim3(64), lds_rt, st, logits, E, top_k, ids, scores);
-        e = hipGetLastError();
+        e = launch_beast_route(logits, E, top_k, ids, scores, st);
         if (e != hipSuccess) return e;
         // about four workgroups a CU over top_k * n_ff sweep rows
         const int64_t total = (int64_t)top_k * n_ff;
@@ -1023,11 +1026,23 @@ hipError_t launch_beast_moe(const uint8_t* gate, const uint8_t* up, const uint8_
                       : launch_beast_gate_up_np<8>(gate, up, gu_bytes, n_ff, nb_e, ids, E, top_k, hidden, H, (int)rpw,
                                                    (int)((total + rpw - 1) / rpw), lds_e, st);
     }
-    if (e != hipSuccess) return e;
+    return e;
+}
+
+hipError_t launch_beast_down(const uint8_t* down, int E, int n_embd, int n_ff, const int32_t* ids,
+                             const float* scores, int top_k, const float* H, float* out, int num_cus,
+                             hipStream_t st) {
+    if (E < 1 || E > BEAST_MAX_EXPERTS || top_k < 1 || top_k > BEAST_MAX_TOPK || n_embd % 256 || n_ff % 256)
+        return hipErrorInvalidValue;
+    const int nb_f = n_ff / 256;
+    const size_t lds_f = dequant_matvec_lds_bytes(1, nb_f);
+    if (lds_f > DQ_MATVEC_LDS_MAX) return hipErrorInvalidValue;
+    const size_t dn_bytes = (size_t)n_embd * nb_f * Q4K_BYTES;
     // down and the weighted sum
     if (nb_f <= 16)
-        return launch_beast_short_nb(nb_f, gate, up, down, gu_bytes, dn_bytes, n_embd, n_ff, nb_e, nb_f, logits, E,
-                                     top_k, ids, scores, hidden, H, out, false, num_cus, st);
+        return launch_beast_short_nb(nb_f, nullptr, nullptr, down, 0, dn_bytes, n_embd, n_ff, 0, nb_f, nullptr, E,
+                                     top_k, const_cast<int32_t*>(ids), const_cast<float*>(scores), nullptr,
+                                     const_cast<float*>(H), out, false, num_cus, st);
     // rows in runs of a multiple of 4, at most BEAST_DOWN_RPW a wave, about two
     // workgroups a CU: each workgroup stages every selected expert's whole
     // hidden row, so longer runs read less of it again (4096 x 14336, top-2:

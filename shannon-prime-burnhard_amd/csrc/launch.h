@@ -277,16 +277,36 @@ constexpr size_t DQ_MATVEC_LDS_MAX = 128 * 1024;
 // the BurnHard MoE forward (k_dqdot.hip): routing of E <= BEAST_MAX_EXPERTS
 // logits to top_k <= BEAST_MAX_TOPK experts (ids, scores), H [top_k][n_ff]
 // the silu(gate) * up rows, out [n_embd]; Q4_K banks, n_embd and n_ff
-// multiples of 256 whose rows fit the x staging
+// multiples of 256 whose rows fit the x staging. Its parts: the routing
+// alone; routing + gate / up -> H; down and the weighted sum from H.
 constexpr int BEAST_MAX_EXPERTS = 4096;
 constexpr int BEAST_MAX_TOPK = 16;
 constexpr int BEAST_DOWN_RPW = 8;
-hipError_t launch_beast_moe(const uint8_t* gate, const uint8_t* up, const uint8_t* down, int E, int n_embd, int n_ff,
-                            const float* logits, int top_k, const float* hidden, float* out, int32_t* ids,
-                            float* scores, float* H, int num_cus, hipStream_t st);
+hipError_t launch_beast_route(const float* logits, int E, int top_k, int32_t* ids, float* scores, hipStream_t st);
+hipError_t launch_beast_route_gate_up(const uint8_t* gate, const uint8_t* up, int E, int n_embd, int n_ff,
+                                      const float* logits, int top_k, const float* hidden, int32_t* ids,
+                                      float* scores, float* H, int num_cus, hipStream_t st);
+hipError_t launch_beast_down(const uint8_t* down, int E, int n_embd, int n_ff, const int32_t* ids,
+                             const float* scores, int top_k, const float* H, float* out, int num_cus,
+                             hipStream_t st);
 size_t dequant_matvec_lds_bytes(int T, int nb);
 hipError_t launch_dequant_matvec(const uint8_t* W, int M, int nb, const float* X, int64_t x_tstride, float* Y,
                                  int64_t y_tstride, int T, int num_cus, hipStream_t st);
+
+// The same dequant-then-dot for rows of any library type (k_dqdot_x.hip;
+// type = SPQ4K_TYPE_Q4_K, _Q5_K, _Q6_K or _Q8_0; K a multiple of the type's
+// block): dense rows (T <= DQ_MATVEC_MAX_T tokens), the selected experts'
+// rows of one bank against one hidden row (H[s][r] = the dot, or with
+// finish H[s][r] = silu(H[s][r]) * the dot), and the down rows' score-weighted
+// sum out[i] over the selected experts in rank order.
+size_t dqx_lds_bytes(int type, int64_t K, int T);
+hipError_t launch_dqx_matvec(int type, const uint8_t* W, int M, int64_t K, const float* X, int64_t x_tstride,
+                             float* Y, int64_t y_tstride, int T, int num_cus, hipStream_t st);
+hipError_t launch_dqx_experts(int type, bool finish, const uint8_t* bank, int E, int rows, int64_t K,
+                              const int32_t* ids, int top_k, const float* hidden, float* H, int num_cus,
+                              hipStream_t st);
+hipError_t launch_dqx_down(int type, const uint8_t* down, int E, int n_embd, int64_t n_ff, const int32_t* ids,
+                           const float* scores, int top_k, const float* H, float* out, int num_cus, hipStream_t st);
 
 // A chain of dependent T = 1 Q4_K matvec stages in one persistent launch
 // (k_chain.hip). Stage s: x = in0 (+ in1); xout = x when set; x = rms_norm(x)

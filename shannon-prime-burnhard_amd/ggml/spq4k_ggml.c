@@ -118,11 +118,16 @@ static void fail(spq4k_ggml *b, struct ggml_tensor *dst, int code, const char *w
     free(nan);
 }
 
-/* whether t lives in a device (non-host) backend buffer -- on a HIP build of
- * ggml, device memory of this GPU that spq4k can use in place */
-static int on_device(const struct ggml_tensor *t) {
+/* whether t lives in device memory of the binding's GPU, which spq4k can use
+ * in place: a buffer that is not host memory (is_host false, as a HIP build of
+ * ggml's device buffers) whose data the HIP runtime confirms as this GPU's
+ * device memory. ggml's CPU extra buffer types (repack, AMX) and other
+ * backends' buffers report is_host false too; their tensors take the copy
+ * path. */
+static int on_device(const spq4k_ggml *b, const struct ggml_tensor *t) {
     const struct ggml_tensor *s = t->view_src ? t->view_src : t;
-    return s->buffer && !ggml_backend_buffer_is_host(s->buffer);
+    return s->buffer && !ggml_backend_buffer_is_host(s->buffer) && t->data &&
+           spq4k_ptr_on_device(b->ctx, t->data, ggml_nbytes(t)) == 1;
 }
 
 /* tensor bytes in host memory: the tensor's own when it has no backend
@@ -162,7 +167,7 @@ static int resident_weight(spq4k_ggml *b, const struct ggml_tensor *W, int64_t M
     }
     spq4k_weights *w = NULL;
     int rc;
-    if (on_device(W)) {
+    if (on_device(b, W)) {
         /* already in device memory: adopt it in place, no copy */
         rc = spq4k_weights_wrap_type(b->ctx, (int)W->type, W->data, M, K, E, &w);
     } else {
@@ -190,7 +195,7 @@ static void run_mul_mat(struct ggml_tensor *dst, int ith, int nth, void *userdat
         fail(b, dst, rc, "spq4k_ggml_mul_mat: weight upload");
         return;
     }
-    if (on_device(x) && on_device(dst)) {
+    if (on_device(b, x) && on_device(b, dst)) {
         /* device-resident node: the activations and the output stay on the GPU */
         rc = spq4k_mul_mat(b->ctx, w, (const float *)x->data, (float *)dst->data, T);
         if (!rc) rc = spq4k_synchronize(b->ctx);
@@ -227,7 +232,7 @@ static void run_mul_mat_id(struct ggml_tensor *dst, int ith, int nth, void *user
         fail(b, dst, rc, "spq4k_ggml_mul_mat_id: weight upload");
         return;
     }
-    if (on_device(x) && on_device(ids) && on_device(dst)) {
+    if (on_device(b, x) && on_device(b, ids) && on_device(b, dst)) {
         rc = spq4k_moe(b->ctx, w, (const int32_t *)ids->data, n_used, ne11, T, (const float *)x->data,
                        (float *)dst->data);
         if (!rc) rc = spq4k_synchronize(b->ctx);
@@ -263,7 +268,7 @@ static void run_moe_ffn(struct ggml_tensor *dst, int ith, int nth, void *userdat
         fail(b, dst, rc, "spq4k_ggml_moe_ffn: weight upload");
         return;
     }
-    if (on_device(cur) && on_device(sel) && on_device(wts) && on_device(dst)) {
+    if (on_device(b, cur) && on_device(b, sel) && on_device(b, wts) && on_device(b, dst)) {
         rc = spq4k_moe_ffn(b->ctx, wg, wu, wd, (const int32_t *)sel->data, (const float *)wts->data, n_used, T,
                            (const float *)cur->data, (float *)dst->data);
         if (!rc) rc = spq4k_synchronize(b->ctx);

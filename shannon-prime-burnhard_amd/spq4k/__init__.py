@@ -111,6 +111,7 @@ def load_library(path: str | None = None):
         "spq4k_subblock_sums": (I, [V, V, I64, I64, V, V]),
         "spq4k_weights_upload_type": (I, [V, I, V, I64, I64, I64, PV]),
         "spq4k_weights_wrap_type": (I, [V, I, V, I64, I64, I64, PV]),
+        "spq4k_ptr_on_device": (I, [V, V, S]),
         "spq4k_weights_alloc_type": (I, [V, I, I64, I64, I64, PV]),
         "spq4k_weights_type": (I, [V]),
         "spq4k_to_float": (I, [V, I, V, V, I64]),

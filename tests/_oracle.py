@@ -56,6 +56,8 @@ class Oracle:
         L.or_mul_mat_dq_f64_type.restype = I
         L.or_beast_matvec_type.argtypes = [I, V, I64, I64, V, V]
         L.or_beast_matvec_type.restype = I
+        L.or_beast_moe_routed.argtypes = [I, V, I, V, I, V, I64, I64, I64, V, V, I64, V, V]
+        L.or_beast_moe_routed.restype = I
         L.or_synth_fill.argtypes = [V, I64, U64, I, I64, F, F, F, I64]
         L.or_rms_norm.argtypes = [V, I64, I64, V, F, V]
         L.or_swiglu.argtypes = [V, V, I64, V]
@@ -241,10 +243,14 @@ class Oracle:
         return Y
 
     def quantize(self, qtype, x):
+        """weights of the type (Q8_0 with the model-file encoder)"""
+        if qtype == TYPE_Q8_0:
+            return self.quantize_q8_0(x, ref_encoder=True)
         return {TYPE_Q4_K: self.quantize_q4K, TYPE_Q5_K: self.quantize_q5K, TYPE_Q6_K: self.quantize_q6K}[qtype](x)
 
     def to_float(self, qtype, q, k):
-        return {TYPE_Q4_K: self.dequant, TYPE_Q5_K: self.dequant_q5K, TYPE_Q6_K: self.dequant_q6K}[qtype](q, k)
+        return {TYPE_Q4_K: self.dequant, TYPE_Q5_K: self.dequant_q5K, TYPE_Q6_K: self.dequant_q6K,
+                TYPE_Q8_0: self.dequant_q8_0}[qtype](q, k)
 
     def mul_mat_type(self, qtype, W, M, K, X, order=1):
         X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
@@ -323,6 +329,19 @@ class Oracle:
         y = np.empty(M, np.float32)
         assert self.L.or_beast_matvec_type(qtype, _p(np.ascontiguousarray(W)), M, K, _p(x), _p(y)) == 0
         return y
+
+    def beast_moe_routed(self, types, gate, up, down, E, n_embd, n_ff, ids, scores, hidden) -> np.ndarray:
+        """the MoE forward's per-expert loop over a given routing, a type per
+        bank (types = (gate, up, down))"""
+        ids = np.ascontiguousarray(ids, np.int32).ravel()
+        scores = np.ascontiguousarray(scores, np.float32).ravel()
+        hidden = np.ascontiguousarray(hidden, np.float32).ravel()
+        out = np.empty(n_embd, np.float32)
+        rc = self.L.or_beast_moe_routed(types[0], _p(np.ascontiguousarray(gate)), types[1],
+                                        _p(np.ascontiguousarray(up)), types[2], _p(np.ascontiguousarray(down)), E,
+                                        n_embd, n_ff, _p(ids), _p(scores), ids.size, _p(hidden), _p(out))
+        assert rc == 0
+        return out
 
     def synth(self, n, seed, dist=0, cols=0, mean=0.0, std=1.0, mult=1.0, offset=0) -> np.ndarray:
         out = np.empty(n, np.float32)
@@ -523,6 +542,8 @@ class BeastRef:
         self.L.ref_beast_route.restype = I
         self.L.ref_beast_moe.argtypes = [V, V, V, C.c_uint, I, I, I, V, I, V, V, V, V]
         self.L.ref_beast_moe.restype = I
+        self.L.ref_beast_moe_types.argtypes = [V, C.c_uint, V, C.c_uint, V, C.c_uint, I, I, I, V, I, V, V, V, V]
+        self.L.ref_beast_moe_types.restype = I
 
     def matvec(self, qtype, W, M, K, x):
         x = np.ascontiguousarray(x, np.float32).ravel()
@@ -540,15 +561,17 @@ class BeastRef:
         return ids[:n].copy(), scores[:n].copy()
 
     def moe(self, qtype, gate, up, down, E, n_embd, n_ff, logits, top_k, hidden):
-        """sp_beast_moe_forward (:455-562) on contiguous expert banks: output, ids, scores"""
+        """sp_beast_moe_forward (:455-562) on contiguous expert banks: output,
+        ids, scores; qtype one type for all banks or a (gate, up, down) tuple"""
+        types = tuple(qtype) if isinstance(qtype, (tuple, list)) else (qtype,) * 3
         logits = np.ascontiguousarray(logits, np.float32).ravel()
         hidden = np.ascontiguousarray(hidden, np.float32).ravel()
         out = np.empty(n_embd, np.float32)
         ids = np.empty(E, np.int32)
         scores = np.empty(E, np.float32)
-        n = self.L.ref_beast_moe(_p(np.ascontiguousarray(gate)), _p(np.ascontiguousarray(up)),
-                                 _p(np.ascontiguousarray(down)), qtype, E, n_embd, n_ff, _p(logits), top_k,
-                                 _p(hidden), _p(out), _p(ids), _p(scores))
+        n = self.L.ref_beast_moe_types(_p(np.ascontiguousarray(gate)), types[0], _p(np.ascontiguousarray(up)),
+                                       types[1], _p(np.ascontiguousarray(down)), types[2], E, n_embd, n_ff,
+                                       _p(logits), top_k, _p(hidden), _p(out), _p(ids), _p(scores))
         assert n > 0
         return out, ids[:n].copy(), scores[:n].copy()
 

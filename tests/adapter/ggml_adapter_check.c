@@ -305,6 +305,41 @@ static struct ggml_backend_buffer_type dv_buft = {
     .iface = {.get_name = dvt_name, .alloc_buffer = dvt_alloc, .get_alignment = dvt_align, .is_host = dvt_is_host},
 };
 
+/* A buffer type in plain host memory (malloc) that reports is_host false, as
+ * ggml's CPU extra buffer types (repack, AMX) and other backends' buffers do:
+ * its tensors are not this GPU's memory and must take the adapter's copy
+ * path. */
+static void hm_free(ggml_backend_buffer_t buf) { free(buf->context); }
+static void hm_memset(ggml_backend_buffer_t buf, struct ggml_tensor *t, uint8_t v, size_t off, size_t size) {
+    (void)buf;
+    memset((char *)t->data + off, v, size);
+}
+static void hm_set(ggml_backend_buffer_t buf, struct ggml_tensor *t, const void *d, size_t off, size_t size) {
+    (void)buf;
+    memcpy((char *)t->data + off, d, size);
+}
+static void hm_get(ggml_backend_buffer_t buf, const struct ggml_tensor *t, void *d, size_t off, size_t size) {
+    (void)buf;
+    memcpy(d, (const char *)t->data + off, size);
+}
+static void hm_clear(ggml_backend_buffer_t buf, uint8_t v) { memset(buf->context, v, buf->size); }
+static const struct ggml_backend_buffer_i hm_iface = {
+    .free_buffer = hm_free, .get_base = dv_base, .memset_tensor = hm_memset, .set_tensor = hm_set,
+    .get_tensor = hm_get, .clear = hm_clear,
+};
+static const char *hmt_name(ggml_backend_buffer_type_t t) {
+    (void)t;
+    return "spq4k-test-hostmem-not-host";
+}
+static ggml_backend_buffer_t hmt_alloc(ggml_backend_buffer_type_t t, size_t size) {
+    void *p = aligned_alloc(256, ((size ? size : 256) + 255) & ~(size_t)255);
+    if (!p) return NULL;
+    return ggml_backend_buffer_init(t, hm_iface, p, size);
+}
+static struct ggml_backend_buffer_type hm_buft = {
+    .iface = {.get_name = hmt_name, .alloc_buffer = hmt_alloc, .get_alignment = dvt_align, .is_host = dvt_is_host},
+};
+
 static int compute_graph(struct ggml_tensor *out, int nthreads) {
     struct ggml_init_params ip = {(size_t)16 << 20, NULL, false};
     struct ggml_context *gctx = ggml_init(ip);
@@ -320,15 +355,17 @@ static int compute_graph(struct ggml_tensor *out, int nthreads) {
 }
 
 /* The same node on host tensors (ggml's own MUL_MAT / the stock routed-expert
- * graph, y_ref) and on device-resident tensors through the adapter (y_ada).
+ * graph, y_ref) and through the adapter (y_ada) on tensors in a backend
+ * buffer that is not host memory: GPU memory (check_device) or host memory
+ * behind is_host false (check_hostmem_not_host).
  * mode 0: y [M, T] = W [K, M] x x [K, T] of ggml type `type`; mode 1: the
  * routed-expert FFN block (gate / up Q4_K [K, M, E], down of `type`
  * [M, K, E], n_used of E experts, ids_in / w_in [T][n_used]). Returns 0, or
  * the step that failed; *wrapped is set when the binding adopted the device
  * weight in place (its resident copy is W->data). */
-int check_device(int mode, int type, int64_t M, int64_t K, int64_t E, int64_t n_used, int64_t T,
-                 const int32_t *ids_in, const float *w_in, uint64_t seed, int nthreads, float *y_ref, float *y_ada,
-                 int *wrapped, char *err, int errlen) {
+static int check_in(ggml_backend_buffer_type_t buft, int mode, int type, int64_t M, int64_t K, int64_t E,
+                    int64_t n_used, int64_t T, const int32_t *ids_in, const float *w_in, uint64_t seed, int nthreads,
+                    float *y_ref, float *y_ada, int *wrapped, char *err, int errlen) {
     spq4k_ggml *b;
     int rc = spq4k_ggml_init(0, &b);
     if (rc) {
@@ -376,7 +413,7 @@ int check_device(int mode, int type, int64_t M, int64_t K, int64_t E, int64_t n_
     int step = 0;
     ggml_backend_buffer_t dbuf = NULL;
     if (!ya) step = 1;
-    if (!step && !(dbuf = ggml_backend_alloc_ctx_tensors_from_buft(dctx, &dv_buft))) step = 2;
+    if (!step && !(dbuf = ggml_backend_alloc_ctx_tensors_from_buft(dctx, buft))) step = 2;
     if (!step) {
         for (int i = 0; i < nsrc; ++i) ggml_backend_tensor_set(dsrc[i], hsrc[i]->data, 0, ggml_nbytes(hsrc[i]));
         if (compute_graph(yr, nthreads) || compute_graph(ya, 1)) step = 3;
@@ -388,12 +425,26 @@ int check_device(int mode, int type, int64_t M, int64_t K, int64_t E, int64_t n_
         const struct ggml_tensor *W = mode ? dsrc[3] : dsrc[0];
         *wrapped = spq4k_ggml_resident_data(b, W) == W->data;
     }
-    if (step) snprintf(err, errlen, "device-resident check step %d: %s", step, spq4k_ggml_last_error(b));
+    if (step) snprintf(err, errlen, "%s check step %d: %s", ggml_backend_buft_name(buft), step, spq4k_ggml_last_error(b));
     spq4k_ggml_free(b);
     if (dbuf) ggml_backend_buffer_free(dbuf);
     ggml_free(dctx);
     ggml_free(hctx);
     return step;
+}
+
+int check_device(int mode, int type, int64_t M, int64_t K, int64_t E, int64_t n_used, int64_t T,
+                 const int32_t *ids_in, const float *w_in, uint64_t seed, int nthreads, float *y_ref, float *y_ada,
+                 int *wrapped, char *err, int errlen) {
+    return check_in(&dv_buft, mode, type, M, K, E, n_used, T, ids_in, w_in, seed, nthreads, y_ref, y_ada, wrapped,
+                    err, errlen);
+}
+
+int check_hostmem_not_host(int mode, int type, int64_t M, int64_t K, int64_t E, int64_t n_used, int64_t T,
+                           const int32_t *ids_in, const float *w_in, uint64_t seed, int nthreads, float *y_ref,
+                           float *y_ada, int *wrapped, char *err, int errlen) {
+    return check_in(&hm_buft, mode, type, M, K, E, n_used, T, ids_in, w_in, seed, nthreads, y_ref, y_ada, wrapped,
+                    err, errlen);
 }
 
 /* A small dense decoder built twice in one graph of the reference's ggml --

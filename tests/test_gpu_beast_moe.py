@@ -18,7 +18,7 @@ import os
 import numpy as np
 import pytest
 
-from _oracle import BEAST_SO, TYPE_Q4_K, BeastRef, close_enough, parity_ok
+from _oracle import BEAST_SO, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, BeastRef, close_enough, parity_ok
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -30,18 +30,18 @@ def _check(got, exp, what, exact=None):
     assert ok.all(), f"{what}: {int((~ok).sum())}/{ok.size} outside tolerance, first {np.argwhere(~ok)[0]}"
 
 
-def _forward_f64(oracle, Wg, Wu, Wd, E, n_embd, n_ff, ids, scores, hidden):
+def _forward_f64(oracle, Wg, Wu, Wd, E, n_embd, n_ff, ids, scores, hidden, types=(TYPE_Q4_K,) * 3):
     """sp_beast_moe_forward's sum over the selected experts in double: each
     expert's dequantised banks (fp32 values, exact in double) against the fp32
     hidden state, silu(g) * u, down, score-weighted"""
-    def deq(bank, e, rows, cols):
+    def deq(t, bank, e, rows, cols):
         eb = bank.size // E
-        return oracle.dequant(bank[e * eb:(e + 1) * eb], rows * cols).reshape(rows, cols).astype(np.float64)
+        return oracle.to_float(t, bank[e * eb:(e + 1) * eb], rows * cols).reshape(rows, cols).astype(np.float64)
     x = hidden.astype(np.float64)
     y = np.zeros(n_embd)
     for e, sc in zip(ids, scores):
-        g, u = deq(Wg, e, n_ff, n_embd) @ x, deq(Wu, e, n_ff, n_embd) @ x
-        y += float(sc) * (deq(Wd, e, n_embd, n_ff) @ (g / (1.0 + np.exp(-g)) * u))
+        g, u = deq(types[0], Wg, e, n_ff, n_embd) @ x, deq(types[1], Wu, e, n_ff, n_embd) @ x
+        y += float(sc) * (deq(types[2], Wd, e, n_embd, n_ff) @ (g / (1.0 + np.exp(-g)) * u))
     return y
 
 
@@ -153,15 +153,94 @@ def test_beast_moe_device_pointers_and_rejects(ctx):
     ctx.synchronize()
     assert np.array_equal(od.to_host().view(np.uint32), y_host.view(np.uint32))
     assert ids_host.tolist() == [1, 3]
-    q6 = ctx.upload(o.quantize_q6K((rng.standard_normal((E * n, n)) * 0.05).astype(np.float32)), n, n, E=E,
-                    type=14)
-    with pytest.raises(spq4k.Spq4kError):
-        ctx.beast_moe_forward(q6, banks[1], banks[2], logits, 2, hidden)
     wide = ctx.upload(o.quantize_q4K((rng.standard_normal((E * n, 2 * n)) * 0.05).astype(np.float32)), n, 2 * n,
                       E=E)
     with pytest.raises(spq4k.Spq4kError):
         ctx.beast_moe_forward(banks[0], banks[1], wide, logits, 2, hidden)
+    q6 = ctx.upload(o.quantize_q6K((rng.standard_normal((E * 2 * n, n)) * 0.05).astype(np.float32)), 2 * n, n, E=E,
+                    type=TYPE_Q6_K)
+    with pytest.raises(spq4k.Spq4kError):       # a gate bank of another shape than up's, whatever its type
+        ctx.beast_moe_forward(q6, banks[1], banks[2], logits, 2, hidden)
     for w in banks + [q6, wide]:
         w.free()
     for d in (ld, hd, od):
         d.free()
+
+
+def _mixed_banks(oracle, rng, types, E, n_embd, n_ff):
+    def bank(t, rows, cols):
+        return oracle.quantize(t, rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.03))
+    return bank(types[0], E * n_ff, n_embd), bank(types[1], E * n_ff, n_embd), bank(types[2], E * n_embd, n_ff)
+
+
+def _upload3(ctx, types, Wg, Wu, Wd, E, n_embd, n_ff):
+    return (ctx.upload(Wg, n_ff, n_embd, E=E, type=types[0]), ctx.upload(Wu, n_ff, n_embd, E=E, type=types[1]),
+            ctx.upload(Wd, n_embd, n_ff, E=E, type=types[2]))
+
+
+@pytest.mark.skipif(not os.path.exists(BEAST_SO), reason="oracle/_ref/beast (the reference) not built")
+@pytest.mark.parametrize("types", [(TYPE_Q8_0,) * 3, (TYPE_Q4_K, TYPE_Q4_K, TYPE_Q8_0), (TYPE_Q8_0, TYPE_Q8_0, TYPE_Q4_K),
+                                   (TYPE_Q8_0, TYPE_Q4_K, TYPE_Q8_0)])
+@pytest.mark.parametrize("E,k,n_embd,n_ff", [(32, 8, 2048, 768), (8, 2, 1024, 4352), (4, 3, 4608, 512),
+                                             (6, 2, 256, 256)])
+def test_beast_moe_q8_0_banks_vs_reference(ctx, oracle, types, E, k, n_embd, n_ff):
+    """Q8_0 banks, alone and beside Q4_K ones, against the reference's own
+    forward (its beast_dequant_q8_0 is the format's): the same experts and
+    scores, the output within close_enough of the reference's or of the
+    forward in double"""
+    rng = np.random.default_rng(E + k + n_embd + sum(types))
+    Wg, Wu, Wd = _mixed_banks(oracle, rng, types, E, n_embd, n_ff)
+    logits = (rng.standard_normal(E) * 2.0).astype(np.float32)
+    hidden = rng.standard_normal(n_embd).astype(np.float32)
+    y_ref, ids_ref, sc_ref = BeastRef().moe(types, Wg, Wu, Wd, E, n_embd, n_ff, logits, k, hidden)
+    banks = _upload3(ctx, types, Wg, Wu, Wd, E, n_embd, n_ff)
+    y, ids, sc = ctx.beast_moe_forward(*banks, logits, k, hidden)
+    assert np.array_equal(ids, ids_ref), f"experts {ids} against {ids_ref}"
+    np.testing.assert_allclose(sc, sc_ref, rtol=2e-6)
+    _check(y, y_ref, f"types {types} E={E} k={k} {n_embd}->{n_ff}",
+           _forward_f64(oracle, Wg, Wu, Wd, E, n_embd, n_ff, ids_ref, sc_ref, hidden, types))
+    for w in banks:
+        w.free()
+
+
+@pytest.mark.skipif(not os.path.exists(BEAST_SO), reason="oracle/_ref/beast (the reference) not built")
+@pytest.mark.parametrize("types", [(TYPE_Q4_K, TYPE_Q4_K, TYPE_Q6_K), (TYPE_Q6_K,) * 3, (TYPE_Q5_K, TYPE_Q5_K, TYPE_Q6_K),
+                                   (TYPE_Q8_0, TYPE_Q8_0, TYPE_Q6_K)])
+@pytest.mark.parametrize("E,k,n_embd,n_ff", [(32, 8, 2048, 768), (8, 2, 4096, 1536), (4, 2, 512, 8448)])
+def test_beast_moe_q6k_down_vs_oracle(ctx, oracle, types, E, k, n_embd, n_ff):
+    """a Q6_K down bank (the Q4_K_M files' usual one) and Q5_K / Q6_K gate /
+    up banks: the reference's routing (its own build), and the output against
+    the oracle's forward over that routing with the formats' dequantisers
+    (the reference's beast_dequant_q5_K / _q6_K are not the formats') within
+    close_enough, or of the forward in double"""
+    rng = np.random.default_rng(3 * E + k + n_ff + sum(types))
+    Wg, Wu, Wd = _mixed_banks(oracle, rng, types, E, n_embd, n_ff)
+    logits = (rng.standard_normal(E) * 2.0).astype(np.float32)
+    hidden = rng.standard_normal(n_embd).astype(np.float32)
+    ids_ref, sc_ref = BeastRef().route(logits, k)
+    banks = _upload3(ctx, types, Wg, Wu, Wd, E, n_embd, n_ff)
+    y, ids, sc = ctx.beast_moe_forward(*banks, logits, k, hidden)
+    assert np.array_equal(ids, ids_ref), f"experts {ids} against {ids_ref}"
+    np.testing.assert_allclose(sc, sc_ref, rtol=2e-6)
+    y_or = oracle.beast_moe_routed(types, Wg, Wu, Wd, E, n_embd, n_ff, ids_ref, sc_ref, hidden)
+    _check(y, y_or, f"types {types} E={E} k={k} {n_embd}->{n_ff}",
+           _forward_f64(oracle, Wg, Wu, Wd, E, n_embd, n_ff, ids_ref, sc_ref, hidden, types))
+    for w in banks:
+        w.free()
+
+
+def test_beast_moe_q8_0_ragged_rows(ctx, oracle):
+    """Q8_0 banks whose rows are not a multiple of 256 values (n_embd 2880,
+    n_ff 1440: partial groups of eight blocks) against the oracle's forward"""
+    types = (TYPE_Q8_0,) * 3
+    E, k, n_embd, n_ff = 8, 4, 2880, 1440
+    rng = np.random.default_rng(11)
+    Wg, Wu, Wd = _mixed_banks(oracle, rng, types, E, n_embd, n_ff)
+    logits = (rng.standard_normal(E) * 2.0).astype(np.float32)
+    hidden = rng.standard_normal(n_embd).astype(np.float32)
+    banks = _upload3(ctx, types, Wg, Wu, Wd, E, n_embd, n_ff)
+    y, ids, sc = ctx.beast_moe_forward(*banks, logits, k, hidden)
+    y_or = oracle.beast_moe_routed(types, Wg, Wu, Wd, E, n_embd, n_ff, ids, sc, hidden)
+    _check(y, y_or, "ragged Q8_0", _forward_f64(oracle, Wg, Wu, Wd, E, n_embd, n_ff, ids, sc, hidden, types))
+    for w in banks:
+        w.free()

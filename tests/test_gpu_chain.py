@@ -284,12 +284,17 @@ def test_chain_rejects_bad_stages(ctx):
     W12, _ = _weights(ctx, 16, 12288, 5)
     x = DeviceArray(27648, np.float32)
     y = DeviceArray(4096, np.float32)
+    z = DeviceArray(16384, np.float32)
     good = {"W": [W], "y": [y.ptr], "in0": x.ptr}
     bad = [
         {"W": [W, W, W], "y": [y.ptr, y.ptr, y.ptr], "glu": 1, "in0": x.ptr},          # glu needs two
         {"W": [Wbig], "y": [y.ptr], "in0": x.ptr},                                        # K > 12288
         {"W": [W], "y": [y.ptr + 4], "in0": x.ptr},                                       # misaligned output
         {"W": [W], "y": [x.ptr + 64], "in0": x.ptr},                                      # output overlaps input
+        {"W": [W], "y": [z.ptr + 512], "in0": x.ptr, "norm_w": z.ptr},                    # output overlaps norm_w
+        {"W": [W, W], "y": [y.ptr, y.ptr + 128], "in0": x.ptr},                           # outputs overlap
+        {"W": [W], "y": [z.ptr + 256], "in0": x.ptr, "x_out": z.ptr},                     # output overlaps x_out
+        {"W": [W], "y": [y.ptr], "in0": x.ptr, "x_out": z.ptr, "norm_w": z.ptr + 4096},  # x_out overlaps norm_w
         {"W": [W12], "y": [y.ptr], "in0": x.ptr, "in1": x.ptr},                          # 2 x 12288 inputs
         {"W": [W], "y": [y.ptr], "in0": 0},                                               # no input
     ]

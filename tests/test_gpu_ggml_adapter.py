@@ -139,21 +139,25 @@ def test_adapter_resident_table(drv):
     assert rc == 0, err.value.decode()
 
 
-def _device_check(drv, mode, qtype, M, K, E, k, T, ids, w, seed):
+def _device_check(drv, mode, qtype, M, K, E, k, T, ids, w, seed, fn="check_device", want_wrapped=1):
     f32p = ctypes.POINTER(ctypes.c_float)
     i64 = ctypes.c_int64
-    drv.check_device.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64, i64, i64, i64, ctypes.POINTER(ctypes.c_int32),
-                                 f32p, ctypes.c_uint64, ctypes.c_int, f32p, f32p, ctypes.POINTER(ctypes.c_int),
-                                 ctypes.c_char_p, ctypes.c_int]
+    f = getattr(drv, fn)
+    f.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64, i64, i64, i64, ctypes.POINTER(ctypes.c_int32),
+                  f32p, ctypes.c_uint64, ctypes.c_int, f32p, f32p, ctypes.POINTER(ctypes.c_int),
+                  ctypes.c_char_p, ctypes.c_int]
     n = (M if mode == 0 else K) * T
     yr, ya = np.full(n, np.nan, np.float32), np.full(n, np.nan, np.float32)
-    wrapped = ctypes.c_int(0)
+    wrapped = ctypes.c_int(-1)
     err = ctypes.create_string_buffer(256)
-    rc = drv.check_device(mode, qtype, M, K, E, k, T, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
-                          w.ctypes.data_as(f32p), seed, 8, yr.ctypes.data_as(f32p), ya.ctypes.data_as(f32p),
-                          ctypes.byref(wrapped), err, 256)
+    rc = f(mode, qtype, M, K, E, k, T, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+           w.ctypes.data_as(f32p), seed, 8, yr.ctypes.data_as(f32p), ya.ctypes.data_as(f32p),
+           ctypes.byref(wrapped), err, 256)
     assert rc == 0, err.value.decode()
-    assert wrapped.value == 1, "the device-resident weight was copied instead of adopted in place"
+    if want_wrapped:
+        assert wrapped.value == 1, "the device-resident weight was copied instead of adopted in place"
+    else:
+        assert wrapped.value == 0, "a weight outside this GPU's memory was adopted in place"
     return yr, ya
 
 
@@ -182,6 +186,35 @@ def test_adapter_device_resident_moe_ffn(drv, T):
     assert np.isfinite(ya).all()
     rel = float(np.linalg.norm(ya.astype(np.float64) - yr) / np.linalg.norm(yr.astype(np.float64)))
     assert rel <= FF_NORMWISE, f"device-resident moe ffn T={T}: normwise {rel:.3e} > {FF_NORMWISE}"
+
+
+@pytest.mark.parametrize("qtype", [TYPE_Q4_K, TYPE_Q8_0])
+@pytest.mark.parametrize("M,K,T", [(512, 4096, 1), (300, 2048, 5)])
+def test_adapter_not_host_buffer_in_host_memory_is_copied(drv, qtype, M, K, T):
+    """A buffer that reports is_host false but holds plain host memory (as
+    ggml's CPU extra buffer types do) is not this GPU's memory: the adapter
+    must take the copy path -- the weight uploaded (its resident copy is not
+    W->data), the activations and output staged through the host -- and agree
+    with ggml's MUL_MAT as above. Deciding from is_host alone would hand host
+    pointers to the GPU kernels."""
+    none_i, none_f = np.zeros(1, np.int32), np.zeros(1, np.float32)
+    yr, ya = _device_check(drv, 0, qtype, M, K, 1, 1, T, none_i, none_f, 91 + T, fn="check_hostmem_not_host",
+                           want_wrapped=0)
+    _check(yr, ya, f"host-memory not-host buffer mul_mat type={qtype} M={M} K={K} T={T}")
+
+
+def test_adapter_not_host_buffer_moe_ffn_is_copied(drv):
+    """The routed-expert FFN block node on the same host-memory, is_host-false
+    buffer: copy path, normwise agreement with ggml's routed-expert graph."""
+    E, D, F, k, T = 16, 1024, 512, 4, 3
+    rng = np.random.default_rng(95)
+    ids = np.ascontiguousarray(np.argsort(-rng.standard_normal((T, E)), axis=1, kind="stable")[:, :k].astype(np.int32))
+    w = np.ascontiguousarray(rng.random((T, k)).astype(np.float32))
+    yr, ya = _device_check(drv, 1, TYPE_Q4_K, F, D, E, k, T, ids, w, 96, fn="check_hostmem_not_host",
+                           want_wrapped=0)
+    assert np.isfinite(ya).all()
+    rel = float(np.linalg.norm(ya.astype(np.float64) - yr) / np.linalg.norm(yr.astype(np.float64)))
+    assert rel <= FF_NORMWISE, f"not-host moe ffn T={T}: normwise {rel:.3e} > {FF_NORMWISE}"
 
 
 # ||logits_adapter - logits_ggml|| / ||logits_ggml|| after four layers: the

@@ -12,7 +12,7 @@ import os
 import numpy as np
 import pytest
 
-from _oracle import BEAST_SO, TYPE_Q4_K, BeastRef
+from _oracle import BEAST_SO, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, BeastRef
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 G = np.load(os.path.join(HERE, "golden", "beast_moe_golden.npz"))
@@ -75,3 +75,58 @@ def test_moe_golden_and_decomposition(oracle):
     # expf in the last place): normwise against the double sum
     err = np.linalg.norm(acc - y) / np.linalg.norm(acc)
     assert err < 1e-6, f"normwise {err:.2e}"
+
+
+def _banks(oracle, rng, types, E, n_embd, n_ff):
+    def bank(t, rows, cols):
+        return oracle.quantize(t, (rng.standard_normal((rows, cols)) * 0.03).astype(np.float32))
+    return bank(types[0], E * n_ff, n_embd), bank(types[1], E * n_ff, n_embd), bank(types[2], E * n_embd, n_ff)
+
+
+@live
+@pytest.mark.parametrize("types", [(TYPE_Q4_K,) * 3, (TYPE_Q8_0,) * 3, (TYPE_Q4_K, TYPE_Q4_K, TYPE_Q8_0),
+                                   (TYPE_Q8_0, TYPE_Q8_0, TYPE_Q4_K)])
+def test_moe_routed_is_the_reference_forward(oracle, types):
+    """or_beast_moe_routed (the per-expert loop over a given routing, a type
+    per bank) on the reference's own routing reproduces the reference's
+    forward bit for bit wherever the reference's dequantisers are the
+    formats' (Q4_K, Q8_0), mixed banks included"""
+    rng = np.random.default_rng(sum(types))
+    E, k, n_embd, n_ff = 8, 3, 512, 768
+    Wg, Wu, Wd = _banks(oracle, rng, types, E, n_embd, n_ff)
+    logits = (rng.standard_normal(E) * 2).astype(np.float32)
+    hidden = rng.standard_normal(n_embd).astype(np.float32)
+    y_ref, ids, sc = BeastRef().moe(types, Wg, Wu, Wd, E, n_embd, n_ff, logits, k, hidden)
+    y = oracle.beast_moe_routed(types, Wg, Wu, Wd, E, n_embd, n_ff, ids, sc, hidden)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("types", [(TYPE_Q4_K, TYPE_Q4_K, TYPE_Q6_K), (TYPE_Q6_K,) * 3, (TYPE_Q5_K,) * 3])
+def test_moe_routed_q5k_q6k_against_double(oracle, types):
+    """banks of Q5_K / Q6_K, whose reference dequantisers are not the
+    format's: the routed forward against the same forward in double over the
+    format's dequantised weights (normwise, fp32 rounding of each stage)"""
+    rng = np.random.default_rng(7 + sum(types))
+    E, n_embd, n_ff = 6, 512, 512
+    Wg, Wu, Wd = _banks(oracle, rng, types, E, n_embd, n_ff)
+    ids = np.array([4, 1, 5], np.int32)
+    sc = np.array([0.5, 0.3, 0.2], np.float32)
+    hidden = rng.standard_normal(n_embd).astype(np.float32)
+    y = oracle.beast_moe_routed(types, Wg, Wu, Wd, E, n_embd, n_ff, ids, sc, hidden)
+
+    def deq(t, bank, e, rows, cols):
+        eb = bank.size // E
+        return oracle.to_float(t, bank[e * eb:(e + 1) * eb], rows * cols).reshape(rows, cols).astype(np.float64)
+    x = hidden.astype(np.float64)
+    acc = np.zeros(n_embd)
+    for e, s in zip(ids, sc):
+        g, u = deq(types[0], Wg, e, n_ff, n_embd) @ x, deq(types[1], Wu, e, n_ff, n_embd) @ x
+        acc += float(s) * (deq(types[2], Wd, e, n_embd, n_ff) @ (g / (1.0 + np.exp(-g)) * u))
+    err = np.linalg.norm(acc - y) / np.linalg.norm(acc)
+    assert err < 1e-5, f"normwise {err:.2e}"
+    # an id outside the bank is skipped
+    y2 = oracle.beast_moe_routed(types, Wg, Wu, Wd, E, n_embd, n_ff, np.array([4, 99, 1], np.int32),
+                                 np.array([0.5, 0.3, 0.2], np.float32), hidden)
+    y3 = oracle.beast_moe_routed(types, Wg, Wu, Wd, E, n_embd, n_ff, np.array([4, 1], np.int32),
+                                 np.array([0.5, 0.2], np.float32), hidden)
+    assert np.array_equal(y2.view(np.uint32), y3.view(np.uint32))

@@ -14,6 +14,11 @@
 - or_beast_matvec_type: bit for bit against the reference's beast_matvec
   (desktop/beast_canyon/sp_beast_canyon.c:1122-1134) compiled from its source
   (golden vectors; live when oracle/_ref/beast is built), plus closed forms.
+  For Q5_K and Q6_K rows it runs beast_matvec's loop over the format's own
+  dequantiser (the reference's beast_dequant_q5_K / _q6_K read other bits,
+  which test_reference_q5k_q6k_dequant_is_not_the_format records): one-hot
+  inputs give the pinned dequantisers' weights bit for bit, and the loop is
+  the one the Q4_K / Q8_0 goldens pin.
 """
 import os
 from fractions import Fraction
@@ -154,3 +159,50 @@ def test_beast_closed_forms(oracle):
         for c in range(K):
             s = np.float32(s + np.float32(wd[r, c] * x[c]))
         assert _bits(oracle.beast_matvec(TYPE_Q4_K, W, M, K, x))[r] == _bits(np.array([s]))[0]
+
+
+@pytest.mark.parametrize("qtype", [TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, TYPE_Q4_K])
+def test_beast_one_hot_is_the_format_dequant(oracle, qtype):
+    """a one-hot input picks one weight of each row, times 1.0 plus zeros:
+    the format's dequantised weights (or_dequantize_row_*, pinned to the
+    reference's ggml by the golden vectors) bit for bit, at every position
+    class of the block (sub-block and nibble boundaries)"""
+    rng = np.random.default_rng(qtype)
+    M, K = 6, 512
+    W = oracle.quantize(qtype, (rng.standard_normal((M, K)) * 0.05).astype(np.float32))
+    wd = oracle.to_float(qtype, W, M * K).reshape(M, K)
+    for c in (0, 15, 16, 31, 32, 63, 64, 100, 127, 128, 191, 200, 255, 256, 300, 511):
+        x = np.zeros(K, np.float32)
+        x[c] = 1.0
+        # + 0.0: a weight of -0 (a negative scale times q = 0) sums to +0 from 0.0
+        assert np.array_equal(_bits(oracle.beast_matvec(qtype, W, M, K, x)), _bits(wd[:, c] + np.float32(0))), \
+            f"column {c}"
+    # and the sum is within fp32 reassociation of the exact dequant-then-dot
+    x = rng.standard_normal(K).astype(np.float32)
+    exact = oracle.mul_mat_dequant_f64(qtype, W, M, K, x[None, :])[0]
+    got = oracle.beast_matvec(qtype, W, M, K, x).astype(np.float64)
+    bound = 2 * K * np.finfo(np.float32).eps * (np.abs(wd.astype(np.float64)) @ np.abs(x.astype(np.float64)))
+    assert (np.abs(got - exact) <= bound).all()
+
+
+@pytest.mark.skipif(not os.path.exists(BEAST_SO), reason="oracle/_ref/beast (the reference's beast_matvec) not built")
+def test_reference_q5k_q6k_dequant_is_not_the_format(oracle):
+    """why the format's dequantiser is followed for Q5_K / Q6_K rows: the
+    reference's beast_matvec on those rows (beast_dequant_q5_K / _q6_K,
+    sp_beast_canyon.c:1025-1085) does not return the format's weights for
+    one-hot inputs, where for Q4_K and Q8_0 it does"""
+    b = BeastRef()
+    rng = np.random.default_rng(3)
+    M, K = 4, 256
+    differs = {}
+    for qtype in (TYPE_Q4_K, TYPE_Q8_0, TYPE_Q5_K, TYPE_Q6_K):
+        W = oracle.quantize(qtype, (rng.standard_normal((M, K)) * 0.05).astype(np.float32))
+        wd = oracle.to_float(qtype, W, M * K).reshape(M, K)
+        n = 0
+        for c in range(K):
+            x = np.zeros(K, np.float32)
+            x[c] = 1.0
+            n += int(not np.array_equal(b.matvec(qtype, W, M, K, x), wd[:, c]))
+        differs[qtype] = n
+    assert differs[TYPE_Q4_K] == 0 and differs[TYPE_Q8_0] == 0
+    assert differs[TYPE_Q5_K] > K // 4 and differs[TYPE_Q6_K] > K // 4, differs
