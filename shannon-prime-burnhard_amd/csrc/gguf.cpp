@@ -115,7 +115,7 @@ struct Cursor {
     }
     bool bytes(void* dst, uint64_t n) {
         if (remain < n) return false;
-        memcpy(dst, p, n);
+        if (n) memcpy(dst, p, n);   // an empty array's buffer may be null: no copy at all
         p += n;
         remain -= n;
         return true;

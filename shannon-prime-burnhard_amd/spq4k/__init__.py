@@ -123,30 +123,6 @@ def load_library(path: str | None = None):
         "spq4k_subblock_sums_type": (I, [V, I, V, I64, I64, V, V]),
         "spq4k_get_device": (I, [V]),
         "spq4k_weights_shape": (I, [V, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64)]),
-        "spq4k_gguf_open": (I, [C.c_char_p, PV]),
-        "spq4k_gguf_close": (None, [V]),
-        "spq4k_gguf_strerror": (C.c_char_p, []),
-        "spq4k_gguf_version": (C.c_uint32, [V]),
-        "spq4k_gguf_alignment": (S, [V]),
-        "spq4k_gguf_data_offset": (S, [V]),
-        "spq4k_gguf_data_size": (S, [V]),
-        "spq4k_gguf_file_size": (S, [V]),
-        "spq4k_gguf_n_kv": (I64, [V]),
-        "spq4k_gguf_find_key": (I64, [V, C.c_char_p]),
-        "spq4k_gguf_key": (C.c_char_p, [V, I64]),
-        "spq4k_gguf_kv_type": (I, [V, I64]),
-        "spq4k_gguf_arr_type": (I, [V, I64]),
-        "spq4k_gguf_arr_n": (I64, [V, I64]),
-        "spq4k_gguf_val_data": (V, [V, I64]),
-        "spq4k_gguf_val_str": (C.c_char_p, [V, I64, I64]),
-        "spq4k_gguf_n_tensors": (I64, [V]),
-        "spq4k_gguf_find_tensor": (I64, [V, C.c_char_p]),
-        "spq4k_gguf_tensor_name": (C.c_char_p, [V, I64]),
-        "spq4k_gguf_tensor_type": (I, [V, I64]),
-        "spq4k_gguf_tensor_shape": (I, [V, I64, C.POINTER(C.c_int64)]),
-        "spq4k_gguf_tensor_offset": (S, [V, I64]),
-        "spq4k_gguf_tensor_nbytes": (S, [V, I64]),
-        "spq4k_gguf_tensor_data": (V, [V, I64]),
         "spq4k_model_load": (I, [V, V, I, I, PV]),
         "spq4k_model_free": (None, [V]),
         "spq4k_model_weights": (V, [V, C.c_char_p]),
@@ -172,12 +148,70 @@ def load_library(path: str | None = None):
         "spq4k_chain_info": (I, [V, C.POINTER(I), C.POINTER(I), C.POINTER(I)]),
         "spq4k_chain_set_stamps": (I, [V, V, V]),
     }
+    sig.update(_gguf_sig())
+    _bind(lib, sig)
+    _lib = lib
+    return lib
+
+
+def _bind(lib, sig):
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    _lib = lib
-    return lib
+
+
+def _gguf_sig():
+    """the GGUF reader's entry points (include/spq4k_gguf.h)"""
+    V, I, I64, S = C.c_void_p, C.c_int, C.c_int64, C.c_size_t
+    PV = C.POINTER(C.c_void_p)
+    return {
+        "spq4k_gguf_open": (I, [C.c_char_p, PV]),
+        "spq4k_gguf_close": (None, [V]),
+        "spq4k_gguf_strerror": (C.c_char_p, []),
+        "spq4k_gguf_version": (C.c_uint32, [V]),
+        "spq4k_gguf_alignment": (S, [V]),
+        "spq4k_gguf_data_offset": (S, [V]),
+        "spq4k_gguf_data_size": (S, [V]),
+        "spq4k_gguf_file_size": (S, [V]),
+        "spq4k_gguf_n_kv": (I64, [V]),
+        "spq4k_gguf_find_key": (I64, [V, C.c_char_p]),
+        "spq4k_gguf_key": (C.c_char_p, [V, I64]),
+        "spq4k_gguf_kv_type": (I, [V, I64]),
+        "spq4k_gguf_arr_type": (I, [V, I64]),
+        "spq4k_gguf_arr_n": (I64, [V, I64]),
+        "spq4k_gguf_val_data": (V, [V, I64]),
+        "spq4k_gguf_val_str": (C.c_char_p, [V, I64, I64]),
+        "spq4k_gguf_n_tensors": (I64, [V]),
+        "spq4k_gguf_find_tensor": (I64, [V, C.c_char_p]),
+        "spq4k_gguf_tensor_name": (C.c_char_p, [V, I64]),
+        "spq4k_gguf_tensor_type": (I, [V, I64]),
+        "spq4k_gguf_tensor_shape": (I, [V, I64, C.POINTER(C.c_int64)]),
+        "spq4k_gguf_tensor_offset": (S, [V, I64]),
+        "spq4k_gguf_tensor_nbytes": (S, [V, I64]),
+        "spq4k_gguf_tensor_data": (V, [V, I64]),
+    }
+
+
+_gguf_lib = None
+
+
+def load_gguf_library():
+    """The library the GGUF reader is called in: libspq4k.so, or the one the
+    SPQ4K_GGUF_LIB environment variable names -- a host-only build of
+    csrc/gguf.cpp that exports the same entry points, such as the
+    AddressSanitizer / UndefinedBehaviorSanitizer build `make -C oracle asan`
+    makes and tests with."""
+    global _gguf_lib
+    if _gguf_lib is None:
+        p = os.environ.get("SPQ4K_GGUF_LIB")
+        if p:
+            lib = C.CDLL(p)
+            _bind(lib, _gguf_sig())
+            _gguf_lib = lib
+        else:
+            _gguf_lib = load_library()
+    return _gguf_lib
 
 
 class ChainStage(C.Structure):
@@ -255,7 +289,7 @@ class Gguf:
     mapping. Host only."""
 
     def __init__(self, path: str):
-        self.lib = load_library()
+        self.lib = load_gguf_library()
         h = C.c_void_p()
         rc = self.lib.spq4k_gguf_open(os.fsencode(path), C.byref(h))
         if rc != 0:
@@ -710,7 +744,7 @@ class Context:
                                                                   outlier_mult, offset))
 
 
-__all__ = ["Context", "Weights", "Spq4kError", "load_library", "LIB_PATH", "QK_K", "Q4K_BLOCK_BYTES",
+__all__ = ["Context", "Weights", "Spq4kError", "load_library", "load_gguf_library", "LIB_PATH", "QK_K", "Q4K_BLOCK_BYTES",
            "Q5K_BLOCK_BYTES", "Q6K_BLOCK_BYTES", "Q8K_BLOCK_BYTES", "QK8_0", "Q8_0_BLOCK_BYTES", "TYPE_Q8_0",
            "TYPE_Q4_K", "TYPE_Q5_K", "TYPE_Q6_K", "BLOCK_BYTES", "BLOCK_VALUES", "GEMV_MAX_T", "Gguf", "Model",
            "DIST_NORMAL", "DIST_STUDENT_T4"]

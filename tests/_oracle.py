@@ -8,7 +8,9 @@ import os
 import numpy as np
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-ORACLE_SO = os.path.join(REPO, "oracle", "liboracle_q4k.so")
+# SPQ4K_ORACLE_SO names another build of the oracle (the sanitizer build of
+# `make -C oracle asan`)
+ORACLE_SO = os.environ.get("SPQ4K_ORACLE_SO") or os.path.join(REPO, "oracle", "liboracle_q4k.so")
 REF_DIR = os.path.join(REPO, "oracle", "_ref")
 
 QK_K = 256
