@@ -753,6 +753,81 @@ def run_moe(args):
     ctx.close()
 
 
+def qtype_bytes(qtype, M, K):
+    return M * (K // spq4k.BLOCK_VALUES[qtype]) * spq4k.BLOCK_BYTES[qtype]
+
+
+def run_beastmix(args):
+    """The fp32-activation dequant-then-dot (spq4k_dequant_matvec) and the
+    BurnHard MoE forward (spq4k_beast_moe_forward) on the other weight types a
+    Q4_K model file carries: the Q6_K down banks of Q4_K_M files beside Q4_K
+    gate / up banks, and Q8_0 banks; configs[3] widths (128 experts of
+    2048 -> 768 -> 2048, top-8 of seeded N(0,1) logits, one token), 8 layers
+    of banks replayed as one graph (cold), all-Q4_K beside them. Then the
+    dense matvec of Q6_K and Q8_0 rows at 8B decode shapes (4096 x 4096 and
+    the down projection 4096 x 12288), 8 distinct matrices a shape (cold).
+    Algorithmic bytes: the chosen experts' weights (or the matrix) + fp32 in
+    and out."""
+    ctx = spq4k.Context(0)
+    Q4, Q6, Q8 = spq4k.TYPE_Q4_K, spq4k.TYPE_Q6_K, spq4k.TYPE_Q8_0
+    E, k, NL, n_embd, n_ff = 128, 8, 8, 2048, 768
+    syn = Synth(ctx, E * n_ff * n_embd)
+    lg = [DeviceArray.from_host(np.random.default_rng(50 + L).standard_normal(E).astype(np.float32))
+          for L in range(NL)]
+    xg = syn.activations(n_embd, 11)
+    Yb = DeviceArray(n_embd)
+    names = {Q4: "Q4_K", Q6: "Q6_K", Q8: "Q8_0"}
+    for types in ((Q4, Q4, Q6), (Q8, Q8, Q8), (Q4, Q4, Q4)):
+        shapes = ((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))
+        layers = [[syn.weights(M, K, 800 + 10 * L + i, qtype=t, E=E) for i, ((M, K), t) in
+                   enumerate(zip(shapes, types))] for L in range(NL)]
+        ctx.synchronize()
+        ctx.beast_moe_forward_dev(*layers[0], lg[0].ptr, k, xg.ptr, Yb.ptr)   # sizes the scratch
+        ctx.synchronize()
+        with Graph.capture(ctx.stream) as g:
+            for L in range(NL):
+                ctx.beast_moe_forward_dev(*layers[L], lg[L].ptr, k, xg.ptr, Yb.ptr)
+        ms = time_graph(ctx, g, max(5, args.steps // 5), 2) / NL
+        nbytes = k * sum(qtype_bytes(t, M, K) for (M, K), t in zip(shapes, types)) + 4 * (E + 2 * n_embd)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        print(json.dumps({"metric": "BurnHard MoE forward (routing, fp32 dequant-then-dot), T=1, "
+                                    f"gate/up/down {'/'.join(names[t] for t in types)}",
+                          "value": round(gbs, 1), "unit": "GB/s", "us_per_layer": round(ms * 1e3, 2),
+                          "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2),
+                          "config": {"workload": "128 experts of 2048 -> 768 -> 2048, top-8, "
+                                                 "8 layers of banks (cold)", "T": 1}}), flush=True)
+        for lay in layers:
+            for w in lay:
+                w.free()
+    for qtype in (Q6, Q8):
+        for (M, K) in ((4096, 4096), (4096, 12288)):
+            mats = [syn.weights(M, K, 900 + i, qtype=qtype) for i in range(8)]
+            x = syn.activations(K, 13)
+            y = DeviceArray(M)
+            ctx.synchronize()
+            with Graph.capture(ctx.stream) as g:
+                for w in mats:
+                    ctx.dequant_matvec_dev(w, x.ptr, y.ptr, 1)
+            ms = time_graph(ctx, g, max(5, args.steps // 5), 2) / len(mats)
+            nbytes = qtype_bytes(qtype, M, K) + 4 * (M + K)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            print(json.dumps({"metric": f"fp32-activation dequant-then-dot {names[qtype]}, T=1",
+                              "value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(ms * 1e3, 2),
+                              "pct_of_peak_hbm": round(gbs * 1e9 / PEAK_HBM * 100, 2),
+                              "config": {"workload": f"{M} x {K}, 8 distinct matrices (cold)", "T": 1}}),
+                  flush=True)
+            for w in mats:
+                w.free()
+            x.free()
+            y.free()
+    for a in lg:
+        a.free()
+    xg.free()
+    Yb.free()
+    syn.tmp.free()
+    ctx.close()
+
+
 def run_kquant(args, qtype):
     """The other types a Q4_K model file stores some tensors in (Q6_K:
     attn_v, ffn_down, output; Q5_K in Q5_K_M files; Q8_0 for small or
@@ -1032,7 +1107,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "q8_0",
-                                                          "single", "gguf", "fusion", "copy", "floor", "beastwide", "chain"])
+                                                          "single", "gguf", "fusion", "copy", "floor", "beastwide", "beastmix", "chain"])
     ap.add_argument("--M", type=int, default=4096, help="rows (--config single)")
     ap.add_argument("--K", type=int, default=4096, help="inputs (--config single)")
     ap.add_argument("--T", type=int, default=1, help="tokens (--config single)")
@@ -1040,7 +1115,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-chain", action="store_true", help="decode8b: skip the one-launch chain leg")
     ap.add_argument("--op", default="mul_mat", choices=["mul_mat", "dequant_matvec"],
-                    help="--config single: the entry point timed (dequant_matvec: Q4_K, fp32 activations)")
+                    help="--config single: the entry point timed (dequant_matvec: fp32 activations, any --qtype)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested). The Q4_K path "
@@ -1056,6 +1131,8 @@ def main():
         run_moe(args)
     elif args.config == "beastwide":
         run_beastwide(args)
+    elif args.config == "beastmix":
+        run_beastmix(args)
     elif args.config == "q6k":
         run_kquant(args, spq4k.TYPE_Q6_K)
     elif args.config == "q5k":
