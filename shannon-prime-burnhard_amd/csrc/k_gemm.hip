@@ -829,9 +829,10 @@ GemmPlan gemm_plan(const GemmParams& p, int num_cus, size_t max_partial_bytes) {
             if (g0 >= num_cus || (p.T >= 128 && rt >= 24)) cfg = 11;
             // From T = 256 on 12288 rows or more: the same 32x32 tiles in
             // 4-wave workgroups of 128 rows, two a CU, whose barriers do not
-            // hold all eight waves of a CU in step (24576 x 4096 at T = 512:
-            // 166 against 178 us; 6144 rows: 54.3 against 52.2; T = 128 on
-            // 24576 rows: 55.0 against 53.9)
+            // hold all eight waves of a CU in step (24576 x 4096 at T = 512,
+            // cold weights: 164-165 against 169 us, in one run of both; 6144
+            // rows: 54.3 against 52.2; T = 128 on 24576 rows: 55.0 against
+            // 53.9)
             if (cfg == 11 && p.T >= 256 && p.rows >= 12288) cfg = 32;
         }
     }
