@@ -2008,13 +2008,19 @@ int spq4k_beast_moe_forward(spq4k_ctx* c, const spq4k_weights* gate, const spq4k
         e = launch_beast_route_gate_up(gate->data, up->data, (int)E, (int)n_embd, (int)n_ff, router_logits, (int)top_k,
                                        hidden, rid, rsc, H, c->num_cus, c->stream);
     } else {
+        // gate and up in one launch when they share a type, else the gate
+        // rows into H and the up rows finishing it
         e = launch_beast_route(router_logits, (int)E, (int)top_k, rid, rsc, c->stream);
-        if (e == hipSuccess)
-            e = launch_dqx_experts(gate->type, false, gate->data, (int)E, (int)n_ff, n_embd, rid, (int)top_k, hidden, H,
-                                   c->num_cus, c->stream);
-        if (e == hipSuccess)
-            e = launch_dqx_experts(up->type, true, up->data, (int)E, (int)n_ff, n_embd, rid, (int)top_k, hidden, H,
-                                   c->num_cus, c->stream);
+        if (e == hipSuccess && gate->type == up->type) {
+            e = launch_dqx_experts(gate->type, 2, gate->data, up->data, (int)E, (int)n_ff, n_embd, rid, (int)top_k,
+                                   hidden, H, c->num_cus, c->stream);
+        } else if (e == hipSuccess) {
+            e = launch_dqx_experts(gate->type, 0, gate->data, nullptr, (int)E, (int)n_ff, n_embd, rid, (int)top_k,
+                                   hidden, H, c->num_cus, c->stream);
+            if (e == hipSuccess)
+                e = launch_dqx_experts(up->type, 1, up->data, nullptr, (int)E, (int)n_ff, n_embd, rid, (int)top_k,
+                                       hidden, H, c->num_cus, c->stream);
+        }
     }
     if (e != hipSuccess) return hip_fail(c, e, "beast moe gate / up launch");
     e = q4_dn ? launch_beast_down(down->data, (int)E, (int)n_embd, (int)n_ff, rid, rsc, (int)top_k, H, output,

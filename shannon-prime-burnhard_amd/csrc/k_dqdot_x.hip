@@ -295,6 +295,12 @@ __host__ __device__ constexpr int dqx_units(int64_t K) {
 }
 
 // ---- kernels -----------------------------------------------------------------
+// Each lane group walks the pieces of its rows (a piece: a pass of LPR / 4
+// groups of a row) with the next piece's loads in flight while it computes
+// the current one, across row boundaries too; the first piece's loads go out
+// before the activations are staged. Every load is unconditional (a row past
+// the end is clamped to a valid one and dropped), so the wait before a
+// piece's use counts exactly the loads issued after it.
 
 // dense rows: Y[t * y_ts + r] for r < M, t < nt <= T (tokens past nt are
 // neither staged nor stored; their products, of unstaged LDS, are dropped);
@@ -308,32 +314,51 @@ __global__ __launch_bounds__(256) void dqx_matvec_kernel(const uint8_t* __restri
     const int ngroup = dqx_groups<P>(K), nunit = dqx_units<P>(K);
     const int npass = (ngroup + GPP - 1) / GPP;
     const int tstride = npass * 16 * LPR;
-    for (int t = 0; t < nt; ++t) dqx_stage<P, LPR>(X + t * x_ts, K, dqx_x + (size_t)t * tstride);
-    __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane / LPR, ll = lane % LPR;
     const int l4 = ll & 3, gl = ll >> 2;
-    const lf32x4* xl = (const lf32x4*)dqx_x + ll;
     const int r0 = blockIdx.x * rows_per_wg;
     const int r1 = r0 + rows_per_wg < M ? r0 + rows_per_wg : M;
-    for (int rb = r0 + wave * RW; rb < r1; rb += 4 * RW) {      // uniform over the wave
+    // the wave's rows rb + grp, rb = r0 + wave RW, + 4 RW, ...
+    auto row_at = [&](int rb) {
         const int r = rb + grp;
-        const uint8_t* row = W + (size_t)(r < r1 ? r : r1 - 1) * row_bytes;
+        return W + (size_t)(r < r1 ? r : r1 - 1) * row_bytes;
+    };
+    int rb = r0 + wave * RW;
+    typename P::W cur = P::load(row_at(rb < r1 ? rb : r0), gl, l4, nunit);
+    for (int t = 0; t < nt; ++t) dqx_stage<P, LPR>(X + t * x_ts, K, dqx_x + (size_t)t * tstride);
+    __syncthreads();
+    const lf32x4* xl = (const lf32x4*)dqx_x + ll;
+    for (; rb < r1; rb += 4 * RW) {                                // uniform over the wave
+        const uint8_t* row = row_at(rb);
+        const uint8_t* nrow = row_at(rb + 4 * RW < r1 ? rb + 4 * RW : rb);
         float acc[T];
-        dqx_row<P, LPR, T>(row, npass, nunit, l4, gl, xl, tstride, acc);
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t] = 0.0f;
+        for (int it = 0; it < npass; ++it) {
+            const int g = gl + GPP * it;
+            const bool same = it + 1 < npass;                        // the next piece: this row's next pass,
+            const typename P::W nxt = P::load(same ? row : nrow, same ? g + GPP : gl, l4, nunit);   // else the next row's first
+            dqx_piece<P, LPR, T>(cur, l4, g, nunit, xl + it * 16 * LPR, tstride, acc);
+            cur = nxt;
+        }
+        const int r = rb + grp;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const float s = group_sum_last<LPR>(acc[t]);
-            if (ll == LPR - 1 && r < r1 && t < nt) Y[(int64_t)t * y_ts + r] = s;
+            const float sm = group_sum_last<LPR>(acc[t]);
+            if (ll == LPR - 1 && r < r1 && t < nt) Y[(int64_t)t * y_ts + r] = sm;
         }
     }
 }
 
-// the selected experts' rows of one bank against the hidden row: sweep row
-// q = s * rows + r (s < top_k) is row r of expert ids[s]; H[q] = the dot, or
-// with FINISH H[q] = silu(H[q]) * the dot (beast_silu_mul, :1168-1173: the
-// gate's dot there, this bank the up one); 0 where ids[s] names no expert
-template <class P, int LPR, bool FINISH>
-__global__ __launch_bounds__(256) void dqx_experts_kernel(const uint8_t* __restrict__ bank, size_t expert_bytes,
+// the selected experts' rows against the hidden row: sweep row q = s rows + r
+// (s < top_k) is row r of expert ids[s]. MODE 0: H[q] = the dot of `bank`'s
+// row; MODE 1: H[q] = silu(H[q]) * the dot (beast_silu_mul, :1168-1173, with
+// the gate's dot stored by a MODE 0 launch); MODE 2: gate (`bank`) and up
+// (`bank1`, the same type) in one launch, H[q] = silu(gate . x) * (up . x).
+// 0 where ids[s] names no expert.
+template <class P, int LPR, int MODE>
+__global__ __launch_bounds__(256) void dqx_experts_kernel(const uint8_t* __restrict__ bank,
+                                                          const uint8_t* __restrict__ bank1, size_t expert_bytes,
                                                           size_t row_bytes, int rows, int K,
                                                           const int32_t* __restrict__ ids, int E, int top_k,
                                                           const float* __restrict__ hidden, float* __restrict__ H,
@@ -342,39 +367,157 @@ __global__ __launch_bounds__(256) void dqx_experts_kernel(const uint8_t* __restr
     constexpr int GPP = LPR / 4, RW = 64 / LPR;
     const int ngroup = dqx_groups<P>(K), nunit = dqx_units<P>(K);
     const int npass = (ngroup + GPP - 1) / GPP;
-    dqx_stage<P, LPR>(hidden, K, dqx_x);
-    __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane / LPR, ll = lane % LPR;
     const int l4 = ll & 3, gl = ll >> 2;
-    const lf32x4* xl = (const lf32x4*)dqx_x + ll;
     const int total = top_k * rows;
     const int q0 = blockIdx.x * rows_per_wg;
     const int q1 = q0 + rows_per_wg < total ? q0 + rows_per_wg : total;
-    for (int qb = q0 + wave * RW; qb < q1; qb += 4 * RW) {      // uniform over the wave
+    struct Src {
+        const uint8_t* w;
+        const uint8_t* w1;
+        bool live;
+    };
+    auto src_at = [&](int qb) {
+        Src o;
         const int q = qb + grp < q1 ? qb + grp : q1 - 1;
         const int s = q / rows, r = q - s * rows;
         const int e = ids[s];
-        const bool live = e >= 0 && e < E;
-        const uint8_t* row = bank + (size_t)(live ? e : 0) * expert_bytes + (size_t)r * row_bytes;
-        float acc[1];
-        dqx_row<P, LPR, 1>(row, npass, nunit, l4, gl, xl, 0, acc);
+        o.live = e >= 0 && e < E;
+        const size_t off = (size_t)(o.live ? e : 0) * expert_bytes + (size_t)r * row_bytes;
+        o.w = bank + off;
+        o.w1 = (MODE == 2 ? bank1 : bank) + off;
+        return o;
+    };
+    int qb = q0 + wave * RW;
+    Src cs = src_at(qb < q1 ? qb : q0);
+    typename P::W cur = P::load(cs.w, gl, l4, nunit);
+    typename P::W cur1 = cur;
+    if (MODE == 2) cur1 = P::load(cs.w1, gl, l4, nunit);
+    dqx_stage<P, LPR>(hidden, K, dqx_x);
+    __syncthreads();
+    const lf32x4* xl = (const lf32x4*)dqx_x + ll;
+    for (; qb < q1; qb += 4 * RW) {                                // uniform over the wave
+        const Src ns = src_at(qb + 4 * RW < q1 ? qb + 4 * RW : qb);
+        float acc[1] = {0.0f}, acc1[1] = {0.0f};
+        for (int it = 0; it < npass; ++it) {
+            const int g = gl + GPP * it;
+            const bool same = it + 1 < npass;
+            const typename P::W nxt = P::load(same ? cs.w : ns.w, same ? g + GPP : gl, l4, nunit);
+            typename P::W nxt1 = nxt;
+            if (MODE == 2) nxt1 = P::load(same ? cs.w1 : ns.w1, same ? g + GPP : gl, l4, nunit);
+            dqx_piece<P, LPR, 1>(cur, l4, g, nunit, xl + it * 16 * LPR, 0, acc);
+            if (MODE == 2) dqx_piece<P, LPR, 1>(cur1, l4, g, nunit, xl + it * 16 * LPR, 0, acc1);
+            cur = nxt;
+            cur1 = nxt1;
+        }
         const float d = group_sum_last<LPR>(acc[0]);
-        if (ll == LPR - 1 && qb + grp < q1) {
-            if (FINISH) {
-                const float g = H[q];
-                H[q] = live ? (g / (1.0f + expf(-g))) * d : 0.0f;
+        const float d1 = MODE == 2 ? group_sum_last<LPR>(acc1[0]) : 0.0f;
+        const int q = qb + grp;
+        if (ll == LPR - 1 && q < q1) {
+            if (MODE == 0) {
+                H[q] = cs.live ? d : 0.0f;
+            } else if (MODE == 1) {
+                const float gt = H[q];
+                H[q] = cs.live ? (gt / (1.0f + expf(-gt))) * d : 0.0f;
             } else {
-                H[q] = live ? d : 0.0f;
+                H[q] = cs.live ? (d / (1.0f + expf(-d))) * d1 : 0.0f;
             }
         }
+        cs = ns;
     }
 }
 
-// down rows of every selected expert against that expert's H row, summed in
-// rank order as out[i] += score * down (:541-543, fused multiply-add as the
-// reference's GCC build contracts it): a lane group holds up to DQX_DOWN_RPW
-// rows, its workgroup rows_per_wg consecutive rows; the H rows are staged one
-// expert at a time
+// down rows of the selected experts against their H rows, summed in rank
+// order as out[i] += score * down (:541-543, fused multiply-add as the
+// reference's GCC build contracts it), one wave a row: the valid selected
+// experts, compacted in rank order, are dealt to the lane groups (slot v to
+// group v % GPW), each group walking the pieces of its slots' rows with the
+// next piece in flight; the wave then adds the slots' products in rank order.
+// Every selected expert's H row is staged once a workgroup (top_k rows in
+// LDS); an id outside [0, E) is skipped.
+constexpr int DQX_DOWN_WAVES = 8;
+
+template <class P, int LPR>
+__global__ __launch_bounds__(DQX_DOWN_WAVES * 64) void dqx_down_rows_kernel(
+    const uint8_t* __restrict__ down, size_t expert_bytes, size_t row_bytes, int n_embd, int n_ff,
+    const int32_t* __restrict__ ids, int E, const float* __restrict__ scores, int top_k, const float* __restrict__ H,
+    float* __restrict__ out) {
+    extern __shared__ __align__(16) f32x4 dqx_x[];
+    __shared__ int v_e[BEAST_MAX_TOPK], v_s[BEAST_MAX_TOPK];
+    __shared__ float v_sc[BEAST_MAX_TOPK];
+    __shared__ float v_d[DQX_DOWN_WAVES * BEAST_MAX_TOPK];
+    __shared__ int v_n;
+    constexpr int GPP = LPR / 4, GPW = 64 / LPR;
+    const int ngroup = dqx_groups<P>(n_ff), nunit = dqx_units<P>(n_ff);
+    const int npass = (ngroup + GPP - 1) / GPP;
+    const int tstride = npass * 16 * LPR;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, grp = lane / LPR, ll = lane % LPR;
+    const int l4 = ll & 3, gl = ll >> 2;
+    const int row = blockIdx.x * DQX_DOWN_WAVES + wave;
+    const size_t roff = (size_t)(row < n_embd ? row : n_embd - 1) * row_bytes;
+    // this group's first slot (the grp-th valid one, rank order), found by
+    // every lane from the ids so that its loads go out before the staging
+    int fe = 0, cnt = 0;
+    for (int s = 0; s < top_k; ++s) {
+        const int e = ids[s];
+        const bool ok = e >= 0 && e < E;
+        if (ok && cnt == grp) fe = e;
+        cnt += ok ? 1 : 0;
+    }
+    typename P::W cur = P::load(down + (size_t)fe * expert_bytes + roff, gl, l4, nunit);
+    if (threadIdx.x == 0) {
+        int n = 0;
+        for (int s = 0; s < top_k; ++s) {
+            const int e = ids[s];
+            if (e >= 0 && e < E) {
+                v_e[n] = e;
+                v_s[n] = s;
+                v_sc[n] = scores[s];
+                ++n;
+            }
+        }
+        v_n = n;
+    }
+    for (int s = 0; s < top_k; ++s) dqx_stage<P, LPR>(H + (size_t)s * n_ff, n_ff, dqx_x + (size_t)s * tstride);
+    __syncthreads();
+    const int nv = v_n;
+    const int per = (nv + GPW - 1) / GPW;                             // slots a group (uniform)
+    const int pieces = per * npass;
+    // piece c of the group: its slot k = c / npass (the valid slot grp + GPW k),
+    // pass c % npass; nv >= 1 whenever a piece runs, so v_e[0] is set
+    int k = 0, it = 0;
+    float acc[1] = {0.0f};
+    for (int c = 0; c < pieces; ++c) {
+        const int nk = it + 1 < npass ? k : k + 1;
+        const int nit = it + 1 < npass ? it + 1 : 0;
+        const int nvi = grp + GPW * nk;
+        const int ne = v_e[nvi < nv ? nvi : (grp < nv ? grp : 0)];
+        const typename P::W nxt = P::load(down + (size_t)ne * expert_bytes + roff, gl + GPP * nit, l4, nunit);
+        const int vi = grp + GPW * k;
+        const bool live = vi < nv;
+        const lf32x4* xl = (const lf32x4*)dqx_x + (size_t)v_s[live ? vi : 0] * tstride + it * 16 * LPR + ll;
+        if (live) dqx_piece<P, LPR, 1>(cur, l4, gl + GPP * it, nunit, xl, 0, acc);
+        if (it == npass - 1) {                                        // uniform: the slot's last pass
+            const float d = group_sum_last<LPR>(acc[0]);
+            if (ll == LPR - 1 && live) v_d[wave * BEAST_MAX_TOPK + vi] = d;
+            acc[0] = 0.0f;
+        }
+        cur = nxt;
+        k = nk;
+        it = nit;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0 && row < n_embd) {
+        float o = 0.0f;
+        for (int v = 0; v < nv; ++v) o = fmaf(v_sc[v], v_d[wave * BEAST_MAX_TOPK + v], o);
+        out[row] = o;
+    }
+}
+
+// The same sum for rows whose selected experts' H rows do not all fit the
+// staging area: a lane group holds up to DQX_DOWN_RPW rows, its workgroup
+// rows_per_wg consecutive rows; the H rows are staged one expert at a time.
 constexpr int DQX_DOWN_RPW = 8;
 
 template <class P, int LPR>
@@ -443,10 +586,11 @@ hipError_t dqx_lds_attr(Kern k, size_t lds) {
     return hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
 
-// about four workgroups a CU, each a contiguous run of rows (a multiple of the
-// rows its four waves take side by side)
+// about two workgroups a CU, each a contiguous run of rows (a multiple of the
+// rows its four waves take side by side): every workgroup stages the whole
+// activation row, so fewer, longer runs read less of it again
 int64_t dqx_rows_per_wg(int64_t total, int rw, int num_cus) {
-    const int64_t want = (int64_t)num_cus * 4, unit = 4LL * rw;
+    const int64_t want = (int64_t)num_cus * 2, unit = 4LL * rw;
     int64_t per = (total + want - 1) / want;
     return (per + unit - 1) / unit * unit;
 }
@@ -482,39 +626,38 @@ hipError_t dqx_matvec_p(const uint8_t* W, int M, int K, const float* X, int64_t 
     return dqx_matvec_lt<P, 64, 8>(W, M, K, X, x_ts, T, Y, y_ts, num_cus, st);
 }
 
-template <class P, int LPR>
-hipError_t dqx_experts_l(bool finish, const uint8_t* bank, int E, int rows, int K, const int32_t* ids, int top_k,
-                         const float* hidden, float* H, int num_cus, hipStream_t st) {
+template <class P, int LPR, int MODE>
+hipError_t dqx_experts_m(const uint8_t* bank, const uint8_t* bank1, int E, int rows, int K, const int32_t* ids,
+                         int top_k, const float* hidden, float* H, int num_cus, hipStream_t st) {
     const size_t row_bytes = (size_t)(K / P::UNIT) * P::UNIT_BYTES;
     const size_t expert_bytes = row_bytes * rows;
     const size_t lds = dqx_row_lds<P>(K, LPR);
     const int64_t total = (int64_t)top_k * rows;
     const int64_t rpw = dqx_rows_per_wg(total, 64 / LPR, num_cus);
-    const dim3 grid((unsigned)((total + rpw - 1) / rpw));
-    hipError_t e;
-    if (finish) {
-        e = dqx_lds_attr(dqx_experts_kernel<P, LPR, true>, lds);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((dqx_experts_kernel<P, LPR, true>), grid, dim3(256), lds, st, bank, expert_bytes, row_bytes,
-                           rows, K, ids, E, top_k, hidden, H, (int)rpw);
-    } else {
-        e = dqx_lds_attr(dqx_experts_kernel<P, LPR, false>, lds);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((dqx_experts_kernel<P, LPR, false>), grid, dim3(256), lds, st, bank, expert_bytes,
-                           row_bytes, rows, K, ids, E, top_k, hidden, H, (int)rpw);
-    }
+    hipError_t e = dqx_lds_attr(dqx_experts_kernel<P, LPR, MODE>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((dqx_experts_kernel<P, LPR, MODE>), dim3((unsigned)((total + rpw - 1) / rpw)), dim3(256), lds,
+                       st, bank, bank1, expert_bytes, row_bytes, rows, K, ids, E, top_k, hidden, H, (int)rpw);
     return hipGetLastError();
 }
 
+template <class P, int LPR>
+hipError_t dqx_experts_l(int mode, const uint8_t* bank, const uint8_t* bank1, int E, int rows, int K,
+                         const int32_t* ids, int top_k, const float* hidden, float* H, int num_cus, hipStream_t st) {
+    if (mode == 2) return dqx_experts_m<P, LPR, 2>(bank, bank1, E, rows, K, ids, top_k, hidden, H, num_cus, st);
+    if (mode == 1) return dqx_experts_m<P, LPR, 1>(bank, bank1, E, rows, K, ids, top_k, hidden, H, num_cus, st);
+    return dqx_experts_m<P, LPR, 0>(bank, bank1, E, rows, K, ids, top_k, hidden, H, num_cus, st);
+}
+
 template <class P>
-hipError_t dqx_experts_p(bool finish, const uint8_t* bank, int E, int rows, int K, const int32_t* ids, int top_k,
-                         const float* hidden, float* H, int num_cus, hipStream_t st) {
+hipError_t dqx_experts_p(int mode, const uint8_t* bank, const uint8_t* bank1, int E, int rows, int K,
+                         const int32_t* ids, int top_k, const float* hidden, float* H, int num_cus, hipStream_t st) {
     switch (dqx_lpr(dqx_groups<P>(K))) {
-        case 4: return dqx_experts_l<P, 4>(finish, bank, E, rows, K, ids, top_k, hidden, H, num_cus, st);
-        case 8: return dqx_experts_l<P, 8>(finish, bank, E, rows, K, ids, top_k, hidden, H, num_cus, st);
-        case 16: return dqx_experts_l<P, 16>(finish, bank, E, rows, K, ids, top_k, hidden, H, num_cus, st);
-        case 32: return dqx_experts_l<P, 32>(finish, bank, E, rows, K, ids, top_k, hidden, H, num_cus, st);
-        default: return dqx_experts_l<P, 64>(finish, bank, E, rows, K, ids, top_k, hidden, H, num_cus, st);
+        case 4: return dqx_experts_l<P, 4>(mode, bank, bank1, E, rows, K, ids, top_k, hidden, H, num_cus, st);
+        case 8: return dqx_experts_l<P, 8>(mode, bank, bank1, E, rows, K, ids, top_k, hidden, H, num_cus, st);
+        case 16: return dqx_experts_l<P, 16>(mode, bank, bank1, E, rows, K, ids, top_k, hidden, H, num_cus, st);
+        case 32: return dqx_experts_l<P, 32>(mode, bank, bank1, E, rows, K, ids, top_k, hidden, H, num_cus, st);
+        default: return dqx_experts_l<P, 64>(mode, bank, bank1, E, rows, K, ids, top_k, hidden, H, num_cus, st);
     }
 }
 
@@ -524,7 +667,17 @@ hipError_t dqx_down_l(const uint8_t* down, int E, int n_embd, int n_ff, const in
     const size_t row_bytes = (size_t)(n_ff / P::UNIT) * P::UNIT_BYTES;
     const size_t expert_bytes = row_bytes * n_embd;
     const size_t lds = dqx_row_lds<P>(n_ff, LPR);
-    hipError_t e = dqx_lds_attr(dqx_down_kernel<P, LPR>, lds);
+    hipError_t e;
+    if ((size_t)top_k * lds <= DQ_MATVEC_LDS_MAX) {
+        // every selected expert's H row staged at once: a wave a row
+        e = dqx_lds_attr(dqx_down_rows_kernel<P, LPR>, (size_t)top_k * lds);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((dqx_down_rows_kernel<P, LPR>), dim3((unsigned)((n_embd + DQX_DOWN_WAVES - 1) / DQX_DOWN_WAVES)),
+                           dim3(DQX_DOWN_WAVES * 64), (size_t)top_k * lds, st, down, expert_bytes, row_bytes, n_embd,
+                           n_ff, ids, E, scores, top_k, H, out);
+        return hipGetLastError();
+    }
+    e = dqx_lds_attr(dqx_down_kernel<P, LPR>, lds);
     if (e != hipSuccess) return e;
     // rows in runs of a multiple of the workgroup's side-by-side rows, at most
     // DQX_DOWN_RPW a lane group, about two workgroups a CU: each workgroup
@@ -594,21 +747,23 @@ hipError_t launch_dqx_matvec(int type, const uint8_t* W, int M, int64_t K, const
     }
 }
 
-hipError_t launch_dqx_experts(int type, bool finish, const uint8_t* bank, int E, int rows, int64_t K,
-                              const int32_t* ids, int top_k, const float* hidden, float* H, int num_cus,
+hipError_t launch_dqx_experts(int type, int mode, const uint8_t* bank, const uint8_t* bank1, int E, int rows,
+                              int64_t K, const int32_t* ids, int top_k, const float* hidden, float* H, int num_cus,
                               hipStream_t st) {
     const int unit = dqx_unit(type);
-    if (!unit || E < 1 || rows <= 0 || K <= 0 || K % unit || K > INT32_MAX || top_k < 1 || top_k > BEAST_MAX_TOPK ||
-        (int64_t)top_k * rows > INT32_MAX || dqx_lds_bytes(type, K, 1) > DQ_MATVEC_LDS_MAX)
+    if (!unit || mode < 0 || mode > 2 || (mode == 2 && !bank1) || E < 1 || rows <= 0 || K <= 0 || K % unit ||
+        K > INT32_MAX || top_k < 1 || top_k > BEAST_MAX_TOPK || (int64_t)top_k * rows > INT32_MAX ||
+        dqx_lds_bytes(type, K, 1) > DQ_MATVEC_LDS_MAX)
         return hipErrorInvalidValue;
     switch (type) {
         case SPQ4K_TYPE_Q8_0:
-            return dqx_experts_p<DqxQ8_0>(finish, bank, E, rows, (int)K, ids, top_k, hidden, H, num_cus, st);
+            return dqx_experts_p<DqxQ8_0>(mode, bank, bank1, E, rows, (int)K, ids, top_k, hidden, H, num_cus, st);
         case SPQ4K_TYPE_Q6_K:
-            return dqx_experts_p<DqxQ6K>(finish, bank, E, rows, (int)K, ids, top_k, hidden, H, num_cus, st);
+            return dqx_experts_p<DqxQ6K>(mode, bank, bank1, E, rows, (int)K, ids, top_k, hidden, H, num_cus, st);
         case SPQ4K_TYPE_Q5_K:
-            return dqx_experts_p<DqxQ5K>(finish, bank, E, rows, (int)K, ids, top_k, hidden, H, num_cus, st);
-        default: return dqx_experts_p<DqxQ4K>(finish, bank, E, rows, (int)K, ids, top_k, hidden, H, num_cus, st);
+            return dqx_experts_p<DqxQ5K>(mode, bank, bank1, E, rows, (int)K, ids, top_k, hidden, H, num_cus, st);
+        default:
+            return dqx_experts_p<DqxQ4K>(mode, bank, bank1, E, rows, (int)K, ids, top_k, hidden, H, num_cus, st);
     }
 }
 

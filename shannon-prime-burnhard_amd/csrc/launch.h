@@ -296,14 +296,15 @@ hipError_t launch_dequant_matvec(const uint8_t* W, int M, int nb, const float* X
 // The same dequant-then-dot for rows of any library type (k_dqdot_x.hip;
 // type = SPQ4K_TYPE_Q4_K, _Q5_K, _Q6_K or _Q8_0; K a multiple of the type's
 // block): dense rows (T <= DQ_MATVEC_MAX_T tokens), the selected experts'
-// rows of one bank against one hidden row (H[s][r] = the dot, or with
-// finish H[s][r] = silu(H[s][r]) * the dot), and the down rows' score-weighted
-// sum out[i] over the selected experts in rank order.
+// rows against one hidden row (mode 0: H[s][r] = the dot of bank's row;
+// mode 1: H[s][r] = silu(H[s][r]) * the dot; mode 2: H[s][r] = silu(bank
+// row . x) * (bank1 row . x), both banks of `type`), and the down rows'
+// score-weighted sum out[i] over the selected experts in rank order.
 size_t dqx_lds_bytes(int type, int64_t K, int T);
 hipError_t launch_dqx_matvec(int type, const uint8_t* W, int M, int64_t K, const float* X, int64_t x_tstride,
                              float* Y, int64_t y_tstride, int T, int num_cus, hipStream_t st);
-hipError_t launch_dqx_experts(int type, bool finish, const uint8_t* bank, int E, int rows, int64_t K,
-                              const int32_t* ids, int top_k, const float* hidden, float* H, int num_cus,
+hipError_t launch_dqx_experts(int type, int mode, const uint8_t* bank, const uint8_t* bank1, int E, int rows,
+                              int64_t K, const int32_t* ids, int top_k, const float* hidden, float* H, int num_cus,
                               hipStream_t st);
 hipError_t launch_dqx_down(int type, const uint8_t* down, int E, int n_embd, int64_t n_ff, const int32_t* ids,
                            const float* scores, int top_k, const float* H, float* out, int num_cus, hipStream_t st);

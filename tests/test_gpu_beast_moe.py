@@ -244,3 +244,24 @@ def test_beast_moe_q8_0_ragged_rows(ctx, oracle):
     _check(y, y_or, "ragged Q8_0", _forward_f64(oracle, Wg, Wu, Wd, E, n_embd, n_ff, ids, sc, hidden, types))
     for w in banks:
         w.free()
+
+
+@pytest.mark.skipif(not os.path.exists(BEAST_SO), reason="oracle/_ref/beast (the reference) not built")
+def test_beast_moe_q8_0_long_hidden_rows_vs_reference(ctx, oracle):
+    """hidden rows too long for every selected expert's row to be staged at
+    once (3 x 16384 values): the down sum that stages one expert at a time,
+    against the reference's own forward"""
+    types = (TYPE_Q8_0,) * 3
+    E, k, n_embd, n_ff = 4, 3, 256, 16384
+    rng = np.random.default_rng(17)
+    Wg, Wu, Wd = _mixed_banks(oracle, rng, types, E, n_embd, n_ff)
+    logits = (rng.standard_normal(E) * 2.0).astype(np.float32)
+    hidden = rng.standard_normal(n_embd).astype(np.float32)
+    y_ref, ids_ref, sc_ref = BeastRef().moe(types, Wg, Wu, Wd, E, n_embd, n_ff, logits, k, hidden)
+    banks = _upload3(ctx, types, Wg, Wu, Wd, E, n_embd, n_ff)
+    y, ids, sc = ctx.beast_moe_forward(*banks, logits, k, hidden)
+    assert np.array_equal(ids, ids_ref)
+    _check(y, y_ref, "long hidden rows", _forward_f64(oracle, Wg, Wu, Wd, E, n_embd, n_ff, ids_ref, sc_ref, hidden,
+                                                      types))
+    for w in banks:
+        w.free()
