@@ -243,16 +243,20 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
 //   K = 12288, Q4_K        : 8 waves, weights first (4096 x 12288: 8.21 against
 //                            8.52 us with 16 waves x-first; 1024 rows 5.25 against
 //                            6.53, 28672 rows 35.7 against 36.8, 12288 rows 16.8
-//                            against 16.7); other formats 12 waves, x-first
+//                            against 16.7), two rows a wave with the second row's
+//                            loads issued after the quantisation barrier (8.50-8.52
+//                            against 8.61-8.63 us with one row in flight; both rows
+//                            at the start 9.55); other formats 12 waves, x-first
 //   K = 27648              : 8 waves (the registers of 7 Q8_K blocks a lane), x-first
-DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb_rows, int64_t rows) {
+DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb_rows, int64_t rows, bool fused = false) {
     DecodeCfg d{};
     // register limits follow the row length the kernel instance is compiled for
     const int nb = decode_bucket(fmt, nb_rows) > 0 ? decode_bucket(fmt, nb_rows) : nb_rows;
     if (nb > 48) {
         d.waves = 8; d.depth = 1; d.xfirst = true;
     } else if (nb >= 48 && fmt == WF_Q4K) {
-        d.waves = 8; d.depth = 1; d.xfirst = false;
+        // fused forms load x first, where a second row at the start is slower
+        d.waves = 8; d.depth = fused ? 1 : 2; d.xfirst = false;
     } else if (nb >= 48) {
         d.waves = 16; d.depth = 1; d.xfirst = true;
     } else if (rows <= 4096) {
@@ -499,7 +503,7 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
     }
     if (fuse) {
         if (c->no_decode || !decode_supported(p.fmt, p.nb)) return 1;
-        DecodeCfg dc = plan_decode(c, p.fmt, p.nb, fuse->glu ? W[0]->M : total);
+        DecodeCfg dc = plan_decode(c, p.fmt, p.nb, fuse->glu ? W[0]->M : total, true);
         dc.norm = fuse->norm_w != nullptr;
         dc.glu = fuse->glu;
         dc.xfirst = true;

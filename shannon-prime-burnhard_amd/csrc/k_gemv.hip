@@ -251,17 +251,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
         quantise();
         __builtin_amdgcn_sched_barrier(0);
     }
+    // LATE (two rows in flight, weights first): only the first row's loads go
+    // out with x's; the second row's follow the quantisation barrier, before
+    // the first row is consumed, so x does not queue behind both rows
+    constexpr bool LATE = D == 2 && !XFW && !GLU;
     if (GLU) {
         load_glu(0, 0, buf[0]);
         load_glu(0, 1, buf[D - 1]);
     } else {
 #pragma unroll
-        for (int u = 0; u < D; ++u) load_row(u, buf[u]);
+        for (int u = 0; u < D; ++u)
+            if (!LATE || u == 0) load_row(u, buf[u]);
     }
     if (!XFW) quantise();
     // all quantised blocks visible (LDS writes only: weight loads stay in flight)
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
+    if (LATE) load_row(1, buf[1]);
 
     typename Fmt::R qr[NIT];
 #pragma unroll
