@@ -62,6 +62,7 @@ struct spq4k_ctx {
     // takes 49.0 us against 56.5 on the ring
     int moe_dec_max_t = 8;
     int moe_ring_waves = 0;      // SPQ4K_MOE_RING_WAVES: 4 or 8 waves (64- or 128-row tiles) in the expert ring kernel, 0 by format
+    int moe_dec_waves = 0;       // SPQ4K_MOE_DEC_WAVES: 8 or 12 waves in a GLU expert sweep, 0 by grid
     int moe_mode = 0;            // SPQ4K_MOE_MODE: 2 skips the small-batch decode mapping, 3 takes the single-launch sdot4 kernel
     int gemm_mode = 0;           // SPQ4K_GEMM_MODE: 0 auto, 1 skinny kernel, 2 tiled kernel
     int gemm_cfg = -1;           // SPQ4K_GEMM_CFG: tiled launch shape, -1 automatic
@@ -715,6 +716,10 @@ int spq4k_init(int device, spq4k_ctx** out) {
     if (const char* f = getenv("SPQ4K_MOE_DEC_MAX_T")) {
         const int v = atoi(f);
         if (v >= 1 && v <= 8) c->moe_dec_max_t = v;
+    }
+    if (const char* f = getenv("SPQ4K_MOE_DEC_WAVES")) {
+        const int v = atoi(f);
+        if (v == 8 || v == 12) c->moe_dec_waves = v;
     }
     if (const char* f = getenv("SPQ4K_MOE_RING_WAVES")) {
         const int v = atoi(f);
@@ -1600,7 +1605,18 @@ int moe_decode_try(spq4k_ctx* c, const spq4k_weights* const* banks, int nbank, c
         f.M1 = glu ? 0 : M1;
         f.glu = glu ? 1 : 0;
     }
-    const int64_t per_wg = moe_decode_rows_per_wg(nb);
+    // a GLU sweep that 12-wave workgroups cover in one workgroup a CU runs
+    // so: these 8-wave workgroups start one a CU (their registers), so a
+    // grid above the CU count runs in two rounds (the 30B-A3B block at T = 1:
+    // 384 workgroups of 8 waves, the last 128 starting when the first end)
+    int waves = 8;
+    if (glu) {
+        const int64_t pw12 = moe_decode_rows_per_wg(nb, 12);
+        if ((n_pairs * MV + pw12 - 1) / pw12 <= c->num_cus) waves = 12;
+        if (c->moe_dec_waves) waves = c->moe_dec_waves;
+    }
+    f.waves = waves;
+    const int64_t per_wg = moe_decode_rows_per_wg(nb, waves);
     const int64_t need = (n_pairs * MV + per_wg - 1) / per_wg;
     const int grid = (int)(need < 2 * c->num_cus ? need : 2 * c->num_cus);
     moe_decode_plan(f, grid, &f.rows_per_wg, &f.xwin_rows);

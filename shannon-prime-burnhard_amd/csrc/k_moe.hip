@@ -625,26 +625,28 @@ hipError_t launch_moe_down_sum(const MoeFusedParams& p, const float* cw, float* 
 
 template <typename Fmt, int NB, int BSL>
 static hipError_t launch_mdec(const MoeFusedParams& p, int grid, hipStream_t st) {
-    constexpr int WAVES = 8;
     const size_t lds = (size_t)q8lds_bytes(p.xwin_rows * NB);
-    if (p.glu)
-        hipLaunchKernelGGL((moe_decode_kernel<Fmt, NB, BSL, WAVES, true>), dim3(grid), dim3(WAVES * 64), lds, st, p);
+    if (p.glu && p.waves == 12)
+        hipLaunchKernelGGL((moe_decode_kernel<Fmt, NB, BSL, 12, true>), dim3(grid), dim3(12 * 64), lds, st, p);
+    else if (p.glu)
+        hipLaunchKernelGGL((moe_decode_kernel<Fmt, NB, BSL, 8, true>), dim3(grid), dim3(8 * 64), lds, st, p);
     else
-        hipLaunchKernelGGL((moe_decode_kernel<Fmt, NB, BSL, WAVES, false>), dim3(grid), dim3(WAVES * 64), lds, st, p);
+        hipLaunchKernelGGL((moe_decode_kernel<Fmt, NB, BSL, 8, false>), dim3(grid), dim3(8 * 64), lds, st, p);
     return hipGetLastError();
 }
 
 bool moe_decode_supported(int nb) { return nb == 3 || nb == 8 || nb == 16; }
 
-// rows of the sweep per workgroup pass: WAVES * 64 / (4 * BSL)
-int moe_decode_rows_per_wg(int nb) { return nb == 3 ? 32 : (nb == 8 ? 16 : 8); }
+// rows of the sweep per workgroup pass: waves * 64 / (4 * BSL), BSL = 4, 8, 16
+// for rows of 3, 8 and 16 blocks
+int moe_decode_rows_per_wg(int nb, int waves) { return waves * (nb == 3 ? 4 : (nb == 8 ? 2 : 1)); }
 
 // rows per workgroup (a whole number of passes) and the input rows the
 // largest run of that many sweep rows can read
 void moe_decode_plan(const MoeFusedParams& p, int grid, int32_t* rows_per_wg, int32_t* xwin_rows) {
     const int64_t MV = p.glu ? (int64_t)p.M : (int64_t)p.M + p.M1;
     const int64_t total = (int64_t)p.n_pairs * MV;
-    const int64_t pass = moe_decode_rows_per_wg(p.nb);
+    const int64_t pass = moe_decode_rows_per_wg(p.nb, p.waves ? p.waves : 8);
     int64_t rw = (total + grid - 1) / grid;
     rw = (rw + pass - 1) / pass * pass;
     *rows_per_wg = (int32_t)rw;

@@ -131,6 +131,8 @@ struct MoeFusedParams {
     // moe_decode_kernel only: bank1 is the up bank beside the gate bank (same
     // M); Y[pair][r] = silu(gate row r . x) * (up row r . x), Y1 unused
     int32_t glu;
+    // moe_decode_kernel: waves a workgroup, 8, or 12 for a GLU sweep (0 = 8)
+    int32_t waves;
 };
 hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, hipStream_t st);
 
@@ -138,7 +140,7 @@ hipError_t launch_moe_fused(const MoeFusedParams& p, int tc, int bpr, int grid, 
 constexpr int MOE_DEC_MAX_PAIRS = 64;
 constexpr int MOE_DEC_MAX_XROWS = 64;
 bool moe_decode_supported(int nb);
-int moe_decode_rows_per_wg(int nb);
+int moe_decode_rows_per_wg(int nb, int waves = 8);
 void moe_decode_plan(const MoeFusedParams& p, int grid, int32_t* rows_per_wg, int32_t* xwin_rows);
 hipError_t launch_moe_decode(const MoeFusedParams& p, int grid, hipStream_t st);
 // the routed-expert block's down projection with the weighted slot sum as its
