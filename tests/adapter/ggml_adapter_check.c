@@ -456,9 +456,24 @@ int check_hostmem_not_host(int mode, int type, int64_t M, int64_t K, int64_t E, 
  * attention and are left out), then x = x + down(silu(gate(xb)) * up(xb)) with
  * xb = rms_norm(x) * ffn_norm; logits = out(rms_norm(x) * out_norm). All
  * matrices Q4_K; norms, residual adds, SiLU and the product are ggml CPU ops
- * in both graphs. y_* are the logits [n_vocab, T]. */
+ * in both graphs. y_* are the logits [n_vocab, T].
+ * Per node: every adapter matmul of the second graph (q, o, gate, up, down of
+ * each layer, then the head) has a shadow ggml MUL_MAT on the same weight and
+ * the same input tensor, so the CPU node is fed the adapter path's own
+ * intermediate activations. When nodes_ada / nodes_chk are not NULL, the
+ * adapter outputs and their shadows are written there, node after node in
+ * that order ([rows, T] each: T * (n_q + 2 n_embd + 2 n_ff) a layer, then
+ * T * n_vocab). */
+#define DEC_MAX_NODES 64
 int check_decoder(int n_layers, int64_t n_embd, int64_t n_q, int64_t n_ff, int64_t n_vocab, int64_t T,
-                  uint64_t seed, int nthreads, float *y_ref, float *y_ada, char *err, int errlen) {
+                  uint64_t seed, int nthreads, float *y_ref, float *y_ada, float *nodes_ada, float *nodes_chk,
+                  char *err, int errlen) {
+    if (5 * n_layers + 1 > DEC_MAX_NODES) {
+        snprintf(err, errlen, "at most %d layers", (DEC_MAX_NODES - 1) / 5);
+        return -1;
+    }
+    struct ggml_tensor *node_a[DEC_MAX_NODES], *node_c[DEC_MAX_NODES];
+    int nn = 0;
     spq4k_ggml *b;
     int rc = spq4k_ggml_init(0, &b);
     if (rc) {
@@ -490,15 +505,19 @@ int check_decoder(int n_layers, int64_t n_embd, int64_t n_q, int64_t n_ff, int64
         }
         for (int g = 0; g < 2; ++g) {
             struct ggml_tensor **x = g ? &xa : &xr;
+            /* the adapter's node for g = 1 (and its shadow), ggml's for g = 0 */
+#define DEC_MM(W, IN) (g ? (node_c[nn] = ggml_mul_mat(ctx, W, IN), node_a[nn++] = spq4k_ggml_mul_mat(ctx, W, IN, b)) \
+                         : ggml_mul_mat(ctx, W, IN))
             struct ggml_tensor *h = ggml_mul(ctx, ggml_rms_norm(ctx, *x, eps), an);
-            struct ggml_tensor *q = g ? spq4k_ggml_mul_mat(ctx, wq, h, b) : ggml_mul_mat(ctx, wq, h);
-            struct ggml_tensor *o = g ? spq4k_ggml_mul_mat(ctx, wo, q, b) : ggml_mul_mat(ctx, wo, q);
+            struct ggml_tensor *q = DEC_MM(wq, h);
+            struct ggml_tensor *o = DEC_MM(wo, q);
             struct ggml_tensor *x1 = ggml_add(ctx, *x, o);
             struct ggml_tensor *hb = ggml_mul(ctx, ggml_rms_norm(ctx, x1, eps), fn);
-            struct ggml_tensor *gt = g ? spq4k_ggml_mul_mat(ctx, wg, hb, b) : ggml_mul_mat(ctx, wg, hb);
-            struct ggml_tensor *ut = g ? spq4k_ggml_mul_mat(ctx, wu, hb, b) : ggml_mul_mat(ctx, wu, hb);
+            struct ggml_tensor *gt = DEC_MM(wg, hb);
+            struct ggml_tensor *ut = DEC_MM(wu, hb);
             struct ggml_tensor *par = ggml_mul(ctx, ggml_silu(ctx, gt), ut);
-            struct ggml_tensor *dn = g ? spq4k_ggml_mul_mat(ctx, wd, par, b) : ggml_mul_mat(ctx, wd, par);
+            struct ggml_tensor *dn = DEC_MM(wd, par);
+#undef DEC_MM
             *x = ggml_add(ctx, x1, dn);
         }
     }
@@ -508,6 +527,31 @@ int check_decoder(int n_layers, int64_t n_embd, int64_t n_q, int64_t n_ff, int64
     for (int64_t i = 0; i < n_embd; ++i) ((float *)on->data)[i] += 1.0f;
     free(tmp);
     struct ggml_tensor *yr = ggml_mul_mat(ctx, wout, ggml_mul(ctx, ggml_rms_norm(ctx, xr, eps), on));
-    struct ggml_tensor *ya = spq4k_ggml_mul_mat(ctx, wout, ggml_mul(ctx, ggml_rms_norm(ctx, xa, eps), on), b);
+    struct ggml_tensor *ha = ggml_mul(ctx, ggml_rms_norm(ctx, xa, eps), on);
+    struct ggml_tensor *ya = spq4k_ggml_mul_mat(ctx, wout, ha, b);
+    node_c[nn] = ggml_mul_mat(ctx, wout, ha);
+    node_a[nn++] = ya;
+    for (int i = 0; i < nn; ++i)
+        if (!node_a[i]) ya = NULL;   /* graph construction failed */
+    if (ya && nodes_ada && nodes_chk) {
+        /* the shadows in the graph first, then the logits (finish computes
+         * the same graph again, with every node already evaluated once) */
+        struct ggml_cgraph *gf = ggml_new_graph(ctx);
+        for (int i = 0; i < nn; ++i) {
+            ggml_build_forward_expand(gf, node_c[i]);
+            ggml_build_forward_expand(gf, node_a[i]);
+        }
+        ggml_build_forward_expand(gf, yr);
+        if (ggml_graph_compute_with_ctx(ctx, gf, nthreads) != GGML_STATUS_SUCCESS) {
+            ya = NULL;
+        } else {
+            size_t off = 0;
+            for (int i = 0; i < nn; ++i) {
+                memcpy(nodes_ada + off, node_a[i]->data, ggml_nbytes(node_a[i]));
+                memcpy(nodes_chk + off, node_c[i]->data, ggml_nbytes(node_c[i]));
+                off += (size_t)ggml_nelements(node_a[i]);
+            }
+        }
+    }
     return finish(ctx, b, yr, ya, nthreads, y_ref, y_ada, err, errlen);
 }

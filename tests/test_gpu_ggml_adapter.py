@@ -231,18 +231,33 @@ def test_adapter_decoder_logits(drv, T):
     every position. Each layer re-quantises activations that already differ
     from the CPU's in the last bits (the reason given above for the
     feed-forward block), so element-wise agreement is not expected after
-    several layers."""
+    several layers.
+
+    Node by node, element-wise: each of the 21 adapter matmuls (q, o, gate,
+    up, down of every layer, then the head) against a ggml CPU MUL_MAT of the
+    same weight on the same input tensor, i.e. the CPU fed the adapter path's
+    own intermediate activations, within close_enough."""
     n_layers, n_embd, n_q, n_ff, n_vocab = 4, 1024, 1024, 2816, 8192
     f32p = ctypes.POINTER(ctypes.c_float)
     i64 = ctypes.c_int64
     drv.check_decoder.argtypes = [ctypes.c_int, i64, i64, i64, i64, i64, ctypes.c_uint64, ctypes.c_int, f32p, f32p,
-                                  ctypes.c_char_p, ctypes.c_int]
+                                  f32p, f32p, ctypes.c_char_p, ctypes.c_int]
     yr = np.full(n_vocab * T, np.nan, np.float32)
     ya = np.full(n_vocab * T, np.nan, np.float32)
+    rows = [("q", n_q), ("o", n_embd), ("gate", n_ff), ("up", n_ff), ("down", n_embd)] * n_layers + [("head", n_vocab)]
+    n_nodes = T * sum(r for _, r in rows)
+    na = np.full(n_nodes, np.nan, np.float32)
+    nc = np.full(n_nodes, np.nan, np.float32)
     err = ctypes.create_string_buffer(256)
     rc = drv.check_decoder(n_layers, n_embd, n_q, n_ff, n_vocab, T, 90 + T, 8, yr.ctypes.data_as(f32p),
-                           ya.ctypes.data_as(f32p), err, 256)
+                           ya.ctypes.data_as(f32p), na.ctypes.data_as(f32p), nc.ctypes.data_as(f32p), err, 256)
     assert rc == 0, err.value.decode()
+    off = 0
+    for i, (name, r) in enumerate(rows):
+        a, c = na[off:off + r * T], nc[off:off + r * T]
+        off += r * T
+        _check(c, a, f"decoder node {i} ({name}, layer {i // 5}) T={T}")
+    assert off == n_nodes
     assert np.isfinite(yr).all() and np.isfinite(ya).all()
     rel = float(np.linalg.norm(ya.astype(np.float64) - yr) / np.linalg.norm(yr.astype(np.float64)))
     assert rel <= LOGITS_NORMWISE, f"decoder logits T={T}: normwise {rel:.3e} > {LOGITS_NORMWISE}"
