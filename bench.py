@@ -1032,6 +1032,80 @@ def run_fusion(args):
     ctx.close()
 
 
+def run_decode_stamps(args):
+    """Wave timestamps of the decode kernel inside the 8B step
+    (spq4k_set_decode_stamps, include/spq4k_diag.h). The whole step is
+    captured as in decode8b, with the stamps switched on for every stage of
+    layers 9, 18 and 27 and for lm_head (a buffer per launch), and replayed;
+    per stage kind, the medians over those layers of, in us from the launch's
+    first wave start (the device's 100 MHz clock):
+      start     the last wave's start,
+      barrier   the median / last wave past the quantisation barrier,
+      first     the median wave's first row store issued,
+      end       the median / last wave's last row store issued,
+      gap       from the previous stage's last store issued to this launch's
+                first wave start (store completion, kernel end and dispatch)."""
+    ctx = spq4k.Context(0)
+    stages = build_decode8b(ctx)
+    layers = (9, 18, 27)
+    picked = ({f"L{L}.{k}" for L in layers for k in ("qkv", "o", "gate_up", "down")} |
+              {f"L{L - 1}.down" for L in layers} | {"lm_head", f"L{LAYERS - 1}.down"})
+    n = 256 * 16 * 4
+    bufs = {}
+    with Graph.capture(ctx.stream) as g:
+        for st in stages:
+            if st[0] in picked:
+                bufs[st[0]] = DeviceArray(n, np.uint64)
+                ctx.set_decode_stamps(bufs[st[0]].ptr, n)
+            enqueue_step(ctx, [st])
+            ctx.set_decode_stamps(None)
+    for b in bufs.values():
+        b.fill_byte(0)
+    ctx.synchronize()
+    # the step with and without the timestamped launches (their instances
+    # carry four clock reads and one store a wave more)
+    g_plain, _ = capture_step(ctx, stages)
+    ms_plain = time_graph(ctx, g_plain, 20, max(args.warmup, 1))
+    ms_stamped = time_graph(ctx, g, 20, max(args.warmup, 1))
+    log(f"[bench] step {ms_plain * 1e3:.1f} us; with {len(bufs)} launches timestamped {ms_stamped * 1e3:.1f} us")
+    stamp = {}
+    for name, b in bufs.items():
+        s = b.to_host().reshape(-1, 4).astype(np.int64)
+        stamp[name] = s[s[:, 0] != 0]
+    us = lambda v: round(float(v) / 100.0, 2)   # 100 MHz ticks -> us
+    def previous(kind, L):
+        if kind == "lm_head":
+            return f"L{LAYERS - 1}.down"
+        return {"qkv": f"L{L - 1}.down", "o": f"L{L}.qkv", "gate_up": f"L{L}.o", "down": f"L{L}.gate_up"}[kind]
+    out = {}
+    for kind in ("qkv", "o", "gate_up", "down", "lm_head"):
+        names = [("lm_head", None)] if kind == "lm_head" else [(f"L{L}.{kind}", L) for L in layers]
+        rec = {"start": [], "barrier_med": [], "barrier_last": [], "first_med": [], "end_med": [], "end_last": [],
+               "gap": []}
+        for nm, L in names:
+            s = stamp[nm]
+            t0 = s[:, 0].min()
+            rec["start"].append(s[:, 0].max() - t0)
+            rec["barrier_med"].append(np.median(s[:, 1]) - t0)
+            rec["barrier_last"].append(s[:, 1].max() - t0)
+            rows = s[s[:, 2] != 0]
+            rec["first_med"].append(np.median(rows[:, 2]) - t0)
+            rec["end_med"].append(np.median(rows[:, 3]) - t0)
+            rec["end_last"].append(rows[:, 3].max() - t0)
+            rec["gap"].append(t0 - stamp[previous(kind, L)][:, 3].max())
+        out[kind] = {k: us(np.median(v)) for k, v in rec.items()}
+        out[kind]["waves"] = int(len(stamp[names[0][0]]))
+        log(f"[bench] {kind:8s} " + "  ".join(f"{k} {v}" for k, v in out[kind].items()))
+    print(json.dumps({"metric": "decode kernel wave timestamps in the 8B step (us from the launch's first wave)",
+                      "stages": out, "step_us": round(ms_plain * 1e3, 1),
+                      "step_us_timestamped": round(ms_stamped * 1e3, 1),
+                      "config": {"workload": "decode8b step replayed as one graph; stamps on layers 9, 18, 27 "
+                                             "and lm_head"}}), flush=True)
+    for b in bufs.values():
+        b.free()
+    ctx.close()
+
+
 def run_floor(args):
     """The streaming floor of the 8B decode sweep: the same 145 dependent
     launches as decode8b, each a kernel that only reads its stage's bytes
@@ -1107,7 +1181,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="decode8b", choices=["decode8b", "gemv4096", "largek", "prefill", "moe", "q6k", "q5k", "q8_0",
-                                                          "single", "gguf", "fusion", "copy", "floor", "beastwide", "beastmix", "chain"])
+                                                          "single", "gguf", "fusion", "copy", "floor", "beastwide", "beastmix", "chain",
+                                                          "decode_stamps"])
     ap.add_argument("--M", type=int, default=4096, help="rows (--config single)")
     ap.add_argument("--K", type=int, default=4096, help="inputs (--config single)")
     ap.add_argument("--T", type=int, default=1, help="tokens (--config single)")
@@ -1149,6 +1224,8 @@ def main():
                    f"{tag[args.qtype]} {args.M}x{args.K} T={args.T}", args.qtype)
     elif args.config == "floor":
         run_floor(args)
+    elif args.config == "decode_stamps":
+        run_decode_stamps(args)
     elif args.config == "chain":
         run_chain(args)
     elif args.config == "copy":

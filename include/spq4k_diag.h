@@ -55,6 +55,22 @@ int spq4k_stream_read(spq4k_ctx *ctx, const void *p, size_t bytes);
 int spq4k_chain_info(const spq4k_chain *chain, int *version, int *grid, int *n_stages);
 int spq4k_chain_set_stamps(spq4k_ctx *ctx, spq4k_chain *chain, uint64_t *stamps);
 
+/* ---- decode-kernel wave timestamps -------------------------------------
+ * spq4k_set_decode_stamps gives ctx a device buffer of n uint64 (NULL stops
+ * it). While it is set, every T = 1 matvec on ctx that runs the decode
+ * kernel unfused writes, for wave v of workgroup w at [(w * waves + v) * 4 + k],
+ * the device's constant 100 MHz clock (s_memrealtime) when
+ *   k = 0  the wave started,
+ *   k = 1  it passed the barrier that publishes the workgroup's Q8_K
+ *          activations in LDS,
+ *   k = 2  it had issued the store of its first row (0: a wave without rows),
+ *   k = 3  it had issued the store of its last row.
+ * Each launch overwrites the buffer. Only the Q4_K launch shapes the planner
+ * picks for rows of K = 4096 and K = 12288 (the 8B step's) have a
+ * timestamped instance: another shape, or a launch whose grid * waves * 4
+ * exceeds n, fails with -EINVAL while stamps are set. */
+int spq4k_set_decode_stamps(spq4k_ctx *ctx, uint64_t *stamps, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

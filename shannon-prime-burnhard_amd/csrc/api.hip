@@ -63,6 +63,8 @@ struct spq4k_ctx {
     int moe_dec_max_t = 8;
     int moe_ring_waves = 0;      // SPQ4K_MOE_RING_WAVES: 4 or 8 waves (64- or 128-row tiles) in the expert ring kernel, 0 by format
     int moe_dec_waves = 0;       // SPQ4K_MOE_DEC_WAVES: 8 or 12 waves in a GLU expert sweep, 0 by grid
+    uint64_t* dec_stamps = nullptr;   // spq4k_set_decode_stamps: the decode kernel's wave timestamps
+    size_t dec_stamps_n = 0;
     int moe_mode = 0;            // SPQ4K_MOE_MODE: 2 skips the small-batch decode mapping, 3 takes the single-launch sdot4 kernel
     int gemm_mode = 0;           // SPQ4K_GEMM_MODE: 0 auto, 1 skinny kernel, 2 tiled kernel
     int gemm_cfg = -1;           // SPQ4K_GEMM_CFG: tiled launch shape, -1 automatic
@@ -527,6 +529,13 @@ int gemv_launch(spq4k_ctx* c, int n, const spq4k_weights* const* W, const float*
     }
     if (T == 1 && !c->no_decode && c->preq_mode != 1 && decode_supported(p.fmt, p.nb)) {
         const DecodeCfg dc = plan_decode(c, p.fmt, p.nb, total);
+        if (c->dec_stamps) {
+            if (!decode_stamps_supported(p.fmt, p.nb, dc))
+                return set_err(c, -EINVAL, "decode stamps: no timestamped instance for this launch shape");
+            if ((size_t)dc.grid * dc.waves * 4 > c->dec_stamps_n)
+                return set_err(c, -EINVAL, "decode stamps: buffer smaller than grid * waves * 4");
+            p.stamps = c->dec_stamps;
+        }
         hipError_t e = launch_gemv_decode(p, dc, c->stream);
         if (e != hipSuccess) return hip_fail(c, e, "gemv decode launch");
         return 0;
@@ -2557,6 +2566,15 @@ int spq4k_chain_info(const spq4k_chain* ch, int* version, int* grid, int* n_stag
     if (version) *version = ch->version;
     if (grid) *grid = ch->grid;
     if (n_stages) *n_stages = ch->nstages;
+    return 0;
+}
+
+int spq4k_set_decode_stamps(spq4k_ctx* c, uint64_t* stamps, size_t n) {
+    if (!c) return -EINVAL;
+    if (stamps && (!aligned(stamps, 8) || n == 0))
+        return set_err(c, -EINVAL, "set_decode_stamps: misaligned or empty buffer");
+    c->dec_stamps = stamps;
+    c->dec_stamps_n = stamps ? n : 0;
     return 0;
 }
 

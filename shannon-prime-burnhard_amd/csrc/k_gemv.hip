@@ -131,9 +131,18 @@ __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)
 // RT: the row length is p.nb, any value up to NB (NB a multiple of 16, the
 // registers and LDS sized for NB); otherwise exactly NB blocks, known at
 // compile time.
-template <typename Fmt, int NB, int WAVES, int D, bool XFW, bool NORM, bool GLU, bool RT>
+template <typename Fmt, int NB, int WAVES, int D, bool XFW, bool NORM, bool GLU, bool RT, bool STAMP = false,
+          bool OP = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     static_assert(!GLU || D == 2, "the fused gate/up pair is the two rows in flight");
+    static_assert(!STAMP || !GLU, "timestamps cover the unfused form");
+    static_assert(!OP || (D > 1 && !GLU), "one pass of D rows a wave (OP) is an unfused form with D > 1");
+    // STAMP: the wave's start, its quantisation barrier, its first and its
+    // last row's store issued (s_memrealtime, 100 MHz), written by lane 0 at
+    // the end, after the last load (a store earlier would enter the vmcnt
+    // accounting of the loads in flight)
+    uint64_t st0 = 0, st1 = 0, st2 = 0;
+    if constexpr (STAMP) st0 = __builtin_amdgcn_s_memrealtime();
     static_assert(!RT || NB % 16 == 0, "a runtime row length is bounded by whole 16-block passes");
     using W = typename Fmt::W;
     constexpr int NIT = (NB + 15) / 16;           // blocks per lane per row
@@ -267,6 +276,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     // all quantised blocks visible (LDS writes only: weight loads stay in flight)
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
+    if constexpr (STAMP) st1 = __builtin_amdgcn_s_memrealtime();
     if (LATE) load_row(1, buf[1]);
 
     typename Fmt::R qr[NIT];
@@ -308,7 +318,35 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
             const Loc l = locate(g + i * G);
             l.y[l.row] = acc;
         }
+        if constexpr (STAMP)
+            if (i == 0) st2 = __builtin_amdgcn_s_memrealtime();
     };
+    auto finish = [&]() {
+        if constexpr (STAMP) {
+            const uint64_t st3 = __builtin_amdgcn_s_memrealtime();
+            if (lane == 0) {
+                uint64_t* s = p.stamps + ((size_t)blockIdx.x * WAVES + wave) * 4;
+                s[0] = st0;
+                s[1] = st1;
+                s[2] = st2;
+                s[3] = st3;
+            }
+        }
+    };
+    if constexpr (OP) {
+        // Every wave has at most D rows (the down projection's two): the
+        // pass written out, with no loop. At a loop header (the tail loop
+        // below), paths with different buffers loaded last meet and the
+        // compiler waits there for every load in flight, so the first row
+        // would wait for the second's loads too (issued late, after the
+        // quantisation barrier) and both rows would be consumed only after
+        // the second arrived.
+#pragma unroll
+        for (int u = 0; u < D; ++u)
+            if (u < nrows) consume(u, buf[u]);
+        finish();
+        return;
+    }
     int i0 = 0;
     if (D > 1) {
         // Whole passes whose reloads are all real rows: every pass reloads
@@ -335,6 +373,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
             }
         }
     }
+    finish();
 }
 
 // RMS norm of T rows (one workgroup of 256 threads a row): the squares
@@ -435,11 +474,45 @@ static hipError_t launch_t(const GemvParams& p, int bpr, int ntiles, hipStream_t
 
 int gemv_rows_per_tile(int bpr) { return 4 * (64 / (4 * bpr)); }
 
-template <typename Fmt, int NB, bool RT, int WAVES, int D, bool XFW, bool NORM = false, bool GLU = false>
+template <typename Fmt, int NB, bool RT, int WAVES, int D, bool XFW, bool NORM = false, bool GLU = false,
+          bool STAMP = false, bool OP = false>
 static hipError_t launch_dec(const GemvParams& p, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((gemv_decode_kernel<Fmt, NB, WAVES, D, XFW, NORM, GLU, RT>), dim3(grid), dim3(WAVES * 64), 0,
-                       st, p);
+    hipLaunchKernelGGL((gemv_decode_kernel<Fmt, NB, WAVES, D, XFW, NORM, GLU, RT, STAMP, OP>), dim3(grid),
+                       dim3(WAVES * 64), 0, st, p);
     return hipGetLastError();
+}
+
+// whether every wave of the launch has at most D rows (the one-pass form)
+static bool one_pass(const GemvParams& p, const DecodeCfg& c) {
+    return (int64_t)p.total_rows <= (int64_t)c.grid * c.waves * c.depth;
+}
+
+// the timestamped instances: the unfused Q4_K shapes the planner picks for
+// rows of 4096 (o, q/k/v, gate/up, lm_head) and 12288 (down, one or two rows
+// in flight)
+#define SPQ_DEC_STAMPED(X) \
+    X(16, 16, 1, false) X(16, 12, 1, false) X(16, 12, 2, true) X(48, 8, 2, false) X(48, 8, 1, false)
+
+bool decode_stamps_supported(int fmt, int nb, const DecodeCfg& c) {
+    if (fmt != WF_Q4K || c.norm || c.glu) return false;
+#define SPQ_STOK(N, W, DD, XF) \
+    if (nb == N && c.waves == W && c.depth == DD && c.xfirst == XF) return true;
+    SPQ_DEC_STAMPED(SPQ_STOK)
+#undef SPQ_STOK
+    return false;
+}
+
+static hipError_t launch_dec_stamped(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
+    if (!decode_stamps_supported(p.fmt, p.nb, c)) return hipErrorInvalidValue;
+#define SPQ_STL(N, W, DD, XF)                                                                      \
+    if (p.nb == N && c.waves == W && c.depth == DD && c.xfirst == XF) {                            \
+        if constexpr (DD == 2 && !XF)                                                               \
+            if (one_pass(p, c)) return launch_dec<FmtQ4K, N, false, W, DD, XF, false, false, true, true>(p, c.grid, st); \
+        return launch_dec<FmtQ4K, N, false, W, DD, XF, false, false, true>(p, c.grid, st);         \
+    }
+    SPQ_DEC_STAMPED(SPQ_STL)
+#undef SPQ_STL
+    return hipErrorInvalidValue;
 }
 
 // launch shapes that fit the register file: K = 12288 with two rows in flight
@@ -477,7 +550,11 @@ static hipError_t launch_dec_nb(const GemvParams& p, const DecodeCfg& c, hipStre
     }
 #define SPQ_DEC(W, DD, X)                                                                  \
     if constexpr (dec_shape_ok_fmt<Fmt>(NB, W, DD))                                        \
-        if (c.waves == W && c.depth == DD && c.xfirst == X) return launch_dec<Fmt, NB, RT, W, DD, X>(p, c.grid, st);
+        if (c.waves == W && c.depth == DD && c.xfirst == X) {                              \
+            if constexpr (DD == 2 && !X)                                                   \
+                if (one_pass(p, c)) return launch_dec<Fmt, NB, RT, W, DD, X, false, false, false, true>(p, c.grid, st); \
+            return launch_dec<Fmt, NB, RT, W, DD, X>(p, c.grid, st);                      \
+        }
     SPQ_DEC(16, 1, false) SPQ_DEC(16, 1, true) SPQ_DEC(16, 2, false) SPQ_DEC(16, 2, true)
     SPQ_DEC(12, 1, false) SPQ_DEC(12, 1, true) SPQ_DEC(12, 2, false) SPQ_DEC(12, 2, true)
     SPQ_DEC(8, 1, false) SPQ_DEC(8, 1, true) SPQ_DEC(8, 2, false) SPQ_DEC(8, 2, true)
@@ -551,6 +628,7 @@ static hipError_t launch_dec_bucket(const GemvParams& p, const DecodeCfg& c, hip
 }
 
 hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st) {
+    if (p.stamps) return launch_dec_stamped(p, c, st);
     if (p.fmt == WF_Q6K) {
         if (p.nb == 16) return launch_dec_nb<FmtQ6K, 16>(p, c, st);
         if (p.nb == 48) return launch_dec_nb<FmtQ6K, 48>(p, c, st);

@@ -41,6 +41,9 @@ struct GemvParams {
     // fusions of the T = 1 decode kernel (DecodeCfg.norm / .glu)
     const float* norm_w;  // x -> (x * 1/sqrt(mean(x^2) + eps)) * norm_w before quantisation
     float eps;
+    // wave timestamps of the T = 1 decode kernel (spq4k_set_decode_stamps):
+    // 4 uint64 a wave, or null
+    uint64_t* stamps;
 };
 
 // Launch shape of the T = 1 decode kernel (gemv_decode_kernel).
@@ -63,6 +66,9 @@ bool decode_supported(int fmt, int nb);
 constexpr int DEC_MAX_NB = 112;
 int decode_bucket(int fmt, int nb);
 hipError_t launch_gemv_decode(const GemvParams& p, const DecodeCfg& c, hipStream_t st);
+// whether the decode kernel has a timestamped instance (p.stamps) for this
+// shape: the unfused Q4_K launch shapes of rows of 4096 and 12288
+bool decode_stamps_supported(int fmt, int nb, const DecodeCfg& c);
 // whether the decode kernel has the fused form c (norm / glu) for this format and row length
 bool decode_fused_supported(int fmt, int nb, const DecodeCfg& c);
 // ggml_rms_norm then ggml_mul by w (ggml-cpu/ops.cpp:3724-3784): y[t] = (x[t] * s_t) * w,

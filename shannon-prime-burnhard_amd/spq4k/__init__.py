@@ -147,6 +147,7 @@ def load_library(path: str | None = None):
         "spq4k_chain_free": (None, [V]),
         "spq4k_chain_info": (I, [V, C.POINTER(I), C.POINTER(I), C.POINTER(I)]),
         "spq4k_chain_set_stamps": (I, [V, V, V]),
+        "spq4k_set_decode_stamps": (I, [V, V, S]),
     }
     sig.update(_gguf_sig())
     _bind(lib, sig)
@@ -615,6 +616,11 @@ class Context:
         yb = (C.c_void_p * n)(*Y_devs)
         self._check("spq4k_moe_multi", self.lib.spq4k_moe_multi(self.handle, n, hb, ids_dev, n_used, ne11, T,
                                                                X_dev, yb))
+
+    def set_decode_stamps(self, ptr, n: int = 0):
+        """spq4k_set_decode_stamps (include/spq4k_diag.h): a device buffer of n uint64
+        for the decode kernel's wave timestamps, or None to stop."""
+        self._check("spq4k_set_decode_stamps", self.lib.spq4k_set_decode_stamps(self.handle, ptr or None, n))
 
     def stream_read_dev(self, p: int, nbytes: int):
         """spq4k_stream_read: one launch that only reads nbytes at p (the streaming floor)."""

@@ -68,10 +68,10 @@ def test_no_device_is_an_error_not_a_fallback():
 
 def test_dropin_header_declares_no_diagnostics():
     """include/spq4k.h holds the drop-in entry points only; the measurement
-    probe, the integer-sum views and the chain timestamps live in
-    include/spq4k_diag.h"""
+    probe, the integer-sum views and the chain and decode-kernel timestamps
+    live in include/spq4k_diag.h"""
     diag = {"spq4k_stream_read", "spq4k_subblock_sums", "spq4k_subblock_sums_type", "spq4k_chain_info",
-            "spq4k_chain_set_stamps"}
+            "spq4k_chain_set_stamps", "spq4k_set_decode_stamps"}
     dropin = set(declared_functions([os.path.join(REPO, "include", "spq4k.h")]))
     assert not (dropin & diag), f"diagnostics in the drop-in header: {sorted(dropin & diag)}"
     assert diag <= set(declared_functions([os.path.join(REPO, "include", "spq4k_diag.h")]))

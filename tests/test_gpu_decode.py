@@ -168,3 +168,58 @@ def test_decode_any_k_q5k_q6k(ctx, oracle, qtype, K):
     got = ctx.mul_mat(ctx.upload(W, M, K, type=qtype), x)
     _check(got, oracle.mul_mat_type(qtype, W, M, K, x), f"decode type={qtype} K={K}",
            oracle.mul_mat_dq_f64(qtype, W, M, K, x))
+
+
+@pytest.mark.parametrize("M,K,shape", [(4096, 4096, (16, 1)), (6144, 4096, (12, 1)), (33000, 4096, (12, 2)),
+                                       (4096, 12288, (8, 2)), (300, 12288, (8, 2))])
+def test_decode_stamps(ctx, oracle, M, K, shape):
+    """The timestamped decode instances (spq4k_set_decode_stamps,
+    include/spq4k_diag.h): the same outputs bit for bit as the plain
+    instances, one stamp set per wave of the launch, each wave's stamps in
+    order (start <= barrier <= first row <= last row), and -EINVAL for a
+    buffer too small or a shape without a timestamped instance."""
+    from spq4k import Spq4kError
+    from spq4k.hip import DeviceArray
+    rng = np.random.default_rng(M + K)
+    W = _weights(oracle, rng, M, K)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    Wd = ctx.upload(W, M, K)
+    plain = ctx.mul_mat(Wd, x)
+    n = 256 * 16 * 4
+    buf = DeviceArray(n, np.uint64)
+    buf.fill_byte(0)
+    try:
+        ctx.set_decode_stamps(buf.ptr, n)
+        stamped = ctx.mul_mat(Wd, x)
+        ctx.set_decode_stamps(None)
+        np.testing.assert_array_equal(stamped.view(np.uint32), plain.view(np.uint32))
+        _check(stamped, oracle.mul_mat(W, M, K, x), f"stamped decode M={M} K={K}")
+        s = buf.to_host().reshape(-1, 4).astype(np.int64)
+        live = s[:, 0] != 0
+        waves, _ = shape
+        grid = min(256, (M + waves - 1) // waves)
+        assert live.sum() == grid * waves and live[:grid * waves].all(), (int(live.sum()), grid * waves)
+        s = s[live]
+        rows = s[:, 2] != 0
+        assert rows.sum() == min(M, grid * waves)
+        assert (s[:, 0] <= s[:, 1]).all() and (s[:, 1] <= s[:, 3]).all()
+        assert (s[rows, 1] <= s[rows, 2]).all() and (s[rows, 2] <= s[rows, 3]).all()
+        assert (s[:, 3] - s[:, 0]).max() < 100_000_000   # under a second of the 100 MHz clock
+        # errors while stamps are set: a buffer smaller than grid * waves * 4,
+        # and a row length without a timestamped instance
+        ctx.set_decode_stamps(buf.ptr, 4 * grid * waves - 1)
+        with pytest.raises(Spq4kError):
+            ctx.mul_mat(Wd, x)
+        ctx.set_decode_stamps(buf.ptr, n)
+        W2 = _weights(oracle, rng, 64, 8192)
+        W2d = ctx.upload(W2, 64, 8192)
+        x2 = rng.standard_normal((1, 8192)).astype(np.float32)
+        with pytest.raises(Spq4kError):
+            ctx.mul_mat(W2d, x2)
+        ctx.set_decode_stamps(None)
+        _check(ctx.mul_mat(W2d, x2), oracle.mul_mat(W2, 64, 8192, x2), "after stamps off")
+        W2d.free()
+    finally:
+        ctx.set_decode_stamps(None)
+        buf.free()
+        Wd.free()
