@@ -249,7 +249,9 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
 //                            against 16.7), two rows a wave with the second row's
 //                            loads issued after the quantisation barrier (8.50-8.52
 //                            against 8.61-8.63 us with one row in flight; both rows
-//                            at the start 9.55); other formats 12 waves, x-first
+//                            at the start 9.55), each consumed as it arrives (the
+//                            one-pass form when a wave has at most two rows: 8.07
+//                            in the 8B step); other formats 12 waves, x-first
 //   K = 27648              : 8 waves (the registers of 7 Q8_K blocks a lane), x-first
 DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb_rows, int64_t rows, bool fused = false) {
     DecodeCfg d{};
