@@ -365,93 +365,137 @@ __global__ __launch_bounds__(WAVES * 64) void moe_decode_kernel(MoeFusedParams p
             }
         }
     };
-    // order of the loads (they complete in order): the expert id of the first
-    // row, the first pass of input rows, then that row's weights, so that the
-    // quantisation waits only for x while the weights are in flight
+    // order of the loads (they complete in order): the expert ids of the
+    // call (for the LDS copy the later passes read), the expert id of the
+    // first row, the first pass of input rows, then the first passes'
+    // weights, so that the quantisation waits only for x while the weights
+    // are in flight
+    __shared__ int32_t ids_s[MOE_DEC_MAX_PAIRS];
+    auto locate_s = [&](int r) {                 // locate with the expert id from LDS
+        Loc l;
+        const int rc = r < r1 ? r : r1 - 1;
+        const int pr = rc / MV;
+        const int v = rc - pr * MV;
+        const bool second = !GLU && v >= M;
+        const int lr = second ? v - M : v;
+        const int e = ids_s[pr];
+        l.e = (r < r1 && e >= 0 && e < p.E) ? e : -1;
+        l.xs = (xrow(rc) - xlo) * NB;
+        const size_t eo = (size_t)(l.e >= 0 ? l.e : 0);
+        l.w = (second ? p.bank1 + eo * p.expert_bytes1 : p.bank + eo * p.expert_bytes) +
+              (size_t)lr * ((size_t)NB * Fmt::BYTES);
+        l.w1 = GLU ? p.bank1 + eo * p.expert_bytes1 + (size_t)lr * ((size_t)NB * Fmt::BYTES) : l.w;
+        l.y = second ? p.Y1 + (int64_t)pr * p.M1 + lr : p.Y + (int64_t)pr * M + lr;
+        return l;
+    };
     const int item_a = wave * 4 + (lane >> 4);
     const int ci_a = item_a < nitems ? item_a : nitems - 1;
-    // passes of the workgroup's rows, DP at a time: the next DP passes are
-    // loaded while these are computed (uniform over the workgroup; a lane
-    // whose row lies past r1 loads row r1 - 1 again and drops it). Two for
-    // the plain sweep of rows of 8 or more blocks; one for the GLU sweep,
-    // whose gate and up rows already double the loads of a pass and whose
-    // registers would allow only one workgroup a CU with two, and for short
-    // rows (the down bank's 3 blocks: measured no faster, one token slower)
+    // passes of the workgroup's rows, DP at a time in register slots. With
+    // more passes than slots, each slot is reloaded with the pass DP ahead as
+    // soon as it is computed, every reload unconditional (a lane whose row
+    // lies past r1 loads row r1 - 1 again and drops it) and its expert id
+    // read from LDS, so the next passes' weights are in flight while these
+    // are computed and the compiler's waits stay exact (a load under a
+    // branch, or one whose address waits for an id load, would make it wait
+    // for every load in flight). One slot for the GLU sweep, whose gate and
+    // up rows already double the loads of a pass (two slots: T = 4 26.9
+    // against 25.3 us for the routed-expert block), and for the down bank's
+    // short rows (3 blocks: measured no faster, one token slower).
     constexpr int DP = (GLU || NB < 8) ? 1 : 2;
     const int npass = (r1 - r0 + RPG - 1) / RPG;
     Loc cur[DP];
     W w[DP][NIT];
     W w1[DP][GLU ? NIT : 1];
-    cur[0] = locate(g0);
-    const XRegs xa = load_x16(p.X, p.K, xlo + ci_a / NB, ci_a % NB);
-#pragma unroll
-    for (int d = 0; d < DP; ++d) {
-        if (d > 0) {
-            cur[d] = locate(g0 + d * RPG);
-            if (d < npass) load(cur[d], w[d], w1[d]);   // uniform
-        } else {
-            load(cur[d], w[d], w1[d]);
+    // the rest of the staging (the first pass of x already loaded) and, for
+    // the multi-pass form, the LDS copy of the expert ids
+    auto stage_rest = [&](const XRegs& xa, bool copy_ids, int32_t id_mine) {
+        store_q8_item(xa, item_a < nitems, ci_a, L);
+        for (int base = 4 * WAVES; base < nitems; base += 4 * WAVES) {
+            const int item0 = base + item_a;
+            const bool valid = item0 < nitems;
+            const int item = valid ? item0 : nitems - 1;
+            const XRegs r = load_x16(p.X, p.K, xlo + item / NB, item % NB);
+            store_q8_item(r, valid, item, L);
         }
-    }
-    store_q8_item(xa, item_a < nitems, ci_a, L);
-    for (int base = 4 * WAVES; base < nitems; base += 4 * WAVES) {
-        const int item0 = base + item_a;
-        const bool valid = item0 < nitems;
-        const int item = valid ? item0 : nitems - 1;
-        const XRegs r = load_x16(p.X, p.K, xlo + item / NB, item % NB);
-        store_q8_item(r, valid, item, L);
-    }
-    __syncthreads();
-    for (int pass = 0; pass < npass; pass += DP) {
-        Loc nxt[DP];
-        W wn[DP][NIT];
-        W wn1[DP][GLU ? NIT : 1];
-        const bool more = pass + DP < npass;
-        if (more) {
+        if (copy_ids && (int)threadIdx.x < p.n_pairs) ids_s[threadIdx.x] = id_mine;
+        __syncthreads();
+    };
+    // the sweep row r (pass pd of this lane) with the weights in wv / wv1
+    auto compute = [&](int pd, const Loc& l, const W (&wv)[NIT], const W (&wv1)[GLU ? NIT : 1]) {
+        const int r = g0 + pd * RPG;
+        float acc[1] = {0.0f};
 #pragma unroll
-            for (int d = 0; d < DP; ++d) {
-                nxt[d] = locate(g0 + (pass + DP + d) * RPG);
-                if (pass + DP + d < npass) load(nxt[d], wn[d], wn1[d]);   // uniform
-            }
+        for (int it = 0; it < NIT; ++it) {
+            const int bb = bsub + BSL * it;
+            Fmt::template dot<1>(wv[it], l4, L, l.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && l.e >= 0, acc);
         }
-#pragma unroll
-        for (int d = 0; d < DP; ++d) {
-            if (pass + d >= npass) break;        // uniform
-            const int r = g0 + (pass + d) * RPG;
-            float acc[1] = {0.0f};
+        float sum = group_sum_last<LPR>(acc[0]);
+        if constexpr (GLU) {
+            float acc1[1] = {0.0f};
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 const int bb = bsub + BSL * it;
-                Fmt::template dot<1>(w[d][it], l4, L, cur[d].xs + (bb < NB ? bb : NB - 1), 0,
-                                     bb < NB && cur[d].e >= 0, acc);
+                Fmt::template dot<1>(wv1[it], l4, L, l.xs + (bb < NB ? bb : NB - 1), 0, bb < NB && l.e >= 0, acc1);
             }
-            float sum = group_sum_last<LPR>(acc[0]);
-            if constexpr (GLU) {
-                float acc1[1] = {0.0f};
-#pragma unroll
-                for (int it = 0; it < NIT; ++it) {
-                    const int bb = bsub + BSL * it;
-                    Fmt::template dot<1>(w1[d][it], l4, L, cur[d].xs + (bb < NB ? bb : NB - 1), 0,
-                                         bb < NB && cur[d].e >= 0, acc1);
-                }
-                sum = moe_silu(sum) * group_sum_last<LPR>(acc1[0]);
-            }
-            if (r < r1 && cur[d].e >= 0 && (lane & (LPR - 1)) == LPR - 1) *cur[d].y = sum;
+            sum = moe_silu(sum) * group_sum_last<LPR>(acc1[0]);
         }
-        if (more) {
+        if (r < r1 && l.e >= 0 && (lane & (LPR - 1)) == LPR - 1) *l.y = sum;
+    };
+    if (npass > DP) {   // uniform over the workgroup
+        // the call's expert ids (copied to LDS with the staging), every
+        // slot's expert id, then x, then every slot's weights: a weight load
+        // then waits only for its own id, and at the loop header the slots'
+        // loads are in flight in slot order, as on every pass
+        const int32_t id_mine = p.ids[(int)threadIdx.x < p.n_pairs ? threadIdx.x : 0];
+#pragma unroll
+        for (int d = 0; d < DP; ++d) cur[d] = locate(g0 + d * RPG);
+        const XRegs xa = load_x16(p.X, p.K, xlo + ci_a / NB, ci_a % NB);
+#pragma unroll
+        for (int d = 0; d < DP; ++d) load(cur[d], w[d], w1[d]);
+        stage_rest(xa, true, id_mine);
+        int pass = 0;
+        for (; pass + 2 * DP <= npass; pass += DP) {
 #pragma unroll
             for (int d = 0; d < DP; ++d) {
-                cur[d] = nxt[d];
+                compute(pass + d, cur[d], w[d], w1[d]);
+                cur[d] = locate_s(g0 + (pass + DP + d) * RPG);
+                load(cur[d], w[d], w1[d]);
+            }
+        }
+        // the last one or two rounds, written out, reloading only real passes
 #pragma unroll
-                for (int it = 0; it < NIT; ++it) w[d][it] = wn[d][it];
-                if constexpr (GLU) {
-#pragma unroll
-                    for (int it = 0; it < NIT; ++it) w1[d][it] = wn1[d][it];
+        for (int d = 0; d < DP; ++d) {
+            if (pass + d < npass) {
+                compute(pass + d, cur[d], w[d], w1[d]);
+                if (pass + DP + d < npass) {
+                    cur[d] = locate_s(g0 + (pass + DP + d) * RPG);
+                    load(cur[d], w[d], w1[d]);
                 }
             }
         }
+        pass += DP;
+#pragma unroll
+        for (int d = 0; d < DP; ++d)
+            if (pass + d < npass) compute(pass + d, cur[d], w[d], w1[d]);
+    } else {
+        cur[0] = locate(g0);
+        const XRegs xa = load_x16(p.X, p.K, xlo + ci_a / NB, ci_a % NB);
+#pragma unroll
+        for (int d = 0; d < DP; ++d) {
+            if (d > 0) {
+                cur[d] = locate(g0 + d * RPG);
+                if (d < npass) load(cur[d], w[d], w1[d]);   // uniform
+            } else {
+                load(cur[d], w[d], w1[d]);
+            }
+        }
+        stage_rest(xa, false, 0);
+#pragma unroll
+        for (int d = 0; d < DP; ++d)
+            if (d < npass) compute(d, cur[d], w[d], w1[d]);
     }
 }
+
 
 // The routed-expert block's down projection with the weighted sum over the
 // slots as its epilogue (small batches, n_used <= 8): one wave per output
