@@ -1041,7 +1041,8 @@ def run_decode_stamps(args):
     first wave start (the device's 100 MHz clock):
       start     the last wave's start,
       barrier   the median / last wave past the quantisation barrier,
-      first     the median wave's first row store issued,
+      first     the median wave's first row done (its store issued, in
+                the forms that store each row at once),
       end       the median / last wave's last row store issued,
       gap       from the previous stage's last store issued to this launch's
                 first wave start (store completion, kernel end and dispatch)."""

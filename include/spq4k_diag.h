@@ -63,8 +63,10 @@ int spq4k_chain_set_stamps(spq4k_ctx *ctx, spq4k_chain *chain, uint64_t *stamps)
  *   k = 0  the wave started,
  *   k = 1  it passed the barrier that publishes the workgroup's Q8_K
  *          activations in LDS,
- *   k = 2  it had issued the store of its first row (0: a wave without rows),
- *   k = 3  it had issued the store of its last row.
+ *   k = 2  its first row's dot product was done and, in the forms that
+ *          store each row at once, its store issued (0: a wave without rows),
+ *   k = 3  it had issued the store of its last row (every row's store, in
+ *          the forms that collect a wave's results for one store at the end).
  * Each launch overwrites the buffer. Only the Q4_K launch shapes the planner
  * picks for rows of K = 4096 and K = 12288 (the 8B step's) have a
  * timestamped instance: another shape, or a launch whose grid * waves * 4

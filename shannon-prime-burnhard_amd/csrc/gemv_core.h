@@ -326,7 +326,8 @@ __device__ __forceinline__ float block_dot_reg(const W4& w, int l4, const Q8Reg&
     int sc0, sc1, m0, m1, S0, S1;
     scales_of_quarter(w.hdr, l4, sc0, sc1, m0, m1);
     subblock_sums_reg(w, q.a, S0, S1);
-    const int A = sc0 * S0 + sc1 * S1;
+    // |S| <= 32 * 15 * 127 and sc <= 63: exact in 24-bit multiplies (full rate)
+    const int A = __mul24(sc0, S0) + __mul24(sc1, S1);
     const int B = m0 * q.bsA + m1 * q.bsB;
     acc = fmaf(d * q.d8, (float)A, acc);
     acc = fmaf(-(dmin * q.d8), (float)B, acc);

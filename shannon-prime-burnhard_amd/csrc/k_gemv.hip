@@ -91,6 +91,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
     }
 }
 
+template <int N>
+struct RegWords {
+    uint32_t v[N];
+};
+
+// Marks every register of the row buffers b as needed here, so that the
+// compiler waits for their loads at this point (loads complete in order: the
+// wait covers those loads and the ones before them, not the later ones).
+template <int NIT, typename W>
+__device__ __forceinline__ void arrived(const W (&b)[NIT]) {
+    static_assert(sizeof(W) % 4 == 0, "row buffers are whole registers");
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const auto w = __builtin_bit_cast(RegWords<sizeof(W) / 4>, b[it]);
+#pragma unroll
+        for (int k = 0; k < (int)(sizeof(W) / 4); ++k) asm volatile("" ::"v"(w.v[k]));
+    }
+}
+
 // Sum of squares of the lane's 16 x values in double (ggml_float), as the
 // CPU's rms_norm accumulates them (ops.cpp:3757-3761: each square rounded to
 // fp32, then added in double).
@@ -137,8 +156,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     static_assert(!GLU || D == 2, "the fused gate/up pair is the two rows in flight");
     static_assert(!STAMP || !GLU, "timestamps cover the unfused form");
     static_assert(!OP || (D > 1 && !GLU), "one pass of D rows a wave (OP) is an unfused form with D > 1");
-    // STAMP: the wave's start, its quantisation barrier, its first and its
-    // last row's store issued (s_memrealtime, 100 MHz), written by lane 0 at
+    // claimed rows: the unfused form with one row in flight
+    // EI: one row in flight, the next row's loads issued early (K <= 4096;
+    // at K = 12288 two rows in flight from the start are faster)
+    constexpr int NIT_ = (NB + 15) / 16;
+    constexpr bool EI = D == 1 && !GLU && !OP && NIT_ == 1;
+    // DYN2: two rows in flight, rows claimed from the workgroup's counter
+    constexpr bool DYN2 = D == 2 && !GLU && !OP;
+    // STAMP: the wave's start, its quantisation barrier, its first row done
+    // and its last row's store issued (s_memrealtime, 100 MHz), written by lane 0 at
     // the end, after the last load (a store earlier would enter the vmcnt
     // accounting of the loads in flight)
     uint64_t st0 = 0, st1 = 0, st2 = 0;
@@ -152,6 +178,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     const int QW = (nb + 3) / 4;                  // quantising waves
     const size_t ROWB = (size_t)nb * Fmt::BYTES;
     __shared__ __align__(16) char q8s[q8lds_bytes(NB)];
+    __shared__ int next_slot;                    // DYN2: the workgroup's next row slot
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l4 = lane & 3;
@@ -186,13 +213,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
         else { l.w = W0; l.y = Y0; l.row = r; }
         return l;
     };
-    W buf[D][NIT];
+    W buf[EI ? 2 : D][NIT];
     // rows past the end re-read the last row (in bounds; never stored): the
     // first D loads are unconditional so that the compiler's wait counts for
     // x stay exact (a load under a branch makes it wait for every load)
     auto load_row = [&](int i, W (&b)[NIT]) {
         const int r0 = g + i * G;
         const int r = r0 < Mtot ? r0 : Mtot - 1;
+        const Loc l = locate(r);
+        const uint8_t* wr = l.w + (size_t)l.row * ROWB;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int bb = bsub + 16 * it;
+            b[it] = Fmt::load(wr + (size_t)(bb < nb ? bb : nb - 1) * Fmt::BYTES, l4);
+        }
+    };
+    // row r (< Mtot) of the concatenated segments
+    auto load_at = [&](int r, W (&b)[NIT]) {
         const Loc l = locate(r);
         const uint8_t* wr = l.w + (size_t)l.row * ROWB;
 #pragma unroll
@@ -273,6 +310,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
             if (!LATE || u == 0) load_row(u, buf[u]);
     }
     if (!XFW) quantise();
+    if (DYN2 && threadIdx.x == 0) next_slot = 0;
     // all quantised blocks visible (LDS writes only: weight loads stay in flight)
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
@@ -306,21 +344,27 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
         }
         return;
     }
-    auto consume = [&](int i, const W (&b)[NIT]) {
+    // the dot product of the row in buffer b with x, in lane 63
+    auto dot_row = [&](const W (&b)[NIT]) -> float {
         float acc = 0.0f;
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const float a = Fmt::dot_reg(b[it], l4, qr[it], acc);
             acc = (bsub + 16 * it < nb) ? a : acc;
         }
-        acc = group_sum_last<64>(acc);
+        return group_sum_last<64>(acc);
+    };
+    // row r of the concatenated segments from the buffer b; first: the wave's first row
+    auto consume_row = [&](int r, bool first, const W (&b)[NIT]) {
+        const float acc = dot_row(b);
         if (lane == 63) {
-            const Loc l = locate(g + i * G);
+            const Loc l = locate(r);
             l.y[l.row] = acc;
         }
         if constexpr (STAMP)
-            if (i == 0) st2 = __builtin_amdgcn_s_memrealtime();
+            if (first) st2 = __builtin_amdgcn_s_memrealtime();
     };
+    auto consume = [&](int i, const W (&b)[NIT]) { consume_row(g + i * G, i == 0, b); };
     auto finish = [&]() {
         if constexpr (STAMP) {
             const uint64_t st3 = __builtin_amdgcn_s_memrealtime();
@@ -344,6 +388,97 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
 #pragma unroll
         for (int u = 0; u < D; ++u)
             if (u < nrows) consume(u, buf[u]);
+        finish();
+        return;
+    }
+    if (EI && Mtot > G) {
+        // One row in flight, the next row's loads issued as soon as the
+        // current row has arrived, before its dot product: the wave's
+        // compute no longer sits between one row's arrival and the next
+        // row's request. (Issuing them earlier, two rows in flight, is slower
+        // at these sizes; so is claiming rows from a workgroup counter.)
+        // Taken when waves have two rows or more; a wave of one row runs the
+        // loop below. Two buffers alternate. The results are collected in a
+        // register, lane k holding the wave's row k, and stored together at
+        // the end (every 64 rows): with no store in the loop, the wait for
+        // each row is for that row's loads alone (a store in flight would be
+        // waited for too, and a load into a register that a store in flight
+        // reads waits for everything before it). A load past the wave's last
+        // row re-reads that row (cached), so that the loop is entered and
+        // re-entered with the same loads in flight.
+        if (nrows > 0) {
+            auto row_of = [&](int i) { return g + (i < nrows ? i : nrows - 1) * G; };
+            float res = 0.0f;
+            auto flush = [&](int i0, int n) {
+                const int r = g + (i0 + lane) * G;
+                if (lane < n) {
+                    float* y = r >= R3 ? Y3 + (r - R3) : r >= R2 ? Y2 + (r - R2) : r >= R1 ? Y1 + (r - R1) : Y0 + r;
+                    *y = res;
+                }
+            };
+            auto put = [&](int i, float acc) {
+                const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 63));
+                res = lane == (i & 63) ? v : res;
+                if ((i & 63) == 63) flush(i - 63, 64);
+            };
+            arrived<NIT>(buf[0]);
+            load_at(row_of(1), buf[EI]);
+            put(0, dot_row(buf[0]));
+            if constexpr (STAMP) st2 = __builtin_amdgcn_s_memrealtime();
+            int i = 1;
+            for (; i + 1 < nrows; i += 2) {
+                arrived<NIT>(buf[EI]);
+                load_at(row_of(i + 1), buf[0]);
+                put(i, dot_row(buf[EI]));
+                arrived<NIT>(buf[0]);
+                load_at(row_of(i + 2), buf[EI]);
+                put(i + 1, dot_row(buf[0]));
+            }
+            if (i < nrows) put(i, dot_row(buf[EI]));
+            if (nrows & 63) flush(nrows & ~63, nrows & 63);
+        }
+        finish();
+        return;
+    }
+    if (DYN2 && Mtot > 2 * G) {
+        // Two rows in flight, claimed likewise after each wave's first two
+        // (slots wave and wave + WAVES, rows g and g + G): every pass consumes
+        // each buffer and reloads it with a claimed row, so the loop header
+        // always has both buffers' loads in flight in the same order; the
+        // first claim past the rows ends the loop and the other buffer's row
+        // is consumed after it. A wave with fewer than two rows has no claims
+        // to make (every slot after its first two lies past the rows).
+        if (nrows >= 2) {
+            int r0 = g, r1 = g + G;
+            bool first = true;
+            for (;;) {
+                int slot = 0;
+                if (lane == 0) slot = __hip_atomic_fetch_add(&next_slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                consume_row(r0, first, buf[0]);
+                first = false;
+                slot = __builtin_amdgcn_readfirstlane(slot) + 2 * WAVES;
+                int next = blockIdx.x * WAVES + slot % WAVES + (slot / WAVES) * G;
+                if (next >= Mtot) {
+                    consume_row(r1, false, buf[1]);
+                    break;
+                }
+                r0 = next;
+                load_at(r0, buf[0]);
+                slot = 0;
+                if (lane == 0) slot = __hip_atomic_fetch_add(&next_slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                consume_row(r1, false, buf[1]);
+                slot = __builtin_amdgcn_readfirstlane(slot) + 2 * WAVES;
+                next = blockIdx.x * WAVES + slot % WAVES + (slot / WAVES) * G;
+                if (next >= Mtot) {
+                    consume_row(r0, false, buf[0]);
+                    break;
+                }
+                r1 = next;
+                load_at(r1, buf[1]);
+            }
+        } else if (nrows == 1) {
+            consume_row(g, true, buf[0]);
+        }
         finish();
         return;
     }

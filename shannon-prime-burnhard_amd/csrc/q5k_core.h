@@ -69,7 +69,8 @@ __device__ __forceinline__ float block_dot5_reg(const W5& w, int l4, const Q8Reg
         S0 = dot4(n.lo[i], q.a[i], S0);
         S1 = dot4(n.hi[i], q.a[8 + i], S1);
     }
-    const int A = sc0 * S0 + sc1 * S1;
+    // |S| <= 32 * 31 * 127 and sc <= 63: exact in 24-bit multiplies (full rate)
+    const int A = __mul24(sc0, S0) + __mul24(sc1, S1);
     const int B = m0 * q.bsA + m1 * q.bsB;
     acc = fmaf(d * q.d8, (float)A, acc);
     acc = fmaf(-(dmin * q.d8), (float)B, acc);

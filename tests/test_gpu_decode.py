@@ -69,10 +69,12 @@ _CFGS = [(w, d, xf) for w in (8, 12, 16) for d in (1, 2) for xf in (0, 1)]
 @pytest.mark.parametrize("waves,depth,xfirst", _CFGS)
 def test_decode_launch_shapes(oracle, waves, depth, xfirst):
     """Every compiled instantiation, with a small grid so that each wave walks
-    several rows (the depth pipeline and its ragged tail) and a full grid
-    (K = 27648 runs 8 waves and one row in flight whatever is asked)."""
+    several rows (the depth pipeline and its ragged tail; 2000 rows over 24
+    waves: 84 rows a wave, past the 64 results one register collects) and a
+    full grid (K = 27648 runs 8 waves and one row in flight whatever is
+    asked)."""
     rng = np.random.default_rng(1000 + waves * 10 + depth * 2 + xfirst)
-    cases = [(1000, 4096), (333, 12288), (210, 5120), (77, 27648), (130, 2048), (90, 8192), (61, 14336),
+    cases = [(1000, 4096), (2000, 4096), (333, 12288), (210, 5120), (77, 27648), (130, 2048), (90, 8192), (61, 14336),
              (40, 20480), (33, 24576), (29, 28416)]
     data = [(M, K, _weights(oracle, rng, M, K), rng.standard_normal((1, K)).astype(np.float32)) for M, K in cases]
     for grid in (3, 0):
