@@ -238,11 +238,16 @@ int pick_bpr(const spq4k_ctx* c, const int64_t* M, int n) {
 
 // Launch shape of the T = 1 decode kernel. One workgroup per CU, so that x is
 // quantised once per CU, one wave per row; measured on MI355X for the 8B
-// decode shapes (cold weights, graph replay):
-//   K = 4096,  M <= 4096   : 16 waves                   (o projection)
-//   K = 4096,  M <= 8192   : 12 waves = 2 rows a wave   (q/k/v, 6144 rows)
-//   K = 4096,  M <= 32768  : 16 waves                   (gate/up, 24576 rows)
-//   K = 4096,  larger M    : 12 waves, 2 rows in flight, x-first (lm_head)
+// decode shapes (cold weights, graph replay, us a launch in the step's
+// stage replay, one run against the previous choice):
+//   K = 4096,  M <= 4096   : 16 waves, x-first          (o projection: 4.05
+//                            against 4.11 without x-first)
+//   K = 4096,  M <= 8192   : 16 waves                   (q/k/v, 6144 rows: 5.20
+//                            against 5.46 with 12 waves = 2 rows a wave)
+//   K = 4096,  M <= 32768  : 16 waves                   (gate/up, 24576 rows:
+//                            11.11 against 11.24 x-first)
+//   K = 4096,  larger M    : 8 waves, 2 rows in flight, x-first (lm_head:
+//                            62.0 against 63.4 with 12 waves)
 //   K = 12288, Q4_K        : 8 waves, weights first (4096 x 12288: 8.21 against
 //                            8.52 us with 16 waves x-first; 1024 rows 5.25 against
 //                            6.53, 28672 rows 35.7 against 36.8, 12288 rows 16.8
@@ -265,13 +270,13 @@ DecodeCfg plan_decode(const spq4k_ctx* c, int fmt, int nb_rows, int64_t rows, bo
     } else if (nb >= 48) {
         d.waves = 16; d.depth = 1; d.xfirst = true;
     } else if (rows <= 4096) {
-        d.waves = 16; d.depth = 1; d.xfirst = false;
+        d.waves = 16; d.depth = 1; d.xfirst = true;
     } else if (rows <= 8192) {
-        d.waves = 12; d.depth = 1; d.xfirst = false;
+        d.waves = 16; d.depth = 1; d.xfirst = false;
     } else if (rows <= 32768) {
         d.waves = 16; d.depth = 1; d.xfirst = false;
     } else {
-        d.waves = 12; d.depth = 2; d.xfirst = true;
+        d.waves = 8; d.depth = 2; d.xfirst = true;
     }
     if (c->dec_force.waves) d.waves = c->dec_force.waves;
     if (c->dec_force.depth) d.depth = c->dec_force.depth;

@@ -626,7 +626,7 @@ static bool one_pass(const GemvParams& p, const DecodeCfg& c) {
 // rows of 4096 (o, q/k/v, gate/up, lm_head) and 12288 (down, one or two rows
 // in flight)
 #define SPQ_DEC_STAMPED(X) \
-    X(16, 16, 1, false) X(16, 12, 1, false) X(16, 12, 2, true) X(48, 8, 2, false) X(48, 8, 1, false)
+    X(16, 16, 1, false) X(16, 16, 1, true) X(16, 8, 2, true) X(48, 8, 2, false) X(48, 8, 1, false)
 
 bool decode_stamps_supported(int fmt, int nb, const DecodeCfg& c) {
     if (fmt != WF_Q4K || c.norm || c.glu) return false;

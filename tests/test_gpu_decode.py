@@ -172,7 +172,7 @@ def test_decode_any_k_q5k_q6k(ctx, oracle, qtype, K):
            oracle.mul_mat_dq_f64(qtype, W, M, K, x))
 
 
-@pytest.mark.parametrize("M,K,shape", [(4096, 4096, (16, 1)), (6144, 4096, (12, 1)), (33000, 4096, (12, 2)),
+@pytest.mark.parametrize("M,K,shape", [(4096, 4096, (16, 1)), (6144, 4096, (16, 1)), (33000, 4096, (8, 2)),
                                        (4096, 12288, (8, 2)), (300, 12288, (8, 2))])
 def test_decode_stamps(ctx, oracle, M, K, shape):
     """The timestamped decode instances (spq4k_set_decode_stamps,
