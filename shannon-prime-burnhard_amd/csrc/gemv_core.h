@@ -334,6 +334,25 @@ __device__ __forceinline__ float block_dot_reg(const W4& w, int l4, const Q8Reg&
     return acc;
 }
 
+template <int N>
+struct RegWords {
+    uint32_t v[N];
+};
+
+// Marks every register of the row buffers b as needed here, so that the
+// compiler waits for their loads at this point (loads complete in order: the
+// wait covers those loads and the ones before them, not the later ones).
+template <int NIT, typename W>
+__device__ __forceinline__ void arrived(const W (&b)[NIT]) {
+    static_assert(sizeof(W) % 4 == 0, "row buffers are whole registers");
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const auto w = __builtin_bit_cast(RegWords<sizeof(W) / 4>, b[it]);
+#pragma unroll
+        for (int k = 0; k < (int)(sizeof(W) / 4); ++k) asm volatile("" ::"v"(w.v[k]));
+    }
+}
+
 // Quantise activation blocks into LDS. Work items are (t, block) pairs,
 // item i -> t = i / nblk, block kb0 + i % nblk. Each 16-lane row of a wave
 // quantises one item per pass. X rows are 16-byte aligned (checked on host).

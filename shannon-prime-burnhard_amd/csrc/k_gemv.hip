@@ -91,25 +91,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
     }
 }
 
-template <int N>
-struct RegWords {
-    uint32_t v[N];
-};
-
-// Marks every register of the row buffers b as needed here, so that the
-// compiler waits for their loads at this point (loads complete in order: the
-// wait covers those loads and the ones before them, not the later ones).
-template <int NIT, typename W>
-__device__ __forceinline__ void arrived(const W (&b)[NIT]) {
-    static_assert(sizeof(W) % 4 == 0, "row buffers are whole registers");
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const auto w = __builtin_bit_cast(RegWords<sizeof(W) / 4>, b[it]);
-#pragma unroll
-        for (int k = 0; k < (int)(sizeof(W) / 4); ++k) asm volatile("" ::"v"(w.v[k]));
-    }
-}
-
 // Sum of squares of the lane's 16 x values in double (ggml_float), as the
 // CPU's rms_norm accumulates them (ops.cpp:3757-3761: each square rounded to
 // fp32, then added in double).
