@@ -422,13 +422,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
         return;
     }
     if (DYN2 && Mtot > 2 * G) {
-        // Two rows in flight, claimed likewise after each wave's first two
-        // (slots wave and wave + WAVES, rows g and g + G): every pass consumes
-        // each buffer and reloads it with a claimed row, so the loop header
-        // always has both buffers' loads in flight in the same order; the
+        // Two rows requested at a time, the rows after each wave's first two
+        // (slots wave and wave + WAVES, rows g and g + G) claimed from the
+        // workgroup's LDS counter: slot j of workgroup b is row
+        // b * WAVES + j % WAVES + (j / WAVES) * G, so a wave whose rows arrive
+        // early takes more of them and the waves of a CU end closer together
+        // (lm_head's ended up to 7.5 us apart in the static order). Every
+        // pass consumes each buffer and reloads it with a claimed row; the
         // first claim past the rows ends the loop and the other buffer's row
-        // is consumed after it. A wave with fewer than two rows has no claims
-        // to make (every slot after its first two lies past the rows).
+        // is consumed after it. The compiler waits for both buffers at the
+        // loop header (the stores in the loop), so a wave consumes its two
+        // rows after both have arrived, then requests two more; that measured
+        // faster for lm_head than the static loop, which keeps two rows in
+        // flight throughout. A wave with fewer than two rows has no claims to
+        // make (every slot after its first two lies past the rows). Every row
+        // is computed with the same arithmetic by whichever wave takes it.
         if (nrows >= 2) {
             int r0 = g, r1 = g + G;
             bool first = true;
