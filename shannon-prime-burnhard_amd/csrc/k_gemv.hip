@@ -119,7 +119,11 @@ __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)
 // g, g + G, g + 2G, ... of the concatenated segments (G = waves in the grid),
 // with D rows of loads in flight. With XFW the quantising waves fetch and
 // quantise x before issuing their own weight loads, so that x is not queued
-// behind the weight requests of the whole CU.
+// behind the weight requests of the whole CU. The row loop takes one of four
+// forms: OP (every wave at most D rows: no loop), EI (one row in flight, the
+// next row's loads issued on the current row's arrival, results stored once
+// a wave), DYN2 (two rows at a time, the later rows claimed within the
+// workgroup), or the static loop (the rest: fused forms, one row a wave).
 // NORM: x is RMS-normalised and multiplied by p.norm_w before quantisation
 // (ggml_rms_norm + ggml_mul, ggml-cpu/ops.cpp:3724-3784): the quantising
 // waves reduce the sum of squares in double across the workgroup (one more
@@ -137,9 +141,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_decode_kernel(GemvParams p) {
     static_assert(!GLU || D == 2, "the fused gate/up pair is the two rows in flight");
     static_assert(!STAMP || !GLU, "timestamps cover the unfused form");
     static_assert(!OP || (D > 1 && !GLU), "one pass of D rows a wave (OP) is an unfused form with D > 1");
-    // claimed rows: the unfused form with one row in flight
-    // EI: one row in flight, the next row's loads issued early (K <= 4096;
-    // at K = 12288 two rows in flight from the start are faster)
+    // EI: one row in flight, the next row's loads issued early, results
+    // stored once a wave (K <= 4096; at K = 12288 the two-row forms are faster)
     constexpr int NIT_ = (NB + 15) / 16;
     constexpr bool EI = D == 1 && !GLU && !OP && NIT_ == 1;
     // DYN2: two rows in flight, rows claimed from the workgroup's counter
